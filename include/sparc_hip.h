@@ -1,0 +1,232 @@
+/*
+ * sparc_hip.h -- C ABI of the MI355X (gfx950) SPARC scan library
+ * (libsparc_hip.so).
+ *
+ * Plain pointers and sizes only.  Every tensor is caller-allocated device
+ * memory, row-major and contiguous; every call is enqueued on the caller's
+ * HIP stream and returns without synchronising.  Scratch memory comes in
+ * through ``workspace`` (size from the matching *_workspace_bytes query,
+ * contents undefined on entry); calls that share one workspace must be
+ * ordered on one stream.  No entry point allocates device memory.
+ *
+ * Shapes: B batch rows, T time steps, M complex modes (or M real channels for
+ * the real scan), G gate groups per token with group size M/G (mode m uses
+ * gate m / (M/G)).  The mode axis of a model with D channels of N states is
+ * m = d*N + n, so G = D shares one gate pair across a channel's N states and
+ * G = 1 is the reference module (one (eta, delta) pair per token).
+ *
+ * Errors: a non-zero sparc_status; sparc_last_error() describes the most
+ * recent failure of the calling thread.
+ */
+#ifndef SPARC_HIP_H
+#define SPARC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* sparc_stream_t; /* a hipStream_t; NULL = default stream */
+
+typedef enum sparc_status {
+  SPARC_OK = 0,
+  SPARC_EINVAL = 1,       /* bad shape, pointer, dtype or flag combination */
+  SPARC_EUNSUPPORTED = 2, /* valid request this build does not implement */
+  SPARC_EHIP = 3,         /* a HIP runtime call failed */
+  SPARC_EWORKSPACE = 4    /* workspace missing or too small */
+} sparc_status;
+
+typedef enum sparc_dtype { SPARC_F32 = 0, SPARC_BF16 = 1 } sparc_dtype;
+
+typedef enum sparc_transition {
+  /* a = rho*exp(i*(theta_m + (1-rho)*delta)), rho = exp(-nu_m*exp(eta));
+   * gate0 = eta, gate1 = delta (fp32), nu_m = exp(nu_log), theta_m = exp(theta_log).
+   * sparc-kernal/forward/scan.py:941-946 (reference P1 transition) */
+  SPARC_TRANSITION_P1 = 0,
+  /* a = r*exp(i*phi); gate0 = r (retention), gate1 = phi (phase) */
+  SPARC_TRANSITION_POLAR = 1,
+  /* a = gate0 + i*gate1 (G = M is the reference's complex_scan) */
+  SPARC_TRANSITION_CARTESIAN = 2,
+  /* real scan h = a*h + b; gate0 = a (G = M is the reference's real scans);
+   * w_im, y_im, gate1 and every imaginary pointer are NULL */
+  SPARC_TRANSITION_REAL = 3
+} sparc_transition;
+
+enum {
+  /* y is the module output relu(cat(h_re, h_im)) [B,T,2M] written through
+   * y_re (y_im NULL); in the backward dy_re is the gradient of that output
+   * (dy_im NULL).  Complex transitions only. */
+  SPARC_FLAG_RELU_OUTPUT = 1,
+  /* the transition of step 0 is replaced by 0 (drops h0).  A non-NULL
+   * segment_pos takes precedence: steps with segment_pos[b,t] == 0 reset. */
+  SPARC_FLAG_RESET_FIRST = 2
+};
+
+typedef struct sparc_scan_desc {
+  int64_t batch;      /* B */
+  int64_t length;     /* T >= 0 */
+  int64_t modes;      /* M */
+  int64_t groups;     /* G, divides M */
+  int32_t transition; /* sparc_transition */
+  int32_t io_dtype;   /* sparc_dtype of w, y, dy, dw */
+  int32_t gate_dtype; /* sparc_dtype of gate0/gate1/dgate*: F32 for P1, io_dtype otherwise */
+  int32_t flags;      /* SPARC_FLAG_* */
+} sparc_scan_desc;
+
+/* Time steps per chunk (the granularity of saved chunk states) and the
+ * number of chunks, ceil(T / chunk). */
+int64_t sparc_scan_chunk_length(const sparc_scan_desc* d);
+int64_t sparc_scan_chunk_count(const sparc_scan_desc* d);
+
+/* Bytes of workspace needed by sparc_scan_forward (direction 0) or
+ * sparc_scan_backward (direction 1). */
+size_t sparc_scan_workspace_bytes(const sparc_scan_desc* d, int direction);
+
+/*
+ * Forward chunked scan: h_t = a_t h_{t-1} + w_t, fp32 state, one pass over
+ * the inputs.  Replaces _SPARCChunkScan.forward
+ * (sparc-kernal/backward/scan.py:1126-1372: _sparc_chunk_summary,
+ * _sparc_chunk_prefix / hierarchical / grouped carries, _sparc_chunk_replay),
+ * _RealChunkScan.forward (:825-860), _ComplexScan.forward (:887-904),
+ * _SPARCScan / _SPARCTiledSerialScan forward (:922-1015) and the output
+ * epilogue torch.cat((out_r, out_i), -1).relu() (forward/scan.py:1598-1603).
+ *
+ *   gate0, gate1   [B,T,G] gate_dtype
+ *   nu_log, theta_log [M] fp32 (P1 only, else NULL)
+ *   w_re, w_im     [B,T,M] io_dtype
+ *   h0_re, h0_im   [B,M] fp32 initial state, or NULL for zero
+ *   segment_pos    [B,T] int32 or NULL
+ *   y_re, y_im     [B,T,M] io_dtype (or y_re = [B,T,2M] with RELU_OUTPUT)
+ *   chunk_state    [B, n_chunks, M, 2] fp32 (real: [B, n_chunks, M]): the
+ *                  state after the last step of every chunk.  Its last chunk
+ *                  is the final state ("cache" of return_cache=True); the
+ *                  backward reads it to recompute states.
+ */
+sparc_status sparc_scan_forward(const sparc_scan_desc* d,
+                                const void* gate0, const void* gate1,
+                                const float* nu_log, const float* theta_log,
+                                const void* w_re, const void* w_im,
+                                const float* h0_re, const float* h0_im,
+                                const int32_t* segment_pos,
+                                void* y_re, void* y_im,
+                                float* chunk_state,
+                                void* workspace, size_t workspace_bytes,
+                                sparc_stream_t stream);
+
+/*
+ * Backward of sparc_scan_forward: reverse-time scan of the adjoint
+ * lambda_{t-1} = conj(a_t) lambda_t + dy_{t-1}, with states recomputed in
+ * fp32 from chunk_state (no [B,T,M] state is saved).  Replaces
+ * _SPARCChunkScan.backward (sparc-kernal/backward/scan.py:1375-1640:
+ * _sparc_reverse_chunk_summary / _prefix / _replay and
+ * _reduce_shared_control_gradients, backward/control.py:139-152),
+ * _RealChunkScan.backward (:862-884), _ComplexScan.backward (:906-919) and
+ * _SPARCTiledSerialScan.backward (:1023-1070).  Gate and parameter
+ * gradient reductions are deterministic (fixed-order partial sums, no float
+ * atomics).
+ *
+ *   dy_re, dy_im   [B,T,M] io_dtype (or dy_re = [B,T,2M] with RELU_OUTPUT)
+ *   dlast_re/_im   [B,M] fp32 gradient of the final state, or NULL
+ *   dw_re, dw_im   [B,T,M] io_dtype, written
+ *   dgate0/dgate1  [B,T,G] gate_dtype, written
+ *   dnu_log, dtheta_log [M] fp32 (P1 only), written (not accumulated)
+ *   dh0_re/_im     [B,M] fp32, written when h0 was given (else NULL)
+ */
+sparc_status sparc_scan_backward(const sparc_scan_desc* d,
+                                 const void* gate0, const void* gate1,
+                                 const float* nu_log, const float* theta_log,
+                                 const void* w_re, const void* w_im,
+                                 const float* h0_re, const float* h0_im,
+                                 const int32_t* segment_pos,
+                                 const float* chunk_state,
+                                 const void* dy_re, const void* dy_im,
+                                 const float* dlast_re, const float* dlast_im,
+                                 void* dw_re, void* dw_im,
+                                 void* dgate0, void* dgate1,
+                                 float* dnu_log, float* dtheta_log,
+                                 float* dh0_re, float* dh0_im,
+                                 void* workspace, size_t workspace_bytes,
+                                 sparc_stream_t stream);
+
+/* Host-synchronising check of a workspace after forward/backward calls: 0 if
+ * no cross-workgroup wait exceeded its bound, else 1.  For tests. */
+int sparc_scan_workspace_error(const void* workspace, sparc_stream_t stream);
+
+/*
+ * P1 write prologue w = gain * (tanh x_re + i tanh x_im) with
+ * gain = exp(wlg) * sqrt(expm1(-2 nu e^eta) / expm1(-2 nu)) * 2 sigmoid(q),
+ * q = (delta/(pi/2)) * wpr + (eta/log 16) * wrr.  rows = B*T.
+ * Replaces _latest_write_forward (sparc-kernal/forward/control.py:166-195).
+ *   x [rows, 2M] io_dtype; eta, delta [rows] fp32; nu_log, write_log_gain,
+ *   write_phase_response, write_radial_response [M] fp32;
+ *   w_re, w_im [rows, M] io_dtype.
+ */
+sparc_status sparc_write_forward(int64_t rows, int64_t modes, int32_t io_dtype,
+                                 const void* x, const float* eta, const float* delta,
+                                 const float* nu_log, const float* write_log_gain,
+                                 const float* write_phase_response,
+                                 const float* write_radial_response,
+                                 void* w_re, void* w_im, sparc_stream_t stream);
+
+size_t sparc_write_workspace_bytes(int64_t rows, int64_t modes);
+
+/*
+ * Backward of the write prologue.  Replaces _latest_write_backward
+ * (sparc-kernal/backward/control.py:10-89) with deterministic reductions.
+ *   dw_re, dw_im [rows, M] io_dtype; dx [rows, 2M] io_dtype (written);
+ *   deta, ddelta [rows] fp32 (written); dnu_log, dwrite_log_gain,
+ *   dwrite_phase_response, dwrite_radial_response [M] fp32 (written).
+ */
+sparc_status sparc_write_backward(int64_t rows, int64_t modes, int32_t io_dtype,
+                                  const void* x, const float* eta, const float* delta,
+                                  const float* nu_log, const float* write_log_gain,
+                                  const float* write_phase_response,
+                                  const float* write_radial_response,
+                                  const void* dw_re, const void* dw_im,
+                                  void* dx, float* deta, float* ddelta,
+                                  float* dnu_log, float* dwrite_log_gain,
+                                  float* dwrite_phase_response,
+                                  float* dwrite_radial_response,
+                                  void* workspace, size_t workspace_bytes,
+                                  sparc_stream_t stream);
+
+/*
+ * One fused P1 decode step for B independent rows: controls (two dot
+ * products over 2M), transition, write, state update, relu(cat) output.
+ * Replaces _latest_sparc_decode / latest_sparc_decode
+ * (sparc-kernal/forward/decode.py:10-75) and the eager step (:296-306).
+ *   x [B, 2M] io_dtype; phase_direction, radial_direction [2M+1] fp32;
+ *   nu_log, theta_log, write_log_gain, write_phase_response,
+ *   write_radial_response [M] fp32; state_re/_im [B,M] fp32 (read);
+ *   new_re/_im [B,M] fp32 (written; may alias state_re/_im for an in-place
+ *   update: every element is read before it is written, by the same thread);
+ *   y [B, 2M] io_dtype.
+ */
+sparc_status sparc_decode_step(int64_t batch, int64_t modes, int32_t io_dtype,
+                               const void* x,
+                               const float* phase_direction, const float* radial_direction,
+                               const float* nu_log, const float* theta_log,
+                               const float* write_log_gain,
+                               const float* write_phase_response,
+                               const float* write_radial_response,
+                               const float* state_re, const float* state_im,
+                               float* new_re, float* new_im, void* y,
+                               sparc_stream_t stream);
+
+/*
+ * Deterministic sum over rows of a [rows, cols] fp32 matrix into [cols]
+ * (or accumulate into out when accumulate != 0).  Used for the reductions of
+ * per-tile partial gradients.
+ */
+sparc_status sparc_column_sum(int64_t rows, int64_t cols, const float* in,
+                              float* out, int accumulate, sparc_stream_t stream);
+
+const char* sparc_last_error(void);
+const char* sparc_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SPARC_HIP_H */

@@ -1,0 +1,99 @@
+"""P1 controls and write prologue.
+
+``make_controls`` keeps the reference's torch formulation
+(sparc-kernal/forward/control.py:129-139); the write ``gain * tanh(x)`` and
+its backward run as HIP kernels (sparc_write_forward / sparc_write_backward)
+in place of ``_latest_write_forward`` / ``_latest_write_backward``
+(sparc-kernal/forward/control.py:166-195, backward/control.py:10-89).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+LOG16 = math.log(16.0)
+HALF_PI = math.pi / 2.0
+
+
+def make_controls(module, x: torch.Tensor):
+    """(eta, delta) fp32 [B, L]: eta = log16*tanh(x.u_r + b_r),
+    delta = (pi/2)*tanh(x.u_p + b_p).  sparc-kernal/forward/control.py:129-139."""
+    directions = torch.stack((module.phase_direction, module.radial_direction))
+    with torch.autocast(device_type=x.device.type, enabled=False):
+        projected = F.linear(x.float(), directions[:, :-1].float(), directions[:, -1].float())
+        inactive_energy_slot = 0.0 * module.energy_response.sum()
+        return (
+            LOG16 * torch.tanh(projected[..., 1]) + inactive_energy_slot,
+            HALF_PI * torch.tanh(projected[..., 0]),
+        )
+
+
+class _LatestSPARCWrite(torch.autograd.Function):
+    """``_LatestSPARCWrite`` (sparc-kernal/backward/control.py:92-129)."""
+
+    @staticmethod
+    def forward(ctx, raw_x, eta, delta, nu_log, write_log_gain, phase_response, radial_response):
+        lib = _lib.load()
+        dev = _lib.require_gpu(raw_x, eta, delta, nu_log)
+        raw_x = raw_x.contiguous()
+        eta, delta = eta.float().contiguous(), delta.float().contiguous()
+        params = [p.float().contiguous() for p in (nu_log, write_log_gain, phase_response, radial_response)]
+        B, L, W = raw_x.shape
+        M, rows = W // 2, B * L
+        w_r = torch.empty(B, L, M, dtype=raw_x.dtype, device=dev)
+        w_i = torch.empty_like(w_r)
+        P = _lib.ptr
+        _lib.check(lib.sparc_write_forward(
+            rows, M, _lib.io_code(raw_x.dtype), P(raw_x), P(eta), P(delta),
+            *[P(p) for p in params], P(w_r), P(w_i), _lib.stream_of(dev)), "sparc_write_forward")
+        ctx.save_for_backward(raw_x, eta, delta, *params)
+        ctx.param_dtypes = (nu_log.dtype, write_log_gain.dtype, phase_response.dtype, radial_response.dtype)
+        return w_r, w_i
+
+    @staticmethod
+    def backward(ctx, grad_r, grad_i):
+        raw_x, eta, delta, nu_log, wlg, wpr, wrr = ctx.saved_tensors
+        lib = _lib.load()
+        dev = raw_x.device
+        B, L, W = raw_x.shape
+        M, rows = W // 2, B * L
+        if grad_r is None:
+            grad_r = torch.zeros(B, L, M, dtype=raw_x.dtype, device=dev)
+        if grad_i is None:
+            grad_i = torch.zeros(B, L, M, dtype=raw_x.dtype, device=dev)
+        grad_r = grad_r.to(raw_x.dtype).contiguous()
+        grad_i = grad_i.to(raw_x.dtype).contiguous()
+        dx = torch.empty_like(raw_x)
+        deta = torch.empty(B, L, dtype=torch.float32, device=dev)
+        ddelta = torch.empty_like(deta)
+        grads = [torch.empty(M, dtype=torch.float32, device=dev) for _ in range(4)]
+        ws_bytes = lib.sparc_write_workspace_bytes(rows, M)
+        ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+        P = _lib.ptr
+        _lib.check(lib.sparc_write_backward(
+            rows, M, _lib.io_code(raw_x.dtype), P(raw_x), P(eta), P(delta), P(nu_log), P(wlg),
+            P(wpr), P(wrr), P(grad_r), P(grad_i), P(dx), P(deta), P(ddelta),
+            *[P(g) for g in grads], P(ws), ws.numel(), _lib.stream_of(dev)), "sparc_write_backward")
+        grads = [g.to(dt) for g, dt in zip(grads, ctx.param_dtypes)]
+        return (dx, deta, ddelta, *grads)
+
+
+def latest_sparc_write(raw_x, eta, delta, nu_log, write_log_gain, phase_response, radial_response):
+    """``latest_sparc_write`` (sparc-kernal/backward/control.py:132-137)."""
+    return _LatestSPARCWrite.apply(raw_x, eta, delta, nu_log, write_log_gain,
+                                   phase_response, radial_response)
+
+
+def make_scan_inputs(module, x: torch.Tensor):
+    """``make_scan_inputs`` (sparc-kernal/forward/control.py:141-149):
+    (eta, delta, write_r, write_i)."""
+    eta, delta = make_controls(module, x)
+    write_r, write_i = latest_sparc_write(
+        x, eta, delta, module.nu_log, module.write_log_gain,
+        module.write_phase_response, module.write_radial_response)
+    return eta, delta, write_r, write_i

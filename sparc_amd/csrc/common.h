@@ -1,0 +1,201 @@
+// Device helpers shared by the SPARC HIP kernels (gfx950 / CDNA4).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sparc {
+
+// ---------------------------------------------------------------------------
+// element types
+// ---------------------------------------------------------------------------
+struct bf16 {  // storage tag: raw IEEE bfloat16 bits
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950), two at a time.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+  typedef __attribute__((__vector_size__(2 * sizeof(float)))) float float2_t;
+  float2_t f = {lo, hi};
+  bf16x2_t b = __builtin_convertvector(f, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, b);
+}
+__device__ __forceinline__ uint16_t pack_bf16(float v) {
+  return (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
+}
+
+// Raw vector of V elements of type IO, loaded/stored with one instruction.
+template <typename IO, int V> struct Raw;
+template <> struct Raw<bf16, 1> { using T = uint16_t; };
+template <> struct Raw<bf16, 2> { using T = uint32_t; };
+template <> struct Raw<bf16, 4> { using T = uint2; };
+template <> struct Raw<bf16, 8> { using T = uint4; };
+template <> struct Raw<float, 1> { using T = float; };
+template <> struct Raw<float, 2> { using T = float2; };
+template <> struct Raw<float, 4> { using T = float4; };
+
+template <typename IO, int V>
+__device__ __forceinline__ typename Raw<IO, V>::T load_raw(const void* base, int64_t index) {
+  using R = typename Raw<IO, V>::T;
+  return reinterpret_cast<const R*>(static_cast<const IO*>(base) + index)[0];
+}
+template <typename IO, int V>
+__device__ __forceinline__ void store_raw(void* base, int64_t index, typename Raw<IO, V>::T v) {
+  using R = typename Raw<IO, V>::T;
+  reinterpret_cast<R*>(static_cast<IO*>(base) + index)[0] = v;
+}
+
+template <typename IO, int V>
+__device__ __forceinline__ void unpack(const typename Raw<IO, V>::T& r, float (&o)[V]) {
+  if constexpr (sizeof(IO) == 4) {
+    const float* f = reinterpret_cast<const float*>(&r);
+#pragma unroll
+    for (int v = 0; v < V; ++v) o[v] = f[v];
+  } else if constexpr (V == 1) {
+    o[0] = bf16_bits_to_float(r);
+  } else {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(&r);
+#pragma unroll
+    for (int v = 0; v < V / 2; ++v) {
+      o[2 * v] = __uint_as_float(w[v] << 16);
+      o[2 * v + 1] = __uint_as_float(w[v] & 0xffff0000u);
+    }
+  }
+}
+
+template <typename IO, int V>
+__device__ __forceinline__ typename Raw<IO, V>::T pack(const float (&i)[V]) {
+  typename Raw<IO, V>::T r;
+  if constexpr (sizeof(IO) == 4) {
+    float* f = reinterpret_cast<float*>(&r);
+#pragma unroll
+    for (int v = 0; v < V; ++v) f[v] = i[v];
+  } else if constexpr (V == 1) {
+    r = pack_bf16(i[0]);
+  } else {
+    uint32_t* w = reinterpret_cast<uint32_t*>(&r);
+#pragma unroll
+    for (int v = 0; v < V / 2; ++v) w[v] = pack_bf16x2(i[2 * v], i[2 * v + 1]);
+  }
+  return r;
+}
+
+template <typename IO>
+__device__ __forceinline__ float load1(const void* base, int64_t index) {
+  if constexpr (sizeof(IO) == 4) return static_cast<const float*>(base)[index];
+  else return bf16_bits_to_float(static_cast<const uint16_t*>(base)[index]);
+}
+template <typename IO>
+__device__ __forceinline__ void store1(void* base, int64_t index, float v) {
+  if constexpr (sizeof(IO) == 4) static_cast<float*>(base)[index] = v;
+  else static_cast<uint16_t*>(base)[index] = pack_bf16(v);
+}
+
+// ---------------------------------------------------------------------------
+// math
+// ---------------------------------------------------------------------------
+// exp(x) through the hardware base-2 exponential (v_exp_f32).
+__device__ __forceinline__ float fast_exp(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
+// sin and cos of |x| <= pi/4 by their Taylor series (truncation error below
+// 1e-9 on that interval, i.e. well under one fp32 ulp of the result).
+__device__ __forceinline__ void sincos_quarter(float x, float& s, float& c) {
+  const float x2 = x * x;
+  // sin x = x (1 - x^2/3! + x^4/5! - x^6/7! + x^8/9!)
+  float ps = 2.7557319223985893e-6f;          // 1/9!
+  ps = fmaf(ps, x2, -1.9841269841269841e-4f); // 1/7!
+  ps = fmaf(ps, x2, 8.3333333333333332e-3f);  // 1/5!
+  ps = fmaf(ps, x2, -1.6666666666666666e-1f); // 1/3!
+  s = fmaf(ps * x2, x, x);
+  // cos x = 1 - x^2/2! + x^4/4! - x^6/6! + x^8/8! - x^10/10!
+  float pc = -2.7557319223985888e-7f;         // 1/10!
+  pc = fmaf(pc, x2, 2.4801587301587302e-5f);  // 1/8!
+  pc = fmaf(pc, x2, -1.3888888888888889e-3f); // 1/6!
+  pc = fmaf(pc, x2, 4.1666666666666664e-2f);  // 1/4!
+  pc = fmaf(pc, x2, -0.5f);
+  c = fmaf(pc, x2, 1.0f);
+}
+
+// sin and cos for moderate |x| (gate phases, a few multiples of pi):
+// x = k*(pi/2) + r with a two-term Cody-Waite split of pi/2, then the quadrant
+// k mod 4 selects sign and swap.
+__device__ __forceinline__ void sincos_moderate(float x, float& s, float& c) {
+  const float k = rintf(x * 0.63661977236758134f);  // 2/pi
+  float r = fmaf(k, -1.5707963705062866f, x);        // pi/2 rounded to fp32
+  r = fmaf(k, 4.3711388286737929e-8f, r);            // minus the rounding error of that constant
+  float sr, cr;
+  sincos_quarter(r, sr, cr);
+  const int q = static_cast<int>(k) & 3;
+  const float ss = (q & 1) ? cr : sr;
+  const float cc = (q & 1) ? sr : cr;
+  s = (q & 2) ? -ss : ss;
+  c = ((q + 1) & 2) ? -cc : cc;
+}
+
+// ---------------------------------------------------------------------------
+// cross-workgroup publication of chunk carries
+// ---------------------------------------------------------------------------
+// Carries travel between workgroups that may sit on different XCDs, whose L2
+// caches are not coherent with each other.  Every value a consumer reads is
+// written with an agent-scope store (the sc1 cache policy: written through to
+// the device coherence point) and read with an agent-scope load (sc1: not
+// served from a possibly stale L2 line).  The producer waits for its own
+// stores to complete (s_waitcnt vmcnt(0)) before it stores the flag, so a
+// consumer that has observed the flag observes the data.  No L2 writeback or
+// invalidate is needed for these few lines.
+template <typename T>
+__device__ __forceinline__ void store_agent(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T load_agent(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores_complete() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt untouched (gfx9 encoding)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+enum : uint32_t { FLAG_EMPTY = 0, FLAG_AGGREGATE = 1, FLAG_INCLUSIVE = 2 };
+
+// Bounded spin on a flag word (uniform across the wave).  Returns the flag, or
+// FLAG_INCLUSIVE after ``limit`` polls having set *error: a wait that could
+// never end (it cannot, by the ticket order, but the bound makes that a
+// property of the code rather than an assumption) turns into a reported error.
+__device__ __forceinline__ uint32_t poll_flag(const uint32_t* flag, uint32_t* error,
+                                              uint32_t limit) {
+  for (uint32_t it = 0; it < limit; ++it) {
+    uint32_t f = load_agent(flag);
+    f = __builtin_amdgcn_readfirstlane(f);
+    if (f != FLAG_EMPTY) {
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      return f;
+    }
+    // once any wait of this launch has failed, stop waiting at all
+    if ((it & 255u) == 255u && __builtin_amdgcn_readfirstlane(load_agent(error)) != 0u) break;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  store_agent(error, 1u);
+  return FLAG_INCLUSIVE;
+}
+
+}  // namespace sparc
+
+// ---------------------------------------------------------------------------
+// host-side error reporting shared by every translation unit of the library
+// ---------------------------------------------------------------------------
+#include <stdarg.h>
+#include <stdio.h>
+namespace sparc {
+inline char* error_buffer() {
+  static thread_local char buf[512] = "";
+  return buf;
+}
+}  // namespace sparc

@@ -1,0 +1,413 @@
+// SPARC P1 write prologue (forward/backward), fused decode step and
+// deterministic column reductions for gfx950.
+//
+// Reference kernels replaced: _latest_write_forward
+// (sparc-kernal/forward/control.py:166-195), _latest_write_backward
+// (sparc-kernal/backward/control.py:10-89), _latest_sparc_decode
+// (sparc-kernal/forward/decode.py:10-56).
+
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+#include "sparc_hip.h"
+
+namespace sparc {
+
+constexpr float kLog16 = 2.772588722239781f;       // log(16)
+constexpr float kInvLog16 = 0.36067376022224085f;  // 1/log(16)
+constexpr float kHalfPi = 1.5707963267948966f;
+constexpr float kTwoOverPi = 0.6366197723675814f;
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---------------------------------------------------------------------------
+// write forward: one block = 256 threads x WV modes, R rows
+// ---------------------------------------------------------------------------
+constexpr int WV = 2;
+constexpr int WR = 16;  // rows per block
+
+template <typename IO>
+__global__ void __launch_bounds__(256)
+write_fwd_kernel(int64_t rows, int M, const void* x, const float* eta, const float* delta,
+                 const float* nu_log, const float* wlg, const float* wpr, const float* wrr,
+                 void* w_re, void* w_im) {
+  const int m0 = (blockIdx.x * 256 + threadIdx.x) * WV;
+  if (m0 >= M) return;
+  float nu[WV], den[WV], g0[WV], pr[WV], rr[WV];
+#pragma unroll
+  for (int v = 0; v < WV; ++v) {
+    nu[v] = expf(nu_log[m0 + v]);
+    den[v] = -expm1f(-2.0f * nu[v]);
+    g0[v] = expf(wlg[m0 + v]);
+    pr[v] = wpr[m0 + v];
+    rr[v] = wrr[m0 + v];
+  }
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * WR;
+  for (int i = 0; i < WR; ++i) {
+    const int64_t r = r0 + i;
+    if (r >= rows) break;
+    const float e = eta[r], dl = delta[r];
+    const float E = expf(e);
+    const float phase = dl * kTwoOverPi, radial = e * kInvLog16;
+    float xr[WV], xi[WV], outr[WV], outi[WV];
+    unpack<IO, WV>(load_raw<IO, WV>(x, r * 2 * M + m0), xr);
+    unpack<IO, WV>(load_raw<IO, WV>(x, r * 2 * M + M + m0), xi);
+#pragma unroll
+    for (int v = 0; v < WV; ++v) {
+      const float ratio = sqrtf(-expm1f(-2.0f * nu[v] * E) / den[v]);
+      const float gate = 2.0f * sigmoidf_(phase * pr[v] + radial * rr[v]);
+      const float gain = g0[v] * ratio * gate;
+      outr[v] = gain * tanhf(xr[v]);
+      outi[v] = gain * tanhf(xi[v]);
+    }
+    store_raw<IO, WV>(w_re, r * M + m0, pack<IO, WV>(outr));
+    store_raw<IO, WV>(w_im, r * M + m0, pack<IO, WV>(outi));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// write backward: block = 256 threads x WV modes, WB rows.
+//   dx written directly; per-row (deta, ddelta) partials per mode slice;
+//   per-mode parameter partials per row block.  Reduced afterwards in fixed
+//   order.
+// ---------------------------------------------------------------------------
+constexpr int WB = 32;
+
+template <typename IO>
+__global__ void __launch_bounds__(256)
+write_bwd_kernel(int64_t rows, int M, int n_slices, const void* x, const float* eta, const float* delta,
+                 const float* nu_log, const float* wlg, const float* wpr, const float* wrr,
+                 const void* dw_re, const void* dw_im, void* dx,
+                 float* part_eta, float* part_delta,   // [rows, n_slices]
+                 float* part_par) {                    // [4, n_row_blocks, M]
+  __shared__ float red[2][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m0 = (blockIdx.x * 256 + threadIdx.x) * WV;
+  const bool ok = m0 < M;
+  float nu[WV], den[WV], stat[WV], g0[WV], pr[WV], rr[WV];
+#pragma unroll
+  for (int v = 0; v < WV; ++v) {
+    const int m = ok ? m0 + v : 0;
+    nu[v] = expf(nu_log[m]);
+    den[v] = -expm1f(-2.0f * nu[v]);
+    stat[v] = nu[v] * expf(-2.0f * nu[v]) / den[v];
+    g0[v] = expf(wlg[m]);
+    pr[v] = wpr[m];
+    rr[v] = wrr[m];
+  }
+  float acc_nu[WV] = {}, acc_g[WV] = {}, acc_p[WV] = {}, acc_r[WV] = {};
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * WB;
+  for (int i = 0; i < WB; ++i) {
+    const int64_t r = r0 + i;
+    if (r >= rows) break;
+    const float e = eta[r], dl = delta[r];
+    const float E = expf(e);
+    const float phase = dl * kTwoOverPi, radial = e * kInvLog16;
+    float de = 0.0f, dd = 0.0f;
+    if (ok) {
+      float xr[WV], xi[WV], gr[WV], gi[WV], oxr[WV], oxi[WV];
+      unpack<IO, WV>(load_raw<IO, WV>(x, r * 2 * M + m0), xr);
+      unpack<IO, WV>(load_raw<IO, WV>(x, r * 2 * M + M + m0), xi);
+      unpack<IO, WV>(load_raw<IO, WV>(dw_re, r * M + m0), gr);
+      unpack<IO, WV>(load_raw<IO, WV>(dw_im, r * M + m0), gi);
+#pragma unroll
+      for (int v = 0; v < WV; ++v) {
+        const float eff = nu[v] * E;
+        const float num = -expm1f(-2.0f * eff);
+        const float ratio = sqrtf(num / den[v]);
+        const float gate = 2.0f * sigmoidf_(phase * pr[v] + radial * rr[v]);
+        const float gain = g0[v] * ratio * gate;
+        const float cr = tanhf(xr[v]), ci = tanhf(xi[v]);
+        const float gain_grad = gain * (gr[v] * cr + gi[v] * ci);
+        const float gate_grad = gain_grad * (1.0f - 0.5f * gate);
+        const float dyn = eff * expf(-2.0f * eff) / num;
+        de += gain_grad * dyn + gate_grad * rr[v] * kInvLog16;
+        dd += gate_grad * pr[v] * kTwoOverPi;
+        oxr[v] = gr[v] * gain * (1.0f - cr * cr);
+        oxi[v] = gi[v] * gain * (1.0f - ci * ci);
+        acc_nu[v] += gain_grad * (dyn - stat[v]);
+        acc_g[v] += gain_grad;
+        acc_p[v] += gate_grad * phase;
+        acc_r[v] += gate_grad * radial;
+      }
+      store_raw<IO, WV>(dx, r * 2 * M + m0, pack<IO, WV>(oxr));
+      store_raw<IO, WV>(dx, r * 2 * M + M + m0, pack<IO, WV>(oxi));
+    }
+    // block sum of (de, dd): wave butterfly, then the 4 waves in order
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      de += __shfl_xor(de, off, 64);
+      dd += __shfl_xor(dd, off, 64);
+    }
+    if (lane == 0) { red[0][wave] = de; red[1][wave] = dd; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      part_eta[r * n_slices + blockIdx.x] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+      part_delta[r * n_slices + blockIdx.x] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    }
+    __syncthreads();
+  }
+  if (ok) {
+    const int64_t base = static_cast<int64_t>(blockIdx.y) * M + m0;
+    const int64_t plane = static_cast<int64_t>(gridDim.y) * M;
+#pragma unroll
+    for (int v = 0; v < WV; ++v) {
+      part_par[base + v] = acc_nu[v];
+      part_par[plane + base + v] = acc_g[v];
+      part_par[2 * plane + base + v] = acc_p[v];
+      part_par[3 * plane + base + v] = acc_r[v];
+    }
+  }
+}
+
+__global__ void fill_zero_kernel(float* p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+// out[r] = sum_j in[r, j] over a [rows, cols] matrix, j in order.
+__global__ void row_sum_kernel(int64_t rows, int64_t cols, const float* in, float* out) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  float acc = 0.0f;
+  for (int64_t j = 0; j < cols; ++j) acc += in[r * cols + j];
+  out[r] = acc;
+}
+
+// out[c] (+)= sum_r in[r, c]; rows summed in order, one column per thread.
+__global__ void column_sum_kernel(int64_t rows, int64_t cols, const float* in, float* out, int accumulate) {
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  float acc = 0.0f;
+  for (int64_t r = 0; r < rows; ++r) acc += in[r * cols + c];
+  out[c] = accumulate ? out[c] + acc : acc;
+}
+
+// ---------------------------------------------------------------------------
+// decode step: one workgroup of 1024 threads per batch row
+// ---------------------------------------------------------------------------
+template <typename IO>
+__global__ void __launch_bounds__(1024)
+decode_kernel(int M, const void* x, const float* pdir, const float* rdir,
+              const float* nu_log, const float* theta_log, const float* wlg,
+              const float* wpr, const float* wrr,
+              const float* state_re, const float* state_im, float* new_re, float* new_im, void* y) {
+  __shared__ float red[2][16];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int W = 2 * M;
+  const int64_t xrow = static_cast<int64_t>(b) * W;
+  // controls: two dot products over the 2M inputs (+ bias)
+  float p0 = 0.0f, p1 = 0.0f;
+  for (int i = tid * 2; i < W; i += 2048) {
+    float xv[2];
+    unpack<IO, 2>(load_raw<IO, 2>(x, xrow + i), xv);
+    p0 = fmaf(xv[0], pdir[i], fmaf(xv[1], pdir[i + 1], p0));
+    p1 = fmaf(xv[0], rdir[i], fmaf(xv[1], rdir[i + 1], p1));
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    p0 += __shfl_xor(p0, off, 64);
+    p1 += __shfl_xor(p1, off, 64);
+  }
+  if (lane == 0) { red[0][wave] = p0; red[1][wave] = p1; }
+  __syncthreads();
+  float s0 = pdir[W], s1 = rdir[W];
+  for (int k = 0; k < 16; ++k) { s0 += red[0][k]; s1 += red[1][k]; }
+  const float phase_signal = tanhf(s0);
+  const float radial_signal = tanhf(s1);
+  const float eta = kLog16 * radial_signal;
+  const float delta = kHalfPi * phase_signal;
+  const float E = expf(eta);
+  const int64_t srow = static_cast<int64_t>(b) * M;
+  for (int m0 = tid * 2; m0 < M; m0 += 2048) {
+    float xr[2], xi[2], yr[2], yi[2];
+    unpack<IO, 2>(load_raw<IO, 2>(x, xrow + m0), xr);
+    unpack<IO, 2>(load_raw<IO, 2>(x, xrow + M + m0), xi);
+    const float2 orr = *reinterpret_cast<const float2*>(state_re + srow + m0);
+    const float2 oii = *reinterpret_cast<const float2*>(state_im + srow + m0);
+    const float o_r[2] = {orr.x, orr.y}, o_i[2] = {oii.x, oii.y};
+    float n_r[2], n_i[2];
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int m = m0 + v;
+      const float nu = expf(nu_log[m]);
+      const float theta = expf(theta_log[m]);
+      const float eff = nu * E;
+      const float rho = expf(-eff);
+      float sn, cs;
+      sincosf(theta + (1.0f - rho) * delta, &sn, &cs);
+      const float ar = rho * cs, ai = rho * sn;
+      const float ratio = sqrtf(expm1f(-2.0f * eff) / expm1f(-2.0f * nu));
+      const float gate = 2.0f * sigmoidf_(phase_signal * wpr[m] + radial_signal * wrr[m]);
+      const float gain = expf(wlg[m]) * ratio * gate;
+      n_r[v] = ar * o_r[v] - ai * o_i[v] + gain * tanhf(xr[v]);
+      n_i[v] = ai * o_r[v] + ar * o_i[v] + gain * tanhf(xi[v]);
+      yr[v] = fmaxf(n_r[v], 0.0f);
+      yi[v] = fmaxf(n_i[v], 0.0f);
+    }
+    *reinterpret_cast<float2*>(new_re + srow + m0) = make_float2(n_r[0], n_r[1]);
+    *reinterpret_cast<float2*>(new_im + srow + m0) = make_float2(n_i[0], n_i[1]);
+    store_raw<IO, 2>(y, xrow + m0, pack<IO, 2>(yr));
+    store_raw<IO, 2>(y, xrow + M + m0, pack<IO, 2>(yi));
+  }
+}
+
+}  // namespace sparc
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+namespace {
+sparc_status fail2(sparc_status s, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+sparc_status fail2(sparc_status s, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(sparc::error_buffer(), 512, fmt, ap);
+  va_end(ap);
+  return s;
+}
+bool al(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+}  // namespace
+
+extern "C" {
+
+sparc_status sparc_write_forward(int64_t rows, int64_t modes, int32_t io_dtype, const void* x,
+                                 const float* eta, const float* delta, const float* nu_log,
+                                 const float* write_log_gain, const float* write_phase_response,
+                                 const float* write_radial_response, void* w_re, void* w_im,
+                                 sparc_stream_t stream) {
+  if (rows < 0 || modes <= 0 || modes % 2 || modes > INT32_MAX / 4)
+    return fail2(SPARC_EINVAL, "write: rows >= 0, modes > 0 and even required");
+  if (io_dtype != SPARC_F32 && io_dtype != SPARC_BF16) return fail2(SPARC_EINVAL, "write: io_dtype");
+  if (!x || !eta || !delta || !nu_log || !write_log_gain || !write_phase_response || !write_radial_response || !w_re || !w_im)
+    return fail2(SPARC_EINVAL, "write: NULL pointer");
+  const size_t va = (io_dtype == SPARC_BF16 ? 2 : 4) * 2;
+  if (!al(x, va) || !al(w_re, va) || !al(w_im, va)) return fail2(SPARC_EINVAL, "write: misaligned tensor");
+  if (rows == 0) return SPARC_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  dim3 g(static_cast<unsigned>((modes / 2 + 255) / 256), static_cast<unsigned>((rows + sparc::WR - 1) / sparc::WR));
+  if (g.y > 65535u * 1024u) return fail2(SPARC_EINVAL, "write: too many rows");
+  if (io_dtype == SPARC_BF16)
+    hipLaunchKernelGGL(sparc::write_fwd_kernel<sparc::bf16>, g, dim3(256), 0, st, rows, static_cast<int>(modes), x, eta, delta,
+                       nu_log, write_log_gain, write_phase_response, write_radial_response, w_re, w_im);
+  else
+    hipLaunchKernelGGL(sparc::write_fwd_kernel<float>, g, dim3(256), 0, st, rows, static_cast<int>(modes), x, eta, delta,
+                       nu_log, write_log_gain, write_phase_response, write_radial_response, w_re, w_im);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "write forward: %s", hipGetErrorString(e));
+}
+
+static void write_bwd_sizes(int64_t rows, int64_t modes, int64_t* n_slices, int64_t* n_rb, size_t* bytes) {
+  *n_slices = (modes / 2 + 255) / 256;
+  *n_rb = (rows + sparc::WB - 1) / sparc::WB;
+  const size_t pe = static_cast<size_t>(rows) * *n_slices;
+  const size_t pp = static_cast<size_t>(4) * *n_rb * modes;
+  *bytes = (2 * pe + pp) * 4 + 256;
+}
+
+size_t sparc_write_workspace_bytes(int64_t rows, int64_t modes) {
+  if (rows < 0 || modes <= 0) return 0;
+  int64_t a, b;
+  size_t bytes;
+  write_bwd_sizes(rows, modes, &a, &b, &bytes);
+  return bytes;
+}
+
+sparc_status sparc_write_backward(int64_t rows, int64_t modes, int32_t io_dtype, const void* x,
+                                  const float* eta, const float* delta, const float* nu_log,
+                                  const float* write_log_gain, const float* write_phase_response,
+                                  const float* write_radial_response, const void* dw_re, const void* dw_im,
+                                  void* dx, float* deta, float* ddelta, float* dnu_log,
+                                  float* dwrite_log_gain, float* dwrite_phase_response,
+                                  float* dwrite_radial_response, void* workspace, size_t workspace_bytes,
+                                  sparc_stream_t stream) {
+  if (rows < 0 || modes <= 0 || modes % 2 || modes > INT32_MAX / 4)
+    return fail2(SPARC_EINVAL, "write backward: rows >= 0, modes > 0 and even required");
+  if (io_dtype != SPARC_F32 && io_dtype != SPARC_BF16) return fail2(SPARC_EINVAL, "write backward: io_dtype");
+  if (!x || !eta || !delta || !nu_log || !write_log_gain || !write_phase_response || !write_radial_response ||
+      !dw_re || !dw_im || !dx || !deta || !ddelta || !dnu_log || !dwrite_log_gain || !dwrite_phase_response ||
+      !dwrite_radial_response)
+    return fail2(SPARC_EINVAL, "write backward: NULL pointer");
+  int64_t n_slices, n_rb;
+  size_t need;
+  write_bwd_sizes(rows, modes, &n_slices, &n_rb, &need);
+  if (!workspace || workspace_bytes < need) return fail2(SPARC_EWORKSPACE, "write backward: workspace too small (%zu < %zu)", workspace_bytes, need);
+  const size_t va = (io_dtype == SPARC_BF16 ? 2 : 4) * 2;
+  if (!al(x, va) || !al(dw_re, va) || !al(dw_im, va) || !al(dx, va) || !al(workspace, 256))
+    return fail2(SPARC_EINVAL, "write backward: misaligned tensor");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  float* pe = static_cast<float*>(workspace);
+  float* pd = pe + rows * n_slices;
+  float* pp = pd + rows * n_slices;
+  if (rows == 0) {
+    const dim3 gz(static_cast<unsigned>((modes + 255) / 256));
+    for (float* o : {dnu_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response})
+      hipLaunchKernelGGL(sparc::fill_zero_kernel, gz, dim3(256), 0, st, o, modes);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "write backward: %s", hipGetErrorString(e));
+  }
+  dim3 g(static_cast<unsigned>(n_slices), static_cast<unsigned>(n_rb));
+  if (io_dtype == SPARC_BF16)
+    hipLaunchKernelGGL(sparc::write_bwd_kernel<sparc::bf16>, g, dim3(256), 0, st, rows, static_cast<int>(modes),
+                       static_cast<int>(n_slices), x, eta, delta, nu_log, write_log_gain, write_phase_response,
+                       write_radial_response, dw_re, dw_im, dx, pe, pd, pp);
+  else
+    hipLaunchKernelGGL(sparc::write_bwd_kernel<float>, g, dim3(256), 0, st, rows, static_cast<int>(modes),
+                       static_cast<int>(n_slices), x, eta, delta, nu_log, write_log_gain, write_phase_response,
+                       write_radial_response, dw_re, dw_im, dx, pe, pd, pp);
+  // deterministic reductions: per-row over the mode slices, per-mode over the row blocks
+  const dim3 gr(static_cast<unsigned>((rows + 255) / 256));
+  hipLaunchKernelGGL(sparc::row_sum_kernel, gr, dim3(256), 0, st, rows, n_slices, pe, deta);
+  hipLaunchKernelGGL(sparc::row_sum_kernel, gr, dim3(256), 0, st, rows, n_slices, pd, ddelta);
+  const int64_t plane = n_rb * modes;
+  const dim3 gm(static_cast<unsigned>((modes + 255) / 256));
+  hipLaunchKernelGGL(sparc::column_sum_kernel, gm, dim3(256), 0, st, n_rb, modes, pp, dnu_log, 0);
+  hipLaunchKernelGGL(sparc::column_sum_kernel, gm, dim3(256), 0, st, n_rb, modes, pp + plane, dwrite_log_gain, 0);
+  hipLaunchKernelGGL(sparc::column_sum_kernel, gm, dim3(256), 0, st, n_rb, modes, pp + 2 * plane, dwrite_phase_response, 0);
+  hipLaunchKernelGGL(sparc::column_sum_kernel, gm, dim3(256), 0, st, n_rb, modes, pp + 3 * plane, dwrite_radial_response, 0);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "write backward: %s", hipGetErrorString(e));
+}
+
+sparc_status sparc_column_sum(int64_t rows, int64_t cols, const float* in, float* out, int accumulate,
+                              sparc_stream_t stream) {
+  if (rows < 0 || cols <= 0 || !out || (rows > 0 && !in)) return fail2(SPARC_EINVAL, "column_sum: bad arguments");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(sparc::column_sum_kernel, dim3(static_cast<unsigned>((cols + 255) / 256)), dim3(256), 0, st,
+                     rows, cols, in, out, accumulate);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "column_sum: %s", hipGetErrorString(e));
+}
+
+sparc_status sparc_decode_step(int64_t batch, int64_t modes, int32_t io_dtype, const void* x,
+                               const float* phase_direction, const float* radial_direction,
+                               const float* nu_log, const float* theta_log, const float* write_log_gain,
+                               const float* write_phase_response, const float* write_radial_response,
+                               const float* state_re, const float* state_im, float* new_re, float* new_im,
+                               void* y, sparc_stream_t stream) {
+  if (batch < 0 || modes <= 0 || modes % 2 || modes > INT32_MAX / 4)
+    return fail2(SPARC_EINVAL, "decode: batch >= 0, modes > 0 and even required");
+  if (io_dtype != SPARC_F32 && io_dtype != SPARC_BF16) return fail2(SPARC_EINVAL, "decode: io_dtype");
+  if (!x || !phase_direction || !radial_direction || !nu_log || !theta_log || !write_log_gain ||
+      !write_phase_response || !write_radial_response || !state_re || !state_im || !new_re || !new_im || !y)
+    return fail2(SPARC_EINVAL, "decode: NULL pointer");
+  const size_t va = (io_dtype == SPARC_BF16 ? 2 : 4) * 2;
+  if (!al(x, va) || !al(y, va) || !al(state_re, 8) || !al(state_im, 8) || !al(new_re, 8) || !al(new_im, 8))
+    return fail2(SPARC_EINVAL, "decode: misaligned tensor");
+  if (batch == 0) return SPARC_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (io_dtype == SPARC_BF16)
+    hipLaunchKernelGGL(sparc::decode_kernel<sparc::bf16>, dim3(static_cast<unsigned>(batch)), dim3(1024), 0, st,
+                       static_cast<int>(modes), x, phase_direction, radial_direction, nu_log, theta_log, write_log_gain,
+                       write_phase_response, write_radial_response, state_re, state_im, new_re, new_im, y);
+  else
+    hipLaunchKernelGGL(sparc::decode_kernel<float>, dim3(static_cast<unsigned>(batch)), dim3(1024), 0, st,
+                       static_cast<int>(modes), x, phase_direction, radial_direction, nu_log, theta_log, write_log_gain,
+                       write_phase_response, write_radial_response, state_re, state_im, new_re, new_im, y);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "decode: %s", hipGetErrorString(e));
+}
+
+}  // extern "C"

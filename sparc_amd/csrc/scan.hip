@@ -1,0 +1,1449 @@
+// SPARC chunked diagonal linear scan for gfx950: forward and backward.
+//
+// h_t = a_t * h_{t-1} + w_t over T steps for every (batch row, mode), complex
+// (M modes, planar re/im tensors) or real, fp32 state, bf16 or fp32 I/O.
+//
+// Work decomposition (both directions)
+//   tile  = (batch row b, mode block of 64*V modes, chunk of C = S*NW steps)
+//   chain = the tiles of one (b, mode block), ordered in time
+//   one workgroup = NW waves per tile; wave k owns steps [k*S, (k+1)*S) of the
+//   chunk and every lane owns V adjacent modes, so each step of a wave is one
+//   coalesced V-element load per plane.
+// Single pass: every input element is loaded from HBM once, kept in
+// registers, summarised, and replayed once the carry into the chunk is known.
+//   1. each wave scans its S steps from a zero state -> (P_k, Q_k), the affine
+//      map "state in -> state out" of its sub-chunk (P = prod a, Q = local h);
+//   2. the NW maps are composed in LDS into the tile aggregate;
+//   3. the tile publishes its aggregate, then looks back along its chain
+//      (decoupled look-back) until it finds a published inclusive carry,
+//      composing aggregates on the way; it publishes its own inclusive carry
+//      (= the state after its last step, which is also the saved chunk state
+//      the backward recomputes from);
+//   4. every wave replays its S steps from its exact start state and stores.
+// Tiles are claimed through an atomic ticket in chunk-major order, so every
+// tile's predecessors were claimed earlier by running workgroups: the
+// look-back waits always end.  The waits are bounded anyway (poll_flag).
+//
+// The backward runs the same machinery on the adjoint in reverse time
+// (lambda_{t-1} = conj(a_t) lambda_t + dy_{t-1}) after recomputing the
+// forward states of the chunk from the saved chunk state, so no [B,T,M]
+// state is stored by the forward.
+//
+// Reference kernels replaced: _sparc_chunk_summary / _sparc_chunk_prefix /
+// _sparc_chunk_replay (sparc-kernal/forward/scan.py:885-1003, 1276-1354),
+// the hierarchical and grouped carries (forward/scan.py:1082-1273), the real
+// and complex scans (forward/scan.py:621-722), the serial SPARC scans
+// (forward/scan.py:724-854) and their reverse-time counterparts
+// (sparc-kernal/backward/scan.py:34-781).
+
+#include <type_traits>
+
+#include "common.h"
+#include "sparc_hip.h"
+
+namespace sparc {
+
+enum Transition : int { TR_P1 = 0, TR_POLAR = 1, TR_CART = 2, TR_REAL = 3 };
+
+// How a lane's V modes map to gates.
+enum GateMode : int {
+  GATE_LANE = 0,   // all V modes of a lane share one gate; a group fits in one tile
+  GATE_MODE = 1,   // one gate per mode (G == M)
+  GATE_CROSS = 2   // group spans several tiles (or G == 1): partial sums per tile
+};
+
+struct ScanArgs {
+  int B, T, M, G, gs;
+  int n_chunks, n_mblocks, n_chains;
+  uint32_t flags;
+  uint32_t spin_limit;
+  const void* g0;
+  const void* g1;
+  const float* nu_log;
+  const float* theta_log;
+  const void* w_re;
+  const void* w_im;
+  const float* h0_re;
+  const float* h0_im;
+  const int32_t* segpos;
+  void* y_re;
+  void* y_im;
+  float* chunk_state;
+  // backward
+  const float* chunk_state_in;
+  const void* dy_re;
+  const void* dy_im;
+  const float* dlast_re;
+  const float* dlast_im;
+  void* dw_re;
+  void* dw_im;
+  void* dg0;
+  void* dg1;
+  float* part_g0;     // [B*T, n_mblocks] (GATE_CROSS)
+  float* part_g1;
+  float* part_nu;     // [B*n_chunks, M] (P1)
+  float* part_theta;
+  float* dh0_re;
+  float* dh0_im;
+  // workspace
+  uint32_t* ticket;
+  uint32_t* error;
+  uint32_t* flagv;    // [n_chains, n_chunks]
+  float* agg;         // [n_chains, n_chunks, 64*V, NQ]
+  float* carry;       // backward inclusive adjoint carries [B, n_chunks, M, NH]
+};
+
+template <typename T> struct IsBf16 : std::false_type {};
+template <> struct IsBf16<bf16> : std::true_type {};
+
+// ----- small complex helpers ----------------------------------------------
+__device__ __forceinline__ void cmul(float ar, float ai, float br, float bi, float& cr, float& ci) {
+  cr = ar * br - ai * bi;
+  ci = ar * bi + ai * br;
+}
+
+// Loads a lane's V-element fp32 vector with agent-scope (sc1) loads.
+template <int N>
+__device__ __forceinline__ void load_agent_vec(const float* p, float (&o)[N]) {
+  if constexpr (N % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      uint64_t u = load_agent(reinterpret_cast<const uint64_t*>(p) + i);
+      o[2 * i] = __uint_as_float(static_cast<uint32_t>(u));
+      o[2 * i + 1] = __uint_as_float(static_cast<uint32_t>(u >> 32));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) o[i] = __uint_as_float(load_agent(reinterpret_cast<const uint32_t*>(p) + i));
+  }
+}
+template <int N>
+__device__ __forceinline__ void store_agent_vec(float* p, const float (&v)[N]) {
+  if constexpr (N % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      uint64_t u = static_cast<uint64_t>(__float_as_uint(v[2 * i])) |
+                   (static_cast<uint64_t>(__float_as_uint(v[2 * i + 1])) << 32);
+      store_agent(reinterpret_cast<uint64_t*>(p) + i, u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) store_agent(reinterpret_cast<uint32_t*>(p) + i, __float_as_uint(v[i]));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Per-lane transition machinery
+// ---------------------------------------------------------------------------
+template <int TR, typename IO, int V, int GM>
+struct TransitionLane {
+  static constexpr bool CPLX = TR != TR_REAL;
+  static constexpr bool P1 = TR == TR_P1;
+  // number of distinct gate values per lane and step
+  static constexpr int GV = (GM == GATE_MODE) ? V : 1;
+  // number of distinct transition values per lane and step
+  static constexpr int AV = (P1 || GM == GATE_MODE) ? V : 1;
+  using GT = std::conditional_t<P1, float, IO>;
+
+  // P1 per-mode constants
+  float nu[P1 ? V : 1], th[P1 ? V : 1], ct[P1 ? V : 1], st[P1 ? V : 1];
+
+  __device__ __forceinline__ void init(const ScanArgs& p, int m0, bool ok) {
+    if constexpr (P1) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float nl = ok ? p.nu_log[m0 + v] : 0.0f;
+        const float tl = ok ? p.theta_log[m0 + v] : 0.0f;
+        nu[v] = expf(nl);
+        th[v] = expf(tl);
+        sincosf(th[v], &st[v], &ct[v]);
+      }
+    }
+  }
+
+  // gate index of the lane's first mode
+  __device__ __forceinline__ int64_t gate_index(const ScanArgs& p, int b, int t, int m0) const {
+    const int64_t row = static_cast<int64_t>(b) * p.T + t;
+    if constexpr (GM == GATE_MODE) return row * p.M + m0;
+    else return row * p.G + m0 / p.gs;
+  }
+
+  __device__ __forceinline__ void load_gates(const ScanArgs& p, int64_t gi, float (&g0)[GV], float (&g1)[GV]) const {
+    if constexpr (GM == GATE_MODE) {
+      float tmp[V];
+      unpack<GT, V>(load_raw<GT, V>(p.g0, gi), tmp);
+#pragma unroll
+      for (int v = 0; v < V; ++v) g0[v] = tmp[v];
+      if constexpr (CPLX) {
+        unpack<GT, V>(load_raw<GT, V>(p.g1, gi), tmp);
+#pragma unroll
+        for (int v = 0; v < V; ++v) g1[v] = tmp[v];
+      } else {
+#pragma unroll
+        for (int v = 0; v < V; ++v) g1[v] = 0.0f;
+      }
+    } else {
+      g0[0] = load1<GT>(p.g0, gi);
+      g1[0] = CPLX ? load1<GT>(p.g1, gi) : 0.0f;
+    }
+  }
+
+  // a = transition(g0, g1) for every distinct value
+  __device__ __forceinline__ void transition(const float (&g0)[GV], const float (&g1)[GV],
+                                             float (&ar)[AV], float (&ai)[AV]) const {
+    if constexpr (P1) {
+      const float E = fast_exp(g0[0]);  // GV == 1 for P1
+      const float delta = g1[0];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float rho = fast_exp(-nu[v] * E);
+        float sd, cd;
+        sincos_quarter_or_half((1.0f - rho) * delta, sd, cd);
+        ar[v] = rho * (ct[v] * cd - st[v] * sd);
+        ai[v] = rho * (st[v] * cd + ct[v] * sd);
+      }
+    } else if constexpr (TR == TR_POLAR) {
+#pragma unroll
+      for (int v = 0; v < AV; ++v) {
+        float s, c;
+        sincos_moderate(g1[v], s, c);
+        ar[v] = g0[v] * c;
+        ai[v] = g0[v] * s;
+      }
+    } else if constexpr (TR == TR_CART) {
+#pragma unroll
+      for (int v = 0; v < AV; ++v) {
+        ar[v] = g0[v];
+        ai[v] = g1[v];
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < AV; ++v) {
+        ar[v] = g0[v];
+        ai[v] = 0.0f;
+      }
+    }
+  }
+
+  // |delta*(1-rho)| <= pi/2 for the P1 controls (|delta| <= pi/2), but
+  // eta/delta are caller data: reduce generally when out of the quarter range.
+  __device__ __forceinline__ static void sincos_quarter_or_half(float x, float& s, float& c) {
+    sincos_moderate(x, s, c);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Forward kernel
+// ---------------------------------------------------------------------------
+template <int TR, typename IO, int V, int GM, int S, int NW>
+__global__ void __launch_bounds__(NW * 64)
+scan_fwd_kernel(ScanArgs p) {
+  using TL = TransitionLane<TR, IO, V, GM>;
+  constexpr bool CPLX = TL::CPLX;
+  constexpr int AV = TL::AV;
+  constexpr int GV = TL::GV;
+  constexpr int C = S * NW;
+  constexpr int MB = 64 * V;
+  constexpr int NQ = CPLX ? 4 : 2;   // (P re, P im, Q re, Q im) or (P, Q)
+  constexpr int NH = CPLX ? 2 : 1;
+  using RawT = typename Raw<IO, V>::T;
+
+  __shared__ float s_pq[NW][NQ][V][64];
+  __shared__ float s_start[NW][NH][V][64];
+  __shared__ uint32_t s_tile;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) s_tile = atomicAdd(p.ticket, 1u);
+  __syncthreads();
+  const uint32_t tile = s_tile;
+  const int chain = static_cast<int>(tile % static_cast<uint32_t>(p.n_chains));
+  const int chunk = static_cast<int>(tile / static_cast<uint32_t>(p.n_chains));
+  const int b = chain / p.n_mblocks;
+  const int mb = chain - b * p.n_mblocks;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < p.M;
+  const int t0 = chunk * C + wave * S;
+  const bool relu_out = CPLX && (p.flags & SPARC_FLAG_RELU_OUTPUT);
+  const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
+
+  TL tl;
+  tl.init(p, m0, lane_ok);
+
+  // ---- load the sub-chunk: inputs, gates, transitions --------------------
+  RawT wr_raw[S], wi_raw[S];
+  float g0[S][GV], g1[S][GV];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int t = t0 + s;
+    const bool ok = lane_ok && t < p.T;
+    const int64_t idx = (static_cast<int64_t>(b) * p.T + t) * p.M + m0;
+    if (ok) {
+      wr_raw[s] = load_raw<IO, V>(p.w_re, idx);
+      if constexpr (CPLX) wi_raw[s] = load_raw<IO, V>(p.w_im, idx);
+      tl.load_gates(p, tl.gate_index(p, b, t, m0), g0[s], g1[s]);
+    } else {
+      float z[V] = {};
+      wr_raw[s] = pack<IO, V>(z);
+      if constexpr (CPLX) wi_raw[s] = wr_raw[s];
+#pragma unroll
+      for (int v = 0; v < GV; ++v) { g0[s][v] = 0.0f; g1[s][v] = 0.0f; }
+    }
+  }
+  float a_r[S][AV], a_i[S][AV];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int t = t0 + s;
+    tl.transition(g0[s], g1[s], a_r[s], a_i[s]);
+    bool reset;
+    if (p.segpos) reset = (t < p.T) && p.segpos[static_cast<int64_t>(b) * p.T + t] == 0;
+    else reset = reset_first && t == 0;
+    const bool ident = !(lane_ok && t < p.T);
+#pragma unroll
+    for (int v = 0; v < AV; ++v) {
+      if (ident) { a_r[s][v] = 1.0f; a_i[s][v] = 0.0f; }
+      if (reset) { a_r[s][v] = 0.0f; a_i[s][v] = 0.0f; }
+    }
+  }
+
+  // ---- 1. local scan of the sub-chunk from a zero state ------------------
+  float Pr[AV], Pi[AV], Qr[V], Qi[V];
+#pragma unroll
+  for (int v = 0; v < AV; ++v) { Pr[v] = 1.0f; Pi[v] = 0.0f; }
+#pragma unroll
+  for (int v = 0; v < V; ++v) { Qr[v] = 0.0f; Qi[v] = 0.0f; }
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    float wr[V], wi[V];
+    unpack<IO, V>(wr_raw[s], wr);
+    if constexpr (CPLX) unpack<IO, V>(wi_raw[s], wi);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int av = AV == 1 ? 0 : v;
+      if constexpr (CPLX) {
+        const float nr = a_r[s][av] * Qr[v] - a_i[s][av] * Qi[v] + wr[v];
+        const float ni = a_i[s][av] * Qr[v] + a_r[s][av] * Qi[v] + wi[v];
+        Qr[v] = nr;
+        Qi[v] = ni;
+      } else {
+        Qr[v] = a_r[s][av] * Qr[v] + wr[v];
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < AV; ++v) {
+      if constexpr (CPLX) {
+        float nr, ni;
+        cmul(a_r[s][v], a_i[s][v], Pr[v], Pi[v], nr, ni);
+        Pr[v] = nr;
+        Pi[v] = ni;
+      } else {
+        Pr[v] = a_r[s][v] * Pr[v];
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int av = AV == 1 ? 0 : v;
+    s_pq[wave][0][v][lane] = Pr[av];
+    if constexpr (CPLX) {
+      s_pq[wave][1][v][lane] = Pi[av];
+      s_pq[wave][2][v][lane] = Qr[v];
+      s_pq[wave][3][v][lane] = Qi[v];
+    } else {
+      s_pq[wave][1][v][lane] = Qr[v];
+    }
+  }
+  __syncthreads();
+
+  // ---- 2./3. tile aggregate, look-back, inclusive carry (wave 0) ---------
+  if (wave == 0) {
+    float TPr[V], TPi[V], TQr[V], TQi[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) { TPr[v] = 1.0f; TPi[v] = 0.0f; TQr[v] = 0.0f; TQi[v] = 0.0f; }
+#pragma unroll
+    for (int k = 0; k < NW; ++k) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if constexpr (CPLX) {
+          const float pr = s_pq[k][0][v][lane], pi = s_pq[k][1][v][lane];
+          const float qr = s_pq[k][2][v][lane], qi = s_pq[k][3][v][lane];
+          float nr, ni;
+          cmul(pr, pi, TQr[v], TQi[v], nr, ni);
+          TQr[v] = nr + qr;
+          TQi[v] = ni + qi;
+          cmul(pr, pi, TPr[v], TPi[v], nr, ni);
+          TPr[v] = nr;
+          TPi[v] = ni;
+        } else {
+          const float pr = s_pq[k][0][v][lane], qr = s_pq[k][1][v][lane];
+          TQr[v] = pr * TQr[v] + qr;
+          TPr[v] = pr * TPr[v];
+        }
+      }
+    }
+    float cr[V], ci[V];
+    if (chunk == 0) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+        cr[v] = (p.h0_re && lane_ok) ? p.h0_re[hi] : 0.0f;
+        ci[v] = (CPLX && p.h0_im && lane_ok) ? p.h0_im[hi] : 0.0f;
+      }
+    } else {
+      // publish the aggregate of this tile
+      float* my_agg = p.agg + ((static_cast<int64_t>(chain) * p.n_chunks + chunk) * MB + lane * V) * NQ;
+      float pv[V * NQ];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        pv[v * NQ + 0] = TPr[v];
+        if constexpr (CPLX) {
+          pv[v * NQ + 1] = TPi[v];
+          pv[v * NQ + 2] = TQr[v];
+          pv[v * NQ + 3] = TQi[v];
+        } else {
+          pv[v * NQ + 1] = TQr[v];
+        }
+      }
+      store_agent_vec<V * NQ>(my_agg, pv);
+      wait_stores_complete();
+      if (lane == 0) store_agent(p.flagv + static_cast<int64_t>(chain) * p.n_chunks + chunk, uint32_t(FLAG_AGGREGATE));
+      // look back: X = composition of the aggregates of chunks j+1 .. chunk-1
+      float Xpr[V], Xpi[V], Xqr[V], Xqi[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) { Xpr[v] = 1.0f; Xpi[v] = 0.0f; Xqr[v] = 0.0f; Xqi[v] = 0.0f; }
+      int j = chunk - 1;
+      while (true) {
+        const uint32_t f = poll_flag(p.flagv + static_cast<int64_t>(chain) * p.n_chunks + j, p.error, p.spin_limit);
+        if (f == FLAG_INCLUSIVE) {
+          float h[V * NH] = {};
+          if (lane_ok)
+            load_agent_vec<V * NH>(p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + j) * p.M + m0) * NH, h);
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            if constexpr (CPLX) {
+              float nr, ni;
+              cmul(Xpr[v], Xpi[v], h[2 * v], h[2 * v + 1], nr, ni);
+              cr[v] = nr + Xqr[v];
+              ci[v] = ni + Xqi[v];
+            } else {
+              cr[v] = Xpr[v] * h[v] + Xqr[v];
+              ci[v] = 0.0f;
+            }
+          }
+          break;
+        }
+        float q[V * NQ];
+        load_agent_vec<V * NQ>(p.agg + ((static_cast<int64_t>(chain) * p.n_chunks + j) * MB + lane * V) * NQ, q);
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) {
+            float nr, ni;
+            cmul(Xpr[v], Xpi[v], q[v * 4 + 2], q[v * 4 + 3], nr, ni);
+            Xqr[v] += nr;
+            Xqi[v] += ni;
+            cmul(Xpr[v], Xpi[v], q[v * 4 + 0], q[v * 4 + 1], nr, ni);
+            Xpr[v] = nr;
+            Xpi[v] = ni;
+          } else {
+            Xqr[v] += Xpr[v] * q[v * 2 + 1];
+            Xpr[v] *= q[v * 2 + 0];
+          }
+        }
+        if (--j < 0) {  // unreachable: chunk 0 only ever publishes an inclusive carry
+          store_agent(p.error, 2u);
+          break;
+        }
+      }
+    }
+    // start state of every wave, and the inclusive carry of the tile
+#pragma unroll
+    for (int k = 0; k < NW; ++k) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        s_start[k][0][v][lane] = cr[v];
+        if constexpr (CPLX) s_start[k][1][v][lane] = ci[v];
+        if constexpr (CPLX) {
+          const float pr = s_pq[k][0][v][lane], pi = s_pq[k][1][v][lane];
+          const float qr = s_pq[k][2][v][lane], qi = s_pq[k][3][v][lane];
+          float nr, ni;
+          cmul(pr, pi, cr[v], ci[v], nr, ni);
+          cr[v] = nr + qr;
+          ci[v] = ni + qi;
+        } else {
+          cr[v] = s_pq[k][0][v][lane] * cr[v] + s_pq[k][1][v][lane];
+        }
+      }
+    }
+    if (lane_ok) {
+      float h[V * NH];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if constexpr (CPLX) { h[2 * v] = cr[v]; h[2 * v + 1] = ci[v]; }
+        else h[v] = cr[v];
+      }
+      store_agent_vec<V * NH>(p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + chunk) * p.M + m0) * NH, h);
+    }
+    wait_stores_complete();
+    if (lane == 0) store_agent(p.flagv + static_cast<int64_t>(chain) * p.n_chunks + chunk, uint32_t(FLAG_INCLUSIVE));
+  }
+  __syncthreads();
+
+  // ---- 4. replay the sub-chunk from its start state and store -------------
+  float hr[V], hi[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    hr[v] = s_start[wave][0][v][lane];
+    hi[v] = CPLX ? s_start[wave][1][v][lane] : 0.0f;
+  }
+  if (!lane_ok) return;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int t = t0 + s;
+    float wr[V], wi[V];
+    unpack<IO, V>(wr_raw[s], wr);
+    if constexpr (CPLX) unpack<IO, V>(wi_raw[s], wi);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int av = AV == 1 ? 0 : v;
+      if constexpr (CPLX) {
+        const float nr = a_r[s][av] * hr[v] - a_i[s][av] * hi[v] + wr[v];
+        const float ni = a_i[s][av] * hr[v] + a_r[s][av] * hi[v] + wi[v];
+        hr[v] = nr;
+        hi[v] = ni;
+      } else {
+        hr[v] = a_r[s][av] * hr[v] + wr[v];
+      }
+    }
+    if (t < p.T) {
+      const int64_t row = static_cast<int64_t>(b) * p.T + t;
+      if (relu_out) {
+        float rr[V], ri[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
+        store_raw<IO, V>(p.y_re, row * 2 * p.M + m0, pack<IO, V>(rr));
+        store_raw<IO, V>(p.y_re, row * 2 * p.M + p.M + m0, pack<IO, V>(ri));
+      } else {
+        store_raw<IO, V>(p.y_re, row * p.M + m0, pack<IO, V>(hr));
+        if constexpr (CPLX) store_raw<IO, V>(p.y_im, row * p.M + m0, pack<IO, V>(hi));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward kernel
+// ---------------------------------------------------------------------------
+template <int TR, typename IO, int V, int GM, int S, int NW>
+__global__ void __launch_bounds__(NW * 64)
+scan_bwd_kernel(ScanArgs p) {
+  using TL = TransitionLane<TR, IO, V, GM>;
+  using GT = typename TL::GT;
+  constexpr bool CPLX = TL::CPLX;
+  constexpr bool P1 = TR == TR_P1;
+  constexpr int AV = TL::AV;
+  constexpr int GV = TL::GV;
+  constexpr int C = S * NW;
+  constexpr int MB = 64 * V;
+  constexpr int NQ = CPLX ? 4 : 2;
+  constexpr int NH = CPLX ? 2 : 1;
+  using RawT = typename Raw<IO, V>::T;
+
+  __shared__ float s_pq[NW][NQ][V][64];
+  __shared__ float s_start[NW][NH][V][64];
+  __shared__ float s_par[P1 ? NW : 1][2][V][64];   // P1 parameter-gradient partials
+  __shared__ uint32_t s_tile;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (threadIdx.x == 0) s_tile = atomicAdd(p.ticket, 1u);
+  __syncthreads();
+  const uint32_t tile = s_tile;
+  const int chain = static_cast<int>(tile % static_cast<uint32_t>(p.n_chains));
+  const int chunk = p.n_chunks - 1 - static_cast<int>(tile / static_cast<uint32_t>(p.n_chains));
+  const int b = chain / p.n_mblocks;
+  const int mb = chain - b * p.n_mblocks;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < p.M;
+  const int t0 = chunk * C + wave * S;
+  const bool relu_out = CPLX && (p.flags & SPARC_FLAG_RELU_OUTPUT);
+  const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
+
+  TL tl;
+  tl.init(p, m0, lane_ok);
+
+  // ---- loads ----------------------------------------------------------------
+  RawT wr_raw[S], wi_raw[S], dr_raw[S], di_raw[S];
+  float g0[S][GV], g1[S][GV];
+  bool rst[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int t = t0 + s;
+    const bool ok = lane_ok && t < p.T;
+    const int64_t row = static_cast<int64_t>(b) * p.T + t;
+    const int64_t idx = row * p.M + m0;
+    if (ok) {
+      wr_raw[s] = load_raw<IO, V>(p.w_re, idx);
+      if constexpr (CPLX) wi_raw[s] = load_raw<IO, V>(p.w_im, idx);
+      if (relu_out) {
+        dr_raw[s] = load_raw<IO, V>(p.dy_re, row * 2 * p.M + m0);
+        di_raw[s] = load_raw<IO, V>(p.dy_re, row * 2 * p.M + p.M + m0);
+      } else {
+        dr_raw[s] = load_raw<IO, V>(p.dy_re, idx);
+        if constexpr (CPLX) di_raw[s] = load_raw<IO, V>(p.dy_im, idx);
+      }
+      tl.load_gates(p, tl.gate_index(p, b, t, m0), g0[s], g1[s]);
+    } else {
+      float z[V] = {};
+      wr_raw[s] = pack<IO, V>(z);
+      wi_raw[s] = wr_raw[s];
+      dr_raw[s] = wr_raw[s];
+      di_raw[s] = wr_raw[s];
+#pragma unroll
+      for (int v = 0; v < GV; ++v) { g0[s][v] = 0.0f; g1[s][v] = 0.0f; }
+    }
+    if (p.segpos) rst[s] = (t < p.T) && p.segpos[row] == 0;
+    else rst[s] = reset_first && t == 0;
+  }
+  float a_r[S][AV], a_i[S][AV];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int t = t0 + s;
+    tl.transition(g0[s], g1[s], a_r[s], a_i[s]);
+    const bool ident = !(lane_ok && t < p.T);
+#pragma unroll
+    for (int v = 0; v < AV; ++v) {
+      if (ident) { a_r[s][v] = 1.0f; a_i[s][v] = 0.0f; }
+      if (rst[s]) { a_r[s][v] = 0.0f; a_i[s][v] = 0.0f; }
+    }
+  }
+
+  // ---- forward sub-chunk maps (identical arithmetic to the forward kernel) --
+  {
+    float Pr[AV], Pi[AV], Qr[V], Qi[V];
+#pragma unroll
+    for (int v = 0; v < AV; ++v) { Pr[v] = 1.0f; Pi[v] = 0.0f; }
+#pragma unroll
+    for (int v = 0; v < V; ++v) { Qr[v] = 0.0f; Qi[v] = 0.0f; }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      float wr[V], wi[V];
+      unpack<IO, V>(wr_raw[s], wr);
+      if constexpr (CPLX) unpack<IO, V>(wi_raw[s], wi);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int av = AV == 1 ? 0 : v;
+        if constexpr (CPLX) {
+          const float nr = a_r[s][av] * Qr[v] - a_i[s][av] * Qi[v] + wr[v];
+          const float ni = a_i[s][av] * Qr[v] + a_r[s][av] * Qi[v] + wi[v];
+          Qr[v] = nr;
+          Qi[v] = ni;
+        } else {
+          Qr[v] = a_r[s][av] * Qr[v] + wr[v];
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < AV; ++v) {
+        if constexpr (CPLX) {
+          float nr, ni;
+          cmul(a_r[s][v], a_i[s][v], Pr[v], Pi[v], nr, ni);
+          Pr[v] = nr;
+          Pi[v] = ni;
+        } else {
+          Pr[v] = a_r[s][v] * Pr[v];
+        }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int av = AV == 1 ? 0 : v;
+      s_pq[wave][0][v][lane] = Pr[av];
+      if constexpr (CPLX) {
+        s_pq[wave][1][v][lane] = Pi[av];
+        s_pq[wave][2][v][lane] = Qr[v];
+        s_pq[wave][3][v][lane] = Qi[v];
+      } else {
+        s_pq[wave][1][v][lane] = Qr[v];
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float cr[V], ci[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      if (chunk == 0) {
+        const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+        cr[v] = (p.h0_re && lane_ok) ? p.h0_re[hi] : 0.0f;
+        ci[v] = (CPLX && p.h0_im && lane_ok) ? p.h0_im[hi] : 0.0f;
+      } else {
+        const int64_t ci_ = ((static_cast<int64_t>(b) * p.n_chunks + chunk - 1) * p.M + m0 + v) * NH;
+        cr[v] = lane_ok ? p.chunk_state_in[ci_] : 0.0f;
+        ci[v] = (CPLX && lane_ok) ? p.chunk_state_in[ci_ + 1] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < NW; ++k) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        s_start[k][0][v][lane] = cr[v];
+        if constexpr (CPLX) s_start[k][1][v][lane] = ci[v];
+        if constexpr (CPLX) {
+          const float pr = s_pq[k][0][v][lane], pi = s_pq[k][1][v][lane];
+          const float qr = s_pq[k][2][v][lane], qi = s_pq[k][3][v][lane];
+          float nr, ni;
+          cmul(pr, pi, cr[v], ci[v], nr, ni);
+          cr[v] = nr + qr;
+          ci[v] = ni + qi;
+        } else {
+          cr[v] = s_pq[k][0][v][lane] * cr[v] + s_pq[k][1][v][lane];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- recompute the states h_{t-1} of the sub-chunk; masked dy -------------
+  float hpr[S][V], hpi[S][V];   // state before step s
+  float dyr[S][V], dyi[S][V];   // effective output gradient at step s
+  {
+    float hr[V], hi[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      hr[v] = s_start[wave][0][v][lane];
+      hi[v] = CPLX ? s_start[wave][1][v][lane] : 0.0f;
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      float wr[V], wi[V], gr[V], gi[V];
+      unpack<IO, V>(wr_raw[s], wr);
+      unpack<IO, V>(dr_raw[s], gr);
+      if constexpr (CPLX) {
+        unpack<IO, V>(wi_raw[s], wi);
+        unpack<IO, V>(di_raw[s], gi);
+      }
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        hpr[s][v] = hr[v];
+        hpi[s][v] = CPLX ? hi[v] : 0.0f;
+        const int av = AV == 1 ? 0 : v;
+        if constexpr (CPLX) {
+          const float nr = a_r[s][av] * hr[v] - a_i[s][av] * hi[v] + wr[v];
+          const float ni = a_i[s][av] * hr[v] + a_r[s][av] * hi[v] + wi[v];
+          hr[v] = nr;
+          hi[v] = ni;
+          dyr[s][v] = (relu_out && !(hr[v] > 0.0f)) ? 0.0f : gr[v];
+          dyi[s][v] = (relu_out && !(hi[v] > 0.0f)) ? 0.0f : gi[v];
+        } else {
+          hr[v] = a_r[s][av] * hr[v] + wr[v];
+          dyr[s][v] = gr[v];
+          dyi[s][v] = 0.0f;
+        }
+      }
+    }
+  }
+
+  // ---- reverse sub-chunk maps: xi_out = conj(P) xi_in + Q ------------------
+  {
+    float Xr[V], Xi[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) { Xr[v] = 0.0f; Xi[v] = 0.0f; }
+#pragma unroll
+    for (int s = S - 1; s >= 0; --s) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int av = AV == 1 ? 0 : v;
+        const float lr = dyr[s][v] + Xr[v];
+        const float li = dyi[s][v] + Xi[v];
+        if constexpr (CPLX) {
+          Xr[v] = a_r[s][av] * lr + a_i[s][av] * li;
+          Xi[v] = -a_i[s][av] * lr + a_r[s][av] * li;
+        } else {
+          Xr[v] = a_r[s][av] * lr;
+        }
+      }
+    }
+    __syncthreads();  // s_pq of the forward maps is no longer read
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      if constexpr (CPLX) {
+        // the product of conj(a) over the sub-chunk is conj of the forward product
+        s_pq[wave][1][v][lane] = -s_pq[wave][1][v][lane];
+        s_pq[wave][2][v][lane] = Xr[v];
+        s_pq[wave][3][v][lane] = Xi[v];
+      } else {
+        s_pq[wave][1][v][lane] = Xr[v];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- tile reverse aggregate, look-back over later chunks (wave 0) -------
+  if (wave == 0) {
+    float TPr[V], TPi[V], TQr[V], TQi[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) { TPr[v] = 1.0f; TPi[v] = 0.0f; TQr[v] = 0.0f; TQi[v] = 0.0f; }
+#pragma unroll
+    for (int k = NW - 1; k >= 0; --k) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if constexpr (CPLX) {
+          const float pr = s_pq[k][0][v][lane], pi = s_pq[k][1][v][lane];
+          const float qr = s_pq[k][2][v][lane], qi = s_pq[k][3][v][lane];
+          float nr, ni;
+          cmul(pr, pi, TQr[v], TQi[v], nr, ni);
+          TQr[v] = nr + qr;
+          TQi[v] = ni + qi;
+          cmul(pr, pi, TPr[v], TPi[v], nr, ni);
+          TPr[v] = nr;
+          TPi[v] = ni;
+        } else {
+          const float pr = s_pq[k][0][v][lane], qr = s_pq[k][1][v][lane];
+          TQr[v] = pr * TQr[v] + qr;
+          TPr[v] = pr * TPr[v];
+        }
+      }
+    }
+    float cr[V], ci[V];
+    if (chunk == p.n_chunks - 1) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+        cr[v] = (p.dlast_re && lane_ok) ? p.dlast_re[hi] : 0.0f;
+        ci[v] = (CPLX && p.dlast_im && lane_ok) ? p.dlast_im[hi] : 0.0f;
+      }
+    } else {
+      float* my_agg = p.agg + ((static_cast<int64_t>(chain) * p.n_chunks + chunk) * MB + lane * V) * NQ;
+      float pv[V * NQ];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        pv[v * NQ + 0] = TPr[v];
+        if constexpr (CPLX) {
+          pv[v * NQ + 1] = TPi[v];
+          pv[v * NQ + 2] = TQr[v];
+          pv[v * NQ + 3] = TQi[v];
+        } else {
+          pv[v * NQ + 1] = TQr[v];
+        }
+      }
+      store_agent_vec<V * NQ>(my_agg, pv);
+      wait_stores_complete();
+      if (lane == 0) store_agent(p.flagv + static_cast<int64_t>(chain) * p.n_chunks + chunk, uint32_t(FLAG_AGGREGATE));
+      float Xpr[V], Xpi[V], Xqr[V], Xqi[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) { Xpr[v] = 1.0f; Xpi[v] = 0.0f; Xqr[v] = 0.0f; Xqi[v] = 0.0f; }
+      int j = chunk + 1;
+      while (true) {
+        const uint32_t f = poll_flag(p.flagv + static_cast<int64_t>(chain) * p.n_chunks + j, p.error, p.spin_limit);
+        if (f == FLAG_INCLUSIVE) {
+          float h[V * NH] = {};
+          if (lane_ok)
+            load_agent_vec<V * NH>(p.carry + ((static_cast<int64_t>(b) * p.n_chunks + j) * p.M + m0) * NH, h);
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            if constexpr (CPLX) {
+              float nr, ni;
+              cmul(Xpr[v], Xpi[v], h[2 * v], h[2 * v + 1], nr, ni);
+              cr[v] = nr + Xqr[v];
+              ci[v] = ni + Xqi[v];
+            } else {
+              cr[v] = Xpr[v] * h[v] + Xqr[v];
+              ci[v] = 0.0f;
+            }
+          }
+          break;
+        }
+        float q[V * NQ];
+        load_agent_vec<V * NQ>(p.agg + ((static_cast<int64_t>(chain) * p.n_chunks + j) * MB + lane * V) * NQ, q);
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) {
+            float nr, ni;
+            cmul(Xpr[v], Xpi[v], q[v * 4 + 2], q[v * 4 + 3], nr, ni);
+            Xqr[v] += nr;
+            Xqi[v] += ni;
+            cmul(Xpr[v], Xpi[v], q[v * 4 + 0], q[v * 4 + 1], nr, ni);
+            Xpr[v] = nr;
+            Xpi[v] = ni;
+          } else {
+            Xqr[v] += Xpr[v] * q[v * 2 + 1];
+            Xpr[v] *= q[v * 2 + 0];
+          }
+        }
+        if (++j >= p.n_chunks) {  // unreachable: the last chunk only publishes an inclusive carry
+          store_agent(p.error, 2u);
+          break;
+        }
+      }
+    }
+    // incoming adjoint of every wave; the tile's outgoing adjoint
+#pragma unroll
+    for (int k = NW - 1; k >= 0; --k) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        s_start[k][0][v][lane] = cr[v];
+        if constexpr (CPLX) s_start[k][1][v][lane] = ci[v];
+        if constexpr (CPLX) {
+          const float pr = s_pq[k][0][v][lane], pi = s_pq[k][1][v][lane];
+          const float qr = s_pq[k][2][v][lane], qi = s_pq[k][3][v][lane];
+          float nr, ni;
+          cmul(pr, pi, cr[v], ci[v], nr, ni);
+          cr[v] = nr + qr;
+          ci[v] = ni + qi;
+        } else {
+          cr[v] = s_pq[k][0][v][lane] * cr[v] + s_pq[k][1][v][lane];
+        }
+      }
+    }
+    if (chunk > 0) {
+      if (lane_ok) {
+        float h[V * NH];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) { h[2 * v] = cr[v]; h[2 * v + 1] = ci[v]; }
+          else h[v] = cr[v];
+        }
+        store_agent_vec<V * NH>(p.carry + ((static_cast<int64_t>(b) * p.n_chunks + chunk) * p.M + m0) * NH, h);
+      }
+      wait_stores_complete();
+      if (lane == 0) store_agent(p.flagv + static_cast<int64_t>(chain) * p.n_chunks + chunk, uint32_t(FLAG_INCLUSIVE));
+    } else if (lane_ok && p.dh0_re) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+        p.dh0_re[hi] = cr[v];
+        if constexpr (CPLX) p.dh0_im[hi] = ci[v];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- final reverse pass: dw, transition gradients ------------------------
+  float Xr[V], Xi[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    Xr[v] = s_start[wave][0][v][lane];
+    Xi[v] = CPLX ? s_start[wave][1][v][lane] : 0.0f;
+  }
+  float acc_nu[P1 ? V : 1], acc_th[P1 ? V : 1];
+#pragma unroll
+  for (int v = 0; v < (P1 ? V : 1); ++v) { acc_nu[v] = 0.0f; acc_th[v] = 0.0f; }
+
+  // group reduction width (lanes) for GATE_LANE
+  const int glanes = (GM == GATE_LANE) ? (p.gs / V) : 1;
+
+#pragma unroll
+  for (int s = S - 1; s >= 0; --s) {
+    const int t = t0 + s;
+    const bool t_ok = t < p.T;
+    const int64_t row = static_cast<int64_t>(b) * p.T + t;
+    float lr[V], li[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      lr[v] = dyr[s][v] + Xr[v];
+      li[v] = dyi[s][v] + Xi[v];
+    }
+    if (lane_ok && t_ok) {
+      store_raw<IO, V>(p.dw_re, row * p.M + m0, pack<IO, V>(lr));
+      if constexpr (CPLX) store_raw<IO, V>(p.dw_im, row * p.M + m0, pack<IO, V>(li));
+    }
+    // gradient of the transition: dL/da = lambda * conj(h_{t-1})
+    float d0[GV], d1[GV];   // per-gate gradient contributions (summed over the lane's modes when GV == 1)
+#pragma unroll
+    for (int v = 0; v < GV; ++v) { d0[v] = 0.0f; d1[v] = 0.0f; }
+    const bool live = lane_ok && t_ok && !rst[s];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int av = AV == 1 ? 0 : v;
+      const int gv = GV == 1 ? 0 : v;
+      float gar, gai;
+      if constexpr (CPLX) {
+        gar = lr[v] * hpr[s][v] + li[v] * hpi[s][v];
+        gai = -lr[v] * hpi[s][v] + li[v] * hpr[s][v];
+      } else {
+        gar = lr[v] * hpr[s][v];
+        gai = 0.0f;
+      }
+      if (!live) { gar = 0.0f; gai = 0.0f; }
+      if constexpr (P1) {
+        const float E = fast_exp(g0[s][0]);
+        const float delta = g1[s][0];
+        const float lrad = -tl.nu[v] * E;
+        const float rho = fast_exp(lrad);
+        const float ar = a_r[s][av], ai = a_i[s][av];
+        float radial = lrad * (gar * ar + gai * ai);
+        const float phase = -gar * ai + gai * ar;
+        acc_th[v] += tl.th[v] * phase;
+        radial += (-lrad) * rho * delta * phase;
+        acc_nu[v] += radial;
+        d0[gv] += radial;
+        d1[gv] += phase * (1.0f - rho);
+      } else if constexpr (TR == TR_POLAR) {
+        const float r = g0[s][gv];
+        const float ar = a_r[s][av], ai = a_i[s][av];
+        // d|a|: (gar cos phi + gai sin phi); with a = r (cos, sin)
+        float cphi, sphi;
+        sincos_moderate(g1[s][gv], sphi, cphi);
+        d0[gv] += gar * cphi + gai * sphi;
+        d1[gv] += -gar * ai + gai * ar;
+        (void)r;
+      } else if constexpr (TR == TR_CART) {
+        d0[gv] += gar;
+        d1[gv] += gai;
+      } else {
+        d0[gv] += gar;
+      }
+      // propagate: X = conj(a) * lambda
+      if constexpr (CPLX) {
+        Xr[v] = a_r[s][av] * lr[v] + a_i[s][av] * li[v];
+        Xi[v] = -a_i[s][av] * lr[v] + a_r[s][av] * li[v];
+      } else {
+        Xr[v] = a_r[s][av] * lr[v];
+      }
+    }
+    // store gate gradients
+    if constexpr (GM == GATE_MODE) {
+      if (lane_ok && t_ok) {
+        store_raw<GT, V>(p.dg0, row * p.M + m0, pack<GT, V>(d0));
+        if constexpr (CPLX) store_raw<GT, V>(p.dg1, row * p.M + m0, pack<GT, V>(d1));
+      }
+    } else if constexpr (GM == GATE_LANE) {
+      float x0 = d0[0], x1 = d1[0];
+      for (int off = 1; off < glanes; off <<= 1) {
+        x0 += __shfl_xor(x0, off, 64);
+        if constexpr (CPLX) x1 += __shfl_xor(x1, off, 64);
+      }
+      if (lane_ok && t_ok && (lane & (glanes - 1)) == 0) {
+        const int64_t gi = row * p.G + m0 / p.gs;
+        store1<GT>(p.dg0, gi, x0);
+        if constexpr (CPLX) store1<GT>(p.dg1, gi, x1);
+      }
+    } else {  // GATE_CROSS: wave partial over its modes -> [B*T, n_mblocks]
+      float x0 = d0[0], x1 = d1[0];
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        x0 += __shfl_xor(x0, off, 64);
+        if constexpr (CPLX) x1 += __shfl_xor(x1, off, 64);
+      }
+      if (lane == 0 && t_ok) {
+        p.part_g0[row * p.n_mblocks + mb] = x0;
+        if constexpr (CPLX) p.part_g1[row * p.n_mblocks + mb] = x1;
+      }
+    }
+  }
+
+  // ---- P1 parameter gradients: sum the NW waves -> one partial per tile ----
+  if constexpr (P1) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      s_par[wave][0][v][lane] = acc_nu[v];
+      s_par[wave][1][v][lane] = acc_th[v];
+    }
+    __syncthreads();
+    if (wave == 0 && lane_ok) {
+      float pn[V], pt[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) { pn[v] = 0.0f; pt[v] = 0.0f; }
+#pragma unroll
+      for (int k = 0; k < NW; ++k) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          pn[v] += s_par[k][0][v][lane];
+          pt[v] += s_par[k][1][v][lane];
+        }
+      }
+      const int64_t prow = static_cast<int64_t>(b) * p.n_chunks + chunk;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        p.part_nu[prow * p.M + m0 + v] = pn[v];
+        p.part_theta[prow * p.M + m0 + v] = pt[v];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// helpers: workspace clear, partial reductions
+// ---------------------------------------------------------------------------
+__global__ void clear_u32_kernel(uint32_t* p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// out[r, g] = sum_{j < per} part[r, g*per + j] for G columns; fixed order.
+template <typename GT>
+__global__ void reduce_groups_kernel(const float* part, int64_t rows, int n_mblocks, int G, int per,
+                                     void* out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * G) return;
+  const int64_t r = i / G;
+  const int g = static_cast<int>(i - r * G);
+  const float* src = part + r * n_mblocks + static_cast<int64_t>(g) * per;
+  float acc = 0.0f;
+  for (int j = 0; j < per; ++j) acc += src[j];
+  store1<GT>(out, i, acc);
+}
+
+}  // namespace sparc
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+#include <stdio.h>
+#include <string.h>
+
+namespace {
+
+sparc_status fail(sparc_status s, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+sparc_status fail(sparc_status s, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(sparc::error_buffer(), 512, fmt, ap);
+  va_end(ap);
+  return s;
+}
+
+constexpr int kChunk = 64;  // C = S * NW for every instantiation
+
+struct Plan {
+  int V = 1;
+  int gm = sparc::GATE_LANE;
+  int n_chunks = 0, n_mblocks = 0, n_chains = 0;
+  int64_t n_tiles = 0;
+  size_t flags_off = 0, agg_off = 0, carry_off = 0, part_off = 0, total = 0;
+  int64_t part_g_elems = 0, part_p_elems = 0;
+};
+
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// Chooses V and the gate mode; fills sizes.  Returns an error message or NULL.
+const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl) {
+  if (!d) return "desc is NULL";
+  if (d->batch <= 0 || d->length < 0 || d->modes <= 0 || d->groups <= 0) return "B, M, G must be > 0 and T >= 0";
+  if (d->modes % d->groups) return "groups must divide modes";
+  if (d->transition < 0 || d->transition > 3) return "unknown transition";
+  if (d->io_dtype != SPARC_F32 && d->io_dtype != SPARC_BF16) return "unknown io_dtype";
+  const bool p1 = d->transition == SPARC_TRANSITION_P1;
+  if (p1 && d->gate_dtype != SPARC_F32) return "P1 gates (eta, delta) must be fp32";
+  if (!p1 && d->gate_dtype != d->io_dtype) return "gate_dtype must equal io_dtype for this transition";
+  if ((d->flags & SPARC_FLAG_RELU_OUTPUT) && d->transition == SPARC_TRANSITION_REAL)
+    return "RELU_OUTPUT needs a complex transition";
+  if (d->batch * d->length * d->modes * 2 >= (int64_t(1) << 62)) return "tensor too large";
+  if (d->modes > INT32_MAX / 2 || d->length > INT32_MAX - kChunk || d->batch > INT32_MAX) return "dimension too large";
+  const int64_t M = d->modes, G = d->groups, gs = M / G;
+  const int vmax = (d->transition == SPARC_TRANSITION_REAL) ? 4 : 2;
+  int V = 0, gm = 0;
+  auto try_v = [&](int v) -> bool {
+    if (M % v) return false;
+    if (gs == 1 && (d->transition == SPARC_TRANSITION_CARTESIAN || d->transition == SPARC_TRANSITION_REAL)) {
+      V = v; gm = sparc::GATE_MODE; return true;
+    }
+    if (gs % v) return false;
+    const int64_t mbm = 64 * v;
+    if (G == 1 || gs % mbm == 0) { V = v; gm = sparc::GATE_CROSS; return true; }
+    if (mbm % gs == 0 && is_pow2(gs / v)) { V = v; gm = sparc::GATE_LANE; return true; }
+    return false;
+  };
+  if (!try_v(vmax) && !try_v(1)) return "unsupported gate group size (need G == 1, M/G == 1, M/G dividing 64*V or a multiple of it)";
+  pl->V = V;
+  pl->gm = gm;
+  pl->n_chunks = static_cast<int>((d->length + kChunk - 1) / kChunk);
+  pl->n_mblocks = static_cast<int>((M + 64 * V - 1) / (64 * V));
+  pl->n_chains = static_cast<int>(d->batch * pl->n_mblocks);
+  pl->n_tiles = static_cast<int64_t>(pl->n_chains) * pl->n_chunks;
+  const bool cplx = d->transition != SPARC_TRANSITION_REAL;
+  const int NQ = cplx ? 4 : 2, NH = cplx ? 2 : 1;
+  size_t off = 256;  // [0] ticket, [1] error
+  pl->flags_off = off;
+  off += ((static_cast<size_t>(pl->n_tiles) * 4 + 255) / 256) * 256;
+  pl->agg_off = off;
+  off += ((static_cast<size_t>(pl->n_tiles) * 64 * V * NQ * 4 + 255) / 256) * 256;
+  pl->carry_off = off;
+  if (direction == 1) off += ((static_cast<size_t>(d->batch) * pl->n_chunks * M * NH * 4 + 255) / 256) * 256;
+  pl->part_off = off;
+  pl->part_g_elems = 0;
+  pl->part_p_elems = 0;
+  if (direction == 1) {
+    if (gm == sparc::GATE_CROSS) pl->part_g_elems = d->batch * d->length * pl->n_mblocks;
+    if (p1) pl->part_p_elems = d->batch * static_cast<int64_t>(pl->n_chunks) * M;
+    off += ((static_cast<size_t>(2 * pl->part_g_elems + 2 * pl->part_p_elems) * 4 + 255) / 256) * 256;
+  }
+  pl->total = off;
+  return nullptr;
+}
+
+template <int TR, typename IO, int V, int GM>
+struct Kernels {
+  static constexpr int S = 8;
+  static constexpr int NW = kChunk / S;
+  static void fwd(dim3 g, hipStream_t st, const sparc::ScanArgs& a) {
+    hipLaunchKernelGGL((sparc::scan_fwd_kernel<TR, IO, V, GM, S, NW>), g, dim3(NW * 64), 0, st, a);
+  }
+  static void bwd(dim3 g, hipStream_t st, const sparc::ScanArgs& a) {
+    hipLaunchKernelGGL((sparc::scan_bwd_kernel<TR, IO, V, GM, S, NW>), g, dim3(NW * 64), 0, st, a);
+  }
+};
+
+template <int TR, typename IO>
+void launch_v(int dir, int V, int gm, dim3 g, hipStream_t st, const sparc::ScanArgs& a) {
+  constexpr int VM = (TR == sparc::TR_REAL) ? 4 : 2;
+#define SPARC_LAUNCH(VV, GG)                                                            \
+  if (V == VV && gm == GG) {                                                           \
+    if (dir == 0) Kernels<TR, IO, VV, GG>::fwd(g, st, a); else Kernels<TR, IO, VV, GG>::bwd(g, st, a); \
+    return;                                                                             \
+  }
+  SPARC_LAUNCH(VM, sparc::GATE_LANE)
+  SPARC_LAUNCH(VM, sparc::GATE_CROSS)
+  SPARC_LAUNCH(1, sparc::GATE_LANE)
+  SPARC_LAUNCH(1, sparc::GATE_CROSS)
+  if constexpr (TR == sparc::TR_CART || TR == sparc::TR_REAL) {
+    SPARC_LAUNCH(VM, sparc::GATE_MODE)
+    SPARC_LAUNCH(1, sparc::GATE_MODE)
+  }
+#undef SPARC_LAUNCH
+}
+
+void launch(int dir, const sparc_scan_desc* d, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
+  dim3 g(static_cast<unsigned>(pl.n_tiles));
+  const bool bf = d->io_dtype == SPARC_BF16;
+  switch (d->transition) {
+    case SPARC_TRANSITION_P1:
+      if (bf) launch_v<sparc::TR_P1, sparc::bf16>(dir, pl.V, pl.gm, g, st, a);
+      else launch_v<sparc::TR_P1, float>(dir, pl.V, pl.gm, g, st, a);
+      break;
+    case SPARC_TRANSITION_POLAR:
+      if (bf) launch_v<sparc::TR_POLAR, sparc::bf16>(dir, pl.V, pl.gm, g, st, a);
+      else launch_v<sparc::TR_POLAR, float>(dir, pl.V, pl.gm, g, st, a);
+      break;
+    case SPARC_TRANSITION_CARTESIAN:
+      if (bf) launch_v<sparc::TR_CART, sparc::bf16>(dir, pl.V, pl.gm, g, st, a);
+      else launch_v<sparc::TR_CART, float>(dir, pl.V, pl.gm, g, st, a);
+      break;
+    default:
+      if (bf) launch_v<sparc::TR_REAL, sparc::bf16>(dir, pl.V, pl.gm, g, st, a);
+      else launch_v<sparc::TR_REAL, float>(dir, pl.V, pl.gm, g, st, a);
+      break;
+  }
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* sparc_last_error(void) { return sparc::error_buffer(); }
+const char* sparc_version(void) { return "sparc_hip 0.1 gfx950"; }
+
+int64_t sparc_scan_chunk_length(const sparc_scan_desc*) { return kChunk; }
+
+int64_t sparc_scan_chunk_count(const sparc_scan_desc* d) {
+  if (!d || d->length < 0) return -1;
+  return (d->length + kChunk - 1) / kChunk;
+}
+
+size_t sparc_scan_workspace_bytes(const sparc_scan_desc* d, int direction) {
+  Plan pl;
+  if (make_plan(d, direction, &pl)) return 0;
+  return pl.total;
+}
+
+static sparc_status common_checks(const sparc_scan_desc* d, int dir, Plan* pl,
+                                  void* workspace, size_t workspace_bytes) {
+  if (const char* e = make_plan(d, dir, pl)) return fail(SPARC_EINVAL, "%s", e);
+  if (!workspace) return fail(SPARC_EWORKSPACE, "workspace is NULL");
+  if (workspace_bytes < pl->total)
+    return fail(SPARC_EWORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, pl->total);
+  if (!aligned(workspace, 256)) return fail(SPARC_EINVAL, "workspace must be 256-byte aligned");
+  return SPARC_OK;
+}
+
+static void fill_ws(sparc::ScanArgs& a, const Plan& pl, void* ws) {
+  char* base = static_cast<char*>(ws);
+  a.ticket = reinterpret_cast<uint32_t*>(base);
+  a.error = reinterpret_cast<uint32_t*>(base) + 1;
+  a.flagv = reinterpret_cast<uint32_t*>(base + pl.flags_off);
+  a.agg = reinterpret_cast<float*>(base + pl.agg_off);
+  a.carry = reinterpret_cast<float*>(base + pl.carry_off);
+  float* part = reinterpret_cast<float*>(base + pl.part_off);
+  a.part_g0 = part;
+  a.part_g1 = part + pl.part_g_elems;
+  a.part_nu = part + 2 * pl.part_g_elems;
+  a.part_theta = part + 2 * pl.part_g_elems + pl.part_p_elems;
+}
+
+static sparc_status clear_ws(const Plan& pl, void* ws, hipStream_t st) {
+  // ticket + error words and one flag per tile
+  char* base = static_cast<char*>(ws);
+  hipLaunchKernelGGL(sparc::clear_u32_kernel, dim3(1), dim3(64), 0, st,
+                     reinterpret_cast<uint32_t*>(base), int64_t(64));
+  const int64_t n = pl.n_tiles;
+  if (n > 0)
+    hipLaunchKernelGGL(sparc::clear_u32_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st,
+                       reinterpret_cast<uint32_t*>(base + pl.flags_off), n);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SPARC_EHIP, "clear launch: %s", hipGetErrorString(e));
+  return SPARC_OK;
+}
+
+static sparc_status check_io_ptrs(const sparc_scan_desc* d, const Plan& pl, const void* const* ptrs, int n) {
+  const size_t esz = d->io_dtype == SPARC_BF16 ? 2 : 4;
+  for (int i = 0; i < n; ++i)
+    if (ptrs[i] && !aligned(ptrs[i], esz * pl.V))
+      return fail(SPARC_EINVAL, "tensor %d not aligned to %zu bytes", i, esz * pl.V);
+  return SPARC_OK;
+}
+
+sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, const void* gate1,
+                                const float* nu_log, const float* theta_log,
+                                const void* w_re, const void* w_im,
+                                const float* h0_re, const float* h0_im,
+                                const int32_t* segment_pos,
+                                void* y_re, void* y_im, float* chunk_state,
+                                void* workspace, size_t workspace_bytes, sparc_stream_t stream) {
+  Plan pl;
+  if (sparc_status s = common_checks(d, 0, &pl, workspace, workspace_bytes)) return s;
+  const bool cplx = d->transition != SPARC_TRANSITION_REAL;
+  const bool relu = (d->flags & SPARC_FLAG_RELU_OUTPUT) != 0;
+  if (!gate0 || !w_re || !y_re || !chunk_state) return fail(SPARC_EINVAL, "gate0, w_re, y_re, chunk_state are required");
+  if (cplx && (!gate1 || !w_im)) return fail(SPARC_EINVAL, "complex transitions need gate1 and w_im");
+  if (cplx && !relu && !y_im) return fail(SPARC_EINVAL, "y_im is required");
+  if (d->transition == SPARC_TRANSITION_P1 && (!nu_log || !theta_log)) return fail(SPARC_EINVAL, "P1 needs nu_log, theta_log");
+  if (cplx && ((h0_re == nullptr) != (h0_im == nullptr))) return fail(SPARC_EINVAL, "h0_re/h0_im must both be given");
+  const void* ptrs[] = {w_re, w_im, y_re, relu ? nullptr : y_im};
+  if (sparc_status s = check_io_ptrs(d, pl, ptrs, 4)) return s;
+  if (pl.gm == sparc::GATE_MODE) {
+    const void* gp[] = {gate0, gate1};
+    if (sparc_status s = check_io_ptrs(d, pl, gp, 2)) return s;
+  }
+  if (!aligned(chunk_state, 8 * pl.V)) return fail(SPARC_EINVAL, "chunk_state must be %d-byte aligned", 8 * pl.V);
+  if (d->length == 0) return SPARC_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (sparc_status s = clear_ws(pl, workspace, st)) return s;
+  sparc::ScanArgs a{};
+  a.B = static_cast<int>(d->batch);
+  a.T = static_cast<int>(d->length);
+  a.M = static_cast<int>(d->modes);
+  a.G = static_cast<int>(d->groups);
+  a.gs = static_cast<int>(d->modes / d->groups);
+  a.n_chunks = pl.n_chunks;
+  a.n_mblocks = pl.n_mblocks;
+  a.n_chains = pl.n_chains;
+  a.flags = static_cast<uint32_t>(d->flags);
+  a.spin_limit = 1u << 20;
+  a.g0 = gate0; a.g1 = gate1; a.nu_log = nu_log; a.theta_log = theta_log;
+  a.w_re = w_re; a.w_im = w_im; a.h0_re = h0_re; a.h0_im = h0_im; a.segpos = segment_pos;
+  a.y_re = y_re; a.y_im = y_im; a.chunk_state = chunk_state;
+  fill_ws(a, pl, workspace);
+  launch(0, d, pl, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SPARC_EHIP, "scan forward launch: %s", hipGetErrorString(e));
+  return SPARC_OK;
+}
+
+sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, const void* gate1,
+                                 const float* nu_log, const float* theta_log,
+                                 const void* w_re, const void* w_im,
+                                 const float* h0_re, const float* h0_im,
+                                 const int32_t* segment_pos, const float* chunk_state,
+                                 const void* dy_re, const void* dy_im,
+                                 const float* dlast_re, const float* dlast_im,
+                                 void* dw_re, void* dw_im, void* dgate0, void* dgate1,
+                                 float* dnu_log, float* dtheta_log,
+                                 float* dh0_re, float* dh0_im,
+                                 void* workspace, size_t workspace_bytes, sparc_stream_t stream) {
+  Plan pl;
+  if (sparc_status s = common_checks(d, 1, &pl, workspace, workspace_bytes)) return s;
+  const bool cplx = d->transition != SPARC_TRANSITION_REAL;
+  const bool relu = (d->flags & SPARC_FLAG_RELU_OUTPUT) != 0;
+  const bool p1 = d->transition == SPARC_TRANSITION_P1;
+  if (!gate0 || !w_re || !dy_re || !dw_re || !dgate0 || !chunk_state)
+    return fail(SPARC_EINVAL, "gate0, w_re, dy_re, dw_re, dgate0, chunk_state are required");
+  if (cplx && (!gate1 || !w_im || !dw_im || !dgate1)) return fail(SPARC_EINVAL, "complex transitions need gate1, w_im, dw_im, dgate1");
+  if (cplx && !relu && !dy_im) return fail(SPARC_EINVAL, "dy_im is required");
+  if (p1 && (!nu_log || !theta_log || !dnu_log || !dtheta_log)) return fail(SPARC_EINVAL, "P1 needs nu_log, theta_log, dnu_log, dtheta_log");
+  if (cplx && ((dh0_re == nullptr) != (dh0_im == nullptr))) return fail(SPARC_EINVAL, "dh0_re/dh0_im must both be given");
+  if (dh0_re && !h0_re) return fail(SPARC_EINVAL, "dh0 requested without h0");
+  const void* ptrs[] = {w_re, w_im, dy_re, relu ? nullptr : dy_im, dw_re, dw_im};
+  if (sparc_status s = check_io_ptrs(d, pl, ptrs, 6)) return s;
+  if (pl.gm == sparc::GATE_MODE) {
+    const void* gp[] = {gate0, gate1, dgate0, dgate1};
+    if (sparc_status s = check_io_ptrs(d, pl, gp, 4)) return s;
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (d->length == 0) {
+    // no steps: dh0 = dlast, parameter gradients are zero
+    const size_t bm = static_cast<size_t>(d->batch * d->modes) * 4;
+    if (dh0_re) {
+      if (dlast_re) { hipMemcpyAsync(dh0_re, dlast_re, bm, hipMemcpyDeviceToDevice, st); }
+      else hipLaunchKernelGGL(sparc::clear_u32_kernel, dim3((d->batch * d->modes + 255) / 256), dim3(256), 0, st,
+                              reinterpret_cast<uint32_t*>(dh0_re), d->batch * d->modes);
+      if (cplx) {
+        if (dlast_im) hipMemcpyAsync(dh0_im, dlast_im, bm, hipMemcpyDeviceToDevice, st);
+        else hipLaunchKernelGGL(sparc::clear_u32_kernel, dim3((d->batch * d->modes + 255) / 256), dim3(256), 0, st,
+                                reinterpret_cast<uint32_t*>(dh0_im), d->batch * d->modes);
+      }
+    }
+    if (p1) {
+      hipLaunchKernelGGL(sparc::clear_u32_kernel, dim3((d->modes + 255) / 256), dim3(256), 0, st,
+                         reinterpret_cast<uint32_t*>(dnu_log), d->modes);
+      hipLaunchKernelGGL(sparc::clear_u32_kernel, dim3((d->modes + 255) / 256), dim3(256), 0, st,
+                         reinterpret_cast<uint32_t*>(dtheta_log), d->modes);
+    }
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "%s", hipGetErrorString(e));
+  }
+  if (sparc_status s = clear_ws(pl, workspace, st)) return s;
+  sparc::ScanArgs a{};
+  a.B = static_cast<int>(d->batch);
+  a.T = static_cast<int>(d->length);
+  a.M = static_cast<int>(d->modes);
+  a.G = static_cast<int>(d->groups);
+  a.gs = static_cast<int>(d->modes / d->groups);
+  a.n_chunks = pl.n_chunks;
+  a.n_mblocks = pl.n_mblocks;
+  a.n_chains = pl.n_chains;
+  a.flags = static_cast<uint32_t>(d->flags);
+  a.spin_limit = 1u << 20;
+  a.g0 = gate0; a.g1 = gate1; a.nu_log = nu_log; a.theta_log = theta_log;
+  a.w_re = w_re; a.w_im = w_im; a.h0_re = h0_re; a.h0_im = h0_im; a.segpos = segment_pos;
+  a.chunk_state_in = chunk_state;
+  a.dy_re = dy_re; a.dy_im = dy_im; a.dlast_re = dlast_re; a.dlast_im = dlast_im;
+  a.dw_re = dw_re; a.dw_im = dw_im; a.dg0 = dgate0; a.dg1 = dgate1;
+  a.dh0_re = dh0_re; a.dh0_im = dh0_im;
+  fill_ws(a, pl, workspace);
+  launch(1, d, pl, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SPARC_EHIP, "scan backward launch: %s", hipGetErrorString(e));
+  // deterministic reductions of the per-tile partials
+  const int64_t rows = d->batch * d->length;
+  if (pl.gm == sparc::GATE_CROSS) {
+    const int per = pl.n_mblocks / static_cast<int>(d->groups);
+    const int64_t n = rows * d->groups;
+    const dim3 g(static_cast<unsigned>((n + 255) / 256));
+    if (d->gate_dtype == SPARC_BF16) {
+      hipLaunchKernelGGL(sparc::reduce_groups_kernel<sparc::bf16>, g, dim3(256), 0, st, a.part_g0, rows, pl.n_mblocks, static_cast<int>(d->groups), per, dgate0);
+      if (cplx) hipLaunchKernelGGL(sparc::reduce_groups_kernel<sparc::bf16>, g, dim3(256), 0, st, a.part_g1, rows, pl.n_mblocks, static_cast<int>(d->groups), per, dgate1);
+    } else {
+      hipLaunchKernelGGL(sparc::reduce_groups_kernel<float>, g, dim3(256), 0, st, a.part_g0, rows, pl.n_mblocks, static_cast<int>(d->groups), per, dgate0);
+      if (cplx) hipLaunchKernelGGL(sparc::reduce_groups_kernel<float>, g, dim3(256), 0, st, a.part_g1, rows, pl.n_mblocks, static_cast<int>(d->groups), per, dgate1);
+    }
+  }
+  if (p1) {
+    const int64_t prow = d->batch * pl.n_chunks;
+    if (sparc_status s = sparc_column_sum(prow, d->modes, a.part_nu, dnu_log, 0, stream)) return s;
+    if (sparc_status s = sparc_column_sum(prow, d->modes, a.part_theta, dtheta_log, 0, stream)) return s;
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail(SPARC_EHIP, "scan backward reductions: %s", hipGetErrorString(e));
+  return SPARC_OK;
+}
+
+int sparc_scan_workspace_error(const void* workspace, sparc_stream_t stream) {
+  uint32_t err = 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (hipMemcpyAsync(&err, static_cast<const uint32_t*>(workspace) + 1, 4, hipMemcpyDeviceToHost, st) != hipSuccess) return -1;
+  if (hipStreamSynchronize(st) != hipSuccess) return -1;
+  return err ? 1 : 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,135 @@
+"""CPU checks of the C ABI and the host logic: the library loads, exports
+every symbol include/sparc_hip.h declares, validates descriptors on the host
+(no GPU call is made for an invalid request), and the Python operators raise
+the reference's ValueErrors.  No compute call is made here."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import sparc_amd
+from sparc_amd import _lib, ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "sparc_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sparc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = header_symbols()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert sorted(_lib.EXPORTED_SYMBOLS) == declared
+    assert lib.sparc_version().startswith(b"sparc_hip")
+
+
+def _desc(**kw):
+    base = dict(batch=2, length=100, modes=256, groups=16, transition=1, io_dtype=1,
+                gate_dtype=1, flags=0)
+    base.update(kw)
+    return _lib.ScanDesc(**base)
+
+
+def test_workspace_and_chunk_queries():
+    lib = _lib.load()
+    d = _desc()
+    assert lib.sparc_scan_chunk_length(ctypes.byref(d)) == 64
+    assert lib.sparc_scan_chunk_count(ctypes.byref(d)) == 2
+    assert lib.sparc_scan_workspace_bytes(ctypes.byref(d), 0) > 0
+    assert lib.sparc_scan_workspace_bytes(ctypes.byref(d), 1) >= lib.sparc_scan_workspace_bytes(ctypes.byref(d), 0)
+    # cfg2 shape: 8 x 4096 x 16384 modes, 1024 gate groups
+    big = _desc(batch=8, length=4096, modes=16384, groups=1024)
+    assert lib.sparc_scan_chunk_count(ctypes.byref(big)) == 64
+    assert 0 < lib.sparc_scan_workspace_bytes(ctypes.byref(big), 1) < 1 << 30
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(groups=3), b"groups must divide"),
+    (dict(transition=7), b"unknown transition"),
+    (dict(io_dtype=5), b"io_dtype"),
+    (dict(transition=0, gate_dtype=1), b"P1 gates"),
+    (dict(gate_dtype=0), b"gate_dtype must equal"),
+    (dict(transition=3, flags=1), b"RELU_OUTPUT"),
+    (dict(batch=0), b"must be > 0"),
+    (dict(groups=256 // 3 * 0 + 64, modes=192), b"unsupported gate group"),
+])
+def test_invalid_descriptors_rejected_on_host(kw, msg):
+    lib = _lib.load()
+    d = _desc(**kw)
+    assert lib.sparc_scan_workspace_bytes(ctypes.byref(d), 0) == 0
+    st = lib.sparc_scan_forward(ctypes.byref(d), *([None] * 13), 0, None)
+    assert st == 1
+    assert msg in lib.sparc_last_error()
+
+
+def test_forward_requires_workspace():
+    lib = _lib.load()
+    d = _desc()
+    st = lib.sparc_scan_forward(ctypes.byref(d), *([None] * 12), None, 0, None)
+    assert st == 4 and b"workspace" in lib.sparc_last_error()
+
+
+def test_reference_value_errors():
+    eta = torch.zeros(2, 48)
+    nu = torch.zeros(8)
+    br = torch.zeros(2, 48, 8)
+    with pytest.raises(ValueError, match="chunk size must be 16, 32 or 64"):
+        ops.sparc_chunk_scan(eta, eta, nu, nu, br, br, chunk_size=40)
+    with pytest.raises(ValueError, match="chunk size must be 16, 32 or 64"):
+        ops.sparc_chunk_scan(eta, eta, nu, nu, br, br, chunk_size=32)  # 48 % 32
+    with pytest.raises(ValueError, match="mode block size"):
+        ops.sparc_chunk_scan(eta, eta, nu, nu, br, br, chunk_size=16, mode_block_size=100)
+    with pytest.raises(ValueError, match="backward chunk group must divide"):
+        ops.sparc_chunk_scan(eta, eta, nu, nu, br, br, chunk_size=16, backward_chunk_group=2)
+    eta64, br64 = torch.zeros(2, 64), torch.zeros(2, 64, 8)
+    with pytest.raises(ValueError, match="grouped replay and fused output"):
+        ops.sparc_chunk_scan(eta64, eta64, nu, nu, br64, br64, chunk_size=16,
+                             backward_chunk_group=2, fused_output_relu=True)
+    with pytest.raises(ValueError, match="real chunk scan expects"):
+        ops.real_chunk_scan(torch.zeros(2, 4, 3), torch.zeros(2, 4, 2))
+    with pytest.raises(ValueError, match="complex scan expects"):
+        ops.complex_scan(br, br, br, torch.zeros(2, 48, 4))
+    with pytest.raises(ValueError, match="block_size must be"):
+        ops.sparc_tiled_serial_scan(eta, eta, nu, nu, br, br, block_size=48)
+    with pytest.raises(ValueError, match="SPARC controls must be matching"):
+        ops.sparc_scan(eta, torch.zeros(2, 47), nu, nu, br, br)
+
+
+def test_module_surface_and_knobs():
+    m = sparc_amd.SPARCMixer(16)
+    names = {n for n, _ in m.named_parameters()}
+    assert names == {"nu_log", "theta_log", "phase_direction", "radial_direction",
+                     "write_log_gain", "energy_response", "write_phase_response",
+                     "write_radial_response"}
+    assert {n for n, _ in m.named_buffers()} == {"phase_amplitude", "radial_amplitude"}
+    with pytest.raises(ValueError):
+        sparc_amd.SPARCMixer(15)
+    with pytest.raises(ValueError):
+        m.set_tiled_training_block_size(100)
+    with pytest.raises(ValueError):
+        m.set_decode_backend("nope")
+    with pytest.raises(ValueError):
+        m.set_controller_projection_dtype("fp64")
+    m.set_scan_backend("bogus")
+    with pytest.raises(ValueError, match="unknown scan backend"):
+        m(torch.zeros(1, 4, 16))
+    for ok in ("auto", "chunk16", "fused_output_shared_sfu_chunk32", "framework_eager",
+               "associative_fp32", "tiled_serial", "affine_tile_s16_m64_w4"):
+        sparc_amd.sparc._validate_backend(ok)
+
+
+def test_cpu_tensors_fail_loudly():
+    """No CPU fallback: the HIP operators refuse host tensors."""
+    eta = torch.zeros(1, 16)
+    nu = torch.zeros(4)
+    br = torch.zeros(1, 16, 4)
+    with pytest.raises(RuntimeError, match="need GPU tensors"):
+        ops.sparc_scan(eta, eta, nu, nu, br, br)

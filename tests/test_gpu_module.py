@@ -1,0 +1,184 @@
+"""GPU parity of the drop-in SPARCMixer (HIP write prologue + P1 scan with the
+fused relu(cat) epilogue + HIP backward) and of the fused decode step,
+against the float64 oracle and the reference golden vectors."""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import sparc_amd
+from oracle import sparc_oracle as O
+from sparc_amd import control
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ["nu_log", "theta_log", "phase_direction", "radial_direction", "write_log_gain",
+         "write_phase_response", "write_radial_response"]
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "p1_eager_golden.npz")
+
+
+def rel_err(got, ref):
+    got, ref = got.detach().double().cpu(), ref.detach().double().cpu()
+    return (got - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
+
+
+def make_module(width, seed, active=True):
+    torch.manual_seed(seed)
+    m = sparc_amd.SPARCMixer(width)
+    if active:
+        g = torch.Generator().manual_seed(seed + 1)
+        with torch.no_grad():
+            m.phase_direction.copy_(0.5 * torch.randn(width + 1, generator=g) / math.sqrt(width))
+            m.radial_direction.copy_(0.5 * torch.randn(width + 1, generator=g) / math.sqrt(width))
+            m.write_phase_response.copy_(torch.randn(width // 2, generator=g))
+            m.write_radial_response.copy_(torch.randn(width // 2, generator=g))
+    return m
+
+
+def oracle_params(m, requires_grad=True):
+    return O.MixerParams(**{n: getattr(m, n).detach().double().cpu().clone().requires_grad_(requires_grad)
+                            for n in NAMES})
+
+
+def _masked_dy(p, x, dy):
+    """Zero the output gradient where the state is within rounding of 0, so
+    that the relu mask cannot differ between fp32 and fp64."""
+    with torch.no_grad():
+        eta, delta = O.controls(x, p.phase_direction, p.radial_direction)
+        wr, wi = O.write(x, eta, delta, p.nu_log, p.write_log_gain, p.write_phase_response,
+                         p.write_radial_response)
+        ar, ai = O.p1_transition(eta[..., None], delta[..., None], p.nu_log, p.theta_log)
+        (hr, hi), _ = O.complex_scan(ar, ai, wr, wi)
+        h = torch.cat((hr, hi), -1)
+        return dy * (h.abs() > 1e-3 * h.abs().max())
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("B,L,width", [(2, 256, 128), (2, 100, 64)])
+def test_mixer_forward_backward_parity(dtype, tol, B, L, width):
+    print(f"[case] mixer B={B} L={L} width={width} {dtype}", flush=True)
+    m = make_module(width, seed=7).cuda()
+    g = torch.Generator().manual_seed(3)
+    x64 = torch.randn(B, L, width, generator=g, dtype=torch.float64)
+    x_in = x64.to(dtype)
+    p = oracle_params(m)
+    dy = _masked_dy(p, x_in.double(), torch.randn(B, L, width, generator=g, dtype=torch.float64))
+    dl = (torch.randn(B, width // 2, generator=g, dtype=torch.float64),
+          torch.randn(B, width // 2, generator=g, dtype=torch.float64))
+    # GPU
+    x = x_in.cuda().requires_grad_()
+    y, cache = m(x, return_cache=True)
+    assert y.dtype == dtype and y.shape == (B, L, width)
+    loss = (y.float() * dy.cuda().float()).sum() + (cache[0] * dl[0].cuda().float()).sum() \
+        + (cache[1] * dl[1].cuda().float()).sum()
+    params = [getattr(m, n) for n in NAMES]
+    grads = torch.autograd.grad(loss, [x] + params)
+    # oracle
+    xo = x_in.double().clone().requires_grad_()
+    yo, lasto = O.mixer_forward(p, xo, return_cache=True)
+    lo = (yo * dy).sum() + (lasto[0] * dl[0]).sum() + (lasto[1] * dl[1]).sum()
+    grads_o = torch.autograd.grad(lo, [xo] + [getattr(p, n) for n in NAMES])
+    assert rel_err(y, yo) <= tol
+    assert rel_err(cache[0], lasto[0]) <= tol and rel_err(cache[1], lasto[1]) <= tol
+    for name, a, b in zip(["x"] + NAMES, grads, grads_o):
+        e = rel_err(a, b)
+        assert e <= tol, f"grad {name}: {e:.3g}"
+
+
+def test_mixer_matches_reference_golden():
+    """The HIP module on the reference's own golden inputs (fp32 I/O)."""
+    print("[case] golden", flush=True)
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        gd = {k: torch.from_numpy(z[k]) for k in z.files}
+    width = gd["x"].shape[-1]
+    m = sparc_amd.SPARCMixer(width).cuda()
+    with torch.no_grad():
+        for n in NAMES:
+            getattr(m, n).copy_(gd[n].float())
+    x = gd["x"].float().cuda().requires_grad_()
+    y, cache = m(x, return_cache=True)
+    loss = (y * gd["dy"].float().cuda()).sum() + (cache[0] * gd["dlast_re"].float().cuda()).sum() \
+        + (cache[1] * gd["dlast_im"].float().cuda()).sum()
+    grads = torch.autograd.grad(loss, [x] + [getattr(m, n) for n in NAMES])
+    assert rel_err(y, gd["y"]) <= 1e-4
+    assert rel_err(cache[0], gd["last_re"]) <= 1e-4 and rel_err(cache[1], gd["last_im"]) <= 1e-4
+    assert rel_err(grads[0], gd["grad_x"]) <= 1e-4
+    for n, gr in zip(NAMES, grads[1:]):
+        assert rel_err(gr, gd["grad_" + n]) <= 1e-4, n
+    # decode continues from the cache
+    m.prepare_inference()
+    state = (gd["last_re"].float().cuda(), gd["last_im"].float().cuda())
+    for t in range(gd["decode_x"].shape[0]):
+        yt, state = m.step(gd["decode_x"][t].float().cuda(), state, segment_pos=None)
+        assert rel_err(yt, gd["decode_y"][t]) <= 1e-4
+        assert rel_err(state[0], gd["decode_re"][t]) <= 1e-4
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_write_prologue_parity(dtype, tol):
+    print(f"[case] write {dtype}", flush=True)
+    m = make_module(96, seed=5).cuda()
+    g = torch.Generator().manual_seed(8)
+    x_in = torch.randn(3, 50, 96, generator=g).to(dtype)
+    p = oracle_params(m)
+    eta64 = O.LOG16 * torch.tanh(torch.randn(3, 50, generator=g, dtype=torch.float64))
+    delta64 = O.HALF_PI * torch.tanh(torch.randn(3, 50, generator=g, dtype=torch.float64))
+    dwr = torch.randn(3, 50, 48, generator=g).to(dtype)
+    dwi = torch.randn(3, 50, 48, generator=g).to(dtype)
+    x = x_in.cuda().requires_grad_()
+    eta = eta64.float().cuda().requires_grad_()
+    delta = delta64.float().cuda().requires_grad_()
+    params = [m.nu_log, m.write_log_gain, m.write_phase_response, m.write_radial_response]
+    wr, wi = control.latest_sparc_write(x, eta, delta, *params)
+    loss = (wr.float() * dwr.float().cuda()).sum() + (wi.float() * dwi.float().cuda()).sum()
+    grads = torch.autograd.grad(loss, [x, eta, delta] + params)
+    xo = x_in.double().clone().requires_grad_()
+    eo, do = eta64.float().double().clone().requires_grad_(), delta64.float().double().clone().requires_grad_()
+    po = [p.nu_log, p.write_log_gain, p.write_phase_response, p.write_radial_response]
+    wro, wio = O.write(xo, eo, do, *po)
+    lo = (wro * dwr.double()).sum() + (wio * dwi.double()).sum()
+    grads_o = torch.autograd.grad(lo, [xo, eo, do] + po)
+    assert rel_err(wr, wro) <= tol and rel_err(wi, wio) <= tol
+    for i, (a, b) in enumerate(zip(grads, grads_o)):
+        assert rel_err(a, b) <= tol, i
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_decode_matches_sequence_and_oracle(dtype, tol):
+    print(f"[case] decode {dtype}", flush=True)
+    width, B = 256, 4
+    m = make_module(width, seed=11).cuda()
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(B, 40, width, generator=g).to(dtype)
+    p = oracle_params(m, requires_grad=False)
+    with torch.no_grad():
+        _, cache = m(x[:, :32].cuda(), return_cache=True)
+        m.prepare_inference()
+        state = cache
+        ys = []
+        for t in range(32, 40):
+            yt, state = m.step(x[:, t].cuda(), state, segment_pos=None)
+            ys.append(yt)
+    y_full, last_full = O.mixer_forward(p, x.double(), return_cache=True)
+    assert rel_err(torch.stack(ys, 1), y_full[:, 32:]) <= tol
+    assert rel_err(state[0], last_full[0]) <= tol and rel_err(state[1], last_full[1]) <= tol
+
+
+def test_decode_in_place_state():
+    print("[case] decode in place", flush=True)
+    m = make_module(128, seed=13).cuda()
+    m.decode_in_place = True
+    m.prepare_inference()
+    g = torch.Generator().manual_seed(1)
+    sr = (0.1 * torch.randn(8, 64, generator=g)).cuda()
+    si = (0.1 * torch.randn(8, 64, generator=g)).cuda()
+    ref_r, ref_i = sr.clone(), si.clone()
+    x = torch.randn(8, 128, generator=g).to(torch.bfloat16).cuda()
+    m.decode_in_place = False
+    y_ref, (nr, ni) = m.step(x, (ref_r, ref_i), None)
+    m.decode_in_place = True
+    y, (r2, i2) = m.step(x, (sr, si), None)
+    assert r2.data_ptr() == sr.data_ptr()
+    assert torch.equal(y, y_ref) and torch.equal(sr, nr) and torch.equal(si, ni)
