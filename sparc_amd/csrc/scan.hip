@@ -1302,6 +1302,7 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, con
                                 void* workspace, size_t workspace_bytes, sparc_stream_t stream) {
   Plan pl;
   if (sparc_status s = common_checks(d, 0, &pl, workspace, workspace_bytes)) return s;
+  if (d->length == 0) return SPARC_OK;  // nothing to read or write
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
   const bool relu = (d->flags & SPARC_FLAG_RELU_OUTPUT) != 0;
   if (!gate0 || !w_re || !y_re || !chunk_state) return fail(SPARC_EINVAL, "gate0, w_re, y_re, chunk_state are required");
@@ -1316,7 +1317,6 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, con
     if (sparc_status s = check_io_ptrs(d, pl, gp, 2)) return s;
   }
   if (!aligned(chunk_state, 8 * pl.V)) return fail(SPARC_EINVAL, "chunk_state must be %d-byte aligned", 8 * pl.V);
-  if (d->length == 0) return SPARC_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (sparc_status s = clear_ws(pl, workspace, st)) return s;
   sparc::ScanArgs a{};
@@ -1340,6 +1340,27 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, con
   return SPARC_OK;
 }
 
+// T == 0: no step touches the state, so dh0 = dlast and the parameter
+// gradients are zero.
+static sparc_status empty_backward(const sparc_scan_desc* d, const float* dlast_re, const float* dlast_im,
+                                   float* dnu_log, float* dtheta_log, float* dh0_re, float* dh0_im,
+                                   hipStream_t st) {
+  const int64_t bm = d->batch * d->modes;
+  const dim3 gb(static_cast<unsigned>((bm + 255) / 256)), gm(static_cast<unsigned>((d->modes + 255) / 256));
+  if (dh0_re) {
+    if (dlast_re) hipMemcpyAsync(dh0_re, dlast_re, bm * 4, hipMemcpyDeviceToDevice, st);
+    else hipLaunchKernelGGL(sparc::clear_u32_kernel, gb, dim3(256), 0, st, reinterpret_cast<uint32_t*>(dh0_re), bm);
+  }
+  if (dh0_im) {
+    if (dlast_im) hipMemcpyAsync(dh0_im, dlast_im, bm * 4, hipMemcpyDeviceToDevice, st);
+    else hipLaunchKernelGGL(sparc::clear_u32_kernel, gb, dim3(256), 0, st, reinterpret_cast<uint32_t*>(dh0_im), bm);
+  }
+  if (dnu_log) hipLaunchKernelGGL(sparc::clear_u32_kernel, gm, dim3(256), 0, st, reinterpret_cast<uint32_t*>(dnu_log), d->modes);
+  if (dtheta_log) hipLaunchKernelGGL(sparc::clear_u32_kernel, gm, dim3(256), 0, st, reinterpret_cast<uint32_t*>(dtheta_log), d->modes);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "empty backward: %s", hipGetErrorString(e));
+}
+
 sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, const void* gate1,
                                  const float* nu_log, const float* theta_log,
                                  const void* w_re, const void* w_im,
@@ -1356,6 +1377,12 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
   const bool relu = (d->flags & SPARC_FLAG_RELU_OUTPUT) != 0;
   const bool p1 = d->transition == SPARC_TRANSITION_P1;
+  if (d->length == 0) {
+    if (p1 && (!dnu_log || !dtheta_log)) return fail(SPARC_EINVAL, "P1 needs dnu_log, dtheta_log");
+    if (cplx && ((dh0_re == nullptr) != (dh0_im == nullptr))) return fail(SPARC_EINVAL, "dh0_re/dh0_im must both be given");
+    return empty_backward(d, dlast_re, dlast_im, dnu_log, dtheta_log, dh0_re, dh0_im,
+                          reinterpret_cast<hipStream_t>(stream));
+  }
   if (!gate0 || !w_re || !dy_re || !dw_re || !dgate0 || !chunk_state)
     return fail(SPARC_EINVAL, "gate0, w_re, dy_re, dw_re, dgate0, chunk_state are required");
   if (cplx && (!gate1 || !w_im || !dw_im || !dgate1)) return fail(SPARC_EINVAL, "complex transitions need gate1, w_im, dw_im, dgate1");
@@ -1370,28 +1397,6 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
     if (sparc_status s = check_io_ptrs(d, pl, gp, 4)) return s;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (d->length == 0) {
-    // no steps: dh0 = dlast, parameter gradients are zero
-    const size_t bm = static_cast<size_t>(d->batch * d->modes) * 4;
-    if (dh0_re) {
-      if (dlast_re) { hipMemcpyAsync(dh0_re, dlast_re, bm, hipMemcpyDeviceToDevice, st); }
-      else hipLaunchKernelGGL(sparc::clear_u32_kernel, dim3((d->batch * d->modes + 255) / 256), dim3(256), 0, st,
-                              reinterpret_cast<uint32_t*>(dh0_re), d->batch * d->modes);
-      if (cplx) {
-        if (dlast_im) hipMemcpyAsync(dh0_im, dlast_im, bm, hipMemcpyDeviceToDevice, st);
-        else hipLaunchKernelGGL(sparc::clear_u32_kernel, dim3((d->batch * d->modes + 255) / 256), dim3(256), 0, st,
-                                reinterpret_cast<uint32_t*>(dh0_im), d->batch * d->modes);
-      }
-    }
-    if (p1) {
-      hipLaunchKernelGGL(sparc::clear_u32_kernel, dim3((d->modes + 255) / 256), dim3(256), 0, st,
-                         reinterpret_cast<uint32_t*>(dnu_log), d->modes);
-      hipLaunchKernelGGL(sparc::clear_u32_kernel, dim3((d->modes + 255) / 256), dim3(256), 0, st,
-                         reinterpret_cast<uint32_t*>(dtheta_log), d->modes);
-    }
-    hipError_t e = hipGetLastError();
-    return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "%s", hipGetErrorString(e));
-  }
   if (sparc_status s = clear_ws(pl, workspace, st)) return s;
   sparc::ScanArgs a{};
   a.B = static_cast<int>(d->batch);

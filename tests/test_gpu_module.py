@@ -42,9 +42,10 @@ def oracle_params(m, requires_grad=True):
                             for n in NAMES})
 
 
-def _masked_dy(p, x, dy):
-    """Zero the output gradient where the state is within rounding of 0, so
-    that the relu mask cannot differ between fp32 and fp64."""
+def _masked_dy(p, x, dy, band):
+    """Zero the output gradient where |state| < band * max|state|: there the
+    relu mask is ambiguous under the I/O rounding (bf16 writes move states by
+    ~2^-9 relative), so it may legitimately differ from the float64 oracle."""
     with torch.no_grad():
         eta, delta = O.controls(x, p.phase_direction, p.radial_direction)
         wr, wi = O.write(x, eta, delta, p.nu_log, p.write_log_gain, p.write_phase_response,
@@ -52,7 +53,7 @@ def _masked_dy(p, x, dy):
         ar, ai = O.p1_transition(eta[..., None], delta[..., None], p.nu_log, p.theta_log)
         (hr, hi), _ = O.complex_scan(ar, ai, wr, wi)
         h = torch.cat((hr, hi), -1)
-        return dy * (h.abs() > 1e-3 * h.abs().max())
+        return dy * (h.abs() > band * h.abs().max())
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
@@ -64,7 +65,8 @@ def test_mixer_forward_backward_parity(dtype, tol, B, L, width):
     x64 = torch.randn(B, L, width, generator=g, dtype=torch.float64)
     x_in = x64.to(dtype)
     p = oracle_params(m)
-    dy = _masked_dy(p, x_in.double(), torch.randn(B, L, width, generator=g, dtype=torch.float64))
+    dy = _masked_dy(p, x_in.double(), torch.randn(B, L, width, generator=g, dtype=torch.float64),
+                    band=1e-3 if dtype == torch.float32 else 2e-2)
     dl = (torch.randn(B, width // 2, generator=g, dtype=torch.float64),
           torch.randn(B, width // 2, generator=g, dtype=torch.float64))
     # GPU

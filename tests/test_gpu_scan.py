@@ -145,15 +145,17 @@ def check_case(case, tol=None):
     tol = tol or TOL[case["dtype"]]
     mask = None
     if case["relu"]:
-        # elements whose state is within rounding of 0 get no output gradient,
-        # so the relu mask cannot differ between fp32 and fp64 there
+        # elements whose state is within the I/O rounding band of 0 get no
+        # output gradient: there the relu mask may legitimately differ from
+        # the float64 oracle (bf16 moves states by ~2^-9 relative)
         with torch.no_grad():
             y_o, _ = O.grouped_scan_forward(
                 case["transition"], case["g0"].double(), case["g1"].double(), case["w_re"].double(),
                 case["w_im"].double(), case["nu_log"].double(), case["theta_log"].double(),
                 relu_output=False)
             h = torch.cat(y_o, -1)
-            mask = (h.abs() > 1e-3 * h.abs().max()).to(torch.float64)
+            band = 1e-3 if case["dtype"] == torch.float32 else 2e-2
+            mask = (h.abs() > band * h.abs().max()).to(torch.float64)
         case = dict(case)
         case["dy_re"] = (case["dy_re"].double() * mask).to(case["dtype"])
     y, last, grads = run_gpu(case)

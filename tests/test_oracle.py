@@ -10,7 +10,15 @@ import torch
 
 from oracle import sparc_oracle as O
 
-torch.set_default_dtype(torch.float64)
+
+
+@pytest.fixture(autouse=True)
+def _float64_default():
+    """float64 by default inside this module only."""
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
 
 
 def _rand_complex_inputs(B=2, T=37, M=5, seed=0):
