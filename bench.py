@@ -64,7 +64,8 @@ def bench_scan(args, dev):
     B, T, D, N = 8, 4096, 1024, 16
     M, G = D * N, D
     r, phi, w_re, w_im, dy_re, dy_im = scan_case(B, T, M, G, dev)
-    d = _lib.ScanDesc(B, T, M, G, _lib.TRANSITIONS["polar"], _lib.SPARC_BF16, _lib.SPARC_BF16, 0)
+    d = _lib.ScanDesc(B, T, M, G, _lib.TRANSITIONS["polar"], _lib.SPARC_BF16, _lib.SPARC_BF16,
+                      _lib.ALGO_FLAGS[args.algo])
     n_chunks = lib.sparc_scan_chunk_count(ctypes.byref(d))
     y_re, y_im = torch.empty_like(w_re), torch.empty_like(w_im)
     cs = torch.empty(B, n_chunks, M, 2, device=dev, dtype=torch.float32)
@@ -222,6 +223,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--algo", default="auto", choices=["auto", "chain", "lookback"],
+                    help="scan algorithm (auto picks chain-serial at this shape)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="first copy 1 GiB device-to-device (a kernel of known traffic, "
+                         "to calibrate the FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build's scan runs on a single MI355X "
@@ -232,12 +238,18 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda", 0)
+    if args.copy_probe:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        del src, dst
     res = bench_scan(args, dev)
     dec = None if args.no_decode else bench_decode(args, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
     roof = {
         "bound": "hbm",
-        "kernel": "scan_bwd_kernel<POLAR,bf16,V=2,GATE_LANE> (+ workspace clear)",
+        "kernel": f"backward scan, algorithm={args.algo} (polar, bf16, V=2, lane-shared gates)",
         "achieved": round(res["bwd_gbs"], 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",

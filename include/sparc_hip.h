@@ -61,7 +61,15 @@ enum {
   SPARC_FLAG_RELU_OUTPUT = 1,
   /* the transition of step 0 is replaced by 0 (drops h0).  A non-NULL
    * segment_pos takes precedence: steps with segment_pos[b,t] == 0 reset. */
-  SPARC_FLAG_RESET_FIRST = 2
+  SPARC_FLAG_RESET_FIRST = 2,
+  /* Algorithm selection (default: automatic from the shape).  LOOKBACK:
+   * every (chain, chunk) tile is its own workgroup and chunk carries pass
+   * between workgroups (decoupled look-back); parallel over T, for few
+   * (batch row, mode block) chains.  CHAIN: one workgroup walks a whole
+   * chain, carries stay on the CU; for many chains.  Same results up to
+   * float rounding; the saved chunk states of either feed either backward. */
+  SPARC_FLAG_ALGO_LOOKBACK = 4,
+  SPARC_FLAG_ALGO_CHAIN = 8
 };
 
 typedef struct sparc_scan_desc {

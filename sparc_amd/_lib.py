@@ -18,6 +18,9 @@ SPARC_F32, SPARC_BF16 = 0, 1
 TRANSITIONS = {"p1": 0, "polar": 1, "cartesian": 2, "real": 3}
 FLAG_RELU_OUTPUT = 1
 FLAG_RESET_FIRST = 2
+FLAG_ALGO_LOOKBACK = 4
+FLAG_ALGO_CHAIN = 8
+ALGO_FLAGS = {"auto": 0, "lookback": FLAG_ALGO_LOOKBACK, "chain": FLAG_ALGO_CHAIN}
 
 # every symbol declared in include/sparc_hip.h
 EXPORTED_SYMBOLS = (

@@ -1062,6 +1062,1170 @@ scan_bwd_kernel(ScanArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Chain-serial kernels: one workgroup owns one chain (b, mode block) and walks
+// its chunks in order, so the carry between chunks never leaves the CU.  The
+// loads of the next chunk are issued before the current chunk is scanned and
+// stored (two register buffers).  No tickets, flags or look-back: used when
+// there are enough chains to fill the GPU.
+// ---------------------------------------------------------------------------
+template <int TR, typename IO, int V, int GM, int S>
+struct SubChunk {
+  using TL = TransitionLane<TR, IO, V, GM>;
+  using RawT = typename Raw<IO, V>::T;
+  static constexpr bool CPLX = TL::CPLX;
+  static constexpr int GV = TL::GV;
+  RawT wr[S], wi[S];
+  float g0[S][GV], g1[S][GV];
+
+  // loads steps [t0, t0 + S) of row b for the lane's modes
+  __device__ __forceinline__ void load(const ScanArgs& p, const TL& tl, int b, int t0, int m0, bool lane_ok) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int t = t0 + s;
+      if (lane_ok && t < p.T) {
+        const int64_t idx = (static_cast<int64_t>(b) * p.T + t) * p.M + m0;
+        wr[s] = load_raw<IO, V>(p.w_re, idx);
+        if constexpr (CPLX) wi[s] = load_raw<IO, V>(p.w_im, idx);
+        tl.load_gates(p, tl.gate_index(p, b, t, m0), g0[s], g1[s]);
+      } else {
+        float z[V] = {};
+        wr[s] = pack<IO, V>(z);
+        wi[s] = wr[s];
+#pragma unroll
+        for (int v = 0; v < GV; ++v) { g0[s][v] = 0.0f; g1[s][v] = 0.0f; }
+      }
+    }
+  }
+};
+
+// transitions of S steps starting at t0 (identity past T, zero at resets)
+template <class TL, int S>
+__device__ __forceinline__ void make_transitions(const ScanArgs& p, const TL& tl, int b, int t0, bool lane_ok,
+                                                 bool reset_first, const float (&g0)[S][TL::GV],
+                                                 const float (&g1)[S][TL::GV], float (&a_r)[S][TL::AV],
+                                                 float (&a_i)[S][TL::AV], bool (&rst)[S]) {
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int t = t0 + s;
+    tl.transition(g0[s], g1[s], a_r[s], a_i[s]);
+    if (p.segpos) rst[s] = (t < p.T) && p.segpos[static_cast<int64_t>(b) * p.T + t] == 0;
+    else rst[s] = reset_first && t == 0;
+    const bool ident = !(lane_ok && t < p.T);
+#pragma unroll
+    for (int v = 0; v < TL::AV; ++v) {
+      if (ident) { a_r[s][v] = 1.0f; a_i[s][v] = 0.0f; }
+      if (rst[s]) { a_r[s][v] = 0.0f; a_i[s][v] = 0.0f; }
+    }
+  }
+}
+
+// (P, Q) of S steps from a zero state, written to lds[NQ][V][64]
+template <bool CPLX, typename IO, int V, int AV, int S, int NQ>
+__device__ __forceinline__ void local_maps(const typename Raw<IO, V>::T (&wr)[S], const typename Raw<IO, V>::T (&wi)[S],
+                                           const float (&a_r)[S][AV], const float (&a_i)[S][AV],
+                                           float (&lds)[NQ][V][64], int lane) {
+  float Pr[AV], Pi[AV], Qr[V], Qi[V];
+#pragma unroll
+  for (int v = 0; v < AV; ++v) { Pr[v] = 1.0f; Pi[v] = 0.0f; }
+#pragma unroll
+  for (int v = 0; v < V; ++v) { Qr[v] = 0.0f; Qi[v] = 0.0f; }
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    float xr[V], xi[V];
+    unpack<IO, V>(wr[s], xr);
+    if constexpr (CPLX) unpack<IO, V>(wi[s], xi);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int av = AV == 1 ? 0 : v;
+      if constexpr (CPLX) {
+        const float nr = a_r[s][av] * Qr[v] - a_i[s][av] * Qi[v] + xr[v];
+        const float ni = a_i[s][av] * Qr[v] + a_r[s][av] * Qi[v] + xi[v];
+        Qr[v] = nr;
+        Qi[v] = ni;
+      } else {
+        Qr[v] = a_r[s][av] * Qr[v] + xr[v];
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < AV; ++v) {
+      if constexpr (CPLX) {
+        float nr, ni;
+        cmul(a_r[s][v], a_i[s][v], Pr[v], Pi[v], nr, ni);
+        Pr[v] = nr;
+        Pi[v] = ni;
+      } else {
+        Pr[v] = a_r[s][v] * Pr[v];
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int av = AV == 1 ? 0 : v;
+    lds[0][v][lane] = Pr[av];
+    if constexpr (CPLX) {
+      lds[1][v][lane] = Pi[av];
+      lds[2][v][lane] = Qr[v];
+      lds[3][v][lane] = Qi[v];
+    } else {
+      lds[1][v][lane] = Qr[v];
+    }
+  }
+}
+
+// x <- P x + Q with (P, Q) from lds[NQ][V][64]
+template <bool CPLX, int V, int NQ>
+__device__ __forceinline__ void apply_map(const float (&lds)[NQ][V][64], int lane, float (&xr)[V], float (&xi)[V]) {
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    if constexpr (CPLX) {
+      const float pr = lds[0][v][lane], pi = lds[1][v][lane];
+      const float qr = lds[2][v][lane], qi = lds[3][v][lane];
+      float nr, ni;
+      cmul(pr, pi, xr[v], xi[v], nr, ni);
+      xr[v] = nr + qr;
+      xi[v] = ni + qi;
+    } else {
+      xr[v] = lds[0][v][lane] * xr[v] + lds[1][v][lane];
+    }
+  }
+}
+
+template <int TR, typename IO, int V, int GM, int S, int NW>
+__global__ void __launch_bounds__(NW * 64)
+chain_fwd_kernel(ScanArgs p) {
+  using SC = SubChunk<TR, IO, V, GM, S>;
+  using TL = typename SC::TL;
+  constexpr bool CPLX = TL::CPLX;
+  constexpr int AV = TL::AV;
+  constexpr int C = S * NW;
+  constexpr int MB = 64 * V;
+  constexpr int NQ = CPLX ? 4 : 2;
+  constexpr int NH = CPLX ? 2 : 1;
+  __shared__ float s_pq[2][NW][NQ][V][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int chain = blockIdx.x;
+  const int b = chain / p.n_mblocks;
+  const int mb = chain - b * p.n_mblocks;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < p.M;
+  const bool relu_out = CPLX && (p.flags & SPARC_FLAG_RELU_OUTPUT);
+  const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
+  TL tl;
+  tl.init(p, m0, lane_ok);
+
+  float cr[V], ci[V];  // state entering the current chunk
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+    cr[v] = (p.h0_re && lane_ok) ? p.h0_re[hi] : 0.0f;
+    ci[v] = (CPLX && p.h0_im && lane_ok) ? p.h0_im[hi] : 0.0f;
+  }
+  SC buf[2];
+  buf[0].load(p, tl, b, wave * S, m0, lane_ok);
+  for (int c0 = 0; c0 < p.n_chunks; c0 += 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = c0 + h;
+      if (c >= p.n_chunks) break;
+      const int t0 = c * C + wave * S;
+      if (c + 1 < p.n_chunks) buf[1 - h].load(p, tl, b, t0 + C, m0, lane_ok);
+      float a_r[S][AV], a_i[S][AV];
+      bool rst[S];
+      make_transitions<TL, S>(p, tl, b, t0, lane_ok, reset_first, buf[h].g0, buf[h].g1, a_r, a_i, rst);
+      local_maps<CPLX, IO, V, AV, S, NQ>(buf[h].wr, buf[h].wi, a_r, a_i, s_pq[h][wave], lane);
+      __syncthreads();
+      // start state of this wave, and the state after the chunk (same arithmetic in every wave)
+      float sr[V], si[V];
+#pragma unroll
+      for (int k = 0; k < NW; ++k) {
+        if (k == wave) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) { sr[v] = cr[v]; si[v] = ci[v]; }
+        }
+        apply_map<CPLX, V, NQ>(s_pq[h][k], lane, cr, ci);
+      }
+      if (wave == 0 && lane_ok) {
+        float hv[V * NH];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) { hv[2 * v] = cr[v]; hv[2 * v + 1] = ci[v]; }
+          else hv[v] = cr[v];
+        }
+        float* dst = p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + c) * p.M + m0) * NH;
+#pragma unroll
+        for (int i = 0; i < V * NH; ++i) dst[i] = hv[i];
+      }
+      // replay and store
+      if (lane_ok) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const int t = t0 + s;
+          float xr[V], xi[V];
+          unpack<IO, V>(buf[h].wr[s], xr);
+          if constexpr (CPLX) unpack<IO, V>(buf[h].wi[s], xi);
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const int av = AV == 1 ? 0 : v;
+            if constexpr (CPLX) {
+              const float nr = a_r[s][av] * sr[v] - a_i[s][av] * si[v] + xr[v];
+              const float ni = a_i[s][av] * sr[v] + a_r[s][av] * si[v] + xi[v];
+              sr[v] = nr;
+              si[v] = ni;
+            } else {
+              sr[v] = a_r[s][av] * sr[v] + xr[v];
+            }
+          }
+          if (t < p.T) {
+            const int64_t row = static_cast<int64_t>(b) * p.T + t;
+            if (relu_out) {
+              float rr[V], ri[V];
+#pragma unroll
+              for (int v = 0; v < V; ++v) { rr[v] = fmaxf(sr[v], 0.0f); ri[v] = fmaxf(si[v], 0.0f); }
+              store_raw<IO, V>(p.y_re, row * 2 * p.M + m0, pack<IO, V>(rr));
+              store_raw<IO, V>(p.y_re, row * 2 * p.M + p.M + m0, pack<IO, V>(ri));
+            } else {
+              store_raw<IO, V>(p.y_re, row * p.M + m0, pack<IO, V>(sr));
+              if constexpr (CPLX) store_raw<IO, V>(p.y_im, row * p.M + m0, pack<IO, V>(si));
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int TR, typename IO, int V, int GM, int S, int NW>
+__global__ void __launch_bounds__(NW * 64)
+chain_bwd_kernel(ScanArgs p) {
+  using SC = SubChunk<TR, IO, V, GM, S>;
+  using TL = typename SC::TL;
+  using GT = typename TL::GT;
+  using RawT = typename Raw<IO, V>::T;
+  constexpr bool CPLX = TL::CPLX;
+  constexpr bool P1 = TR == TR_P1;
+  constexpr int AV = TL::AV;
+  constexpr int GV = TL::GV;
+  constexpr int C = S * NW;
+  constexpr int MB = 64 * V;
+  constexpr int NQ = CPLX ? 4 : 2;
+  constexpr int NH = CPLX ? 2 : 1;
+  __shared__ float s_fq[NW][NQ][V][64];   // forward sub-chunk maps
+  __shared__ float s_rq[NW][NQ][V][64];   // reverse sub-chunk maps
+  __shared__ float s_par[P1 ? NW : 1][2][V][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int chain = blockIdx.x;
+  const int b = chain / p.n_mblocks;
+  const int mb = chain - b * p.n_mblocks;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < p.M;
+  const bool relu_out = CPLX && (p.flags & SPARC_FLAG_RELU_OUTPUT);
+  const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
+  const int glanes = (GM == GATE_LANE) ? (p.gs / V) : 1;
+  TL tl;
+  tl.init(p, m0, lane_ok);
+
+  float xr_c[V], xi_c[V];  // adjoint entering the current chunk from the future
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+    xr_c[v] = (p.dlast_re && lane_ok) ? p.dlast_re[hi] : 0.0f;
+    xi_c[v] = (CPLX && p.dlast_im && lane_ok) ? p.dlast_im[hi] : 0.0f;
+  }
+  float acc_nu[P1 ? V : 1], acc_th[P1 ? V : 1];
+#pragma unroll
+  for (int v = 0; v < (P1 ? V : 1); ++v) { acc_nu[v] = 0.0f; acc_th[v] = 0.0f; }
+
+  SC buf[2];
+  RawT dr[2][S], di[2][S];
+  float hs[2][V * NH];  // state entering the chunk (saved by the forward)
+  auto load_all = [&](int hb, int c) {
+    const int t0 = c * C + wave * S;
+    buf[hb].load(p, tl, b, t0, m0, lane_ok);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int t = t0 + s;
+      if (lane_ok && t < p.T) {
+        const int64_t row = static_cast<int64_t>(b) * p.T + t;
+        if (relu_out) {
+          dr[hb][s] = load_raw<IO, V>(p.dy_re, row * 2 * p.M + m0);
+          di[hb][s] = load_raw<IO, V>(p.dy_re, row * 2 * p.M + p.M + m0);
+        } else {
+          dr[hb][s] = load_raw<IO, V>(p.dy_re, row * p.M + m0);
+          if constexpr (CPLX) di[hb][s] = load_raw<IO, V>(p.dy_im, row * p.M + m0);
+        }
+      } else {
+        float z[V] = {};
+        dr[hb][s] = pack<IO, V>(z);
+        di[hb][s] = dr[hb][s];
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      if (c == 0) {
+        const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+        hs[hb][v * NH] = (p.h0_re && lane_ok) ? p.h0_re[hi] : 0.0f;
+        if constexpr (CPLX) hs[hb][v * NH + 1] = (p.h0_im && lane_ok) ? p.h0_im[hi] : 0.0f;
+      } else {
+        const int64_t ci_ = ((static_cast<int64_t>(b) * p.n_chunks + c - 1) * p.M + m0 + v) * NH;
+        hs[hb][v * NH] = lane_ok ? p.chunk_state_in[ci_] : 0.0f;
+        if constexpr (CPLX) hs[hb][v * NH + 1] = lane_ok ? p.chunk_state_in[ci_ + 1] : 0.0f;
+      }
+    }
+  };
+
+  load_all(0, p.n_chunks - 1);
+  for (int c0 = p.n_chunks - 1; c0 >= 0; c0 -= 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = c0 - h;
+      if (c < 0) break;
+      const int t0 = c * C + wave * S;
+      if (c - 1 >= 0) load_all(1 - h, c - 1);
+      float a_r[S][AV], a_i[S][AV];
+      bool rst[S];
+      make_transitions<TL, S>(p, tl, b, t0, lane_ok, reset_first, buf[h].g0, buf[h].g1, a_r, a_i, rst);
+      local_maps<CPLX, IO, V, AV, S, NQ>(buf[h].wr, buf[h].wi, a_r, a_i, s_fq[wave], lane);
+      __syncthreads();  // B1: forward maps visible
+      float hr[V], hi[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) { hr[v] = hs[h][v * NH]; hi[v] = CPLX ? hs[h][v * NH + 1] : 0.0f; }
+      for (int k = 0; k < wave; ++k) apply_map<CPLX, V, NQ>(s_fq[k], lane, hr, hi);
+      // recompute h_{t-1}; effective output gradient (relu mask from the recomputed state)
+      float hpr[S][V], hpi[S][V], dyr[S][V], dyi[S][V];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        float xw_r[V], xw_i[V], gr[V], gi[V];
+        unpack<IO, V>(buf[h].wr[s], xw_r);
+        unpack<IO, V>(dr[h][s], gr);
+        if constexpr (CPLX) {
+          unpack<IO, V>(buf[h].wi[s], xw_i);
+          unpack<IO, V>(di[h][s], gi);
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          hpr[s][v] = hr[v];
+          hpi[s][v] = CPLX ? hi[v] : 0.0f;
+          const int av = AV == 1 ? 0 : v;
+          if constexpr (CPLX) {
+            const float nr = a_r[s][av] * hr[v] - a_i[s][av] * hi[v] + xw_r[v];
+            const float ni = a_i[s][av] * hr[v] + a_r[s][av] * hi[v] + xw_i[v];
+            hr[v] = nr;
+            hi[v] = ni;
+            dyr[s][v] = (relu_out && !(hr[v] > 0.0f)) ? 0.0f : gr[v];
+            dyi[s][v] = (relu_out && !(hi[v] > 0.0f)) ? 0.0f : gi[v];
+          } else {
+            hr[v] = a_r[s][av] * hr[v] + xw_r[v];
+            dyr[s][v] = gr[v];
+            dyi[s][v] = 0.0f;
+          }
+        }
+      }
+      // reverse map of the sub-chunk: xi_out = conj(prod a) xi_in + Q
+      {
+        float Xr[V], Xi[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) { Xr[v] = 0.0f; Xi[v] = 0.0f; }
+#pragma unroll
+        for (int s = S - 1; s >= 0; --s) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const int av = AV == 1 ? 0 : v;
+            const float lr = dyr[s][v] + Xr[v];
+            const float li = dyi[s][v] + Xi[v];
+            if constexpr (CPLX) {
+              Xr[v] = a_r[s][av] * lr + a_i[s][av] * li;
+              Xi[v] = -a_i[s][av] * lr + a_r[s][av] * li;
+            } else {
+              Xr[v] = a_r[s][av] * lr;
+            }
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          s_rq[wave][0][v][lane] = s_fq[wave][0][v][lane];
+          if constexpr (CPLX) {
+            s_rq[wave][1][v][lane] = -s_fq[wave][1][v][lane];
+            s_rq[wave][2][v][lane] = Xr[v];
+            s_rq[wave][3][v][lane] = Xi[v];
+          } else {
+            s_rq[wave][1][v][lane] = Xr[v];
+          }
+        }
+      }
+      __syncthreads();  // B2: reverse maps visible
+      // incoming adjoint of this wave; adjoint leaving the chunk (same in every wave)
+      float Xr[V], Xi[V];
+#pragma unroll
+      for (int k = NW - 1; k >= 0; --k) {
+        if (k == wave) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) { Xr[v] = xr_c[v]; Xi[v] = xi_c[v]; }
+        }
+        apply_map<CPLX, V, NQ>(s_rq[k], lane, xr_c, xi_c);
+      }
+      // final reverse pass: dw, transition gradients
+#pragma unroll
+      for (int s = S - 1; s >= 0; --s) {
+        const int t = t0 + s;
+        const bool t_ok = t < p.T;
+        const int64_t row = static_cast<int64_t>(b) * p.T + t;
+        float lr[V], li[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) { lr[v] = dyr[s][v] + Xr[v]; li[v] = dyi[s][v] + Xi[v]; }
+        if (lane_ok && t_ok) {
+          store_raw<IO, V>(p.dw_re, row * p.M + m0, pack<IO, V>(lr));
+          if constexpr (CPLX) store_raw<IO, V>(p.dw_im, row * p.M + m0, pack<IO, V>(li));
+        }
+        float d0[GV], d1[GV];
+#pragma unroll
+        for (int v = 0; v < GV; ++v) { d0[v] = 0.0f; d1[v] = 0.0f; }
+        const bool live = lane_ok && t_ok && !rst[s];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const int av = AV == 1 ? 0 : v;
+          const int gv = GV == 1 ? 0 : v;
+          float gar, gai;
+          if constexpr (CPLX) {
+            gar = lr[v] * hpr[s][v] + li[v] * hpi[s][v];
+            gai = -lr[v] * hpi[s][v] + li[v] * hpr[s][v];
+          } else {
+            gar = lr[v] * hpr[s][v];
+            gai = 0.0f;
+          }
+          if (!live) { gar = 0.0f; gai = 0.0f; }
+          if constexpr (P1) {
+            const float E = fast_exp(buf[h].g0[s][0]);
+            const float delta = buf[h].g1[s][0];
+            const float lrad = -tl.nu[v] * E;
+            const float rho = fast_exp(lrad);
+            const float ar = a_r[s][av], ai = a_i[s][av];
+            float radial = lrad * (gar * ar + gai * ai);
+            const float phase = -gar * ai + gai * ar;
+            acc_th[v] += tl.th[v] * phase;
+            radial += (-lrad) * rho * delta * phase;
+            acc_nu[v] += radial;
+            d0[gv] += radial;
+            d1[gv] += phase * (1.0f - rho);
+          } else if constexpr (TR == TR_POLAR) {
+            const float ar = a_r[s][av], ai = a_i[s][av];
+            float cphi, sphi;
+            sincos_moderate(buf[h].g1[s][gv], sphi, cphi);
+            d0[gv] += gar * cphi + gai * sphi;
+            d1[gv] += -gar * ai + gai * ar;
+          } else if constexpr (TR == TR_CART) {
+            d0[gv] += gar;
+            d1[gv] += gai;
+          } else {
+            d0[gv] += gar;
+          }
+          if constexpr (CPLX) {
+            const float nr = a_r[s][av] * lr[v] + a_i[s][av] * li[v];
+            const float ni = -a_i[s][av] * lr[v] + a_r[s][av] * li[v];
+            Xr[v] = nr;
+            Xi[v] = ni;
+          } else {
+            Xr[v] = a_r[s][av] * lr[v];
+          }
+        }
+        if constexpr (GM == GATE_MODE) {
+          if (lane_ok && t_ok) {
+            store_raw<GT, V>(p.dg0, row * p.M + m0, pack<GT, V>(d0));
+            if constexpr (CPLX) store_raw<GT, V>(p.dg1, row * p.M + m0, pack<GT, V>(d1));
+          }
+        } else if constexpr (GM == GATE_LANE) {
+          float x0 = d0[0], x1 = d1[0];
+          for (int off = 1; off < glanes; off <<= 1) {
+            x0 += __shfl_xor(x0, off, 64);
+            if constexpr (CPLX) x1 += __shfl_xor(x1, off, 64);
+          }
+          if (lane_ok && t_ok && (lane & (glanes - 1)) == 0) {
+            const int64_t gi = row * p.G + m0 / p.gs;
+            store1<GT>(p.dg0, gi, x0);
+            if constexpr (CPLX) store1<GT>(p.dg1, gi, x1);
+          }
+        } else {
+          float x0 = d0[0], x1 = d1[0];
+#pragma unroll
+          for (int off = 1; off < 64; off <<= 1) {
+            x0 += __shfl_xor(x0, off, 64);
+            if constexpr (CPLX) x1 += __shfl_xor(x1, off, 64);
+          }
+          if (lane == 0 && t_ok) {
+            p.part_g0[row * p.n_mblocks + mb] = x0;
+            if constexpr (CPLX) p.part_g1[row * p.n_mblocks + mb] = x1;
+          }
+        }
+      }
+    }
+  }
+  if (wave == 0 && lane_ok && p.dh0_re) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+      p.dh0_re[hi] = xr_c[v];
+      if constexpr (CPLX) p.dh0_im[hi] = xi_c[v];
+    }
+  }
+  if constexpr (P1) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      s_par[wave][0][v][lane] = acc_nu[v];
+      s_par[wave][1][v][lane] = acc_th[v];
+    }
+    __syncthreads();
+    if (wave == 0 && lane_ok) {
+      float pn[V], pt[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) { pn[v] = 0.0f; pt[v] = 0.0f; }
+      for (int k = 0; k < NW; ++k) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) { pn[v] += s_par[k][0][v][lane]; pt[v] += s_par[k][1][v][lane]; }
+      }
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        p.part_nu[static_cast<int64_t>(b) * p.M + m0 + v] = pn[v];
+        p.part_theta[static_cast<int64_t>(b) * p.M + m0 + v] = pt[v];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fast chain-serial kernels for gates shared by the lanes of a group
+// (GATE_LANE; polar, cartesian and real transitions; at most 16 gate groups
+// per wave).  Same decomposition as the chain kernels above, plus:
+//   * each transition a(step, group) is computed once, by one lane, and
+//     shared through a per-wave LDS table (instead of by every lane of the
+//     group);
+//   * every address is a wave-uniform base plus a fixed per-lane byte offset;
+//   * steps past T and reset steps are folded into the transition table, so
+//     the inner loops carry no per-step selects;
+//   * the carry entering each chunk lives in LDS; wave k composes only the
+//     maps of waves 0..k-1, the last wave produces the next carry.
+// ---------------------------------------------------------------------------
+constexpr int kFastMaxGpw = 16;  // gate groups per wave handled by the fast kernels
+
+// A 64-bit value every lane of the wave holds, moved to scalar registers, so
+// that a memory instruction can take (kernel-argument pointer + this offset)
+// as its scalar base and the lane's byte offset as its vector offset.
+__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+template <typename T>
+__device__ __forceinline__ T ld_lane(const void* base, int64_t elem_off, uint32_t lane_bytes, int esz) {
+  const char* row = static_cast<const char*>(base) + wave_uniform(elem_off * esz);
+  return *reinterpret_cast<const T*>(row + lane_bytes);
+}
+template <typename T>
+__device__ __forceinline__ void st_lane(void* base, int64_t elem_off, uint32_t lane_bytes, int esz, T v) {
+  char* row = static_cast<char*>(base) + wave_uniform(elem_off * esz);
+  *reinterpret_cast<T*>(row + lane_bytes) = v;
+}
+
+// Fills tab[pair] = (ar, ai[, cos phi, sin phi]) for the S x gpw (step, group)
+// pairs of one sub-chunk.  Lane l handles pairs l, l + 64, ...
+template <int TR, typename IO, int S, int TW>
+__device__ __forceinline__ void fill_tab(const ScanArgs& p, int b, int t0, int g_base, int gpw, int lane,
+                                         bool reset_first, const float (&r0)[(S * kFastMaxGpw + 63) / 64],
+                                         const float (&r1)[(S * kFastMaxGpw + 63) / 64], float* tab) {
+  constexpr int R = (S * kFastMaxGpw + 63) / 64;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int idx = r * 64 + lane;
+    if (idx < S * gpw) {
+      const int step = idx / gpw;
+      const int t = t0 + step;
+      float ar = 1.0f, ai = 0.0f, cp = 1.0f, sp = 0.0f;
+      if (t < p.T) {
+        if constexpr (TR == TR_POLAR) {
+          sincos_moderate(r1[r], sp, cp);
+          ar = r0[r] * cp;
+          ai = r0[r] * sp;
+        } else if constexpr (TR == TR_CART) {
+          ar = r0[r];
+          ai = r1[r];
+        } else {
+          ar = r0[r];
+        }
+        const bool reset = p.segpos ? (p.segpos[static_cast<int64_t>(b) * p.T + t] == 0) : (reset_first && t == 0);
+        if (reset) { ar = 0.0f; ai = 0.0f; }
+      }
+      float* e = tab + idx * TW;
+      e[0] = ar;
+      if constexpr (TW > 1) e[1] = ai;
+      if constexpr (TW > 2) { e[2] = cp; e[3] = sp; }
+    }
+  }
+  (void)g_base;
+}
+
+// raw gate values of the pairs of one sub-chunk (prefetched with the inputs)
+template <int TR, typename IO, int S>
+__device__ __forceinline__ void load_gate_pairs(const ScanArgs& p, int b, int t0, int g_base, int gpw, int lane,
+                                                float (&r0)[(S * kFastMaxGpw + 63) / 64],
+                                                float (&r1)[(S * kFastMaxGpw + 63) / 64]) {
+  constexpr int R = (S * kFastMaxGpw + 63) / 64;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int idx = r * 64 + lane;
+    r0[r] = 0.0f;
+    r1[r] = 0.0f;
+    if (idx < S * gpw) {
+      const int t = t0 + idx / gpw;
+      if (t < p.T) {
+        const int64_t gi = (static_cast<int64_t>(b) * p.T + t) * p.G + g_base + idx % gpw;
+        r0[r] = load1<IO>(p.g0, gi);
+        if constexpr (TR != TR_REAL) r1[r] = load1<IO>(p.g1, gi);
+      }
+    }
+  }
+}
+
+template <int TR, typename IO, int V, int S, int NW>
+__global__ void __launch_bounds__(NW * 64, 4)
+chain_fwd_fast_kernel(ScanArgs p) {
+  constexpr bool CPLX = TR != TR_REAL;
+  constexpr int C = S * NW;
+  constexpr int MB = 64 * V;
+  constexpr int NH = CPLX ? 2 : 1;
+  constexpr int R = (S * kFastMaxGpw + 63) / 64;
+  constexpr int TW = CPLX ? 2 : 1;
+  constexpr int ESZ = sizeof(IO);
+  using RawT = typename Raw<IO, V>::T;
+  // per wave: sub-chunk map P (NH floats per lane, shared by the lane's modes)
+  // and Q (NH floats per mode)
+  __shared__ float s_p[2][NW][NH][64];
+  __shared__ float s_q[2][NW][NH][V][64];
+  __shared__ float s_carry[2][NH][V][64];
+  __shared__ float s_tab[NW][S * kFastMaxGpw * TW];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int chain = blockIdx.x;
+  const int b = chain / p.n_mblocks;
+  const int mb = chain - b * p.n_mblocks;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < p.M;
+  const int gpw = MB / p.gs;            // gate groups per wave (the tile)
+  const int lpg = p.gs / V;             // lanes per group
+  const int my_g = lane / lpg;
+  const int g_base = mb * gpw;
+  const bool relu_out = CPLX && (p.flags & SPARC_FLAG_RELU_OUTPUT);
+  const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
+  const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
+  // element offset of (b, t=0, mode block) in [B,T,M]; rows are M (or 2M) long
+  const int64_t row0 = static_cast<int64_t>(b) * p.T;
+  const int64_t mbase = static_cast<int64_t>(mb) * MB;
+  float* tab = s_tab[wave];
+
+  if (wave == 0) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+      s_carry[0][0][v][lane] = (p.h0_re && lane_ok) ? p.h0_re[hi] : 0.0f;
+      if constexpr (CPLX) s_carry[0][1][v][lane] = (p.h0_im && lane_ok) ? p.h0_im[hi] : 0.0f;
+    }
+  }
+
+  RawT wr[2][S], wi[2][S];
+  float gr0[2][R], gr1[2][R];
+  auto load_chunk = [&](int hb, int c) {
+    const int t0 = c * C + wave * S;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int t = t0 + s;
+      if (t < p.T && lane_ok) {
+        const int64_t e = (row0 + t) * p.M + mbase;
+        wr[hb][s] = ld_lane<RawT>(p.w_re, e, lane_bytes, ESZ);
+        if constexpr (CPLX) wi[hb][s] = ld_lane<RawT>(p.w_im, e, lane_bytes, ESZ);
+      } else {
+        float z[V] = {};
+        wr[hb][s] = pack<IO, V>(z);
+        wi[hb][s] = wr[hb][s];
+      }
+    }
+    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gr0[hb], gr1[hb]);
+  };
+
+  load_chunk(0, 0);
+  for (int c0 = 0; c0 < p.n_chunks; c0 += 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = c0 + h;
+      if (c >= p.n_chunks) break;
+      const int t0 = c * C + wave * S;
+      if (c + 1 < p.n_chunks) load_chunk(1 - h, c + 1);
+      // transitions of this sub-chunk: table, then the lane's S values
+      fill_tab<TR, IO, S, TW>(p, b, t0, g_base, gpw, lane, reset_first, gr0[h], gr1[h], tab);
+      __builtin_amdgcn_wave_barrier();
+      float ar[S], ai[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        ar[s] = tab[(s * gpw + my_g) * TW];
+        ai[s] = CPLX ? tab[(s * gpw + my_g) * TW + 1] : 0.0f;
+      }
+      // local scan from zero: P (shared), Q (per mode)
+      float Pr = 1.0f, Pi = 0.0f, Qr[V], Qi[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) { Qr[v] = 0.0f; Qi[v] = 0.0f; }
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        float xr[V], xi[V];
+        unpack<IO, V>(wr[h][s], xr);
+        if constexpr (CPLX) unpack<IO, V>(wi[h][s], xi);
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) {
+            const float nr = fmaf(ar[s], Qr[v], fmaf(-ai[s], Qi[v], xr[v]));
+            const float ni = fmaf(ai[s], Qr[v], fmaf(ar[s], Qi[v], xi[v]));
+            Qr[v] = nr;
+            Qi[v] = ni;
+          } else {
+            Qr[v] = fmaf(ar[s], Qr[v], xr[v]);
+          }
+        }
+        if constexpr (CPLX) {
+          const float nr = ar[s] * Pr - ai[s] * Pi;
+          const float ni = ar[s] * Pi + ai[s] * Pr;
+          Pr = nr;
+          Pi = ni;
+        } else {
+          Pr *= ar[s];
+        }
+      }
+      s_p[h][wave][0][lane] = Pr;
+      if constexpr (CPLX) s_p[h][wave][1][lane] = Pi;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        s_q[h][wave][0][v][lane] = Qr[v];
+        if constexpr (CPLX) s_q[h][wave][1][v][lane] = Qi[v];
+      }
+      __syncthreads();
+      // start state of this wave: maps 0..wave-1 applied to the chunk carry
+      float sr[V], si[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        sr[v] = s_carry[h][0][v][lane];
+        si[v] = CPLX ? s_carry[h][1][v][lane] : 0.0f;
+      }
+      const int n_maps = (wave == NW - 1) ? NW : wave;
+      float er[V], ei[V];
+      for (int k = 0; k < n_maps; ++k) {
+        if (k == wave) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) { er[v] = sr[v]; ei[v] = si[v]; }
+        }
+        const float pr = s_p[h][k][0][lane];
+        const float pi = CPLX ? s_p[h][k][1][lane] : 0.0f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) {
+            const float qr = s_q[h][k][0][v][lane], qi = s_q[h][k][1][v][lane];
+            const float nr = fmaf(pr, sr[v], fmaf(-pi, si[v], qr));
+            const float ni = fmaf(pr, si[v], fmaf(pi, sr[v], qi));
+            sr[v] = nr;
+            si[v] = ni;
+          } else {
+            sr[v] = fmaf(pr, sr[v], s_q[h][k][0][v][lane]);
+          }
+        }
+      }
+      if (wave == NW - 1) {
+        // sr/si now hold the state after the chunk; the wave's own start is er/ei
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          s_carry[1 - h][0][v][lane] = sr[v];
+          if constexpr (CPLX) s_carry[1 - h][1][v][lane] = si[v];
+        }
+        if (lane_ok) {
+          float* dst = p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + c) * p.M + m0) * NH;
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            dst[v * NH] = sr[v];
+            if constexpr (CPLX) dst[v * NH + 1] = si[v];
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) { sr[v] = er[v]; si[v] = ei[v]; }
+      }
+      // replay and store
+      if (lane_ok) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const int t = t0 + s;
+          float xr[V], xi[V];
+          unpack<IO, V>(wr[h][s], xr);
+          if constexpr (CPLX) unpack<IO, V>(wi[h][s], xi);
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            if constexpr (CPLX) {
+              const float nr = fmaf(ar[s], sr[v], fmaf(-ai[s], si[v], xr[v]));
+              const float ni = fmaf(ai[s], sr[v], fmaf(ar[s], si[v], xi[v]));
+              sr[v] = nr;
+              si[v] = ni;
+            } else {
+              sr[v] = fmaf(ar[s], sr[v], xr[v]);
+            }
+          }
+          if (t < p.T) {
+            if (relu_out) {
+              float rr[V], ri[V];
+#pragma unroll
+              for (int v = 0; v < V; ++v) { rr[v] = fmaxf(sr[v], 0.0f); ri[v] = fmaxf(si[v], 0.0f); }
+              const int64_t e = (row0 + t) * 2 * p.M + mbase;
+              st_lane<RawT>(p.y_re, e, lane_bytes, ESZ, pack<IO, V>(rr));
+              st_lane<RawT>(p.y_re, e + p.M, lane_bytes, ESZ, pack<IO, V>(ri));
+            } else {
+              const int64_t e = (row0 + t) * p.M + mbase;
+              st_lane<RawT>(p.y_re, e, lane_bytes, ESZ, pack<IO, V>(sr));
+              if constexpr (CPLX) st_lane<RawT>(p.y_im, e, lane_bytes, ESZ, pack<IO, V>(si));
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int TR, typename IO, int V, int S, int NW>
+__global__ void __launch_bounds__(NW * 64, 2)
+chain_bwd_fast_kernel(ScanArgs p) {
+  constexpr bool CPLX = TR != TR_REAL;
+  constexpr int C = S * NW;
+  constexpr int MB = 64 * V;
+  constexpr int NH = CPLX ? 2 : 1;
+  constexpr int R = (S * kFastMaxGpw + 63) / 64;
+  constexpr int TW = (TR == TR_POLAR) ? 4 : (CPLX ? 2 : 1);
+  constexpr int ESZ = sizeof(IO);
+  using RawT = typename Raw<IO, V>::T;
+  // forward maps: written before barrier B1, read between B1 and B2
+  __shared__ float s_fp[NW][NH][64];
+  __shared__ float s_fq[NW][NH][V][64];
+  // reverse maps: written before B2, read after B2 (until the next B1)
+  __shared__ float s_rp[NW][NH][64];
+  __shared__ float s_rq[NW][NH][V][64];
+  __shared__ float s_xi[2][NH][V][64];
+  __shared__ float s_tab[NW][S * kFastMaxGpw * TW];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int chain = blockIdx.x;
+  const int b = chain / p.n_mblocks;
+  const int mb = chain - b * p.n_mblocks;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < p.M;
+  const int gpw = MB / p.gs;
+  const int lpg = p.gs / V;
+  const int my_g = lane / lpg;
+  const int g_base = mb * gpw;
+  const bool relu_out = CPLX && (p.flags & SPARC_FLAG_RELU_OUTPUT);
+  const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
+  const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
+  const int64_t row0 = static_cast<int64_t>(b) * p.T;
+  const int64_t mbase = static_cast<int64_t>(mb) * MB;
+  float* tab = s_tab[wave];
+
+  if (wave == 0) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+      s_xi[(p.n_chunks - 1) & 1][0][v][lane] = (p.dlast_re && lane_ok) ? p.dlast_re[hi] : 0.0f;
+      if constexpr (CPLX) s_xi[(p.n_chunks - 1) & 1][1][v][lane] = (p.dlast_im && lane_ok) ? p.dlast_im[hi] : 0.0f;
+    }
+  }
+
+  RawT wr[2][S], wi[2][S], dr[2][S], di[2][S];
+  float gr0[2][R], gr1[2][R];
+  float hs[2][V * NH];
+  auto load_chunk = [&](int hb, int c) {
+    const int t0 = c * C + wave * S;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int t = t0 + s;
+      if (t < p.T && lane_ok) {
+        const int64_t e = (row0 + t) * p.M + mbase;
+        wr[hb][s] = ld_lane<RawT>(p.w_re, e, lane_bytes, ESZ);
+        if constexpr (CPLX) wi[hb][s] = ld_lane<RawT>(p.w_im, e, lane_bytes, ESZ);
+        if (relu_out) {
+          const int64_t e2 = (row0 + t) * 2 * p.M + mbase;
+          dr[hb][s] = ld_lane<RawT>(p.dy_re, e2, lane_bytes, ESZ);
+          di[hb][s] = ld_lane<RawT>(p.dy_re, e2 + p.M, lane_bytes, ESZ);
+        } else {
+          dr[hb][s] = ld_lane<RawT>(p.dy_re, e, lane_bytes, ESZ);
+          if constexpr (CPLX) di[hb][s] = ld_lane<RawT>(p.dy_im, e, lane_bytes, ESZ);
+        }
+      } else {
+        float z[V] = {};
+        wr[hb][s] = pack<IO, V>(z);
+        wi[hb][s] = wr[hb][s];
+        dr[hb][s] = wr[hb][s];
+        di[hb][s] = wr[hb][s];
+      }
+    }
+    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gr0[hb], gr1[hb]);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float h_r = 0.0f, h_i = 0.0f;
+      if (lane_ok) {
+        if (c == 0) {
+          const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+          if (p.h0_re) { h_r = p.h0_re[hi]; if constexpr (CPLX) h_i = p.h0_im[hi]; }
+        } else {
+          const int64_t ci_ = ((static_cast<int64_t>(b) * p.n_chunks + c - 1) * p.M + m0 + v) * NH;
+          h_r = p.chunk_state_in[ci_];
+          if constexpr (CPLX) h_i = p.chunk_state_in[ci_ + 1];
+        }
+      }
+      hs[hb][v * NH] = h_r;
+      if constexpr (CPLX) hs[hb][v * NH + 1] = h_i;
+    }
+  };
+
+  load_chunk(0, p.n_chunks - 1);
+  for (int c0 = p.n_chunks - 1; c0 >= 0; c0 -= 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = c0 - h;
+      if (c < 0) break;
+      const int t0 = c * C + wave * S;
+      const int xb = c & 1;  // s_xi buffer holding the adjoint entering this chunk
+      if (c - 1 >= 0) load_chunk(1 - h, c - 1);
+      fill_tab<TR, IO, S, TW>(p, b, t0, g_base, gpw, lane, reset_first, gr0[h], gr1[h], tab);
+      __builtin_amdgcn_wave_barrier();
+      float ar[S], ai[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        ar[s] = tab[(s * gpw + my_g) * TW];
+        ai[s] = CPLX ? tab[(s * gpw + my_g) * TW + 1] : 0.0f;
+      }
+      // forward map of the sub-chunk
+      {
+        float Pr = 1.0f, Pi = 0.0f, Qr[V], Qi[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) { Qr[v] = 0.0f; Qi[v] = 0.0f; }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          float xr[V], xi[V];
+          unpack<IO, V>(wr[h][s], xr);
+          if constexpr (CPLX) unpack<IO, V>(wi[h][s], xi);
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            if constexpr (CPLX) {
+              const float nr = fmaf(ar[s], Qr[v], fmaf(-ai[s], Qi[v], xr[v]));
+              const float ni = fmaf(ai[s], Qr[v], fmaf(ar[s], Qi[v], xi[v]));
+              Qr[v] = nr;
+              Qi[v] = ni;
+            } else {
+              Qr[v] = fmaf(ar[s], Qr[v], xr[v]);
+            }
+          }
+          if constexpr (CPLX) {
+            const float nr = ar[s] * Pr - ai[s] * Pi;
+            const float ni = ar[s] * Pi + ai[s] * Pr;
+            Pr = nr;
+            Pi = ni;
+          } else {
+            Pr *= ar[s];
+          }
+        }
+        s_fp[wave][0][lane] = Pr;
+        if constexpr (CPLX) s_fp[wave][1][lane] = Pi;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          s_fq[wave][0][v][lane] = Qr[v];
+          if constexpr (CPLX) s_fq[wave][1][v][lane] = Qi[v];
+        }
+      }
+      __syncthreads();  // B1
+      float hr[V], hi[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) { hr[v] = hs[h][v * NH]; hi[v] = CPLX ? hs[h][v * NH + 1] : 0.0f; }
+      for (int k = 0; k < wave; ++k) {
+        const float pr = s_fp[k][0][lane];
+        const float pi = CPLX ? s_fp[k][1][lane] : 0.0f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) {
+            const float nr = fmaf(pr, hr[v], fmaf(-pi, hi[v], s_fq[k][0][v][lane]));
+            const float ni = fmaf(pr, hi[v], fmaf(pi, hr[v], s_fq[k][1][v][lane]));
+            hr[v] = nr;
+            hi[v] = ni;
+          } else {
+            hr[v] = fmaf(pr, hr[v], s_fq[k][0][v][lane]);
+          }
+        }
+      }
+      // recompute the states before every step; masked output gradient
+      float hpr[S][V], hpi[S][V], gyr[S][V], gyi[S][V];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        float xr[V], xi[V], yr[V], yi[V];
+        unpack<IO, V>(wr[h][s], xr);
+        unpack<IO, V>(dr[h][s], yr);
+        if constexpr (CPLX) {
+          unpack<IO, V>(wi[h][s], xi);
+          unpack<IO, V>(di[h][s], yi);
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          hpr[s][v] = hr[v];
+          hpi[s][v] = CPLX ? hi[v] : 0.0f;
+          if constexpr (CPLX) {
+            const float nr = fmaf(ar[s], hr[v], fmaf(-ai[s], hi[v], xr[v]));
+            const float ni = fmaf(ai[s], hr[v], fmaf(ar[s], hi[v], xi[v]));
+            hr[v] = nr;
+            hi[v] = ni;
+            gyr[s][v] = (relu_out && !(hr[v] > 0.0f)) ? 0.0f : yr[v];
+            gyi[s][v] = (relu_out && !(hi[v] > 0.0f)) ? 0.0f : yi[v];
+          } else {
+            hr[v] = fmaf(ar[s], hr[v], xr[v]);
+            gyr[s][v] = yr[v];
+            gyi[s][v] = 0.0f;
+          }
+        }
+      }
+      // reverse map of the sub-chunk
+      {
+        float Xr[V], Xi[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) { Xr[v] = 0.0f; Xi[v] = 0.0f; }
+#pragma unroll
+        for (int s = S - 1; s >= 0; --s) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const float lr = gyr[s][v] + Xr[v];
+            const float li = gyi[s][v] + Xi[v];
+            if constexpr (CPLX) {
+              Xr[v] = fmaf(ar[s], lr, ai[s] * li);
+              Xi[v] = fmaf(ar[s], li, -ai[s] * lr);
+            } else {
+              Xr[v] = ar[s] * lr;
+            }
+          }
+        }
+        // product of conj(a) over the sub-chunk = conj of the forward product
+        s_rp[wave][0][lane] = s_fp[wave][0][lane];
+        if constexpr (CPLX) s_rp[wave][1][lane] = -s_fp[wave][1][lane];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          s_rq[wave][0][v][lane] = Xr[v];
+          if constexpr (CPLX) s_rq[wave][1][v][lane] = Xi[v];
+        }
+      }
+      __syncthreads();  // B2
+      // adjoint entering this wave: reverse maps NW-1 .. wave+1 applied to the chunk's
+      float xr[V], xi[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        xr[v] = s_xi[xb][0][v][lane];
+        xi[v] = CPLX ? s_xi[xb][1][v][lane] : 0.0f;
+      }
+      const int k_end = (wave == 0) ? -1 : wave;   // wave 0 also applies map 0 -> next carry
+      float er[V], ei[V];
+      for (int k = NW - 1; k > k_end; --k) {
+        if (k == wave) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) { er[v] = xr[v]; ei[v] = xi[v]; }
+        }
+        // conj(P_k) x + Qrev_k
+        const float pr = s_rp[k][0][lane];
+        const float pi = CPLX ? s_rp[k][1][lane] : 0.0f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) {
+            const float nr = fmaf(pr, xr[v], fmaf(-pi, xi[v], s_rq[k][0][v][lane]));
+            const float ni = fmaf(pr, xi[v], fmaf(pi, xr[v], s_rq[k][1][v][lane]));
+            xr[v] = nr;
+            xi[v] = ni;
+          } else {
+            xr[v] = fmaf(pr, xr[v], s_rq[k][0][v][lane]);
+          }
+        }
+      }
+      if (wave == 0) {
+        // xr/xi: adjoint leaving the chunk (entering chunk c-1, or dh0)
+        if (c > 0) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            s_xi[1 - xb][0][v][lane] = xr[v];
+            if constexpr (CPLX) s_xi[1 - xb][1][v][lane] = xi[v];
+          }
+        } else if (lane_ok && p.dh0_re) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const int64_t hi2 = static_cast<int64_t>(b) * p.M + m0 + v;
+            p.dh0_re[hi2] = xr[v];
+            if constexpr (CPLX) p.dh0_im[hi2] = xi[v];
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) { xr[v] = er[v]; xi[v] = ei[v]; }
+      }
+      // final reverse pass
+#pragma unroll
+      for (int s = S - 1; s >= 0; --s) {
+        const int t = t0 + s;
+        const bool t_ok = t < p.T;
+        float lr[V], li[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) { lr[v] = gyr[s][v] + xr[v]; li[v] = gyi[s][v] + xi[v]; }
+        if (lane_ok && t_ok) {
+          const int64_t e = (row0 + t) * p.M + mbase;
+          st_lane<RawT>(p.dw_re, e, lane_bytes, ESZ, pack<IO, V>(lr));
+          if constexpr (CPLX) st_lane<RawT>(p.dw_im, e, lane_bytes, ESZ, pack<IO, V>(li));
+        }
+        // transition gradient summed over the lane's modes
+        float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) {
+            const float gar = fmaf(lr[v], hpr[s][v], li[v] * hpi[s][v]);
+            const float gai = fmaf(li[v], hpr[s][v], -lr[v] * hpi[s][v]);
+            if constexpr (TR == TR_POLAR) {
+              const float cp = tab[(s * gpw + my_g) * TW + 2];
+              const float sp = tab[(s * gpw + my_g) * TW + 3];
+              d0 += fmaf(gar, cp, gai * sp);
+              d1 += fmaf(gai, ar[s], -gar * ai[s]);
+            } else {
+              d0 += gar;
+              d1 += gai;
+            }
+          } else {
+            d0 = fmaf(lr[v], hpr[s][v], d0);
+          }
+          if constexpr (CPLX) {
+            const float nr = fmaf(ar[s], lr[v], ai[s] * li[v]);
+            const float ni = fmaf(ar[s], li[v], -ai[s] * lr[v]);
+            xr[v] = nr;
+            xi[v] = ni;
+          } else {
+            xr[v] = ar[s] * lr[v];
+          }
+        }
+        for (int off = 1; off < lpg; off <<= 1) {
+          d0 += __shfl_xor(d0, off, 64);
+          if constexpr (CPLX) d1 += __shfl_xor(d1, off, 64);
+        }
+        if (lane_ok && t_ok && (lane & (lpg - 1)) == 0) {
+          // a reset step's transition is the constant 0: no gradient
+          const bool reset = p.segpos ? (p.segpos[row0 + t] == 0) : (reset_first && t == 0);
+          const int64_t gi = (row0 + t) * p.G + g_base + my_g;
+          store1<IO>(p.dg0, gi, reset ? 0.0f : d0);
+          if constexpr (CPLX) store1<IO>(p.dg1, gi, reset ? 0.0f : d1);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // helpers: workspace clear, partial reductions
 // ---------------------------------------------------------------------------
 __global__ void clear_u32_kernel(uint32_t* p, int64_t n) {
@@ -1104,9 +2268,15 @@ sparc_status fail(sparc_status s, const char* fmt, ...) {
 
 constexpr int kChunk = 64;  // C = S * NW for every instantiation
 
+// Minimum number of chains for the chain-serial kernels (two resident
+// workgroups per CU on a 256-CU MI355X).
+constexpr int kChainMin = 512;
+
 struct Plan {
   int V = 1;
   int gm = sparc::GATE_LANE;
+  bool chain = false;
+  bool fast = false;  // chain kernels specialised for lane-shared gates
   int n_chunks = 0, n_mblocks = 0, n_chains = 0;
   int64_t n_tiles = 0;
   size_t flags_off = 0, agg_off = 0, carry_off = 0, part_off = 0, total = 0;
@@ -1150,6 +2320,11 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl) {
   pl->n_mblocks = static_cast<int>((M + 64 * V - 1) / (64 * V));
   pl->n_chains = static_cast<int>(d->batch * pl->n_mblocks);
   pl->n_tiles = static_cast<int64_t>(pl->n_chains) * pl->n_chunks;
+  if ((d->flags & SPARC_FLAG_ALGO_LOOKBACK) && (d->flags & SPARC_FLAG_ALGO_CHAIN))
+    return "ALGO_LOOKBACK and ALGO_CHAIN are exclusive";
+  pl->chain = (d->flags & SPARC_FLAG_ALGO_CHAIN) ||
+              (!(d->flags & SPARC_FLAG_ALGO_LOOKBACK) && pl->n_chains >= kChainMin);
+  pl->fast = pl->chain && !p1 && gm == sparc::GATE_LANE && (64 * V) / gs <= sparc::kFastMaxGpw;
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
   const int NQ = cplx ? 4 : 2, NH = cplx ? 2 : 1;
   size_t off = 256;  // [0] ticket, [1] error
@@ -1173,22 +2348,45 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl) {
 
 template <int TR, typename IO, int V, int GM>
 struct Kernels {
+  // look-back kernels: 8 waves x 8 steps
   static constexpr int S = 8;
   static constexpr int NW = kChunk / S;
-  static void fwd(dim3 g, hipStream_t st, const sparc::ScanArgs& a) {
-    hipLaunchKernelGGL((sparc::scan_fwd_kernel<TR, IO, V, GM, S, NW>), g, dim3(NW * 64), 0, st, a);
-  }
-  static void bwd(dim3 g, hipStream_t st, const sparc::ScanArgs& a) {
-    hipLaunchKernelGGL((sparc::scan_bwd_kernel<TR, IO, V, GM, S, NW>), g, dim3(NW * 64), 0, st, a);
+  // chain-serial kernels
+  static constexpr int CS_F = 8, CNW_F = kChunk / CS_F;
+  static constexpr int CS_B = 4, CNW_B = kChunk / CS_B;
+  static void run(int dir, bool chain, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
+    if constexpr (TR != sparc::TR_P1 && GM == sparc::GATE_LANE) {
+      if (chain && pl.fast) {
+        constexpr int FS = 8, FNW = kChunk / FS;
+        const dim3 g(static_cast<unsigned>(pl.n_chains));
+        if (dir == 0)
+          hipLaunchKernelGGL((sparc::chain_fwd_fast_kernel<TR, IO, V, FS, FNW>), g, dim3(FNW * 64), 0, st, a);
+        else
+          hipLaunchKernelGGL((sparc::chain_bwd_fast_kernel<TR, IO, V, FS, FNW>), g, dim3(FNW * 64), 0, st, a);
+        return;
+      }
+    }
+    if (chain) {
+      const dim3 g(static_cast<unsigned>(pl.n_chains));
+      if (dir == 0)
+        hipLaunchKernelGGL((sparc::chain_fwd_kernel<TR, IO, V, GM, CS_F, CNW_F>), g, dim3(CNW_F * 64), 0, st, a);
+      else
+        hipLaunchKernelGGL((sparc::chain_bwd_kernel<TR, IO, V, GM, CS_B, CNW_B>), g, dim3(CNW_B * 64), 0, st, a);
+      return;
+    }
+    const dim3 g(static_cast<unsigned>(pl.n_tiles));
+    if (dir == 0) hipLaunchKernelGGL((sparc::scan_fwd_kernel<TR, IO, V, GM, S, NW>), g, dim3(NW * 64), 0, st, a);
+    else hipLaunchKernelGGL((sparc::scan_bwd_kernel<TR, IO, V, GM, S, NW>), g, dim3(NW * 64), 0, st, a);
   }
 };
 
 template <int TR, typename IO>
-void launch_v(int dir, int V, int gm, dim3 g, hipStream_t st, const sparc::ScanArgs& a) {
+void launch_v(int dir, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
   constexpr int VM = (TR == sparc::TR_REAL) ? 4 : 2;
+  const int V = pl.V, gm = pl.gm;
 #define SPARC_LAUNCH(VV, GG)                                                            \
   if (V == VV && gm == GG) {                                                           \
-    if (dir == 0) Kernels<TR, IO, VV, GG>::fwd(g, st, a); else Kernels<TR, IO, VV, GG>::bwd(g, st, a); \
+    Kernels<TR, IO, VV, GG>::run(dir, pl.chain, pl, st, a);                              \
     return;                                                                             \
   }
   SPARC_LAUNCH(VM, sparc::GATE_LANE)
@@ -1203,24 +2401,23 @@ void launch_v(int dir, int V, int gm, dim3 g, hipStream_t st, const sparc::ScanA
 }
 
 void launch(int dir, const sparc_scan_desc* d, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
-  dim3 g(static_cast<unsigned>(pl.n_tiles));
   const bool bf = d->io_dtype == SPARC_BF16;
   switch (d->transition) {
     case SPARC_TRANSITION_P1:
-      if (bf) launch_v<sparc::TR_P1, sparc::bf16>(dir, pl.V, pl.gm, g, st, a);
-      else launch_v<sparc::TR_P1, float>(dir, pl.V, pl.gm, g, st, a);
+      if (bf) launch_v<sparc::TR_P1, sparc::bf16>(dir, pl, st, a);
+      else launch_v<sparc::TR_P1, float>(dir, pl, st, a);
       break;
     case SPARC_TRANSITION_POLAR:
-      if (bf) launch_v<sparc::TR_POLAR, sparc::bf16>(dir, pl.V, pl.gm, g, st, a);
-      else launch_v<sparc::TR_POLAR, float>(dir, pl.V, pl.gm, g, st, a);
+      if (bf) launch_v<sparc::TR_POLAR, sparc::bf16>(dir, pl, st, a);
+      else launch_v<sparc::TR_POLAR, float>(dir, pl, st, a);
       break;
     case SPARC_TRANSITION_CARTESIAN:
-      if (bf) launch_v<sparc::TR_CART, sparc::bf16>(dir, pl.V, pl.gm, g, st, a);
-      else launch_v<sparc::TR_CART, float>(dir, pl.V, pl.gm, g, st, a);
+      if (bf) launch_v<sparc::TR_CART, sparc::bf16>(dir, pl, st, a);
+      else launch_v<sparc::TR_CART, float>(dir, pl, st, a);
       break;
     default:
-      if (bf) launch_v<sparc::TR_REAL, sparc::bf16>(dir, pl.V, pl.gm, g, st, a);
-      else launch_v<sparc::TR_REAL, float>(dir, pl.V, pl.gm, g, st, a);
+      if (bf) launch_v<sparc::TR_REAL, sparc::bf16>(dir, pl, st, a);
+      else launch_v<sparc::TR_REAL, float>(dir, pl, st, a);
       break;
   }
 }
@@ -1318,7 +2515,8 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, con
   }
   if (!aligned(chunk_state, 8 * pl.V)) return fail(SPARC_EINVAL, "chunk_state must be %d-byte aligned", 8 * pl.V);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (sparc_status s = clear_ws(pl, workspace, st)) return s;
+  if (!pl.chain)
+    if (sparc_status s = clear_ws(pl, workspace, st)) return s;
   sparc::ScanArgs a{};
   a.B = static_cast<int>(d->batch);
   a.T = static_cast<int>(d->length);
@@ -1397,7 +2595,8 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
     if (sparc_status s = check_io_ptrs(d, pl, gp, 4)) return s;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (sparc_status s = clear_ws(pl, workspace, st)) return s;
+  if (!pl.chain)
+    if (sparc_status s = clear_ws(pl, workspace, st)) return s;
   sparc::ScanArgs a{};
   a.B = static_cast<int>(d->batch);
   a.T = static_cast<int>(d->length);
@@ -1434,7 +2633,8 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
     }
   }
   if (p1) {
-    const int64_t prow = d->batch * pl.n_chunks;
+    // one partial row per tile (look-back) or per batch row (chain)
+    const int64_t prow = pl.chain ? d->batch : d->batch * pl.n_chunks;
     if (sparc_status s = sparc_column_sum(prow, d->modes, a.part_nu, dnu_log, 0, stream)) return s;
     if (sparc_status s = sparc_column_sum(prow, d->modes, a.part_theta, dtheta_log, 0, stream)) return s;
   }

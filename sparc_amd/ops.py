@@ -19,7 +19,28 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import FLAG_RELU_OUTPUT, FLAG_RESET_FIRST, TRANSITIONS
+from ._lib import ALGO_FLAGS, FLAG_RELU_OUTPUT, FLAG_RESET_FIRST, TRANSITIONS
+
+_algorithm = "auto"
+
+
+def set_algorithm(name: str) -> None:
+    """Scan algorithm for every later call: "auto" (by shape), "lookback"
+    (one workgroup per (chain, chunk) tile, carries between workgroups) or
+    "chain" (one workgroup per (batch row, mode block) chain)."""
+    global _algorithm
+    if name not in ALGO_FLAGS:
+        raise ValueError(f"unknown scan algorithm {name!r}")
+    _algorithm = name
+
+
+def get_algorithm() -> str:
+    return _algorithm
+
+
+def _flags(relu_output, reset_first):
+    return ((FLAG_RELU_OUTPUT if relu_output else 0) | (FLAG_RESET_FIRST if reset_first else 0)
+            | ALGO_FLAGS[_algorithm])
 
 
 # ---------------------------------------------------------------------------
@@ -44,8 +65,7 @@ def scan_forward_raw(transition, g0, g1, w_re, w_im, nu_log=None, theta_log=None
     G = g0.shape[-1]
     io = _lib.io_code(w_re.dtype)
     gate_io = _lib.io_code(g0.dtype)
-    flags = (FLAG_RELU_OUTPUT if relu_output else 0) | (FLAG_RESET_FIRST if reset_first else 0)
-    d = _desc(transition, B, T, M, G, io, gate_io, flags)
+    d = _desc(transition, B, T, M, G, io, gate_io, _flags(relu_output, reset_first))
     n_chunks = lib.sparc_scan_chunk_count(ctypes.byref(d))
     cplx = transition != "real"
     if relu_output:
@@ -78,8 +98,7 @@ def scan_backward_raw(transition, g0, g1, w_re, w_im, chunk_state, dy_re, dy_im,
     G = g0.shape[-1]
     io = _lib.io_code(w_re.dtype)
     gate_io = _lib.io_code(g0.dtype)
-    flags = (FLAG_RELU_OUTPUT if relu_output else 0) | (FLAG_RESET_FIRST if reset_first else 0)
-    d = _desc(transition, B, T, M, G, io, gate_io, flags)
+    d = _desc(transition, B, T, M, G, io, gate_io, _flags(relu_output, reset_first))
     cplx = transition != "real"
     dw_re = torch.empty_like(w_re)
     dw_im = torch.empty_like(w_im) if cplx else None

@@ -149,10 +149,13 @@ def check_case(case, tol=None):
         # output gradient: there the relu mask may legitimately differ from
         # the float64 oracle (bf16 moves states by ~2^-9 relative)
         with torch.no_grad():
+            d = lambda t: None if t is None else t.double()  # noqa: E731
+            init = case["init"]
             y_o, _ = O.grouped_scan_forward(
-                case["transition"], case["g0"].double(), case["g1"].double(), case["w_re"].double(),
-                case["w_im"].double(), case["nu_log"].double(), case["theta_log"].double(),
-                relu_output=False)
+                case["transition"], d(case["g0"]), d(case["g1"]), d(case["w_re"]), d(case["w_im"]),
+                d(case["nu_log"]), d(case["theta_log"]),
+                h0=None if init is None else tuple(t.double() for t in init),
+                segment_pos=case["segpos"], reset_first=case["reset_first"], relu_output=False)
             h = torch.cat(y_o, -1)
             band = 1e-3 if case["dtype"] == torch.float32 else 2e-2
             mask = (h.abs() > band * h.abs().max()).to(torch.float64)
@@ -192,6 +195,12 @@ CASES = [
     ("cart_odd_modes_v1_f32", "cartesian", 2, 50, 33, 33, F32, {}),
     ("real_grouped_f32", "real", 2, 300, 256, 32, F32, {}),
     ("real_per_element_f32", "real", 2, 129, 300, 300, F32, {}),
+    ("real_grouped16_f32", "real", 2, 200, 512, 32, F32, {}),
+    ("real_grouped16_bf16", "real", 1, 128, 512, 32, BF16, {}),
+    ("real_grouped16_h0_segments_f32", "real", 2, 150, 512, 32, F32, dict(h0=True, dlast=True, seg=True)),
+    ("polar_h0_segments_bf16", "polar", 2, 140, 256, 16, BF16, dict(h0=True, dlast=True, seg=True)),
+    ("polar_reset_first_f32", "polar", 1, 70, 256, 16, F32, dict(h0=True, reset_first=True)),
+    ("polar_relu_out_bf16", "polar", 2, 96, 256, 16, BF16, dict(relu=True)),
     ("real_per_element_bf16", "real", 2, 64, 256, 256, BF16, {}),
     ("p1_h0_dlast_f32", "p1", 2, 150, 128, 1, F32, dict(h0=True, dlast=True)),
     ("p1_segments_f32", "p1", 2, 140, 128, 1, F32, dict(h0=True, dlast=True, seg=True)),
@@ -204,14 +213,22 @@ CASES = [
 ]
 
 
+@pytest.fixture(params=["lookback", "chain"])
+def algorithm(request):
+    """Runs a test under each scan algorithm (forward and backward)."""
+    ops.set_algorithm(request.param)
+    yield request.param
+    ops.set_algorithm("auto")
+
+
 @pytest.mark.parametrize("cid,transition,B,T,M,G,dtype,extra", CASES, ids=[c[0] for c in CASES])
-def test_scan_parity(cid, transition, B, T, M, G, dtype, extra):
-    print(f"[case] {cid} B={B} T={T} M={M} G={G} {dtype}", flush=True)
+def test_scan_parity(cid, transition, B, T, M, G, dtype, extra, algorithm):
+    print(f"[case] {cid} B={B} T={T} M={M} G={G} {dtype} algo={algorithm}", flush=True)
     case = make_case(transition, B, T, M, G, dtype, seed=sum(map(ord, cid)) % 1000, **extra)
     check_case(case)
 
 
-def test_long_real_drift():
+def test_long_real_drift(algorithm):
     """Long real scan with |a| up to 0.9999: chunk carries over 64 chunks keep
     fp32 within 1e-4 of the float64 sequential recurrence, including the last
     step."""
@@ -223,7 +240,7 @@ def test_long_real_drift():
     assert rel_err(y[:, -1], yo[:, -1]) <= 1e-4
 
 
-def test_empty_sequence():
+def test_empty_sequence(algorithm):
     print("[case] empty T=0", flush=True)
     w = torch.zeros(2, 0, 64, device="cuda")
     g = torch.zeros(2, 0, 64, device="cuda")
@@ -254,7 +271,7 @@ def test_workspace_no_spin_errors():
     assert lib.sparc_scan_workspace_error(P(ws), st) == 0
 
 
-def test_deterministic_gradients():
+def test_deterministic_gradients(algorithm):
     """Two backward passes give bit-identical gradients (no float atomics)."""
     print("[case] determinism p1 G=1", flush=True)
     case = make_case("p1", 2, 256, 512, 1, F32, seed=21)
