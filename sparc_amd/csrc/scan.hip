@@ -1600,14 +1600,33 @@ chain_bwd_kernel(ScanArgs p) {
 // per wave).  Same decomposition as the chain kernels above, plus:
 //   * each transition a(step, group) is computed once, by one lane, and
 //     shared through a per-wave LDS table (instead of by every lane of the
-//     group);
-//   * every address is a wave-uniform base plus a fixed per-lane byte offset;
-//   * steps past T and reset steps are folded into the transition table, so
+//     group); steps past T and reset steps are folded into that table, so
 //     the inner loops carry no per-step selects;
+//   * addresses are a wave-uniform running byte offset (scalar registers)
+//     plus a fixed per-lane byte offset;
+//   * the relu(cat) epilogue is a template parameter;
+//   * gate gradients are summed over the lanes of a group with DPP lane
+//     permutations (no LDS round trip);
 //   * the carry entering each chunk lives in LDS; wave k composes only the
 //     maps of waves 0..k-1, the last wave produces the next carry.
 // ---------------------------------------------------------------------------
 constexpr int kFastMaxGpw = 16;  // gate groups per wave handled by the fast kernels
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of lpg lanes (a power of two, uniform), in every lane.
+__device__ __forceinline__ float group_sum(float x, int lpg) {
+  if (lpg >= 2) x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
+  if (lpg >= 4) x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
+  if (lpg >= 8) x += dpp_mov<0x141>(x);  // row_half_mirror: the other quad of the 8 lanes
+  if (lpg >= 16) x += dpp_mov<0x140>(x); // row_mirror: the other half of the 16-lane row
+  if (lpg >= 32) x += __shfl_xor(x, 16, 64);
+  if (lpg >= 64) x += __shfl_xor(x, 32, 64);
+  return x;
+}
 
 // A 64-bit value every lane of the wave holds, moved to scalar registers, so
 // that a memory instruction can take (kernel-argument pointer + this offset)
@@ -1619,29 +1638,47 @@ __device__ __forceinline__ int64_t wave_uniform(int64_t v) {
 }
 
 template <typename T>
-__device__ __forceinline__ T ld_lane(const void* base, int64_t elem_off, uint32_t lane_bytes, int esz) {
-  const char* row = static_cast<const char*>(base) + wave_uniform(elem_off * esz);
-  return *reinterpret_cast<const T*>(row + lane_bytes);
+__device__ __forceinline__ T ldb(const void* base, int64_t byte_off, uint32_t lane_bytes) {
+  return *reinterpret_cast<const T*>(static_cast<const char*>(base) + byte_off + lane_bytes);
 }
 template <typename T>
-__device__ __forceinline__ void st_lane(void* base, int64_t elem_off, uint32_t lane_bytes, int esz, T v) {
-  char* row = static_cast<char*>(base) + wave_uniform(elem_off * esz);
-  *reinterpret_cast<T*>(row + lane_bytes) = v;
+__device__ __forceinline__ void stb(void* base, int64_t byte_off, uint32_t lane_bytes, T v) {
+  *reinterpret_cast<T*>(static_cast<char*>(base) + byte_off + lane_bytes) = v;
 }
 
-// Fills tab[pair] = (ar, ai[, cos phi, sin phi]) for the S x gpw (step, group)
-// pairs of one sub-chunk.  Lane l handles pairs l, l + 64, ...
-template <int TR, typename IO, int S, int TW>
-__device__ __forceinline__ void fill_tab(const ScanArgs& p, int b, int t0, int g_base, int gpw, int lane,
-                                         bool reset_first, const float (&r0)[(S * kFastMaxGpw + 63) / 64],
-                                         const float (&r1)[(S * kFastMaxGpw + 63) / 64], float* tab) {
-  constexpr int R = (S * kFastMaxGpw + 63) / 64;
+constexpr int fast_rounds(int S) { return (S * kFastMaxGpw + 63) / 64; }
+
+// raw gate values of the (step, group) pairs of one sub-chunk; lane l owns
+// pairs l, l + 64, ...  (pair = step * gpw + group)
+template <int TR, typename IO, int S>
+__device__ __forceinline__ void load_gate_pairs(const ScanArgs& p, int b, int t0, int g_base, int gpw, int lane,
+                                                float (&r0)[fast_rounds(S)], float (&r1)[fast_rounds(S)]) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
+  for (int r = 0; r < fast_rounds(S); ++r) {
+    const int idx = r * 64 + lane;
+    r0[r] = 0.0f;
+    r1[r] = 0.0f;
+    if (idx < S * gpw) {
+      const int t = t0 + idx / gpw;
+      if (t < p.T) {
+        const int64_t gi = (static_cast<int64_t>(b) * p.T + t) * p.G + g_base + idx % gpw;
+        r0[r] = load1<IO>(p.g0, gi);
+        if constexpr (TR != TR_REAL) r1[r] = load1<IO>(p.g1, gi);
+      }
+    }
+  }
+}
+
+// tab[pair] = (ar, ai[, cos phi, sin phi]); identity past T, zero at resets
+template <int TR, int S, int TW>
+__device__ __forceinline__ void fill_tab(const ScanArgs& p, int b, int t0, int gpw, int lane, bool reset_first,
+                                         const float (&r0)[fast_rounds(S)], const float (&r1)[fast_rounds(S)],
+                                         float* tab) {
+#pragma unroll
+  for (int r = 0; r < fast_rounds(S); ++r) {
     const int idx = r * 64 + lane;
     if (idx < S * gpw) {
-      const int step = idx / gpw;
-      const int t = t0 + step;
+      const int t = t0 + idx / gpw;
       float ar = 1.0f, ai = 0.0f, cp = 1.0f, sp = 0.0f;
       if (t < p.T) {
         if constexpr (TR == TR_POLAR) {
@@ -1663,44 +1700,19 @@ __device__ __forceinline__ void fill_tab(const ScanArgs& p, int b, int t0, int g
       if constexpr (TW > 2) { e[2] = cp; e[3] = sp; }
     }
   }
-  (void)g_base;
 }
 
-// raw gate values of the pairs of one sub-chunk (prefetched with the inputs)
-template <int TR, typename IO, int S>
-__device__ __forceinline__ void load_gate_pairs(const ScanArgs& p, int b, int t0, int g_base, int gpw, int lane,
-                                                float (&r0)[(S * kFastMaxGpw + 63) / 64],
-                                                float (&r1)[(S * kFastMaxGpw + 63) / 64]) {
-  constexpr int R = (S * kFastMaxGpw + 63) / 64;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int idx = r * 64 + lane;
-    r0[r] = 0.0f;
-    r1[r] = 0.0f;
-    if (idx < S * gpw) {
-      const int t = t0 + idx / gpw;
-      if (t < p.T) {
-        const int64_t gi = (static_cast<int64_t>(b) * p.T + t) * p.G + g_base + idx % gpw;
-        r0[r] = load1<IO>(p.g0, gi);
-        if constexpr (TR != TR_REAL) r1[r] = load1<IO>(p.g1, gi);
-      }
-    }
-  }
-}
-
-template <int TR, typename IO, int V, int S, int NW>
+template <int TR, typename IO, int V, int S, int NW, bool RELU>
 __global__ void __launch_bounds__(NW * 64, 4)
 chain_fwd_fast_kernel(ScanArgs p) {
   constexpr bool CPLX = TR != TR_REAL;
   constexpr int C = S * NW;
   constexpr int MB = 64 * V;
   constexpr int NH = CPLX ? 2 : 1;
-  constexpr int R = (S * kFastMaxGpw + 63) / 64;
+  constexpr int R = fast_rounds(S);
   constexpr int TW = CPLX ? 2 : 1;
   constexpr int ESZ = sizeof(IO);
   using RawT = typename Raw<IO, V>::T;
-  // per wave: sub-chunk map P (NH floats per lane, shared by the lane's modes)
-  // and Q (NH floats per mode)
   __shared__ float s_p[2][NW][NH][64];
   __shared__ float s_q[2][NW][NH][V][64];
   __shared__ float s_carry[2][NH][V][64];
@@ -1713,16 +1725,16 @@ chain_fwd_fast_kernel(ScanArgs p) {
   const int mb = chain - b * p.n_mblocks;
   const int m0 = mb * MB + lane * V;
   const bool lane_ok = m0 < p.M;
-  const int gpw = MB / p.gs;            // gate groups per wave (the tile)
-  const int lpg = p.gs / V;             // lanes per group
+  const int gpw = MB / p.gs;
+  const int lpg = p.gs / V;
   const int my_g = lane / lpg;
   const int g_base = mb * gpw;
-  const bool relu_out = CPLX && (p.flags & SPARC_FLAG_RELU_OUTPUT);
   const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
   const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
-  // element offset of (b, t=0, mode block) in [B,T,M]; rows are M (or 2M) long
   const int64_t row0 = static_cast<int64_t>(b) * p.T;
   const int64_t mbase = static_cast<int64_t>(mb) * MB;
+  const int64_t stride = static_cast<int64_t>(p.M) * ESZ;     // bytes per step, [B,T,M]
+  const int64_t ostride = (RELU ? 2 : 1) * stride;             // bytes per step of y
   float* tab = s_tab[wave];
 
   if (wave == 0) {
@@ -1738,13 +1750,12 @@ chain_fwd_fast_kernel(ScanArgs p) {
   float gr0[2][R], gr1[2][R];
   auto load_chunk = [&](int hb, int c) {
     const int t0 = c * C + wave * S;
+    const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const int t = t0 + s;
-      if (t < p.T && lane_ok) {
-        const int64_t e = (row0 + t) * p.M + mbase;
-        wr[hb][s] = ld_lane<RawT>(p.w_re, e, lane_bytes, ESZ);
-        if constexpr (CPLX) wi[hb][s] = ld_lane<RawT>(p.w_im, e, lane_bytes, ESZ);
+      if (t0 + s < p.T && lane_ok) {
+        wr[hb][s] = ldb<RawT>(p.w_re, off + s * stride, lane_bytes);
+        if constexpr (CPLX) wi[hb][s] = ldb<RawT>(p.w_im, off + s * stride, lane_bytes);
       } else {
         float z[V] = {};
         wr[hb][s] = pack<IO, V>(z);
@@ -1762,8 +1773,7 @@ chain_fwd_fast_kernel(ScanArgs p) {
       if (c >= p.n_chunks) break;
       const int t0 = c * C + wave * S;
       if (c + 1 < p.n_chunks) load_chunk(1 - h, c + 1);
-      // transitions of this sub-chunk: table, then the lane's S values
-      fill_tab<TR, IO, S, TW>(p, b, t0, g_base, gpw, lane, reset_first, gr0[h], gr1[h], tab);
+      fill_tab<TR, S, TW>(p, b, t0, gpw, lane, reset_first, gr0[h], gr1[h], tab);
       __builtin_amdgcn_wave_barrier();
       float ar[S], ai[S];
 #pragma unroll
@@ -1771,7 +1781,7 @@ chain_fwd_fast_kernel(ScanArgs p) {
         ar[s] = tab[(s * gpw + my_g) * TW];
         ai[s] = CPLX ? tab[(s * gpw + my_g) * TW + 1] : 0.0f;
       }
-      // local scan from zero: P (shared), Q (per mode)
+      // local scan from zero: P (shared by the lane's modes), Q (per mode)
       float Pr = 1.0f, Pi = 0.0f, Qr[V], Qi[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) { Qr[v] = 0.0f; Qi[v] = 0.0f; }
@@ -1808,15 +1818,15 @@ chain_fwd_fast_kernel(ScanArgs p) {
         if constexpr (CPLX) s_q[h][wave][1][v][lane] = Qi[v];
       }
       __syncthreads();
-      // start state of this wave: maps 0..wave-1 applied to the chunk carry
-      float sr[V], si[V];
+      // start state of this wave: maps 0..wave-1 applied to the chunk carry;
+      // the last wave also applies its own map: the carry of the next chunk
+      float sr[V], si[V], er[V], ei[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         sr[v] = s_carry[h][0][v][lane];
         si[v] = CPLX ? s_carry[h][1][v][lane] : 0.0f;
       }
       const int n_maps = (wave == NW - 1) ? NW : wave;
-      float er[V], ei[V];
       for (int k = 0; k < n_maps; ++k) {
         if (k == wave) {
 #pragma unroll
@@ -1827,9 +1837,8 @@ chain_fwd_fast_kernel(ScanArgs p) {
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           if constexpr (CPLX) {
-            const float qr = s_q[h][k][0][v][lane], qi = s_q[h][k][1][v][lane];
-            const float nr = fmaf(pr, sr[v], fmaf(-pi, si[v], qr));
-            const float ni = fmaf(pr, si[v], fmaf(pi, sr[v], qi));
+            const float nr = fmaf(pr, sr[v], fmaf(-pi, si[v], s_q[h][k][0][v][lane]));
+            const float ni = fmaf(pr, si[v], fmaf(pi, sr[v], s_q[h][k][1][v][lane]));
             sr[v] = nr;
             si[v] = ni;
           } else {
@@ -1838,7 +1847,6 @@ chain_fwd_fast_kernel(ScanArgs p) {
         }
       }
       if (wave == NW - 1) {
-        // sr/si now hold the state after the chunk; the wave's own start is er/ei
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           s_carry[1 - h][0][v][lane] = sr[v];
@@ -1857,9 +1865,9 @@ chain_fwd_fast_kernel(ScanArgs p) {
       }
       // replay and store
       if (lane_ok) {
+        const int64_t yoff = wave_uniform(((row0 + t0) * (RELU ? 2 * p.M : p.M) + mbase) * ESZ);
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-          const int t = t0 + s;
           float xr[V], xi[V];
           unpack<IO, V>(wr[h][s], xr);
           if constexpr (CPLX) unpack<IO, V>(wi[h][s], xi);
@@ -1874,18 +1882,17 @@ chain_fwd_fast_kernel(ScanArgs p) {
               sr[v] = fmaf(ar[s], sr[v], xr[v]);
             }
           }
-          if (t < p.T) {
-            if (relu_out) {
+          if (t0 + s < p.T) {
+            const int64_t o = yoff + s * ostride;
+            if constexpr (RELU) {
               float rr[V], ri[V];
 #pragma unroll
               for (int v = 0; v < V; ++v) { rr[v] = fmaxf(sr[v], 0.0f); ri[v] = fmaxf(si[v], 0.0f); }
-              const int64_t e = (row0 + t) * 2 * p.M + mbase;
-              st_lane<RawT>(p.y_re, e, lane_bytes, ESZ, pack<IO, V>(rr));
-              st_lane<RawT>(p.y_re, e + p.M, lane_bytes, ESZ, pack<IO, V>(ri));
+              stb<RawT>(p.y_re, o, lane_bytes, pack<IO, V>(rr));
+              stb<RawT>(p.y_re, o + stride, lane_bytes, pack<IO, V>(ri));
             } else {
-              const int64_t e = (row0 + t) * p.M + mbase;
-              st_lane<RawT>(p.y_re, e, lane_bytes, ESZ, pack<IO, V>(sr));
-              if constexpr (CPLX) st_lane<RawT>(p.y_im, e, lane_bytes, ESZ, pack<IO, V>(si));
+              stb<RawT>(p.y_re, o, lane_bytes, pack<IO, V>(sr));
+              if constexpr (CPLX) stb<RawT>(p.y_im, o, lane_bytes, pack<IO, V>(si));
             }
           }
         }
@@ -1894,25 +1901,30 @@ chain_fwd_fast_kernel(ScanArgs p) {
   }
 }
 
-template <int TR, typename IO, int V, int S, int NW>
+template <int TR, typename IO, int V, int S, int NW, bool RELU>
 __global__ void __launch_bounds__(NW * 64, 2)
 chain_bwd_fast_kernel(ScanArgs p) {
   constexpr bool CPLX = TR != TR_REAL;
   constexpr int C = S * NW;
   constexpr int MB = 64 * V;
   constexpr int NH = CPLX ? 2 : 1;
-  constexpr int R = (S * kFastMaxGpw + 63) / 64;
+  constexpr int R = fast_rounds(S);
   constexpr int TW = (TR == TR_POLAR) ? 4 : (CPLX ? 2 : 1);
   constexpr int ESZ = sizeof(IO);
+  constexpr int NG = CPLX ? 2 : 1;    // gate gradients per (step, group)
+  constexpr int RED = S * NG + 1;     // padded LDS row of one lane's partial gate gradients
   using RawT = typename Raw<IO, V>::T;
-  // forward maps: written before barrier B1, read between B1 and B2
+  // Forward maps (s_fp, s_fq) and reverse maps (s_rp, s_rq) of every wave's
+  // sub-chunk.  Without relu both are built before one barrier and read
+  // after it.  With relu the reverse map needs the recomputed states, so the
+  // reverse maps are built after a first barrier and read after a second.
   __shared__ float s_fp[NW][NH][64];
   __shared__ float s_fq[NW][NH][V][64];
-  // reverse maps: written before B2, read after B2 (until the next B1)
   __shared__ float s_rp[NW][NH][64];
   __shared__ float s_rq[NW][NH][V][64];
   __shared__ float s_xi[2][NH][V][64];
   __shared__ float s_tab[NW][S * kFastMaxGpw * TW];
+  __shared__ float s_red[NW][64 * RED];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -1925,12 +1937,14 @@ chain_bwd_fast_kernel(ScanArgs p) {
   const int lpg = p.gs / V;
   const int my_g = lane / lpg;
   const int g_base = mb * gpw;
-  const bool relu_out = CPLX && (p.flags & SPARC_FLAG_RELU_OUTPUT);
   const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
   const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
   const int64_t row0 = static_cast<int64_t>(b) * p.T;
   const int64_t mbase = static_cast<int64_t>(mb) * MB;
+  const int64_t stride = static_cast<int64_t>(p.M) * ESZ;
+  const int64_t dstride = (RELU ? 2 : 1) * stride;  // bytes per step of dy
   float* tab = s_tab[wave];
+  float* red = s_red[wave];
 
   if (wave == 0) {
 #pragma unroll
@@ -1946,20 +1960,19 @@ chain_bwd_fast_kernel(ScanArgs p) {
   float hs[2][V * NH];
   auto load_chunk = [&](int hb, int c) {
     const int t0 = c * C + wave * S;
+    const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
+    const int64_t doff = wave_uniform(((row0 + t0) * (RELU ? 2 * p.M : p.M) + mbase) * ESZ);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const int t = t0 + s;
-      if (t < p.T && lane_ok) {
-        const int64_t e = (row0 + t) * p.M + mbase;
-        wr[hb][s] = ld_lane<RawT>(p.w_re, e, lane_bytes, ESZ);
-        if constexpr (CPLX) wi[hb][s] = ld_lane<RawT>(p.w_im, e, lane_bytes, ESZ);
-        if (relu_out) {
-          const int64_t e2 = (row0 + t) * 2 * p.M + mbase;
-          dr[hb][s] = ld_lane<RawT>(p.dy_re, e2, lane_bytes, ESZ);
-          di[hb][s] = ld_lane<RawT>(p.dy_re, e2 + p.M, lane_bytes, ESZ);
+      if (t0 + s < p.T && lane_ok) {
+        wr[hb][s] = ldb<RawT>(p.w_re, off + s * stride, lane_bytes);
+        if constexpr (CPLX) wi[hb][s] = ldb<RawT>(p.w_im, off + s * stride, lane_bytes);
+        if constexpr (RELU) {
+          dr[hb][s] = ldb<RawT>(p.dy_re, doff + s * dstride, lane_bytes);
+          di[hb][s] = ldb<RawT>(p.dy_re, doff + s * dstride + stride, lane_bytes);
         } else {
-          dr[hb][s] = ld_lane<RawT>(p.dy_re, e, lane_bytes, ESZ);
-          if constexpr (CPLX) di[hb][s] = ld_lane<RawT>(p.dy_im, e, lane_bytes, ESZ);
+          dr[hb][s] = ldb<RawT>(p.dy_re, doff + s * dstride, lane_bytes);
+          if constexpr (CPLX) di[hb][s] = ldb<RawT>(p.dy_im, doff + s * dstride, lane_bytes);
         }
       } else {
         float z[V] = {};
@@ -1997,7 +2010,7 @@ chain_bwd_fast_kernel(ScanArgs p) {
       const int t0 = c * C + wave * S;
       const int xb = c & 1;  // s_xi buffer holding the adjoint entering this chunk
       if (c - 1 >= 0) load_chunk(1 - h, c - 1);
-      fill_tab<TR, IO, S, TW>(p, b, t0, g_base, gpw, lane, reset_first, gr0[h], gr1[h], tab);
+      fill_tab<TR, S, TW>(p, b, t0, gpw, lane, reset_first, gr0[h], gr1[h], tab);
       __builtin_amdgcn_wave_barrier();
       float ar[S], ai[S];
 #pragma unroll
@@ -2036,72 +2049,40 @@ chain_bwd_fast_kernel(ScanArgs p) {
           }
         }
         s_fp[wave][0][lane] = Pr;
-        if constexpr (CPLX) s_fp[wave][1][lane] = Pi;
+        s_rp[wave][0][lane] = Pr;   // the reverse product is the conjugate
+        if constexpr (CPLX) { s_fp[wave][1][lane] = Pi; s_rp[wave][1][lane] = -Pi; }
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           s_fq[wave][0][v][lane] = Qr[v];
           if constexpr (CPLX) s_fq[wave][1][v][lane] = Qi[v];
         }
       }
-      __syncthreads();  // B1
-      float hr[V], hi[V];
+      // output gradient of step s; with relu masked by the state after step s
+      auto dy_raw = [&](int s, float (&gy_r)[V], float (&gy_i)[V]) {
+        unpack<IO, V>(dr[h][s], gy_r);
+        if constexpr (CPLX) unpack<IO, V>(di[h][s], gy_i);
+        else {
 #pragma unroll
-      for (int v = 0; v < V; ++v) { hr[v] = hs[h][v * NH]; hi[v] = CPLX ? hs[h][v * NH + 1] : 0.0f; }
-      for (int k = 0; k < wave; ++k) {
-        const float pr = s_fp[k][0][lane];
-        const float pi = CPLX ? s_fp[k][1][lane] : 0.0f;
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-          if constexpr (CPLX) {
-            const float nr = fmaf(pr, hr[v], fmaf(-pi, hi[v], s_fq[k][0][v][lane]));
-            const float ni = fmaf(pr, hi[v], fmaf(pi, hr[v], s_fq[k][1][v][lane]));
-            hr[v] = nr;
-            hi[v] = ni;
-          } else {
-            hr[v] = fmaf(pr, hr[v], s_fq[k][0][v][lane]);
-          }
+          for (int v = 0; v < V; ++v) gy_i[v] = 0.0f;
         }
-      }
-      // recompute the states before every step; masked output gradient
-      float hpr[S][V], hpi[S][V], gyr[S][V], gyi[S][V];
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        float xr[V], xi[V], yr[V], yi[V];
-        unpack<IO, V>(wr[h][s], xr);
-        unpack<IO, V>(dr[h][s], yr);
-        if constexpr (CPLX) {
-          unpack<IO, V>(wi[h][s], xi);
-          unpack<IO, V>(di[h][s], yi);
-        }
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-          hpr[s][v] = hr[v];
-          hpi[s][v] = CPLX ? hi[v] : 0.0f;
-          if constexpr (CPLX) {
-            const float nr = fmaf(ar[s], hr[v], fmaf(-ai[s], hi[v], xr[v]));
-            const float ni = fmaf(ai[s], hr[v], fmaf(ar[s], hi[v], xi[v]));
-            hr[v] = nr;
-            hi[v] = ni;
-            gyr[s][v] = (relu_out && !(hr[v] > 0.0f)) ? 0.0f : yr[v];
-            gyi[s][v] = (relu_out && !(hi[v] > 0.0f)) ? 0.0f : yi[v];
-          } else {
-            hr[v] = fmaf(ar[s], hr[v], xr[v]);
-            gyr[s][v] = yr[v];
-            gyi[s][v] = 0.0f;
-          }
-        }
-      }
-      // reverse map of the sub-chunk
-      {
+      };
+      // reverse map of the sub-chunk from zero: xi_out = conj(prod a) xi_in + Q
+      auto reverse_map = [&](const float (&hpr)[S + 1][V], const float (&hpi)[S + 1][V]) {
         float Xr[V], Xi[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) { Xr[v] = 0.0f; Xi[v] = 0.0f; }
 #pragma unroll
         for (int s = S - 1; s >= 0; --s) {
+          float gy_r[V], gy_i[V];
+          dy_raw(s, gy_r, gy_i);
 #pragma unroll
           for (int v = 0; v < V; ++v) {
-            const float lr = gyr[s][v] + Xr[v];
-            const float li = gyi[s][v] + Xi[v];
+            if constexpr (RELU) {
+              gy_r[v] = hpr[s + 1][v] > 0.0f ? gy_r[v] : 0.0f;
+              gy_i[v] = hpi[s + 1][v] > 0.0f ? gy_i[v] : 0.0f;
+            }
+            const float lr = gy_r[v] + Xr[v];
+            const float li = gy_i[v] + Xi[v];
             if constexpr (CPLX) {
               Xr[v] = fmaf(ar[s], lr, ai[s] * li);
               Xi[v] = fmaf(ar[s], li, -ai[s] * lr);
@@ -2110,31 +2091,84 @@ chain_bwd_fast_kernel(ScanArgs p) {
             }
           }
         }
-        // product of conj(a) over the sub-chunk = conj of the forward product
-        s_rp[wave][0][lane] = s_fp[wave][0][lane];
-        if constexpr (CPLX) s_rp[wave][1][lane] = -s_fp[wave][1][lane];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           s_rq[wave][0][v][lane] = Xr[v];
           if constexpr (CPLX) s_rq[wave][1][v][lane] = Xi[v];
         }
+      };
+      // start state of this wave: forward maps 0..wave-1 applied to the chunk start
+      auto start_state = [&](float (&hr)[V], float (&hi)[V]) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) { hr[v] = hs[h][v * NH]; hi[v] = CPLX ? hs[h][v * NH + 1] : 0.0f; }
+        for (int k = 0; k < wave; ++k) {
+          const float pr = s_fp[k][0][lane];
+          const float pi = CPLX ? s_fp[k][1][lane] : 0.0f;
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            if constexpr (CPLX) {
+              const float nr = fmaf(pr, hr[v], fmaf(-pi, hi[v], s_fq[k][0][v][lane]));
+              const float ni = fmaf(pr, hi[v], fmaf(pi, hr[v], s_fq[k][1][v][lane]));
+              hr[v] = nr;
+              hi[v] = ni;
+            } else {
+              hr[v] = fmaf(pr, hr[v], s_fq[k][0][v][lane]);
+            }
+          }
+        }
+      };
+      // recompute the state before every step (and after the last one)
+      auto recompute = [&](float (&hr)[V], float (&hi)[V], float (&hpr)[S + 1][V], float (&hpi)[S + 1][V]) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          float xr[V], xi[V];
+          unpack<IO, V>(wr[h][s], xr);
+          if constexpr (CPLX) unpack<IO, V>(wi[h][s], xi);
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            hpr[s][v] = hr[v];
+            hpi[s][v] = CPLX ? hi[v] : 0.0f;
+            if constexpr (CPLX) {
+              const float nr = fmaf(ar[s], hr[v], fmaf(-ai[s], hi[v], xr[v]));
+              const float ni = fmaf(ai[s], hr[v], fmaf(ar[s], hi[v], xi[v]));
+              hr[v] = nr;
+              hi[v] = ni;
+            } else {
+              hr[v] = fmaf(ar[s], hr[v], xr[v]);
+            }
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) { hpr[S][v] = hr[v]; hpi[S][v] = CPLX ? hi[v] : 0.0f; }
+      };
+
+      float hpr[S + 1][V], hpi[S + 1][V];
+      float hr[V], hi[V];
+      if constexpr (!RELU) {
+        reverse_map(hpr, hpi);  // (states unused without relu)
+        __syncthreads();        // maps of all waves visible
+        start_state(hr, hi);
+        recompute(hr, hi, hpr, hpi);
+      } else {
+        __syncthreads();        // B1: forward maps
+        start_state(hr, hi);
+        recompute(hr, hi, hpr, hpi);
+        reverse_map(hpr, hpi);
+        __syncthreads();        // B2: reverse maps
       }
-      __syncthreads();  // B2
       // adjoint entering this wave: reverse maps NW-1 .. wave+1 applied to the chunk's
-      float xr[V], xi[V];
+      float xr[V], xi[V], er[V], ei[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         xr[v] = s_xi[xb][0][v][lane];
         xi[v] = CPLX ? s_xi[xb][1][v][lane] : 0.0f;
       }
       const int k_end = (wave == 0) ? -1 : wave;   // wave 0 also applies map 0 -> next carry
-      float er[V], ei[V];
       for (int k = NW - 1; k > k_end; --k) {
         if (k == wave) {
 #pragma unroll
           for (int v = 0; v < V; ++v) { er[v] = xr[v]; ei[v] = xi[v]; }
         }
-        // conj(P_k) x + Qrev_k
         const float pr = s_rp[k][0][lane];
         const float pi = CPLX ? s_rp[k][1][lane] : 0.0f;
 #pragma unroll
@@ -2150,7 +2184,6 @@ chain_bwd_fast_kernel(ScanArgs p) {
         }
       }
       if (wave == 0) {
-        // xr/xi: adjoint leaving the chunk (entering chunk c-1, or dh0)
         if (c > 0) {
 #pragma unroll
           for (int v = 0; v < V; ++v) {
@@ -2168,57 +2201,84 @@ chain_bwd_fast_kernel(ScanArgs p) {
 #pragma unroll
         for (int v = 0; v < V; ++v) { xr[v] = er[v]; xi[v] = ei[v]; }
       }
-      // final reverse pass
+      // final reverse pass: dw, and every lane's partial transition gradients
+      const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
+      float d0[S], d1[S];
 #pragma unroll
       for (int s = S - 1; s >= 0; --s) {
-        const int t = t0 + s;
-        const bool t_ok = t < p.T;
-        float lr[V], li[V];
+        float gy_r[V], gy_i[V], lr[V], li[V];
+        dy_raw(s, gy_r, gy_i);
 #pragma unroll
-        for (int v = 0; v < V; ++v) { lr[v] = gyr[s][v] + xr[v]; li[v] = gyi[s][v] + xi[v]; }
-        if (lane_ok && t_ok) {
-          const int64_t e = (row0 + t) * p.M + mbase;
-          st_lane<RawT>(p.dw_re, e, lane_bytes, ESZ, pack<IO, V>(lr));
-          if constexpr (CPLX) st_lane<RawT>(p.dw_im, e, lane_bytes, ESZ, pack<IO, V>(li));
+        for (int v = 0; v < V; ++v) {
+          if constexpr (RELU) {
+            gy_r[v] = hpr[s + 1][v] > 0.0f ? gy_r[v] : 0.0f;
+            gy_i[v] = hpi[s + 1][v] > 0.0f ? gy_i[v] : 0.0f;
+          }
+          lr[v] = gy_r[v] + xr[v];
+          li[v] = gy_i[v] + xi[v];
         }
-        // transition gradient summed over the lane's modes
-        float d0 = 0.0f, d1 = 0.0f;
+        if (lane_ok && t0 + s < p.T) {
+          stb<RawT>(p.dw_re, off + s * stride, lane_bytes, pack<IO, V>(lr));
+          if constexpr (CPLX) stb<RawT>(p.dw_im, off + s * stride, lane_bytes, pack<IO, V>(li));
+        }
+        float e0 = 0.0f, e1 = 0.0f;
+        float cp = 1.0f, sp = 0.0f;
+        if constexpr (TR == TR_POLAR) {
+          cp = tab[(s * gpw + my_g) * TW + 2];
+          sp = tab[(s * gpw + my_g) * TW + 3];
+        }
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           if constexpr (CPLX) {
             const float gar = fmaf(lr[v], hpr[s][v], li[v] * hpi[s][v]);
             const float gai = fmaf(li[v], hpr[s][v], -lr[v] * hpi[s][v]);
             if constexpr (TR == TR_POLAR) {
-              const float cp = tab[(s * gpw + my_g) * TW + 2];
-              const float sp = tab[(s * gpw + my_g) * TW + 3];
-              d0 += fmaf(gar, cp, gai * sp);
-              d1 += fmaf(gai, ar[s], -gar * ai[s]);
+              e0 += fmaf(gar, cp, gai * sp);
+              e1 += fmaf(gai, ar[s], -gar * ai[s]);
             } else {
-              d0 += gar;
-              d1 += gai;
+              e0 += gar;
+              e1 += gai;
             }
-          } else {
-            d0 = fmaf(lr[v], hpr[s][v], d0);
-          }
-          if constexpr (CPLX) {
             const float nr = fmaf(ar[s], lr[v], ai[s] * li[v]);
             const float ni = fmaf(ar[s], li[v], -ai[s] * lr[v]);
             xr[v] = nr;
             xi[v] = ni;
           } else {
+            e0 = fmaf(lr[v], hpr[s][v], e0);
             xr[v] = ar[s] * lr[v];
           }
         }
-        for (int off = 1; off < lpg; off <<= 1) {
-          d0 += __shfl_xor(d0, off, 64);
-          if constexpr (CPLX) d1 += __shfl_xor(d1, off, 64);
-        }
-        if (lane_ok && t_ok && (lane & (lpg - 1)) == 0) {
-          // a reset step's transition is the constant 0: no gradient
-          const bool reset = p.segpos ? (p.segpos[row0 + t] == 0) : (reset_first && t == 0);
-          const int64_t gi = (row0 + t) * p.G + g_base + my_g;
-          store1<IO>(p.dg0, gi, reset ? 0.0f : d0);
-          if constexpr (CPLX) store1<IO>(p.dg1, gi, reset ? 0.0f : d1);
+        d0[s] = e0;
+        d1[s] = e1;
+      }
+      // sum the partials of each (step, group) over the group's lanes through
+      // a transpose in LDS; lane l then owns pair l (step l / gpw, group l % gpw)
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        red[lane * RED + s * NG] = d0[s];
+        if constexpr (CPLX) red[lane * RED + s * NG + 1] = d1[s];
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int idx = r * 64 + lane;
+        if (idx < S * gpw) {
+          const int step = idx / gpw;
+          const int g = idx - step * gpw;
+          float a0 = 0.0f, a1 = 0.0f;
+          for (int j = 0; j < lpg; ++j) {
+            const float* src = red + (g * lpg + j) * RED + step * NG;
+            a0 += src[0];
+            if constexpr (CPLX) a1 += src[1];
+          }
+          const int t = t0 + step;
+          if (t < p.T) {
+            // a reset step's transition is the constant 0: no gradient
+            const bool reset = p.segpos ? (p.segpos[row0 + t] == 0) : (reset_first && t == 0);
+            const int64_t gi = (row0 + t) * p.G + g_base + g;
+            store1<IO>(p.dg0, gi, reset ? 0.0f : a0);
+            if constexpr (CPLX) store1<IO>(p.dg1, gi, reset ? 0.0f : a1);
+          }
         }
       }
     }
@@ -2359,10 +2419,17 @@ struct Kernels {
       if (chain && pl.fast) {
         constexpr int FS = 8, FNW = kChunk / FS;
         const dim3 g(static_cast<unsigned>(pl.n_chains));
-        if (dir == 0)
-          hipLaunchKernelGGL((sparc::chain_fwd_fast_kernel<TR, IO, V, FS, FNW>), g, dim3(FNW * 64), 0, st, a);
-        else
-          hipLaunchKernelGGL((sparc::chain_bwd_fast_kernel<TR, IO, V, FS, FNW>), g, dim3(FNW * 64), 0, st, a);
+        const bool relu = (a.flags & SPARC_FLAG_RELU_OUTPUT) != 0;
+        if constexpr (TR == sparc::TR_REAL) {
+          if (dir == 0) hipLaunchKernelGGL((sparc::chain_fwd_fast_kernel<TR, IO, V, FS, FNW, false>), g, dim3(FNW * 64), 0, st, a);
+          else hipLaunchKernelGGL((sparc::chain_bwd_fast_kernel<TR, IO, V, FS, FNW, false>), g, dim3(FNW * 64), 0, st, a);
+        } else if (relu) {
+          if (dir == 0) hipLaunchKernelGGL((sparc::chain_fwd_fast_kernel<TR, IO, V, FS, FNW, true>), g, dim3(FNW * 64), 0, st, a);
+          else hipLaunchKernelGGL((sparc::chain_bwd_fast_kernel<TR, IO, V, FS, FNW, true>), g, dim3(FNW * 64), 0, st, a);
+        } else {
+          if (dir == 0) hipLaunchKernelGGL((sparc::chain_fwd_fast_kernel<TR, IO, V, FS, FNW, false>), g, dim3(FNW * 64), 0, st, a);
+          else hipLaunchKernelGGL((sparc::chain_bwd_fast_kernel<TR, IO, V, FS, FNW, false>), g, dim3(FNW * 64), 0, st, a);
+        }
         return;
       }
     }

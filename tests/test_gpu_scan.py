@@ -272,11 +272,20 @@ def test_workspace_no_spin_errors():
 
 
 def test_deterministic_gradients(algorithm):
-    """Two backward passes give bit-identical gradients (no float atomics)."""
-    print("[case] determinism p1 G=1", flush=True)
+    """No float atomics anywhere: the chain algorithm composes carries in a
+    fixed order and gives bit-identical results run to run.  The look-back
+    algorithm composes whichever predecessor summaries are published when it
+    looks (an inclusive carry, or aggregates of several chunks), so its
+    association order, and with it the last bits of rounding, depends on
+    timing; two runs agree to rounding."""
+    print(f"[case] determinism p1 G=1 algo={algorithm}", flush=True)
     case = make_case("p1", 2, 256, 512, 1, F32, seed=21)
     _, _, g1 = run_gpu(case)
     _, _, g2 = run_gpu(case)
     for a, b in zip(g1, g2):
-        if a is not None:
+        if a is None:
+            continue
+        if algorithm == "chain":
             assert torch.equal(a, b)
+        else:
+            assert rel_err(a, b) <= 1e-6
