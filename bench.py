@@ -84,8 +84,8 @@ def bench_scan(args, dev):
 
     def bwd():
         _lib.check(lib.sparc_scan_backward(
-            ctypes.byref(d), P(r), P(phi), None, None, P(w_re), P(w_im), None, None, None,
-            P(cs), P(dy_re), P(dy_im), None, None, P(dw_re), P(dw_im), P(dr), P(dphi),
+            ctypes.byref(d), P(r), P(phi), None, None, P(w_re), P(w_im), P(y_re), P(y_im),
+            None, None, None, P(cs), P(dy_re), P(dy_im), None, None, P(dw_re), P(dw_im), P(dr), P(dphi),
             None, None, None, None, P(ws_b), ws_b.numel(), st), "backward")
 
     for _ in range(args.warmup):

@@ -125,8 +125,12 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d,
 
 /*
  * Backward of sparc_scan_forward: reverse-time scan of the adjoint
- * lambda_{t-1} = conj(a_t) lambda_t + dy_{t-1}, with states recomputed in
- * fp32 from chunk_state (no [B,T,M] state is saved).  Replaces
+ * lambda_{t-1} = conj(a_t) lambda_t + dy_{t-1}.  The states h_{t-1} that the
+ * transition gradients need are either read from the forward's saved output
+ * (y_re/y_im given, no RELU_OUTPUT: y is h rounded to the I/O dtype, the
+ * states the reference's own backward uses, backward/scan.py:1325-1329), or
+ * recomputed in fp32 from w and chunk_state (no [B,T,M] state is saved).
+ * Replaces
  * _SPARCChunkScan.backward (sparc-kernal/backward/scan.py:1375-1640:
  * _sparc_reverse_chunk_summary / _prefix / _replay and
  * _reduce_shared_control_gradients, backward/control.py:139-152),
@@ -135,6 +139,13 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d,
  * gradient reductions are deterministic (fixed-order partial sums, no float
  * atomics).
  *
+ *   w_re, w_im, chunk_state   as given to / written by the forward (always
+ *                  required: every plan can fall back to recomputing)
+ *   y_re, y_im     [B,T,M] io_dtype: the forward's outputs, or NULL.  Ignored
+ *                  with RELU_OUTPUT.  When given, plans with lane-shared gates
+ *                  (polar, cartesian, real; chain-serial) read the states
+ *                  from them instead of recomputing them; other plans ignore
+ *                  them.
  *   dy_re, dy_im   [B,T,M] io_dtype (or dy_re = [B,T,2M] with RELU_OUTPUT)
  *   dlast_re/_im   [B,M] fp32 gradient of the final state, or NULL
  *   dw_re, dw_im   [B,T,M] io_dtype, written
@@ -146,6 +157,7 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d,
                                  const void* gate0, const void* gate1,
                                  const float* nu_log, const float* theta_log,
                                  const void* w_re, const void* w_im,
+                                 const void* y_re, const void* y_im,
                                  const float* h0_re, const float* h0_im,
                                  const int32_t* segment_pos,
                                  const float* chunk_state,

@@ -82,7 +82,7 @@ def load() -> ctypes.CDLL:
         lib.sparc_scan_workspace_bytes.restype = _SZ
         lib.sparc_scan_forward.argtypes = [D] + [_P] * 13 + [_SZ, _P]
         lib.sparc_scan_forward.restype = ctypes.c_int
-        lib.sparc_scan_backward.argtypes = [D] + [_P] * 23 + [_SZ, _P]
+        lib.sparc_scan_backward.argtypes = [D] + [_P] * 25 + [_SZ, _P]
         lib.sparc_scan_backward.restype = ctypes.c_int
         lib.sparc_scan_workspace_error.argtypes = [_P, _P]
         lib.sparc_scan_workspace_error.restype = ctypes.c_int

@@ -99,6 +99,19 @@ __device__ __forceinline__ void store1(void* base, int64_t index, float v) {
 // math
 // ---------------------------------------------------------------------------
 // exp(x) through the hardware base-2 exponential (v_exp_f32).
+// Workgroups of a launch are handed to the 8 XCDs round-robin (workgroup i
+// runs on XCD i % 8), and each XCD has its own L2.  Renumber workgroups so
+// that consecutive work items (here: neighbouring mode blocks of one batch
+// row, which share the 128-byte cache lines of their gates) run on the same
+// XCD: XCD x takes items [x*per + min(x, rem), ...) in dispatch order.  A
+// bijection on [0, n) for any n.
+__device__ __forceinline__ int xcd_swizzle(int bid, int n) {
+  constexpr int kXcds = 8;
+  const int per = n / kXcds, rem = n % kXcds;
+  const int x = bid % kXcds, k = bid / kXcds;
+  return x * per + (x < rem ? x : rem) + k;
+}
+
 __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }

@@ -1193,6 +1193,7 @@ __device__ __forceinline__ void apply_map(const float (&lds)[NQ][V][64], int lan
 template <int TR, typename IO, int V, int GM, int S, int NW>
 __global__ void __launch_bounds__(NW * 64)
 chain_fwd_kernel(ScanArgs p) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
   using SC = SubChunk<TR, IO, V, GM, S>;
   using TL = typename SC::TL;
   constexpr bool CPLX = TL::CPLX;
@@ -1205,7 +1206,7 @@ chain_fwd_kernel(ScanArgs p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int chain = blockIdx.x;
+  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
   const int b = chain / p.n_mblocks;
   const int mb = chain - b * p.n_mblocks;
   const int m0 = mb * MB + lane * V;
@@ -1299,6 +1300,7 @@ chain_fwd_kernel(ScanArgs p) {
 template <int TR, typename IO, int V, int GM, int S, int NW>
 __global__ void __launch_bounds__(NW * 64)
 chain_bwd_kernel(ScanArgs p) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
   using SC = SubChunk<TR, IO, V, GM, S>;
   using TL = typename SC::TL;
   using GT = typename TL::GT;
@@ -1317,7 +1319,7 @@ chain_bwd_kernel(ScanArgs p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int chain = blockIdx.x;
+  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
   const int b = chain / p.n_mblocks;
   const int mb = chain - b * p.n_mblocks;
   const int m0 = mb * MB + lane * V;
@@ -1705,6 +1707,7 @@ __device__ __forceinline__ void fill_tab(const ScanArgs& p, int b, int t0, int g
 template <int TR, typename IO, int V, int S, int NW, bool RELU>
 __global__ void __launch_bounds__(NW * 64, 4)
 chain_fwd_fast_kernel(ScanArgs p) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
   constexpr bool CPLX = TR != TR_REAL;
   constexpr int C = S * NW;
   constexpr int MB = 64 * V;
@@ -1720,7 +1723,7 @@ chain_fwd_fast_kernel(ScanArgs p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int chain = blockIdx.x;
+  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
   const int b = chain / p.n_mblocks;
   const int mb = chain - b * p.n_mblocks;
   const int m0 = mb * MB + lane * V;
@@ -1904,6 +1907,7 @@ chain_fwd_fast_kernel(ScanArgs p) {
 template <int TR, typename IO, int V, int S, int NW, bool RELU>
 __global__ void __launch_bounds__(NW * 64, 2)
 chain_bwd_fast_kernel(ScanArgs p) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
   constexpr bool CPLX = TR != TR_REAL;
   constexpr int C = S * NW;
   constexpr int MB = 64 * V;
@@ -1915,20 +1919,23 @@ chain_bwd_fast_kernel(ScanArgs p) {
   constexpr int RED = S * NG + 1;     // padded LDS row of one lane's partial gate gradients
   using RawT = typename Raw<IO, V>::T;
   // Forward maps (s_fp, s_fq) and reverse maps (s_rp, s_rq) of every wave's
-  // sub-chunk.  Without relu both are built before one barrier and read
-  // after it.  With relu the reverse map needs the recomputed states, so the
-  // reverse maps are built after a first barrier and read after a second.
-  __shared__ float s_fp[NW][NH][64];
-  __shared__ float s_fq[NW][NH][V][64];
-  __shared__ float s_rp[NW][NH][64];
-  __shared__ float s_rq[NW][NH][V][64];
+  // sub-chunk, in two buffers by chunk parity.  Without relu both are built
+  // before one barrier and read after it; a wave that runs ahead into the
+  // next chunk writes the other buffer, and cannot reach the one after that
+  // before every wave has passed the next chunk's barrier.  With relu the
+  // reverse map needs the recomputed states, so the reverse maps are built
+  // after a first barrier and read after a second.
+  __shared__ float s_fp[2][NW][NH][64];
+  __shared__ float s_fq[2][NW][NH][V][64];
+  __shared__ float s_rp[2][NW][NH][64];
+  __shared__ float s_rq[2][NW][NH][V][64];
   __shared__ float s_xi[2][NH][V][64];
   __shared__ float s_tab[NW][S * kFastMaxGpw * TW];
   __shared__ float s_red[NW][64 * RED];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int chain = blockIdx.x;
+  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
   const int b = chain / p.n_mblocks;
   const int mb = chain - b * p.n_mblocks;
   const int m0 = mb * MB + lane * V;
@@ -2048,13 +2055,13 @@ chain_bwd_fast_kernel(ScanArgs p) {
             Pr *= ar[s];
           }
         }
-        s_fp[wave][0][lane] = Pr;
-        s_rp[wave][0][lane] = Pr;   // the reverse product is the conjugate
-        if constexpr (CPLX) { s_fp[wave][1][lane] = Pi; s_rp[wave][1][lane] = -Pi; }
+        s_fp[xb][wave][0][lane] = Pr;
+        s_rp[xb][wave][0][lane] = Pr;   // the reverse product is the conjugate
+        if constexpr (CPLX) { s_fp[xb][wave][1][lane] = Pi; s_rp[xb][wave][1][lane] = -Pi; }
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-          s_fq[wave][0][v][lane] = Qr[v];
-          if constexpr (CPLX) s_fq[wave][1][v][lane] = Qi[v];
+          s_fq[xb][wave][0][v][lane] = Qr[v];
+          if constexpr (CPLX) s_fq[xb][wave][1][v][lane] = Qi[v];
         }
       }
       // output gradient of step s; with relu masked by the state after step s
@@ -2093,8 +2100,8 @@ chain_bwd_fast_kernel(ScanArgs p) {
         }
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-          s_rq[wave][0][v][lane] = Xr[v];
-          if constexpr (CPLX) s_rq[wave][1][v][lane] = Xi[v];
+          s_rq[xb][wave][0][v][lane] = Xr[v];
+          if constexpr (CPLX) s_rq[xb][wave][1][v][lane] = Xi[v];
         }
       };
       // start state of this wave: forward maps 0..wave-1 applied to the chunk start
@@ -2102,17 +2109,17 @@ chain_bwd_fast_kernel(ScanArgs p) {
 #pragma unroll
         for (int v = 0; v < V; ++v) { hr[v] = hs[h][v * NH]; hi[v] = CPLX ? hs[h][v * NH + 1] : 0.0f; }
         for (int k = 0; k < wave; ++k) {
-          const float pr = s_fp[k][0][lane];
-          const float pi = CPLX ? s_fp[k][1][lane] : 0.0f;
+          const float pr = s_fp[xb][k][0][lane];
+          const float pi = CPLX ? s_fp[xb][k][1][lane] : 0.0f;
 #pragma unroll
           for (int v = 0; v < V; ++v) {
             if constexpr (CPLX) {
-              const float nr = fmaf(pr, hr[v], fmaf(-pi, hi[v], s_fq[k][0][v][lane]));
-              const float ni = fmaf(pr, hi[v], fmaf(pi, hr[v], s_fq[k][1][v][lane]));
+              const float nr = fmaf(pr, hr[v], fmaf(-pi, hi[v], s_fq[xb][k][0][v][lane]));
+              const float ni = fmaf(pr, hi[v], fmaf(pi, hr[v], s_fq[xb][k][1][v][lane]));
               hr[v] = nr;
               hi[v] = ni;
             } else {
-              hr[v] = fmaf(pr, hr[v], s_fq[k][0][v][lane]);
+              hr[v] = fmaf(pr, hr[v], s_fq[xb][k][0][v][lane]);
             }
           }
         }
@@ -2169,17 +2176,17 @@ chain_bwd_fast_kernel(ScanArgs p) {
 #pragma unroll
           for (int v = 0; v < V; ++v) { er[v] = xr[v]; ei[v] = xi[v]; }
         }
-        const float pr = s_rp[k][0][lane];
-        const float pi = CPLX ? s_rp[k][1][lane] : 0.0f;
+        const float pr = s_rp[xb][k][0][lane];
+        const float pi = CPLX ? s_rp[xb][k][1][lane] : 0.0f;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           if constexpr (CPLX) {
-            const float nr = fmaf(pr, xr[v], fmaf(-pi, xi[v], s_rq[k][0][v][lane]));
-            const float ni = fmaf(pr, xi[v], fmaf(pi, xr[v], s_rq[k][1][v][lane]));
+            const float nr = fmaf(pr, xr[v], fmaf(-pi, xi[v], s_rq[xb][k][0][v][lane]));
+            const float ni = fmaf(pr, xi[v], fmaf(pi, xr[v], s_rq[xb][k][1][v][lane]));
             xr[v] = nr;
             xi[v] = ni;
           } else {
-            xr[v] = fmaf(pr, xr[v], s_rq[k][0][v][lane]);
+            xr[v] = fmaf(pr, xr[v], s_rq[xb][k][0][v][lane]);
           }
         }
       }
@@ -2281,6 +2288,287 @@ chain_bwd_fast_kernel(ScanArgs p) {
           }
         }
       }
+    }
+  }
+}
+
+// Backward that reads the states from the saved forward output y (no relu
+// epilogue: y = h rounded to the I/O dtype), as the reference's backward
+// does from its saved out_r/out_i (sparc-kernal/backward/scan.py:1325-1329),
+// instead of recomputing them from w and the chunk states.  Per chunk: the
+// local reverse map of each wave's sub-chunk, one barrier, the composition of
+// the later sub-chunks' maps, and the final reverse pass (dw and the gate
+// gradients, which take h_{t-1} from row t-1 of y, or from h0 at t = 0).
+// Maps are double-buffered by chunk parity, so one barrier per chunk suffices.
+template <int TR, typename IO, int V, int S, int NW>
+__global__ void __launch_bounds__(NW * 64, 2)
+chain_bwd_saved_kernel(ScanArgs p) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
+  constexpr bool CPLX = TR != TR_REAL;
+  constexpr int C = S * NW;
+  constexpr int MB = 64 * V;
+  constexpr int NH = CPLX ? 2 : 1;
+  constexpr int R = fast_rounds(S);
+  constexpr int TW = (TR == TR_POLAR) ? 4 : (CPLX ? 2 : 1);
+  constexpr int ESZ = sizeof(IO);
+  constexpr int NG = CPLX ? 2 : 1;    // gate gradients per (step, group)
+  constexpr int RED = S * NG + 1;     // padded LDS row of one lane's partial gate gradients
+  using RawT = typename Raw<IO, V>::T;
+  __shared__ float s_rp[2][NW][NH][64];
+  __shared__ float s_rq[2][NW][NH][V][64];
+  __shared__ float s_xi[2][NH][V][64];
+  __shared__ float s_tab[NW][S * kFastMaxGpw * TW];
+  __shared__ float s_red[NW][64 * RED];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int b = chain / p.n_mblocks;
+  const int mb = chain - b * p.n_mblocks;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < p.M;
+  const bool block_full = (mb + 1) * MB <= p.M;  // wave-uniform
+  const int gpw = MB / p.gs;
+  const int lpg = p.gs / V;
+  const int my_g = lane / lpg;
+  const int g_base = mb * gpw;
+  const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
+  const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
+  const int64_t row0 = static_cast<int64_t>(b) * p.T;
+  const int64_t mbase = static_cast<int64_t>(mb) * MB;
+  const int64_t stride = static_cast<int64_t>(p.M) * ESZ;
+  float* tab = s_tab[wave];
+  float* red = s_red[wave];
+
+  if (wave == 0) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+      s_xi[(p.n_chunks - 1) & 1][0][v][lane] = (p.dlast_re && lane_ok) ? p.dlast_re[hi] : 0.0f;
+      if constexpr (CPLX) s_xi[(p.n_chunks - 1) & 1][1][v][lane] = (p.dlast_im && lane_ok) ? p.dlast_im[hi] : 0.0f;
+    }
+  }
+
+  // dy rows t0 .. t0+S-1 and y rows t0-1 .. t0+S-2 (the state before each step)
+  RawT dr[2][S], di[2][S], yr[2][S], yi[2][S];
+  float gr0[2][R], gr1[2][R];
+  auto load_chunk = [&](int hb, int c) {
+    const int t0 = c * C + wave * S;
+    const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
+    if (block_full && t0 > 0 && t0 + S <= p.T) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        dr[hb][s] = ldb<RawT>(p.dy_re, off + s * stride, lane_bytes);
+        yr[hb][s] = ldb<RawT>(p.y_re, off + (s - 1) * stride, lane_bytes);
+        if constexpr (CPLX) {
+          di[hb][s] = ldb<RawT>(p.dy_im, off + s * stride, lane_bytes);
+          yi[hb][s] = ldb<RawT>(p.y_im, off + (s - 1) * stride, lane_bytes);
+        }
+      }
+    } else {
+      float z[V] = {};
+      const RawT zero = pack<IO, V>(z);
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int t = t0 + s;
+        dr[hb][s] = zero; di[hb][s] = zero; yr[hb][s] = zero; yi[hb][s] = zero;
+        if (lane_ok && t < p.T) {
+          dr[hb][s] = ldb<RawT>(p.dy_re, off + s * stride, lane_bytes);
+          if constexpr (CPLX) di[hb][s] = ldb<RawT>(p.dy_im, off + s * stride, lane_bytes);
+          if (t > 0) {
+            yr[hb][s] = ldb<RawT>(p.y_re, off + (s - 1) * stride, lane_bytes);
+            if constexpr (CPLX) yi[hb][s] = ldb<RawT>(p.y_im, off + (s - 1) * stride, lane_bytes);
+          }
+        }
+      }
+    }
+    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gr0[hb], gr1[hb]);
+  };
+
+  load_chunk(0, p.n_chunks - 1);
+  for (int c0 = p.n_chunks - 1; c0 >= 0; c0 -= 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = c0 - h;
+      if (c < 0) break;
+      const int t0 = c * C + wave * S;
+      const int xb = c & 1;  // buffers of this chunk (maps, entering adjoint)
+      if (c - 1 >= 0) load_chunk(1 - h, c - 1);
+      fill_tab<TR, S, TW>(p, b, t0, gpw, lane, reset_first, gr0[h], gr1[h], tab);
+      __builtin_amdgcn_wave_barrier();
+      float ar[S], ai[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        ar[s] = tab[(s * gpw + my_g) * TW];
+        ai[s] = CPLX ? tab[(s * gpw + my_g) * TW + 1] : 0.0f;
+      }
+      // reverse map of the sub-chunk from zero: xi_out = conj(prod a) xi_in + X
+      {
+        float Xr[V], Xi[V], Pr = 1.0f, Pi = 0.0f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) { Xr[v] = 0.0f; Xi[v] = 0.0f; }
+#pragma unroll
+        for (int s = S - 1; s >= 0; --s) {
+          float gy_r[V], gy_i[V];
+          unpack<IO, V>(dr[h][s], gy_r);
+          if constexpr (CPLX) unpack<IO, V>(di[h][s], gy_i);
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            if constexpr (CPLX) {
+              const float lr = gy_r[v] + Xr[v];
+              const float li = gy_i[v] + Xi[v];
+              Xr[v] = fmaf(ar[s], lr, ai[s] * li);
+              Xi[v] = fmaf(ar[s], li, -ai[s] * lr);
+            } else {
+              Xr[v] = ar[s] * (gy_r[v] + Xr[v]);
+            }
+          }
+          if constexpr (CPLX) {
+            const float nr = ar[s] * Pr - ai[s] * Pi;
+            const float ni = ar[s] * Pi + ai[s] * Pr;
+            Pr = nr;
+            Pi = ni;
+          } else {
+            Pr *= ar[s];
+          }
+        }
+        s_rp[xb][wave][0][lane] = Pr;
+        if constexpr (CPLX) s_rp[xb][wave][1][lane] = -Pi;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          s_rq[xb][wave][0][v][lane] = Xr[v];
+          if constexpr (CPLX) s_rq[xb][wave][1][v][lane] = Xi[v];
+        }
+      }
+      __syncthreads();  // reverse maps of all waves visible
+      // adjoint entering this wave: maps NW-1 .. wave+1 applied to the chunk's
+      float xr[V], xi[V], er[V], ei[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        xr[v] = s_xi[xb][0][v][lane];
+        xi[v] = CPLX ? s_xi[xb][1][v][lane] : 0.0f;
+      }
+      const int k_end = (wave == 0) ? -1 : wave;   // wave 0 also applies map 0 -> next carry
+      for (int k = NW - 1; k > k_end; --k) {
+        if (k == wave) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) { er[v] = xr[v]; ei[v] = xi[v]; }
+        }
+        const float pr = s_rp[xb][k][0][lane];
+        const float pi = CPLX ? s_rp[xb][k][1][lane] : 0.0f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) {
+            const float nr = fmaf(pr, xr[v], fmaf(-pi, xi[v], s_rq[xb][k][0][v][lane]));
+            const float ni = fmaf(pr, xi[v], fmaf(pi, xr[v], s_rq[xb][k][1][v][lane]));
+            xr[v] = nr;
+            xi[v] = ni;
+          } else {
+            xr[v] = fmaf(pr, xr[v], s_rq[xb][k][0][v][lane]);
+          }
+        }
+      }
+      if (wave == 0) {
+        if (c > 0) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            s_xi[1 - xb][0][v][lane] = xr[v];
+            if constexpr (CPLX) s_xi[1 - xb][1][v][lane] = xi[v];
+          }
+        } else if (lane_ok && p.dh0_re) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const int64_t hi2 = static_cast<int64_t>(b) * p.M + m0 + v;
+            p.dh0_re[hi2] = xr[v];
+            if constexpr (CPLX) p.dh0_im[hi2] = xi[v];
+          }
+        }
+        // wave 0's own entering adjoint, saved before it applied map 0
+#pragma unroll
+        for (int v = 0; v < V; ++v) { xr[v] = er[v]; xi[v] = ei[v]; }
+      }
+      // final reverse pass: dw, and every lane's partial transition gradients
+      const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
+#pragma unroll
+      for (int s = S - 1; s >= 0; --s) {
+        float gy_r[V], gy_i[V], lr[V], li[V], hr[V], hi[V];
+        unpack<IO, V>(dr[h][s], gy_r);
+        unpack<IO, V>(yr[h][s], hr);
+        if constexpr (CPLX) {
+          unpack<IO, V>(di[h][s], gy_i);
+          unpack<IO, V>(yi[h][s], hi);
+        }
+        if (t0 + s == 0) {  // the state before step 0 is h0 (fp32), or zero
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
+            hr[v] = (p.h0_re && lane_ok) ? p.h0_re[i0] : 0.0f;
+            if constexpr (CPLX) hi[v] = (p.h0_im && lane_ok) ? p.h0_im[i0] : 0.0f;
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          lr[v] = gy_r[v] + xr[v];
+          if constexpr (CPLX) li[v] = gy_i[v] + xi[v];
+        }
+        if (lane_ok && t0 + s < p.T) {
+          stb<RawT>(p.dw_re, off + s * stride, lane_bytes, pack<IO, V>(lr));
+          if constexpr (CPLX) stb<RawT>(p.dw_im, off + s * stride, lane_bytes, pack<IO, V>(li));
+        }
+        float e0 = 0.0f, e1 = 0.0f;
+        float cp = 1.0f, sp = 0.0f;
+        if constexpr (TR == TR_POLAR) {
+          cp = tab[(s * gpw + my_g) * TW + 2];
+          sp = tab[(s * gpw + my_g) * TW + 3];
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) {
+            const float gar = fmaf(lr[v], hr[v], li[v] * hi[v]);
+            const float gai = fmaf(li[v], hr[v], -lr[v] * hi[v]);
+            if constexpr (TR == TR_POLAR) {
+              e0 += fmaf(gar, cp, gai * sp);
+              e1 += fmaf(gai, ar[s], -gar * ai[s]);
+            } else {
+              e0 += gar;
+              e1 += gai;
+            }
+            xr[v] = fmaf(ar[s], lr[v], ai[s] * li[v]);
+            xi[v] = fmaf(ar[s], li[v], -ai[s] * lr[v]);
+          } else {
+            e0 = fmaf(lr[v], hr[v], e0);
+            xr[v] = ar[s] * lr[v];
+          }
+        }
+        red[lane * RED + s * NG] = e0;
+        if constexpr (CPLX) red[lane * RED + s * NG + 1] = e1;
+      }
+      // sum the partials of each (step, group) over the group's lanes through
+      // a transpose in LDS; lane l then owns pair l (step l / gpw, group l % gpw)
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int idx = r * 64 + lane;
+        if (idx < S * gpw) {
+          const int step = idx / gpw;
+          const int g = idx - step * gpw;
+          float a0 = 0.0f, a1 = 0.0f;
+          for (int j = 0; j < lpg; ++j) {
+            const float* src = red + (g * lpg + j) * RED + step * NG;
+            a0 += src[0];
+            if constexpr (CPLX) a1 += src[1];
+          }
+          const int t = t0 + step;
+          if (t < p.T) {
+            // a reset step's transition is the constant 0: no gradient
+            const bool reset = p.segpos ? (p.segpos[row0 + t] == 0) : (reset_first && t == 0);
+            const int64_t gi = (row0 + t) * p.G + g_base + g;
+            store1<IO>(p.dg0, gi, reset ? 0.0f : a0);
+            if constexpr (CPLX) store1<IO>(p.dg1, gi, reset ? 0.0f : a1);
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
     }
   }
 }
@@ -2387,19 +2675,23 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl) {
   pl->fast = pl->chain && !p1 && gm == sparc::GATE_LANE && (64 * V) / gs <= sparc::kFastMaxGpw;
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
   const int NQ = cplx ? 4 : 2, NH = cplx ? 2 : 1;
-  size_t off = 256;  // [0] ticket, [1] error
+  // [0] ticket, [1] error; then, for look-back only, one flag and one
+  // aggregate per tile and (backward) the carries; then gradient partials.
+  size_t off = 256;
   pl->flags_off = off;
-  off += ((static_cast<size_t>(pl->n_tiles) * 4 + 255) / 256) * 256;
+  if (!pl->chain) off += ((static_cast<size_t>(pl->n_tiles) * 4 + 255) / 256) * 256;
   pl->agg_off = off;
-  off += ((static_cast<size_t>(pl->n_tiles) * 64 * V * NQ * 4 + 255) / 256) * 256;
+  if (!pl->chain) off += ((static_cast<size_t>(pl->n_tiles) * 64 * V * NQ * 4 + 255) / 256) * 256;
   pl->carry_off = off;
-  if (direction == 1) off += ((static_cast<size_t>(d->batch) * pl->n_chunks * M * NH * 4 + 255) / 256) * 256;
+  if (direction == 1 && !pl->chain)
+    off += ((static_cast<size_t>(d->batch) * pl->n_chunks * M * NH * 4 + 255) / 256) * 256;
   pl->part_off = off;
   pl->part_g_elems = 0;
   pl->part_p_elems = 0;
   if (direction == 1) {
     if (gm == sparc::GATE_CROSS) pl->part_g_elems = d->batch * d->length * pl->n_mblocks;
-    if (p1) pl->part_p_elems = d->batch * static_cast<int64_t>(pl->n_chunks) * M;
+    // P1 nu/theta partials: one row per tile (look-back) or per batch row (chain)
+    if (p1) pl->part_p_elems = d->batch * static_cast<int64_t>(pl->chain ? 1 : pl->n_chunks) * M;
     off += ((static_cast<size_t>(2 * pl->part_g_elems + 2 * pl->part_p_elems) * 4 + 255) / 256) * 256;
   }
   pl->total = off;
@@ -2433,6 +2725,22 @@ struct Kernels {
         return;
       }
     }
+    return run_general(dir, chain, pl, st, a);
+  }
+  // backward from the saved forward output (no relu epilogue); false when
+  // this plan has no such kernel and the caller must fall back to w
+  static bool run_saved(const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
+    if constexpr (TR != sparc::TR_P1 && GM == sparc::GATE_LANE) {
+      if (pl.chain && pl.fast) {
+        constexpr int FS = 8, FNW = kChunk / FS;
+        const dim3 g(static_cast<unsigned>(pl.n_chains));
+        hipLaunchKernelGGL((sparc::chain_bwd_saved_kernel<TR, IO, V, FS, FNW>), g, dim3(FNW * 64), 0, st, a);
+        return true;
+      }
+    }
+    return false;
+  }
+  static void run_general(int dir, bool chain, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
     if (chain) {
       const dim3 g(static_cast<unsigned>(pl.n_chains));
       if (dir == 0)
@@ -2447,14 +2755,18 @@ struct Kernels {
   }
 };
 
+// dir 0: forward, 1: backward (recomputing states from w), 2: backward from
+// the saved forward output if this plan has a kernel for it (returns false
+// without launching anything otherwise)
 template <int TR, typename IO>
-void launch_v(int dir, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
+bool launch_v(int dir, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
   constexpr int VM = (TR == sparc::TR_REAL) ? 4 : 2;
   const int V = pl.V, gm = pl.gm;
 #define SPARC_LAUNCH(VV, GG)                                                            \
   if (V == VV && gm == GG) {                                                           \
+    if (dir == 2) return Kernels<TR, IO, VV, GG>::run_saved(pl, st, a);                  \
     Kernels<TR, IO, VV, GG>::run(dir, pl.chain, pl, st, a);                              \
-    return;                                                                             \
+    return true;                                                                        \
   }
   SPARC_LAUNCH(VM, sparc::GATE_LANE)
   SPARC_LAUNCH(VM, sparc::GATE_CROSS)
@@ -2465,27 +2777,24 @@ void launch_v(int dir, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a)
     SPARC_LAUNCH(1, sparc::GATE_MODE)
   }
 #undef SPARC_LAUNCH
+  return false;
 }
 
-void launch(int dir, const sparc_scan_desc* d, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
+bool launch(int dir, const sparc_scan_desc* d, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
   const bool bf = d->io_dtype == SPARC_BF16;
   switch (d->transition) {
     case SPARC_TRANSITION_P1:
-      if (bf) launch_v<sparc::TR_P1, sparc::bf16>(dir, pl, st, a);
-      else launch_v<sparc::TR_P1, float>(dir, pl, st, a);
-      break;
+      return bf ? launch_v<sparc::TR_P1, sparc::bf16>(dir, pl, st, a)
+                : launch_v<sparc::TR_P1, float>(dir, pl, st, a);
     case SPARC_TRANSITION_POLAR:
-      if (bf) launch_v<sparc::TR_POLAR, sparc::bf16>(dir, pl, st, a);
-      else launch_v<sparc::TR_POLAR, float>(dir, pl, st, a);
-      break;
+      return bf ? launch_v<sparc::TR_POLAR, sparc::bf16>(dir, pl, st, a)
+                : launch_v<sparc::TR_POLAR, float>(dir, pl, st, a);
     case SPARC_TRANSITION_CARTESIAN:
-      if (bf) launch_v<sparc::TR_CART, sparc::bf16>(dir, pl, st, a);
-      else launch_v<sparc::TR_CART, float>(dir, pl, st, a);
-      break;
+      return bf ? launch_v<sparc::TR_CART, sparc::bf16>(dir, pl, st, a)
+                : launch_v<sparc::TR_CART, float>(dir, pl, st, a);
     default:
-      if (bf) launch_v<sparc::TR_REAL, sparc::bf16>(dir, pl, st, a);
-      else launch_v<sparc::TR_REAL, float>(dir, pl, st, a);
-      break;
+      return bf ? launch_v<sparc::TR_REAL, sparc::bf16>(dir, pl, st, a)
+                : launch_v<sparc::TR_REAL, float>(dir, pl, st, a);
   }
 }
 
@@ -2629,6 +2938,7 @@ static sparc_status empty_backward(const sparc_scan_desc* d, const float* dlast_
 sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, const void* gate1,
                                  const float* nu_log, const float* theta_log,
                                  const void* w_re, const void* w_im,
+                                 const void* y_re, const void* y_im,
                                  const float* h0_re, const float* h0_im,
                                  const int32_t* segment_pos, const float* chunk_state,
                                  const void* dy_re, const void* dy_im,
@@ -2655,8 +2965,11 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
   if (p1 && (!nu_log || !theta_log || !dnu_log || !dtheta_log)) return fail(SPARC_EINVAL, "P1 needs nu_log, theta_log, dnu_log, dtheta_log");
   if (cplx && ((dh0_re == nullptr) != (dh0_im == nullptr))) return fail(SPARC_EINVAL, "dh0_re/dh0_im must both be given");
   if (dh0_re && !h0_re) return fail(SPARC_EINVAL, "dh0 requested without h0");
-  const void* ptrs[] = {w_re, w_im, dy_re, relu ? nullptr : dy_im, dw_re, dw_im};
-  if (sparc_status s = check_io_ptrs(d, pl, ptrs, 6)) return s;
+  if (cplx && y_re && !y_im && !relu) return fail(SPARC_EINVAL, "y_im is required with y_re");
+  const bool saved = y_re && !relu;  // y = h (rounded to the I/O dtype) only without the relu epilogue
+  const void* ptrs[] = {w_re, w_im, dy_re, relu ? nullptr : dy_im, dw_re, dw_im,
+                        saved ? y_re : nullptr, saved ? y_im : nullptr};
+  if (sparc_status s = check_io_ptrs(d, pl, ptrs, 8)) return s;
   if (pl.gm == sparc::GATE_MODE) {
     const void* gp[] = {gate0, gate1, dgate0, dgate1};
     if (sparc_status s = check_io_ptrs(d, pl, gp, 4)) return s;
@@ -2681,8 +2994,12 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
   a.dy_re = dy_re; a.dy_im = dy_im; a.dlast_re = dlast_re; a.dlast_im = dlast_im;
   a.dw_re = dw_re; a.dw_im = dw_im; a.dg0 = dgate0; a.dg1 = dgate1;
   a.dh0_re = dh0_re; a.dh0_im = dh0_im;
+  if (saved) {
+    a.y_re = const_cast<void*>(y_re);
+    a.y_im = const_cast<void*>(y_im);
+  }
   fill_ws(a, pl, workspace);
-  launch(1, d, pl, st, a);
+  if (!(saved && launch(2, d, pl, st, a))) launch(1, d, pl, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SPARC_EHIP, "scan backward launch: %s", hipGetErrorString(e));
   // deterministic reductions of the per-tile partials

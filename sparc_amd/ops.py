@@ -90,8 +90,10 @@ def scan_forward_raw(transition, g0, g1, w_re, w_im, nu_log=None, theta_log=None
 def scan_backward_raw(transition, g0, g1, w_re, w_im, chunk_state, dy_re, dy_im,
                       nu_log=None, theta_log=None, h0_re=None, h0_im=None,
                       segment_pos=None, reset_first=False, relu_output=False,
-                      dlast_re=None, dlast_im=None, want_dh0=False):
-    """One backward launch.  Returns dict of gradients."""
+                      dlast_re=None, dlast_im=None, want_dh0=False, y_re=None, y_im=None):
+    """One backward launch.  ``y_re``/``y_im``: the forward's outputs (no relu
+    epilogue), from which plans with lane-shared gates read the states instead
+    of recomputing them.  Returns dict of gradients."""
     lib = _lib.load()
     dev = _lib.require_gpu(g0, w_re, chunk_state, dy_re)
     B, T, M = w_re.shape
@@ -116,7 +118,7 @@ def scan_backward_raw(transition, g0, g1, w_re, w_im, chunk_state, dy_re, dy_im,
     P = _lib.ptr
     _lib.check(lib.sparc_scan_backward(
         ctypes.byref(d), P(g0), P(g1), P(nu_log), P(theta_log), P(w_re), P(w_im),
-        P(h0_re), P(h0_im), P(segment_pos), P(chunk_state), P(dy_re), P(dy_im),
+        P(y_re), P(y_im), P(h0_re), P(h0_im), P(segment_pos), P(chunk_state), P(dy_re), P(dy_im),
         P(dlast_re), P(dlast_im), P(dw_re), P(dw_im), P(dg0), P(dg1), P(dnu), P(dth),
         P(dh0_re), P(dh0_im), P(ws), ws.numel(), _lib.stream_of(dev)), "sparc_scan_backward")
     return dict(dw_re=dw_re, dw_im=dw_im, dg0=dg0, dg1=dg1, dnu=dnu, dth=dth,
@@ -152,7 +154,11 @@ class _ChunkScan(torch.autograd.Function):
             last_re = h0_re.clone() if h0_re is not None else zero
             last_im = (h0_im.clone() if h0_im is not None else zero.clone()) if cplx \
                 else w_re.new_empty(0, dtype=torch.float32)
-        ctx.save_for_backward(g0, g1, nu_log, theta_log, w_re, w_im, h0_re, h0_im, segment_pos, cs)
+        # without the relu epilogue y is the state (rounded to the I/O dtype),
+        # which the backward reads instead of recomputing it
+        saved_y = (None, None) if relu_output else (y_re, y_im)
+        ctx.save_for_backward(g0, g1, nu_log, theta_log, w_re, w_im, h0_re, h0_im, segment_pos, cs,
+                              *saved_y)
         ctx.cfg = (transition, relu_output, reset_first)
         if y_im is None:
             y_im = w_re.new_empty(0)
@@ -161,7 +167,8 @@ class _ChunkScan(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy_re, dy_im, dlast_re, dlast_im):
-        g0, g1, nu_log, theta_log, w_re, w_im, h0_re, h0_im, segment_pos, cs = ctx.saved_tensors
+        g0, g1, nu_log, theta_log, w_re, w_im, h0_re, h0_im, segment_pos, cs, ys_re, ys_im = \
+            ctx.saved_tensors
         transition, relu_output, reset_first = ctx.cfg
         cplx = transition != "real"
         if dy_re is None:
@@ -182,7 +189,7 @@ class _ChunkScan(torch.autograd.Function):
         g = scan_backward_raw(
             transition, g0, g1, w_re, w_im, cs, _c(dy_re).to(w_re.dtype), _c(dy_im).to(w_re.dtype) if dy_im is not None else None,
             nu_log, theta_log, h0_re, h0_im, segment_pos, reset_first, relu_output,
-            dlast_re, dlast_im, want_dh0=h0_re is not None)
+            dlast_re, dlast_im, want_dh0=h0_re is not None, y_re=ys_re, y_im=ys_im)
         return (None, None, None, g["dg0"], g["dg1"], g["dnu"], g["dth"],
                 g["dw_re"], g["dw_im"], g["dh0_re"], g["dh0_im"], None)
 

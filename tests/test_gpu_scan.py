@@ -249,17 +249,20 @@ def test_empty_sequence(algorithm):
     assert last[0].abs().max().item() == 0
 
 
-def test_workspace_no_spin_errors():
+@pytest.mark.parametrize("algo_flag", [4, 8], ids=["lookback", "chain"])
+def test_workspace_no_spin_errors(algo_flag):
     """The look-back waits of a large launch all end without hitting their
-    bound."""
+    bound, and the error word reads 0 after a chain launch too (whose kernels
+    never wait) even when the workspace starts out dirty."""
     import ctypes
     from sparc_amd import _lib
-    print("[case] spin bound B=4 T=2048 M=1024", flush=True)
+    print(f"[case] spin bound B=4 T=2048 M=1024 flags={algo_flag}", flush=True)
     case = make_case("polar", 4, 2048, 1024, 64, BF16, seed=3)
     L = _leaves(case, "cuda")
     lib = _lib.load()
-    d = _lib.ScanDesc(4, 2048, 1024, 64, 1, 1, 1, 0)
-    ws = torch.empty(lib.sparc_scan_workspace_bytes(ctypes.byref(d), 0), dtype=torch.uint8, device="cuda")
+    d = _lib.ScanDesc(4, 2048, 1024, 64, 1, 1, 1, algo_flag)
+    ws = torch.full((lib.sparc_scan_workspace_bytes(ctypes.byref(d), 0),), 255, dtype=torch.uint8,
+                    device="cuda")
     y_re = torch.empty_like(L["w_re"])
     y_im = torch.empty_like(L["w_re"])
     cs = torch.empty(4, lib.sparc_scan_chunk_count(ctypes.byref(d)), 1024, 2, device="cuda")
@@ -289,3 +292,59 @@ def test_deterministic_gradients(algorithm):
             assert torch.equal(a, b)
         else:
             assert rel_err(a, b) <= 1e-6
+
+
+@pytest.mark.parametrize("transition,dtype,G,h0,seg", [
+    ("polar", BF16, 64, True, True),
+    ("cartesian", F32, 32, False, True),
+    ("real", F32, 128, True, False),
+    ("polar", F32, 1024, False, False),
+])
+def test_saved_output_backward_matches_recompute(transition, dtype, G, h0, seg):
+    """The backward that reads the states from the saved forward output and
+    the one that recomputes them from w agree, and both match the oracle
+    (the chain-serial plan, where the saved-output kernel applies)."""
+    print(f"[case] saved-y backward {transition} {dtype} G={G} h0={h0} seg={seg}", flush=True)
+    B, T, M = 2, 640, 2048
+    case = make_case(transition, B, T, M, G, dtype, seed=31, h0=h0, seg=seg, dlast=True)
+    L = _leaves(case, "cuda")
+    cplx = transition != "real"
+    g0, g1 = L["g0"].detach(), (L["g1"].detach() if cplx else None)
+    w_re, w_im = L["w_re"].detach(), (L["w_im"].detach() if cplx else None)
+    init = case["init"]
+    h0_re = h0_im = None
+    if init is not None:
+        h0_re = (init[0] if cplx else init).cuda()
+        h0_im = init[1].cuda() if cplx else None
+    segpos = case["segpos"].cuda() if seg else None
+    dlr = (case["dlast"][0] if cplx else case["dlast"]).cuda()
+    dli = case["dlast"][1].cuda() if cplx else None
+    old = ops.get_algorithm()
+    ops.set_algorithm("chain")
+    try:
+        y_re, y_im, cs = ops.scan_forward_raw(transition, g0, g1, w_re, w_im, None, None,
+                                              h0_re, h0_im, segpos)
+        dy_re = case["dy_re"].cuda()
+        dy_im = case["dy_im"].cuda() if cplx else None
+        kw = dict(h0_re=h0_re, h0_im=h0_im, segment_pos=segpos, dlast_re=dlr, dlast_im=dli,
+                  want_dh0=h0_re is not None)
+        a = ops.scan_backward_raw(transition, g0, g1, w_re, w_im, cs, dy_re, dy_im, **kw)
+        b = ops.scan_backward_raw(transition, g0, g1, w_re, w_im, cs, dy_re, dy_im,
+                                  y_re=y_re, y_im=y_im, **kw)
+    finally:
+        ops.set_algorithm(old)
+    tol = TOL[dtype]
+    for k in a:
+        if a[k] is None:
+            continue
+        # the states differ by the I/O rounding of y; dw/dh0 do not depend on
+        # them (same arithmetic up to instruction order: fp32 agrees to 1e-6,
+        # bf16 outputs to one rounding step, 2^-8 of the largest element)
+        e = rel_err(b[k], a[k])
+        same = 1e-6 if (dtype == F32 or k in ("dh0_re", "dh0_im")) else 2.0 ** -7
+        assert e <= (tol if k in ("dg0", "dg1") else same), f"{k}: {e:.3g}"
+    _, _, gradso = run_oracle(case)
+    names = [k for k in ("g0", "g1", "w_re", "w_im") if case[k] is not None]
+    got = dict(g0=b["dg0"], g1=b["dg1"], w_re=b["dw_re"], w_im=b["dw_im"])
+    for n, go in zip(names, gradso):
+        assert rel_err(got[n], go) <= tol, f"grad {n} vs oracle: {rel_err(got[n], go):.3g}"
