@@ -66,10 +66,14 @@ enum {
    * every (chain, chunk) tile is its own workgroup and chunk carries pass
    * between workgroups (decoupled look-back); parallel over T, for few
    * (batch row, mode block) chains.  CHAIN: one workgroup walks a whole
-   * chain, carries stay on the CU; for many chains.  Same results up to
-   * float rounding; the saved chunk states of either feed either backward. */
+   * chain, carries stay on the CU; for many chains.  SERIAL: one wave walks
+   * a whole chain step by step (no sub-chunk maps, no barriers); for gates
+   * shared by the lanes of a group (polar, cartesian, real) and enough chains
+   * to give every SIMD a wave; other shapes fall back to CHAIN.  Same results
+   * up to float rounding; the saved chunk states of any feed any backward. */
   SPARC_FLAG_ALGO_LOOKBACK = 4,
-  SPARC_FLAG_ALGO_CHAIN = 8
+  SPARC_FLAG_ALGO_CHAIN = 8,
+  SPARC_FLAG_ALGO_SERIAL = 16
 };
 
 typedef struct sparc_scan_desc {

@@ -20,7 +20,9 @@ FLAG_RELU_OUTPUT = 1
 FLAG_RESET_FIRST = 2
 FLAG_ALGO_LOOKBACK = 4
 FLAG_ALGO_CHAIN = 8
-ALGO_FLAGS = {"auto": 0, "lookback": FLAG_ALGO_LOOKBACK, "chain": FLAG_ALGO_CHAIN}
+FLAG_ALGO_SERIAL = 16
+ALGO_FLAGS = {"auto": 0, "lookback": FLAG_ALGO_LOOKBACK, "chain": FLAG_ALGO_CHAIN,
+              "serial": FLAG_ALGO_SERIAL}
 
 # every symbol declared in include/sparc_hip.h
 EXPORTED_SYMBOLS = (

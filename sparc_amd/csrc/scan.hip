@@ -1662,7 +1662,8 @@ __device__ __forceinline__ void load_gate_pairs(const ScanArgs& p, int b, int t0
     r1[r] = 0.0f;
     if (idx < S * gpw) {
       const int t = t0 + idx / gpw;
-      if (t < p.T) {
+      // the last mode block of a row may hold fewer than gpw groups
+      if (t < p.T && g_base + idx % gpw < p.G) {
         const int64_t gi = (static_cast<int64_t>(b) * p.T + t) * p.G + g_base + idx % gpw;
         r0[r] = load1<IO>(p.g0, gi);
         if constexpr (TR != TR_REAL) r1[r] = load1<IO>(p.g1, gi);
@@ -2279,7 +2280,7 @@ chain_bwd_fast_kernel(ScanArgs p) {
             if constexpr (CPLX) a1 += src[1];
           }
           const int t = t0 + step;
-          if (t < p.T) {
+          if (t < p.T && g_base + g < p.G) {  // the last mode block may hold fewer groups
             // a reset step's transition is the constant 0: no gradient
             const bool reset = p.segpos ? (p.segpos[row0 + t] == 0) : (reset_first && t == 0);
             const int64_t gi = (row0 + t) * p.G + g_base + g;
@@ -2559,7 +2560,7 @@ chain_bwd_saved_kernel(ScanArgs p) {
             if constexpr (CPLX) a1 += src[1];
           }
           const int t = t0 + step;
-          if (t < p.T) {
+          if (t < p.T && g_base + g < p.G) {  // the last mode block may hold fewer groups
             // a reset step's transition is the constant 0: no gradient
             const bool reset = p.segpos ? (p.segpos[row0 + t] == 0) : (reset_first && t == 0);
             const int64_t gi = (row0 + t) * p.G + g_base + g;
@@ -2569,6 +2570,339 @@ chain_bwd_saved_kernel(ScanArgs p) {
         }
       }
       __builtin_amdgcn_wave_barrier();
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Serial kernels for lane-shared gates: one wave per chain (batch row, block
+// of 64*V modes) walks every step in order (forward) or in reverse
+// (backward from the saved output).  A step costs one complex multiply-add
+// per mode: no sub-chunk maps, no composition, no barriers.  Parallelism is
+// over chains only, so the plan picks these when every SIMD gets a wave;
+// memory latency is covered by loading the next block of S steps into
+// registers while the current one is computed.
+// ---------------------------------------------------------------------------
+constexpr int kStateChunk = 64;  // steps per saved chunk state
+
+template <int TR, typename IO, int V, int S, bool RELU>
+__global__ void __launch_bounds__(64, 1)
+chain_fwd_serial_kernel(ScanArgs p) {
+  static_assert(kStateChunk % S == 0, "blocks must tile the saved-state chunks");
+  if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
+  constexpr bool CPLX = TR != TR_REAL;
+  constexpr int MB = 64 * V;
+  constexpr int NH = CPLX ? 2 : 1;
+  constexpr int R = fast_rounds(S);
+  constexpr int TW = CPLX ? 2 : 1;
+  constexpr int ESZ = sizeof(IO);
+  using RawT = typename Raw<IO, V>::T;
+  __shared__ float tab[S * kFastMaxGpw * TW];
+
+  const int lane = threadIdx.x;
+  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int b = chain / p.n_mblocks;
+  const int mb = chain - b * p.n_mblocks;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < p.M;
+  const bool block_full = (mb + 1) * MB <= p.M;  // wave-uniform
+  const int gpw = MB / p.gs;
+  const int lpg = p.gs / V;
+  const int my_g = lane / lpg;
+  const int g_base = mb * gpw;
+  const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
+  const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
+  const int64_t row0 = static_cast<int64_t>(b) * p.T;
+  const int64_t mbase = static_cast<int64_t>(mb) * MB;
+  const int64_t stride = static_cast<int64_t>(p.M) * ESZ;   // bytes per step of w
+  const int64_t ostride = (RELU ? 2 : 1) * stride;          // bytes per step of y
+  const int n_blocks = (p.T + S - 1) / S;
+
+  float hr[V], hi[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
+    hr[v] = (p.h0_re && lane_ok) ? p.h0_re[i0] : 0.0f;
+    hi[v] = (CPLX && p.h0_im && lane_ok) ? p.h0_im[i0] : 0.0f;
+  }
+
+  RawT wr[2][S], wi[2][S];
+  float gr0[2][R], gr1[2][R];
+  auto load_block = [&](int hb, int k) {
+    const int t0 = k * S;
+    const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
+    if (block_full && t0 + S <= p.T) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        wr[hb][s] = ldb<RawT>(p.w_re, off + s * stride, lane_bytes);
+        if constexpr (CPLX) wi[hb][s] = ldb<RawT>(p.w_im, off + s * stride, lane_bytes);
+      }
+    } else {
+      float z[V] = {};
+      const RawT zero = pack<IO, V>(z);
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        wr[hb][s] = zero;
+        wi[hb][s] = zero;
+        if (lane_ok && t0 + s < p.T) {
+          wr[hb][s] = ldb<RawT>(p.w_re, off + s * stride, lane_bytes);
+          if constexpr (CPLX) wi[hb][s] = ldb<RawT>(p.w_im, off + s * stride, lane_bytes);
+        }
+      }
+    }
+    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gr0[hb], gr1[hb]);
+  };
+
+  // S steps of one block; FULL: every lane and step in range (no store guards)
+  auto run_block = [&](auto full_tag, int h, int t0) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    const int64_t yoff = wave_uniform(((row0 + t0) * (RELU ? 2 * p.M : p.M) + mbase) * ESZ);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const float ar = tab[(s * gpw + my_g) * TW];
+      const float ai = CPLX ? tab[(s * gpw + my_g) * TW + 1] : 0.0f;
+      float xr[V], xi[V];
+      unpack<IO, V>(wr[h][s], xr);
+      if constexpr (CPLX) unpack<IO, V>(wi[h][s], xi);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if constexpr (CPLX) {
+          const float nr = fmaf(ar, hr[v], fmaf(-ai, hi[v], xr[v]));
+          const float ni = fmaf(ai, hr[v], fmaf(ar, hi[v], xi[v]));
+          hr[v] = nr;
+          hi[v] = ni;
+        } else {
+          hr[v] = fmaf(ar, hr[v], xr[v]);
+        }
+      }
+      if (FULL || (lane_ok && t0 + s < p.T)) {
+        const int64_t o = yoff + s * ostride;
+        if constexpr (RELU) {
+          float rr[V], ri[V];
+#pragma unroll
+          for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
+          stb<RawT>(p.y_re, o, lane_bytes, pack<IO, V>(rr));
+          stb<RawT>(p.y_re, o + stride, lane_bytes, pack<IO, V>(ri));
+        } else {
+          stb<RawT>(p.y_re, o, lane_bytes, pack<IO, V>(hr));
+          if constexpr (CPLX) stb<RawT>(p.y_im, o, lane_bytes, pack<IO, V>(hi));
+        }
+      }
+    }
+  };
+
+  load_block(0, 0);
+  for (int k0 = 0; k0 < n_blocks; k0 += 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = k0 + h;
+      if (k >= n_blocks) break;
+      const int t0 = k * S;
+      if (k + 1 < n_blocks) load_block(1 - h, k + 1);
+      fill_tab<TR, S, TW>(p, b, t0, gpw, lane, reset_first, gr0[h], gr1[h], tab);
+      __builtin_amdgcn_wave_barrier();
+      if (block_full && t0 + S <= p.T) run_block(std::true_type{}, h, t0);
+      else run_block(std::false_type{}, h, t0);
+      // the state after the last step of a saved-state chunk (steps past T
+      // are the identity, so the last block ends on the state after T-1)
+      const int t_end = t0 + S;
+      if (lane_ok && (t_end % kStateChunk == 0 || t_end >= p.T)) {
+        const int c = (min(t_end, p.T) - 1) / kStateChunk;
+        float* dst = p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + c) * p.M + m0) * NH;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          dst[v * NH] = hr[v];
+          if constexpr (CPLX) dst[v * NH + 1] = hi[v];
+        }
+      }
+      __builtin_amdgcn_wave_barrier();  // table reads done before the next fill
+    }
+  }
+}
+
+// Backward from the saved forward output (no relu epilogue), one wave per
+// chain in reverse time: lambda_t = dy_t + conj(a_{t+1}) lambda_{t+1},
+// dw_t = lambda_t, and dL/da_t = lambda_t conj(h_{t-1}) with h_{t-1} read
+// from row t-1 of y (h0 at t = 0).  The transition gradients are summed over
+// the lanes of a group through an LDS transpose once per block, and the
+// polar chain rule (dr, dphi) is applied to the group sums.
+template <int TR, typename IO, int V, int S>
+__global__ void __launch_bounds__(64, 1)
+chain_bwd_serial_kernel(ScanArgs p) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
+  constexpr bool CPLX = TR != TR_REAL;
+  constexpr int MB = 64 * V;
+  constexpr int R = fast_rounds(S);
+  constexpr int TW = (TR == TR_POLAR) ? 4 : (CPLX ? 2 : 1);
+  constexpr int ESZ = sizeof(IO);
+  constexpr int NG = CPLX ? 2 : 1;    // transition gradients per (step, group)
+  constexpr int RED = S * NG + 1;     // padded LDS row of one lane's partials
+  using RawT = typename Raw<IO, V>::T;
+  __shared__ float tab[S * kFastMaxGpw * TW];
+  __shared__ float red[64 * RED];
+
+  const int lane = threadIdx.x;
+  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int b = chain / p.n_mblocks;
+  const int mb = chain - b * p.n_mblocks;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < p.M;
+  const bool block_full = (mb + 1) * MB <= p.M;  // wave-uniform
+  const int gpw = MB / p.gs;
+  const int lpg = p.gs / V;
+  const int my_g = lane / lpg;
+  const int g_base = mb * gpw;
+  const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
+  const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
+  const int64_t row0 = static_cast<int64_t>(b) * p.T;
+  const int64_t mbase = static_cast<int64_t>(mb) * MB;
+  const int64_t stride = static_cast<int64_t>(p.M) * ESZ;
+  const int n_blocks = (p.T + S - 1) / S;
+
+  float xr[V], xi[V];  // conj(a_{t+1}) lambda_{t+1}: the adjoint flowing into step t
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
+    xr[v] = (p.dlast_re && lane_ok) ? p.dlast_re[i0] : 0.0f;
+    xi[v] = (CPLX && p.dlast_im && lane_ok) ? p.dlast_im[i0] : 0.0f;
+  }
+
+  // dy rows t0 .. t0+S-1 and y rows t0-1 .. t0+S-2 (the state before each step)
+  RawT dr[2][S], di[2][S], yr[2][S], yi[2][S];
+  float gr0[2][R], gr1[2][R];
+  auto load_block = [&](int hb, int k) {
+    const int t0 = k * S;
+    const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
+    if (block_full && t0 > 0 && t0 + S <= p.T) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        dr[hb][s] = ldb<RawT>(p.dy_re, off + s * stride, lane_bytes);
+        yr[hb][s] = ldb<RawT>(p.y_re, off + (s - 1) * stride, lane_bytes);
+        if constexpr (CPLX) {
+          di[hb][s] = ldb<RawT>(p.dy_im, off + s * stride, lane_bytes);
+          yi[hb][s] = ldb<RawT>(p.y_im, off + (s - 1) * stride, lane_bytes);
+        }
+      }
+    } else {
+      float z[V] = {};
+      const RawT zero = pack<IO, V>(z);
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int t = t0 + s;
+        dr[hb][s] = zero; di[hb][s] = zero; yr[hb][s] = zero; yi[hb][s] = zero;
+        if (lane_ok && t < p.T) {
+          dr[hb][s] = ldb<RawT>(p.dy_re, off + s * stride, lane_bytes);
+          if constexpr (CPLX) di[hb][s] = ldb<RawT>(p.dy_im, off + s * stride, lane_bytes);
+          if (t > 0) {
+            yr[hb][s] = ldb<RawT>(p.y_re, off + (s - 1) * stride, lane_bytes);
+            if constexpr (CPLX) yi[hb][s] = ldb<RawT>(p.y_im, off + (s - 1) * stride, lane_bytes);
+          }
+        }
+      }
+    }
+    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gr0[hb], gr1[hb]);
+  };
+
+  auto run_block = [&](auto full_tag, int h, int t0) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
+#pragma unroll
+    for (int s = S - 1; s >= 0; --s) {
+      const float ar = tab[(s * gpw + my_g) * TW];
+      const float ai = CPLX ? tab[(s * gpw + my_g) * TW + 1] : 0.0f;
+      float gy_r[V], gy_i[V], hr[V], hi[V], lr[V], li[V];
+      unpack<IO, V>(dr[h][s], gy_r);
+      unpack<IO, V>(yr[h][s], hr);
+      if constexpr (CPLX) {
+        unpack<IO, V>(di[h][s], gy_i);
+        unpack<IO, V>(yi[h][s], hi);
+      }
+      if (!FULL && t0 + s == 0) {  // the state before step 0 is h0 (fp32), or zero
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
+          hr[v] = (p.h0_re && lane_ok) ? p.h0_re[i0] : 0.0f;
+          if constexpr (CPLX) hi[v] = (p.h0_im && lane_ok) ? p.h0_im[i0] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        lr[v] = gy_r[v] + xr[v];
+        if constexpr (CPLX) li[v] = gy_i[v] + xi[v];
+      }
+      if (FULL || (lane_ok && t0 + s < p.T)) {
+        stb<RawT>(p.dw_re, off + s * stride, lane_bytes, pack<IO, V>(lr));
+        if constexpr (CPLX) stb<RawT>(p.dw_im, off + s * stride, lane_bytes, pack<IO, V>(li));
+      }
+      float gar = 0.0f, gai = 0.0f;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if constexpr (CPLX) {
+          gar = fmaf(lr[v], hr[v], fmaf(li[v], hi[v], gar));
+          gai = fmaf(li[v], hr[v], fmaf(-lr[v], hi[v], gai));
+          xr[v] = fmaf(ar, lr[v], ai * li[v]);
+          xi[v] = fmaf(ar, li[v], -ai * lr[v]);
+        } else {
+          gar = fmaf(lr[v], hr[v], gar);
+          xr[v] = ar * lr[v];
+        }
+      }
+      red[lane * RED + s * NG] = gar;
+      if constexpr (CPLX) red[lane * RED + s * NG + 1] = gai;
+    }
+  };
+
+  load_block(0, n_blocks - 1);
+  for (int k0 = n_blocks - 1; k0 >= 0; k0 -= 2) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = k0 - h;
+      if (k < 0) break;
+      const int t0 = k * S;
+      if (k >= 1) load_block(1 - h, k - 1);
+      fill_tab<TR, S, TW>(p, b, t0, gpw, lane, reset_first, gr0[h], gr1[h], tab);
+      __builtin_amdgcn_wave_barrier();
+      if (block_full && t0 > 0 && t0 + S <= p.T) run_block(std::true_type{}, h, t0);
+      else run_block(std::false_type{}, h, t0);
+      __builtin_amdgcn_wave_barrier();
+      // group sums: lane l owns pair l (step l / gpw, group l % gpw)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int idx = r * 64 + lane;
+        if (idx < S * gpw) {
+          const int step = idx / gpw;
+          const int g = idx - step * gpw;
+          float sr = 0.0f, si = 0.0f;
+          for (int j = 0; j < lpg; ++j) {
+            const float* src = red + (g * lpg + j) * RED + step * NG;
+            sr += src[0];
+            if constexpr (CPLX) si += src[1];
+          }
+          const int t = t0 + step;
+          if (t < p.T && g_base + g < p.G) {  // the last mode block may hold fewer groups
+            float d0 = sr, d1 = si;
+            if constexpr (TR == TR_POLAR) {
+              const float* e = tab + idx * TW;   // (ar, ai, cos phi, sin phi) of this pair
+              d0 = fmaf(sr, e[2], si * e[3]);
+              d1 = fmaf(si, e[0], -sr * e[1]);
+            }
+            // a reset step's transition is the constant 0: no gradient
+            const bool reset = p.segpos ? (p.segpos[row0 + t] == 0) : (reset_first && t == 0);
+            const int64_t gi = (row0 + t) * p.G + g_base + g;
+            store1<IO>(p.dg0, gi, reset ? 0.0f : d0);
+            if constexpr (CPLX) store1<IO>(p.dg1, gi, reset ? 0.0f : d1);
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();  // partials and table read before the next block writes them
+    }
+  }
+  if (lane_ok && p.dh0_re) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
+      p.dh0_re[i0] = xr[v];
+      if constexpr (CPLX) p.dh0_im[i0] = xi[v];
     }
   }
 }
@@ -2619,12 +2953,15 @@ constexpr int kChunk = 64;  // C = S * NW for every instantiation
 // Minimum number of chains for the chain-serial kernels (two resident
 // workgroups per CU on a 256-CU MI355X).
 constexpr int kChainMin = 512;
+constexpr int kSerialMin = 1024;  // one wave per chain: a wave for each of the 1024 SIMDs
+static_assert(kChunk == sparc::kStateChunk, "one saved-state chunk length");
 
 struct Plan {
   int V = 1;
   int gm = sparc::GATE_LANE;
   bool chain = false;
   bool fast = false;  // chain kernels specialised for lane-shared gates
+  bool serial = false;  // one wave per chain (lane-shared gates, many chains)
   int n_chunks = 0, n_mblocks = 0, n_chains = 0;
   int64_t n_tiles = 0;
   size_t flags_off = 0, agg_off = 0, carry_off = 0, part_off = 0, total = 0;
@@ -2668,11 +3005,15 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl) {
   pl->n_mblocks = static_cast<int>((M + 64 * V - 1) / (64 * V));
   pl->n_chains = static_cast<int>(d->batch * pl->n_mblocks);
   pl->n_tiles = static_cast<int64_t>(pl->n_chains) * pl->n_chunks;
-  if ((d->flags & SPARC_FLAG_ALGO_LOOKBACK) && (d->flags & SPARC_FLAG_ALGO_CHAIN))
-    return "ALGO_LOOKBACK and ALGO_CHAIN are exclusive";
-  pl->chain = (d->flags & SPARC_FLAG_ALGO_CHAIN) ||
-              (!(d->flags & SPARC_FLAG_ALGO_LOOKBACK) && pl->n_chains >= kChainMin);
-  pl->fast = pl->chain && !p1 && gm == sparc::GATE_LANE && (64 * V) / gs <= sparc::kFastMaxGpw;
+  const bool force_l = (d->flags & SPARC_FLAG_ALGO_LOOKBACK) != 0;
+  const bool force_c = (d->flags & SPARC_FLAG_ALGO_CHAIN) != 0;
+  const bool force_s = (d->flags & SPARC_FLAG_ALGO_SERIAL) != 0;
+  if (int(force_l) + int(force_c) + int(force_s) > 1)
+    return "ALGO_LOOKBACK, ALGO_CHAIN and ALGO_SERIAL are exclusive";
+  const bool lane_shared = !p1 && gm == sparc::GATE_LANE && (64 * V) / gs <= sparc::kFastMaxGpw;
+  pl->serial = lane_shared && (force_s || (!force_l && !force_c && pl->n_chains >= kSerialMin));
+  pl->chain = pl->serial || force_c || force_s || (!force_l && pl->n_chains >= kChainMin);
+  pl->fast = pl->chain && lane_shared;
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
   const int NQ = cplx ? 4 : 2, NH = cplx ? 2 : 1;
   // [0] ticket, [1] error; then, for look-back only, one flag and one
@@ -2698,6 +3039,9 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl) {
   return nullptr;
 }
 
+constexpr int kSerialFwdS = 16;  // steps per prefetched block, serial kernels
+constexpr int kSerialBwdS = 8;
+
 template <int TR, typename IO, int V, int GM>
 struct Kernels {
   // look-back kernels: 8 waves x 8 steps
@@ -2708,6 +3052,14 @@ struct Kernels {
   static constexpr int CS_B = 4, CNW_B = kChunk / CS_B;
   static void run(int dir, bool chain, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
     if constexpr (TR != sparc::TR_P1 && GM == sparc::GATE_LANE) {
+      if (pl.serial && dir == 0) {
+        const dim3 g(static_cast<unsigned>(pl.n_chains));
+        if ((a.flags & SPARC_FLAG_RELU_OUTPUT) && TR != sparc::TR_REAL)
+          hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, true>), g, dim3(64), 0, st, a);
+        else
+          hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, false>), g, dim3(64), 0, st, a);
+        return;
+      }
       if (chain && pl.fast) {
         constexpr int FS = 8, FNW = kChunk / FS;
         const dim3 g(static_cast<unsigned>(pl.n_chains));
@@ -2731,6 +3083,11 @@ struct Kernels {
   // this plan has no such kernel and the caller must fall back to w
   static bool run_saved(const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
     if constexpr (TR != sparc::TR_P1 && GM == sparc::GATE_LANE) {
+      if (pl.serial) {
+        const dim3 g(static_cast<unsigned>(pl.n_chains));
+        hipLaunchKernelGGL((sparc::chain_bwd_serial_kernel<TR, IO, V, kSerialBwdS>), g, dim3(64), 0, st, a);
+        return true;
+      }
       if (pl.chain && pl.fast) {
         constexpr int FS = 8, FNW = kChunk / FS;
         const dim3 g(static_cast<unsigned>(pl.n_chains));

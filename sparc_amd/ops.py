@@ -26,8 +26,9 @@ _algorithm = "auto"
 
 def set_algorithm(name: str) -> None:
     """Scan algorithm for every later call: "auto" (by shape), "lookback"
-    (one workgroup per (chain, chunk) tile, carries between workgroups) or
-    "chain" (one workgroup per (batch row, mode block) chain)."""
+    (one workgroup per (chain, chunk) tile, carries between workgroups),
+    "chain" (one workgroup per (batch row, mode block) chain) or "serial"
+    (one wave per chain, step by step; lane-shared gates only, else "chain")."""
     global _algorithm
     if name not in ALGO_FLAGS:
         raise ValueError(f"unknown scan algorithm {name!r}")

@@ -201,6 +201,8 @@ CASES = [
     ("polar_h0_segments_bf16", "polar", 2, 140, 256, 16, BF16, dict(h0=True, dlast=True, seg=True)),
     ("polar_reset_first_f32", "polar", 1, 70, 256, 16, F32, dict(h0=True, reset_first=True)),
     ("polar_relu_out_bf16", "polar", 2, 96, 256, 16, BF16, dict(relu=True)),
+    ("polar_partial_block_bf16", "polar", 2, 77, 320, 20, BF16, dict(h0=True, dlast=True)),
+    ("cart_partial_block_relu_f32", "cartesian", 1, 33, 192, 24, F32, dict(relu=True, h0=True)),
     ("real_per_element_bf16", "real", 2, 64, 256, 256, BF16, {}),
     ("p1_h0_dlast_f32", "p1", 2, 150, 128, 1, F32, dict(h0=True, dlast=True)),
     ("p1_segments_f32", "p1", 2, 140, 128, 1, F32, dict(h0=True, dlast=True, seg=True)),
@@ -213,7 +215,7 @@ CASES = [
 ]
 
 
-@pytest.fixture(params=["lookback", "chain"])
+@pytest.fixture(params=["lookback", "chain", "serial"])
 def algorithm(request):
     """Runs a test under each scan algorithm (forward and backward)."""
     ops.set_algorithm(request.param)
@@ -249,7 +251,7 @@ def test_empty_sequence(algorithm):
     assert last[0].abs().max().item() == 0
 
 
-@pytest.mark.parametrize("algo_flag", [4, 8], ids=["lookback", "chain"])
+@pytest.mark.parametrize("algo_flag", [4, 8, 16], ids=["lookback", "chain", "serial"])
 def test_workspace_no_spin_errors(algo_flag):
     """The look-back waits of a large launch all end without hitting their
     bound, and the error word reads 0 after a chain launch too (whose kernels
@@ -275,8 +277,8 @@ def test_workspace_no_spin_errors(algo_flag):
 
 
 def test_deterministic_gradients(algorithm):
-    """No float atomics anywhere: the chain algorithm composes carries in a
-    fixed order and gives bit-identical results run to run.  The look-back
+    """No float atomics anywhere: the chain and serial algorithms compose
+    carries in a fixed order and give bit-identical results run to run.  The look-back
     algorithm composes whichever predecessor summaries are published when it
     looks (an inclusive carry, or aggregates of several chunks), so its
     association order, and with it the last bits of rounding, depends on
@@ -288,23 +290,24 @@ def test_deterministic_gradients(algorithm):
     for a, b in zip(g1, g2):
         if a is None:
             continue
-        if algorithm == "chain":
+        if algorithm in ("chain", "serial"):
             assert torch.equal(a, b)
         else:
             assert rel_err(a, b) <= 1e-6
 
 
+@pytest.mark.parametrize("algo", ["chain", "serial"])
 @pytest.mark.parametrize("transition,dtype,G,h0,seg", [
     ("polar", BF16, 64, True, True),
     ("cartesian", F32, 32, False, True),
     ("real", F32, 128, True, False),
     ("polar", F32, 1024, False, False),
 ])
-def test_saved_output_backward_matches_recompute(transition, dtype, G, h0, seg):
+def test_saved_output_backward_matches_recompute(transition, dtype, G, h0, seg, algo):
     """The backward that reads the states from the saved forward output and
     the one that recomputes them from w agree, and both match the oracle
     (the chain-serial plan, where the saved-output kernel applies)."""
-    print(f"[case] saved-y backward {transition} {dtype} G={G} h0={h0} seg={seg}", flush=True)
+    print(f"[case] saved-y backward {transition} {dtype} G={G} h0={h0} seg={seg} {algo}", flush=True)
     B, T, M = 2, 640, 2048
     case = make_case(transition, B, T, M, G, dtype, seed=31, h0=h0, seg=seg, dlast=True)
     L = _leaves(case, "cuda")
@@ -320,7 +323,7 @@ def test_saved_output_backward_matches_recompute(transition, dtype, G, h0, seg):
     dlr = (case["dlast"][0] if cplx else case["dlast"]).cuda()
     dli = case["dlast"][1].cuda() if cplx else None
     old = ops.get_algorithm()
-    ops.set_algorithm("chain")
+    ops.set_algorithm(algo)
     try:
         y_re, y_im, cs = ops.scan_forward_raw(transition, g0, g1, w_re, w_im, None, None,
                                               h0_re, h0_im, segpos)
