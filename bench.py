@@ -8,8 +8,8 @@ single-step decode latency at B=256 (D=2048, N=16, width 2M = 65536).
 
 One step = the forward scan and the backward scan of one batch, inputs
 resident in HBM: the two C-ABI calls sparc_scan_forward / sparc_scan_backward
-(each: a workspace-clear kernel + the scan kernel; the backward also runs its
-gate-gradient reductions when the gate groups span tiles, not at this shape).
+(one kernel each at this shape: the serial one-wave-per-chain kernels; the
+backward reads the states from the forward's saved output).
 
 Algorithmic bytes per step, B*T*(M*10*s + G*6*s_g) with s = s_g = 2:
   forward : read w (re, im), write y (re, im)      -> 8 B per mode-step
@@ -34,6 +34,29 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_FILE = os.path.join("profiles", "scan_cfg2_hbm_traffic.md")
+# kernels each algorithm runs at this shape (backward, forward)
+ALGO_KERNELS = {"auto": ("chain_bwd_serial_kernel", "chain_fwd_serial_kernel"),
+                "serial": ("chain_bwd_serial_kernel", "chain_fwd_serial_kernel"),
+                "chain": ("chain_bwd_saved_kernel", "chain_fwd_fast_kernel"),
+                "lookback": ("scan_bwd_kernel", "scan_fwd_kernel")}
+
+
+def measured_traffic() -> dict:
+    """HBM bytes per launch by kernel name, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (calibrated against a 1 GiB copy); empty
+    if the file is absent."""
+    out = {}
+    try:
+        with open(os.path.join(ROOT, TRAFFIC_FILE)) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic":
+                    out[parts[1]] = int(parts[2])
+    except OSError:
+        pass
+    return out
 
 
 def cpu_model() -> str:
@@ -223,8 +246,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--algo", default="auto", choices=["auto", "chain", "lookback"],
-                    help="scan algorithm (auto picks chain-serial at this shape)")
+    ap.add_argument("--algo", default="auto", choices=["auto", "serial", "chain", "lookback"],
+                    help="scan algorithm (auto picks the serial kernels at this shape)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first copy 1 GiB device-to-device (a kernel of known traffic, "
                          "to calibrate the FETCH_SIZE/WRITE_SIZE counters)")
@@ -247,17 +270,21 @@ def main():
     res = bench_scan(args, dev)
     dec = None if args.no_decode else bench_decode(args, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
+    k_bwd, k_fwd = ALGO_KERNELS[args.algo]
+    traffic = measured_traffic()
     roof = {
         "bound": "hbm",
-        "kernel": f"backward scan, algorithm={args.algo} (polar, bf16, V=2, lane-shared gates)",
+        "kernel": f"{k_bwd} (backward scan, polar, bf16 I/O, fp32 state, 2 modes per lane)",
         "achieved": round(res["bwd_gbs"], 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(res["bwd_gbs"] / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": traffic.get(k_bwd),
+        "traffic_source": TRAFFIC_FILE if k_bwd in traffic else None,
         "bytes_per_launch": res["bytes_bwd"],
         "avg_launch_ms": round(res["bwd_ms"], 4),
-        "forward": {"achieved": round(res["fwd_gbs"], 1), "frac": round(res["fwd_gbs"] / HBM_PEAK_GBS, 4),
+        "forward": {"kernel": k_fwd, "achieved": round(res["fwd_gbs"], 1),
+                    "frac": round(res["fwd_gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic.get(k_fwd),
                     "bytes_per_launch": res["bytes_fwd"], "avg_launch_ms": round(res["fwd_ms"], 4)},
         "step_frac": round(res["step_gbs"] / HBM_PEAK_GBS, 4),
     }
@@ -272,11 +299,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 I/O, fp32 state",
+        "dtype": "f32",
         "data": "synthetic: w, dy ~ N(0,1); r = sigmoid(N(2,1)); phi ~ U(-pi,pi)",
         "config": {"workload": "complex chunked scan fwd+bwd (polar gates shared per channel)",
                    "B": res["B"], "T": res["T"], "D": res["D"], "N": res["N"], "M": res["M"],
-                   "G": res["G"], "parallelism": "single GPU"},
+                   "G": res["G"], "io_dtype": "bf16", "state_dtype": "f32", "algorithm": args.algo,
+                   "parallelism": "single GPU"},
         "roofline": roof,
         "decode": None if dec is None else {
             "us_per_step": round(dec["us_per_step"], 2), "tokens_per_s": round(dec["tokens_per_s"], 1),

@@ -3039,8 +3039,15 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl) {
   return nullptr;
 }
 
-constexpr int kSerialFwdS = 16;  // steps per prefetched block, serial kernels
-constexpr int kSerialBwdS = 8;
+// steps per prefetched block of the serial kernels (compile-time tunable)
+#ifndef SPARC_SERIAL_FWD_S
+#define SPARC_SERIAL_FWD_S 16
+#endif
+#ifndef SPARC_SERIAL_BWD_S
+#define SPARC_SERIAL_BWD_S 8
+#endif
+constexpr int kSerialFwdS = SPARC_SERIAL_FWD_S;
+constexpr int kSerialBwdS = SPARC_SERIAL_BWD_S;
 
 template <int TR, typename IO, int V, int GM>
 struct Kernels {
