@@ -150,6 +150,66 @@ def bench_scan(args, dev):
     )
 
 
+def _graph_time_us(dev, n_graph, reps, step_fn):
+    """Captures reps HIP graphs of n_graph calls step_fn(i) (i = global step)
+    after one eager call, replays them all once untimed and once timed;
+    returns microseconds per step."""
+    step_fn(0)
+    torch.cuda.synchronize(dev)
+    graphs = []
+    cap_stream = torch.cuda.Stream(dev)
+    cap_stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(cap_stream):
+        for rep in range(reps):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=cap_stream):
+                for i in range(n_graph):
+                    step_fn(rep * n_graph + i)
+            graphs.append(gr)
+    torch.cuda.current_stream(dev).wait_stream(cap_stream)
+    torch.cuda.synchronize(dev)
+    for gr in graphs[:1]:
+        gr.replay()
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s = torch.cuda.current_stream(dev)
+    e0.record(s)
+    for gr in graphs:
+        gr.replay()
+    e1.record(s)
+    torch.cuda.synchronize(dev)
+    return e0.elapsed_time(e1) * 1e3 / (n_graph * reps)
+
+
+def bench_decode_core(args, dev):
+    """cfg4, scan-core form: B=256 rows, M = 32768 modes (D=2048, N=16), fresh
+    bf16 writes and fresh polar gates per (row, channel) every step (the cfg2
+    distributions), fp32 state N(0, 0.1) updated in place by sparc_scan_step;
+    steps replayed from captured HIP graphs of 100 steps."""
+    from sparc_amd import ops
+    B, D, N = 256, 2048, 16
+    M, G = D * N, D
+    n_graph = 100
+    reps = max(1, args.decode_steps // n_graph)
+    n = n_graph * reps
+    g = torch.Generator(device=dev).manual_seed(2)
+    w_re = torch.randn(n, B, M, device=dev, generator=g, dtype=torch.bfloat16)
+    w_im = torch.randn(n, B, M, device=dev, generator=g, dtype=torch.bfloat16)
+    r = torch.sigmoid(torch.randn(n, B, G, device=dev, generator=g) + 2.0).to(torch.bfloat16)
+    phi = ((torch.rand(n, B, G, device=dev, generator=g) * 2 - 1) * math.pi).to(torch.bfloat16)
+    sr = 0.1 * torch.randn(B, M, device=dev, generator=g)
+    si = 0.1 * torch.randn(B, M, device=dev, generator=g)
+
+    def step(i):
+        ops.scan_step("polar", r[i], phi[i], w_re[i], w_im[i], (sr, si))
+
+    us = _graph_time_us(dev, n_graph, reps, step)
+    bytes_step = B * (M * 20 + G * 4)  # state read + written (16 B), w (4 B), gates (4 B per group)
+    del w_re, w_im, r, phi
+    return dict(B=B, M=M, G=G, steps=n, us_per_step=us, tokens_per_s=B / (us * 1e-6),
+                bytes_per_step=bytes_step, gbs=bytes_step / (us * 1e-6) / 1e9)
+
+
 def bench_decode(args, dev):
     """cfg4: B=256 rows, width 65536 (M = 32768 = D*N, D=2048, N=16), fresh
     bf16 x every step, fp32 state N(0, 0.1) updated in place; steps replayed
@@ -168,41 +228,21 @@ def bench_decode(args, dev):
         m.write_radial_response.normal_()
     m.prepare_inference()
     n_graph = 100
-    steps = args.decode_steps
-    reps = max(1, steps // n_graph)
+    reps = max(1, args.decode_steps // n_graph)
     g = torch.Generator(device=dev).manual_seed(1)
     xs = torch.randn(n_graph * reps, B, width, device=dev, generator=g, dtype=torch.bfloat16)
     sr = 0.1 * torch.randn(B, M, device=dev, generator=g)
     si = 0.1 * torch.randn(B, M, device=dev, generator=g)
-    # one eager step first (validates arguments, warms the allocator)
-    y0, _ = latest_sparc_decode(m, xs[0], (sr, si), out_state=(sr, si))
-    torch.cuda.synchronize(dev)
-    graphs = []
-    cap_stream = torch.cuda.Stream(dev)
-    cap_stream.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(cap_stream):
-        for rep in range(reps):
-            gr = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(gr, stream=cap_stream):
-                for i in range(n_graph):
-                    latest_sparc_decode(m, xs[rep * n_graph + i], (sr, si), out_state=(sr, si))
-            graphs.append(gr)
-    torch.cuda.current_stream(dev).wait_stream(cap_stream)
-    torch.cuda.synchronize(dev)
-    for gr in graphs[:1]:
-        gr.replay()
-    torch.cuda.synchronize(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s = torch.cuda.current_stream(dev)
-    e0.record(s)
-    for gr in graphs:
-        gr.replay()
-    e1.record(s)
-    torch.cuda.synchronize(dev)
-    us = e0.elapsed_time(e1) * 1e3 / (n_graph * reps)
+
+    def step(i):
+        latest_sparc_decode(m, xs[i], (sr, si), out_state=(sr, si))
+
+    us = _graph_time_us(dev, n_graph, reps, step)
     bytes_step = B * M * 24
+    del xs
     return dict(B=B, D=D, N=N, M=M, steps=n_graph * reps, us_per_step=us,
-                tokens_per_s=B / (us * 1e-6), gbs=bytes_step / (us * 1e-6) / 1e9)
+                tokens_per_s=B / (us * 1e-6), bytes_per_step=bytes_step,
+                gbs=bytes_step / (us * 1e-6) / 1e9)
 
 
 def cpu_baseline(args):
@@ -268,6 +308,7 @@ def main():
         torch.cuda.synchronize(dev)
         del src, dst
     res = bench_scan(args, dev)
+    core = None if args.no_decode else bench_decode_core(args, dev)
     dec = None if args.no_decode else bench_decode(args, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
     k_bwd, k_fwd = ALGO_KERNELS[args.algo]
@@ -306,10 +347,16 @@ def main():
                    "G": res["G"], "io_dtype": "bf16", "state_dtype": "f32", "algorithm": args.algo,
                    "parallelism": "single GPU"},
         "roofline": roof,
-        "decode": None if dec is None else {
-            "us_per_step": round(dec["us_per_step"], 2), "tokens_per_s": round(dec["tokens_per_s"], 1),
-            "steps": dec["steps"], "B": dec["B"], "M": dec["M"], "GB_s_module_bytes": round(dec["gbs"], 1),
-            "mode": "SPARCMixer.step semantics, bf16 x/y, fp32 state in place, HIP graph of 100 steps"},
+        "decode": None if core is None else {
+            "us_per_step": round(core["us_per_step"], 2), "tokens_per_s": round(core["tokens_per_s"], 1),
+            "steps": core["steps"], "B": core["B"], "M": core["M"], "G": core["G"],
+            "bytes_per_step": core["bytes_per_step"], "GB_s": round(core["gbs"], 1),
+            "form": "scan-core step (sparc_scan_step): fresh bf16 writes and polar gates each step, "
+                    "fp32 state in place, HIP graphs of 100 steps",
+            "module": {
+                "us_per_step": round(dec["us_per_step"], 2), "tokens_per_s": round(dec["tokens_per_s"], 1),
+                "steps": dec["steps"], "bytes_per_step": dec["bytes_per_step"], "GB_s": round(dec["gbs"], 1),
+                "form": "SPARCMixer.step (P1 controls and write from x), bf16 x/y, fp32 state in place"}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -240,6 +240,30 @@ sparc_status sparc_decode_step(int64_t batch, int64_t modes, int32_t io_dtype,
                                sparc_stream_t stream);
 
 /*
+ * One step of the scan for B independent rows, with the state carried by the
+ * caller: h <- a h + w, fp32 state updated in place (the scan-core decode
+ * step).  The same as sparc_scan_forward with T = 1 and h0 = state: the
+ * reference's serial scan with an initial state at L = 1
+ * (_sparc_tiled_serial_forward, sparc-kernal/forward/scan.py:806-854, as
+ * called by sparc_scan_with_last, sparc-kernal/backward/scan.py:1857-1877).
+ *   d             batch, modes, groups, transition, dtypes; flags RELU_OUTPUT
+ *                 (y layout) and RESET_FIRST (a := 0); length is ignored
+ *   gate0, gate1  [B,G] (fp32 eta, delta for P1)
+ *   nu_log, theta_log [M] fp32 (P1 only)
+ *   w_re, w_im    [B,M] io_dtype
+ *   state_re/_im  [B,M] fp32, read and written
+ *   y_re, y_im    [B,M] io_dtype copy of the new state (or y_re = relu(cat)
+ *                 [B,2M] with RELU_OUTPUT), or NULL for none
+ */
+sparc_status sparc_scan_step(const sparc_scan_desc* d,
+                             const void* gate0, const void* gate1,
+                             const float* nu_log, const float* theta_log,
+                             const void* w_re, const void* w_im,
+                             float* state_re, float* state_im,
+                             void* y_re, void* y_im,
+                             sparc_stream_t stream);
+
+/*
  * Deterministic sum over rows of a [rows, cols] fp32 matrix into [cols]
  * (or accumulate into out when accumulate != 0).  Used for the reductions of
  * per-tile partial gradients.

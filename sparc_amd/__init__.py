@@ -15,6 +15,7 @@ from .ops import (
     real_chunk_scan,
     real_scan,
     real_scan_with_last,
+    scan_step,
     sparc_chunk_scan,
     sparc_scan,
     sparc_scan_with_last,
@@ -28,5 +29,5 @@ __all__ = [
     "prepare_decode", "run_decode_step", "latest_sparc_decode", "chunk_scan", "complex_scan",
     "complex_scan_with_last", "real_scan", "real_chunk_scan", "real_scan_with_last",
     "sparc_scan", "sparc_scan_with_last", "sparc_chunk_scan", "sparc_tiled_serial_scan",
-    "sparc_training_scan_dispatch", "polar_chunk_scan", "grouped_real_scan",
+    "sparc_training_scan_dispatch", "polar_chunk_scan", "grouped_real_scan", "scan_step",
 ]

@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "sparc_write_workspace_bytes",
     "sparc_write_backward",
     "sparc_decode_step",
+    "sparc_scan_step",
     "sparc_column_sum",
     "sparc_last_error",
     "sparc_version",
@@ -96,6 +97,8 @@ def load() -> ctypes.CDLL:
         lib.sparc_write_backward.restype = ctypes.c_int
         lib.sparc_decode_step.argtypes = [_I64, _I64, _I32] + [_P] * 14
         lib.sparc_decode_step.restype = ctypes.c_int
+        lib.sparc_scan_step.argtypes = [D] + [_P] * 10 + [_P]
+        lib.sparc_scan_step.restype = ctypes.c_int
         lib.sparc_column_sum.argtypes = [_I64, _I64, _P, _P, ctypes.c_int, _P]
         lib.sparc_column_sum.restype = ctypes.c_int
         lib.sparc_last_error.argtypes = []

@@ -28,6 +28,9 @@ __device__ __forceinline__ uint16_t pack_bf16(float v) {
   return (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
 }
 
+// transitions (values of sparc_transition)
+enum Transition : int { TR_P1 = 0, TR_POLAR = 1, TR_CART = 2, TR_REAL = 3 };
+
 // Raw vector of V elements of type IO, loaded/stored with one instruction.
 template <typename IO, int V> struct Raw;
 template <> struct Raw<bf16, 1> { using T = uint16_t; };
@@ -98,7 +101,6 @@ __device__ __forceinline__ void store1(void* base, int64_t index, float v) {
 // ---------------------------------------------------------------------------
 // math
 // ---------------------------------------------------------------------------
-// exp(x) through the hardware base-2 exponential (v_exp_f32).
 // Workgroups of a launch are handed to the 8 XCDs round-robin (workgroup i
 // runs on XCD i % 8), and each XCD has its own L2.  Renumber workgroups so
 // that consecutive work items (here: neighbouring mode blocks of one batch
@@ -112,6 +114,7 @@ __device__ __forceinline__ int xcd_swizzle(int bid, int n) {
   return x * per + (x < rem ? x : rem) + k;
 }
 
+// exp(x) through the hardware base-2 exponential (v_exp_f32).
 __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }

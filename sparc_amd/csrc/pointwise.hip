@@ -254,6 +254,90 @@ decode_kernel(int M, const void* x, const float* pdir, const float* rdir,
   }
 }
 
+// ---------------------------------------------------------------------------
+// one scan step h <- a h + w for B rows, fp32 state in place (scan-core decode)
+// ---------------------------------------------------------------------------
+// SV modes per thread (4: one 16-byte state load per plane).  A thread's modes
+// lie in one gate group when the group size is a multiple of SV, and then a
+// polar, cartesian or real transition is computed once per thread.
+template <int TR, typename IO, int SV, bool RELU>
+__global__ void __launch_bounds__(256)
+scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* g0, const void* g1,
+                 const float* nu_log, const float* theta_log, const void* w_re, const void* w_im,
+                 float* st_re, float* st_im, void* y_re, void* y_im) {
+  constexpr bool CPLX = TR != TR_REAL;
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (q >= n_items) return;
+  const int64_t i = q * SV;  // flat index b*M + m
+  const int b = static_cast<int>(i / M);
+  const int m = static_cast<int>(i - static_cast<int64_t>(b) * M);
+  float hr[SV], hi[SV], wr[SV], wi[SV];
+  unpack<float, SV>(load_raw<float, SV>(st_re, i), hr);
+  unpack<IO, SV>(load_raw<IO, SV>(w_re, i), wr);
+  if constexpr (CPLX) {
+    unpack<float, SV>(load_raw<float, SV>(st_im, i), hi);
+    unpack<IO, SV>(load_raw<IO, SV>(w_im, i), wi);
+  }
+  // P1 transitions also depend on each mode's nu and theta
+  const bool shared = TR != TR_P1 && gs % SV == 0;  // uniform over the launch
+  float ar[SV], ai[SV];
+#pragma unroll
+  for (int v = 0; v < SV; ++v) {
+    if (v > 0 && shared) { ar[v] = ar[0]; ai[v] = ai[0]; continue; }
+    const int64_t gi = static_cast<int64_t>(b) * G + (m + v) / gs;
+    if constexpr (TR == TR_P1) {
+      const float eta = static_cast<const float*>(g0)[gi];
+      const float delta = static_cast<const float*>(g1)[gi];
+      const float nu = expf(nu_log[m + v]);
+      const float theta = expf(theta_log[m + v]);
+      const float rho = expf(-nu * expf(eta));
+      float sn, cs;
+      sincosf(theta + (1.0f - rho) * delta, &sn, &cs);
+      ar[v] = rho * cs;
+      ai[v] = rho * sn;
+    } else if constexpr (TR == TR_POLAR) {
+      const float r = load1<IO>(g0, gi);
+      float sn, cs;
+      sincos_moderate(load1<IO>(g1, gi), sn, cs);
+      ar[v] = r * cs;
+      ai[v] = r * sn;
+    } else if constexpr (TR == TR_CART) {
+      ar[v] = load1<IO>(g0, gi);
+      ai[v] = load1<IO>(g1, gi);
+    } else {
+      ar[v] = load1<IO>(g0, gi);
+      ai[v] = 0.0f;
+    }
+    if (reset) { ar[v] = 0.0f; ai[v] = 0.0f; }
+  }
+#pragma unroll
+  for (int v = 0; v < SV; ++v) {
+    if constexpr (CPLX) {
+      const float nr = fmaf(ar[v], hr[v], fmaf(-ai[v], hi[v], wr[v]));
+      const float ni = fmaf(ai[v], hr[v], fmaf(ar[v], hi[v], wi[v]));
+      hr[v] = nr;
+      hi[v] = ni;
+    } else {
+      hr[v] = fmaf(ar[v], hr[v], wr[v]);
+    }
+  }
+  store_raw<float, SV>(st_re, i, pack<float, SV>(hr));
+  if constexpr (CPLX) store_raw<float, SV>(st_im, i, pack<float, SV>(hi));
+  if (y_re) {
+    if constexpr (RELU) {
+      float rr[SV], ri[SV];
+#pragma unroll
+      for (int v = 0; v < SV; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
+      const int64_t yrow = static_cast<int64_t>(b) * 2 * M + m;
+      store_raw<IO, SV>(y_re, yrow, pack<IO, SV>(rr));
+      store_raw<IO, SV>(y_re, yrow + M, pack<IO, SV>(ri));
+    } else {
+      store_raw<IO, SV>(y_re, i, pack<IO, SV>(hr));
+      if constexpr (CPLX) store_raw<IO, SV>(y_im, i, pack<IO, SV>(hi));
+    }
+  }
+}
+
 }  // namespace sparc
 
 // ===========================================================================
@@ -408,6 +492,82 @@ sparc_status sparc_decode_step(int64_t batch, int64_t modes, int32_t io_dtype, c
                        write_phase_response, write_radial_response, state_re, state_im, new_re, new_im, y);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "decode: %s", hipGetErrorString(e));
+}
+
+}  // extern "C"
+
+namespace {
+template <int TR, typename IO>
+void launch_step(bool v4, bool relu, int64_t B, int M, int G, bool reset, const void* g0, const void* g1,
+                 const float* nu_log, const float* theta_log, const void* w_re, const void* w_im,
+                 float* st_re, float* st_im, void* y_re, void* y_im, hipStream_t st) {
+  const int gs = M / G;
+  const int64_t n = B * static_cast<int64_t>(M) / (v4 ? 4 : 1);
+  const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+#define SPARC_STEP(SVV, RR)                                                                         \
+  hipLaunchKernelGGL((sparc::scan_step_kernel<TR, IO, SVV, RR>), grid, dim3(256), 0, st, n, M, G, gs, \
+                     reset, g0, g1, nu_log, theta_log, w_re, w_im, st_re, st_im, y_re, y_im)
+  if constexpr (TR == sparc::TR_REAL) {
+    if (v4) SPARC_STEP(4, false); else SPARC_STEP(1, false);
+  } else {
+    if (v4 && relu) SPARC_STEP(4, true);
+    else if (v4) SPARC_STEP(4, false);
+    else if (relu) SPARC_STEP(1, true);
+    else SPARC_STEP(1, false);
+  }
+#undef SPARC_STEP
+}
+}  // namespace
+
+extern "C" {
+
+sparc_status sparc_scan_step(const sparc_scan_desc* d, const void* gate0, const void* gate1,
+                             const float* nu_log, const float* theta_log,
+                             const void* w_re, const void* w_im,
+                             float* state_re, float* state_im, void* y_re, void* y_im,
+                             sparc_stream_t stream) {
+  if (!d) return fail2(SPARC_EINVAL, "step: desc is NULL");
+  const int64_t B = d->batch, M = d->modes, G = d->groups;
+  if (B < 0 || M <= 0 || G <= 0 || M % G) return fail2(SPARC_EINVAL, "step: B >= 0, M > 0, G > 0 dividing M required");
+  if (M > INT32_MAX / 4 || B * M >= (int64_t(1) << 40)) return fail2(SPARC_EINVAL, "step: too large");
+  if (d->transition < 0 || d->transition > 3) return fail2(SPARC_EINVAL, "step: unknown transition");
+  if (d->io_dtype != SPARC_F32 && d->io_dtype != SPARC_BF16) return fail2(SPARC_EINVAL, "step: io_dtype");
+  const bool p1 = d->transition == SPARC_TRANSITION_P1;
+  const bool cplx = d->transition != SPARC_TRANSITION_REAL;
+  const bool relu = (d->flags & SPARC_FLAG_RELU_OUTPUT) != 0;
+  if (p1 && d->gate_dtype != SPARC_F32) return fail2(SPARC_EINVAL, "step: P1 gates must be fp32");
+  if (!p1 && d->gate_dtype != d->io_dtype) return fail2(SPARC_EINVAL, "step: gate_dtype must equal io_dtype");
+  if (relu && !cplx) return fail2(SPARC_EINVAL, "step: RELU_OUTPUT needs a complex transition");
+  if (!gate0 || !w_re || !state_re) return fail2(SPARC_EINVAL, "step: gate0, w_re, state_re are required");
+  if (cplx && (!gate1 || !w_im || !state_im)) return fail2(SPARC_EINVAL, "step: complex transitions need gate1, w_im, state_im");
+  if (p1 && (!nu_log || !theta_log)) return fail2(SPARC_EINVAL, "step: P1 needs nu_log, theta_log");
+  if (cplx && !relu && y_re && !y_im) return fail2(SPARC_EINVAL, "step: y_im is required with y_re");
+  if (B == 0) return SPARC_OK;
+  const size_t esz = d->io_dtype == SPARC_BF16 ? 2 : 4;
+  const void* io_ptrs[] = {w_re, w_im, y_re, relu ? nullptr : y_im};
+  bool v4 = M % 4 == 0 && al(state_re, 16) && (!state_im || al(state_im, 16));
+  for (const void* ptr : io_ptrs) v4 = v4 && (!ptr || al(ptr, 4 * esz));
+  for (const void* ptr : io_ptrs)
+    if (ptr && !al(ptr, esz)) return fail2(SPARC_EINVAL, "step: misaligned tensor");
+  if (!al(state_re, 4) || (state_im && !al(state_im, 4))) return fail2(SPARC_EINVAL, "step: misaligned state");
+  const bool reset = (d->flags & SPARC_FLAG_RESET_FIRST) != 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool bf = d->io_dtype == SPARC_BF16;
+  const int m = static_cast<int>(M), g = static_cast<int>(G);
+#define SPARC_STEP_TR(TRV)                                                                               \
+  (bf ? launch_step<TRV, sparc::bf16>(v4, relu, B, m, g, reset, gate0, gate1, nu_log, theta_log, w_re,    \
+                                      w_im, state_re, state_im, y_re, y_im, st)                          \
+      : launch_step<TRV, float>(v4, relu, B, m, g, reset, gate0, gate1, nu_log, theta_log, w_re, w_im,    \
+                                state_re, state_im, y_re, y_im, st))
+  switch (d->transition) {
+    case SPARC_TRANSITION_P1: SPARC_STEP_TR(sparc::TR_P1); break;
+    case SPARC_TRANSITION_POLAR: SPARC_STEP_TR(sparc::TR_POLAR); break;
+    case SPARC_TRANSITION_CARTESIAN: SPARC_STEP_TR(sparc::TR_CART); break;
+    default: SPARC_STEP_TR(sparc::TR_REAL); break;
+  }
+#undef SPARC_STEP_TR
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "scan step: %s", hipGetErrorString(e));
 }
 
 }  // extern "C"

@@ -43,7 +43,6 @@
 
 namespace sparc {
 
-enum Transition : int { TR_P1 = 0, TR_POLAR = 1, TR_CART = 2, TR_REAL = 3 };
 
 // How a lane's V modes map to gates.
 enum GateMode : int {

@@ -126,6 +126,59 @@ def scan_backward_raw(transition, g0, g1, w_re, w_im, chunk_state, dy_re, dy_im,
                 dh0_re=dh0_re, dh0_im=dh0_im)
 
 
+@torch.no_grad()
+def scan_step(transition, g0, g1, w_re, w_im, state, nu_log=None, theta_log=None,
+              relu_output=False, want_output=False, reset_first=False):
+    """One scan step for B independent rows with the state updated in place
+    (the scan-core decode step): h <- a h + w, the same as ``chunk_scan`` with
+    T = 1 and the state as initial state.
+
+    g0, g1: gates [B, G] (fp32 eta, delta for "p1"; w's dtype otherwise);
+    w_re, w_im: [B, M]; state: (state_re, state_im) fp32 [B, M] contiguous
+    (a single tensor for "real"), modified in place.  Returns the new state in
+    w's dtype (``relu(cat)`` [B, 2M] with ``relu_output``) when
+    ``want_output``, else None."""
+    if transition not in TRANSITIONS:
+        raise ValueError(f"unknown transition {transition!r}")
+    cplx = transition != "real"
+    st_re, st_im = (state if cplx else (state, None))
+    if w_re.ndim != 2 or st_re.shape != w_re.shape or st_re.dtype != torch.float32:
+        raise ValueError("scan_step expects w [B, M] and an fp32 state [B, M]")
+    if not st_re.is_contiguous() or (st_im is not None and not st_im.is_contiguous()):
+        raise ValueError("scan_step updates the state in place: it must be contiguous")
+    if cplx and (st_im is None or st_im.shape != st_re.shape or w_im is None):
+        raise ValueError("complex scan steps need (state_re, state_im) and w_im")
+    B, M = w_re.shape
+    G = g0.shape[-1]
+    if g0.shape != (B, G) or M % G or (cplx and (g1 is None or g1.shape != g0.shape)):
+        raise ValueError("gates must be [B, G] with G dividing M")
+    p1 = transition == "p1"
+    io = _lib.io_code(w_re.dtype)
+    if not p1:
+        g0 = g0.to(w_re.dtype)
+        g1 = None if g1 is None else g1.to(w_re.dtype)
+    else:
+        g0, g1 = g0.float(), g1.float()
+    gate_io = _lib.io_code(g0.dtype)
+    lib = _lib.load()
+    dev = _lib.require_gpu(g0, w_re, st_re)
+    y_re = y_im = None
+    if want_output:
+        if relu_output:
+            y_re = torch.empty(B, 2 * M, dtype=w_re.dtype, device=dev)
+        else:
+            y_re = torch.empty_like(w_re)
+            y_im = torch.empty_like(w_re) if cplx else None
+    d = _desc(transition, B, 1, M, G, io, gate_io, _flags(relu_output, reset_first) & 3)
+    P = _lib.ptr
+    _lib.check(lib.sparc_scan_step(
+        ctypes.byref(d), P(_c(g0)), P(_c(g1)), P(nu_log), P(theta_log), P(_c(w_re)), P(_c(w_im)),
+        P(st_re), P(st_im), P(y_re), P(y_im), _lib.stream_of(dev)), "sparc_scan_step")
+    if not want_output:
+        return None
+    return y_re if (relu_output or not cplx) else (y_re, y_im)
+
+
 # ---------------------------------------------------------------------------
 # autograd
 # ---------------------------------------------------------------------------

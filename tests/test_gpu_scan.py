@@ -351,3 +351,50 @@ def test_saved_output_backward_matches_recompute(transition, dtype, G, h0, seg, 
     got = dict(g0=b["dg0"], g1=b["dg1"], w_re=b["dw_re"], w_im=b["dw_im"])
     for n, go in zip(names, gradso):
         assert rel_err(got[n], go) <= tol, f"grad {n} vs oracle: {rel_err(got[n], go):.3g}"
+
+
+@pytest.mark.parametrize("transition,B,M,G,dtype,relu", [
+    ("polar", 3, 512, 32, BF16, False),
+    ("polar", 2, 30, 15, F32, True),
+    ("cartesian", 2, 256, 256, F32, False),
+    ("real", 2, 256, 64, F32, False),
+    ("p1", 2, 128, 1, F32, True),
+    ("p1", 2, 128, 1, BF16, False),
+])
+def test_scan_step_matches_sequence(transition, B, M, G, dtype, relu):
+    """Chained single steps with the state updated in place equal the
+    sequence scan from the same initial state (per-step outputs and final
+    state), against the oracle."""
+    print(f"[case] scan step {transition} B={B} M={M} G={G} {dtype} relu={relu}", flush=True)
+    T = 6
+    case = make_case(transition, B, T, M, G, dtype, seed=41, h0=True)
+    cplx = transition != "real"
+    init = case["init"]
+    if cplx:
+        state = (init[0].clone().cuda(), init[1].clone().cuda())
+    else:
+        state = init.clone().cuda()
+    nu = case["nu_log"].cuda() if case["nu_log"] is not None else None
+    th = case["theta_log"].cuda() if case["theta_log"] is not None else None
+    outs = []
+    for t in range(T):
+        g1 = case["g1"][:, t].cuda() if case["g1"] is not None else None
+        w_im = case["w_im"][:, t].cuda() if cplx else None
+        outs.append(ops.scan_step(transition, case["g0"][:, t].cuda(), g1, case["w_re"][:, t].cuda(),
+                                  w_im, state, nu, th, relu_output=relu, want_output=True))
+    d = lambda x: None if x is None else x.double()  # noqa: E731
+    h0 = tuple(x.double() for x in init) if cplx else init.double()
+    yo, lasto = O.grouped_scan_forward(transition, d(case["g0"]), d(case["g1"]), d(case["w_re"]),
+                                       d(case["w_im"]), d(case["nu_log"]), d(case["theta_log"]),
+                                       h0=h0, relu_output=relu)
+    tol = TOL[dtype]
+    if relu or not cplx:
+        got = torch.stack(outs, 1)
+        assert rel_err(got, yo) <= tol
+    else:
+        assert rel_err(torch.stack([o[0] for o in outs], 1), yo[0]) <= tol
+        assert rel_err(torch.stack([o[1] for o in outs], 1), yo[1]) <= tol
+    lasts = state if cplx else (state,)
+    lastos = lasto if cplx else (lasto,)
+    for a, b in zip(lasts, lastos):
+        assert rel_err(a, b) <= (1e-4 if dtype == F32 else 1e-2)
