@@ -240,6 +240,33 @@ sparc_status sparc_decode_step(int64_t batch, int64_t modes, int32_t io_dtype,
                                sparc_stream_t stream);
 
 /*
+ * Prepared decode: the per-mode constants of the P1 step are computed once
+ * (consts [M, 8] fp32: nu, cos theta, sin theta, exp(write_log_gain),
+ * 1/expm1(-2 nu), write_phase_response, write_radial_response, theta) and
+ * reused by every step while the parameters do not change.  The step runs the
+ * two control dot products split over several workgroups per row (partials in
+ * the workspace) and then the per-(row, mode) update.  Same semantics and
+ * arguments as sparc_decode_step otherwise (sparc-kernal/forward/decode.py:
+ * 10-75); modes must be a multiple of 4.  The reference recomputes every
+ * per-mode quantity on each step (decode.py:37-47).
+ */
+size_t sparc_decode_workspace_bytes(int64_t batch, int64_t modes);
+sparc_status sparc_decode_prepare(int64_t modes, const float* nu_log, const float* theta_log,
+                                  const float* write_log_gain,
+                                  const float* write_phase_response,
+                                  const float* write_radial_response,
+                                  float* consts, sparc_stream_t stream);
+sparc_status sparc_decode_step_prepared(int64_t batch, int64_t modes, int32_t io_dtype,
+                                        const void* x,
+                                        const float* phase_direction,
+                                        const float* radial_direction,
+                                        const float* consts,
+                                        const float* state_re, const float* state_im,
+                                        float* new_re, float* new_im, void* y,
+                                        void* workspace, size_t workspace_bytes,
+                                        sparc_stream_t stream);
+
+/*
  * One step of the scan for B independent rows, with the state carried by the
  * caller: h <- a h + w, fp32 state updated in place (the scan-core decode
  * step).  The same as sparc_scan_forward with T = 1 and h0 = state: the

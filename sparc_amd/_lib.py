@@ -36,6 +36,9 @@ EXPORTED_SYMBOLS = (
     "sparc_write_workspace_bytes",
     "sparc_write_backward",
     "sparc_decode_step",
+    "sparc_decode_workspace_bytes",
+    "sparc_decode_prepare",
+    "sparc_decode_step_prepared",
     "sparc_scan_step",
     "sparc_column_sum",
     "sparc_last_error",
@@ -97,6 +100,12 @@ def load() -> ctypes.CDLL:
         lib.sparc_write_backward.restype = ctypes.c_int
         lib.sparc_decode_step.argtypes = [_I64, _I64, _I32] + [_P] * 14
         lib.sparc_decode_step.restype = ctypes.c_int
+        lib.sparc_decode_workspace_bytes.argtypes = [_I64, _I64]
+        lib.sparc_decode_workspace_bytes.restype = _SZ
+        lib.sparc_decode_prepare.argtypes = [_I64] + [_P] * 6 + [_P]
+        lib.sparc_decode_prepare.restype = ctypes.c_int
+        lib.sparc_decode_step_prepared.argtypes = [_I64, _I64, _I32] + [_P] * 9 + [_P, _SZ, _P]
+        lib.sparc_decode_step_prepared.restype = ctypes.c_int
         lib.sparc_scan_step.argtypes = [D] + [_P] * 10 + [_P]
         lib.sparc_scan_step.restype = ctypes.c_int
         lib.sparc_column_sum.argtypes = [_I64, _I64, _P, _P, ctypes.c_int, _P]

@@ -52,6 +52,32 @@ __device__ __forceinline__ void store_raw(void* base, int64_t index, typename Ra
   reinterpret_cast<R*>(static_cast<IO*>(base) + index)[0] = v;
 }
 
+// Non-temporal variants: streamed data that is touched once per kernel (the
+// nt cache hint: do not keep it in the caches ahead of data that is reused).
+template <int NB> struct NtBits;
+template <> struct NtBits<2> { using T = unsigned short; };
+template <> struct NtBits<4> { using T = unsigned int; };
+template <> struct NtBits<8> { typedef unsigned int T __attribute__((ext_vector_type(2))); };
+template <> struct NtBits<16> { typedef unsigned int T __attribute__((ext_vector_type(4))); };
+
+template <typename IO, int V>
+__device__ __forceinline__ typename Raw<IO, V>::T load_raw_nt(const void* base, int64_t index) {
+  using R = typename Raw<IO, V>::T;
+  using N = typename NtBits<sizeof(R)>::T;
+  const N n = __builtin_nontemporal_load(reinterpret_cast<const N*>(static_cast<const IO*>(base) + index));
+  R r;
+  __builtin_memcpy(&r, &n, sizeof(R));
+  return r;
+}
+template <typename IO, int V>
+__device__ __forceinline__ void store_raw_nt(void* base, int64_t index, typename Raw<IO, V>::T v) {
+  using R = typename Raw<IO, V>::T;
+  using N = typename NtBits<sizeof(R)>::T;
+  N n;
+  __builtin_memcpy(&n, &v, sizeof(R));
+  __builtin_nontemporal_store(n, reinterpret_cast<N*>(static_cast<IO*>(base) + index));
+}
+
 template <typename IO, int V>
 __device__ __forceinline__ void unpack(const typename Raw<IO, V>::T& r, float (&o)[V]) {
   if constexpr (sizeof(IO) == 4) {
@@ -91,6 +117,11 @@ template <typename IO>
 __device__ __forceinline__ float load1(const void* base, int64_t index) {
   if constexpr (sizeof(IO) == 4) return static_cast<const float*>(base)[index];
   else return bf16_bits_to_float(static_cast<const uint16_t*>(base)[index]);
+}
+template <typename IO>
+__device__ __forceinline__ float load1_nt(const void* base, int64_t index) {
+  if constexpr (sizeof(IO) == 4) return __builtin_nontemporal_load(static_cast<const float*>(base) + index);
+  else return bf16_bits_to_float(__builtin_nontemporal_load(static_cast<const uint16_t*>(base) + index));
 }
 template <typename IO>
 __device__ __forceinline__ void store1(void* base, int64_t index, float v) {

@@ -255,6 +255,172 @@ decode_kernel(int M, const void* x, const float* pdir, const float* rdir,
 }
 
 // ---------------------------------------------------------------------------
+// prepared decode: per-mode constants once, row controls split over
+// workgroups, per-(row, mode) update with cheap arithmetic
+// ---------------------------------------------------------------------------
+constexpr int kDecodeConsts = 8;  // floats per mode in the constants table
+constexpr int kDotSplit = 8;      // workgroups per row for the control dot products
+constexpr int kDecodeRows = 4;    // rows per update workgroup (constants reused)
+
+// consts[m] = (nu, cos theta, sin theta, gamma, 1/expm1(-2 nu), wpr, wrr, theta)
+__global__ void __launch_bounds__(256)
+decode_prepare_kernel(int M, const float* nu_log, const float* theta_log, const float* wlg,
+                      const float* wpr, const float* wrr, float* consts) {
+  const int m = blockIdx.x * 256 + threadIdx.x;
+  if (m >= M) return;
+  const float nu = expf(nu_log[m]);
+  const float theta = expf(theta_log[m]);
+  float sn, cs;
+  sincosf(theta, &sn, &cs);
+  float4* c = reinterpret_cast<float4*>(consts + static_cast<int64_t>(m) * kDecodeConsts);
+  c[0] = make_float4(nu, cs, sn, expf(wlg[m]));
+  c[1] = make_float4(1.0f / expm1f(-2.0f * nu), wpr[m], wrr[m], theta);
+}
+
+// part[b, k, 0..1] = partial dot products of row b's inputs with the phase and
+// radial directions over slice k of the 2M inputs
+template <typename IO>
+__global__ void __launch_bounds__(256)
+decode_dots_kernel(int W, const void* x, const float* pdir, const float* rdir, float* part) {
+  __shared__ float red[2][4];
+  const int b = blockIdx.y, k = blockIdx.x;
+  const int slice = ((W / 2 + kDotSplit - 1) / kDotSplit) * 2;  // even: pairs stay in one slice
+  const int lo = k * slice, hi = min(W, lo + slice);
+  const int64_t xrow = static_cast<int64_t>(b) * W;
+  float p0 = 0.0f, p1 = 0.0f;
+  for (int i = lo + threadIdx.x * 2; i < hi; i += 512) {
+    float xv[2];
+    unpack<IO, 2>(load_raw<IO, 2>(x, xrow + i), xv);
+    const float2 pd = *reinterpret_cast<const float2*>(pdir + i);
+    const float2 rd = *reinterpret_cast<const float2*>(rdir + i);
+    p0 = fmaf(xv[0], pd.x, fmaf(xv[1], pd.y, p0));
+    p1 = fmaf(xv[0], rd.x, fmaf(xv[1], rd.y, p1));
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    p0 += __shfl_xor(p0, off, 64);
+    p1 += __shfl_xor(p1, off, 64);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { red[0][wave] = p0; red[1][wave] = p1; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float* o = part + (static_cast<int64_t>(b) * kDotSplit + k) * 2;
+    o[0] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    o[1] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  }
+}
+
+// expm1(x) for x <= 0 to ~1e-7 relative: Taylor series (8 terms) near 0,
+// exp(x) - 1 further out (no cancellation there)
+__device__ __forceinline__ float expm1_nonpos(float x) {
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, x, 1.0f / 720.0f);
+  p = fmaf(p, x, 1.0f / 120.0f);
+  p = fmaf(p, x, 1.0f / 24.0f);
+  p = fmaf(p, x, 1.0f / 6.0f);
+  p = fmaf(p, x, 0.5f);
+  p = fmaf(p, x, 1.0f);
+  p *= x;
+  return x > -0.25f ? p : fast_exp(x) - 1.0f;
+}
+
+// sin and cos of |u| <= pi/2 by Taylor series to x^11 / x^12 (error < 6e-8)
+__device__ __forceinline__ void sincos_half(float u, float& s, float& c) {
+  const float u2 = u * u;
+  float ps = -1.0f / 39916800.0f;
+  ps = fmaf(ps, u2, 1.0f / 362880.0f);
+  ps = fmaf(ps, u2, -1.0f / 5040.0f);
+  ps = fmaf(ps, u2, 1.0f / 120.0f);
+  ps = fmaf(ps, u2, -1.0f / 6.0f);
+  s = fmaf(ps * u2, u, u);
+  float pc = 1.0f / 479001600.0f;
+  pc = fmaf(pc, u2, -1.0f / 3628800.0f);
+  pc = fmaf(pc, u2, 1.0f / 40320.0f);
+  pc = fmaf(pc, u2, -1.0f / 720.0f);
+  pc = fmaf(pc, u2, 1.0f / 24.0f);
+  pc = fmaf(pc, u2, -0.5f);
+  c = fmaf(pc, u2, 1.0f);
+}
+
+// tanh through one hardware exponential and reciprocal (absolute error ~1e-7)
+__device__ __forceinline__ float tanh_fast(float x) {
+  const float e = fast_exp(-2.0f * fabsf(x));
+  return copysignf((1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e), x);
+}
+
+template <typename IO>
+__global__ void __launch_bounds__(256)
+decode_update_kernel(int B, int M, const void* x, const float* pbias, const float* rbias, const float* part,
+                     const float* consts, const float* st_re, const float* st_im,
+                     float* new_re, float* new_im, void* y) {
+  constexpr int SV = 4;
+  __shared__ float s_row[kDecodeRows][4];  // phase signal, radial signal, exp(eta), delta
+  const int m0 = (blockIdx.x * 256 + threadIdx.x) * SV;
+  const int b0 = blockIdx.y * kDecodeRows;
+  if (threadIdx.x < kDecodeRows && b0 + static_cast<int>(threadIdx.x) < B) {
+    const int b = b0 + threadIdx.x;
+    float p0 = *pbias, p1 = *rbias;  // the directions' bias entries
+    for (int k = 0; k < kDotSplit; ++k) {
+      p0 += part[(static_cast<int64_t>(b) * kDotSplit + k) * 2];
+      p1 += part[(static_cast<int64_t>(b) * kDotSplit + k) * 2 + 1];
+    }
+    const float ps = tanhf(p0), rs = tanhf(p1);
+    s_row[threadIdx.x][0] = ps;
+    s_row[threadIdx.x][1] = rs;
+    s_row[threadIdx.x][2] = expf(kLog16 * rs);
+    s_row[threadIdx.x][3] = kHalfPi * ps;
+  }
+  __syncthreads();
+  if (m0 >= M) return;
+  float nu[SV], ct[SV], stt[SV], gam[SV], cinv[SV], wp[SV], wrr_[SV];
+#pragma unroll
+  for (int v = 0; v < SV; ++v) {
+    const float4* c = reinterpret_cast<const float4*>(consts + static_cast<int64_t>(m0 + v) * kDecodeConsts);
+    const float4 c0 = c[0], c1 = c[1];
+    nu[v] = c0.x; ct[v] = c0.y; stt[v] = c0.z; gam[v] = c0.w;
+    cinv[v] = c1.x; wp[v] = c1.y; wrr_[v] = c1.z;
+  }
+  for (int r = 0; r < kDecodeRows; ++r) {
+    const int b = b0 + r;
+    if (b >= B) break;
+    const float ps = s_row[r][0], rs = s_row[r][1], E = s_row[r][2], delta = s_row[r][3];
+    const int64_t srow = static_cast<int64_t>(b) * M + m0;
+    const int64_t xrow = static_cast<int64_t>(b) * 2 * M + m0;
+    float xr[SV], xi[SV], hr[SV], hi[SV];
+    unpack<IO, SV>(load_raw_nt<IO, SV>(x, xrow), xr);
+    unpack<IO, SV>(load_raw_nt<IO, SV>(x, xrow + M), xi);
+    unpack<float, SV>(load_raw<float, SV>(st_re, srow), hr);
+    unpack<float, SV>(load_raw<float, SV>(st_im, srow), hi);
+    float yr[SV], yi[SV];
+#pragma unroll
+    for (int v = 0; v < SV; ++v) {
+      const float em = expm1_nonpos(-nu[v] * E);  // rho - 1
+      const float rho = 1.0f + em;
+      float su, cu;
+      sincos_half(-em * delta, su, cu);            // (1 - rho) * delta
+      const float ar = rho * fmaf(ct[v], cu, -stt[v] * su);
+      const float ai = rho * fmaf(stt[v], cu, ct[v] * su);
+      // expm1(-2 nu E) = em (2 + em); ratio = sqrt(expm1(-2 nu E) / expm1(-2 nu))
+      const float ratio = __builtin_sqrtf(em * (2.0f + em) * cinv[v]);
+      const float q = fmaf(ps, wp[v], rs * wrr_[v]);
+      const float gate = 2.0f * __builtin_amdgcn_rcpf(1.0f + fast_exp(-q));
+      const float gain = gam[v] * ratio * gate;
+      const float nr = fmaf(ar, hr[v], fmaf(-ai, hi[v], gain * tanh_fast(xr[v])));
+      const float ni = fmaf(ai, hr[v], fmaf(ar, hi[v], gain * tanh_fast(xi[v])));
+      hr[v] = nr;
+      hi[v] = ni;
+      yr[v] = fmaxf(nr, 0.0f);
+      yi[v] = fmaxf(ni, 0.0f);
+    }
+    store_raw<float, SV>(new_re, srow, pack<float, SV>(hr));
+    store_raw<float, SV>(new_im, srow, pack<float, SV>(hi));
+    store_raw_nt<IO, SV>(y, xrow, pack<IO, SV>(yr));
+    store_raw_nt<IO, SV>(y, xrow + M, pack<IO, SV>(yi));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // one scan step h <- a h + w for B rows, fp32 state in place (scan-core decode)
 // ---------------------------------------------------------------------------
 // SV modes per thread (4: one 16-byte state load per plane).  A thread's modes
@@ -272,11 +438,12 @@ scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* 
   const int b = static_cast<int>(i / M);
   const int m = static_cast<int>(i - static_cast<int64_t>(b) * M);
   float hr[SV], hi[SV], wr[SV], wi[SV];
-  unpack<float, SV>(load_raw<float, SV>(st_re, i), hr);
-  unpack<IO, SV>(load_raw<IO, SV>(w_re, i), wr);
+  // everything here is touched once per step: non-temporal accesses
+  unpack<float, SV>(load_raw_nt<float, SV>(st_re, i), hr);
+  unpack<IO, SV>(load_raw_nt<IO, SV>(w_re, i), wr);
   if constexpr (CPLX) {
-    unpack<float, SV>(load_raw<float, SV>(st_im, i), hi);
-    unpack<IO, SV>(load_raw<IO, SV>(w_im, i), wi);
+    unpack<float, SV>(load_raw_nt<float, SV>(st_im, i), hi);
+    unpack<IO, SV>(load_raw_nt<IO, SV>(w_im, i), wi);
   }
   // P1 transitions also depend on each mode's nu and theta
   const bool shared = TR != TR_P1 && gs % SV == 0;  // uniform over the launch
@@ -296,9 +463,9 @@ scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* 
       ar[v] = rho * cs;
       ai[v] = rho * sn;
     } else if constexpr (TR == TR_POLAR) {
-      const float r = load1<IO>(g0, gi);
+      const float r = load1_nt<IO>(g0, gi);
       float sn, cs;
-      sincos_moderate(load1<IO>(g1, gi), sn, cs);
+      sincos_moderate(load1_nt<IO>(g1, gi), sn, cs);
       ar[v] = r * cs;
       ai[v] = r * sn;
     } else if constexpr (TR == TR_CART) {
@@ -321,8 +488,8 @@ scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* 
       hr[v] = fmaf(ar[v], hr[v], wr[v]);
     }
   }
-  store_raw<float, SV>(st_re, i, pack<float, SV>(hr));
-  if constexpr (CPLX) store_raw<float, SV>(st_im, i, pack<float, SV>(hi));
+  store_raw_nt<float, SV>(st_re, i, pack<float, SV>(hr));
+  if constexpr (CPLX) store_raw_nt<float, SV>(st_im, i, pack<float, SV>(hi));
   if (y_re) {
     if constexpr (RELU) {
       float rr[SV], ri[SV];
@@ -520,6 +687,63 @@ void launch_step(bool v4, bool relu, int64_t B, int M, int G, bool reset, const 
 }  // namespace
 
 extern "C" {
+
+size_t sparc_decode_workspace_bytes(int64_t batch, int64_t modes) {
+  if (batch < 0 || modes <= 0) return 0;
+  return static_cast<size_t>(batch) * sparc::kDotSplit * 2 * sizeof(float) + 256;
+}
+
+sparc_status sparc_decode_prepare(int64_t modes, const float* nu_log, const float* theta_log,
+                                  const float* write_log_gain, const float* write_phase_response,
+                                  const float* write_radial_response, float* consts,
+                                  sparc_stream_t stream) {
+  if (modes <= 0 || modes > INT32_MAX / 8) return fail2(SPARC_EINVAL, "decode prepare: modes");
+  if (!nu_log || !theta_log || !write_log_gain || !write_phase_response || !write_radial_response || !consts)
+    return fail2(SPARC_EINVAL, "decode prepare: NULL pointer");
+  if (!al(consts, 16)) return fail2(SPARC_EINVAL, "decode prepare: consts must be 16-byte aligned");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(sparc::decode_prepare_kernel, dim3(static_cast<unsigned>((modes + 255) / 256)), dim3(256), 0, st,
+                     static_cast<int>(modes), nu_log, theta_log, write_log_gain, write_phase_response,
+                     write_radial_response, consts);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "decode prepare: %s", hipGetErrorString(e));
+}
+
+sparc_status sparc_decode_step_prepared(int64_t batch, int64_t modes, int32_t io_dtype, const void* x,
+                                        const float* phase_direction, const float* radial_direction,
+                                        const float* consts, const float* state_re, const float* state_im,
+                                        float* new_re, float* new_im, void* y,
+                                        void* workspace, size_t workspace_bytes, sparc_stream_t stream) {
+  if (batch < 0 || modes <= 0 || modes % 4 || modes > INT32_MAX / 4)
+    return fail2(SPARC_EINVAL, "decode: batch >= 0 and modes > 0, a multiple of 4, required");
+  if (batch > 65535LL * sparc::kDecodeRows) return fail2(SPARC_EINVAL, "decode: batch too large");
+  if (io_dtype != SPARC_F32 && io_dtype != SPARC_BF16) return fail2(SPARC_EINVAL, "decode: io_dtype");
+  if (!x || !phase_direction || !radial_direction || !consts || !state_re || !state_im || !new_re || !new_im || !y)
+    return fail2(SPARC_EINVAL, "decode: NULL pointer");
+  if (!workspace || workspace_bytes < sparc_decode_workspace_bytes(batch, modes))
+    return fail2(SPARC_EWORKSPACE, "decode: workspace missing or too small");
+  const size_t esz = io_dtype == SPARC_BF16 ? 2 : 4;
+  if (!al(x, 4 * esz) || !al(y, 4 * esz) || !al(state_re, 16) || !al(state_im, 16) || !al(new_re, 16) ||
+      !al(new_im, 16) || !al(consts, 16) || !al(phase_direction, 8) || !al(radial_direction, 8))
+    return fail2(SPARC_EINVAL, "decode: misaligned tensor");
+  if (batch == 0) return SPARC_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int M = static_cast<int>(modes), W = 2 * M;
+  float* part = static_cast<float*>(workspace);
+  const dim3 gd(sparc::kDotSplit, static_cast<unsigned>(batch));
+  const dim3 gu(static_cast<unsigned>((M / 4 + 255) / 256), static_cast<unsigned>((batch + sparc::kDecodeRows - 1) / sparc::kDecodeRows));
+  if (io_dtype == SPARC_BF16) {
+    hipLaunchKernelGGL(sparc::decode_dots_kernel<sparc::bf16>, gd, dim3(256), 0, st, W, x, phase_direction, radial_direction, part);
+    hipLaunchKernelGGL(sparc::decode_update_kernel<sparc::bf16>, gu, dim3(256), 0, st, static_cast<int>(batch), M, x,
+                       phase_direction + W, radial_direction + W, part, consts, state_re, state_im, new_re, new_im, y);
+  } else {
+    hipLaunchKernelGGL(sparc::decode_dots_kernel<float>, gd, dim3(256), 0, st, W, x, phase_direction, radial_direction, part);
+    hipLaunchKernelGGL(sparc::decode_update_kernel<float>, gu, dim3(256), 0, st, static_cast<int>(batch), M, x,
+                       phase_direction + W, radial_direction + W, part, consts, state_re, state_im, new_re, new_im, y);
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "decode: %s", hipGetErrorString(e));
+}
 
 sparc_status sparc_scan_step(const sparc_scan_desc* d, const void* gate0, const void* gate1,
                              const float* nu_log, const float* theta_log,

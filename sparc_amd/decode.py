@@ -1,6 +1,9 @@
 """Single-step decode: ``prepare_decode`` / ``run_decode_step``
-(sparc-kernal/forward/decode.py:252-306) over the fused HIP decode kernel
-(``sparc_decode_step``, replacing ``_latest_sparc_decode``, decode.py:10-75).
+(sparc-kernal/forward/decode.py:252-306) over the HIP decode step, replacing
+``_latest_sparc_decode`` (decode.py:10-75): ``sparc_decode_step_prepared``
+(per-mode constants cached on the module, controls split over workgroups)
+when the mode count is a multiple of 4, else the single-kernel
+``sparc_decode_step``.
 """
 from __future__ import annotations
 
@@ -9,10 +12,57 @@ import torch
 from . import _lib
 
 
+_CONST_PARAMS = ("nu_log", "theta_log", "write_log_gain", "write_phase_response",
+                 "write_radial_response")
+
+
+def _param_key(module):
+    """Identity of the parameters the per-mode constants derive from: their
+    storage and in-place version counters (optimizer steps and ``copy_`` bump
+    the counters)."""
+    return tuple((getattr(module, n).data_ptr(), getattr(module, n)._version, getattr(module, n).device)
+                 for n in _CONST_PARAMS)
+
+
+def _decode_constants(module):
+    """The per-mode constants table [M, 8] of the prepared decode step, built
+    by ``sparc_decode_prepare`` and rebuilt when a parameter changes."""
+    key = _param_key(module)
+    cache = getattr(module, "_decode_consts", None)
+    if cache is not None and cache[0] == key:
+        return cache[1]
+    lib = _lib.load()
+    params = [getattr(module, n).detach().float().contiguous() for n in _CONST_PARAMS]
+    dev = _lib.require_gpu(*params)
+    modes = params[0].numel()
+    consts = torch.empty(modes, 8, dtype=torch.float32, device=dev)
+    P = _lib.ptr
+    _lib.check(lib.sparc_decode_prepare(modes, *[P(t) for t in params], P(consts), _lib.stream_of(dev)),
+               "sparc_decode_prepare")
+    module._decode_consts = (key, consts)
+    return consts
+
+
+def _decode_workspace(module, batch, modes, dev):
+    lib = _lib.load()
+    need = lib.sparc_decode_workspace_bytes(batch, modes)
+    ws = getattr(module, "_decode_ws", None)
+    if ws is None or ws.numel() < need or ws.device != dev:
+        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        module._decode_ws = ws
+    return ws
+
+
 def prepare_decode(module) -> None:
-    """``prepare_decode`` (forward/decode.py:252-255)."""
+    """``prepare_decode`` (forward/decode.py:252-255).  Also (re)builds the
+    per-mode constants of the prepared decode step when the module is on the
+    GPU; later steps rebuild them by themselves if a parameter changes in
+    place."""
     module._inference_fused = True
     module._inference_pack = None
+    module._decode_consts = None
+    if module.nu_log.is_cuda and module.nu_log.numel() % 4 == 0:
+        _decode_constants(module)
 
 
 @torch.no_grad()
@@ -41,10 +91,19 @@ def latest_sparc_decode(module, x: torch.Tensor, state, out_state=None):
                 or not new_i.is_contiguous() or new_r.shape != (batch, modes) or new_i.shape != (batch, modes)):
             raise ValueError("out_state must be contiguous fp32 [B, M] tensors")
     y = torch.empty_like(x)
+    P = _lib.ptr
+    if modes % 4 == 0:
+        dirs = [p.detach().float().contiguous() for p in (module.phase_direction, module.radial_direction)]
+        consts = _decode_constants(module)
+        ws = _decode_workspace(module, batch, modes, dev)
+        _lib.check(lib.sparc_decode_step_prepared(
+            batch, modes, _lib.io_code(x.dtype), P(x), P(dirs[0]), P(dirs[1]), P(consts),
+            P(state_r), P(state_i), P(new_r), P(new_i), P(y), P(ws), ws.numel(), _lib.stream_of(dev)),
+            "sparc_decode_step_prepared")
+        return y, (new_r, new_i)
     params = [p.detach().float().contiguous() for p in (
         module.phase_direction, module.radial_direction, module.nu_log, module.theta_log,
         module.write_log_gain, module.write_phase_response, module.write_radial_response)]
-    P = _lib.ptr
     _lib.check(lib.sparc_decode_step(
         batch, modes, _lib.io_code(x.dtype), P(x), *[P(p) for p in params],
         P(state_r), P(state_i), P(new_r), P(new_i), P(y), _lib.stream_of(dev)), "sparc_decode_step")

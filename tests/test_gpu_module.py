@@ -184,3 +184,45 @@ def test_decode_in_place_state():
     y, (r2, i2) = m.step(x, (sr, si), None)
     assert r2.data_ptr() == sr.data_ptr()
     assert torch.equal(y, y_ref) and torch.equal(sr, nr) and torch.equal(si, ni)
+
+
+def _single_kernel_decode(m, x, state):
+    """The unprepared one-kernel decode (sparc_decode_step) through the C ABI."""
+    from sparc_amd import _lib
+    lib = _lib.load()
+    B, W = x.shape
+    M = W // 2
+    y = torch.empty_like(x)
+    nr, ni = torch.empty_like(state[0]), torch.empty_like(state[1])
+    params = [p.detach().float().contiguous() for p in (
+        m.phase_direction, m.radial_direction, m.nu_log, m.theta_log, m.write_log_gain,
+        m.write_phase_response, m.write_radial_response)]
+    P = _lib.ptr
+    _lib.check(lib.sparc_decode_step(B, M, _lib.io_code(x.dtype), P(x), *[P(p) for p in params],
+                                     P(state[0]), P(state[1]), P(nr), P(ni), P(y),
+                                     _lib.stream_of(x.device)), "sparc_decode_step")
+    return y, (nr, ni)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_prepared_decode_matches_single_kernel_and_tracks_updates(dtype):
+    """The prepared decode (cached per-mode constants, split control dots,
+    fast arithmetic) agrees with the one-kernel decode, and an in-place
+    parameter update rebuilds the cached constants."""
+    from sparc_amd.decode import latest_sparc_decode
+    print(f"[case] prepared decode {dtype}", flush=True)
+    m = make_module(512, seed=17).cuda()
+    m.prepare_inference()
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(6, 512, generator=g).to(dtype).cuda()
+    state = ((0.1 * torch.randn(6, 256, generator=g)).cuda(), (0.1 * torch.randn(6, 256, generator=g)).cuda())
+    for update in (False, True):
+        if update:
+            with torch.no_grad():
+                m.nu_log.add_(0.3)
+                m.write_phase_response.mul_(-1.0)
+        y1, s1 = latest_sparc_decode(m, x, state)
+        y2, s2 = _single_kernel_decode(m, x, state)
+        assert rel_err(s1[0], s2[0]) <= 1e-5 and rel_err(s1[1], s2[1]) <= 1e-5
+        # outputs in bf16 may differ by one rounding step
+        assert rel_err(y1, y2) <= (1e-5 if dtype == torch.float32 else 2.0 ** -7)
