@@ -8,8 +8,9 @@ single-step decode latency at B=256 (D=2048, N=16, width 2M = 65536).
 
 One step = the forward scan and the backward scan of one batch, inputs
 resident in HBM: the two C-ABI calls sparc_scan_forward / sparc_scan_backward
-(one kernel each at this shape: the serial one-wave-per-chain kernels; the
-backward reads the states from the forward's saved output).
+(one kernel each at this shape: the serial one-chain-per-workgroup kernels
+with 4 modes per lane; the backward reads the states from the forward's saved
+output).
 
 Algorithmic bytes per step, B*T*(M*10*s + G*6*s_g) with s = s_g = 2:
   forward : read w (re, im), write y (re, im)      -> 8 B per mode-step
@@ -315,7 +316,7 @@ def main():
     traffic = measured_traffic()
     roof = {
         "bound": "hbm",
-        "kernel": f"{k_bwd} (backward scan, polar, bf16 I/O, fp32 state, 2 modes per lane)",
+        "kernel": f"{k_bwd} (backward scan, polar, bf16 I/O, fp32 state, 4 modes per lane)",
         "achieved": round(res["bwd_gbs"], 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",

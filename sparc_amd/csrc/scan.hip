@@ -1646,55 +1646,115 @@ template <typename T>
 __device__ __forceinline__ void stb(void* base, int64_t byte_off, uint32_t lane_bytes, T v) {
   *reinterpret_cast<T*>(static_cast<char*>(base) + byte_off + lane_bytes) = v;
 }
+// Non-temporal forms of ldb / stb for the streamed planes of the serial
+// kernels, each element of which is read or written once per launch: the nt
+// cache policy keeps them from displacing lines that are reused.
+// Cache policy of the serial kernels' plane loads and stores: bit 0 loads,
+// bit 1 stores non-temporal (forward and backward separately).
+#ifndef SPARC_FWD_NT
+#define SPARC_FWD_NT 3
+#endif
+#ifndef SPARC_BWD_NT
+#define SPARC_BWD_NT 3
+#endif
+template <typename T, bool NT = true>
+__device__ __forceinline__ T ldn(const void* base, int64_t byte_off, uint32_t lane_bytes) {
+  if constexpr (!NT) return ldb<T>(base, byte_off, lane_bytes);
+  using N = typename NtBits<sizeof(T)>::T;
+  const N n = __builtin_nontemporal_load(
+      reinterpret_cast<const N*>(static_cast<const char*>(base) + byte_off + lane_bytes));
+  T r;
+  __builtin_memcpy(&r, &n, sizeof(T));
+  return r;
+}
+template <typename T, bool NT = true>
+__device__ __forceinline__ void stn(void* base, int64_t byte_off, uint32_t lane_bytes, T v) {
+  if constexpr (!NT) { stb<T>(base, byte_off, lane_bytes, v); return; }
+  using N = typename NtBits<sizeof(T)>::T;
+  N n;
+  __builtin_memcpy(&n, &v, sizeof(T));
+  __builtin_nontemporal_store(n, reinterpret_cast<N*>(static_cast<char*>(base) + byte_off + lane_bytes));
+}
 
 constexpr int fast_rounds(int S) { return (S * kFastMaxGpw + 63) / 64; }
 
-// raw gate values of the (step, group) pairs of one sub-chunk; lane l owns
-// pairs l, l + 64, ...  (pair = step * gpw + group)
+// Raw gate bits (and segment positions) of the (step, group) pairs of one
+// block of S steps; lane l owns pairs l, l + 64, ...  (pair = step * gpw +
+// group).  They are loaded a block ahead and stay raw until fill_tab converts
+// them: a conversion right after the load would make the wave wait for it,
+// and with it for every plane load of the prefetch issued just before.
+template <int S>
+struct GateBlock {
+  uint32_t g0[fast_rounds(S)], g1[fast_rounds(S)];
+  int32_t pos[fast_rounds(S)];
+};
+
+template <typename IO>
+__device__ __forceinline__ uint32_t load_bits(const void* base, int64_t index) {
+  if constexpr (sizeof(IO) == 4) return static_cast<const uint32_t*>(base)[index];
+  else return static_cast<const uint16_t*>(base)[index];
+}
+template <typename IO>
+__device__ __forceinline__ float bits_to_float(uint32_t bits) {
+  if constexpr (sizeof(IO) == 4) return __uint_as_float(bits);
+  else return __uint_as_float(bits << 16);
+}
+
+// Every lane loads: pairs outside the tensors (steps past T, groups past G in
+// the last mode block, rounds past S * gpw) read element 0, and fill_tab
+// discards them.
 template <int TR, typename IO, int S>
 __device__ __forceinline__ void load_gate_pairs(const ScanArgs& p, int b, int t0, int g_base, int gpw, int lane,
-                                                float (&r0)[fast_rounds(S)], float (&r1)[fast_rounds(S)]) {
+                                                GateBlock<S>& gb) {
 #pragma unroll
   for (int r = 0; r < fast_rounds(S); ++r) {
     const int idx = r * 64 + lane;
-    r0[r] = 0.0f;
-    r1[r] = 0.0f;
-    if (idx < S * gpw) {
-      const int t = t0 + idx / gpw;
-      // the last mode block of a row may hold fewer than gpw groups
-      if (t < p.T && g_base + idx % gpw < p.G) {
-        const int64_t gi = (static_cast<int64_t>(b) * p.T + t) * p.G + g_base + idx % gpw;
-        r0[r] = load1<IO>(p.g0, gi);
-        if constexpr (TR != TR_REAL) r1[r] = load1<IO>(p.g1, gi);
-      }
-    }
+    const int step = idx / gpw;
+    const int t = t0 + step;
+    const int g = g_base + idx - step * gpw;
+    const bool in_t = idx < S * gpw && t < p.T;
+    const int64_t row = static_cast<int64_t>(b) * p.T + t;
+    const int64_t gi = (in_t && g < p.G) ? row * p.G + g : 0;
+    gb.g0[r] = load_bits<IO>(p.g0, gi);
+    if constexpr (TR != TR_REAL) gb.g1[r] = load_bits<IO>(p.g1, gi);
+    if (p.segpos) gb.pos[r] = p.segpos[in_t ? row : 0];
   }
 }
 
 // tab[pair] = (ar, ai[, cos phi, sin phi]); identity past T, zero at resets
-template <int TR, int S, int TW>
-__device__ __forceinline__ void fill_tab(const ScanArgs& p, int b, int t0, int gpw, int lane, bool reset_first,
-                                         const float (&r0)[fast_rounds(S)], const float (&r1)[fast_rounds(S)],
-                                         float* tab) {
+// and for groups past G.  Returns the lane's reset pairs as a bit mask (bit r:
+// pair r * 64 + lane).
+template <int TR, typename IO, int S, int TW>
+__device__ __forceinline__ uint32_t fill_tab(const ScanArgs& p, int t0, int g_base, int gpw, int lane,
+                                             bool reset_first, const GateBlock<S>& gb, float* tab) {
+  uint32_t rmask = 0u;
 #pragma unroll
   for (int r = 0; r < fast_rounds(S); ++r) {
     const int idx = r * 64 + lane;
     if (idx < S * gpw) {
-      const int t = t0 + idx / gpw;
+      const int step = idx / gpw;
+      const int t = t0 + step;
+      const bool g_ok = g_base + idx - step * gpw < p.G;
       float ar = 1.0f, ai = 0.0f, cp = 1.0f, sp = 0.0f;
       if (t < p.T) {
+        const float v0 = g_ok ? bits_to_float<IO>(gb.g0[r]) : 0.0f;
+        const float v1 = (TR != TR_REAL && g_ok) ? bits_to_float<IO>(gb.g1[r]) : 0.0f;
         if constexpr (TR == TR_POLAR) {
-          sincos_moderate(r1[r], sp, cp);
-          ar = r0[r] * cp;
-          ai = r0[r] * sp;
+          sincos_moderate(v1, sp, cp);
+          ar = v0 * cp;
+          ai = v0 * sp;
         } else if constexpr (TR == TR_CART) {
-          ar = r0[r];
-          ai = r1[r];
+          ar = v0;
+          ai = v1;
         } else {
-          ar = r0[r];
+          ar = v0;
         }
-        const bool reset = p.segpos ? (p.segpos[static_cast<int64_t>(b) * p.T + t] == 0) : (reset_first && t == 0);
-        if (reset) { ar = 0.0f; ai = 0.0f; }
+        const bool reset = p.segpos ? (gb.pos[r] == 0) : (reset_first && t == 0);
+        if (reset) {
+          ar = 0.0f;
+          ai = 0.0f;
+          rmask |= 1u << r;
+        }
       }
       float* e = tab + idx * TW;
       e[0] = ar;
@@ -1702,6 +1762,7 @@ __device__ __forceinline__ void fill_tab(const ScanArgs& p, int b, int t0, int g
       if constexpr (TW > 2) { e[2] = cp; e[3] = sp; }
     }
   }
+  return rmask;
 }
 
 template <int TR, typename IO, int V, int S, int NW, bool RELU>
@@ -1712,7 +1773,6 @@ chain_fwd_fast_kernel(ScanArgs p) {
   constexpr int C = S * NW;
   constexpr int MB = 64 * V;
   constexpr int NH = CPLX ? 2 : 1;
-  constexpr int R = fast_rounds(S);
   constexpr int TW = CPLX ? 2 : 1;
   constexpr int ESZ = sizeof(IO);
   using RawT = typename Raw<IO, V>::T;
@@ -1750,7 +1810,7 @@ chain_fwd_fast_kernel(ScanArgs p) {
   }
 
   RawT wr[2][S], wi[2][S];
-  float gr0[2][R], gr1[2][R];
+  GateBlock<S> gb[2];
   auto load_chunk = [&](int hb, int c) {
     const int t0 = c * C + wave * S;
     const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
@@ -1765,7 +1825,7 @@ chain_fwd_fast_kernel(ScanArgs p) {
         wi[hb][s] = wr[hb][s];
       }
     }
-    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gr0[hb], gr1[hb]);
+    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gb[hb]);
   };
 
   load_chunk(0, 0);
@@ -1776,7 +1836,7 @@ chain_fwd_fast_kernel(ScanArgs p) {
       if (c >= p.n_chunks) break;
       const int t0 = c * C + wave * S;
       if (c + 1 < p.n_chunks) load_chunk(1 - h, c + 1);
-      fill_tab<TR, S, TW>(p, b, t0, gpw, lane, reset_first, gr0[h], gr1[h], tab);
+      fill_tab<TR, IO, S, TW>(p, t0, g_base, gpw, lane, reset_first, gb[h], tab);
       __builtin_amdgcn_wave_barrier();
       float ar[S], ai[S];
 #pragma unroll
@@ -1963,7 +2023,7 @@ chain_bwd_fast_kernel(ScanArgs p) {
   }
 
   RawT wr[2][S], wi[2][S], dr[2][S], di[2][S];
-  float gr0[2][R], gr1[2][R];
+  GateBlock<S> gb[2];
   float hs[2][V * NH];
   auto load_chunk = [&](int hb, int c) {
     const int t0 = c * C + wave * S;
@@ -1989,7 +2049,7 @@ chain_bwd_fast_kernel(ScanArgs p) {
         di[hb][s] = wr[hb][s];
       }
     }
-    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gr0[hb], gr1[hb]);
+    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gb[hb]);
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       float h_r = 0.0f, h_i = 0.0f;
@@ -2017,7 +2077,7 @@ chain_bwd_fast_kernel(ScanArgs p) {
       const int t0 = c * C + wave * S;
       const int xb = c & 1;  // s_xi buffer holding the adjoint entering this chunk
       if (c - 1 >= 0) load_chunk(1 - h, c - 1);
-      fill_tab<TR, S, TW>(p, b, t0, gpw, lane, reset_first, gr0[h], gr1[h], tab);
+      const uint32_t rmask = fill_tab<TR, IO, S, TW>(p, t0, g_base, gpw, lane, reset_first, gb[h], tab);
       __builtin_amdgcn_wave_barrier();
       float ar[S], ai[S];
 #pragma unroll
@@ -2281,7 +2341,7 @@ chain_bwd_fast_kernel(ScanArgs p) {
           const int t = t0 + step;
           if (t < p.T && g_base + g < p.G) {  // the last mode block may hold fewer groups
             // a reset step's transition is the constant 0: no gradient
-            const bool reset = p.segpos ? (p.segpos[row0 + t] == 0) : (reset_first && t == 0);
+            const bool reset = (rmask >> r) & 1u;
             const int64_t gi = (row0 + t) * p.G + g_base + g;
             store1<IO>(p.dg0, gi, reset ? 0.0f : a0);
             if constexpr (CPLX) store1<IO>(p.dg1, gi, reset ? 0.0f : a1);
@@ -2351,7 +2411,7 @@ chain_bwd_saved_kernel(ScanArgs p) {
 
   // dy rows t0 .. t0+S-1 and y rows t0-1 .. t0+S-2 (the state before each step)
   RawT dr[2][S], di[2][S], yr[2][S], yi[2][S];
-  float gr0[2][R], gr1[2][R];
+  GateBlock<S> gb[2];
   auto load_chunk = [&](int hb, int c) {
     const int t0 = c * C + wave * S;
     const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
@@ -2382,7 +2442,7 @@ chain_bwd_saved_kernel(ScanArgs p) {
         }
       }
     }
-    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gr0[hb], gr1[hb]);
+    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gb[hb]);
   };
 
   load_chunk(0, p.n_chunks - 1);
@@ -2394,7 +2454,7 @@ chain_bwd_saved_kernel(ScanArgs p) {
       const int t0 = c * C + wave * S;
       const int xb = c & 1;  // buffers of this chunk (maps, entering adjoint)
       if (c - 1 >= 0) load_chunk(1 - h, c - 1);
-      fill_tab<TR, S, TW>(p, b, t0, gpw, lane, reset_first, gr0[h], gr1[h], tab);
+      const uint32_t rmask = fill_tab<TR, IO, S, TW>(p, t0, g_base, gpw, lane, reset_first, gb[h], tab);
       __builtin_amdgcn_wave_barrier();
       float ar[S], ai[S];
 #pragma unroll
@@ -2561,7 +2621,7 @@ chain_bwd_saved_kernel(ScanArgs p) {
           const int t = t0 + step;
           if (t < p.T && g_base + g < p.G) {  // the last mode block may hold fewer groups
             // a reset step's transition is the constant 0: no gradient
-            const bool reset = p.segpos ? (p.segpos[row0 + t] == 0) : (reset_first && t == 0);
+            const bool reset = (rmask >> r) & 1u;
             const int64_t gi = (row0 + t) * p.G + g_base + g;
             store1<IO>(p.dg0, gi, reset ? 0.0f : a0);
             if constexpr (CPLX) store1<IO>(p.dg1, gi, reset ? 0.0f : a1);
@@ -2574,37 +2634,62 @@ chain_bwd_saved_kernel(ScanArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// Serial kernels for lane-shared gates: one wave per chain (batch row, block
-// of 64*V modes) walks every step in order (forward) or in reverse
-// (backward from the saved output).  A step costs one complex multiply-add
-// per mode: no sub-chunk maps, no composition, no barriers.  Parallelism is
-// over chains only, so the plan picks these when every SIMD gets a wave;
-// memory latency is covered by loading the next block of S steps into
-// registers while the current one is computed.
+// Serial kernels for lane-shared gates: one chain (batch row, block of 64*V
+// modes) per workgroup of two waves.
+//   * Wave 0 streams the chain.  It walks every step in order (forward) or in
+//     reverse (backward, reading the states from the saved output), one
+//     complex multiply-add per mode and step, and loads the next block of S
+//     steps of the planes into registers while it computes the current one.
+//   * Wave 1 does the rest.  It loads the gates two blocks ahead and turns
+//     them into the transition table of the next block (double-buffered in
+//     LDS).  Backward, it also sums the transition gradients of the previous
+//     block over the lanes of each group (an LDS transpose) and stores the
+//     gate gradients.
+// Wave 0 thus issues no memory instruction but its plane loads and stores, so
+// the wait before a block covers that block's loads only, never the prefetch
+// of the next one (a gate load in the same wave, used one block later, made
+// the compiler drain the whole prefetch).  One workgroup barrier per block
+// hands the buffers over.  Parallelism is over chains only; the plan picks
+// these kernels when there are enough chains to fill the GPU.
 // ---------------------------------------------------------------------------
 constexpr int kStateChunk = 64;  // steps per saved chunk state
 
+// s_waitcnt vmcnt(0): every vector memory operation of the wave has completed.
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// blocks of gates in flight in the helper wave (loaded kGateDepth-1 blocks
+// before their table is built); an even number
+#ifndef SPARC_GATE_DEPTH
+#define SPARC_GATE_DEPTH 4
+#endif
+constexpr int kGateDepth = SPARC_GATE_DEPTH;
+static_assert(kGateDepth % 2 == 0 && kGateDepth >= 2, "the loops pair plane buffers with even depths");
+#ifndef SPARC_SERIAL_SWIZZLE
+#define SPARC_SERIAL_SWIZZLE 1
+#endif
+
 template <int TR, typename IO, int V, int S, bool RELU>
-__global__ void __launch_bounds__(64, 1)
+__global__ void __launch_bounds__(128, 1)
 chain_fwd_serial_kernel(ScanArgs p) {
   static_assert(kStateChunk % S == 0, "blocks must tile the saved-state chunks");
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
   constexpr bool CPLX = TR != TR_REAL;
   constexpr int MB = 64 * V;
   constexpr int NH = CPLX ? 2 : 1;
-  constexpr int R = fast_rounds(S);
   constexpr int TW = CPLX ? 2 : 1;
   constexpr int ESZ = sizeof(IO);
   using RawT = typename Raw<IO, V>::T;
-  __shared__ float tab[S * kFastMaxGpw * TW];
+  __shared__ float tab[2][S * kFastMaxGpw * TW];
 
-  const int lane = threadIdx.x;
-  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int n_blocks = (p.T + S - 1) / S;
+  if (n_blocks == 0) return;  // the whole workgroup: no barrier is skipped by one wave only
+  const int lane = threadIdx.x & 63;
+  const bool streamer = threadIdx.x < 64;  // wave-uniform
+  const int chain = SPARC_SERIAL_SWIZZLE ? xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x))
+                                         : static_cast<int>(blockIdx.x);
   const int b = chain / p.n_mblocks;
   const int mb = chain - b * p.n_mblocks;
   const int m0 = mb * MB + lane * V;
   const bool lane_ok = m0 < p.M;
-  const bool block_full = (mb + 1) * MB <= p.M;  // wave-uniform
   const int gpw = MB / p.gs;
   const int lpg = p.gs / V;
   const int my_g = lane / lpg;
@@ -2615,118 +2700,139 @@ chain_fwd_serial_kernel(ScanArgs p) {
   const int64_t mbase = static_cast<int64_t>(mb) * MB;
   const int64_t stride = static_cast<int64_t>(p.M) * ESZ;   // bytes per step of w
   const int64_t ostride = (RELU ? 2 : 1) * stride;          // bytes per step of y
-  const int n_blocks = (p.T + S - 1) / S;
 
   float hr[V], hi[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
-    hr[v] = (p.h0_re && lane_ok) ? p.h0_re[i0] : 0.0f;
-    hi[v] = (CPLX && p.h0_im && lane_ok) ? p.h0_im[i0] : 0.0f;
+    hr[v] = (streamer && p.h0_re && lane_ok) ? p.h0_re[i0] : 0.0f;
+    hi[v] = (streamer && CPLX && p.h0_im && lane_ok) ? p.h0_im[i0] : 0.0f;
   }
+  // The initial state is loop-carried: complete its loads here, or the
+  // compiler, unsure at the loop head whether they are still pending, waits
+  // for the whole prefetch before each block.
+  wait_vm_all();
 
-  RawT wr[2][S], wi[2][S];
-  float gr0[2][R], gr1[2][R];
+  RawT wr[2][S], wi[2][S];     // wave 0: plane registers, double-buffered
+  GateBlock<S> gb[kGateDepth];  // wave 1: raw gates of block j in gb[j % kGateDepth]
+  // The loads are unconditional: steps past T re-read row T-1 and lanes past
+  // M read the first element of their mode block; run_block discards both.
+  // (Loads under a branch made the compiler's wait bookkeeping drain the whole
+  // prefetch before every block.)
+  const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
   auto load_block = [&](int hb, int k) {
     const int t0 = k * S;
     const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
-    if (block_full && t0 + S <= p.T) {
+    const int last = p.T - 1 - t0;  // the block's last step inside T (wave-uniform)
 #pragma unroll
-      for (int s = 0; s < S; ++s) {
-        wr[hb][s] = ldb<RawT>(p.w_re, off + s * stride, lane_bytes);
-        if constexpr (CPLX) wi[hb][s] = ldb<RawT>(p.w_im, off + s * stride, lane_bytes);
-      }
-    } else {
-      float z[V] = {};
-      const RawT zero = pack<IO, V>(z);
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        wr[hb][s] = zero;
-        wi[hb][s] = zero;
-        if (lane_ok && t0 + s < p.T) {
-          wr[hb][s] = ldb<RawT>(p.w_re, off + s * stride, lane_bytes);
-          if constexpr (CPLX) wi[hb][s] = ldb<RawT>(p.w_im, off + s * stride, lane_bytes);
-        }
-      }
+    for (int s = 0; s < S; ++s) {
+      const int64_t o = off + static_cast<int64_t>(s <= last ? s : last) * stride;
+      wr[hb][s] = ldn<RawT, (SPARC_FWD_NT & 1) != 0>(p.w_re, o, lane_ld);
+      if constexpr (CPLX) wi[hb][s] = ldn<RawT, (SPARC_FWD_NT & 1) != 0>(p.w_im, o, lane_ld);
     }
-    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gr0[hb], gr1[hb]);
   };
 
-  // S steps of one block; FULL: every lane and step in range (no store guards)
-  auto run_block = [&](auto full_tag, int h, int t0) {
-    constexpr bool FULL = decltype(full_tag)::value;
+  // S steps of one block from transition table tb (identity past T)
+  auto run_block = [&](int h, int t0, const float* tb) {
+    const bool tail = t0 + S > p.T;  // wave-uniform
+    float ar[S], ai[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      ar[s] = tb[(s * gpw + my_g) * TW];
+      ai[s] = CPLX ? tb[(s * gpw + my_g) * TW + 1] : 0.0f;
+    }
     const int64_t yoff = wave_uniform(((row0 + t0) * (RELU ? 2 * p.M : p.M) + mbase) * ESZ);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      const float ar = tab[(s * gpw + my_g) * TW];
-      const float ai = CPLX ? tab[(s * gpw + my_g) * TW + 1] : 0.0f;
       float xr[V], xi[V];
       unpack<IO, V>(wr[h][s], xr);
       if constexpr (CPLX) unpack<IO, V>(wi[h][s], xi);
+      if (tail && t0 + s >= p.T) {  // no write past T
+#pragma unroll
+        for (int v = 0; v < V; ++v) { xr[v] = 0.0f; xi[v] = 0.0f; }
+      }
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         if constexpr (CPLX) {
-          const float nr = fmaf(ar, hr[v], fmaf(-ai, hi[v], xr[v]));
-          const float ni = fmaf(ai, hr[v], fmaf(ar, hi[v], xi[v]));
+          const float nr = fmaf(ar[s], hr[v], fmaf(-ai[s], hi[v], xr[v]));
+          const float ni = fmaf(ai[s], hr[v], fmaf(ar[s], hi[v], xi[v]));
           hr[v] = nr;
           hi[v] = ni;
         } else {
-          hr[v] = fmaf(ar, hr[v], xr[v]);
+          hr[v] = fmaf(ar[s], hr[v], xr[v]);
         }
       }
-      if (FULL || (lane_ok && t0 + s < p.T)) {
+      if (lane_ok && t0 + s < p.T) {
         const int64_t o = yoff + s * ostride;
         if constexpr (RELU) {
           float rr[V], ri[V];
 #pragma unroll
           for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
-          stb<RawT>(p.y_re, o, lane_bytes, pack<IO, V>(rr));
-          stb<RawT>(p.y_re, o + stride, lane_bytes, pack<IO, V>(ri));
+          stn<RawT, (SPARC_FWD_NT & 2) != 0>(p.y_re, o, lane_bytes, pack<IO, V>(rr));
+          stn<RawT, (SPARC_FWD_NT & 2) != 0>(p.y_re, o + stride, lane_bytes, pack<IO, V>(ri));
         } else {
-          stb<RawT>(p.y_re, o, lane_bytes, pack<IO, V>(hr));
-          if constexpr (CPLX) stb<RawT>(p.y_im, o, lane_bytes, pack<IO, V>(hi));
+          stn<RawT, (SPARC_FWD_NT & 2) != 0>(p.y_re, o, lane_bytes, pack<IO, V>(hr));
+          if constexpr (CPLX) stn<RawT, (SPARC_FWD_NT & 2) != 0>(p.y_im, o, lane_bytes, pack<IO, V>(hi));
         }
       }
     }
   };
 
-  load_block(0, 0);
-  for (int k0 = 0; k0 < n_blocks; k0 += 2) {
+  if (streamer) {
+    load_block(0, 0);
+  } else {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int d = 0; d < kGateDepth - 1; ++d)
+      if (d < n_blocks) load_gate_pairs<TR, IO, S>(p, b, d * S, g_base, gpw, lane, gb[d]);
+    fill_tab<TR, IO, S, TW>(p, 0, g_base, gpw, lane, reset_first, gb[0], tab[0]);
+  }
+  __syncthreads();
+  // block k = k0 + h: planes and table in buffers k & 1 = h & 1, gates in
+  // gb[k % kGateDepth] = gb[h] (k0 is a multiple of kGateDepth)
+  for (int k0 = 0; k0 < n_blocks; k0 += kGateDepth) {
+#pragma unroll
+    for (int h = 0; h < kGateDepth; ++h) {
       const int k = k0 + h;
       if (k >= n_blocks) break;
       const int t0 = k * S;
-      if (k + 1 < n_blocks) load_block(1 - h, k + 1);
-      fill_tab<TR, S, TW>(p, b, t0, gpw, lane, reset_first, gr0[h], gr1[h], tab);
-      __builtin_amdgcn_wave_barrier();
-      if (block_full && t0 + S <= p.T) run_block(std::true_type{}, h, t0);
-      else run_block(std::false_type{}, h, t0);
-      // the state after the last step of a saved-state chunk (steps past T
-      // are the identity, so the last block ends on the state after T-1)
-      const int t_end = t0 + S;
-      if (lane_ok && (t_end % kStateChunk == 0 || t_end >= p.T)) {
-        const int c = (min(t_end, p.T) - 1) / kStateChunk;
-        float* dst = p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + c) * p.M + m0) * NH;
+      const int x = h & 1;
+      if (streamer) {
+        // unconditional (the last block re-reads itself): a path without the
+        // prefetch would make the waits below cover it as well
+        load_block(1 - x, k + 1 < n_blocks ? k + 1 : k);
+        run_block(x, t0, tab[x]);
+        // the state after the last step of a saved-state chunk (steps past T
+        // are the identity, so the last block ends on the state after T-1)
+        const int t_end = t0 + S;
+        if (lane_ok && (t_end % kStateChunk == 0 || t_end >= p.T)) {
+          const int c = (min(t_end, p.T) - 1) / kStateChunk;
+          float* dst = p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + c) * p.M + m0) * NH;
 #pragma unroll
-        for (int v = 0; v < V; ++v) {
-          dst[v * NH] = hr[v];
-          if constexpr (CPLX) dst[v * NH + 1] = hi[v];
+          for (int v = 0; v < V; ++v) {
+            dst[v * NH] = hr[v];
+            if constexpr (CPLX) dst[v * NH + 1] = hi[v];
+          }
         }
+      } else if (k + 1 < n_blocks) {
+        fill_tab<TR, IO, S, TW>(p, t0 + S, g_base, gpw, lane, reset_first, gb[(h + 1) % kGateDepth], tab[1 - x]);
+        if (k + kGateDepth - 1 < n_blocks)
+          load_gate_pairs<TR, IO, S>(p, b, t0 + (kGateDepth - 1) * S, g_base, gpw, lane,
+                                     gb[(h + kGateDepth - 1) % kGateDepth]);
       }
-      __builtin_amdgcn_wave_barrier();  // table reads done before the next fill
+      __syncthreads();
     }
   }
 }
 
-// Backward from the saved forward output (no relu epilogue), one wave per
-// chain in reverse time: lambda_t = dy_t + conj(a_{t+1}) lambda_{t+1},
+// Backward from the saved forward output (no relu epilogue), one chain per
+// workgroup in reverse time: lambda_t = dy_t + conj(a_{t+1}) lambda_{t+1},
 // dw_t = lambda_t, and dL/da_t = lambda_t conj(h_{t-1}) with h_{t-1} read
-// from row t-1 of y (h0 at t = 0).  The transition gradients are summed over
-// the lanes of a group through an LDS transpose once per block, and the
-// polar chain rule (dr, dphi) is applied to the group sums.
+// from row t-1 of y (h0 at t = 0).  Wave 0 runs the adjoint and leaves each
+// lane's per-step transition gradients in LDS; wave 1 sums them over the
+// lanes of each group one block later, applies the polar chain rule (dr,
+// dphi) to the group sums and stores the gate gradients.
 template <int TR, typename IO, int V, int S>
-__global__ void __launch_bounds__(64, 1)
+__global__ void __launch_bounds__(128, 1)
 chain_bwd_serial_kernel(ScanArgs p) {
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
   constexpr bool CPLX = TR != TR_REAL;
@@ -2737,16 +2843,19 @@ chain_bwd_serial_kernel(ScanArgs p) {
   constexpr int NG = CPLX ? 2 : 1;    // transition gradients per (step, group)
   constexpr int RED = S * NG + 1;     // padded LDS row of one lane's partials
   using RawT = typename Raw<IO, V>::T;
-  __shared__ float tab[S * kFastMaxGpw * TW];
-  __shared__ float red[64 * RED];
+  __shared__ float tab[2][S * kFastMaxGpw * TW];
+  __shared__ float red[2][64 * RED];
 
-  const int lane = threadIdx.x;
-  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int n_blocks = (p.T + S - 1) / S;
+  if (n_blocks == 0) return;  // the whole workgroup
+  const int lane = threadIdx.x & 63;
+  const bool streamer = threadIdx.x < 64;  // wave-uniform
+  const int chain = SPARC_SERIAL_SWIZZLE ? xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x))
+                                         : static_cast<int>(blockIdx.x);
   const int b = chain / p.n_mblocks;
   const int mb = chain - b * p.n_mblocks;
   const int m0 = mb * MB + lane * V;
   const bool lane_ok = m0 < p.M;
-  const bool block_full = (mb + 1) * MB <= p.M;  // wave-uniform
   const int gpw = MB / p.gs;
   const int lpg = p.gs / V;
   const int my_g = lane / lpg;
@@ -2756,59 +2865,62 @@ chain_bwd_serial_kernel(ScanArgs p) {
   const int64_t row0 = static_cast<int64_t>(b) * p.T;
   const int64_t mbase = static_cast<int64_t>(mb) * MB;
   const int64_t stride = static_cast<int64_t>(p.M) * ESZ;
-  const int n_blocks = (p.T + S - 1) / S;
 
   float xr[V], xi[V];  // conj(a_{t+1}) lambda_{t+1}: the adjoint flowing into step t
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
-    xr[v] = (p.dlast_re && lane_ok) ? p.dlast_re[i0] : 0.0f;
-    xi[v] = (CPLX && p.dlast_im && lane_ok) ? p.dlast_im[i0] : 0.0f;
+    xr[v] = (streamer && p.dlast_re && lane_ok) ? p.dlast_re[i0] : 0.0f;
+    xi[v] = (streamer && CPLX && p.dlast_im && lane_ok) ? p.dlast_im[i0] : 0.0f;
   }
 
-  // dy rows t0 .. t0+S-1 and y rows t0-1 .. t0+S-2 (the state before each step)
+  // wave 0: dy rows t0 .. t0+S-1 and y rows t0-1 .. t0+S-2 (the state before each step)
   RawT dr[2][S], di[2][S], yr[2][S], yi[2][S];
-  float gr0[2][R], gr1[2][R];
+  GateBlock<S> gb[kGateDepth];  // wave 1: raw gates of iteration j in gb[j % kGateDepth]
+  // Unconditional loads, as in the forward: rows are clamped into [0, T-1]
+  // and lanes past M read the first element of their mode block; run_block
+  // discards what lies outside (dy past T, y before step 0, lanes past M).
+  const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
   auto load_block = [&](int hb, int k) {
     const int t0 = k * S;
     const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
-    if (block_full && t0 > 0 && t0 + S <= p.T) {
+    const int last = p.T - 1 - t0;  // the block's last step inside T (wave-uniform)
 #pragma unroll
-      for (int s = 0; s < S; ++s) {
-        dr[hb][s] = ldb<RawT>(p.dy_re, off + s * stride, lane_bytes);
-        yr[hb][s] = ldb<RawT>(p.y_re, off + (s - 1) * stride, lane_bytes);
-        if constexpr (CPLX) {
-          di[hb][s] = ldb<RawT>(p.dy_im, off + s * stride, lane_bytes);
-          yi[hb][s] = ldb<RawT>(p.y_im, off + (s - 1) * stride, lane_bytes);
-        }
-      }
-    } else {
-      float z[V] = {};
-      const RawT zero = pack<IO, V>(z);
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        const int t = t0 + s;
-        dr[hb][s] = zero; di[hb][s] = zero; yr[hb][s] = zero; yi[hb][s] = zero;
-        if (lane_ok && t < p.T) {
-          dr[hb][s] = ldb<RawT>(p.dy_re, off + s * stride, lane_bytes);
-          if constexpr (CPLX) di[hb][s] = ldb<RawT>(p.dy_im, off + s * stride, lane_bytes);
-          if (t > 0) {
-            yr[hb][s] = ldb<RawT>(p.y_re, off + (s - 1) * stride, lane_bytes);
-            if constexpr (CPLX) yi[hb][s] = ldb<RawT>(p.y_im, off + (s - 1) * stride, lane_bytes);
-          }
-        }
+    for (int s = 0; s < S; ++s) {
+      const int sd = s <= last ? s : last;       // dy row t, clamped
+      const int sy = max(min(s - 1, last), -t0);  // y row t-1, clamped
+      const int64_t od = off + static_cast<int64_t>(sd) * stride;
+      const int64_t oy = off + static_cast<int64_t>(sy) * stride;
+      dr[hb][s] = ldn<RawT, (SPARC_BWD_NT & 1) != 0>(p.dy_re, od, lane_ld);
+      yr[hb][s] = ldn<RawT, (SPARC_BWD_NT & 1) != 0>(p.y_re, oy, lane_ld);
+      if constexpr (CPLX) {
+        di[hb][s] = ldn<RawT, (SPARC_BWD_NT & 1) != 0>(p.dy_im, od, lane_ld);
+        yi[hb][s] = ldn<RawT, (SPARC_BWD_NT & 1) != 0>(p.y_im, oy, lane_ld);
       }
     }
-    load_gate_pairs<TR, IO, S>(p, b, t0, g_base, gpw, lane, gr0[hb], gr1[hb]);
   };
 
-  auto run_block = [&](auto full_tag, int h, int t0) {
-    constexpr bool FULL = decltype(full_tag)::value;
+  // the state before step 0: h0 (fp32) or zero, read once
+  float h0r[V], h0i[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
+    h0r[v] = (streamer && p.h0_re && lane_ok) ? p.h0_re[i0] : 0.0f;
+    h0i[v] = (streamer && CPLX && p.h0_im && lane_ok) ? p.h0_im[i0] : 0.0f;
+  }
+  wait_vm_all();  // the loop-carried adjoint and h0: as in the forward
+
+  auto run_block = [&](int h, int t0, const float* tb, float* rd) {
+    const bool edge = t0 == 0 || t0 + S > p.T;  // wave-uniform
+    float ar[S], ai[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      ar[s] = tb[(s * gpw + my_g) * TW];
+      ai[s] = CPLX ? tb[(s * gpw + my_g) * TW + 1] : 0.0f;
+    }
     const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
 #pragma unroll
     for (int s = S - 1; s >= 0; --s) {
-      const float ar = tab[(s * gpw + my_g) * TW];
-      const float ai = CPLX ? tab[(s * gpw + my_g) * TW + 1] : 0.0f;
       float gy_r[V], gy_i[V], hr[V], hi[V], lr[V], li[V];
       unpack<IO, V>(dr[h][s], gy_r);
       unpack<IO, V>(yr[h][s], hr);
@@ -2816,12 +2928,14 @@ chain_bwd_serial_kernel(ScanArgs p) {
         unpack<IO, V>(di[h][s], gy_i);
         unpack<IO, V>(yi[h][s], hi);
       }
-      if (!FULL && t0 + s == 0) {  // the state before step 0 is h0 (fp32), or zero
+      if (edge) {
+        if (t0 + s >= p.T) {  // past T: no incoming gradient (the transition is the identity)
 #pragma unroll
-        for (int v = 0; v < V; ++v) {
-          const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
-          hr[v] = (p.h0_re && lane_ok) ? p.h0_re[i0] : 0.0f;
-          if constexpr (CPLX) hi[v] = (p.h0_im && lane_ok) ? p.h0_im[i0] : 0.0f;
+          for (int v = 0; v < V; ++v) { gy_r[v] = 0.0f; gy_i[v] = 0.0f; }
+        }
+        if (t0 + s == 0) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) { hr[v] = h0r[v]; hi[v] = h0i[v]; }
         }
       }
 #pragma unroll
@@ -2829,9 +2943,9 @@ chain_bwd_serial_kernel(ScanArgs p) {
         lr[v] = gy_r[v] + xr[v];
         if constexpr (CPLX) li[v] = gy_i[v] + xi[v];
       }
-      if (FULL || (lane_ok && t0 + s < p.T)) {
-        stb<RawT>(p.dw_re, off + s * stride, lane_bytes, pack<IO, V>(lr));
-        if constexpr (CPLX) stb<RawT>(p.dw_im, off + s * stride, lane_bytes, pack<IO, V>(li));
+      if (lane_ok && t0 + s < p.T) {
+        stn<RawT, (SPARC_BWD_NT & 2) != 0>(p.dw_re, off + s * stride, lane_bytes, pack<IO, V>(lr));
+        if constexpr (CPLX) stn<RawT, (SPARC_BWD_NT & 2) != 0>(p.dw_im, off + s * stride, lane_bytes, pack<IO, V>(li));
       }
       float gar = 0.0f, gai = 0.0f;
 #pragma unroll
@@ -2839,70 +2953,103 @@ chain_bwd_serial_kernel(ScanArgs p) {
         if constexpr (CPLX) {
           gar = fmaf(lr[v], hr[v], fmaf(li[v], hi[v], gar));
           gai = fmaf(li[v], hr[v], fmaf(-lr[v], hi[v], gai));
-          xr[v] = fmaf(ar, lr[v], ai * li[v]);
-          xi[v] = fmaf(ar, li[v], -ai * lr[v]);
+          xr[v] = fmaf(ar[s], lr[v], ai[s] * li[v]);
+          xi[v] = fmaf(ar[s], li[v], -ai[s] * lr[v]);
         } else {
           gar = fmaf(lr[v], hr[v], gar);
-          xr[v] = ar * lr[v];
+          xr[v] = ar[s] * lr[v];
         }
       }
-      red[lane * RED + s * NG] = gar;
-      if constexpr (CPLX) red[lane * RED + s * NG + 1] = gai;
+      rd[lane * RED + s * NG] = gar;
+      if constexpr (CPLX) rd[lane * RED + s * NG + 1] = gai;
     }
   };
 
-  load_block(0, n_blocks - 1);
-  for (int k0 = n_blocks - 1; k0 >= 0; k0 -= 2) {
+  // wave 1: group sums of one block's partials rd (table tb, reset mask rm)
+  auto store_block_grads = [&](int t0, const float* tb, const float* rd, uint32_t rm) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int k = k0 - h;
-      if (k < 0) break;
-      const int t0 = k * S;
-      if (k >= 1) load_block(1 - h, k - 1);
-      fill_tab<TR, S, TW>(p, b, t0, gpw, lane, reset_first, gr0[h], gr1[h], tab);
-      __builtin_amdgcn_wave_barrier();
-      if (block_full && t0 > 0 && t0 + S <= p.T) run_block(std::true_type{}, h, t0);
-      else run_block(std::false_type{}, h, t0);
-      __builtin_amdgcn_wave_barrier();
-      // group sums: lane l owns pair l (step l / gpw, group l % gpw)
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int idx = r * 64 + lane;
-        if (idx < S * gpw) {
-          const int step = idx / gpw;
-          const int g = idx - step * gpw;
-          float sr = 0.0f, si = 0.0f;
-          for (int j = 0; j < lpg; ++j) {
-            const float* src = red + (g * lpg + j) * RED + step * NG;
-            sr += src[0];
-            if constexpr (CPLX) si += src[1];
+    for (int r = 0; r < R; ++r) {
+      const int idx = r * 64 + lane;  // pair: step idx / gpw, group idx % gpw
+      if (idx < S * gpw) {
+        const int step = idx / gpw;
+        const int g = idx - step * gpw;
+        float sr = 0.0f, si = 0.0f;
+        for (int j = 0; j < lpg; ++j) {
+          const float* src = rd + (g * lpg + j) * RED + step * NG;
+          sr += src[0];
+          if constexpr (CPLX) si += src[1];
+        }
+        const int t = t0 + step;
+        if (t < p.T && g_base + g < p.G) {  // the last mode block may hold fewer groups
+          float d0 = sr, d1 = si;
+          if constexpr (TR == TR_POLAR) {
+            const float* e = tb + idx * TW;   // (ar, ai, cos phi, sin phi) of this pair
+            d0 = fmaf(sr, e[2], si * e[3]);
+            d1 = fmaf(si, e[0], -sr * e[1]);
           }
-          const int t = t0 + step;
-          if (t < p.T && g_base + g < p.G) {  // the last mode block may hold fewer groups
-            float d0 = sr, d1 = si;
-            if constexpr (TR == TR_POLAR) {
-              const float* e = tab + idx * TW;   // (ar, ai, cos phi, sin phi) of this pair
-              d0 = fmaf(sr, e[2], si * e[3]);
-              d1 = fmaf(si, e[0], -sr * e[1]);
-            }
-            // a reset step's transition is the constant 0: no gradient
-            const bool reset = p.segpos ? (p.segpos[row0 + t] == 0) : (reset_first && t == 0);
-            const int64_t gi = (row0 + t) * p.G + g_base + g;
-            store1<IO>(p.dg0, gi, reset ? 0.0f : d0);
-            if constexpr (CPLX) store1<IO>(p.dg1, gi, reset ? 0.0f : d1);
-          }
+          // a reset step's transition is the constant 0: no gradient
+          const bool reset = (rm >> r) & 1u;
+          const int64_t gi = (row0 + t) * p.G + g_base + g;
+          store1<IO>(p.dg0, gi, reset ? 0.0f : d0);
+          if constexpr (CPLX) store1<IO>(p.dg1, gi, reset ? 0.0f : d1);
         }
       }
-      __builtin_amdgcn_wave_barrier();  // partials and table read before the next block writes them
+    }
+  };
+
+  // Iteration j handles block k = n_blocks-1-j with planes, table and
+  // partials in buffers x = j & 1.  Wave 1, at iteration j: group sums of
+  // block k+1 (table and partials in buffers 1-x), then the table of block
+  // k-1 (into buffers 1-x, after those reads), then the gates of block
+  // k-(kGateDepth-1).
+  uint32_t rm_old = 0u, rm_mid = 0u;  // reset masks: block k+1, block k
+  if (streamer) {
+    load_block(0, n_blocks - 1);
+  } else {
+#pragma unroll
+    for (int d = 0; d < kGateDepth - 1; ++d)
+      if (d < n_blocks) load_gate_pairs<TR, IO, S>(p, b, (n_blocks - 1 - d) * S, g_base, gpw, lane, gb[d]);
+    rm_mid = fill_tab<TR, IO, S, TW>(p, (n_blocks - 1) * S, g_base, gpw, lane, reset_first, gb[0], tab[0]);
+  }
+  __syncthreads();
+  for (int j0 = 0; j0 < n_blocks; j0 += kGateDepth) {
+#pragma unroll
+    for (int h = 0; h < kGateDepth; ++h) {
+      const int j = j0 + h;
+      if (j >= n_blocks) break;
+      const int k = n_blocks - 1 - j;
+      const int t0 = k * S;
+      const int x = h & 1;
+      if (streamer) {
+        load_block(1 - x, k >= 1 ? k - 1 : 0);  // unconditional, as in the forward
+        run_block(x, t0, tab[x], red[x]);
+      } else {
+        if (j >= 1) store_block_grads(t0 + S, tab[1 - x], red[1 - x], rm_old);
+        rm_old = rm_mid;
+        rm_mid = 0u;
+        if (k >= 1) {
+          rm_mid = fill_tab<TR, IO, S, TW>(p, t0 - S, g_base, gpw, lane, reset_first,
+                                           gb[(h + 1) % kGateDepth], tab[1 - x]);
+          if (k >= kGateDepth - 1)
+            load_gate_pairs<TR, IO, S>(p, b, t0 - (kGateDepth - 1) * S, g_base, gpw, lane,
+                                       gb[(h + kGateDepth - 1) % kGateDepth]);
+        }
+      }
+      __syncthreads();
     }
   }
-  if (lane_ok && p.dh0_re) {
+  if (streamer) {
+    if (lane_ok && p.dh0_re) {
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-      const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
-      p.dh0_re[i0] = xr[v];
-      if constexpr (CPLX) p.dh0_im[i0] = xi[v];
+      for (int v = 0; v < V; ++v) {
+        const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
+        p.dh0_re[i0] = xr[v];
+        if constexpr (CPLX) p.dh0_im[i0] = xi[v];
+      }
     }
+  } else {
+    const int hl = (n_blocks - 1) & 1;  // buffers of the last iteration (block 0)
+    store_block_grads(0, tab[hl], red[hl], rm_old);
   }
 }
 
@@ -2953,6 +3100,15 @@ constexpr int kChunk = 64;  // C = S * NW for every instantiation
 // workgroups per CU on a 256-CU MI355X).
 constexpr int kChainMin = 512;
 constexpr int kSerialMin = 1024;  // one wave per chain: a wave for each of the 1024 SIMDs
+// Serial kernels with 4 bf16 modes per lane (8-byte loads per plane): a
+// streaming probe of this access pattern on MI355X moved 5.8 TB/s with 512
+// such waves against 4.9 TB/s with 1024 waves of 4-byte loads, and fell off
+// again at 256 waves.
+constexpr int kWideV = 4;
+#ifndef SPARC_SERIAL_WIDE_MIN
+#define SPARC_SERIAL_WIDE_MIN 512
+#endif
+constexpr int kSerialWideMin = SPARC_SERIAL_WIDE_MIN;
 static_assert(kChunk == sparc::kStateChunk, "one saved-state chunk length");
 
 struct Plan {
@@ -2970,7 +3126,9 @@ struct Plan {
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
 // Chooses V and the gate mode; fills sizes.  Returns an error message or NULL.
-const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl) {
+// allow_wide: the caller can use the 4-mode serial kernels (their pointers are
+// 8-byte aligned and, backward, the states come from the saved output).
+const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl, bool allow_wide = true) {
   if (!d) return "desc is NULL";
   if (d->batch <= 0 || d->length < 0 || d->modes <= 0 || d->groups <= 0) return "B, M, G must be > 0 and T >= 0";
   if (d->modes % d->groups) return "groups must divide modes";
@@ -2997,20 +3155,34 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl) {
     if (mbm % gs == 0 && is_pow2(gs / v)) { V = v; gm = sparc::GATE_LANE; return true; }
     return false;
   };
-  if (!try_v(vmax) && !try_v(1)) return "unsupported gate group size (need G == 1, M/G == 1, M/G dividing 64*V or a multiple of it)";
+  const bool force_l = (d->flags & SPARC_FLAG_ALGO_LOOKBACK) != 0;
+  const bool force_c = (d->flags & SPARC_FLAG_ALGO_CHAIN) != 0;
+  const bool force_s = (d->flags & SPARC_FLAG_ALGO_SERIAL) != 0;
+  if (int(force_l) + int(force_c) + int(force_s) > 1)
+    return "ALGO_LOOKBACK, ALGO_CHAIN and ALGO_SERIAL are exclusive";
+  // Complex bf16 with lane-shared gates: the serial kernels stream 8 bytes
+  // per lane and plane (4 modes) when that still leaves enough chains.
+  bool wide = false;
+  if (!p1 && d->transition != SPARC_TRANSITION_REAL && d->io_dtype == SPARC_BF16 && M % kWideV == 0 &&
+      gs % kWideV == 0 && (64 * kWideV) % gs == 0 && is_pow2(gs / kWideV) &&
+      (64 * kWideV) / gs <= sparc::kFastMaxGpw && !force_l && !force_c && allow_wide) {
+    const int64_t chains = d->batch * ((M + 64 * kWideV - 1) / (64 * kWideV));
+    wide = force_s || chains >= kSerialWideMin;
+  }
+  if (wide) {
+    V = kWideV;
+    gm = sparc::GATE_LANE;
+  } else if (!try_v(vmax) && !try_v(1)) {
+    return "unsupported gate group size (need G == 1, M/G == 1, M/G dividing 64*V or a multiple of it)";
+  }
   pl->V = V;
   pl->gm = gm;
   pl->n_chunks = static_cast<int>((d->length + kChunk - 1) / kChunk);
   pl->n_mblocks = static_cast<int>((M + 64 * V - 1) / (64 * V));
   pl->n_chains = static_cast<int>(d->batch * pl->n_mblocks);
   pl->n_tiles = static_cast<int64_t>(pl->n_chains) * pl->n_chunks;
-  const bool force_l = (d->flags & SPARC_FLAG_ALGO_LOOKBACK) != 0;
-  const bool force_c = (d->flags & SPARC_FLAG_ALGO_CHAIN) != 0;
-  const bool force_s = (d->flags & SPARC_FLAG_ALGO_SERIAL) != 0;
-  if (int(force_l) + int(force_c) + int(force_s) > 1)
-    return "ALGO_LOOKBACK, ALGO_CHAIN and ALGO_SERIAL are exclusive";
   const bool lane_shared = !p1 && gm == sparc::GATE_LANE && (64 * V) / gs <= sparc::kFastMaxGpw;
-  pl->serial = lane_shared && (force_s || (!force_l && !force_c && pl->n_chains >= kSerialMin));
+  pl->serial = wide || (lane_shared && (force_s || (!force_l && !force_c && pl->n_chains >= kSerialMin)));
   pl->chain = pl->serial || force_c || force_s || (!force_l && pl->n_chains >= kChainMin);
   pl->fast = pl->chain && lane_shared;
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
@@ -3061,9 +3233,9 @@ struct Kernels {
       if (pl.serial && dir == 0) {
         const dim3 g(static_cast<unsigned>(pl.n_chains));
         if ((a.flags & SPARC_FLAG_RELU_OUTPUT) && TR != sparc::TR_REAL)
-          hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, true>), g, dim3(64), 0, st, a);
+          hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, true>), g, dim3(128), 0, st, a);
         else
-          hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, false>), g, dim3(64), 0, st, a);
+          hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, false>), g, dim3(128), 0, st, a);
         return;
       }
       if (chain && pl.fast) {
@@ -3091,7 +3263,7 @@ struct Kernels {
     if constexpr (TR != sparc::TR_P1 && GM == sparc::GATE_LANE) {
       if (pl.serial) {
         const dim3 g(static_cast<unsigned>(pl.n_chains));
-        hipLaunchKernelGGL((sparc::chain_bwd_serial_kernel<TR, IO, V, kSerialBwdS>), g, dim3(64), 0, st, a);
+        hipLaunchKernelGGL((sparc::chain_bwd_serial_kernel<TR, IO, V, kSerialBwdS>), g, dim3(128), 0, st, a);
         return true;
       }
       if (pl.chain && pl.fast) {
@@ -3131,6 +3303,23 @@ bool launch_v(int dir, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a)
     Kernels<TR, IO, VV, GG>::run(dir, pl.chain, pl, st, a);                              \
     return true;                                                                        \
   }
+  if constexpr ((TR == sparc::TR_POLAR || TR == sparc::TR_CART) && sparc::IsBf16<IO>::value) {
+    if (V == kWideV) {
+      if (!pl.serial || gm != sparc::GATE_LANE) return false;
+      if (dir == 1) return false;  // no recomputing kernel: wide plans need the saved output
+      if (dir == 2) {
+        const dim3 g(static_cast<unsigned>(pl.n_chains));
+        hipLaunchKernelGGL((sparc::chain_bwd_serial_kernel<TR, IO, kWideV, kSerialBwdS>), g, dim3(128), 0, st, a);
+        return true;
+      }
+      const dim3 g(static_cast<unsigned>(pl.n_chains));
+      if (a.flags & SPARC_FLAG_RELU_OUTPUT)
+        hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, kWideV, kSerialFwdS, true>), g, dim3(128), 0, st, a);
+      else
+        hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, kWideV, kSerialFwdS, false>), g, dim3(128), 0, st, a);
+      return true;
+    }
+  }
   SPARC_LAUNCH(VM, sparc::GATE_LANE)
   SPARC_LAUNCH(VM, sparc::GATE_CROSS)
   SPARC_LAUNCH(1, sparc::GATE_LANE)
@@ -3162,6 +3351,7 @@ bool launch(int dir, const sparc_scan_desc* d, const Plan& pl, hipStream_t st, c
 }
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+bool aligned8(const void* p) { return aligned(p, 8); }  // NULL counts as aligned
 
 }  // namespace
 
@@ -3178,14 +3368,15 @@ int64_t sparc_scan_chunk_count(const sparc_scan_desc* d) {
 }
 
 size_t sparc_scan_workspace_bytes(const sparc_scan_desc* d, int direction) {
-  Plan pl;
-  if (make_plan(d, direction, &pl)) return 0;
-  return pl.total;
+  // enough for either plan: the call decides from its pointers
+  Plan pw, pn;
+  if (make_plan(d, direction, &pw, true) || make_plan(d, direction, &pn, false)) return 0;
+  return pw.total > pn.total ? pw.total : pn.total;
 }
 
 static sparc_status common_checks(const sparc_scan_desc* d, int dir, Plan* pl,
-                                  void* workspace, size_t workspace_bytes) {
-  if (const char* e = make_plan(d, dir, pl)) return fail(SPARC_EINVAL, "%s", e);
+                                  void* workspace, size_t workspace_bytes, bool allow_wide) {
+  if (const char* e = make_plan(d, dir, pl, allow_wide)) return fail(SPARC_EINVAL, "%s", e);
   if (!workspace) return fail(SPARC_EWORKSPACE, "workspace is NULL");
   if (workspace_bytes < pl->total)
     return fail(SPARC_EWORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, pl->total);
@@ -3237,7 +3428,8 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, con
                                 void* y_re, void* y_im, float* chunk_state,
                                 void* workspace, size_t workspace_bytes, sparc_stream_t stream) {
   Plan pl;
-  if (sparc_status s = common_checks(d, 0, &pl, workspace, workspace_bytes)) return s;
+  const bool wide_ok = aligned8(w_re) && aligned8(w_im) && aligned8(y_re) && aligned8(y_im);
+  if (sparc_status s = common_checks(d, 0, &pl, workspace, workspace_bytes, wide_ok)) return s;
   if (d->length == 0) return SPARC_OK;  // nothing to read or write
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
   const bool relu = (d->flags & SPARC_FLAG_RELU_OUTPUT) != 0;
@@ -3271,7 +3463,7 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, con
   a.w_re = w_re; a.w_im = w_im; a.h0_re = h0_re; a.h0_im = h0_im; a.segpos = segment_pos;
   a.y_re = y_re; a.y_im = y_im; a.chunk_state = chunk_state;
   fill_ws(a, pl, workspace);
-  launch(0, d, pl, st, a);
+  if (!launch(0, d, pl, st, a)) return fail(SPARC_EUNSUPPORTED, "no forward kernel for this plan");
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SPARC_EHIP, "scan forward launch: %s", hipGetErrorString(e));
   return SPARC_OK;
@@ -3311,9 +3503,13 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
                                  float* dh0_re, float* dh0_im,
                                  void* workspace, size_t workspace_bytes, sparc_stream_t stream) {
   Plan pl;
-  if (sparc_status s = common_checks(d, 1, &pl, workspace, workspace_bytes)) return s;
+  const bool relu = d && (d->flags & SPARC_FLAG_RELU_OUTPUT) != 0;
+  // the 4-mode serial backward reads the states from the saved output
+  const bool wide_ok = y_re && !relu && aligned8(w_re) && aligned8(w_im) && aligned8(y_re) &&
+                       aligned8(y_im) && aligned8(dy_re) && aligned8(dy_im) && aligned8(dw_re) &&
+                       aligned8(dw_im);
+  if (sparc_status s = common_checks(d, 1, &pl, workspace, workspace_bytes, wide_ok)) return s;
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
-  const bool relu = (d->flags & SPARC_FLAG_RELU_OUTPUT) != 0;
   const bool p1 = d->transition == SPARC_TRANSITION_P1;
   if (d->length == 0) {
     if (p1 && (!dnu_log || !dtheta_log)) return fail(SPARC_EINVAL, "P1 needs dnu_log, dtheta_log");
@@ -3362,7 +3558,8 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
     a.y_im = const_cast<void*>(y_im);
   }
   fill_ws(a, pl, workspace);
-  if (!(saved && launch(2, d, pl, st, a))) launch(1, d, pl, st, a);
+  if (!(saved && launch(2, d, pl, st, a)) && !launch(1, d, pl, st, a))
+    return fail(SPARC_EUNSUPPORTED, "no backward kernel for this plan");
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SPARC_EHIP, "scan backward launch: %s", hipGetErrorString(e));
   // deterministic reductions of the per-tile partials
