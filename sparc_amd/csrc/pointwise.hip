@@ -259,8 +259,12 @@ decode_kernel(int M, const void* x, const float* pdir, const float* rdir,
 // workgroups, per-(row, mode) update with cheap arithmetic
 // ---------------------------------------------------------------------------
 constexpr int kDecodeConsts = 8;  // floats per mode in the constants table
-constexpr int kDotSplit = 8;      // workgroups per row for the control dot products
+constexpr int kDotSplit = 16;     // slices per row for the control dot products
+constexpr int kDotRows = 4;       // rows per dot workgroup (direction loads reused)
 constexpr int kDecodeRows = 4;    // rows per update workgroup (constants reused)
+#ifndef SPARC_DECODE_PREFETCH
+#define SPARC_DECODE_PREFETCH 1
+#endif
 
 // consts[m] = (nu, cos theta, sin theta, gamma, 1/expm1(-2 nu), wpr, wrr, theta)
 __global__ void __launch_bounds__(256)
@@ -278,36 +282,53 @@ decode_prepare_kernel(int M, const float* nu_log, const float* theta_log, const 
 }
 
 // part[b, k, 0..1] = partial dot products of row b's inputs with the phase and
-// radial directions over slice k of the 2M inputs
+// radial directions over slice k of the 2M inputs.  A workgroup covers
+// kDotRows rows of one slice, so each direction value it loads serves every
+// row; each thread takes 4 consecutive inputs per row and pass.
 template <typename IO>
 __global__ void __launch_bounds__(256)
-decode_dots_kernel(int W, const void* x, const float* pdir, const float* rdir, float* part) {
-  __shared__ float red[2][4];
-  const int b = blockIdx.y, k = blockIdx.x;
-  const int slice = ((W / 2 + kDotSplit - 1) / kDotSplit) * 2;  // even: pairs stay in one slice
+decode_dots_kernel(int B, int W, const void* x, const float* pdir, const float* rdir, float* part) {
+  __shared__ float red[kDotRows][2][4];
+  const int k = blockIdx.x, b0 = blockIdx.y * kDotRows;
+  const int slice = ((W + kDotSplit * 4 - 1) / (kDotSplit * 4)) * 4;  // a multiple of 4 (W is)
   const int lo = k * slice, hi = min(W, lo + slice);
-  const int64_t xrow = static_cast<int64_t>(b) * W;
-  float p0 = 0.0f, p1 = 0.0f;
-  for (int i = lo + threadIdx.x * 2; i < hi; i += 512) {
-    float xv[2];
-    unpack<IO, 2>(load_raw<IO, 2>(x, xrow + i), xv);
-    const float2 pd = *reinterpret_cast<const float2*>(pdir + i);
-    const float2 rd = *reinterpret_cast<const float2*>(rdir + i);
-    p0 = fmaf(xv[0], pd.x, fmaf(xv[1], pd.y, p0));
-    p1 = fmaf(xv[0], rd.x, fmaf(xv[1], rd.y, p1));
-  }
+  float p0[kDotRows], p1[kDotRows];
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    p0 += __shfl_xor(p0, off, 64);
-    p1 += __shfl_xor(p1, off, 64);
+  for (int r = 0; r < kDotRows; ++r) { p0[r] = 0.0f; p1[r] = 0.0f; }
+  for (int i = lo + threadIdx.x * 4; i < hi; i += 1024) {
+    const float2 pa = *reinterpret_cast<const float2*>(pdir + i);
+    const float2 pb = *reinterpret_cast<const float2*>(pdir + i + 2);
+    const float2 ra = *reinterpret_cast<const float2*>(rdir + i);
+    const float2 rb = *reinterpret_cast<const float2*>(rdir + i + 2);
+    float xv[kDotRows][4];
+#pragma unroll
+    for (int r = 0; r < kDotRows; ++r) {  // every load first, then the arithmetic
+      const int b = min(b0 + r, B - 1);   // rows past B repeat the last row, unused
+      // a cached load: the update kernel reads x again right after this one
+      unpack<IO, 4>(load_raw<IO, 4>(x, static_cast<int64_t>(b) * W + i), xv[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < kDotRows; ++r) {
+      p0[r] = fmaf(xv[r][0], pa.x, fmaf(xv[r][1], pa.y, fmaf(xv[r][2], pb.x, fmaf(xv[r][3], pb.y, p0[r]))));
+      p1[r] = fmaf(xv[r][0], ra.x, fmaf(xv[r][1], ra.y, fmaf(xv[r][2], rb.x, fmaf(xv[r][3], rb.y, p1[r]))));
+    }
   }
   const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) { red[0][wave] = p0; red[1][wave] = p1; }
+#pragma unroll
+  for (int r = 0; r < kDotRows; ++r) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      p0[r] += __shfl_xor(p0[r], off, 64);
+      p1[r] += __shfl_xor(p1[r], off, 64);
+    }
+    if ((threadIdx.x & 63) == 0) { red[r][0][wave] = p0[r]; red[r][1][wave] = p1[r]; }
+  }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float* o = part + (static_cast<int64_t>(b) * kDotSplit + k) * 2;
-    o[0] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
-    o[1] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  if (threadIdx.x < kDotRows && b0 + static_cast<int>(threadIdx.x) < B) {
+    const int r = threadIdx.x;
+    float* o = part + (static_cast<int64_t>(b0 + r) * kDotSplit + k) * 2;
+    o[0] = red[r][0][0] + red[r][0][1] + red[r][0][2] + red[r][0][3];
+    o[1] = red[r][1][0] + red[r][1][1] + red[r][1][2] + red[r][1][3];
   }
 }
 
@@ -381,17 +402,50 @@ decode_update_kernel(int B, int M, const void* x, const float* pbias, const floa
     nu[v] = c0.x; ct[v] = c0.y; stt[v] = c0.z; gam[v] = c0.w;
     cinv[v] = c1.x; wp[v] = c1.y; wrr_[v] = c1.z;
   }
+  // Row loads are issued ahead of the stores of earlier rows (the new state
+  // may be the old one, in place, so the compiler cannot hoist them itself):
+  // SPARC_DECODE_PREFETCH 0: none, 1: the next row, 2: every row first.  Rows
+  // past B repeat the last row and are not stored.
+  using XR = typename Raw<IO, SV>::T;
+  constexpr int NB = SPARC_DECODE_PREFETCH == 2 ? kDecodeRows : (SPARC_DECODE_PREFETCH == 1 ? 2 : 1);
+  XR xr_raw[NB], xi_raw[NB];
+  float4 hr_raw[NB], hi_raw[NB];
+  auto load_row = [&](int slot, int r) {
+    const int b = min(b0 + r, B - 1);
+    const int64_t srow = static_cast<int64_t>(b) * M + m0;
+    const int64_t xrow = static_cast<int64_t>(b) * 2 * M + m0;
+    xr_raw[slot] = load_raw_nt<IO, SV>(x, xrow);
+    xi_raw[slot] = load_raw_nt<IO, SV>(x, xrow + M);
+    hr_raw[slot] = load_raw<float, SV>(st_re, srow);
+    hi_raw[slot] = load_raw<float, SV>(st_im, srow);
+  };
+  if constexpr (SPARC_DECODE_PREFETCH == 2) {
+#pragma unroll
+    for (int r = 0; r < kDecodeRows; ++r) load_row(r, r);
+  } else if constexpr (SPARC_DECODE_PREFETCH == 1) {
+    load_row(0, 0);
+  }
+#pragma unroll
   for (int r = 0; r < kDecodeRows; ++r) {
     const int b = b0 + r;
     if (b >= B) break;
+    int slot = 0;
+    if constexpr (SPARC_DECODE_PREFETCH == 2) {
+      slot = r;
+    } else if constexpr (SPARC_DECODE_PREFETCH == 1) {
+      slot = r & 1;
+      if (r + 1 < kDecodeRows) load_row((r + 1) & 1, r + 1);
+    } else {
+      load_row(0, r);
+    }
     const float ps = s_row[r][0], rs = s_row[r][1], E = s_row[r][2], delta = s_row[r][3];
     const int64_t srow = static_cast<int64_t>(b) * M + m0;
     const int64_t xrow = static_cast<int64_t>(b) * 2 * M + m0;
     float xr[SV], xi[SV], hr[SV], hi[SV];
-    unpack<IO, SV>(load_raw_nt<IO, SV>(x, xrow), xr);
-    unpack<IO, SV>(load_raw_nt<IO, SV>(x, xrow + M), xi);
-    unpack<float, SV>(load_raw<float, SV>(st_re, srow), hr);
-    unpack<float, SV>(load_raw<float, SV>(st_im, srow), hi);
+    unpack<IO, SV>(xr_raw[slot], xr);
+    unpack<IO, SV>(xi_raw[slot], xi);
+    unpack<float, SV>(hr_raw[slot], hr);
+    unpack<float, SV>(hi_raw[slot], hi);
     float yr[SV], yi[SV];
 #pragma unroll
     for (int v = 0; v < SV; ++v) {
@@ -426,6 +480,14 @@ decode_update_kernel(int B, int M, const void* x, const float* pbias, const floa
 // SV modes per thread (4: one 16-byte state load per plane).  A thread's modes
 // lie in one gate group when the group size is a multiple of SV, and then a
 // polar, cartesian or real transition is computed once per thread.
+// Cache policy of the decode step: the state (reused next step) and the
+// step's writes (read once) separately; 1 = non-temporal.
+#ifndef SPARC_STEP_STATE_NT
+#define SPARC_STEP_STATE_NT 1
+#endif
+#ifndef SPARC_STEP_W_NT
+#define SPARC_STEP_W_NT 1
+#endif
 template <int TR, typename IO, int SV, bool RELU>
 __global__ void __launch_bounds__(256)
 scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* g0, const void* g1,
@@ -438,12 +500,19 @@ scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* 
   const int b = static_cast<int>(i / M);
   const int m = static_cast<int>(i - static_cast<int64_t>(b) * M);
   float hr[SV], hi[SV], wr[SV], wi[SV];
-  // everything here is touched once per step: non-temporal accesses
-  unpack<float, SV>(load_raw_nt<float, SV>(st_re, i), hr);
-  unpack<IO, SV>(load_raw_nt<IO, SV>(w_re, i), wr);
-  if constexpr (CPLX) {
-    unpack<float, SV>(load_raw_nt<float, SV>(st_im, i), hi);
-    unpack<IO, SV>(load_raw_nt<IO, SV>(w_im, i), wi);
+  if constexpr (SPARC_STEP_STATE_NT) {
+    unpack<float, SV>(load_raw_nt<float, SV>(st_re, i), hr);
+    if constexpr (CPLX) unpack<float, SV>(load_raw_nt<float, SV>(st_im, i), hi);
+  } else {
+    unpack<float, SV>(load_raw<float, SV>(st_re, i), hr);
+    if constexpr (CPLX) unpack<float, SV>(load_raw<float, SV>(st_im, i), hi);
+  }
+  if constexpr (SPARC_STEP_W_NT) {
+    unpack<IO, SV>(load_raw_nt<IO, SV>(w_re, i), wr);
+    if constexpr (CPLX) unpack<IO, SV>(load_raw_nt<IO, SV>(w_im, i), wi);
+  } else {
+    unpack<IO, SV>(load_raw<IO, SV>(w_re, i), wr);
+    if constexpr (CPLX) unpack<IO, SV>(load_raw<IO, SV>(w_im, i), wi);
   }
   // P1 transitions also depend on each mode's nu and theta
   const bool shared = TR != TR_P1 && gs % SV == 0;  // uniform over the launch
@@ -488,8 +557,13 @@ scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* 
       hr[v] = fmaf(ar[v], hr[v], wr[v]);
     }
   }
-  store_raw_nt<float, SV>(st_re, i, pack<float, SV>(hr));
-  if constexpr (CPLX) store_raw_nt<float, SV>(st_im, i, pack<float, SV>(hi));
+  if constexpr (SPARC_STEP_STATE_NT) {
+    store_raw_nt<float, SV>(st_re, i, pack<float, SV>(hr));
+    if constexpr (CPLX) store_raw_nt<float, SV>(st_im, i, pack<float, SV>(hi));
+  } else {
+    store_raw<float, SV>(st_re, i, pack<float, SV>(hr));
+    if constexpr (CPLX) store_raw<float, SV>(st_im, i, pack<float, SV>(hi));
+  }
   if (y_re) {
     if constexpr (RELU) {
       float rr[SV], ri[SV];
@@ -730,14 +804,14 @@ sparc_status sparc_decode_step_prepared(int64_t batch, int64_t modes, int32_t io
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int M = static_cast<int>(modes), W = 2 * M;
   float* part = static_cast<float*>(workspace);
-  const dim3 gd(sparc::kDotSplit, static_cast<unsigned>(batch));
+  const dim3 gd(sparc::kDotSplit, static_cast<unsigned>((batch + sparc::kDotRows - 1) / sparc::kDotRows));
   const dim3 gu(static_cast<unsigned>((M / 4 + 255) / 256), static_cast<unsigned>((batch + sparc::kDecodeRows - 1) / sparc::kDecodeRows));
   if (io_dtype == SPARC_BF16) {
-    hipLaunchKernelGGL(sparc::decode_dots_kernel<sparc::bf16>, gd, dim3(256), 0, st, W, x, phase_direction, radial_direction, part);
+    hipLaunchKernelGGL(sparc::decode_dots_kernel<sparc::bf16>, gd, dim3(256), 0, st, static_cast<int>(batch), W, x, phase_direction, radial_direction, part);
     hipLaunchKernelGGL(sparc::decode_update_kernel<sparc::bf16>, gu, dim3(256), 0, st, static_cast<int>(batch), M, x,
                        phase_direction + W, radial_direction + W, part, consts, state_re, state_im, new_re, new_im, y);
   } else {
-    hipLaunchKernelGGL(sparc::decode_dots_kernel<float>, gd, dim3(256), 0, st, W, x, phase_direction, radial_direction, part);
+    hipLaunchKernelGGL(sparc::decode_dots_kernel<float>, gd, dim3(256), 0, st, static_cast<int>(batch), W, x, phase_direction, radial_direction, part);
     hipLaunchKernelGGL(sparc::decode_update_kernel<float>, gu, dim3(256), 0, st, static_cast<int>(batch), M, x,
                        phase_direction + W, radial_direction + W, part, consts, state_re, state_im, new_re, new_im, y);
   }
