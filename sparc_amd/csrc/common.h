@@ -78,6 +78,47 @@ __device__ __forceinline__ void store_raw_nt(void* base, int64_t index, typename
   __builtin_nontemporal_store(n, reinterpret_cast<N*>(static_cast<IO*>(base) + index));
 }
 
+// Buffer loads and stores with an explicit cache policy (the cpol immediate of
+// gfx950 vector memory instructions: sc0 = 1, nt = 2, sc1 = 16).  sc1 on data
+// that is reused only by the next launch keeps it out of the per-XCD L2 and
+// serves it from the memory-side Infinity Cache.  A resource covers ``bytes``
+// from ``base``; accesses past it read 0 and drop stores.
+enum : int { CPOL_DEFAULT = 0, CPOL_SC0 = 1, CPOL_NT = 2, CPOL_SC1 = 16 };
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), bytes,
+                                           0x00020000);
+}
+template <int V, int CPOL>
+__device__ __forceinline__ void buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float (&o)[V]) {
+  static_assert(V == 1 || V == 2 || V == 4, "1, 2 or 4 floats");
+  if constexpr (V == 4) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, CPOL);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = __uint_as_float(v[k]);
+  } else if constexpr (V == 2) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, CPOL);
+    o[0] = __uint_as_float(v[0]);
+    o[1] = __uint_as_float(v[1]);
+  } else {
+    o[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, CPOL));
+  }
+}
+template <int V, int CPOL>
+__device__ __forceinline__ void buffer_store_f32(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, const float (&i)[V]) {
+  static_assert(V == 1 || V == 2 || V == 4, "1, 2 or 4 floats");
+  if constexpr (V == 4) {
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const u4 v = {__float_as_uint(i[0]), __float_as_uint(i[1]), __float_as_uint(i[2]), __float_as_uint(i[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, byte_off, 0, CPOL);
+  } else if constexpr (V == 2) {
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    const u2 v = {__float_as_uint(i[0]), __float_as_uint(i[1])};
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, byte_off, 0, CPOL);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(i[0]), r, byte_off, 0, CPOL);
+  }
+}
+
 template <typename IO, int V>
 __device__ __forceinline__ void unpack(const typename Raw<IO, V>::T& r, float (&o)[V]) {
   if constexpr (sizeof(IO) == 4) {
