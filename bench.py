@@ -151,6 +151,79 @@ def bench_scan(args, dev):
     )
 
 
+def bench_cfg3(args, dev):
+    """cfg3, reported beside the headline: the real scan, B=4, T=65536,
+    D=512, N=8 (M = 4096 modes, G = 512 gate groups of 8), fp32 throughout,
+    a ~ U[0.95, 0.9999] per (b, t, d), w and dy ~ N(0, 1).  64 chains of 256
+    modes: the decoupled look-back kernels, one workgroup per (chain, 64-step
+    chunk); the backward reads the states from the saved output.
+
+    Algorithmic bytes: forward B*T*(8*M + 4*G) (read w, write y; read a),
+    backward B*T*(12*M + 8*G) (read dy and y, write dw; read a, write da)."""
+    from sparc_amd import _lib
+    lib = _lib.load()
+    B, T, D, N = 4, 65536, 512, 8
+    M, G = D * N, D
+    g = torch.Generator(device=dev).manual_seed(0)
+    a = 0.95 + 0.0499 * torch.rand(B, T, G, device=dev, generator=g)
+    w = torch.randn(B, T, M, device=dev, generator=g)
+    dy = torch.randn(B, T, M, device=dev, generator=g)
+    y, dw, da = torch.empty_like(w), torch.empty_like(w), torch.empty_like(a)
+    d = _lib.ScanDesc(B, T, M, G, _lib.TRANSITIONS["real"], _lib.SPARC_F32, _lib.SPARC_F32, 0)
+    cs = torch.empty(B, lib.sparc_scan_chunk_count(ctypes.byref(d)), M, device=dev)
+    ws_f = torch.empty(lib.sparc_scan_workspace_bytes(ctypes.byref(d), 0), dtype=torch.uint8, device=dev)
+    ws_b = torch.empty(lib.sparc_scan_workspace_bytes(ctypes.byref(d), 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    st = stream.cuda_stream
+    P = _lib.ptr
+
+    def fwd():
+        _lib.check(lib.sparc_scan_forward(ctypes.byref(d), P(a), None, None, None, P(w), None, None, None,
+                                          None, P(y), None, P(cs), P(ws_f), ws_f.numel(), st), "forward")
+
+    def bwd():
+        _lib.check(lib.sparc_scan_backward(
+            ctypes.byref(d), P(a), None, None, None, P(w), None, P(y), None, None, None, None, P(cs),
+            P(dy), None, None, None, P(dw), None, P(da), None, None, None, None, None,
+            P(ws_b), ws_b.numel(), st), "backward")
+
+    for _ in range(2):
+        fwd()
+        bwd()
+    steps = max(3, args.steps // 4)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for e0, e1, e2 in ev:
+        e0.record(stream)
+        fwd()
+        e1.record(stream)
+        bwd()
+        e2.record(stream)
+    torch.cuda.synchronize(dev)
+    elapsed = time.perf_counter() - t0
+    if lib.sparc_scan_workspace_error(P(ws_f), st) or lib.sparc_scan_workspace_error(P(ws_b), st):
+        raise RuntimeError("a look-back wait hit its bound in the cfg3 run")
+    fwd_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in ev) / steps
+    bwd_ms = sum(e1.elapsed_time(e2) for _, e1, e2 in ev) / steps
+    bytes_fwd = B * T * (8 * M + 4 * G)
+    bytes_bwd = B * T * (12 * M + 8 * G)
+    ms_step = elapsed * 1e3 / steps
+    del a, w, dy, y, dw, da, cs
+    return {
+        "workload": "real scan fwd+bwd, fp32, gates shared by the N=8 states of a channel",
+        "B": B, "T": T, "D": D, "N": N, "M": M, "G": G, "steps": steps,
+        "tokens_per_s": round(B * T * steps / elapsed, 1), "ms_per_step": round(ms_step, 4),
+        "step_frac": round((bytes_fwd + bytes_bwd) / ms_step / 1e6 / HBM_PEAK_GBS, 4),
+        "forward": {"kernel": "scan_fwd_kernel (look-back)", "avg_launch_ms": round(fwd_ms, 4),
+                    "bytes_per_launch": bytes_fwd,
+                    "frac": round(bytes_fwd / fwd_ms / 1e6 / HBM_PEAK_GBS, 4)},
+        "backward": {"kernel": "scan_bwd_kernel (look-back, saved output)", "avg_launch_ms": round(bwd_ms, 4),
+                     "bytes_per_launch": bytes_bwd,
+                     "frac": round(bytes_bwd / bwd_ms / 1e6 / HBM_PEAK_GBS, 4)},
+    }
+
+
 def _graph_time_us(dev, n_graph, reps, step_fn):
     """Captures reps HIP graphs of n_graph calls step_fn(i) (i = global step)
     after one eager call, replays them all once untimed and once timed;
@@ -287,6 +360,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cfg3", action="store_true", help="skip the cfg3 (real, T=65536) report")
     ap.add_argument("--algo", default="auto", choices=["auto", "serial", "chain", "lookback"],
                     help="scan algorithm (auto picks the serial kernels at this shape)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -309,6 +383,7 @@ def main():
         torch.cuda.synchronize(dev)
         del src, dst
     res = bench_scan(args, dev)
+    cfg3 = None if args.no_cfg3 else bench_cfg3(args, dev)
     core = None if args.no_decode else bench_decode_core(args, dev)
     dec = None if args.no_decode else bench_decode(args, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
@@ -358,6 +433,7 @@ def main():
                 "us_per_step": round(dec["us_per_step"], 2), "tokens_per_s": round(dec["tokens_per_s"], 1),
                 "steps": dec["steps"], "bytes_per_step": dec["bytes_per_step"], "GB_s": round(dec["gbs"], 1),
                 "form": "SPARCMixer.step (P1 controls and write from x), bf16 x/y, fp32 state in place"}},
+        "cfg3": cfg3,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

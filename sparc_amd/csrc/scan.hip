@@ -92,6 +92,76 @@ struct ScanArgs {
   float* carry;       // backward inclusive adjoint carries [B, n_chunks, M, NH]
 };
 
+// A 64-bit value every lane of the wave holds, moved to scalar registers, so
+// that a memory instruction can take (kernel-argument pointer + this offset)
+// as its scalar base and the lane's byte offset as its vector offset.
+__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+template <typename T>
+__device__ __forceinline__ T ldb(const void* base, int64_t byte_off, uint32_t lane_bytes) {
+  return *reinterpret_cast<const T*>(static_cast<const char*>(base) + byte_off + lane_bytes);
+}
+template <typename T>
+__device__ __forceinline__ void stb(void* base, int64_t byte_off, uint32_t lane_bytes, T v) {
+  *reinterpret_cast<T*>(static_cast<char*>(base) + byte_off + lane_bytes) = v;
+}
+// Non-temporal forms of ldb / stb for the streamed planes of the serial
+// kernels, each element of which is read or written once per launch: the nt
+// cache policy keeps them from displacing lines that are reused.
+// Cache policy of the serial kernels' plane loads and stores: bit 0 loads,
+// bit 1 stores non-temporal (forward and backward separately).
+#ifndef SPARC_FWD_NT
+#define SPARC_FWD_NT 3
+#endif
+#ifndef SPARC_BWD_NT
+#define SPARC_BWD_NT 3
+#endif
+template <typename T, bool NT = true>
+__device__ __forceinline__ T ldn(const void* base, int64_t byte_off, uint32_t lane_bytes) {
+  if constexpr (!NT) return ldb<T>(base, byte_off, lane_bytes);
+  using N = typename NtBits<sizeof(T)>::T;
+  const N n = __builtin_nontemporal_load(
+      reinterpret_cast<const N*>(static_cast<const char*>(base) + byte_off + lane_bytes));
+  T r;
+  __builtin_memcpy(&r, &n, sizeof(T));
+  return r;
+}
+template <typename T, bool NT = true>
+__device__ __forceinline__ void stn(void* base, int64_t byte_off, uint32_t lane_bytes, T v) {
+  if constexpr (!NT) { stb<T>(base, byte_off, lane_bytes, v); return; }
+  using N = typename NtBits<sizeof(T)>::T;
+  N n;
+  __builtin_memcpy(&n, &v, sizeof(T));
+  __builtin_nontemporal_store(n, reinterpret_cast<N*>(static_cast<char*>(base) + byte_off + lane_bytes));
+}
+
+// Cache policy of the look-back kernels' streamed planes (w, y, dy, dw): bit 0
+// non-temporal loads, bit 1 non-temporal stores.  Measured at B=4, T=65536,
+// M=4096 (real, fp32): both non-temporal 1.64 / 2.66 ms forward / backward,
+// neither 1.72 / 2.79 ms.
+#ifndef SPARC_LB_NT
+#define SPARC_LB_NT 3
+#endif
+// A plane row of the look-back kernels: ``row_elems`` (wave-uniform element
+// offset of the row's mode block) in scalar registers, the lane's V elements
+// at ``lane_bytes`` in a vector register.
+template <typename IO, int V>
+__device__ __forceinline__ typename Raw<IO, V>::T lb_load(const void* base, int64_t row_elems,
+                                                          uint32_t lane_bytes) {
+  return ldn<typename Raw<IO, V>::T, (SPARC_LB_NT & 1) != 0>(
+      base, wave_uniform(row_elems * static_cast<int64_t>(sizeof(IO))), lane_bytes);
+}
+template <typename IO, int V>
+__device__ __forceinline__ void lb_store(void* base, int64_t row_elems, uint32_t lane_bytes,
+                                         typename Raw<IO, V>::T v) {
+  stn<typename Raw<IO, V>::T, (SPARC_LB_NT & 2) != 0>(
+      base, wave_uniform(row_elems * static_cast<int64_t>(sizeof(IO))), lane_bytes, v);
+}
+
 template <typename T> struct IsBf16 : std::false_type {};
 template <> struct IsBf16<bf16> : std::true_type {};
 
@@ -262,6 +332,8 @@ scan_fwd_kernel(ScanArgs p) {
   const int mb = chain - b * p.n_mblocks;
   const int m0 = mb * MB + lane * V;
   const bool lane_ok = m0 < p.M;
+  const int mb0 = mb * MB;                                           // the block's first mode
+  const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * sizeof(IO));
   const int t0 = chunk * C + wave * S;
   const bool relu_out = CPLX && (p.flags & SPARC_FLAG_RELU_OUTPUT);
   const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
@@ -276,10 +348,10 @@ scan_fwd_kernel(ScanArgs p) {
   for (int s = 0; s < S; ++s) {
     const int t = t0 + s;
     const bool ok = lane_ok && t < p.T;
-    const int64_t idx = (static_cast<int64_t>(b) * p.T + t) * p.M + m0;
+    const int64_t idx = (static_cast<int64_t>(b) * p.T + t) * p.M + mb0;  // row of the block
     if (ok) {
-      wr_raw[s] = load_raw<IO, V>(p.w_re, idx);
-      if constexpr (CPLX) wi_raw[s] = load_raw<IO, V>(p.w_im, idx);
+      wr_raw[s] = lb_load<IO, V>(p.w_re, idx, lane_bytes);
+      if constexpr (CPLX) wi_raw[s] = lb_load<IO, V>(p.w_im, idx, lane_bytes);
       tl.load_gates(p, tl.gate_index(p, b, t, m0), g0[s], g1[s]);
     } else {
       float z[V] = {};
@@ -519,11 +591,11 @@ scan_fwd_kernel(ScanArgs p) {
         float rr[V], ri[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
-        store_raw<IO, V>(p.y_re, row * 2 * p.M + m0, pack<IO, V>(rr));
-        store_raw<IO, V>(p.y_re, row * 2 * p.M + p.M + m0, pack<IO, V>(ri));
+        lb_store<IO, V>(p.y_re, row * 2 * p.M + mb0, lane_bytes, pack<IO, V>(rr));
+        lb_store<IO, V>(p.y_re, row * 2 * p.M + p.M + mb0, lane_bytes, pack<IO, V>(ri));
       } else {
-        store_raw<IO, V>(p.y_re, row * p.M + m0, pack<IO, V>(hr));
-        if constexpr (CPLX) store_raw<IO, V>(p.y_im, row * p.M + m0, pack<IO, V>(hi));
+        lb_store<IO, V>(p.y_re, row * p.M + mb0, lane_bytes, pack<IO, V>(hr));
+        if constexpr (CPLX) lb_store<IO, V>(p.y_im, row * p.M + mb0, lane_bytes, pack<IO, V>(hi));
       }
     }
   }
@@ -532,8 +604,23 @@ scan_fwd_kernel(ScanArgs p) {
 // ---------------------------------------------------------------------------
 // Backward kernel
 // ---------------------------------------------------------------------------
-template <int TR, typename IO, int V, int GM, int S, int NW>
-__global__ void __launch_bounds__(NW * 64)
+// SAVED: the states h_{t-1} come from the forward's saved output y (no relu
+// epilogue) instead of being recomputed from w and the chunk states, so the
+// tile skips the forward maps, their composition and the state replay.
+// SAVED backward: load the states after the look-back (1) or with dy (0)
+#ifndef SPARC_LB_SAVED_LATE
+#define SPARC_LB_SAVED_LATE 1
+#endif
+// Waves per SIMD the SAVED backward of real scans is compiled for: 4 (two
+// workgroups per CU) spills 8-21 registers but, at B=4, T=65536, M=4096
+// (fp32), runs in 2.42 ms against 2.87 ms at the unconstrained 172 registers
+// (one workgroup per CU).  Complex transitions would spill 40-150 registers
+// under the same bound and keep the compiler's choice.
+#ifndef SPARC_LB_BWD_WAVES
+#define SPARC_LB_BWD_WAVES 4
+#endif
+template <int TR, typename IO, int V, int GM, int S, int NW, bool SAVED>
+__global__ void __launch_bounds__(NW * 64, (SAVED && TR == TR_REAL) ? SPARC_LB_BWD_WAVES : 1)
 scan_bwd_kernel(ScanArgs p) {
   using TL = TransitionLane<TR, IO, V, GM>;
   using GT = typename TL::GT;
@@ -563,6 +650,8 @@ scan_bwd_kernel(ScanArgs p) {
   const int mb = chain - b * p.n_mblocks;
   const int m0 = mb * MB + lane * V;
   const bool lane_ok = m0 < p.M;
+  const int mb0 = mb * MB;                                           // the block's first mode
+  const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * sizeof(IO));
   const int t0 = chunk * C + wave * S;
   const bool relu_out = CPLX && (p.flags & SPARC_FLAG_RELU_OUTPUT);
   const bool reset_first = (p.flags & SPARC_FLAG_RESET_FIRST) != 0;
@@ -579,16 +668,24 @@ scan_bwd_kernel(ScanArgs p) {
     const int t = t0 + s;
     const bool ok = lane_ok && t < p.T;
     const int64_t row = static_cast<int64_t>(b) * p.T + t;
-    const int64_t idx = row * p.M + m0;
+    const int64_t idx = row * p.M + mb0;  // row of the block
     if (ok) {
-      wr_raw[s] = load_raw<IO, V>(p.w_re, idx);
-      if constexpr (CPLX) wi_raw[s] = load_raw<IO, V>(p.w_im, idx);
-      if (relu_out) {
-        dr_raw[s] = load_raw<IO, V>(p.dy_re, row * 2 * p.M + m0);
-        di_raw[s] = load_raw<IO, V>(p.dy_re, row * 2 * p.M + p.M + m0);
+      if constexpr (SAVED) {
+        if constexpr (!SPARC_LB_SAVED_LATE) {  // y at t-1 (t = 0: own row, replaced by h0)
+          const int64_t pidx = t > 0 ? idx - p.M : idx;
+          wr_raw[s] = lb_load<IO, V>(p.y_re, pidx, lane_bytes);
+          if constexpr (CPLX) wi_raw[s] = lb_load<IO, V>(p.y_im, pidx, lane_bytes);
+        }
       } else {
-        dr_raw[s] = load_raw<IO, V>(p.dy_re, idx);
-        if constexpr (CPLX) di_raw[s] = load_raw<IO, V>(p.dy_im, idx);
+        wr_raw[s] = lb_load<IO, V>(p.w_re, idx, lane_bytes);
+        if constexpr (CPLX) wi_raw[s] = lb_load<IO, V>(p.w_im, idx, lane_bytes);
+      }
+      if (relu_out) {
+        dr_raw[s] = lb_load<IO, V>(p.dy_re, row * 2 * p.M + mb0, lane_bytes);
+        di_raw[s] = lb_load<IO, V>(p.dy_re, row * 2 * p.M + p.M + mb0, lane_bytes);
+      } else {
+        dr_raw[s] = lb_load<IO, V>(p.dy_re, idx, lane_bytes);
+        if constexpr (CPLX) di_raw[s] = lb_load<IO, V>(p.dy_im, idx, lane_bytes);
       }
       tl.load_gates(p, tl.gate_index(p, b, t, m0), g0[s], g1[s]);
     } else {
@@ -617,7 +714,7 @@ scan_bwd_kernel(ScanArgs p) {
   }
 
   // ---- forward sub-chunk maps (identical arithmetic to the forward kernel) --
-  {
+  if constexpr (!SAVED) {
     float Pr[AV], Pi[AV], Qr[V], Qi[V];
 #pragma unroll
     for (int v = 0; v < AV; ++v) { Pr[v] = 1.0f; Pi[v] = 0.0f; }
@@ -664,9 +761,9 @@ scan_bwd_kernel(ScanArgs p) {
         s_pq[wave][1][v][lane] = Qr[v];
       }
     }
+    __syncthreads();
   }
-  __syncthreads();
-  if (wave == 0) {
+  if (!SAVED && wave == 0) {
     float cr[V], ci[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
@@ -699,12 +796,24 @@ scan_bwd_kernel(ScanArgs p) {
       }
     }
   }
-  __syncthreads();
+  if constexpr (!SAVED) __syncthreads();
 
   // ---- recompute the states h_{t-1} of the sub-chunk; masked dy -------------
   float hpr[S][V], hpi[S][V];   // state before step s
   float dyr[S][V], dyi[S][V];   // effective output gradient at step s
-  {
+  if constexpr (SAVED) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      float gr[V], gi[V];
+      unpack<IO, V>(dr_raw[s], gr);
+      if constexpr (CPLX) unpack<IO, V>(di_raw[s], gi);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        dyr[s][v] = gr[v];
+        dyi[s][v] = CPLX ? gi[v] : 0.0f;
+      }
+    }
+  } else {
     float hr[V], hi[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
@@ -744,10 +853,26 @@ scan_bwd_kernel(ScanArgs p) {
   // ---- reverse sub-chunk maps: xi_out = conj(P) xi_in + Q ------------------
   {
     float Xr[V], Xi[V];
+    float Pr[AV], Pi[AV];  // SAVED: the sub-chunk's transition product, formed here
 #pragma unroll
     for (int v = 0; v < V; ++v) { Xr[v] = 0.0f; Xi[v] = 0.0f; }
 #pragma unroll
+    for (int v = 0; v < AV; ++v) { Pr[v] = 1.0f; Pi[v] = 0.0f; }
+#pragma unroll
     for (int s = S - 1; s >= 0; --s) {
+      if constexpr (SAVED) {
+#pragma unroll
+        for (int v = 0; v < AV; ++v) {
+          if constexpr (CPLX) {
+            float nr, ni;
+            cmul(a_r[s][v], a_i[s][v], Pr[v], Pi[v], nr, ni);
+            Pr[v] = nr;
+            Pi[v] = ni;
+          } else {
+            Pr[v] = a_r[s][v] * Pr[v];
+          }
+        }
+      }
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         const int av = AV == 1 ? 0 : v;
@@ -761,18 +886,27 @@ scan_bwd_kernel(ScanArgs p) {
         }
       }
     }
-    __syncthreads();  // s_pq of the forward maps is no longer read
+    if constexpr (!SAVED) __syncthreads();  // s_pq of the forward maps is no longer read
 #pragma unroll
     for (int v = 0; v < V; ++v) {
+      const int av = AV == 1 ? 0 : v;
       if constexpr (CPLX) {
         // the product of conj(a) over the sub-chunk is conj of the forward product
-        s_pq[wave][1][v][lane] = -s_pq[wave][1][v][lane];
+        if constexpr (SAVED) {
+          s_pq[wave][0][v][lane] = Pr[av];
+          s_pq[wave][1][v][lane] = -Pi[av];
+        } else {
+          s_pq[wave][1][v][lane] = -s_pq[wave][1][v][lane];
+        }
         s_pq[wave][2][v][lane] = Xr[v];
         s_pq[wave][3][v][lane] = Xi[v];
       } else {
+        if constexpr (SAVED) s_pq[wave][0][v][lane] = Pr[av];
         s_pq[wave][1][v][lane] = Xr[v];
       }
     }
+    (void)Pr;
+    (void)Pi;
   }
   __syncthreads();
 
@@ -917,6 +1051,36 @@ scan_bwd_kernel(ScanArgs p) {
   __syncthreads();
 
   // ---- final reverse pass: dw, transition gradients ------------------------
+  if constexpr (SAVED) {  // the states before each step: y at t-1, h0 (or 0) at t = 0
+#pragma unroll
+    for (int s = 0; s < S && SPARC_LB_SAVED_LATE; ++s) {
+      const int t = t0 + s;
+      if (lane_ok && t < p.T) {
+        // t = 0 re-reads its own row; the value is replaced by h0 below
+        const int64_t pidx = (static_cast<int64_t>(b) * p.T + (t > 0 ? t - 1 : t)) * p.M + mb0;
+        wr_raw[s] = lb_load<IO, V>(p.y_re, pidx, lane_bytes);
+        if constexpr (CPLX) wi_raw[s] = lb_load<IO, V>(p.y_im, pidx, lane_bytes);
+      } else {
+        float z[V] = {};
+        wr_raw[s] = pack<IO, V>(z);
+        wi_raw[s] = wr_raw[s];
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      unpack<IO, V>(wr_raw[s], hpr[s]);
+      if constexpr (CPLX) unpack<IO, V>(wi_raw[s], hpi[s]);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if constexpr (!CPLX) hpi[s][v] = 0.0f;
+        if (t0 + s == 0) {
+          const int64_t hi = static_cast<int64_t>(b) * p.M + m0 + v;
+          hpr[s][v] = (p.h0_re && lane_ok) ? p.h0_re[hi] : 0.0f;
+          if constexpr (CPLX) hpi[s][v] = (p.h0_im && lane_ok) ? p.h0_im[hi] : 0.0f;
+        }
+      }
+    }
+  }
   float Xr[V], Xi[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
@@ -942,8 +1106,8 @@ scan_bwd_kernel(ScanArgs p) {
       li[v] = dyi[s][v] + Xi[v];
     }
     if (lane_ok && t_ok) {
-      store_raw<IO, V>(p.dw_re, row * p.M + m0, pack<IO, V>(lr));
-      if constexpr (CPLX) store_raw<IO, V>(p.dw_im, row * p.M + m0, pack<IO, V>(li));
+      lb_store<IO, V>(p.dw_re, row * p.M + mb0, lane_bytes, pack<IO, V>(lr));
+      if constexpr (CPLX) lb_store<IO, V>(p.dw_im, row * p.M + mb0, lane_bytes, pack<IO, V>(li));
     }
     // gradient of the transition: dL/da = lambda * conj(h_{t-1})
     float d0[GV], d1[GV];   // per-gate gradient contributions (summed over the lane's modes when GV == 1)
@@ -1627,53 +1791,6 @@ __device__ __forceinline__ float group_sum(float x, int lpg) {
   if (lpg >= 32) x += __shfl_xor(x, 16, 64);
   if (lpg >= 64) x += __shfl_xor(x, 32, 64);
   return x;
-}
-
-// A 64-bit value every lane of the wave holds, moved to scalar registers, so
-// that a memory instruction can take (kernel-argument pointer + this offset)
-// as its scalar base and the lane's byte offset as its vector offset.
-__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
-  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-template <typename T>
-__device__ __forceinline__ T ldb(const void* base, int64_t byte_off, uint32_t lane_bytes) {
-  return *reinterpret_cast<const T*>(static_cast<const char*>(base) + byte_off + lane_bytes);
-}
-template <typename T>
-__device__ __forceinline__ void stb(void* base, int64_t byte_off, uint32_t lane_bytes, T v) {
-  *reinterpret_cast<T*>(static_cast<char*>(base) + byte_off + lane_bytes) = v;
-}
-// Non-temporal forms of ldb / stb for the streamed planes of the serial
-// kernels, each element of which is read or written once per launch: the nt
-// cache policy keeps them from displacing lines that are reused.
-// Cache policy of the serial kernels' plane loads and stores: bit 0 loads,
-// bit 1 stores non-temporal (forward and backward separately).
-#ifndef SPARC_FWD_NT
-#define SPARC_FWD_NT 3
-#endif
-#ifndef SPARC_BWD_NT
-#define SPARC_BWD_NT 3
-#endif
-template <typename T, bool NT = true>
-__device__ __forceinline__ T ldn(const void* base, int64_t byte_off, uint32_t lane_bytes) {
-  if constexpr (!NT) return ldb<T>(base, byte_off, lane_bytes);
-  using N = typename NtBits<sizeof(T)>::T;
-  const N n = __builtin_nontemporal_load(
-      reinterpret_cast<const N*>(static_cast<const char*>(base) + byte_off + lane_bytes));
-  T r;
-  __builtin_memcpy(&r, &n, sizeof(T));
-  return r;
-}
-template <typename T, bool NT = true>
-__device__ __forceinline__ void stn(void* base, int64_t byte_off, uint32_t lane_bytes, T v) {
-  if constexpr (!NT) { stb<T>(base, byte_off, lane_bytes, v); return; }
-  using N = typename NtBits<sizeof(T)>::T;
-  N n;
-  __builtin_memcpy(&n, &v, sizeof(T));
-  __builtin_nontemporal_store(n, reinterpret_cast<N*>(static_cast<char*>(base) + byte_off + lane_bytes));
 }
 
 constexpr int fast_rounds(int S) { return (S * kFastMaxGpw + 63) / 64; }
@@ -3260,6 +3377,11 @@ struct Kernels {
   // backward from the saved forward output (no relu epilogue); false when
   // this plan has no such kernel and the caller must fall back to w
   static bool run_saved(const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
+    if (!pl.chain) {  // look-back tiles, any transition and gate layout
+      const dim3 g(static_cast<unsigned>(pl.n_tiles));
+      hipLaunchKernelGGL((sparc::scan_bwd_kernel<TR, IO, V, GM, S, NW, true>), g, dim3(NW * 64), 0, st, a);
+      return true;
+    }
     if constexpr (TR != sparc::TR_P1 && GM == sparc::GATE_LANE) {
       if (pl.serial) {
         const dim3 g(static_cast<unsigned>(pl.n_chains));
@@ -3286,7 +3408,7 @@ struct Kernels {
     }
     const dim3 g(static_cast<unsigned>(pl.n_tiles));
     if (dir == 0) hipLaunchKernelGGL((sparc::scan_fwd_kernel<TR, IO, V, GM, S, NW>), g, dim3(NW * 64), 0, st, a);
-    else hipLaunchKernelGGL((sparc::scan_bwd_kernel<TR, IO, V, GM, S, NW>), g, dim3(NW * 64), 0, st, a);
+    else hipLaunchKernelGGL((sparc::scan_bwd_kernel<TR, IO, V, GM, S, NW, false>), g, dim3(NW * 64), 0, st, a);
   }
 };
 
