@@ -162,6 +162,58 @@ __device__ __forceinline__ void lb_store(void* base, int64_t row_elems, uint32_t
       base, wave_uniform(row_elems * static_cast<int64_t>(sizeof(IO))), lane_bytes, v);
 }
 
+// Look-back publication.  Aggregates and inclusive carries travel between
+// workgroups (possibly on different XCDs) through sc1 stores and loads, the
+// cache policy of agent-scope atomics (written through to, and read from, the
+// device coherence point), here as wide vector accesses through a buffer
+// resource at a wave-uniform base.  No access needs to be atomic: a consumer
+// reads only after the producer's flag, which the producer stores after its
+// data stores have completed.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_rsrc(const float* base, uint32_t bytes) {
+  return make_rsrc(reinterpret_cast<const float*>(wave_uniform(reinterpret_cast<int64_t>(base))), bytes);
+}
+// A tile's aggregate, N floats per lane.  For N a multiple of 4 they are kept
+// as 16-byte pieces at [piece][lane], so that each store and load instruction
+// of the wave covers 1 KiB contiguously; else [lane][N].
+template <int N>
+__device__ __forceinline__ void agg_store(float* tile, int lane, const float (&v)[N]) {
+  const __amdgpu_buffer_rsrc_t r = uniform_rsrc(tile, 64 * N * 4);
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int k = 0; k < N / 4; ++k) {
+      const float t[4] = {v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+      buffer_store_f32<4, CPOL_SC1>(r, static_cast<uint32_t>((k * 64 + lane) * 16), t);
+    }
+  } else {
+    buffer_store_f32<N, CPOL_SC1>(r, static_cast<uint32_t>(lane * N * 4), v);
+  }
+}
+template <int N>
+__device__ __forceinline__ void agg_load(const float* tile, int lane, float (&v)[N]) {
+  const __amdgpu_buffer_rsrc_t r = uniform_rsrc(tile, 64 * N * 4);
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int k = 0; k < N / 4; ++k) {
+      float t[4];
+      buffer_load_f32<4, CPOL_SC1>(r, static_cast<uint32_t>((k * 64 + lane) * 16), t);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[4 * k + i] = t[i];
+    }
+  } else {
+    buffer_load_f32<N, CPOL_SC1>(r, static_cast<uint32_t>(lane * N * 4), v);
+  }
+}
+// A lane's N <= 4 contiguous floats of a [..., M, NH] state plane (chunk
+// states, backward carries); ``block`` is the mode block's first element.
+template <int N>
+__device__ __forceinline__ void state_store(float* block, int lane, const float (&v)[N]) {
+  buffer_store_f32<N, CPOL_SC1>(uniform_rsrc(block, 64 * N * 4), static_cast<uint32_t>(lane * N * 4), v);
+}
+template <int N>
+__device__ __forceinline__ void state_load(const float* block, int lane, float (&v)[N]) {
+  buffer_load_f32<N, CPOL_SC1>(uniform_rsrc(block, 64 * N * 4), static_cast<uint32_t>(lane * N * 4), v);
+}
+
 template <typename T> struct IsBf16 : std::false_type {};
 template <> struct IsBf16<bf16> : std::true_type {};
 
@@ -171,7 +223,9 @@ __device__ __forceinline__ void cmul(float ar, float ai, float br, float bi, flo
   ci = ar * bi + ai * br;
 }
 
-// Loads a lane's V-element fp32 vector with agent-scope (sc1) loads.
+// Per-lane agent-scope (sc1) loads and stores of a lane's N floats, 8 bytes at
+// a time (the backward look-back: its register allocation under the 4-wave
+// bound runs faster with these than with the wide accesses above).
 template <int N>
 __device__ __forceinline__ void load_agent_vec(const float* p, float (&o)[N]) {
   if constexpr (N % 2 == 0) {
@@ -462,7 +516,7 @@ scan_fwd_kernel(ScanArgs p) {
       }
     } else {
       // publish the aggregate of this tile
-      float* my_agg = p.agg + ((static_cast<int64_t>(chain) * p.n_chunks + chunk) * MB + lane * V) * NQ;
+      float* my_agg = p.agg + (static_cast<int64_t>(chain) * p.n_chunks + chunk) * MB * NQ;
       float pv[V * NQ];
 #pragma unroll
       for (int v = 0; v < V; ++v) {
@@ -475,7 +529,7 @@ scan_fwd_kernel(ScanArgs p) {
           pv[v * NQ + 1] = TQr[v];
         }
       }
-      store_agent_vec<V * NQ>(my_agg, pv);
+      agg_store<V * NQ>(my_agg, lane, pv);
       wait_stores_complete();
       if (lane == 0) store_agent(p.flagv + static_cast<int64_t>(chain) * p.n_chunks + chunk, uint32_t(FLAG_AGGREGATE));
       // look back: X = composition of the aggregates of chunks j+1 .. chunk-1
@@ -488,7 +542,7 @@ scan_fwd_kernel(ScanArgs p) {
         if (f == FLAG_INCLUSIVE) {
           float h[V * NH] = {};
           if (lane_ok)
-            load_agent_vec<V * NH>(p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + j) * p.M + m0) * NH, h);
+            state_load<V * NH>(p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + j) * p.M + mb0) * NH, lane, h);
 #pragma unroll
           for (int v = 0; v < V; ++v) {
             if constexpr (CPLX) {
@@ -504,7 +558,7 @@ scan_fwd_kernel(ScanArgs p) {
           break;
         }
         float q[V * NQ];
-        load_agent_vec<V * NQ>(p.agg + ((static_cast<int64_t>(chain) * p.n_chunks + j) * MB + lane * V) * NQ, q);
+        agg_load<V * NQ>(p.agg + (static_cast<int64_t>(chain) * p.n_chunks + j) * MB * NQ, lane, q);
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           if constexpr (CPLX) {
@@ -552,7 +606,7 @@ scan_fwd_kernel(ScanArgs p) {
         if constexpr (CPLX) { h[2 * v] = cr[v]; h[2 * v + 1] = ci[v]; }
         else h[v] = cr[v];
       }
-      store_agent_vec<V * NH>(p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + chunk) * p.M + m0) * NH, h);
+      state_store<V * NH>(p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + chunk) * p.M + mb0) * NH, lane, h);
     }
     wait_stores_complete();
     if (lane == 0) store_agent(p.flagv + static_cast<int64_t>(chain) * p.n_chunks + chunk, uint32_t(FLAG_INCLUSIVE));
@@ -3598,14 +3652,16 @@ static sparc_status empty_backward(const sparc_scan_desc* d, const float* dlast_
                                    hipStream_t st) {
   const int64_t bm = d->batch * d->modes;
   const dim3 gb(static_cast<unsigned>((bm + 255) / 256)), gm(static_cast<unsigned>((d->modes + 255) / 256));
+  hipError_t ce = hipSuccess;
   if (dh0_re) {
-    if (dlast_re) hipMemcpyAsync(dh0_re, dlast_re, bm * 4, hipMemcpyDeviceToDevice, st);
+    if (dlast_re) ce = hipMemcpyAsync(dh0_re, dlast_re, bm * 4, hipMemcpyDeviceToDevice, st);
     else hipLaunchKernelGGL(sparc::clear_u32_kernel, gb, dim3(256), 0, st, reinterpret_cast<uint32_t*>(dh0_re), bm);
   }
-  if (dh0_im) {
-    if (dlast_im) hipMemcpyAsync(dh0_im, dlast_im, bm * 4, hipMemcpyDeviceToDevice, st);
+  if (dh0_im && ce == hipSuccess) {
+    if (dlast_im) ce = hipMemcpyAsync(dh0_im, dlast_im, bm * 4, hipMemcpyDeviceToDevice, st);
     else hipLaunchKernelGGL(sparc::clear_u32_kernel, gb, dim3(256), 0, st, reinterpret_cast<uint32_t*>(dh0_im), bm);
   }
+  if (ce != hipSuccess) return fail(SPARC_EHIP, "empty backward copy: %s", hipGetErrorString(ce));
   if (dnu_log) hipLaunchKernelGGL(sparc::clear_u32_kernel, gm, dim3(256), 0, st, reinterpret_cast<uint32_t*>(dnu_log), d->modes);
   if (dtheta_log) hipLaunchKernelGGL(sparc::clear_u32_kernel, gm, dim3(256), 0, st, reinterpret_cast<uint32_t*>(dtheta_log), d->modes);
   hipError_t e = hipGetLastError();
