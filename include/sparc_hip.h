@@ -301,6 +301,56 @@ sparc_status sparc_column_sum(int64_t rows, int64_t cols, const float* in,
 const char* sparc_last_error(void);
 const char* sparc_version(void);
 
+/* ---------------------------------------------------------------------------
+ * The module's sequence path, fused (SPARCMixer forward and backward): the
+ * P1 controls, the gain*tanh write, the scan and the relu(cat) epilogue
+ * read x directly, with no [B,T,M] write tensors.
+ *
+ * x [B,T,2M] (io_dtype; x[..., :M] feeds the real parts, x[..., M:] the
+ * imaginary ones), directions [2M+1] fp32 (the last entry is the bias),
+ * parameters [M] fp32.  M must be a multiple of 4; x, y, dy, dx and the
+ * directions 16-byte aligned.
+ * ------------------------------------------------------------------------- */
+/* Workspace bytes of sparc_mixer_forward (direction 0) or _backward (1); 0 if
+ * the shape is invalid. */
+size_t sparc_mixer_workspace_bytes(int64_t batch, int64_t length, int64_t modes, int direction);
+
+/* eta, delta [B*T] fp32: the controls eta = log16 tanh(x.u_r + b_r), delta =
+ * (pi/2) tanh(x.u_p + b_p).  y [B,T,2M] = relu(cat(h_re, h_im)) and h_re,
+ * h_im [B,T,M] (the states, kept for the backward) in io_dtype.  last_re,
+ * last_im [B,M] fp32: the state after step T-1 (both NULL: not written).
+ * Replaces run_sequence's P1 path: make_controls and make_scan_inputs
+ * (sparc-kernal/forward/control.py:129-195), _SPARCChunkScan.forward
+ * (sparc-kernal/backward/scan.py:1126-1372) and the output epilogue
+ * (sparc-kernal/forward/scan.py:1598-1603). */
+sparc_status sparc_mixer_forward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                                 const void* x, const float* phase_direction, const float* radial_direction,
+                                 const float* nu_log, const float* theta_log, const float* write_log_gain,
+                                 const float* write_phase_response, const float* write_radial_response,
+                                 float* eta, float* delta, void* y, void* h_re, void* h_im,
+                                 float* last_re, float* last_im, void* workspace, size_t workspace_bytes,
+                                 sparc_stream_t stream);
+
+/* dy [B,T,2M] (io_dtype): the gradient of y; dlast_re, dlast_im [B,M] fp32:
+ * of the last state (both NULL: zero).  eta, delta, h_re, h_im as the
+ * forward wrote them.  Writes dx [B,T,2M] (io_dtype) and, overwriting, the
+ * direction gradients [2M+1] and the parameter gradients [M] (fp32).
+ * Deterministic (fixed-order reductions, no atomics).
+ * Replaces _SPARCChunkScan.backward (sparc-kernal/backward/scan.py:1375-1640),
+ * _LatestSPARCWrite.backward (sparc-kernal/backward/control.py:92-129, kernel
+ * :10-89) and the autograd of make_controls' F.linear
+ * (sparc-kernal/forward/control.py:129-139). */
+sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                                  const void* x, const float* phase_direction, const float* radial_direction,
+                                  const float* nu_log, const float* theta_log, const float* write_log_gain,
+                                  const float* write_phase_response, const float* write_radial_response,
+                                  const float* eta, const float* delta, const void* h_re, const void* h_im,
+                                  const void* dy, const float* dlast_re, const float* dlast_im, void* dx,
+                                  float* dphase_direction, float* dradial_direction, float* dnu_log,
+                                  float* dtheta_log, float* dwrite_log_gain, float* dwrite_phase_response,
+                                  float* dwrite_radial_response, void* workspace, size_t workspace_bytes,
+                                  sparc_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

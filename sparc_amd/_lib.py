@@ -41,6 +41,9 @@ EXPORTED_SYMBOLS = (
     "sparc_decode_step_prepared",
     "sparc_scan_step",
     "sparc_column_sum",
+    "sparc_mixer_workspace_bytes",
+    "sparc_mixer_forward",
+    "sparc_mixer_backward",
     "sparc_last_error",
     "sparc_version",
 )
@@ -110,6 +113,12 @@ def load() -> ctypes.CDLL:
         lib.sparc_scan_step.restype = ctypes.c_int
         lib.sparc_column_sum.argtypes = [_I64, _I64, _P, _P, ctypes.c_int, _P]
         lib.sparc_column_sum.restype = ctypes.c_int
+        lib.sparc_mixer_workspace_bytes.argtypes = [_I64, _I64, _I64, ctypes.c_int]
+        lib.sparc_mixer_workspace_bytes.restype = _SZ
+        lib.sparc_mixer_forward.argtypes = [_I64, _I64, _I64, _I32] + [_P] * 16 + [_SZ, _P]
+        lib.sparc_mixer_forward.restype = ctypes.c_int
+        lib.sparc_mixer_backward.argtypes = [_I64, _I64, _I64, _I32] + [_P] * 24 + [_SZ, _P]
+        lib.sparc_mixer_backward.restype = ctypes.c_int
         lib.sparc_last_error.argtypes = []
         lib.sparc_last_error.restype = ctypes.c_char_p
         lib.sparc_version.argtypes = []

@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_NAME = "libsparc_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["scan.hip", "pointwise.hip"]
+SOURCES = ["scan.hip", "pointwise.hip", "mixer.hip"]
 ARCH = os.environ.get("SPARC_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

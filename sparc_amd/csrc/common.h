@@ -119,6 +119,48 @@ __device__ __forceinline__ void buffer_store_f32(__amdgpu_buffer_rsrc_t r, uint3
   }
 }
 
+// s_waitcnt vmcnt(0): every vector memory operation of the wave has completed.
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// A 64-bit value every lane of the wave holds, moved to scalar registers, so
+// that a memory instruction can take (kernel-argument pointer + this offset)
+// as its scalar base and the lane's byte offset as its vector offset.
+__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+template <typename T>
+__device__ __forceinline__ T ldb(const void* base, int64_t byte_off, uint32_t lane_bytes) {
+  return *reinterpret_cast<const T*>(static_cast<const char*>(base) + byte_off + lane_bytes);
+}
+template <typename T>
+__device__ __forceinline__ void stb(void* base, int64_t byte_off, uint32_t lane_bytes, T v) {
+  *reinterpret_cast<T*>(static_cast<char*>(base) + byte_off + lane_bytes) = v;
+}
+// Non-temporal forms of ldb / stb for streamed planes, each element of which is
+// read or written once per launch: the nt cache policy keeps them from
+// displacing lines that are reused.
+template <typename T, bool NT = true>
+__device__ __forceinline__ T ldn(const void* base, int64_t byte_off, uint32_t lane_bytes) {
+  if constexpr (!NT) return ldb<T>(base, byte_off, lane_bytes);
+  using N = typename NtBits<sizeof(T)>::T;
+  const N n = __builtin_nontemporal_load(
+      reinterpret_cast<const N*>(static_cast<const char*>(base) + byte_off + lane_bytes));
+  T r;
+  __builtin_memcpy(&r, &n, sizeof(T));
+  return r;
+}
+template <typename T, bool NT = true>
+__device__ __forceinline__ void stn(void* base, int64_t byte_off, uint32_t lane_bytes, T v) {
+  if constexpr (!NT) { stb<T>(base, byte_off, lane_bytes, v); return; }
+  using N = typename NtBits<sizeof(T)>::T;
+  N n;
+  __builtin_memcpy(&n, &v, sizeof(T));
+  __builtin_nontemporal_store(n, reinterpret_cast<N*>(static_cast<char*>(base) + byte_off + lane_bytes));
+}
+
 template <typename IO, int V>
 __device__ __forceinline__ void unpack(const typename Raw<IO, V>::T& r, float (&o)[V]) {
   if constexpr (sizeof(IO) == 4) {
@@ -208,6 +250,44 @@ __device__ __forceinline__ void sincos_quarter(float x, float& s, float& c) {
   pc = fmaf(pc, x2, 4.1666666666666664e-2f);  // 1/4!
   pc = fmaf(pc, x2, -0.5f);
   c = fmaf(pc, x2, 1.0f);
+}
+
+// expm1(x) for x <= 0 to ~1e-7 relative: Taylor series (8 terms) near 0,
+// exp(x) - 1 further out (no cancellation there)
+__device__ __forceinline__ float expm1_nonpos(float x) {
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, x, 1.0f / 720.0f);
+  p = fmaf(p, x, 1.0f / 120.0f);
+  p = fmaf(p, x, 1.0f / 24.0f);
+  p = fmaf(p, x, 1.0f / 6.0f);
+  p = fmaf(p, x, 0.5f);
+  p = fmaf(p, x, 1.0f);
+  p *= x;
+  return x > -0.25f ? p : fast_exp(x) - 1.0f;
+}
+
+// sin and cos of |u| <= pi/2 by Taylor series to x^11 / x^12 (error < 6e-8)
+__device__ __forceinline__ void sincos_half(float u, float& s, float& c) {
+  const float u2 = u * u;
+  float ps = -1.0f / 39916800.0f;
+  ps = fmaf(ps, u2, 1.0f / 362880.0f);
+  ps = fmaf(ps, u2, -1.0f / 5040.0f);
+  ps = fmaf(ps, u2, 1.0f / 120.0f);
+  ps = fmaf(ps, u2, -1.0f / 6.0f);
+  s = fmaf(ps * u2, u, u);
+  float pc = 1.0f / 479001600.0f;
+  pc = fmaf(pc, u2, -1.0f / 3628800.0f);
+  pc = fmaf(pc, u2, 1.0f / 40320.0f);
+  pc = fmaf(pc, u2, -1.0f / 720.0f);
+  pc = fmaf(pc, u2, 1.0f / 24.0f);
+  pc = fmaf(pc, u2, -0.5f);
+  c = fmaf(pc, u2, 1.0f);
+}
+
+// tanh through one hardware exponential and reciprocal (absolute error ~1e-7)
+__device__ __forceinline__ float tanh_fast(float x) {
+  const float e = fast_exp(-2.0f * fabsf(x));
+  return copysignf((1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e), x);
 }
 
 // sin and cos for moderate |x| (gate phases, a few multiples of pi):

@@ -1,0 +1,924 @@
+// SPARC mixer sequence path for gfx950: the drop-in module's forward and
+// backward with the P1 controls, the gain*tanh write, the scan and the
+// relu(cat) epilogue fused, reading x directly.
+//
+// Forward (sparc_mixer_forward):
+//   1. mixer_prepare_kernel: per-mode constants (nu, e^{i theta}, gain, ...).
+//   2. ctrl_fwd_kernel: eta, delta per token (two dot products over the 2M
+//      inputs, tanh).
+//   3. mixer_fwd_kernel: one wave per chain (batch row, block of 64*V modes)
+//      walks T in order: per step and mode the P1 transition, the write
+//      gain*tanh(x) and h <- a h + w in fp32, stores y = relu(cat(h_re, h_im))
+//      and the state h in the I/O dtype (saved for the backward, as the
+//      reference saves out_r / out_i).
+// Backward (sparc_mixer_backward):
+//   4. mixer_bwd_kernel: one chain per workgroup in reverse time.  Wave 0
+//      runs the adjoint lambda_t = mask_t dy_t + conj(a_{t+1}) lambda_{t+1},
+//      writes the write path's dx, and accumulates per-mode parameter
+//      gradients in registers; its per-(step, lane) contributions to
+//      d eta_t and d delta_t go through LDS to wave 1, which sums them over
+//      the lanes and stores one partial per (token, mode block).
+//   5. deterministic reductions: per token over mode blocks, per mode over
+//      batch rows.
+//   6. ctrl_bwd_kernel: dx += d p0_t * u_phase + d p1_t * u_radial (the
+//      controls' input gradient) in place, and the direction gradients as
+//      partial sums over row blocks.
+//
+// Reference replaced: make_controls / make_scan_inputs / _latest_write_forward
+// (sparc-kernal/forward/control.py:129-195), _SPARCChunkScan forward and
+// backward (sparc-kernal/backward/scan.py:1126-1640), the output epilogue
+// (sparc-kernal/forward/scan.py:1598-1603), _latest_write_backward and
+// _LatestSPARCWrite (sparc-kernal/backward/control.py:10-137).
+
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <type_traits>
+
+#include "common.h"
+#include "sparc_hip.h"
+
+namespace sparc {
+namespace mix {
+
+constexpr float kLog16 = 2.772588722239781f;
+constexpr float kInvLog16 = 0.36067376022224085f;
+constexpr float kHalfPi = 1.5707963267948966f;
+constexpr float kTwoOverPi = 0.6366197723675814f;
+constexpr int kConsts = 8;     // floats per mode in the constants table
+constexpr int kS = 8;          // steps per prefetched block of the forward scan
+constexpr int kCtrlRows = 16;  // rows per workgroup of the controls forward
+constexpr int kCtrlBwdRows = 128;  // rows per workgroup of the controls backward
+
+struct Args {
+  int B, T, M, n_mb;
+  const void* x;
+  const float* consts;
+  const float* eta;
+  const float* delta;
+  void* y;
+  void* h_re;
+  void* h_im;
+  float* last_re;
+  float* last_im;
+  // backward
+  const void* dy;
+  const float* dlast_re;
+  const float* dlast_im;
+  void* dx;
+  float* part_tok;   // [2][n_mb][B*T]: d eta, d delta partials per mode block
+  float* part_mode;  // [5][B][M]: nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response
+};
+
+// consts[m] = (nu, cos theta, sin theta, gamma = e^{wlg}, cinv = 1/expm1(-2 nu), wpr, wrr, theta)
+__global__ void __launch_bounds__(256)
+mixer_prepare_kernel(int M, const float* nu_log, const float* theta_log, const float* wlg,
+                     const float* wpr, const float* wrr, float* consts) {
+  const int m = blockIdx.x * 256 + threadIdx.x;
+  if (m >= M) return;
+  const float nu = expf(nu_log[m]);
+  const float theta = expf(theta_log[m]);
+  float sn, cs;
+  sincosf(theta, &sn, &cs);
+  float4* c = reinterpret_cast<float4*>(consts + static_cast<int64_t>(m) * kConsts);
+  c[0] = make_float4(nu, cs, sn, expf(wlg[m]));
+  c[1] = make_float4(1.0f / expm1f(-2.0f * nu), wpr[m], wrr[m], theta);
+}
+
+// ---------------------------------------------------------------------------
+// wave reductions
+// ---------------------------------------------------------------------------
+// N values per lane -> the wave sums of all N: a reduce-scatter butterfly
+// (each xor step keeps half of the values and adds the partner's copy of
+// them), then plain xor steps.  On return lane l holds the sum of value
+// (l / (64 / N)) in v[0].
+template <int N>
+__device__ __forceinline__ void wave_reduce_scatter(float (&v)[N], int lane) {
+  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "power of two");
+  int n = N;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    if (n > 1) {
+      const bool lo = (lane & o) == 0;
+#pragma unroll
+      for (int i = 0; i < N / 2; ++i) {
+        if (i < n / 2) {
+          const float send = lo ? v[i + n / 2] : v[i];
+          const float recv = __shfl_xor(send, o, 64);
+          v[i] = (lo ? v[i] : v[i + n / 2]) + recv;
+        }
+      }
+      n >>= 1;
+    } else {
+      v[0] += __shfl_xor(v[0], o, 64);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// controls forward: eta = log16 tanh(x.u_r + b_r), delta = pi/2 tanh(x.u_p + b_p)
+// ---------------------------------------------------------------------------
+// A workgroup takes kCtrlRows rows; each thread 8 consecutive inputs per pass,
+// the direction values it loads serving every row of the workgroup.
+template <typename IO>
+__global__ void __launch_bounds__(256)
+ctrl_fwd_kernel(int64_t R, int W, const void* x, const float* pdir, const float* rdir,
+                float* eta, float* delta) {
+  __shared__ float red[4][2 * kCtrlRows];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kCtrlRows;
+  float acc[2 * kCtrlRows];
+#pragma unroll
+  for (int i = 0; i < 2 * kCtrlRows; ++i) acc[i] = 0.0f;
+  for (int c = threadIdx.x * 8; c < W; c += 256 * 8) {
+    float u0[8], u1[8];
+    *reinterpret_cast<float4*>(u0) = *reinterpret_cast<const float4*>(pdir + c);
+    *reinterpret_cast<float4*>(u0 + 4) = *reinterpret_cast<const float4*>(pdir + c + 4);
+    *reinterpret_cast<float4*>(u1) = *reinterpret_cast<const float4*>(rdir + c);
+    *reinterpret_cast<float4*>(u1 + 4) = *reinterpret_cast<const float4*>(rdir + c + 4);
+#pragma unroll
+    for (int r = 0; r < kCtrlRows; ++r) {
+      const int64_t row = r0 + r < R ? r0 + r : R - 1;  // rows past R repeat the last, unused
+      float xv[8];
+      if constexpr (sizeof(IO) == 2) {
+        unpack<bf16, 8>(load_raw_nt<bf16, 8>(x, row * W + c), xv);
+      } else {
+        float a[4], b[4];
+        unpack<float, 4>(load_raw_nt<float, 4>(x, row * W + c), a);
+        unpack<float, 4>(load_raw_nt<float, 4>(x, row * W + c + 4), b);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { xv[i] = a[i]; xv[4 + i] = b[i]; }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        acc[2 * r] = fmaf(xv[i], u0[i], acc[2 * r]);
+        acc[2 * r + 1] = fmaf(xv[i], u1[i], acc[2 * r + 1]);
+      }
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  wave_reduce_scatter<2 * kCtrlRows>(acc, lane);
+  constexpr int per = 64 / (2 * kCtrlRows);  // lanes holding one value
+  if (lane % per == 0) red[wave][lane / per] = acc[0];
+  __syncthreads();
+  if (threadIdx.x < kCtrlRows) {
+    const int r = threadIdx.x;
+    if (r0 + r < R) {
+      float p0 = pdir[W], p1 = rdir[W];  // the bias entries
+#pragma unroll
+      for (int w = 0; w < 4; ++w) { p0 += red[w][2 * r]; p1 += red[w][2 * r + 1]; }
+      eta[r0 + r] = kLog16 * tanhf(p1);
+      delta[r0 + r] = kHalfPi * tanhf(p0);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// per-mode constants of a lane's V modes
+// ---------------------------------------------------------------------------
+template <int V>
+struct ModeConsts {
+  float nu[V], ct[V], st[V], gam[V], cinv[V], wpr[V], wrr[V], th[V];
+  __device__ __forceinline__ void load(const float* consts, int m0, bool ok) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int m = ok ? m0 + v : 0;
+      const float4 c0 = *reinterpret_cast<const float4*>(consts + static_cast<int64_t>(m) * kConsts);
+      const float4 c1 = *reinterpret_cast<const float4*>(consts + static_cast<int64_t>(m) * kConsts + 4);
+      nu[v] = c0.x; ct[v] = c0.y; st[v] = c0.z; gam[v] = c0.w;
+      cinv[v] = c1.x; wpr[v] = c1.y; wrr[v] = c1.z; th[v] = c1.w;
+    }
+  }
+};
+
+// Per-step values of the P1 transition and write of one mode.
+struct StepMode {
+  float em, rho, ar, ai, gain, sg;
+};
+__device__ __forceinline__ StepMode p1_step(float nu, float ct, float st, float gam, float cinv, float wpr,
+                                             float wrr, float E, float delta, float ps, float rs) {
+  StepMode o;
+  o.em = expm1_nonpos(-nu * E);  // rho - 1
+  o.rho = 1.0f + o.em;
+  float su, cu;
+  sincos_half(-o.em * delta, su, cu);  // phase (1 - rho) delta, |.| <= pi/2
+  o.ar = o.rho * fmaf(ct, cu, -st * su);
+  o.ai = o.rho * fmaf(st, cu, ct * su);
+  // expm1(-2 nu E) = em (2 + em); ratio = sqrt(expm1(-2 nu E) / expm1(-2 nu))
+  const float ratio = __builtin_amdgcn_sqrtf(o.em * (2.0f + o.em) * cinv);
+  const float q = fmaf(ps, wpr, rs * wrr);
+  o.sg = __builtin_amdgcn_rcpf(1.0f + fast_exp(-q));  // sigmoid(q)
+  o.gain = gam * ratio * 2.0f * o.sg;
+  return o;
+}
+
+// ---------------------------------------------------------------------------
+// forward scan: one wave per chain
+// ---------------------------------------------------------------------------
+// Plane loads are unconditional with clamped addresses (steps past T re-read
+// row T-1; lanes past M read their block's first element) and the next
+// block is always prefetched (the last block re-reads itself), so that the
+// wait before a block never covers the prefetch of the next one.
+template <typename IO, int V>
+__global__ void __launch_bounds__(64, 1)
+mixer_fwd_kernel(Args a) {
+  using RawT = typename Raw<IO, V>::T;
+  constexpr int ESZ = sizeof(IO);
+  constexpr int MB = 64 * V;
+  const int lane = threadIdx.x;
+  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int b = chain / a.n_mb;
+  const int mb = chain - b * a.n_mb;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < a.M;
+  const int n_blocks = (a.T + kS - 1) / kS;
+  ModeConsts<V> mc;
+  mc.load(a.consts, m0, lane_ok);
+  const int64_t row0 = static_cast<int64_t>(b) * a.T;
+  const int64_t mbase = static_cast<int64_t>(mb) * MB;
+  const int64_t W = 2 * static_cast<int64_t>(a.M);
+  const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
+  const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
+  // the constants are loop-carried: complete their loads before the loop (else
+  // the waits inside it would also cover the prefetch)
+  wait_vm_all();
+
+  RawT xr[2][kS], xi[2][kS];
+  float ev[2], dv[2];  // lane s < kS: eta, delta of step s of the block
+  auto load_block = [&](auto h_tag, int k) {
+    constexpr int h = decltype(h_tag)::value;
+    const int t0 = k * kS;
+    const int last = a.T - 1 - t0;
+    const int64_t off = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      const int64_t o = off + static_cast<int64_t>(s <= last ? s : last) * W * ESZ;
+      xr[h][s] = ldn<RawT>(a.x, o, lane_ld);
+      xi[h][s] = ldn<RawT>(a.x, o + static_cast<int64_t>(a.M) * ESZ, lane_ld);
+    }
+    const int sl = lane & (kS - 1);
+    const int64_t ti = row0 + t0 + (sl <= last ? sl : last);
+    ev[h] = a.eta[ti];
+    dv[h] = a.delta[ti];
+  };
+
+  float hr[V], hi[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) { hr[v] = 0.0f; hi[v] = 0.0f; }
+  // One block of kS steps in two phases: (A) every step's transition and
+  // write, independent of the state, as one straight-line region the
+  // compiler can interleave; (B) the recurrence and the stores.  TAIL: the
+  // last block, with steps past T (no update, no store).
+  auto run_block = [&](auto h_tag, int t0, auto tail_tag) {
+    constexpr int h = decltype(h_tag)::value;
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    float ar[kS][V], ai[kS][V], wr[kS][V], wi[kS][V];
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
+      const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), s));
+      const float E = fast_exp(eta);
+      const float ps = delta * kTwoOverPi, rs = eta * kInvLog16;
+      float cr[V], ci[V];
+      unpack<IO, V>(xr[h][s], cr);
+      unpack<IO, V>(xi[h][s], ci);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const StepMode q = p1_step(mc.nu[v], mc.ct[v], mc.st[v], mc.gam[v], mc.cinv[v], mc.wpr[v], mc.wrr[v],
+                                   E, delta, ps, rs);
+        ar[s][v] = q.ar;
+        ai[s][v] = q.ai;
+        wr[s][v] = q.gain * tanh_fast(cr[v]);
+        wi[s][v] = q.gain * tanh_fast(ci[v]);
+      }
+    }
+    const int64_t yoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
+    const int64_t hoff = wave_uniform(((row0 + t0) * a.M + mbase) * ESZ);
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      if (TAIL && t0 + s >= a.T) break;  // wave-uniform
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float nr = fmaf(ar[s][v], hr[v], fmaf(-ai[s][v], hi[v], wr[s][v]));
+        const float ni = fmaf(ai[s][v], hr[v], fmaf(ar[s][v], hi[v], wi[s][v]));
+        hr[v] = nr;
+        hi[v] = ni;
+      }
+      float rr[V], ri[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
+      if (lane_ok) {
+        const int64_t yo = yoff + static_cast<int64_t>(s) * W * ESZ;
+        stn<RawT>(a.y, yo, lane_bytes, pack<IO, V>(rr));
+        stn<RawT>(a.y, yo + static_cast<int64_t>(a.M) * ESZ, lane_bytes, pack<IO, V>(ri));
+        const int64_t ho = hoff + static_cast<int64_t>(s) * a.M * ESZ;
+        stn<RawT>(a.h_re, ho, lane_bytes, pack<IO, V>(hr));
+        stn<RawT>(a.h_im, ho, lane_bytes, pack<IO, V>(hi));
+      }
+    }
+  };
+  // block k uses register buffer k & 1; the loop runs over pairs of blocks so
+  // that every buffer index is a compile-time constant (a runtime index into
+  // register arrays becomes indexed register access)
+  auto step_block = [&](auto h_tag, int k) {
+    constexpr int h = decltype(h_tag)::value;
+    load_block(std::integral_constant<int, 1 - h>{}, k + 1 < n_blocks ? k + 1 : k);
+    const int t0 = k * kS;
+    if (t0 + kS <= a.T) run_block(h_tag, t0, std::false_type{});
+    else run_block(h_tag, t0, std::true_type{});
+  };
+  load_block(std::integral_constant<int, 0>{}, 0);
+  for (int k = 0; k < n_blocks; k += 2) {
+    step_block(std::integral_constant<int, 0>{}, k);
+    if (k + 1 < n_blocks) step_block(std::integral_constant<int, 1>{}, k + 1);
+  }
+  if (lane_ok && a.last_re) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      a.last_re[static_cast<int64_t>(b) * a.M + m0 + v] = hr[v];
+      a.last_im[static_cast<int64_t>(b) * a.M + m0 + v] = hi[v];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward scan: one chain per workgroup of two waves, reverse time
+// ---------------------------------------------------------------------------
+// Per step t and mode, with lambda the adjoint of h_t and h' = h_{t-1}:
+//   dx          = lambda * gain * (1 - tanh^2 x)              (the write)
+//   g           = (lambda_re tanh x_re + lambda_im tanh x_im) * gain
+//   dA          = lambda * conj(h')  -> (gar, gai)
+//   dphi        = -gar a_im + gai a_re
+//   radial      = log(rho) (gar a_re + gai a_im) - log(rho) rho delta dphi
+//   wterm       = z rho^2 / (1 - rho^2),  z = nu e^eta   (d log ratio / d eta)
+//   d eta_t    += radial + g (wterm + (1 - sig) wrr / log16)
+//   d delta_t  += dphi (1 - rho) + g (1 - sig) wpr 2/pi
+//   d nu_log   += radial + g (wterm - kappa),  kappa = nu e^{-2nu} / (1 - e^{-2nu})
+//   d theta_log+= theta dphi
+//   d wlg += g, d wpr += g (1 - sig) delta 2/pi, d wrr += g (1 - sig) eta / log16
+// (the P1 chain rule of sparc-kernal/backward/scan.py:593-644 and the write
+// gradients of sparc-kernal/backward/control.py:10-89).
+template <typename IO, int V, int kS>
+__global__ void __launch_bounds__(64, 2)
+mixer_bwd_kernel(Args a) {
+  using RawT = typename Raw<IO, V>::T;
+  constexpr int ESZ = sizeof(IO);
+  constexpr int MB = 64 * V;
+  const int lane = threadIdx.x;
+  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int b = chain / a.n_mb;
+  const int mb = chain - b * a.n_mb;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < a.M;
+  const int n_blocks = (a.T + kS - 1) / kS;
+  const int64_t R = static_cast<int64_t>(a.B) * a.T;
+  const int64_t row0 = static_cast<int64_t>(b) * a.T;
+  const int64_t mbase = static_cast<int64_t>(mb) * MB;
+  const int64_t W = 2 * static_cast<int64_t>(a.M);
+  const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
+  const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
+
+  ModeConsts<V> mc;
+  mc.load(a.consts, m0, lane_ok);
+  float Xr[V], Xi[V];    // conj(a_{t+1}) lambda_{t+1}
+  float hcr[V], hci[V];  // h at the last step of the next block to process
+  float acc[5][V];       // nu_log, theta_log, wlg, wpr, wrr
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int64_t i0 = static_cast<int64_t>(b) * a.M + (lane_ok ? m0 + v : 0);
+    Xr[v] = a.dlast_re ? a.dlast_re[i0] : 0.0f;
+    Xi[v] = a.dlast_im ? a.dlast_im[i0] : 0.0f;
+#pragma unroll
+    for (int p = 0; p < 5; ++p) acc[p][v] = 0.0f;
+  }
+  {  // h_{T-1}: the relu mask of step T-1
+    const int64_t ho = wave_uniform(((row0 + a.T - 1) * a.M + mbase) * ESZ);
+    unpack<IO, V>(ldb<RawT>(a.h_re, ho, lane_ld), hcr);
+    unpack<IO, V>(ldb<RawT>(a.h_im, ho, lane_ld), hci);
+  }
+  wait_vm_all();  // the loop-carried values above, before the first prefetch
+
+  RawT dr[2][kS], di[2][kS], xr[2][kS], xi[2][kS], pr[2][kS], pi[2][kS];
+  float ev[2], dv[2];
+  // block k: steps t0 .. t0+kS-1; the previous states are rows t-1 (row 0
+  // for t = 0, zeroed in the step)
+  auto load_block = [&](auto h_tag, int k) {
+    constexpr int h = decltype(h_tag)::value;
+    const int t0 = k * kS;
+    const int last = a.T - 1 - t0;
+    const int64_t xoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
+    const int64_t poff = wave_uniform(((row0 + t0) * a.M + mbase) * ESZ);
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      const int sc = s <= last ? s : last;
+      const int64_t o = xoff + static_cast<int64_t>(sc) * W * ESZ;
+      dr[h][s] = ldn<RawT>(a.dy, o, lane_ld);
+      di[h][s] = ldn<RawT>(a.dy, o + static_cast<int64_t>(a.M) * ESZ, lane_ld);
+      xr[h][s] = ldn<RawT>(a.x, o, lane_ld);
+      xi[h][s] = ldn<RawT>(a.x, o + static_cast<int64_t>(a.M) * ESZ, lane_ld);
+      const int sp = (t0 + sc > 0) ? sc - 1 : 0;  // row t-1 (t >= 1), else row 0
+      const int64_t q = poff + static_cast<int64_t>(sp) * a.M * ESZ;
+      pr[h][s] = ldn<RawT>(a.h_re, q, lane_ld);
+      pi[h][s] = ldn<RawT>(a.h_im, q, lane_ld);
+    }
+    const int sl = lane & (kS - 1);
+    const int64_t ti = row0 + t0 + (sl <= last ? sl : last);
+    ev[h] = a.eta[ti];
+    dv[h] = a.delta[ti];
+  };
+
+  // One block of kS steps, in phases: (A) every step's transition
+  // (independent of the adjoint); (B) the adjoint, a short serial chain over
+  // the steps in reverse; (C) every step's write gain, tanh and gradients;
+  // (D) the stores and the wave sums of the per-token gradients.  The phases
+  // are straight-line code the compiler can interleave across steps.
+  // TAIL: the block holding T-1 when T is not a multiple of kS.  The relu
+  // mask of step t needs h_t: row t of the saved states, which is the
+  // previous state of step t+1, or (last step of a block, and T-1) the carry
+  // hcr/hci kept from the block processed before.
+  auto run_block = [&](auto h_tag, int t0, auto tail_tag) {
+    constexpr int h = decltype(h_tag)::value;
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    float qar[kS][V], qai[kS][V], qem[kS][V];
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
+      const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), s));
+      const float E = fast_exp(eta);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float em = expm1_nonpos(-mc.nu[v] * E);
+        const float rho = 1.0f + em;
+        float su, cu;
+        sincos_half(-em * delta, su, cu);
+        qar[s][v] = rho * fmaf(mc.ct[v], cu, -mc.st[v] * su);
+        qai[s][v] = rho * fmaf(mc.st[v], cu, mc.ct[v] * su);
+        qem[s][v] = em;
+      }
+    }
+    // (B) the adjoint
+    float lr[kS][V], li[kS][V];
+#pragma unroll
+    for (int s = kS - 1; s >= 0; --s) {
+      const int t = t0 + s;
+      if (TAIL && t >= a.T) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) { lr[s][v] = 0.0f; li[s][v] = 0.0f; }
+        continue;
+      }
+      float gyr[V], gyi[V], mr[V], mi[V];
+      unpack<IO, V>(dr[h][s], gyr);
+      unpack<IO, V>(di[h][s], gyi);
+      const bool carry = s == kS - 1 || (TAIL && t == a.T - 1);  // wave-uniform
+      if (carry) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) { mr[v] = hcr[v]; mi[v] = hci[v]; }
+      } else {
+        unpack<IO, V>(pr[h][s + 1 < kS ? s + 1 : s], mr);
+        unpack<IO, V>(pi[h][s + 1 < kS ? s + 1 : s], mi);
+      }
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        lr[s][v] = (mr[v] > 0.0f ? gyr[v] : 0.0f) + Xr[v];
+        li[s][v] = (mi[v] > 0.0f ? gyi[v] : 0.0f) + Xi[v];
+        Xr[v] = fmaf(qar[s][v], lr[s][v], qai[s][v] * li[s][v]);
+        Xi[v] = fmaf(qar[s][v], li[s][v], -qai[s][v] * lr[s][v]);
+      }
+    }
+    // (C) gradients; e[2s], e[2s+1]: this lane's d eta, d delta of step s
+    float dxr[kS][V], dxi[kS][V], e[2 * kS];
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      const int t = t0 + s;
+      const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
+      const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), s));
+      const float E = fast_exp(eta);
+      const float ps = delta * kTwoOverPi, rs = eta * kInvLog16;
+      float hpr[V], hpi[V], cxr[V], cxi[V];
+      unpack<IO, V>(pr[h][s], hpr);
+      unpack<IO, V>(pi[h][s], hpi);
+      unpack<IO, V>(xr[h][s], cxr);
+      unpack<IO, V>(xi[h][s], cxi);
+      float se = 0.0f, sd = 0.0f;
+      const bool live = !TAIL || t < a.T;  // steps past T contribute nothing (wave-uniform)
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        if (t == 0) { hpr[v] = 0.0f; hpi[v] = 0.0f; }
+        const float l_r = lr[s][v], l_i = li[s][v];
+        const float em = qem[s][v], rho = 1.0f + em;
+        const float ar = qar[s][v], ai = qai[s][v];
+        const float one_m_r2 = -em * (2.0f + em);  // 1 - rho^2 = -expm1(-2 nu E)
+        const float ratio = __builtin_amdgcn_sqrtf(-one_m_r2 * mc.cinv[v]);
+        const float q = fmaf(ps, mc.wpr[v], rs * mc.wrr[v]);
+        const float sg = __builtin_amdgcn_rcpf(1.0f + fast_exp(-q));
+        const float gain = mc.gam[v] * ratio * 2.0f * sg;
+        const float tr = tanh_fast(cxr[v]), ti = tanh_fast(cxi[v]);
+        dxr[s][v] = l_r * gain * fmaf(-tr, tr, 1.0f);
+        dxi[s][v] = l_i * gain * fmaf(-ti, ti, 1.0f);
+        const float g = fmaf(l_r, tr, l_i * ti) * gain;
+        const float gar = fmaf(l_r, hpr[v], l_i * hpi[v]);
+        const float gai = fmaf(l_i, hpr[v], -l_r * hpi[v]);
+        const float dphi = fmaf(-gar, ai, gai * ar);
+        const float z = mc.nu[v] * E;  // -log(rho)
+        const float radial = z * fmaf(rho * delta, dphi, -fmaf(gar, ar, gai * ai));
+        const float wterm = z * rho * rho * __builtin_amdgcn_rcpf(one_m_r2);
+        const float gs = g * (1.0f - sg);
+        se += radial + g * wterm + gs * mc.wrr[v] * kInvLog16;
+        sd += fmaf(dphi, -em, gs * mc.wpr[v] * kTwoOverPi);
+        if (live) {
+          const float kappa = -mc.nu[v] * (1.0f + mc.cinv[v]);
+          acc[0][v] += radial + g * (wterm - kappa);
+          acc[1][v] = fmaf(mc.th[v], dphi, acc[1][v]);
+          acc[2][v] += g;
+          acc[3][v] = fmaf(gs, ps, acc[3][v]);
+          acc[4][v] = fmaf(gs, rs, acc[4][v]);
+        }
+      }
+      e[2 * s] = lane_ok ? se : 0.0f;
+      e[2 * s + 1] = lane_ok ? sd : 0.0f;
+    }
+    // (D) stores; the carry for the next block (in reverse time) is h_{t0-1}
+    const int64_t xoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      if (TAIL && t0 + s >= a.T) break;
+      if (lane_ok) {
+        const int64_t o = xoff + static_cast<int64_t>(s) * W * ESZ;
+        stn<RawT>(a.dx, o, lane_bytes, pack<IO, V>(dxr[s]));
+        stn<RawT>(a.dx, o + static_cast<int64_t>(a.M) * ESZ, lane_bytes, pack<IO, V>(dxi[s]));
+      }
+    }
+    // the lane sums of the block's 2*kS per-token values: lane l ends with
+    // value l / per
+    wave_reduce_scatter<2 * kS>(e, lane);
+    constexpr int per = 64 / (2 * kS);
+    const int i = lane / per;
+    const int t = t0 + (i >> 1);
+    if (lane % per == 0 && t < a.T)
+      a.part_tok[(static_cast<int64_t>(i & 1) * a.n_mb + mb) * R + row0 + t] = e[0];
+    unpack<IO, V>(pr[h][0], hcr);
+    unpack<IO, V>(pi[h][0], hci);
+  };
+
+  // block k uses register buffer k & 1 (compile-time in each call, see the forward)
+  auto step_block = [&](auto h_tag, int k) {
+    constexpr int h = decltype(h_tag)::value;
+    load_block(std::integral_constant<int, 1 - h>{}, k > 0 ? k - 1 : k);
+    const int t0 = k * kS;
+    if (t0 + kS <= a.T) run_block(h_tag, t0, std::false_type{});
+    else run_block(h_tag, t0, std::true_type{});
+  };
+  int k = n_blocks - 1;
+  if (k & 1) {
+    load_block(std::integral_constant<int, 1>{}, k);
+    step_block(std::integral_constant<int, 1>{}, k);
+    --k;
+  } else {
+    load_block(std::integral_constant<int, 0>{}, k);
+  }
+  for (; k >= 0; k -= 2) {  // k even here
+    step_block(std::integral_constant<int, 0>{}, k);
+    if (k >= 1) step_block(std::integral_constant<int, 1>{}, k - 1);
+  }
+  if (lane_ok) {
+#pragma unroll
+    for (int p = 0; p < 5; ++p)
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        a.part_mode[(static_cast<int64_t>(p) * a.B + b) * a.M + m0 + v] = acc[p][v];
+  }
+}
+
+__global__ void fill_zero_f32_kernel(float* p, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+// d eta, d delta per token: the sum of the mode-block partials [n_mb][R]
+__global__ void __launch_bounds__(256)
+token_sum_kernel(int64_t R, int n_mb, const float* part, float* deta, float* ddelta) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (r >= R) return;
+  float s0 = 0.0f, s1 = 0.0f;
+  for (int j = 0; j < n_mb; ++j) {
+    s0 += part[static_cast<int64_t>(j) * R + r];
+    s1 += part[(static_cast<int64_t>(n_mb) + j) * R + r];
+  }
+  deta[r] = s0;
+  ddelta[r] = s1;
+}
+
+// ---------------------------------------------------------------------------
+// controls backward: dx += dp0 u_phase + dp1 u_radial (in place), direction
+// gradient partials per row block
+// ---------------------------------------------------------------------------
+// dp1 = d eta * log16 (1 - tanh^2 p1) = d eta * log16 (1 - (eta/log16)^2),
+// dp0 = d delta * pi/2 (1 - (delta/(pi/2))^2).  A workgroup: 2048 columns (8
+// per thread) of kCtrlBwdRows rows.
+template <typename IO>
+__global__ void __launch_bounds__(256)
+ctrl_bwd_kernel(int64_t R, int W, const void* x, const float* pdir, const float* rdir,
+                const float* eta, const float* delta, const float* deta, const float* ddelta,
+                void* dx, float* pd, float* pbias) {
+  const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kCtrlBwdRows;
+  const int64_t r1 = r0 + kCtrlBwdRows < R ? r0 + kCtrlBwdRows : R;
+  const bool col_ok = c < W;
+  const int cc = col_ok ? c : 0;
+  float u0[8], u1[8], a0[8], a1[8];
+  *reinterpret_cast<float4*>(u0) = *reinterpret_cast<const float4*>(pdir + cc);
+  *reinterpret_cast<float4*>(u0 + 4) = *reinterpret_cast<const float4*>(pdir + cc + 4);
+  *reinterpret_cast<float4*>(u1) = *reinterpret_cast<const float4*>(rdir + cc);
+  *reinterpret_cast<float4*>(u1 + 4) = *reinterpret_cast<const float4*>(rdir + cc + 4);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { a0[i] = 0.0f; a1[i] = 0.0f; }
+  float b0 = 0.0f, b1 = 0.0f;
+  for (int64_t r = r0; r < r1; ++r) {
+    const float e = eta[r] * kInvLog16, d = delta[r] * kTwoOverPi;
+    const float dp1 = deta[r] * kLog16 * fmaf(-e, e, 1.0f);
+    const float dp0 = ddelta[r] * kHalfPi * fmaf(-d, d, 1.0f);
+    b0 += dp0;
+    b1 += dp1;
+    if (!col_ok) continue;
+    float xv[8], gv[8];
+    if constexpr (sizeof(IO) == 2) {
+      unpack<bf16, 8>(load_raw_nt<bf16, 8>(x, r * W + c), xv);
+      unpack<bf16, 8>(load_raw_nt<bf16, 8>(dx, r * W + c), gv);
+    } else {
+      float t[4];
+      unpack<float, 4>(load_raw_nt<float, 4>(x, r * W + c), t);
+      for (int i = 0; i < 4; ++i) xv[i] = t[i];
+      unpack<float, 4>(load_raw_nt<float, 4>(x, r * W + c + 4), t);
+      for (int i = 0; i < 4; ++i) xv[4 + i] = t[i];
+      unpack<float, 4>(load_raw_nt<float, 4>(dx, r * W + c), t);
+      for (int i = 0; i < 4; ++i) gv[i] = t[i];
+      unpack<float, 4>(load_raw_nt<float, 4>(dx, r * W + c + 4), t);
+      for (int i = 0; i < 4; ++i) gv[4 + i] = t[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      gv[i] = fmaf(dp0, u0[i], fmaf(dp1, u1[i], gv[i]));
+      a0[i] = fmaf(dp0, xv[i], a0[i]);
+      a1[i] = fmaf(dp1, xv[i], a1[i]);
+    }
+    if constexpr (sizeof(IO) == 2) {
+      store_raw_nt<bf16, 8>(dx, r * W + c, pack<bf16, 8>(gv));
+    } else {
+      float t[4];
+      for (int i = 0; i < 4; ++i) t[i] = gv[i];
+      store_raw_nt<float, 4>(dx, r * W + c, pack<float, 4>(t));
+      for (int i = 0; i < 4; ++i) t[i] = gv[4 + i];
+      store_raw_nt<float, 4>(dx, r * W + c + 4, pack<float, 4>(t));
+    }
+  }
+  if (col_ok) {
+    float* o0 = pd + static_cast<int64_t>(blockIdx.y) * W + c;
+    float* o1 = pd + (static_cast<int64_t>(gridDim.y) + blockIdx.y) * W + c;
+    *reinterpret_cast<float4*>(o0) = *reinterpret_cast<const float4*>(a0);
+    *reinterpret_cast<float4*>(o0 + 4) = *reinterpret_cast<const float4*>(a0 + 4);
+    *reinterpret_cast<float4*>(o1) = *reinterpret_cast<const float4*>(a1);
+    *reinterpret_cast<float4*>(o1 + 4) = *reinterpret_cast<const float4*>(a1 + 4);
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    pbias[blockIdx.y] = b0;
+    pbias[gridDim.y + blockIdx.y] = b1;
+  }
+}
+
+}  // namespace mix
+}  // namespace sparc
+
+// ===========================================================================
+// host side
+// ===========================================================================
+namespace {
+using namespace sparc::mix;
+
+sparc_status fail(sparc_status s, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+sparc_status fail(sparc_status s, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(sparc::error_buffer(), 512, fmt, ap);
+  va_end(ap);
+  return s;
+}
+bool al(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Modes per lane of the forward (0: automatic) and of the backward.
+#ifndef SPARC_MIXER_FWD_V
+#define SPARC_MIXER_FWD_V 0
+#endif
+#ifndef SPARC_MIXER_BWD_V
+#define SPARC_MIXER_BWD_V 1
+#endif
+// Forward: 2 when that still leaves a wave per SIMD (1024 chains on the
+// 256-CU MI355X), else 1 (twice the chains).  Backward: the fixed choice
+// (its per-step working set is twice the forward's).
+int mixer_v(int64_t B, int64_t M, int direction) {
+  const int fixed = direction == 0 ? SPARC_MIXER_FWD_V : SPARC_MIXER_BWD_V;
+  if (fixed == 1 || M % 2) return 1;
+  if (fixed == 2) return 2;
+  const int64_t chains2 = B * ((M + 127) / 128);
+  return chains2 >= 1024 ? 2 : 1;
+}
+
+struct Layout {
+  int V = 1, n_mb = 0, n_rb = 0;
+  int64_t R = 0;
+  size_t consts = 0, part_tok = 0, tok = 0, part_mode = 0, pd = 0, pbias = 0, total = 0;
+};
+
+Layout layout(int64_t B, int64_t T, int64_t M, int direction) {
+  Layout l;
+  l.V = mixer_v(B, M, direction);
+  l.n_mb = static_cast<int>((M + 64 * l.V - 1) / (64 * l.V));
+  l.R = B * T;
+  l.n_rb = static_cast<int>((l.R + kCtrlBwdRows - 1) / kCtrlBwdRows);
+  auto up = [](size_t n) { return (n + 255) / 256 * 256; };
+  size_t off = 256;
+  l.consts = off;
+  off += up(static_cast<size_t>(M) * kConsts * 4);
+  if (direction == 1) {
+    l.part_tok = off;
+    off += up(static_cast<size_t>(2) * l.n_mb * l.R * 4);
+    l.tok = off;
+    off += up(static_cast<size_t>(2) * l.R * 4);
+    l.part_mode = off;
+    off += up(static_cast<size_t>(5) * B * M * 4);
+    l.pd = off;
+    off += up(static_cast<size_t>(2) * l.n_rb * 2 * M * 4);
+    l.pbias = off;
+    off += up(static_cast<size_t>(2) * l.n_rb * 4);
+  }
+  l.total = off;
+  return l;
+}
+
+sparc_status check_shape(int64_t B, int64_t T, int64_t M, int32_t io) {
+  if (B <= 0 || T < 0 || M <= 0) return fail(SPARC_EINVAL, "mixer: B > 0, T >= 0, M > 0 required");
+  if (M % 4) return fail(SPARC_EINVAL, "mixer: modes must be a multiple of 4");
+  if (io != SPARC_F32 && io != SPARC_BF16) return fail(SPARC_EINVAL, "mixer: io_dtype");
+  if (M > (1 << 26) || B * T > (int64_t(1) << 40) || B * T * 2 * M > (int64_t(1) << 46) || B > INT32_MAX ||
+      T > INT32_MAX)
+    return fail(SPARC_EINVAL, "mixer: shape too large");
+  return SPARC_OK;
+}
+
+template <typename IO, int V>
+void launch_fwd(const Args& a, hipStream_t st) {
+  hipLaunchKernelGGL((mixer_fwd_kernel<IO, V>), dim3(static_cast<unsigned>(a.B) * a.n_mb), dim3(64), 0, st, a);
+}
+#ifndef SPARC_MIXER_BWD_S
+#define SPARC_MIXER_BWD_S 4
+#endif
+template <typename IO, int V>
+void launch_bwd(const Args& a, hipStream_t st) {
+  hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, SPARC_MIXER_BWD_S>), dim3(static_cast<unsigned>(a.B) * a.n_mb), dim3(64), 0, st, a);
+}
+}  // namespace
+
+extern "C" {
+
+size_t sparc_mixer_workspace_bytes(int64_t batch, int64_t length, int64_t modes, int direction) {
+  if (batch <= 0 || length < 0 || modes <= 0 || modes % 4 || (direction != 0 && direction != 1)) return 0;
+  return layout(batch, length, modes, direction).total;
+}
+
+sparc_status sparc_mixer_forward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                                 const void* x, const float* phase_direction, const float* radial_direction,
+                                 const float* nu_log, const float* theta_log, const float* write_log_gain,
+                                 const float* write_phase_response, const float* write_radial_response,
+                                 float* eta, float* delta, void* y, void* h_re, void* h_im,
+                                 float* last_re, float* last_im, void* workspace, size_t workspace_bytes,
+                                 sparc_stream_t stream) {
+  if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
+  if (!x || !phase_direction || !radial_direction || !nu_log || !theta_log || !write_log_gain ||
+      !write_phase_response || !write_radial_response || !eta || !delta || !y || !h_re || !h_im)
+    return fail(SPARC_EINVAL, "mixer forward: NULL pointer");
+  if ((last_re == nullptr) != (last_im == nullptr)) return fail(SPARC_EINVAL, "mixer forward: last_re/last_im");
+  const Layout l = layout(batch, length, modes, 0);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(SPARC_EWORKSPACE, "mixer forward: workspace too small (%zu < %zu)", workspace_bytes, l.total);
+  const size_t esz = io_dtype == SPARC_BF16 ? 2 : 4;
+  if (!al(x, 16) || !al(y, 16) || !al(h_re, esz * l.V) || !al(h_im, esz * l.V) || !al(phase_direction, 16) ||
+      !al(radial_direction, 16) || !al(workspace, 256))
+    return fail(SPARC_EINVAL, "mixer forward: misaligned tensor");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int M = static_cast<int>(modes), W = 2 * M;
+  float* consts = reinterpret_cast<float*>(static_cast<char*>(workspace) + l.consts);
+  hipLaunchKernelGGL(mixer_prepare_kernel, dim3(static_cast<unsigned>((M + 255) / 256)), dim3(256), 0, st, M, nu_log,
+                     theta_log, write_log_gain, write_phase_response, write_radial_response, consts);
+  if (length == 0) {  // the state stays 0
+    if (last_re) {
+      const int64_t n = batch * modes;
+      const dim3 g(static_cast<unsigned>((n + 255) / 256));
+      hipLaunchKernelGGL(fill_zero_f32_kernel, g, dim3(256), 0, st, last_re, n);
+      hipLaunchKernelGGL(fill_zero_f32_kernel, g, dim3(256), 0, st, last_im, n);
+    }
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer forward: %s", hipGetErrorString(e));
+  }
+  const dim3 gc(static_cast<unsigned>((l.R + kCtrlRows - 1) / kCtrlRows));
+  if (io_dtype == SPARC_BF16)
+    hipLaunchKernelGGL(ctrl_fwd_kernel<sparc::bf16>, gc, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction, eta, delta);
+  else
+    hipLaunchKernelGGL(ctrl_fwd_kernel<float>, gc, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction, eta, delta);
+  Args a{};
+  a.B = static_cast<int>(batch);
+  a.T = static_cast<int>(length);
+  a.M = M;
+  a.n_mb = l.n_mb;
+  a.x = x; a.consts = consts; a.eta = eta; a.delta = delta;
+  a.y = y; a.h_re = h_re; a.h_im = h_im; a.last_re = last_re; a.last_im = last_im;
+  if (io_dtype == SPARC_BF16) {
+    if (l.V == 2) launch_fwd<sparc::bf16, 2>(a, st); else launch_fwd<sparc::bf16, 1>(a, st);
+  } else {
+    if (l.V == 2) launch_fwd<float, 2>(a, st); else launch_fwd<float, 1>(a, st);
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer forward: %s", hipGetErrorString(e));
+}
+
+sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                                  const void* x, const float* phase_direction, const float* radial_direction,
+                                  const float* nu_log, const float* theta_log, const float* write_log_gain,
+                                  const float* write_phase_response, const float* write_radial_response,
+                                  const float* eta, const float* delta, const void* h_re, const void* h_im,
+                                  const void* dy, const float* dlast_re, const float* dlast_im, void* dx,
+                                  float* dphase_direction, float* dradial_direction, float* dnu_log,
+                                  float* dtheta_log, float* dwrite_log_gain, float* dwrite_phase_response,
+                                  float* dwrite_radial_response, void* workspace, size_t workspace_bytes,
+                                  sparc_stream_t stream) {
+  if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
+  if (!x || !phase_direction || !radial_direction || !nu_log || !theta_log || !write_log_gain ||
+      !write_phase_response || !write_radial_response || !eta || !delta || !h_re || !h_im || !dy || !dx ||
+      !dphase_direction || !dradial_direction || !dnu_log || !dtheta_log || !dwrite_log_gain ||
+      !dwrite_phase_response || !dwrite_radial_response)
+    return fail(SPARC_EINVAL, "mixer backward: NULL pointer");
+  if ((dlast_re == nullptr) != (dlast_im == nullptr)) return fail(SPARC_EINVAL, "mixer backward: dlast_re/dlast_im");
+  const Layout l = layout(batch, length, modes, 1);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(SPARC_EWORKSPACE, "mixer backward: workspace too small (%zu < %zu)", workspace_bytes, l.total);
+  const size_t esz = io_dtype == SPARC_BF16 ? 2 : 4;
+  if (!al(x, 16) || !al(dy, 16) || !al(dx, 16) || !al(h_re, esz * l.V) || !al(h_im, esz * l.V) ||
+      !al(phase_direction, 16) || !al(radial_direction, 16) || !al(workspace, 256))
+    return fail(SPARC_EINVAL, "mixer backward: misaligned tensor");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int M = static_cast<int>(modes), W = 2 * M;
+  char* ws = static_cast<char*>(workspace);
+  float* consts = reinterpret_cast<float*>(ws + l.consts);
+  float* part_tok = reinterpret_cast<float*>(ws + l.part_tok);
+  float* tok = reinterpret_cast<float*>(ws + l.tok);
+  float* part_mode = reinterpret_cast<float*>(ws + l.part_mode);
+  float* pd = reinterpret_cast<float*>(ws + l.pd);
+  float* pbias = reinterpret_cast<float*>(ws + l.pbias);
+  hipLaunchKernelGGL(mixer_prepare_kernel, dim3(static_cast<unsigned>((M + 255) / 256)), dim3(256), 0, st, M, nu_log,
+                     theta_log, write_log_gain, write_phase_response, write_radial_response, consts);
+  if (length == 0) {
+    const dim3 gz(static_cast<unsigned>((W + 1 + 255) / 256)), gm(static_cast<unsigned>((M + 255) / 256));
+    for (float* o : {dphase_direction, dradial_direction})
+      hipLaunchKernelGGL(fill_zero_f32_kernel, gz, dim3(256), 0, st, o, static_cast<int64_t>(W + 1));
+    for (float* o : {dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response})
+      hipLaunchKernelGGL(fill_zero_f32_kernel, gm, dim3(256), 0, st, o, static_cast<int64_t>(M));
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(e));
+  }
+  Args a{};
+  a.B = static_cast<int>(batch);
+  a.T = static_cast<int>(length);
+  a.M = M;
+  a.n_mb = l.n_mb;
+  a.x = x; a.consts = consts; a.eta = eta; a.delta = delta;
+  a.h_re = const_cast<void*>(h_re); a.h_im = const_cast<void*>(h_im);
+  a.dy = dy; a.dlast_re = dlast_re; a.dlast_im = dlast_im; a.dx = dx;
+  a.part_tok = part_tok; a.part_mode = part_mode;
+  if (io_dtype == SPARC_BF16) {
+    if (l.V == 2) launch_bwd<sparc::bf16, 2>(a, st); else launch_bwd<sparc::bf16, 1>(a, st);
+  } else {
+    if (l.V == 2) launch_bwd<float, 2>(a, st); else launch_bwd<float, 1>(a, st);
+  }
+  float* deta = tok;
+  float* ddelta = tok + l.R;
+  hipLaunchKernelGGL(token_sum_kernel, dim3(static_cast<unsigned>((l.R + 255) / 256)), dim3(256), 0, st, l.R, l.n_mb,
+                     part_tok, deta, ddelta);
+  float* outs[5] = {dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response};
+  for (int p = 0; p < 5; ++p)
+    if (sparc_status s = sparc_column_sum(batch, modes, part_mode + static_cast<int64_t>(p) * batch * modes, outs[p], 0, stream))
+      return s;
+  const dim3 gb(static_cast<unsigned>((W + 2047) / 2048), static_cast<unsigned>(l.n_rb));
+  if (io_dtype == SPARC_BF16)
+    hipLaunchKernelGGL(ctrl_bwd_kernel<sparc::bf16>, gb, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction,
+                       eta, delta, deta, ddelta, dx, pd, pbias);
+  else
+    hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction,
+                       eta, delta, deta, ddelta, dx, pd, pbias);
+  // direction gradients: columns 0..W-1 from the row-block partials, the bias from pbias
+  const int64_t plane = static_cast<int64_t>(l.n_rb) * W;
+  if (sparc_status s = sparc_column_sum(l.n_rb, W, pd, dphase_direction, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(l.n_rb, W, pd + plane, dradial_direction, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(l.n_rb, 1, pbias, dphase_direction + W, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(l.n_rb, 1, pbias + l.n_rb, dradial_direction + W, 0, stream)) return s;
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(e));
+}
+
+}  // extern "C"

@@ -340,44 +340,6 @@ decode_dots_kernel(int B, int W, const void* x, const float* pdir, const float* 
   }
 }
 
-// expm1(x) for x <= 0 to ~1e-7 relative: Taylor series (8 terms) near 0,
-// exp(x) - 1 further out (no cancellation there)
-__device__ __forceinline__ float expm1_nonpos(float x) {
-  float p = 1.0f / 5040.0f;
-  p = fmaf(p, x, 1.0f / 720.0f);
-  p = fmaf(p, x, 1.0f / 120.0f);
-  p = fmaf(p, x, 1.0f / 24.0f);
-  p = fmaf(p, x, 1.0f / 6.0f);
-  p = fmaf(p, x, 0.5f);
-  p = fmaf(p, x, 1.0f);
-  p *= x;
-  return x > -0.25f ? p : fast_exp(x) - 1.0f;
-}
-
-// sin and cos of |u| <= pi/2 by Taylor series to x^11 / x^12 (error < 6e-8)
-__device__ __forceinline__ void sincos_half(float u, float& s, float& c) {
-  const float u2 = u * u;
-  float ps = -1.0f / 39916800.0f;
-  ps = fmaf(ps, u2, 1.0f / 362880.0f);
-  ps = fmaf(ps, u2, -1.0f / 5040.0f);
-  ps = fmaf(ps, u2, 1.0f / 120.0f);
-  ps = fmaf(ps, u2, -1.0f / 6.0f);
-  s = fmaf(ps * u2, u, u);
-  float pc = 1.0f / 479001600.0f;
-  pc = fmaf(pc, u2, -1.0f / 3628800.0f);
-  pc = fmaf(pc, u2, 1.0f / 40320.0f);
-  pc = fmaf(pc, u2, -1.0f / 720.0f);
-  pc = fmaf(pc, u2, 1.0f / 24.0f);
-  pc = fmaf(pc, u2, -0.5f);
-  c = fmaf(pc, u2, 1.0f);
-}
-
-// tanh through one hardware exponential and reciprocal (absolute error ~1e-7)
-__device__ __forceinline__ float tanh_fast(float x) {
-  const float e = fast_exp(-2.0f * fabsf(x));
-  return copysignf((1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e), x);
-}
-
 template <typename IO>
 __global__ void __launch_bounds__(256)
 decode_update_kernel(int B, int M, const void* x, const float* pbias, const float* rbias, const float* part,

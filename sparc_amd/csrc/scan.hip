@@ -92,26 +92,6 @@ struct ScanArgs {
   float* carry;       // backward inclusive adjoint carries [B, n_chunks, M, NH]
 };
 
-// A 64-bit value every lane of the wave holds, moved to scalar registers, so
-// that a memory instruction can take (kernel-argument pointer + this offset)
-// as its scalar base and the lane's byte offset as its vector offset.
-__device__ __forceinline__ int64_t wave_uniform(int64_t v) {
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
-  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-template <typename T>
-__device__ __forceinline__ T ldb(const void* base, int64_t byte_off, uint32_t lane_bytes) {
-  return *reinterpret_cast<const T*>(static_cast<const char*>(base) + byte_off + lane_bytes);
-}
-template <typename T>
-__device__ __forceinline__ void stb(void* base, int64_t byte_off, uint32_t lane_bytes, T v) {
-  *reinterpret_cast<T*>(static_cast<char*>(base) + byte_off + lane_bytes) = v;
-}
-// Non-temporal forms of ldb / stb for the streamed planes of the serial
-// kernels, each element of which is read or written once per launch: the nt
-// cache policy keeps them from displacing lines that are reused.
 // Cache policy of the serial kernels' plane loads and stores: bit 0 loads,
 // bit 1 stores non-temporal (forward and backward separately).
 #ifndef SPARC_FWD_NT
@@ -120,25 +100,6 @@ __device__ __forceinline__ void stb(void* base, int64_t byte_off, uint32_t lane_
 #ifndef SPARC_BWD_NT
 #define SPARC_BWD_NT 3
 #endif
-template <typename T, bool NT = true>
-__device__ __forceinline__ T ldn(const void* base, int64_t byte_off, uint32_t lane_bytes) {
-  if constexpr (!NT) return ldb<T>(base, byte_off, lane_bytes);
-  using N = typename NtBits<sizeof(T)>::T;
-  const N n = __builtin_nontemporal_load(
-      reinterpret_cast<const N*>(static_cast<const char*>(base) + byte_off + lane_bytes));
-  T r;
-  __builtin_memcpy(&r, &n, sizeof(T));
-  return r;
-}
-template <typename T, bool NT = true>
-__device__ __forceinline__ void stn(void* base, int64_t byte_off, uint32_t lane_bytes, T v) {
-  if constexpr (!NT) { stb<T>(base, byte_off, lane_bytes, v); return; }
-  using N = typename NtBits<sizeof(T)>::T;
-  N n;
-  __builtin_memcpy(&n, &v, sizeof(T));
-  __builtin_nontemporal_store(n, reinterpret_cast<N*>(static_cast<char*>(base) + byte_off + lane_bytes));
-}
-
 // Cache policy of the look-back kernels' streamed planes (w, y, dy, dw): bit 0
 // non-temporal loads, bit 1 non-temporal stores.  Measured at B=4, T=65536,
 // M=4096 (real, fp32): both non-temporal 1.64 / 2.66 ms forward / backward,
@@ -2825,8 +2786,6 @@ chain_bwd_saved_kernel(ScanArgs p) {
 // ---------------------------------------------------------------------------
 constexpr int kStateChunk = 64;  // steps per saved chunk state
 
-// s_waitcnt vmcnt(0): every vector memory operation of the wave has completed.
-__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 // blocks of gates in flight in the helper wave (loaded kGateDepth-1 blocks
 // before their table is built); an even number
 #ifndef SPARC_GATE_DEPTH

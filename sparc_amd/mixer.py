@@ -1,0 +1,130 @@
+"""The module's fused sequence path: ``SPARCMixer.forward`` and its backward
+as two C-ABI calls (sparc_mixer_forward / sparc_mixer_backward), reading x
+directly instead of materialising the [B, L, M] write tensors.
+
+Same values and gradients as the composed path (controls, write, scan and
+epilogue as separate operators) up to float rounding; the write is kept in
+fp32 inside the scan instead of being rounded to x's dtype first.  The
+states h are saved in x's dtype for the backward, as the reference saves
+out_r / out_i (sparc-kernal/backward/scan.py:1348-1356).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_PATHS = ("auto", "fused", "composed")
+_path = "auto"
+
+
+def set_mixer_path(name: str) -> None:
+    """Sequence path of ``SPARCMixer.forward``: "fused" (sparc_mixer_*),
+    "composed" (controls, write, chunked scan as separate operators) or
+    "auto" (fused unless the shape has few chains and a long sequence, where
+    the composed path's look-back scan parallelises over time)."""
+    global _path
+    if name not in _PATHS:
+        raise ValueError(f"unknown mixer path {name!r}")
+    _path = name
+
+
+def get_mixer_path() -> str:
+    return _path
+
+
+def fused_supported(x: torch.Tensor, modes: int) -> bool:
+    return (x.is_cuda and x.dtype in (torch.float32, torch.bfloat16) and modes % 4 == 0
+            and x.ndim == 3 and x.shape[0] > 0)
+
+
+def use_fused(x: torch.Tensor, modes: int) -> bool:
+    if _path == "composed":
+        return False
+    ok = fused_supported(x, modes)
+    if _path == "fused":
+        if not ok:
+            raise ValueError("the fused mixer path needs GPU fp32/bf16 x [B, L, 2M] with M % 4 == 0")
+        return True
+    if not ok:
+        return False
+    B, T = x.shape[0], x.shape[1]
+    chains = B * ((modes + 63) // 64)
+    return chains >= 256 or T <= 4096
+
+
+_PARAMS = ("phase_direction", "radial_direction", "nu_log", "theta_log", "write_log_gain",
+           "write_phase_response", "write_radial_response")
+
+
+class _FusedMixer(torch.autograd.Function):
+    """Outputs y = relu(cat(h_re, h_im)) [B, L, 2M] (x's dtype) and the last
+    state (last_re, last_im) fp32 [B, M]."""
+
+    @staticmethod
+    def forward(ctx, x, phase_direction, radial_direction, nu_log, theta_log, write_log_gain,
+                write_phase_response, write_radial_response, energy_response):
+        lib = _lib.load()
+        dev = _lib.require_gpu(x, phase_direction, nu_log)
+        x = x.contiguous()
+        params = [p.detach().float().contiguous() for p in (
+            phase_direction, radial_direction, nu_log, theta_log, write_log_gain,
+            write_phase_response, write_radial_response)]
+        B, T, W = x.shape
+        M = W // 2
+        io = _lib.io_code(x.dtype)
+        eta = torch.empty(B, T, dtype=torch.float32, device=dev)
+        delta = torch.empty_like(eta)
+        y = torch.empty_like(x)
+        h_re = torch.empty(B, T, M, dtype=x.dtype, device=dev)
+        h_im = torch.empty_like(h_re)
+        last_re = torch.empty(B, M, dtype=torch.float32, device=dev)
+        last_im = torch.empty_like(last_re)
+        ws_bytes = lib.sparc_mixer_workspace_bytes(B, T, M, 0)
+        if ws_bytes == 0:
+            raise ValueError("invalid shape for the fused mixer")
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        P = _lib.ptr
+        _lib.check(lib.sparc_mixer_forward(
+            B, T, M, io, P(x), *[P(p) for p in params], P(eta), P(delta), P(y), P(h_re), P(h_im),
+            P(last_re), P(last_im), P(ws), ws.numel(), _lib.stream_of(dev)), "sparc_mixer_forward")
+        ctx.save_for_backward(x, *params, eta, delta, h_re, h_im)
+        ctx.dtypes = [p.dtype for p in (phase_direction, radial_direction, nu_log, theta_log,
+                                        write_log_gain, write_phase_response, write_radial_response)]
+        ctx.energy = (energy_response.shape, energy_response.dtype)
+        return y, last_re, last_im
+
+    @staticmethod
+    def backward(ctx, dy, dlast_re, dlast_im):
+        x, pd, rd, nu, th, wlg, wpr, wrr, eta, delta, h_re, h_im = ctx.saved_tensors
+        lib = _lib.load()
+        dev = x.device
+        B, T, W = x.shape
+        M = W // 2
+        if dy is None:
+            dy = torch.zeros_like(x)
+        dy = dy.to(x.dtype).contiguous()
+        if dlast_re is not None or dlast_im is not None:
+            z = torch.zeros(B, M, dtype=torch.float32, device=dev)
+            dlast_re = z if dlast_re is None else dlast_re.float().contiguous()
+            dlast_im = z.clone() if dlast_im is None else dlast_im.float().contiguous()
+        dx = torch.empty_like(x)
+        grads = [torch.empty(W + 1, dtype=torch.float32, device=dev) for _ in range(2)]
+        grads += [torch.empty(M, dtype=torch.float32, device=dev) for _ in range(5)]
+        ws = torch.empty(lib.sparc_mixer_workspace_bytes(B, T, M, 1), dtype=torch.uint8, device=dev)
+        P = _lib.ptr
+        _lib.check(lib.sparc_mixer_backward(
+            B, T, M, _lib.io_code(x.dtype), P(x), P(pd), P(rd), P(nu), P(th), P(wlg), P(wpr), P(wrr),
+            P(eta), P(delta), P(h_re), P(h_im), P(dy), P(dlast_re), P(dlast_im), P(dx),
+            *[P(g) for g in grads], P(ws), ws.numel(), _lib.stream_of(dev)), "sparc_mixer_backward")
+        grads = [g.to(dt) for g, dt in zip(grads, ctx.dtypes)]
+        shape, dt = ctx.energy
+        # energy_response is an inactive parameter (0 * sum in make_controls): gradient 0
+        return (dx, *grads, torch.zeros(shape, dtype=dt, device=dev))
+
+
+def fused_sequence(module, x: torch.Tensor):
+    """(y, (last_re, last_im)) of the module on x through the fused path."""
+    y, last_re, last_im = _FusedMixer.apply(
+        x, *[getattr(module, n) for n in _PARAMS], module.energy_response)
+    return y, (last_re, last_im)

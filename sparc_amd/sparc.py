@@ -4,9 +4,11 @@ Constructor, parameters and buffers, ``forward(x, return_cache=False)``,
 ``step(x, state, segment_pos)``, ``prepare_inference()`` and the knob setters
 keep the reference's signatures, defaults and ``ValueError``s.  The sequence
 forward is ``run_sequence`` below (reference: sparc-kernal/forward/scan.py:
-1398-1603): torch controls, HIP write prologue, HIP chunked P1 scan with the
-``relu(cat(h_re, h_im))`` epilogue fused into the scan's store, and HIP
-backward kernels underneath autograd.
+1398-1603): by default the fused HIP path (controls, write, P1 scan and
+``relu(cat(h_re, h_im))`` epilogue in two C-ABI calls forward and backward,
+``sparc_amd.mixer``); for few chains over long sequences the composed path
+(torch controls, HIP write prologue, HIP chunked P1 scan with the epilogue
+fused into its store).
 """
 from __future__ import annotations
 
@@ -18,6 +20,7 @@ from torch import nn
 
 from .control import latest_sparc_write, make_controls, make_scan_inputs
 from .decode import prepare_decode, run_decode_step
+from .mixer import fused_sequence, use_fused
 from .ops import chunk_scan
 
 _NAMED_BACKENDS = ("tiled_serial", "triton", "precomputed_decay", "framework_eager",
@@ -48,6 +51,9 @@ def run_sequence(module, x: torch.Tensor, return_cache: bool = False):
     _validate_backend(module.scan_backend)
     if x.ndim != 3 or x.shape[-1] != module.width:
         raise ValueError(f"SPARCMixer expects [B, L, {module.width}] inputs")
+    if use_fused(x, module.modes):
+        y, last = fused_sequence(module, x)
+        return y, (last if return_cache else None)
     eta, delta, write_r, write_i = make_scan_inputs(module, x)
     y, last = chunk_scan("p1", eta, delta, write_r, write_i, module.nu_log, module.theta_log,
                          relu_output=True)

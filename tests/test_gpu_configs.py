@@ -35,12 +35,14 @@ def group_modes(groups, gs):
 # ---------------------------------------------------------------------------
 # cfg1: one SPARC layer, B=2, T=256, d_model=64, N=16 (M=1024, width 2048), fp32
 # ---------------------------------------------------------------------------
+@pytest.mark.parametrize("path", ["fused", "composed"])
 @pytest.mark.parametrize("controller", [False, True], ids=["lti", "controller_on"])
-def test_cfg1_layer_fwd_bwd(controller):
+def test_cfg1_layer_fwd_bwd(controller, path):
     """|a| = exp(-nu) in [0.9, 0.999] (nu = -log r, r ~ U[0.9, 0.999]), theta
     = 2 pi U (the module's init, == U(-pi, pi) mod 2 pi); eta = delta = 0 with
     the default zero directions, or random directions (controller on)."""
-    print(f"[case] cfg1 controller={controller}", flush=True)
+    print(f"[case] cfg1 controller={controller} path={path}", flush=True)
+    sparc_amd.set_mixer_path(path)
     B, T, D, N = 2, 256, 64, 16
     M = D * N
     width = 2 * M
@@ -79,6 +81,7 @@ def test_cfg1_layer_fwd_bwd(controller):
     yo, lasto = O.mixer_forward(p, xo, return_cache=True)
     lo = (yo * dy).sum() + lasto[0].sum() + lasto[1].sum()
     grads_o = torch.autograd.grad(lo, [xo] + [getattr(p, n) for n in names])
+    sparc_amd.set_mixer_path("auto")
     assert rel_err(y, yo) <= 1e-4
     assert rel_err(cache[0], lasto[0]) <= 1e-4 and rel_err(cache[1], lasto[1]) <= 1e-4
     for n, a, b in zip(["x"] + names, grads, grads_o):

@@ -19,6 +19,14 @@ NAMES = ["nu_log", "theta_log", "phase_direction", "radial_direction", "write_lo
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "p1_eager_golden.npz")
 
 
+@pytest.fixture(params=["fused", "composed"])
+def mixer_path(request):
+    """Runs a module test on the fused sequence path and on the composed one."""
+    sparc_amd.set_mixer_path(request.param)
+    yield request.param
+    sparc_amd.set_mixer_path("auto")
+
+
 def rel_err(got, ref):
     got, ref = got.detach().double().cpu(), ref.detach().double().cpu()
     return (got - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
@@ -58,8 +66,8 @@ def _masked_dy(p, x, dy, band):
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
 @pytest.mark.parametrize("B,L,width", [(2, 256, 128), (2, 100, 64)])
-def test_mixer_forward_backward_parity(dtype, tol, B, L, width):
-    print(f"[case] mixer B={B} L={L} width={width} {dtype}", flush=True)
+def test_mixer_forward_backward_parity(dtype, tol, B, L, width, mixer_path):
+    print(f"[case] mixer B={B} L={L} width={width} {dtype} path={mixer_path}", flush=True)
     m = make_module(width, seed=7).cuda()
     g = torch.Generator().manual_seed(3)
     x64 = torch.randn(B, L, width, generator=g, dtype=torch.float64)
@@ -89,9 +97,9 @@ def test_mixer_forward_backward_parity(dtype, tol, B, L, width):
         assert e <= tol, f"grad {name}: {e:.3g}"
 
 
-def test_mixer_matches_reference_golden():
+def test_mixer_matches_reference_golden(mixer_path):
     """The HIP module on the reference's own golden inputs (fp32 I/O)."""
-    print("[case] golden", flush=True)
+    print(f"[case] golden path={mixer_path}", flush=True)
     with np.load(GOLDEN, allow_pickle=False) as z:
         gd = {k: torch.from_numpy(z[k]) for k in z.files}
     width = gd["x"].shape[-1]
@@ -226,3 +234,59 @@ def test_prepared_decode_matches_single_kernel_and_tracks_updates(dtype):
         assert rel_err(s1[0], s2[0]) <= 1e-5 and rel_err(s1[1], s2[1]) <= 1e-5
         # outputs in bf16 may differ by one rounding step
         assert rel_err(y1, y2) <= (1e-5 if dtype == torch.float32 else 2.0 ** -7)
+
+
+@pytest.mark.parametrize("B,L,width,dtype,tol", [
+    (16, 21, 16384, torch.bfloat16, 2e-2),   # two modes per lane in the forward (>= 1024 chains)
+    (3, 45, 200, torch.float32, 1e-4),       # a partial mode block (M = 100), ragged L
+    (2, 9, 8, torch.float32, 1e-4),          # M = 4, one block of steps plus one
+])
+def test_fused_mixer_shapes(B, L, width, dtype, tol):
+    """The fused sequence path against the oracle on the shapes its kernels
+    special-case: two modes per lane, lanes past M, the last block of steps."""
+    print(f"[case] fused mixer B={B} L={L} width={width} {dtype}", flush=True)
+    sparc_amd.set_mixer_path("fused")
+    try:
+        m = make_module(width, seed=11).cuda()
+        g = torch.Generator().manual_seed(12)
+        x_in = torch.randn(B, L, width, generator=g, dtype=torch.float64).to(dtype)
+        p = oracle_params(m)
+        dy = _masked_dy(p, x_in.double(), torch.randn(B, L, width, generator=g, dtype=torch.float64),
+                        band=1e-3 if dtype == torch.float32 else 2e-2)
+        dl = torch.randn(B, width // 2, generator=g, dtype=torch.float64)
+        x = x_in.cuda().requires_grad_()
+        y, cache = m(x, return_cache=True)
+        loss = (y.float() * dy.cuda().float()).sum() + (cache[0] * dl.cuda().float()).sum()
+        grads = torch.autograd.grad(loss, [x] + [getattr(m, n) for n in NAMES])
+        xo = x_in.double().clone().requires_grad_()
+        yo, lasto = O.mixer_forward(p, xo, return_cache=True)
+        lo = (yo * dy).sum() + (lasto[0] * dl).sum()
+        grads_o = torch.autograd.grad(lo, [xo] + [getattr(p, n) for n in NAMES])
+        assert rel_err(y, yo) <= tol
+        assert rel_err(cache[0], lasto[0]) <= tol and rel_err(cache[1], lasto[1]) <= tol
+        for name, a, b in zip(["x"] + NAMES, grads, grads_o):
+            e = rel_err(a, b)
+            assert e <= tol, f"grad {name}: {e:.3g}"
+    finally:
+        sparc_amd.set_mixer_path("auto")
+
+
+def test_fused_mixer_deterministic():
+    """Two fused forward+backward passes give bit-identical outputs and
+    gradients (fixed-order reductions, no atomics)."""
+    print("[case] fused mixer determinism", flush=True)
+    sparc_amd.set_mixer_path("fused")
+    try:
+        m = make_module(512, seed=3).cuda()
+        x = torch.randn(4, 77, 512, device="cuda", dtype=torch.bfloat16)
+        dy = torch.randn_like(x)
+        outs = []
+        for _ in range(2):
+            xx = x.clone().requires_grad_()
+            y, _ = m(xx)
+            grads = torch.autograd.grad((y.float() * dy.float()).sum(), [xx] + [getattr(m, n) for n in NAMES])
+            outs.append([y] + list(grads))
+        for a, b in zip(*outs):
+            assert torch.equal(a, b)
+    finally:
+        sparc_amd.set_mixer_path("auto")
