@@ -252,18 +252,17 @@ __device__ __forceinline__ void sincos_quarter(float x, float& s, float& c) {
   c = fmaf(pc, x2, 1.0f);
 }
 
-// expm1(x) for x <= 0 to ~1e-7 relative: Taylor series (8 terms) near 0,
-// exp(x) - 1 further out (no cancellation there)
+// expm1(x) for x <= 0: the Taylor series to x^5/5! for |x| < 1/16 (relative
+// error < 2e-9), exp(x) - 1 beyond (relative error < 1e-6: no cancellation
+// left to amplify the exponential's rounding)
 __device__ __forceinline__ float expm1_nonpos(float x) {
-  float p = 1.0f / 5040.0f;
-  p = fmaf(p, x, 1.0f / 720.0f);
-  p = fmaf(p, x, 1.0f / 120.0f);
+  float p = 1.0f / 120.0f;
   p = fmaf(p, x, 1.0f / 24.0f);
   p = fmaf(p, x, 1.0f / 6.0f);
   p = fmaf(p, x, 0.5f);
   p = fmaf(p, x, 1.0f);
   p *= x;
-  return x > -0.25f ? p : fast_exp(x) - 1.0f;
+  return x > -0.0625f ? p : fast_exp(x) - 1.0f;
 }
 
 // sin and cos of |u| <= pi/2 by Taylor series to x^11 / x^12 (error < 6e-8)
@@ -284,10 +283,11 @@ __device__ __forceinline__ void sincos_half(float u, float& s, float& c) {
   c = fmaf(pc, u2, 1.0f);
 }
 
-// tanh through one hardware exponential and reciprocal (absolute error ~1e-7)
+// tanh(x) = 1 - 2 / (1 + e^{2x}) through one hardware exponential and
+// reciprocal (absolute error ~1e-7; saturates to +-1 through e^{2x} = inf / 0)
 __device__ __forceinline__ float tanh_fast(float x) {
-  const float e = fast_exp(-2.0f * fabsf(x));
-  return copysignf((1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e), x);
+  const float e = fast_exp(2.0f * x);
+  return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f);
 }
 
 // sin and cos for moderate |x| (gate phases, a few multiples of pi):

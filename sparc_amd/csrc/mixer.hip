@@ -710,15 +710,19 @@ bool al(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) =
 #ifndef SPARC_MIXER_BWD_V
 #define SPARC_MIXER_BWD_V 1
 #endif
-// Forward: 2 when that still leaves a wave per SIMD (1024 chains on the
-// 256-CU MI355X), else 1 (twice the chains).  Backward: the fixed choice
-// (its per-step working set is twice the forward's).
+// Forward: 2 when that leaves at least 1280 chains (1.25 waves per SIMD of the
+// 256-CU MI355X), else 1 (twice the chains).  Measured at B=8, M=16384 (1024
+// chains of 2): 1 mode per lane 2.3 ms against 2.8 ms; at B=16, M=12288 (1536
+// chains of 2): 2 modes 1.4 ms against 1.5 ms.  The forward is VALU-bound:
+// more resident waves hide the latency of its dependent arithmetic.
+// Backward: the fixed choice (its per-step working set is twice the
+// forward's).
 int mixer_v(int64_t B, int64_t M, int direction) {
   const int fixed = direction == 0 ? SPARC_MIXER_FWD_V : SPARC_MIXER_BWD_V;
   if (fixed == 1 || M % 2) return 1;
   if (fixed == 2) return 2;
   const int64_t chains2 = B * ((M + 127) / 128);
-  return chains2 >= 1024 ? 2 : 1;
+  return chains2 >= 1280 ? 2 : 1;
 }
 
 struct Layout {
