@@ -224,6 +224,50 @@ def bench_cfg3(args, dev):
     }
 
 
+def bench_cfg5(args, dev):
+    """cfg5: a 12-layer stack of SPARC blocks (RMSNorm -> Linear(768 -> 2M) ->
+    SPARCMixer -> Linear(2M -> 768), residual; M = 768*16 = 12288), bf16
+    weights and activations, B=16, T=2048, token embeddings ~ N(0, 1).  One
+    step = forward, backward (loss: mean square of the output) and an AdamW
+    update.  The projections are 6 * tokens * 12 * 2 * 768 * 24576 = 89.1
+    TFLOP per step (hipBLASLt GEMMs through torch); the mixers run the fused
+    HIP sequence path."""
+    from sparc_amd.stack import SPARCStack
+    L, d_model, N, B, T = 12, 768, 16, 16, 2048
+    torch.manual_seed(0)
+    model = SPARCStack(L, d_model, N).to(dev).to(torch.bfloat16)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, foreach=True)
+    x = torch.randn(B, T, d_model, device=dev, dtype=torch.bfloat16)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        loss = model(x).float().square().mean()
+        loss.backward()
+        opt.step()
+        return loss
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize(dev)
+    steps = 3
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize(dev)
+    elapsed = time.perf_counter() - t0
+    if not math.isfinite(loss.item()):
+        raise RuntimeError("cfg5: non-finite loss")
+    ms = elapsed * 1e3 / steps
+    flop = 6.0 * B * T * L * 2 * d_model * 2 * d_model * N
+    del model, opt, x
+    torch.cuda.empty_cache()
+    return {"workload": "12 SPARC blocks (RMSNorm, Linear 768->24576, SPARCMixer, Linear 24576->768), "
+                        "fwd + bwd + AdamW", "layers": L, "d_model": d_model, "N": N, "B": B, "T": T,
+            "dtype": "bf16", "steps": steps, "ms_per_step": round(ms, 2),
+            "tokens_per_s": round(B * T / (ms * 1e-3), 1), "gemm_tflop_per_step": round(flop / 1e12, 1),
+            "model_tflops": round(flop / (ms * 1e-3) / 1e12, 1)}
+
+
 def _graph_time_us(dev, n_graph, reps, step_fn):
     """Captures reps HIP graphs of n_graph calls step_fn(i) (i = global step)
     after one eager call, replays them all once untimed and once timed;
@@ -361,6 +405,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cfg3", action="store_true", help="skip the cfg3 (real, T=65536) report")
+    ap.add_argument("--no-cfg5", action="store_true", help="skip the cfg5 (12-layer stack) report")
     ap.add_argument("--algo", default="auto", choices=["auto", "serial", "chain", "lookback"],
                     help="scan algorithm (auto picks the serial kernels at this shape)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -384,6 +429,7 @@ def main():
         del src, dst
     res = bench_scan(args, dev)
     cfg3 = None if args.no_cfg3 else bench_cfg3(args, dev)
+    cfg5 = None if args.no_cfg5 else bench_cfg5(args, dev)
     core = None if args.no_decode else bench_decode_core(args, dev)
     dec = None if args.no_decode else bench_decode(args, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
@@ -434,6 +480,7 @@ def main():
                 "steps": dec["steps"], "bytes_per_step": dec["bytes_per_step"], "GB_s": round(dec["gbs"], 1),
                 "form": "SPARCMixer.step (P1 controls and write from x), bf16 x/y, fp32 state in place"}},
         "cfg3": cfg3,
+        "cfg5": cfg5,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
