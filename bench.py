@@ -37,6 +37,7 @@ import torch
 HBM_PEAK_GBS = 8000.0
 ROOT = os.path.dirname(os.path.abspath(__file__))
 TRAFFIC_FILE = os.path.join("profiles", "scan_cfg2_hbm_traffic.md")
+TRAFFIC_FILE_CFG3 = os.path.join("profiles", "scan_cfg3_hbm_traffic.md")
 # kernels each algorithm runs at this shape (backward, forward)
 ALGO_KERNELS = {"auto": ("chain_bwd_serial_kernel", "chain_fwd_serial_kernel"),
                 "serial": ("chain_bwd_serial_kernel", "chain_fwd_serial_kernel"),
@@ -44,13 +45,13 @@ ALGO_KERNELS = {"auto": ("chain_bwd_serial_kernel", "chain_fwd_serial_kernel"),
                 "lookback": ("scan_bwd_kernel", "scan_fwd_kernel")}
 
 
-def measured_traffic() -> dict:
-    """HBM bytes per launch by kernel name, from the committed rocprofv3
+def measured_traffic(path: str = TRAFFIC_FILE) -> dict:
+    """HBM bytes per launch by kernel name, from a committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary (calibrated against a 1 GiB copy); empty
     if the file is absent."""
     out = {}
     try:
-        with open(os.path.join(ROOT, TRAFFIC_FILE)) as f:
+        with open(os.path.join(ROOT, path)) as f:
             for line in f:
                 parts = line.split()
                 if len(parts) == 3 and parts[0] == "traffic":
@@ -210,17 +211,19 @@ def bench_cfg3(args, dev):
     bytes_bwd = B * T * (12 * M + 8 * G)
     ms_step = elapsed * 1e3 / steps
     del a, w, dy, y, dw, da, cs
+    traffic = measured_traffic(TRAFFIC_FILE_CFG3)
     return {
         "workload": "real scan fwd+bwd, fp32, gates shared by the N=8 states of a channel",
         "B": B, "T": T, "D": D, "N": N, "M": M, "G": G, "steps": steps,
         "tokens_per_s": round(B * T * steps / elapsed, 1), "ms_per_step": round(ms_step, 4),
         "step_frac": round((bytes_fwd + bytes_bwd) / ms_step / 1e6 / HBM_PEAK_GBS, 4),
         "forward": {"kernel": "scan_fwd_kernel (look-back)", "avg_launch_ms": round(fwd_ms, 4),
-                    "bytes_per_launch": bytes_fwd,
+                    "bytes_per_launch": bytes_fwd, "traffic": traffic.get("scan_fwd_kernel"),
                     "frac": round(bytes_fwd / fwd_ms / 1e6 / HBM_PEAK_GBS, 4)},
         "backward": {"kernel": "scan_bwd_kernel (look-back, saved output)", "avg_launch_ms": round(bwd_ms, 4),
-                     "bytes_per_launch": bytes_bwd,
+                     "bytes_per_launch": bytes_bwd, "traffic": traffic.get("scan_bwd_kernel"),
                      "frac": round(bytes_bwd / bwd_ms / 1e6 / HBM_PEAK_GBS, 4)},
+        "traffic_source": TRAFFIC_FILE_CFG3 if traffic else None,
     }
 
 
