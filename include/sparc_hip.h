@@ -331,6 +331,35 @@ sparc_status sparc_mixer_forward(int64_t batch, int64_t length, int64_t modes, i
                                  float* last_re, float* last_im, void* workspace, size_t workspace_bytes,
                                  sparc_stream_t stream);
 
+/* The forward's scan alone, with the controls given: eta, delta [B*T] fp32
+ * are inputs (a caller that has them more cheaply, e.g. folded into the
+ * projection that produces x, skips the two dot products over x).  Outputs
+ * as sparc_mixer_forward.  Replaces _SPARCChunkScan.forward with the write
+ * and epilogue fused (sparc-kernal/backward/scan.py:1126-1372,
+ * forward/control.py:141-195, forward/scan.py:1598-1603). */
+sparc_status sparc_mixer_scan_forward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                                      const void* x, const float* eta, const float* delta, const float* nu_log,
+                                      const float* theta_log, const float* write_log_gain,
+                                      const float* write_phase_response, const float* write_radial_response,
+                                      void* y, void* h_re, void* h_im, float* last_re, float* last_im,
+                                      void* workspace, size_t workspace_bytes, sparc_stream_t stream);
+
+/* The backward of sparc_mixer_scan_forward: dx [B,T,2M] (io_dtype) through
+ * the write only, deta, ddelta [B*T] fp32 (the gradients of the controls)
+ * and the five parameter gradients [M] fp32 (overwritten); the controls'
+ * own backward is the caller's.  Workspace: sparc_mixer_workspace_bytes(...,
+ * 1).  Replaces _SPARCChunkScan.backward (sparc-kernal/backward/scan.py:
+ * 1375-1640) and _LatestSPARCWrite.backward (backward/control.py:92-129). */
+sparc_status sparc_mixer_scan_backward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                                       const void* x, const float* eta, const float* delta, const float* nu_log,
+                                       const float* theta_log, const float* write_log_gain,
+                                       const float* write_phase_response, const float* write_radial_response,
+                                       const void* h_re, const void* h_im, const void* dy, const float* dlast_re,
+                                       const float* dlast_im, void* dx, float* deta, float* ddelta, float* dnu_log,
+                                       float* dtheta_log, float* dwrite_log_gain, float* dwrite_phase_response,
+                                       float* dwrite_radial_response, void* workspace, size_t workspace_bytes,
+                                       sparc_stream_t stream);
+
 /* dy [B,T,2M] (io_dtype): the gradient of y; dlast_re, dlast_im [B,M] fp32:
  * of the last state (both NULL: zero).  eta, delta, h_re, h_im as the
  * forward wrote them.  Writes dx [B,T,2M] (io_dtype) and, overwriting, the

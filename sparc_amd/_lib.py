@@ -44,6 +44,8 @@ EXPORTED_SYMBOLS = (
     "sparc_mixer_workspace_bytes",
     "sparc_mixer_forward",
     "sparc_mixer_backward",
+    "sparc_mixer_scan_forward",
+    "sparc_mixer_scan_backward",
     "sparc_last_error",
     "sparc_version",
 )
@@ -119,6 +121,10 @@ def load() -> ctypes.CDLL:
         lib.sparc_mixer_forward.restype = ctypes.c_int
         lib.sparc_mixer_backward.argtypes = [_I64, _I64, _I64, _I32] + [_P] * 24 + [_SZ, _P]
         lib.sparc_mixer_backward.restype = ctypes.c_int
+        lib.sparc_mixer_scan_forward.argtypes = [_I64, _I64, _I64, _I32] + [_P] * 14 + [_SZ, _P]
+        lib.sparc_mixer_scan_forward.restype = ctypes.c_int
+        lib.sparc_mixer_scan_backward.argtypes = [_I64, _I64, _I64, _I32] + [_P] * 22 + [_SZ, _P]
+        lib.sparc_mixer_scan_backward.restype = ctypes.c_int
         lib.sparc_last_error.argtypes = []
         lib.sparc_last_error.restype = ctypes.c_char_p
         lib.sparc_version.argtypes = []

@@ -778,37 +778,17 @@ template <typename IO, int V>
 void launch_bwd(const Args& a, hipStream_t st) {
   hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, SPARC_MIXER_BWD_S>), dim3(static_cast<unsigned>(a.B) * a.n_mb), dim3(64), 0, st, a);
 }
-}  // namespace
 
-extern "C" {
-
-size_t sparc_mixer_workspace_bytes(int64_t batch, int64_t length, int64_t modes, int direction) {
-  if (batch <= 0 || length < 0 || modes <= 0 || modes % 4 || (direction != 0 && direction != 1)) return 0;
-  return layout(batch, length, modes, direction).total;
-}
-
-sparc_status sparc_mixer_forward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
-                                 const void* x, const float* phase_direction, const float* radial_direction,
-                                 const float* nu_log, const float* theta_log, const float* write_log_gain,
-                                 const float* write_phase_response, const float* write_radial_response,
-                                 float* eta, float* delta, void* y, void* h_re, void* h_im,
-                                 float* last_re, float* last_im, void* workspace, size_t workspace_bytes,
-                                 sparc_stream_t stream) {
-  if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
-  if (!x || !phase_direction || !radial_direction || !nu_log || !theta_log || !write_log_gain ||
-      !write_phase_response || !write_radial_response || !eta || !delta || !y || !h_re || !h_im)
-    return fail(SPARC_EINVAL, "mixer forward: NULL pointer");
-  if ((last_re == nullptr) != (last_im == nullptr)) return fail(SPARC_EINVAL, "mixer forward: last_re/last_im");
-  const Layout l = layout(batch, length, modes, 0);
-  if (!workspace || workspace_bytes < l.total)
-    return fail(SPARC_EWORKSPACE, "mixer forward: workspace too small (%zu < %zu)", workspace_bytes, l.total);
-  const size_t esz = io_dtype == SPARC_BF16 ? 2 : 4;
-  if (!al(x, 16) || !al(y, 16) || !al(h_re, esz * l.V) || !al(h_im, esz * l.V) || !al(phase_direction, 16) ||
-      !al(radial_direction, 16) || !al(workspace, 256))
-    return fail(SPARC_EINVAL, "mixer forward: misaligned tensor");
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int M = static_cast<int>(modes), W = 2 * M;
-  float* consts = reinterpret_cast<float*>(static_cast<char*>(workspace) + l.consts);
+// The scan and its backward with the controls given; the per-mode constants
+// are built in the workspace first.  Shapes, pointers and the workspace are
+// checked by the callers.
+sparc_status scan_forward_impl(const Layout& l, int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                               const void* x, const float* eta, const float* delta, const float* nu_log,
+                               const float* theta_log, const float* write_log_gain,
+                               const float* write_phase_response, const float* write_radial_response, void* y,
+                               void* h_re, void* h_im, float* last_re, float* last_im, char* ws, hipStream_t st) {
+  const int M = static_cast<int>(modes);
+  float* consts = reinterpret_cast<float*>(ws + l.consts);
   hipLaunchKernelGGL(mixer_prepare_kernel, dim3(static_cast<unsigned>((M + 255) / 256)), dim3(256), 0, st, M, nu_log,
                      theta_log, write_log_gain, write_phase_response, write_radial_response, consts);
   if (length == 0) {  // the state stays 0
@@ -818,73 +798,45 @@ sparc_status sparc_mixer_forward(int64_t batch, int64_t length, int64_t modes, i
       hipLaunchKernelGGL(fill_zero_f32_kernel, g, dim3(256), 0, st, last_re, n);
       hipLaunchKernelGGL(fill_zero_f32_kernel, g, dim3(256), 0, st, last_im, n);
     }
-    hipError_t e = hipGetLastError();
-    return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer forward: %s", hipGetErrorString(e));
-  }
-  const dim3 gc(static_cast<unsigned>((l.R + kCtrlRows - 1) / kCtrlRows));
-  if (io_dtype == SPARC_BF16)
-    hipLaunchKernelGGL(ctrl_fwd_kernel<sparc::bf16>, gc, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction, eta, delta);
-  else
-    hipLaunchKernelGGL(ctrl_fwd_kernel<float>, gc, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction, eta, delta);
-  Args a{};
-  a.B = static_cast<int>(batch);
-  a.T = static_cast<int>(length);
-  a.M = M;
-  a.n_mb = l.n_mb;
-  a.x = x; a.consts = consts; a.eta = eta; a.delta = delta;
-  a.y = y; a.h_re = h_re; a.h_im = h_im; a.last_re = last_re; a.last_im = last_im;
-  if (io_dtype == SPARC_BF16) {
-    if (l.V == 2) launch_fwd<sparc::bf16, 2>(a, st); else launch_fwd<sparc::bf16, 1>(a, st);
   } else {
-    if (l.V == 2) launch_fwd<float, 2>(a, st); else launch_fwd<float, 1>(a, st);
+    Args a{};
+    a.B = static_cast<int>(batch);
+    a.T = static_cast<int>(length);
+    a.M = M;
+    a.n_mb = l.n_mb;
+    a.x = x; a.consts = consts; a.eta = eta; a.delta = delta;
+    a.y = y; a.h_re = h_re; a.h_im = h_im; a.last_re = last_re; a.last_im = last_im;
+    if (io_dtype == SPARC_BF16) {
+      if (l.V == 2) launch_fwd<sparc::bf16, 2>(a, st); else launch_fwd<sparc::bf16, 1>(a, st);
+    } else {
+      if (l.V == 2) launch_fwd<float, 2>(a, st); else launch_fwd<float, 1>(a, st);
+    }
   }
   hipError_t e = hipGetLastError();
-  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer forward: %s", hipGetErrorString(e));
+  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer scan forward: %s", hipGetErrorString(e));
 }
 
-sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
-                                  const void* x, const float* phase_direction, const float* radial_direction,
-                                  const float* nu_log, const float* theta_log, const float* write_log_gain,
-                                  const float* write_phase_response, const float* write_radial_response,
-                                  const float* eta, const float* delta, const void* h_re, const void* h_im,
-                                  const void* dy, const float* dlast_re, const float* dlast_im, void* dx,
-                                  float* dphase_direction, float* dradial_direction, float* dnu_log,
-                                  float* dtheta_log, float* dwrite_log_gain, float* dwrite_phase_response,
-                                  float* dwrite_radial_response, void* workspace, size_t workspace_bytes,
-                                  sparc_stream_t stream) {
-  if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
-  if (!x || !phase_direction || !radial_direction || !nu_log || !theta_log || !write_log_gain ||
-      !write_phase_response || !write_radial_response || !eta || !delta || !h_re || !h_im || !dy || !dx ||
-      !dphase_direction || !dradial_direction || !dnu_log || !dtheta_log || !dwrite_log_gain ||
-      !dwrite_phase_response || !dwrite_radial_response)
-    return fail(SPARC_EINVAL, "mixer backward: NULL pointer");
-  if ((dlast_re == nullptr) != (dlast_im == nullptr)) return fail(SPARC_EINVAL, "mixer backward: dlast_re/dlast_im");
-  const Layout l = layout(batch, length, modes, 1);
-  if (!workspace || workspace_bytes < l.total)
-    return fail(SPARC_EWORKSPACE, "mixer backward: workspace too small (%zu < %zu)", workspace_bytes, l.total);
-  const size_t esz = io_dtype == SPARC_BF16 ? 2 : 4;
-  if (!al(x, 16) || !al(dy, 16) || !al(dx, 16) || !al(h_re, esz * l.V) || !al(h_im, esz * l.V) ||
-      !al(phase_direction, 16) || !al(radial_direction, 16) || !al(workspace, 256))
-    return fail(SPARC_EINVAL, "mixer backward: misaligned tensor");
+sparc_status scan_backward_impl(const Layout& l, int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                                const void* x, const float* eta, const float* delta, const float* nu_log,
+                                const float* theta_log, const float* write_log_gain,
+                                const float* write_phase_response, const float* write_radial_response,
+                                const void* h_re, const void* h_im, const void* dy, const float* dlast_re,
+                                const float* dlast_im, void* dx, float* deta, float* ddelta, float* dnu_log,
+                                float* dtheta_log, float* dwrite_log_gain, float* dwrite_phase_response,
+                                float* dwrite_radial_response, char* ws, sparc_stream_t stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int M = static_cast<int>(modes), W = 2 * M;
-  char* ws = static_cast<char*>(workspace);
+  const int M = static_cast<int>(modes);
   float* consts = reinterpret_cast<float*>(ws + l.consts);
   float* part_tok = reinterpret_cast<float*>(ws + l.part_tok);
-  float* tok = reinterpret_cast<float*>(ws + l.tok);
   float* part_mode = reinterpret_cast<float*>(ws + l.part_mode);
-  float* pd = reinterpret_cast<float*>(ws + l.pd);
-  float* pbias = reinterpret_cast<float*>(ws + l.pbias);
+  float* outs[5] = {dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response};
   hipLaunchKernelGGL(mixer_prepare_kernel, dim3(static_cast<unsigned>((M + 255) / 256)), dim3(256), 0, st, M, nu_log,
                      theta_log, write_log_gain, write_phase_response, write_radial_response, consts);
   if (length == 0) {
-    const dim3 gz(static_cast<unsigned>((W + 1 + 255) / 256)), gm(static_cast<unsigned>((M + 255) / 256));
-    for (float* o : {dphase_direction, dradial_direction})
-      hipLaunchKernelGGL(fill_zero_f32_kernel, gz, dim3(256), 0, st, o, static_cast<int64_t>(W + 1));
-    for (float* o : {dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response})
-      hipLaunchKernelGGL(fill_zero_f32_kernel, gm, dim3(256), 0, st, o, static_cast<int64_t>(M));
+    const dim3 gm(static_cast<unsigned>((M + 255) / 256));
+    for (float* o : outs) hipLaunchKernelGGL(fill_zero_f32_kernel, gm, dim3(256), 0, st, o, static_cast<int64_t>(M));
     hipError_t e = hipGetLastError();
-    return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(e));
+    return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer scan backward: %s", hipGetErrorString(e));
   }
   Args a{};
   a.B = static_cast<int>(batch);
@@ -900,14 +852,153 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
   } else {
     if (l.V == 2) launch_bwd<float, 2>(a, st); else launch_bwd<float, 1>(a, st);
   }
-  float* deta = tok;
-  float* ddelta = tok + l.R;
   hipLaunchKernelGGL(token_sum_kernel, dim3(static_cast<unsigned>((l.R + 255) / 256)), dim3(256), 0, st, l.R, l.n_mb,
                      part_tok, deta, ddelta);
-  float* outs[5] = {dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response};
   for (int p = 0; p < 5; ++p)
     if (sparc_status s = sparc_column_sum(batch, modes, part_mode + static_cast<int64_t>(p) * batch * modes, outs[p], 0, stream))
       return s;
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer scan backward: %s", hipGetErrorString(e));
+}
+
+bool params_ok(const float* a, const float* b, const float* c, const float* d, const float* e) {
+  return a && b && c && d && e;
+}
+}  // namespace
+
+extern "C" {
+
+size_t sparc_mixer_workspace_bytes(int64_t batch, int64_t length, int64_t modes, int direction) {
+  if (batch <= 0 || length < 0 || modes <= 0 || modes % 4 || (direction != 0 && direction != 1)) return 0;
+  return layout(batch, length, modes, direction).total;
+}
+
+sparc_status sparc_mixer_scan_forward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                                      const void* x, const float* eta, const float* delta, const float* nu_log,
+                                      const float* theta_log, const float* write_log_gain,
+                                      const float* write_phase_response, const float* write_radial_response,
+                                      void* y, void* h_re, void* h_im, float* last_re, float* last_im,
+                                      void* workspace, size_t workspace_bytes, sparc_stream_t stream) {
+  if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
+  if (!x || !eta || !delta || !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response) ||
+      !y || !h_re || !h_im)
+    return fail(SPARC_EINVAL, "mixer scan forward: NULL pointer");
+  if ((last_re == nullptr) != (last_im == nullptr)) return fail(SPARC_EINVAL, "mixer scan forward: last_re/last_im");
+  const Layout l = layout(batch, length, modes, 0);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(SPARC_EWORKSPACE, "mixer scan forward: workspace too small (%zu < %zu)", workspace_bytes, l.total);
+  const size_t esz = io_dtype == SPARC_BF16 ? 2 : 4;
+  if (!al(x, 16) || !al(y, 16) || !al(h_re, esz * l.V) || !al(h_im, esz * l.V) || !al(workspace, 256))
+    return fail(SPARC_EINVAL, "mixer scan forward: misaligned tensor");
+  return scan_forward_impl(l, batch, length, modes, io_dtype, x, eta, delta, nu_log, theta_log, write_log_gain,
+                           write_phase_response, write_radial_response, y, h_re, h_im, last_re, last_im,
+                           static_cast<char*>(workspace), reinterpret_cast<hipStream_t>(stream));
+}
+
+sparc_status sparc_mixer_forward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                                 const void* x, const float* phase_direction, const float* radial_direction,
+                                 const float* nu_log, const float* theta_log, const float* write_log_gain,
+                                 const float* write_phase_response, const float* write_radial_response,
+                                 float* eta, float* delta, void* y, void* h_re, void* h_im,
+                                 float* last_re, float* last_im, void* workspace, size_t workspace_bytes,
+                                 sparc_stream_t stream) {
+  if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
+  if (!x || !phase_direction || !radial_direction ||
+      !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response) || !eta ||
+      !delta || !y || !h_re || !h_im)
+    return fail(SPARC_EINVAL, "mixer forward: NULL pointer");
+  if ((last_re == nullptr) != (last_im == nullptr)) return fail(SPARC_EINVAL, "mixer forward: last_re/last_im");
+  const Layout l = layout(batch, length, modes, 0);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(SPARC_EWORKSPACE, "mixer forward: workspace too small (%zu < %zu)", workspace_bytes, l.total);
+  const size_t esz = io_dtype == SPARC_BF16 ? 2 : 4;
+  if (!al(x, 16) || !al(y, 16) || !al(h_re, esz * l.V) || !al(h_im, esz * l.V) || !al(phase_direction, 16) ||
+      !al(radial_direction, 16) || !al(workspace, 256))
+    return fail(SPARC_EINVAL, "mixer forward: misaligned tensor");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int W = 2 * static_cast<int>(modes);
+  if (length > 0) {
+    const dim3 gc(static_cast<unsigned>((l.R + kCtrlRows - 1) / kCtrlRows));
+    if (io_dtype == SPARC_BF16)
+      hipLaunchKernelGGL(ctrl_fwd_kernel<sparc::bf16>, gc, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction, eta, delta);
+    else
+      hipLaunchKernelGGL(ctrl_fwd_kernel<float>, gc, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction, eta, delta);
+  }
+  return scan_forward_impl(l, batch, length, modes, io_dtype, x, eta, delta, nu_log, theta_log, write_log_gain,
+                           write_phase_response, write_radial_response, y, h_re, h_im, last_re, last_im,
+                           static_cast<char*>(workspace), st);
+}
+
+sparc_status sparc_mixer_scan_backward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                                       const void* x, const float* eta, const float* delta, const float* nu_log,
+                                       const float* theta_log, const float* write_log_gain,
+                                       const float* write_phase_response, const float* write_radial_response,
+                                       const void* h_re, const void* h_im, const void* dy, const float* dlast_re,
+                                       const float* dlast_im, void* dx, float* deta, float* ddelta, float* dnu_log,
+                                       float* dtheta_log, float* dwrite_log_gain, float* dwrite_phase_response,
+                                       float* dwrite_radial_response, void* workspace, size_t workspace_bytes,
+                                       sparc_stream_t stream) {
+  if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
+  if (!x || !eta || !delta || !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response) ||
+      !h_re || !h_im || !dy || !dx || !deta || !ddelta ||
+      !params_ok(dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response))
+    return fail(SPARC_EINVAL, "mixer scan backward: NULL pointer");
+  if ((dlast_re == nullptr) != (dlast_im == nullptr)) return fail(SPARC_EINVAL, "mixer scan backward: dlast_re/dlast_im");
+  const Layout l = layout(batch, length, modes, 1);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(SPARC_EWORKSPACE, "mixer scan backward: workspace too small (%zu < %zu)", workspace_bytes, l.total);
+  const size_t esz = io_dtype == SPARC_BF16 ? 2 : 4;
+  if (!al(x, 16) || !al(dy, 16) || !al(dx, 16) || !al(h_re, esz * l.V) || !al(h_im, esz * l.V) || !al(workspace, 256))
+    return fail(SPARC_EINVAL, "mixer scan backward: misaligned tensor");
+  return scan_backward_impl(l, batch, length, modes, io_dtype, x, eta, delta, nu_log, theta_log, write_log_gain,
+                            write_phase_response, write_radial_response, h_re, h_im, dy, dlast_re, dlast_im, dx,
+                            deta, ddelta, dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response,
+                            dwrite_radial_response, static_cast<char*>(workspace), stream);
+}
+
+sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                                  const void* x, const float* phase_direction, const float* radial_direction,
+                                  const float* nu_log, const float* theta_log, const float* write_log_gain,
+                                  const float* write_phase_response, const float* write_radial_response,
+                                  const float* eta, const float* delta, const void* h_re, const void* h_im,
+                                  const void* dy, const float* dlast_re, const float* dlast_im, void* dx,
+                                  float* dphase_direction, float* dradial_direction, float* dnu_log,
+                                  float* dtheta_log, float* dwrite_log_gain, float* dwrite_phase_response,
+                                  float* dwrite_radial_response, void* workspace, size_t workspace_bytes,
+                                  sparc_stream_t stream) {
+  if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
+  if (!x || !phase_direction || !radial_direction ||
+      !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response) || !eta ||
+      !delta || !h_re || !h_im || !dy || !dx || !dphase_direction || !dradial_direction ||
+      !params_ok(dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response))
+    return fail(SPARC_EINVAL, "mixer backward: NULL pointer");
+  if ((dlast_re == nullptr) != (dlast_im == nullptr)) return fail(SPARC_EINVAL, "mixer backward: dlast_re/dlast_im");
+  const Layout l = layout(batch, length, modes, 1);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(SPARC_EWORKSPACE, "mixer backward: workspace too small (%zu < %zu)", workspace_bytes, l.total);
+  const size_t esz = io_dtype == SPARC_BF16 ? 2 : 4;
+  if (!al(x, 16) || !al(dy, 16) || !al(dx, 16) || !al(h_re, esz * l.V) || !al(h_im, esz * l.V) ||
+      !al(phase_direction, 16) || !al(radial_direction, 16) || !al(workspace, 256))
+    return fail(SPARC_EINVAL, "mixer backward: misaligned tensor");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int M = static_cast<int>(modes), W = 2 * M;
+  char* ws = static_cast<char*>(workspace);
+  float* deta = reinterpret_cast<float*>(ws + l.tok);
+  float* ddelta = deta + l.R;
+  if (sparc_status s = scan_backward_impl(l, batch, length, modes, io_dtype, x, eta, delta, nu_log, theta_log,
+                                          write_log_gain, write_phase_response, write_radial_response, h_re, h_im,
+                                          dy, dlast_re, dlast_im, dx, deta, ddelta, dnu_log, dtheta_log,
+                                          dwrite_log_gain, dwrite_phase_response, dwrite_radial_response, ws, stream))
+    return s;
+  if (length == 0) {
+    const dim3 gz(static_cast<unsigned>((W + 1 + 255) / 256));
+    for (float* o : {dphase_direction, dradial_direction})
+      hipLaunchKernelGGL(fill_zero_f32_kernel, gz, dim3(256), 0, st, o, static_cast<int64_t>(W + 1));
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(e));
+  }
+  float* pd = reinterpret_cast<float*>(ws + l.pd);
+  float* pbias = reinterpret_cast<float*>(ws + l.pbias);
   const dim3 gb(static_cast<unsigned>((W + 2047) / 2048), static_cast<unsigned>(l.n_rb));
   if (io_dtype == SPARC_BF16)
     hipLaunchKernelGGL(ctrl_bwd_kernel<sparc::bf16>, gb, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction,

@@ -128,3 +128,110 @@ def fused_sequence(module, x: torch.Tensor):
     y, last_re, last_im = _FusedMixer.apply(
         x, *[getattr(module, n) for n in _PARAMS], module.energy_response)
     return y, (last_re, last_im)
+
+
+# ---------------------------------------------------------------------------
+# the mixer behind its input projection, with the controls folded into it
+# ---------------------------------------------------------------------------
+LOG16 = 2.772588722239781
+HALF_PI = 1.5707963267948966
+
+
+class _ProjectedMixer(torch.autograd.Function):
+    """y = SPARCMixer(xn @ W^T) for xn [B, L, D] and the projection W [2M, D].
+
+    The controls are p = x.u + b with x = xn W^T, i.e. p = xn (W^T u) + b: a
+    [B*L, D] x [D, 2] product instead of two dot products over the 2M-wide x.
+    Backward, the controls' input gradient dp0 u_phase + dp1 u_radial is a
+    rank-2 term that the projection's own gradients absorb as
+    d xn += dp (u W) and dW += u^T (dp^T xn); the direction gradient is
+    (dp^T xn) W^T.  The scan, the write and the epilogue run as
+    sparc_mixer_scan_forward / _backward."""
+
+    @staticmethod
+    def forward(ctx, xn, weight, phase_direction, radial_direction, nu_log, theta_log, write_log_gain,
+                write_phase_response, write_radial_response, energy_response):
+        lib = _lib.load()
+        dev = _lib.require_gpu(xn, weight, phase_direction)
+        B, T, D = xn.shape
+        W = weight.shape[0]
+        M = W // 2
+        x = torch.nn.functional.linear(xn, weight).contiguous()  # [B, T, 2M] in the activation dtype
+        dirs = torch.stack((phase_direction, radial_direction)).detach().float()  # [2, 2M + 1]
+        v = dirs[:, :W] @ weight.detach().float()                                  # [2, D]
+        p = torch.addmm(dirs[:, W], xn.detach().reshape(-1, D).float(), v.t())     # [B*T, 2]
+        delta = (HALF_PI * torch.tanh(p[:, 0])).contiguous()
+        eta = (LOG16 * torch.tanh(p[:, 1])).contiguous()
+        params = [t.detach().float().contiguous() for t in (
+            nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response)]
+        io = _lib.io_code(x.dtype)
+        y = torch.empty_like(x)
+        h_re = torch.empty(B, T, M, dtype=x.dtype, device=dev)
+        h_im = torch.empty_like(h_re)
+        last_re = torch.empty(B, M, dtype=torch.float32, device=dev)
+        last_im = torch.empty_like(last_re)
+        ws_bytes = lib.sparc_mixer_workspace_bytes(B, T, M, 0)
+        if ws_bytes == 0:
+            raise ValueError("invalid shape for the fused mixer")
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        P = _lib.ptr
+        _lib.check(lib.sparc_mixer_scan_forward(
+            B, T, M, io, P(x), P(eta), P(delta), *[P(t) for t in params], P(y), P(h_re), P(h_im),
+            P(last_re), P(last_im), P(ws), ws.numel(), _lib.stream_of(dev)), "sparc_mixer_scan_forward")
+        ctx.save_for_backward(xn, weight, dirs, v, x, eta, delta, h_re, h_im, *params)
+        ctx.dtypes = [t.dtype for t in (phase_direction, radial_direction, nu_log, theta_log,
+                                        write_log_gain, write_phase_response, write_radial_response)]
+        ctx.energy = (energy_response.shape, energy_response.dtype)
+        return y, last_re, last_im
+
+    @staticmethod
+    def backward(ctx, dy, dlast_re, dlast_im):
+        xn, weight, dirs, v, x, eta, delta, h_re, h_im, *params = ctx.saved_tensors
+        lib = _lib.load()
+        dev = x.device
+        B, T, W = x.shape
+        D = xn.shape[-1]
+        M = W // 2
+        if dy is None:
+            dy = torch.zeros_like(x)
+        dy = dy.to(x.dtype).contiguous()
+        if dlast_re is not None or dlast_im is not None:
+            z = torch.zeros(B, M, dtype=torch.float32, device=dev)
+            dlast_re = z if dlast_re is None else dlast_re.float().contiguous()
+            dlast_im = z.clone() if dlast_im is None else dlast_im.float().contiguous()
+        dx = torch.empty_like(x)
+        deta = torch.empty(B * T, dtype=torch.float32, device=dev)
+        ddelta = torch.empty_like(deta)
+        grads = [torch.empty(M, dtype=torch.float32, device=dev) for _ in range(5)]
+        ws = torch.empty(lib.sparc_mixer_workspace_bytes(B, T, M, 1), dtype=torch.uint8, device=dev)
+        P = _lib.ptr
+        _lib.check(lib.sparc_mixer_scan_backward(
+            B, T, M, _lib.io_code(x.dtype), P(x), P(eta), P(delta), *[P(t) for t in params],
+            P(h_re), P(h_im), P(dy), P(dlast_re), P(dlast_im), P(dx), P(deta), P(ddelta),
+            *[P(g) for g in grads], P(ws), ws.numel(), _lib.stream_of(dev)), "sparc_mixer_scan_backward")
+        # the controls: dp0 (phase), dp1 (radial) per token
+        dp = torch.stack((ddelta * HALF_PI * (1.0 - (delta / HALF_PI) ** 2),
+                          deta * LOG16 * (1.0 - (eta / LOG16) ** 2)), dim=1)          # [B*T, 2]
+        xn2 = xn.reshape(-1, D)
+        dx2 = dx.reshape(-1, W)
+        g_xn = (dx2 @ weight + (dp @ v).to(dx.dtype)).reshape(B, T, D)
+        dpx = dp.t() @ xn2.float()                                                      # [2, D]
+        g_w = dx2.t() @ xn2 + (dirs[:, :W].t() @ dpx).to(weight.dtype)
+        g_dirs = torch.cat((dpx @ weight.float().t(), dp.sum(0)[:, None]), dim=1)      # [2, 2M + 1]
+        out = [g_dirs[0], g_dirs[1], *grads]
+        out = [g.to(dt) for g, dt in zip(out, ctx.dtypes)]
+        shape, dt = ctx.energy
+        return (g_xn, g_w.to(weight.dtype), *out, torch.zeros(shape, dtype=dt, device=dev))
+
+
+def projected_fused_supported(xn: torch.Tensor, weight: torch.Tensor) -> bool:
+    return (xn.is_cuda and xn.dtype in (torch.float32, torch.bfloat16) and weight.dtype == xn.dtype
+            and weight.shape[0] % 8 == 0 and xn.ndim == 3 and xn.shape[0] > 0)
+
+
+def projected_sequence(module, xn: torch.Tensor, weight: torch.Tensor):
+    """(y, (last_re, last_im)) of ``module`` on ``xn @ weight^T`` with the
+    controls folded into the projection."""
+    y, last_re, last_im = _ProjectedMixer.apply(
+        xn, weight, *[getattr(module, n) for n in _PARAMS], module.energy_response)
+    return y, (last_re, last_im)

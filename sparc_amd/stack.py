@@ -7,7 +7,8 @@ Each block is pre-norm and residual:
 with ``in_proj`` d_model -> 2M and ``out_proj`` 2M -> d_model (M = d_model *
 N complex modes, so the mixer's width is 2M), and a final RMSNorm.  The
 projections are plain GEMMs (torch -> hipBLASLt on MI355X); the mixer is the
-fused HIP sequence path.  The reference ships the layer, not a network
+fused HIP sequence path, with its two control dot products folded into the
+input projection (``fuse_projection``).  The reference ships the layer, not a network
 (sparc-kernal/sparc.py:58-128); this stack is the configuration the layer is
 benchmarked in.
 """
@@ -17,7 +18,12 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from . import mixer as _mixer
 from .sparc import SPARCMixer
+
+# Fold the controls into the input projection (see mixer._ProjectedMixer);
+# False runs the projection and the module separately.
+fuse_projection = True
 
 
 class SPARCBlock(nn.Module):
@@ -32,7 +38,12 @@ class SPARCBlock(nn.Module):
             self.out_proj.weight.mul_(1.0 / (2 * modes) ** 0.5)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        y, _ = self.mixer(self.in_proj(self.norm(x)))
+        xn = self.norm(x)
+        if fuse_projection and _mixer.get_mixer_path() != "composed" and \
+                _mixer.projected_fused_supported(xn, self.in_proj.weight):
+            y, _ = _mixer.projected_sequence(self.mixer, xn, self.in_proj.weight)
+        else:
+            y, _ = self.mixer(self.in_proj(xn))
         return x + self.out_proj(y)
 
 

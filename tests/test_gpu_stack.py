@@ -36,8 +36,11 @@ def reference_stack(model, x):
     return F.rms_norm(h, (h.shape[-1],), leaves["norm.weight"], model.norm.eps), leaves
 
 
-def test_stack_fp32_matches_oracle_stack():
-    print("[case] stack fp32 2 layers d_model=16 N=4 B=2 T=50", flush=True)
+@pytest.mark.parametrize("fold", [True, False], ids=["folded_controls", "separate"])
+def test_stack_fp32_matches_oracle_stack(fold, monkeypatch):
+    print(f"[case] stack fp32 2 layers d_model=16 N=4 B=2 T=50 fold={fold}", flush=True)
+    from sparc_amd import stack
+    monkeypatch.setattr(stack, "fuse_projection", fold)
     torch.manual_seed(0)
     model = SPARCStack(2, 16, 4)
     g = torch.Generator().manual_seed(1)
@@ -65,10 +68,13 @@ def test_stack_fp32_matches_oracle_stack():
         assert rel_err(a, b) <= 1e-4, f"{n}: {rel_err(a, b):.3g}"
 
 
-def test_stack_bf16_training_step():
+@pytest.mark.parametrize("fold", [True, False], ids=["folded_controls", "separate"])
+def test_stack_bf16_training_step(fold, monkeypatch):
     """One bf16 training step (forward, backward, AdamW) at a reduced cfg5
     shape: finite loss and gradients, parameters updated."""
-    print("[case] stack bf16 step 2 layers d_model=64 N=16 B=4 T=128", flush=True)
+    print(f"[case] stack bf16 step 2 layers d_model=64 N=16 B=4 T=128 fold={fold}", flush=True)
+    from sparc_amd import stack
+    monkeypatch.setattr(stack, "fuse_projection", fold)
     torch.manual_seed(0)
     model = SPARCStack(2, 64, 16).cuda().to(torch.bfloat16)
     opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
