@@ -267,9 +267,21 @@ decode_kernel(int M, const void* x, const float* pdir, const float* rdir,
 #define SPARC_STEP_STATE_CPOL 16
 #endif
 constexpr int kDecodeConsts = 8;  // floats per mode in the constants table
-constexpr int kDotSplit = 16;     // slices per row for the control dot products
-constexpr int kDotRows = 4;       // rows per dot workgroup (direction loads reused)
-constexpr int kDecodeRows = 4;    // rows per update workgroup (constants reused)
+#ifndef SPARC_DOT_SPLIT
+#define SPARC_DOT_SPLIT 16
+#endif
+#ifndef SPARC_DOT_ROWS
+#define SPARC_DOT_ROWS 4
+#endif
+// Rows per update workgroup: the per-mode constants a thread loads serve
+// every row.  At B=256, M=32768 (bf16): 4 rows 47.6 us per step, 8 rows 46.1,
+// 16 rows 44.0, 32 rows 47.7 (too few workgroups).
+#ifndef SPARC_DECODE_ROWS
+#define SPARC_DECODE_ROWS 16
+#endif
+constexpr int kDotSplit = SPARC_DOT_SPLIT;   // slices per row for the control dot products
+constexpr int kDotRows = SPARC_DOT_ROWS;     // rows per dot workgroup (direction loads reused)
+constexpr int kDecodeRows = SPARC_DECODE_ROWS;  // rows per update workgroup (constants reused)
 #ifndef SPARC_DECODE_PREFETCH
 #define SPARC_DECODE_PREFETCH 1
 #endif
