@@ -45,7 +45,8 @@ constexpr float kLog16 = 2.772588722239781f;
 constexpr float kInvLog16 = 0.36067376022224085f;
 constexpr float kHalfPi = 1.5707963267948966f;
 constexpr float kTwoOverPi = 0.6366197723675814f;
-constexpr int kConsts = 8;     // floats per mode in the constants table
+constexpr int kConsts = 12;    // floats per mode in the constants table
+constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kS = 8;          // steps per prefetched block of the forward scan
 constexpr int kCtrlRows = 16;  // rows per workgroup of the controls forward
 constexpr int kCtrlBwdRows = 128;  // rows per workgroup of the controls backward
@@ -70,7 +71,14 @@ struct Args {
   float* part_mode;  // [5][B][M]: nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response
 };
 
-// consts[m] = (nu, cos theta, sin theta, gamma = e^{wlg}, cinv = 1/expm1(-2 nu), wpr, wrr, theta)
+// Per-mode constants, folded so that the per-step arithmetic is short:
+//   c0 = (nu, cos theta, sin theta, g2 = 4 gamma^2 / expm1(-2 nu))
+//        gain = sqrt(g2 * em (2 + em)) * sigmoid(q), em = expm1(-nu e^eta)
+//        (= gamma * sqrt(expm1(-2 nu e^eta) / expm1(-2 nu)) * 2 sigmoid(q))
+//   c1 = (pl, rl, theta, kappa): -q log2(e) = delta * pl + eta * rl with
+//        pl = -wpr log2(e) 2/pi, rl = -wrr log2(e) / log16;
+//        kappa = nu e^{-2 nu} / (1 - e^{-2 nu})
+//   c2 = (wrr / log16, wpr 2/pi, 0, 0)
 __global__ void __launch_bounds__(256)
 mixer_prepare_kernel(int M, const float* nu_log, const float* theta_log, const float* wlg,
                      const float* wpr, const float* wrr, float* consts) {
@@ -80,9 +88,12 @@ mixer_prepare_kernel(int M, const float* nu_log, const float* theta_log, const f
   const float theta = expf(theta_log[m]);
   float sn, cs;
   sincosf(theta, &sn, &cs);
+  const float gam = expf(wlg[m]);
+  const float cinv = 1.0f / expm1f(-2.0f * nu);
   float4* c = reinterpret_cast<float4*>(consts + static_cast<int64_t>(m) * kConsts);
-  c[0] = make_float4(nu, cs, sn, expf(wlg[m]));
-  c[1] = make_float4(1.0f / expm1f(-2.0f * nu), wpr[m], wrr[m], theta);
+  c[0] = make_float4(nu, cs, sn, 4.0f * gam * gam * cinv);
+  c[1] = make_float4(-wpr[m] * kLog2e * kTwoOverPi, -wrr[m] * kLog2e * kInvLog16, theta, -nu * (1.0f + cinv));
+  c[2] = make_float4(wrr[m] * kInvLog16, wpr[m] * kTwoOverPi, 0.0f, 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -175,17 +186,22 @@ ctrl_fwd_kernel(int64_t R, int W, const void* x, const float* pdir, const float*
 // ---------------------------------------------------------------------------
 // per-mode constants of a lane's V modes
 // ---------------------------------------------------------------------------
-template <int V>
+template <int V, bool BWD>
 struct ModeConsts {
-  float nu[V], ct[V], st[V], gam[V], cinv[V], wpr[V], wrr[V], th[V];
+  float nu[V], ct[V], st[V], g2[V], pl[V], rl[V], th[V], kappa[V], wrr_s[V], wpr_s[V];
   __device__ __forceinline__ void load(const float* consts, int m0, bool ok) {
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       const int m = ok ? m0 + v : 0;
-      const float4 c0 = *reinterpret_cast<const float4*>(consts + static_cast<int64_t>(m) * kConsts);
-      const float4 c1 = *reinterpret_cast<const float4*>(consts + static_cast<int64_t>(m) * kConsts + 4);
-      nu[v] = c0.x; ct[v] = c0.y; st[v] = c0.z; gam[v] = c0.w;
-      cinv[v] = c1.x; wpr[v] = c1.y; wrr[v] = c1.z; th[v] = c1.w;
+      const float* c = consts + static_cast<int64_t>(m) * kConsts;
+      const float4 c0 = *reinterpret_cast<const float4*>(c);
+      const float4 c1 = *reinterpret_cast<const float4*>(c + 4);
+      nu[v] = c0.x; ct[v] = c0.y; st[v] = c0.z; g2[v] = c0.w;
+      pl[v] = c1.x; rl[v] = c1.y; th[v] = c1.z; kappa[v] = c1.w;
+      if constexpr (BWD) {
+        const float4 c2 = *reinterpret_cast<const float4*>(c + 8);
+        wrr_s[v] = c2.x; wpr_s[v] = c2.y;
+      }
     }
   }
 };
@@ -194,8 +210,8 @@ struct ModeConsts {
 struct StepMode {
   float em, rho, ar, ai, gain, sg;
 };
-__device__ __forceinline__ StepMode p1_step(float nu, float ct, float st, float gam, float cinv, float wpr,
-                                             float wrr, float E, float delta, float ps, float rs) {
+__device__ __forceinline__ StepMode p1_step(float nu, float ct, float st, float g2, float pl, float rl,
+                                             float E, float eta, float delta) {
   StepMode o;
   o.em = expm1_nonpos(-nu * E);  // rho - 1
   o.rho = 1.0f + o.em;
@@ -203,11 +219,9 @@ __device__ __forceinline__ StepMode p1_step(float nu, float ct, float st, float 
   sincos_half(-o.em * delta, su, cu);  // phase (1 - rho) delta, |.| <= pi/2
   o.ar = o.rho * fmaf(ct, cu, -st * su);
   o.ai = o.rho * fmaf(st, cu, ct * su);
-  // expm1(-2 nu E) = em (2 + em); ratio = sqrt(expm1(-2 nu E) / expm1(-2 nu))
-  const float ratio = __builtin_amdgcn_sqrtf(o.em * (2.0f + o.em) * cinv);
-  const float q = fmaf(ps, wpr, rs * wrr);
-  o.sg = __builtin_amdgcn_rcpf(1.0f + fast_exp(-q));  // sigmoid(q)
-  o.gain = gam * ratio * 2.0f * o.sg;
+  // em (2 + em) = expm1(-2 nu E)
+  o.sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(delta, pl, eta * rl)));  // sigmoid(q)
+  o.gain = __builtin_amdgcn_sqrtf(g2 * fmaf(o.em, o.em, o.em + o.em)) * o.sg;
   return o;
 }
 
@@ -231,7 +245,7 @@ mixer_fwd_kernel(Args a) {
   const int m0 = mb * MB + lane * V;
   const bool lane_ok = m0 < a.M;
   const int n_blocks = (a.T + kS - 1) / kS;
-  ModeConsts<V> mc;
+  ModeConsts<V, false> mc;
   mc.load(a.consts, m0, lane_ok);
   const int64_t row0 = static_cast<int64_t>(b) * a.T;
   const int64_t mbase = static_cast<int64_t>(mb) * MB;
@@ -277,14 +291,12 @@ mixer_fwd_kernel(Args a) {
       const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
       const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), s));
       const float E = fast_exp(eta);
-      const float ps = delta * kTwoOverPi, rs = eta * kInvLog16;
       float cr[V], ci[V];
       unpack<IO, V>(xr[h][s], cr);
       unpack<IO, V>(xi[h][s], ci);
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        const StepMode q = p1_step(mc.nu[v], mc.ct[v], mc.st[v], mc.gam[v], mc.cinv[v], mc.wpr[v], mc.wrr[v],
-                                   E, delta, ps, rs);
+        const StepMode q = p1_step(mc.nu[v], mc.ct[v], mc.st[v], mc.g2[v], mc.pl[v], mc.rl[v], E, eta, delta);
         ar[s][v] = q.ar;
         ai[s][v] = q.ai;
         wr[s][v] = q.gain * tanh_fast(cr[v]);
@@ -377,7 +389,7 @@ mixer_bwd_kernel(Args a) {
   const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
   const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
 
-  ModeConsts<V> mc;
+  ModeConsts<V, true> mc;
   mc.load(a.consts, m0, lane_ok);
   float Xr[V], Xi[V];    // conj(a_{t+1}) lambda_{t+1}
   float hcr[V], hci[V];  // h at the last step of the next block to process
@@ -506,11 +518,9 @@ mixer_bwd_kernel(Args a) {
         const float l_r = lr[s][v], l_i = li[s][v];
         const float em = qem[s][v], rho = 1.0f + em;
         const float ar = qar[s][v], ai = qai[s][v];
-        const float one_m_r2 = -em * (2.0f + em);  // 1 - rho^2 = -expm1(-2 nu E)
-        const float ratio = __builtin_amdgcn_sqrtf(-one_m_r2 * mc.cinv[v]);
-        const float q = fmaf(ps, mc.wpr[v], rs * mc.wrr[v]);
-        const float sg = __builtin_amdgcn_rcpf(1.0f + fast_exp(-q));
-        const float gain = mc.gam[v] * ratio * 2.0f * sg;
+        const float e2 = fmaf(em, em, em + em);  // em (2 + em) = expm1(-2 nu E) = -(1 - rho^2)
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(delta, mc.pl[v], eta * mc.rl[v])));
+        const float gain = __builtin_amdgcn_sqrtf(mc.g2[v] * e2) * sg;
         const float tr = tanh_fast(cxr[v]), ti = tanh_fast(cxi[v]);
         dxr[s][v] = l_r * gain * fmaf(-tr, tr, 1.0f);
         dxi[s][v] = l_i * gain * fmaf(-ti, ti, 1.0f);
@@ -520,13 +530,12 @@ mixer_bwd_kernel(Args a) {
         const float dphi = fmaf(-gar, ai, gai * ar);
         const float z = mc.nu[v] * E;  // -log(rho)
         const float radial = z * fmaf(rho * delta, dphi, -fmaf(gar, ar, gai * ai));
-        const float wterm = z * rho * rho * __builtin_amdgcn_rcpf(one_m_r2);
+        const float wterm = -z * rho * rho * __builtin_amdgcn_rcpf(e2);
         const float gs = g * (1.0f - sg);
-        se += radial + g * wterm + gs * mc.wrr[v] * kInvLog16;
-        sd += fmaf(dphi, -em, gs * mc.wpr[v] * kTwoOverPi);
+        se += radial + fmaf(g, wterm, gs * mc.wrr_s[v]);
+        sd += fmaf(dphi, -em, gs * mc.wpr_s[v]);
         if (live) {
-          const float kappa = -mc.nu[v] * (1.0f + mc.cinv[v]);
-          acc[0][v] += radial + g * (wterm - kappa);
+          acc[0][v] += radial + g * (wterm - mc.kappa[v]);
           acc[1][v] = fmaf(mc.th[v], dphi, acc[1][v]);
           acc[2][v] += g;
           acc[3][v] = fmaf(gs, ps, acc[3][v]);
