@@ -122,6 +122,52 @@ __device__ __forceinline__ void buffer_store_f32(__amdgpu_buffer_rsrc_t r, uint3
 // s_waitcnt vmcnt(0): every vector memory operation of the wave has completed.
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// A raw T (2, 4, 8 or 16 bytes) through a buffer resource at the lane's
+// byte offset voff plus a wave-uniform byte offset soff (an SGPR operand: no
+// per-lane address arithmetic), with cache policy CPOL.
+template <typename T, int CPOL>
+__device__ __forceinline__ T buf_load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  T out;
+  if constexpr (sizeof(T) == 2) {
+    const unsigned short v = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, CPOL);
+    __builtin_memcpy(&out, &v, 2);
+  } else if constexpr (sizeof(T) == 4) {
+    const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, CPOL);
+    __builtin_memcpy(&out, &v, 4);
+  } else if constexpr (sizeof(T) == 8) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, CPOL);
+    __builtin_memcpy(&out, &v, 8);
+  } else {
+    static_assert(sizeof(T) == 16, "2, 4, 8 or 16 bytes");
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CPOL);
+    __builtin_memcpy(&out, &v, 16);
+  }
+  return out;
+}
+template <typename T, int CPOL>
+__device__ __forceinline__ void buf_store(T x, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  if constexpr (sizeof(T) == 2) {
+    unsigned short v;
+    __builtin_memcpy(&v, &x, 2);
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, voff, soff, CPOL);
+  } else if constexpr (sizeof(T) == 4) {
+    uint32_t v;
+    __builtin_memcpy(&v, &x, 4);
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, voff, soff, CPOL);
+  } else if constexpr (sizeof(T) == 8) {
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    u2 v;
+    __builtin_memcpy(&v, &x, 8);
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, soff, CPOL);
+  } else {
+    static_assert(sizeof(T) == 16, "2, 4, 8 or 16 bytes");
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    u4 v;
+    __builtin_memcpy(&v, &x, 16);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, CPOL);
+  }
+}
+
 // A 64-bit value every lane of the wave holds, moved to scalar registers, so
 // that a memory instruction can take (kernel-argument pointer + this offset)
 // as its scalar base and the lane's byte offset as its vector offset.

@@ -252,6 +252,10 @@ mixer_fwd_kernel(Args a) {
   const int64_t W = 2 * static_cast<int64_t>(a.M);
   const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
   const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
+  // bytes of one row of x (2M) and of h (M), and of kS rows (< 2^31: the host
+  // limits M to 2^24)
+  const uint32_t row_x = static_cast<uint32_t>(W * ESZ), half_x = static_cast<uint32_t>(a.M * ESZ);
+  const uint32_t blk_x = kS * row_x, blk_h = kS * half_x;
   // the constants are loop-carried: complete their loads before the loop (else
   // the waits inside it would also cover the prefetch)
   wait_vm_all();
@@ -262,12 +266,15 @@ mixer_fwd_kernel(Args a) {
     constexpr int h = decltype(h_tag)::value;
     const int t0 = k * kS;
     const int last = a.T - 1 - t0;
+    // the block's rows of x through one buffer resource: row offsets in
+    // scalar registers, no per-lane address arithmetic
     const int64_t off = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const char*>(a.x) + off, blk_x);
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
-      const int64_t o = off + static_cast<int64_t>(s <= last ? s : last) * W * ESZ;
-      xr[h][s] = ldn<RawT>(a.x, o, lane_ld);
-      xi[h][s] = ldn<RawT>(a.x, o + static_cast<int64_t>(a.M) * ESZ, lane_ld);
+      const uint32_t o = static_cast<uint32_t>(s <= last ? s : last) * row_x;
+      xr[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
+      xi[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
     }
     const int sl = lane & (kS - 1);
     const int64_t ti = row0 + t0 + (sl <= last ? sl : last);
@@ -305,6 +312,9 @@ mixer_fwd_kernel(Args a) {
     }
     const int64_t yoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
     const int64_t hoff = wave_uniform(((row0 + t0) * a.M + mbase) * ESZ);
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<char*>(a.y) + yoff, blk_x);
+    const __amdgpu_buffer_rsrc_t rhr = make_rsrc(static_cast<char*>(a.h_re) + hoff, blk_h);
+    const __amdgpu_buffer_rsrc_t rhi = make_rsrc(static_cast<char*>(a.h_im) + hoff, blk_h);
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
       if (TAIL && t0 + s >= a.T) break;  // wave-uniform
@@ -319,12 +329,12 @@ mixer_fwd_kernel(Args a) {
 #pragma unroll
       for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
       if (lane_ok) {
-        const int64_t yo = yoff + static_cast<int64_t>(s) * W * ESZ;
-        stn<RawT>(a.y, yo, lane_bytes, pack<IO, V>(rr));
-        stn<RawT>(a.y, yo + static_cast<int64_t>(a.M) * ESZ, lane_bytes, pack<IO, V>(ri));
-        const int64_t ho = hoff + static_cast<int64_t>(s) * a.M * ESZ;
-        stn<RawT>(a.h_re, ho, lane_bytes, pack<IO, V>(hr));
-        stn<RawT>(a.h_im, ho, lane_bytes, pack<IO, V>(hi));
+        const uint32_t yo = static_cast<uint32_t>(s) * row_x;
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(rr), ry, lane_bytes, yo);
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(ri), ry, lane_bytes, yo + half_x);
+        const uint32_t ho = static_cast<uint32_t>(s) * half_x;
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(hr), rhr, lane_bytes, ho);
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(hi), rhi, lane_bytes, ho);
       }
     }
   };
@@ -388,6 +398,10 @@ mixer_bwd_kernel(Args a) {
   const int64_t W = 2 * static_cast<int64_t>(a.M);
   const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
   const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
+  // bytes of one row of x / dy / dx (2M) and of h (M), and of kS rows (the host
+  // limits M to 2^24, so these fit in 32 bits)
+  const uint32_t row_x = static_cast<uint32_t>(W * ESZ), half_x = static_cast<uint32_t>(a.M * ESZ);
+  const uint32_t blk_x = kS * row_x, blk_h = kS * half_x;
 
   ModeConsts<V, true> mc;
   mc.load(a.consts, m0, lane_ok);
@@ -417,20 +431,28 @@ mixer_bwd_kernel(Args a) {
     constexpr int h = decltype(h_tag)::value;
     const int t0 = k * kS;
     const int last = a.T - 1 - t0;
+    // buffer resources over the block's rows (row offsets in scalar
+    // registers); the previous states start at row t0-1 (row 0 when t0 = 0)
+    const int hb = t0 > 0 ? t0 - 1 : 0;
     const int64_t xoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
-    const int64_t poff = wave_uniform(((row0 + t0) * a.M + mbase) * ESZ);
+    const int64_t poff = wave_uniform(((row0 + hb) * a.M + mbase) * ESZ);
+    const __amdgpu_buffer_rsrc_t rdy = make_rsrc(static_cast<const char*>(a.dy) + xoff, blk_x);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const char*>(a.x) + xoff, blk_x);
+    const __amdgpu_buffer_rsrc_t rpr = make_rsrc(static_cast<const char*>(a.h_re) + poff, blk_h);
+    const __amdgpu_buffer_rsrc_t rpi = make_rsrc(static_cast<const char*>(a.h_im) + poff, blk_h);
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
       const int sc = s <= last ? s : last;
-      const int64_t o = xoff + static_cast<int64_t>(sc) * W * ESZ;
-      dr[h][s] = ldn<RawT>(a.dy, o, lane_ld);
-      di[h][s] = ldn<RawT>(a.dy, o + static_cast<int64_t>(a.M) * ESZ, lane_ld);
-      xr[h][s] = ldn<RawT>(a.x, o, lane_ld);
-      xi[h][s] = ldn<RawT>(a.x, o + static_cast<int64_t>(a.M) * ESZ, lane_ld);
-      const int sp = (t0 + sc > 0) ? sc - 1 : 0;  // row t-1 (t >= 1), else row 0
-      const int64_t q = poff + static_cast<int64_t>(sp) * a.M * ESZ;
-      pr[h][s] = ldn<RawT>(a.h_re, q, lane_ld);
-      pi[h][s] = ldn<RawT>(a.h_im, q, lane_ld);
+      const uint32_t o = static_cast<uint32_t>(sc) * row_x;
+      dr[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o);
+      di[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o + half_x);
+      xr[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
+      xi[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
+      // row t-1 (t >= 1), else row 0, relative to hb
+      const int rel = t0 > 0 ? sc : (sc > 0 ? sc - 1 : 0);
+      const uint32_t q = static_cast<uint32_t>(rel) * half_x;
+      pr[h][s] = buf_load<RawT, CPOL_NT>(rpr, lane_ld, q);
+      pi[h][s] = buf_load<RawT, CPOL_NT>(rpi, lane_ld, q);
     }
     const int sl = lane & (kS - 1);
     const int64_t ti = row0 + t0 + (sl <= last ? sl : last);
@@ -547,13 +569,14 @@ mixer_bwd_kernel(Args a) {
     }
     // (D) stores; the carry for the next block (in reverse time) is h_{t0-1}
     const int64_t xoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
+    const __amdgpu_buffer_rsrc_t rdx = make_rsrc(static_cast<char*>(a.dx) + xoff, blk_x);
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
       if (TAIL && t0 + s >= a.T) break;
       if (lane_ok) {
-        const int64_t o = xoff + static_cast<int64_t>(s) * W * ESZ;
-        stn<RawT>(a.dx, o, lane_bytes, pack<IO, V>(dxr[s]));
-        stn<RawT>(a.dx, o + static_cast<int64_t>(a.M) * ESZ, lane_bytes, pack<IO, V>(dxi[s]));
+        const uint32_t o = static_cast<uint32_t>(s) * row_x;
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(dxr[s]), rdx, lane_bytes, o);
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(dxi[s]), rdx, lane_bytes, o + half_x);
       }
     }
     // the lane sums of the block's 2*kS per-token values: lane l ends with
@@ -770,7 +793,7 @@ sparc_status check_shape(int64_t B, int64_t T, int64_t M, int32_t io) {
   if (B <= 0 || T < 0 || M <= 0) return fail(SPARC_EINVAL, "mixer: B > 0, T >= 0, M > 0 required");
   if (M % 4) return fail(SPARC_EINVAL, "mixer: modes must be a multiple of 4");
   if (io != SPARC_F32 && io != SPARC_BF16) return fail(SPARC_EINVAL, "mixer: io_dtype");
-  if (M > (1 << 26) || B * T > (int64_t(1) << 40) || B * T * 2 * M > (int64_t(1) << 46) || B > INT32_MAX ||
+  if (M > (1 << 24) || B * T > (int64_t(1) << 40) || B * T * 2 * M > (int64_t(1) << 46) || B > INT32_MAX ||
       T > INT32_MAX)
     return fail(SPARC_EINVAL, "mixer: shape too large");
   return SPARC_OK;
