@@ -664,42 +664,62 @@ ctrl_bwd_kernel(int64_t R, int W, const void* x, const float* pdir, const float*
 #pragma unroll
   for (int i = 0; i < 8; ++i) { a0[i] = 0.0f; a1[i] = 0.0f; }
   float b0 = 0.0f, b1 = 0.0f;
-  for (int64_t r = r0; r < r1; ++r) {
-    const float e = eta[r] * kInvLog16, d = delta[r] * kTwoOverPi;
-    const float dp1 = deta[r] * kLog16 * fmaf(-e, e, 1.0f);
-    const float dp0 = ddelta[r] * kHalfPi * fmaf(-d, d, 1.0f);
-    b0 += dp0;
-    b1 += dp1;
-    if (!col_ok) continue;
-    float xv[8], gv[8];
+  // rows in groups of kG: every load of the group is issued before any of
+  // its arithmetic (rows past r1 re-read row r1-1 and contribute nothing)
+  constexpr int kG = 4;
+  auto load8 = [&](const void* base, int64_t row, float (&o)[8]) {
     if constexpr (sizeof(IO) == 2) {
-      unpack<bf16, 8>(load_raw_nt<bf16, 8>(x, r * W + c), xv);
-      unpack<bf16, 8>(load_raw_nt<bf16, 8>(dx, r * W + c), gv);
+      unpack<bf16, 8>(load_raw_nt<bf16, 8>(base, row * W + cc), o);
     } else {
       float t[4];
-      unpack<float, 4>(load_raw_nt<float, 4>(x, r * W + c), t);
-      for (int i = 0; i < 4; ++i) xv[i] = t[i];
-      unpack<float, 4>(load_raw_nt<float, 4>(x, r * W + c + 4), t);
-      for (int i = 0; i < 4; ++i) xv[4 + i] = t[i];
-      unpack<float, 4>(load_raw_nt<float, 4>(dx, r * W + c), t);
-      for (int i = 0; i < 4; ++i) gv[i] = t[i];
-      unpack<float, 4>(load_raw_nt<float, 4>(dx, r * W + c + 4), t);
-      for (int i = 0; i < 4; ++i) gv[4 + i] = t[i];
+      unpack<float, 4>(load_raw_nt<float, 4>(base, row * W + cc), t);
+      for (int i = 0; i < 4; ++i) o[i] = t[i];
+      unpack<float, 4>(load_raw_nt<float, 4>(base, row * W + cc + 4), t);
+      for (int i = 0; i < 4; ++i) o[4 + i] = t[i];
+    }
+  };
+  for (int64_t r = r0; r < r1; r += kG) {
+    float xv[kG][8], gv[kG][8], dp0[kG], dp1[kG];
+#pragma unroll
+    for (int k = 0; k < kG; ++k) {
+      const int64_t rr = r + k < r1 ? r + k : r1 - 1;
+      load8(x, rr, xv[k]);
+      load8(dx, rr, gv[k]);
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      gv[i] = fmaf(dp0, u0[i], fmaf(dp1, u1[i], gv[i]));
-      a0[i] = fmaf(dp0, xv[i], a0[i]);
-      a1[i] = fmaf(dp1, xv[i], a1[i]);
+    for (int k = 0; k < kG; ++k) {
+      const int64_t rr = r + k < r1 ? r + k : r1 - 1;
+      const float e = eta[rr] * kInvLog16, d = delta[rr] * kTwoOverPi;
+      const bool live = r + k < r1;
+      dp1[k] = live ? deta[rr] * kLog16 * fmaf(-e, e, 1.0f) : 0.0f;
+      dp0[k] = live ? ddelta[rr] * kHalfPi * fmaf(-d, d, 1.0f) : 0.0f;
+      b0 += dp0[k];
+      b1 += dp1[k];
     }
-    if constexpr (sizeof(IO) == 2) {
-      store_raw_nt<bf16, 8>(dx, r * W + c, pack<bf16, 8>(gv));
-    } else {
-      float t[4];
-      for (int i = 0; i < 4; ++i) t[i] = gv[i];
-      store_raw_nt<float, 4>(dx, r * W + c, pack<float, 4>(t));
-      for (int i = 0; i < 4; ++i) t[i] = gv[4 + i];
-      store_raw_nt<float, 4>(dx, r * W + c + 4, pack<float, 4>(t));
+#pragma unroll
+    for (int k = 0; k < kG; ++k) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        gv[k][i] = fmaf(dp0[k], u0[i], fmaf(dp1[k], u1[i], gv[k][i]));
+        a0[i] = fmaf(dp0[k], xv[k][i], a0[i]);
+        a1[i] = fmaf(dp1[k], xv[k][i], a1[i]);
+      }
+    }
+    if (col_ok) {
+#pragma unroll
+      for (int k = 0; k < kG; ++k) {
+        if (r + k >= r1) break;  // wave-uniform
+        const int64_t rr = r + k;
+        if constexpr (sizeof(IO) == 2) {
+          store_raw_nt<bf16, 8>(dx, rr * W + c, pack<bf16, 8>(gv[k]));
+        } else {
+          float t[4];
+          for (int i = 0; i < 4; ++i) t[i] = gv[k][i];
+          store_raw_nt<float, 4>(dx, rr * W + c, pack<float, 4>(t));
+          for (int i = 0; i < 4; ++i) t[i] = gv[k][4 + i];
+          store_raw_nt<float, 4>(dx, rr * W + c + 4, pack<float, 4>(t));
+        }
+      }
     }
   }
   if (col_ok) {
