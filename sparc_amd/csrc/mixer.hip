@@ -47,7 +47,10 @@ constexpr float kHalfPi = 1.5707963267948966f;
 constexpr float kTwoOverPi = 0.6366197723675814f;
 constexpr int kConsts = 12;    // floats per mode in the constants table
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kS = 8;          // steps per prefetched block of the forward scan
+#ifndef SPARC_MIXER_FWD_S
+#define SPARC_MIXER_FWD_S 8
+#endif
+constexpr int kS = SPARC_MIXER_FWD_S;  // steps per prefetched block of the forward scan
 constexpr int kCtrlRows = 16;  // rows per workgroup of the controls forward
 constexpr int kCtrlBwdRows = 128;  // rows per workgroup of the controls backward
 
