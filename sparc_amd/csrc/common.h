@@ -298,12 +298,11 @@ __device__ __forceinline__ void sincos_quarter(float x, float& s, float& c) {
   c = fmaf(pc, x2, 1.0f);
 }
 
-// expm1(x) for x <= 0: the Taylor series to x^5/5! for |x| < 1/16 (relative
-// error < 2e-9), exp(x) - 1 beyond (relative error < 1e-6: no cancellation
-// left to amplify the exponential's rounding)
+// expm1(x) for x <= 0: the Taylor series to x^4/4! for |x| < 1/16 (relative
+// error < 1.3e-7, about one fp32 ulp), exp(x) - 1 beyond (relative error
+// < 1e-6: no cancellation left to amplify the exponential's rounding)
 __device__ __forceinline__ float expm1_nonpos(float x) {
-  float p = 1.0f / 120.0f;
-  p = fmaf(p, x, 1.0f / 24.0f);
+  float p = 1.0f / 24.0f;
   p = fmaf(p, x, 1.0f / 6.0f);
   p = fmaf(p, x, 0.5f);
   p = fmaf(p, x, 1.0f);
@@ -311,20 +310,23 @@ __device__ __forceinline__ float expm1_nonpos(float x) {
   return x > -0.0625f ? p : fast_exp(x) - 1.0f;
 }
 
-// sin and cos of |u| <= pi/2 by Taylor series to x^11 / x^12 (error < 6e-8)
+// sin and cos of |u| <= pi/2 by minimax polynomials, sin u = u + u^3 P(u^2)
+// (P of degree 3) and cos u = 1 + u^2 Q(u^2) (Q of degree 4).  The
+// coefficients minimise the maximum relative error of sin and the absolute
+// error of cos on [0, pi/2] (Lawson's iteratively reweighted least squares);
+// evaluated in fp32 both stay within 1.2e-7 of the true values, the same as
+// the Taylor series to u^11 / u^12 they replace, with two fewer FMAs.
 __device__ __forceinline__ void sincos_half(float u, float& s, float& c) {
   const float u2 = u * u;
-  float ps = -1.0f / 39916800.0f;
-  ps = fmaf(ps, u2, 1.0f / 362880.0f);
-  ps = fmaf(ps, u2, -1.0f / 5040.0f);
-  ps = fmaf(ps, u2, 1.0f / 120.0f);
-  ps = fmaf(ps, u2, -1.0f / 6.0f);
+  float ps = 2.6057807644974673e-6f;
+  ps = fmaf(ps, u2, -1.9809603691101074e-4f);
+  ps = fmaf(ps, u2, 8.33306647837162e-3f);
+  ps = fmaf(ps, u2, -1.6666659712791443e-1f);
   s = fmaf(ps * u2, u, u);
-  float pc = 1.0f / 479001600.0f;
-  pc = fmaf(pc, u2, -1.0f / 3628800.0f);
-  pc = fmaf(pc, u2, 1.0f / 40320.0f);
-  pc = fmaf(pc, u2, -1.0f / 720.0f);
-  pc = fmaf(pc, u2, 1.0f / 24.0f);
+  float pc = -2.607710598567792e-7f;
+  pc = fmaf(pc, u2, 2.4761886379565112e-5f);
+  pc = fmaf(pc, u2, -1.38884037733078e-3f);
+  pc = fmaf(pc, u2, 4.166664183139801e-2f);
   pc = fmaf(pc, u2, -0.5f);
   c = fmaf(pc, u2, 1.0f);
 }
@@ -332,7 +334,7 @@ __device__ __forceinline__ void sincos_half(float u, float& s, float& c) {
 // tanh(x) = 1 - 2 / (1 + e^{2x}) through one hardware exponential and
 // reciprocal (absolute error ~1e-7; saturates to +-1 through e^{2x} = inf / 0)
 __device__ __forceinline__ float tanh_fast(float x) {
-  const float e = fast_exp(2.0f * x);
+  const float e = __builtin_amdgcn_exp2f(x * 2.8853900817779268f);  // 2 log2(e)
   return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f);
 }
 

@@ -296,11 +296,12 @@ mixer_fwd_kernel(Args a) {
     constexpr int h = decltype(h_tag)::value;
     constexpr bool TAIL = decltype(tail_tag)::value;
     float ar[kS][V], ai[kS][V], wr[kS][V], wi[kS][V];
+    const float ee = fast_exp(ev[h]);  // lane s: e^eta of step s
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
       const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
       const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), s));
-      const float E = fast_exp(eta);
+      const float E = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), s));
       float cr[V], ci[V];
       unpack<IO, V>(xr[h][s], cr);
       unpack<IO, V>(xi[h][s], ci);
@@ -476,11 +477,11 @@ mixer_bwd_kernel(Args a) {
     constexpr int h = decltype(h_tag)::value;
     constexpr bool TAIL = decltype(tail_tag)::value;
     float qar[kS][V], qai[kS][V], qem[kS][V];
+    const float ee = fast_exp(ev[h]);  // lane s: e^eta of step s
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
-      const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
       const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), s));
-      const float E = fast_exp(eta);
+      const float E = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), s));
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         const float em = expm1_nonpos(-mc.nu[v] * E);
@@ -528,7 +529,7 @@ mixer_bwd_kernel(Args a) {
       const int t = t0 + s;
       const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
       const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), s));
-      const float E = fast_exp(eta);
+      const float E = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), s));
       const float ps = delta * kTwoOverPi, rs = eta * kInvLog16;
       float hpr[V], hpi[V], cxr[V], cxi[V];
       unpack<IO, V>(pr[h][s], hpr);
@@ -543,9 +544,12 @@ mixer_bwd_kernel(Args a) {
         const float l_r = lr[s][v], l_i = li[s][v];
         const float em = qem[s][v], rho = 1.0f + em;
         const float ar = qar[s][v], ai = qai[s][v];
-        const float e2 = fmaf(em, em, em + em);  // em (2 + em) = expm1(-2 nu E) = -(1 - rho^2)
+        const float e2 = fmaf(em, em, em + em);  // em (2 + em) = expm1(-2 nu E) = rho^2 - 1
         const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(delta, mc.pl[v], eta * mc.rl[v])));
-        const float gain = __builtin_amdgcn_sqrtf(mc.g2[v] * e2) * sg;
+        // one reciprocal square root gives both sqrt(Y) = Y r and 1/e2 = g2 r^2
+        // (Y >= 0; the floor keeps a zero gain at zero instead of 0 * inf)
+        const float Y = mc.g2[v] * e2, r = __builtin_amdgcn_rsqf(fmaxf(Y, 1e-30f));
+        const float gain = Y * r * sg;
         const float tr = tanh_fast(cxr[v]), ti = tanh_fast(cxi[v]);
         dxr[s][v] = l_r * gain * fmaf(-tr, tr, 1.0f);
         dxi[s][v] = l_i * gain * fmaf(-ti, ti, 1.0f);
@@ -555,7 +559,7 @@ mixer_bwd_kernel(Args a) {
         const float dphi = fmaf(-gar, ai, gai * ar);
         const float z = mc.nu[v] * E;  // -log(rho)
         const float radial = z * fmaf(rho * delta, dphi, -fmaf(gar, ar, gai * ai));
-        const float wterm = -z * rho * rho * __builtin_amdgcn_rcpf(e2);
+        const float wterm = -z * fmaf(mc.g2[v], r * r, 1.0f);  // -z rho^2 / e2 = -z (1 + 1/e2)
         const float gs = g * (1.0f - sg);
         se += radial + fmaf(g, wterm, gs * mc.wrr_s[v]);
         sd += fmaf(dphi, -em, gs * mc.wpr_s[v]);
