@@ -232,14 +232,16 @@ def bench_cfg5(args, dev):
     SPARCMixer -> Linear(2M -> 768), residual; M = 768*16 = 12288), bf16
     weights and activations, B=16, T=2048, token embeddings ~ N(0, 1).  One
     step = forward, backward (loss: mean square of the output) and an AdamW
-    update.  The projections are 6 * tokens * 12 * 2 * 768 * 24576 = 89.1
-    TFLOP per step (hipBLASLt GEMMs through torch); the mixers run the fused
-    HIP sequence path."""
-    from sparc_amd.stack import SPARCStack
+    update (torch's fused AdamW kernel).  The projections are 6 * tokens * 12
+    * 2 * 768 * 24576 = 89.1 TFLOP per step (hipBLASLt / rocBLAS GEMMs through
+    torch, with the solutions of the stack's TunableOp file when its library
+    versions match); the mixers run the fused HIP sequence path."""
+    from sparc_amd.stack import SPARCStack, use_default_gemms, use_tuned_gemms
     L, d_model, N, B, T = 12, 768, 16, 16, 2048
     torch.manual_seed(0)
     model = SPARCStack(L, d_model, N).to(dev).to(torch.bfloat16)
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, foreach=True)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)
+    tuned = use_tuned_gemms()
     x = torch.randn(B, T, d_model, device=dev, dtype=torch.bfloat16)
 
     def step():
@@ -262,11 +264,14 @@ def bench_cfg5(args, dev):
         raise RuntimeError("cfg5: non-finite loss")
     ms = elapsed * 1e3 / steps
     flop = 6.0 * B * T * L * 2 * d_model * 2 * d_model * N
+    use_default_gemms()
     del model, opt, x
     torch.cuda.empty_cache()
     return {"workload": "12 SPARC blocks (RMSNorm, Linear 768->24576, SPARCMixer, Linear 24576->768), "
                         "fwd + bwd + AdamW", "layers": L, "d_model": d_model, "N": N, "B": B, "T": T,
-            "dtype": "bf16", "steps": steps, "ms_per_step": round(ms, 2),
+            "dtype": "bf16", "optimizer": "AdamW (fused)",
+            "gemm_solutions": "sparc_amd/tuning/gemm_stack_gfx950.csv" if tuned else "torch default",
+            "steps": steps, "ms_per_step": round(ms, 2),
             "tokens_per_s": round(B * T / (ms * 1e-3), 1), "gemm_tflop_per_step": round(flop / 1e12, 1),
             "model_tflops": round(flop / (ms * 1e-3) / 1e12, 1)}
 

@@ -14,6 +14,8 @@ benchmarked in.
 """
 from __future__ import annotations
 
+import os
+
 import torch
 import torch.nn.functional as F
 from torch import nn
@@ -61,9 +63,34 @@ class SPARCStack(nn.Module):
         return self.norm(x)
 
 
+GEMM_TUNING_FILE = os.path.join(os.path.dirname(__file__), "tuning", "gemm_stack_gfx950.csv")
+
+
+def use_tuned_gemms(path: str = GEMM_TUNING_FILE) -> bool:
+    """Route torch's GEMMs through TunableOp with the solutions recorded in
+    ``path`` (by default the stack's shapes measured on MI355X, written by
+    ``python -m sparc_amd.tuning.tune_stack_gemms``).  Tuning stays off:
+    shapes missing from the file keep torch's default solution, and nothing
+    is written back.  Returns whether the file was accepted (its validator
+    lines must match this torch, HIP, hipBLASLt, rocBLAS and GPU).  The
+    setting is process-wide; ``use_default_gemms()`` undoes it."""
+    import torch.cuda.tunable as tn
+    tn.enable(True)
+    tn.tuning_enable(False)
+    tn.set_filename(path)
+    return bool(tn.read_file(path))
+
+
+def use_default_gemms() -> None:
+    """Switch TunableOp off again (torch's default GEMM solutions)."""
+    import torch.cuda.tunable as tn
+    tn.enable(False)
+
+
 def rms_norm_reference(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """RMSNorm as torch.nn.RMSNorm computes it (for references in other dtypes)."""
     return F.rms_norm(x, (x.shape[-1],), weight, eps)
 
 
-__all__ = ["SPARCBlock", "SPARCStack", "rms_norm_reference"]
+__all__ = ["SPARCBlock", "SPARCStack", "rms_norm_reference", "use_tuned_gemms", "use_default_gemms",
+           "GEMM_TUNING_FILE"]

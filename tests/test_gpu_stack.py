@@ -87,3 +87,36 @@ def test_stack_bf16_training_step(fold, monkeypatch):
         assert p.grad is not None and torch.isfinite(p.grad.float()).all(), n
     opt.step()
     assert not torch.equal(before, model.blocks[0].in_proj.weight)
+
+
+def test_tuned_gemms_match_default():
+    """The stack's TunableOp file is accepted on this GPU, and one block at the
+    cfg5 shape (B=16, T=2048, d_model=768, N=16, bf16) gives the same output
+    and input gradient with the recorded GEMM solutions as with torch's
+    defaults (tolerance 2e-2, bf16), with a fused AdamW step after."""
+    print("[case] stack tuned gemms 1 layer B=16 T=2048 d_model=768 N=16 bf16", flush=True)
+    from sparc_amd.stack import use_default_gemms, use_tuned_gemms
+    torch.manual_seed(0)
+    model = SPARCStack(1, 768, 16).cuda().to(torch.bfloat16)
+    x = torch.randn(16, 2048, 768, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    dy = torch.randn_like(x)
+
+    def run():
+        out = model(x)
+        (gx,) = torch.autograd.grad(out, [x], dy)
+        return out.detach(), gx
+
+    ref, ref_gx = run()
+    try:
+        assert use_tuned_gemms()
+        got, got_gx = run()
+        opt = torch.optim.AdamW(model.parameters(), lr=1e-3, fused=True)
+        model(x).float().square().mean().backward()
+        opt.step()
+        torch.cuda.synchronize()
+    finally:
+        use_default_gemms()
+    assert rel_err(got, ref) <= 2e-2
+    assert rel_err(got_gx, ref_gx) <= 2e-2
+    for n, p in model.named_parameters():
+        assert torch.isfinite(p.float()).all(), n
