@@ -380,6 +380,34 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
                                   float* dwrite_radial_response, void* workspace, size_t workspace_bytes,
                                   sparc_stream_t stream);
 
+/* ---- the controls alone (make_controls) ----------------------------------
+ * Rows x [rows, width] (io_dtype, width a positive multiple of 8, 16-byte
+ * aligned) against two directions [width + 1] fp32 (the bias last, 16-byte
+ * aligned): delta = pi/2 tanh(x.phase_direction), eta = log16
+ * tanh(x.radial_direction), one fp32 value per row.  The mixer entry points
+ * above run the same kernels over the module's input (width 2M); these take
+ * any width, e.g. a normalised input whose projection the directions have
+ * been folded into.  Replaces make_controls
+ * (sparc-kernal/forward/control.py:129-139). */
+sparc_status sparc_controls_forward(int64_t rows, int64_t width, int32_t io_dtype, const void* x,
+                                    const float* phase_direction, const float* radial_direction, float* eta,
+                                    float* delta, sparc_stream_t stream);
+
+/* Workspace bytes of sparc_controls_backward (0: invalid shape). */
+size_t sparc_controls_workspace_bytes(int64_t rows, int64_t width);
+
+/* The backward of sparc_controls_forward given deta, ddelta [rows] fp32:
+ * dx [rows, width] (io_dtype) += dp_phase * phase_direction + dp_radial *
+ * radial_direction in place (dp: the gradients of the two dot products), and
+ * the direction gradients [width + 1] fp32, bias last, overwritten.
+ * Deterministic.  Replaces the autograd of make_controls' tanh and F.linear
+ * (sparc-kernal/forward/control.py:129-139). */
+sparc_status sparc_controls_backward(int64_t rows, int64_t width, int32_t io_dtype, const void* x,
+                                     const float* phase_direction, const float* radial_direction, const float* eta,
+                                     const float* delta, const float* deta, const float* ddelta, void* dx,
+                                     float* dphase_direction, float* dradial_direction, void* workspace,
+                                     size_t workspace_bytes, sparc_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

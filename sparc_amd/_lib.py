@@ -46,6 +46,9 @@ EXPORTED_SYMBOLS = (
     "sparc_mixer_backward",
     "sparc_mixer_scan_forward",
     "sparc_mixer_scan_backward",
+    "sparc_controls_forward",
+    "sparc_controls_workspace_bytes",
+    "sparc_controls_backward",
     "sparc_last_error",
     "sparc_version",
 )
@@ -125,6 +128,12 @@ def load() -> ctypes.CDLL:
         lib.sparc_mixer_scan_forward.restype = ctypes.c_int
         lib.sparc_mixer_scan_backward.argtypes = [_I64, _I64, _I64, _I32] + [_P] * 22 + [_SZ, _P]
         lib.sparc_mixer_scan_backward.restype = ctypes.c_int
+        lib.sparc_controls_forward.argtypes = [_I64, _I64, _I32] + [_P] * 6
+        lib.sparc_controls_forward.restype = ctypes.c_int
+        lib.sparc_controls_workspace_bytes.argtypes = [_I64, _I64]
+        lib.sparc_controls_workspace_bytes.restype = _SZ
+        lib.sparc_controls_backward.argtypes = [_I64, _I64, _I32] + [_P] * 11 + [_SZ, _P]
+        lib.sparc_controls_backward.restype = ctypes.c_int
         lib.sparc_last_error.argtypes = []
         lib.sparc_last_error.restype = ctypes.c_char_p
         lib.sparc_version.argtypes = []

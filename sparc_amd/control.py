@@ -1,9 +1,11 @@
 """P1 controls and write prologue.
 
-``make_controls`` keeps the reference's torch formulation
-(sparc-kernal/forward/control.py:129-139); the write ``gain * tanh(x)`` and
-its backward run as HIP kernels (sparc_write_forward / sparc_write_backward)
-in place of ``_latest_write_forward`` / ``_latest_write_backward``
+``make_controls`` (sparc-kernal/forward/control.py:129-139) runs as HIP
+kernels (sparc_controls_forward / sparc_controls_backward) for inputs whose
+width is a multiple of 8, and in the reference's torch formulation
+otherwise; the write ``gain * tanh(x)`` and its backward run as HIP kernels
+(sparc_write_forward / sparc_write_backward) in place of
+``_latest_write_forward`` / ``_latest_write_backward``
 (sparc-kernal/forward/control.py:166-195, backward/control.py:10-89).
 """
 from __future__ import annotations
@@ -20,13 +22,68 @@ LOG16 = math.log(16.0)
 HALF_PI = math.pi / 2.0
 
 
+def aligned16(t: torch.Tensor) -> torch.Tensor:
+    """``t`` contiguous with a 16-byte aligned start (a copy if needed)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+class _Controls(torch.autograd.Function):
+    """eta, delta of rows x [..., W] against two directions [W + 1] (bias
+    last) through sparc_controls_forward / sparc_controls_backward."""
+
+    @staticmethod
+    def forward(ctx, x, phase_direction, radial_direction):
+        lib = _lib.load()
+        dev = _lib.require_gpu(x, phase_direction, radial_direction)
+        W = x.shape[-1]
+        rows = x.numel() // W
+        x2 = aligned16(x)
+        pd = aligned16(phase_direction.detach().float())
+        rd = aligned16(radial_direction.detach().float())
+        eta = torch.empty(x.shape[:-1], dtype=torch.float32, device=dev)
+        delta = torch.empty_like(eta)
+        P = _lib.ptr
+        _lib.check(lib.sparc_controls_forward(rows, W, _lib.io_code(x.dtype), P(x2), P(pd), P(rd), P(eta), P(delta),
+                                              _lib.stream_of(dev)), "sparc_controls_forward")
+        ctx.save_for_backward(x2, pd, rd, eta, delta)
+        ctx.dtypes = (phase_direction.dtype, radial_direction.dtype)
+        return eta, delta
+
+    @staticmethod
+    def backward(ctx, deta, ddelta):
+        x2, pd, rd, eta, delta = ctx.saved_tensors
+        lib = _lib.load()
+        dev = x2.device
+        W = x2.shape[-1]
+        rows = x2.numel() // W
+        deta = torch.zeros_like(eta) if deta is None else deta.float().contiguous()
+        ddelta = torch.zeros_like(delta) if ddelta is None else ddelta.float().contiguous()
+        dx = torch.zeros_like(x2)  # the kernel adds the controls' term in place
+        dpd = torch.empty(W + 1, dtype=torch.float32, device=dev)
+        drd = torch.empty_like(dpd)
+        ws = torch.empty(lib.sparc_controls_workspace_bytes(rows, W), dtype=torch.uint8, device=dev)
+        P = _lib.ptr
+        _lib.check(lib.sparc_controls_backward(
+            rows, W, _lib.io_code(x2.dtype), P(x2), P(pd), P(rd), P(eta), P(delta), P(deta), P(ddelta), P(dx),
+            P(dpd), P(drd), P(ws), ws.numel(), _lib.stream_of(dev)), "sparc_controls_backward")
+        return dx, dpd.to(ctx.dtypes[0]), drd.to(ctx.dtypes[1])
+
+
+def controls_supported(x: torch.Tensor) -> bool:
+    return x.is_cuda and x.dtype in (torch.float32, torch.bfloat16) and x.shape[-1] % 8 == 0 and x.numel() > 0
+
+
 def make_controls(module, x: torch.Tensor):
     """(eta, delta) fp32 [B, L]: eta = log16*tanh(x.u_r + b_r),
     delta = (pi/2)*tanh(x.u_p + b_p).  sparc-kernal/forward/control.py:129-139."""
+    inactive_energy_slot = 0.0 * module.energy_response.sum()
+    if controls_supported(x):
+        eta, delta = _Controls.apply(x, module.phase_direction, module.radial_direction)
+        return eta + inactive_energy_slot, delta
     directions = torch.stack((module.phase_direction, module.radial_direction))
     with torch.autocast(device_type=x.device.type, enabled=False):
         projected = F.linear(x.float(), directions[:, :-1].float(), directions[:, -1].float())
-        inactive_energy_slot = 0.0 * module.energy_response.sum()
         return (
             LOG16 * torch.tanh(projected[..., 1]) + inactive_energy_slot,
             HALF_PI * torch.tanh(projected[..., 0]),

@@ -12,17 +12,20 @@
 //      and the state h in the I/O dtype (saved for the backward, as the
 //      reference saves out_r / out_i).
 // Backward (sparc_mixer_backward):
-//   4. mixer_bwd_kernel: one chain per workgroup in reverse time.  Wave 0
-//      runs the adjoint lambda_t = mask_t dy_t + conj(a_{t+1}) lambda_{t+1},
-//      writes the write path's dx, and accumulates per-mode parameter
-//      gradients in registers; its per-(step, lane) contributions to
-//      d eta_t and d delta_t go through LDS to wave 1, which sums them over
-//      the lanes and stores one partial per (token, mode block).
-//   5. deterministic reductions: per token over mode blocks, per mode over
-//      batch rows.
+//   4. mixer_bwd_kernel: one wave per chain in reverse time: the adjoint
+//      lambda_t = mask_t dy_t + conj(a_{t+1}) lambda_{t+1}, the write path's
+//      dx and the per-mode parameter gradients (in registers); each step's
+//      per-lane contributions to d eta_t and d delta_t are summed over the
+//      lanes in the wave (reduce-scatter) into one partial per (token, mode
+//      block).
+//   5. deterministic column sums: per token over the mode blocks, per mode
+//      over the batch rows.
 //   6. ctrl_bwd_kernel: dx += d p0_t * u_phase + d p1_t * u_radial (the
 //      controls' input gradient) in place, and the direction gradients as
 //      partial sums over row blocks.
+// sparc_mixer_scan_forward / _backward run 1 + 3 / 4 + 5 (the controls are
+// the caller's); sparc_controls_forward / _backward run 2 / 6 alone over rows
+// of any width that is a multiple of 8.
 //
 // Reference replaced: make_controls / make_scan_inputs / _latest_write_forward
 // (sparc-kernal/forward/control.py:129-195), _SPARCChunkScan forward and
@@ -53,6 +56,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kS = SPARC_MIXER_FWD_S;  // steps per prefetched block of the forward scan
 constexpr int kCtrlRows = 16;  // rows per workgroup of the controls forward
 constexpr int kCtrlBwdRows = 128;  // rows per workgroup of the controls backward
+constexpr int kMaxRowBlocks = 65535;  // grid.y limit: more row blocks loop in the workgroups
 
 struct Args {
   int B, T, M, n_mb;
@@ -132,18 +136,20 @@ __device__ __forceinline__ void wave_reduce_scatter(float (&v)[N], int lane) {
 // ---------------------------------------------------------------------------
 // controls forward: eta = log16 tanh(x.u_r + b_r), delta = pi/2 tanh(x.u_p + b_p)
 // ---------------------------------------------------------------------------
-// A workgroup takes kCtrlRows rows; each thread 8 consecutive inputs per pass,
-// the direction values it loads serving every row of the workgroup.
-template <typename IO>
-__global__ void __launch_bounds__(256)
+// A workgroup of NW waves takes kCtrlRows rows; each thread 8 consecutive
+// inputs per pass, the direction values it loads serving every row of the
+// workgroup.  One wave for rows of up to 1024 inputs (no idle waves in the
+// reduction), four above.
+template <typename IO, int NW>
+__global__ void __launch_bounds__(NW * 64)
 ctrl_fwd_kernel(int64_t R, int W, const void* x, const float* pdir, const float* rdir,
                 float* eta, float* delta) {
-  __shared__ float red[4][2 * kCtrlRows];
+  __shared__ float red[NW][2 * kCtrlRows];
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kCtrlRows;
   float acc[2 * kCtrlRows];
 #pragma unroll
   for (int i = 0; i < 2 * kCtrlRows; ++i) acc[i] = 0.0f;
-  for (int c = threadIdx.x * 8; c < W; c += 256 * 8) {
+  for (int c = threadIdx.x * 8; c < W; c += NW * 64 * 8) {
     float u0[8], u1[8];
     *reinterpret_cast<float4*>(u0) = *reinterpret_cast<const float4*>(pdir + c);
     *reinterpret_cast<float4*>(u0 + 4) = *reinterpret_cast<const float4*>(pdir + c + 4);
@@ -179,11 +185,21 @@ ctrl_fwd_kernel(int64_t R, int W, const void* x, const float* pdir, const float*
     if (r0 + r < R) {
       float p0 = pdir[W], p1 = rdir[W];  // the bias entries
 #pragma unroll
-      for (int w = 0; w < 4; ++w) { p0 += red[w][2 * r]; p1 += red[w][2 * r + 1]; }
+      for (int w = 0; w < NW; ++w) { p0 += red[w][2 * r]; p1 += red[w][2 * r + 1]; }
       eta[r0 + r] = kLog16 * tanhf(p1);
       delta[r0 + r] = kHalfPi * tanhf(p0);
     }
   }
+}
+
+template <typename IO>
+void launch_ctrl_fwd(hipStream_t st, int64_t R, int W, const void* x, const float* pdir, const float* rdir,
+                     float* eta, float* delta) {
+  const dim3 g(static_cast<unsigned>((R + kCtrlRows - 1) / kCtrlRows));
+  if (W <= 1024)
+    hipLaunchKernelGGL((ctrl_fwd_kernel<IO, 1>), g, dim3(64), 0, st, R, W, x, pdir, rdir, eta, delta);
+  else
+    hipLaunchKernelGGL((ctrl_fwd_kernel<IO, 4>), g, dim3(256), 0, st, R, W, x, pdir, rdir, eta, delta);
 }
 
 // ---------------------------------------------------------------------------
@@ -632,35 +648,21 @@ __global__ void fill_zero_f32_kernel(float* p, int64_t n) {
   if (i < n) p[i] = 0.0f;
 }
 
-// d eta, d delta per token: the sum of the mode-block partials [n_mb][R]
-__global__ void __launch_bounds__(256)
-token_sum_kernel(int64_t R, int n_mb, const float* part, float* deta, float* ddelta) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (r >= R) return;
-  float s0 = 0.0f, s1 = 0.0f;
-  for (int j = 0; j < n_mb; ++j) {
-    s0 += part[static_cast<int64_t>(j) * R + r];
-    s1 += part[(static_cast<int64_t>(n_mb) + j) * R + r];
-  }
-  deta[r] = s0;
-  ddelta[r] = s1;
-}
-
 // ---------------------------------------------------------------------------
 // controls backward: dx += dp0 u_phase + dp1 u_radial (in place), direction
 // gradient partials per row block
 // ---------------------------------------------------------------------------
 // dp1 = d eta * log16 (1 - tanh^2 p1) = d eta * log16 (1 - (eta/log16)^2),
 // dp0 = d delta * pi/2 (1 - (delta/(pi/2))^2).  A workgroup: 2048 columns (8
-// per thread) of kCtrlBwdRows rows.
+// per thread) of the row blocks blockIdx.y, blockIdx.y + gridDim.y, ... of
+// `rows` rows each; its partial direction gradients go to partial row
+// blockIdx.y.
 template <typename IO>
 __global__ void __launch_bounds__(256)
-ctrl_bwd_kernel(int64_t R, int W, const void* x, const float* pdir, const float* rdir,
+ctrl_bwd_kernel(int64_t R, int W, int rows, const void* x, const float* pdir, const float* rdir,
                 const float* eta, const float* delta, const float* deta, const float* ddelta,
                 void* dx, float* pd, float* pbias) {
   const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kCtrlBwdRows;
-  const int64_t r1 = r0 + kCtrlBwdRows < R ? r0 + kCtrlBwdRows : R;
   const bool col_ok = c < W;
   const int cc = col_ok ? c : 0;
   float u0[8], u1[8], a0[8], a1[8];
@@ -674,61 +676,64 @@ ctrl_bwd_kernel(int64_t R, int W, const void* x, const float* pdir, const float*
   // rows in groups of kG: every load of the group is issued before any of
   // its arithmetic (rows past r1 re-read row r1-1 and contribute nothing)
   constexpr int kG = 4;
-  auto load8 = [&](const void* base, int64_t row, float (&o)[8]) {
-    if constexpr (sizeof(IO) == 2) {
-      unpack<bf16, 8>(load_raw_nt<bf16, 8>(base, row * W + cc), o);
-    } else {
-      float t[4];
-      unpack<float, 4>(load_raw_nt<float, 4>(base, row * W + cc), t);
-      for (int i = 0; i < 4; ++i) o[i] = t[i];
-      unpack<float, 4>(load_raw_nt<float, 4>(base, row * W + cc + 4), t);
-      for (int i = 0; i < 4; ++i) o[4 + i] = t[i];
-    }
-  };
-  for (int64_t r = r0; r < r1; r += kG) {
-    float xv[kG][8], gv[kG][8], dp0[kG], dp1[kG];
-#pragma unroll
-    for (int k = 0; k < kG; ++k) {
-      const int64_t rr = r + k < r1 ? r + k : r1 - 1;
-      load8(x, rr, xv[k]);
-      load8(dx, rr, gv[k]);
-    }
-#pragma unroll
-    for (int k = 0; k < kG; ++k) {
-      const int64_t rr = r + k < r1 ? r + k : r1 - 1;
-      const float e = eta[rr] * kInvLog16, d = delta[rr] * kTwoOverPi;
-      const bool live = r + k < r1;
-      dp1[k] = live ? deta[rr] * kLog16 * fmaf(-e, e, 1.0f) : 0.0f;
-      dp0[k] = live ? ddelta[rr] * kHalfPi * fmaf(-d, d, 1.0f) : 0.0f;
-      b0 += dp0[k];
-      b1 += dp1[k];
-    }
-#pragma unroll
-    for (int k = 0; k < kG; ++k) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        gv[k][i] = fmaf(dp0[k], u0[i], fmaf(dp1[k], u1[i], gv[k][i]));
-        a0[i] = fmaf(dp0[k], xv[k][i], a0[i]);
-        a1[i] = fmaf(dp1[k], xv[k][i], a1[i]);
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.y) * rows; r0 < R; r0 += static_cast<int64_t>(gridDim.y) * rows) {
+    const int64_t r1 = r0 + rows < R ? r0 + rows : R;
+    auto load8 = [&](const void* base, int64_t row, float (&o)[8]) {
+      if constexpr (sizeof(IO) == 2) {
+        unpack<bf16, 8>(load_raw_nt<bf16, 8>(base, row * W + cc), o);
+      } else {
+        float t[4];
+        unpack<float, 4>(load_raw_nt<float, 4>(base, row * W + cc), t);
+        for (int i = 0; i < 4; ++i) o[i] = t[i];
+        unpack<float, 4>(load_raw_nt<float, 4>(base, row * W + cc + 4), t);
+        for (int i = 0; i < 4; ++i) o[4 + i] = t[i];
       }
-    }
-    if (col_ok) {
+    };
+    for (int64_t r = r0; r < r1; r += kG) {
+      float xv[kG][8], gv[kG][8], dp0[kG], dp1[kG];
 #pragma unroll
       for (int k = 0; k < kG; ++k) {
-        if (r + k >= r1) break;  // wave-uniform
-        const int64_t rr = r + k;
-        if constexpr (sizeof(IO) == 2) {
-          store_raw_nt<bf16, 8>(dx, rr * W + c, pack<bf16, 8>(gv[k]));
-        } else {
-          float t[4];
-          for (int i = 0; i < 4; ++i) t[i] = gv[k][i];
-          store_raw_nt<float, 4>(dx, rr * W + c, pack<float, 4>(t));
-          for (int i = 0; i < 4; ++i) t[i] = gv[k][4 + i];
-          store_raw_nt<float, 4>(dx, rr * W + c + 4, pack<float, 4>(t));
+        const int64_t rr = r + k < r1 ? r + k : r1 - 1;
+        load8(x, rr, xv[k]);
+        load8(dx, rr, gv[k]);
+      }
+#pragma unroll
+      for (int k = 0; k < kG; ++k) {
+        const int64_t rr = r + k < r1 ? r + k : r1 - 1;
+        const float e = eta[rr] * kInvLog16, d = delta[rr] * kTwoOverPi;
+        const bool live = r + k < r1;
+        dp1[k] = live ? deta[rr] * kLog16 * fmaf(-e, e, 1.0f) : 0.0f;
+        dp0[k] = live ? ddelta[rr] * kHalfPi * fmaf(-d, d, 1.0f) : 0.0f;
+        b0 += dp0[k];
+        b1 += dp1[k];
+      }
+#pragma unroll
+      for (int k = 0; k < kG; ++k) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          gv[k][i] = fmaf(dp0[k], u0[i], fmaf(dp1[k], u1[i], gv[k][i]));
+          a0[i] = fmaf(dp0[k], xv[k][i], a0[i]);
+          a1[i] = fmaf(dp1[k], xv[k][i], a1[i]);
+        }
+      }
+      if (col_ok) {
+#pragma unroll
+        for (int k = 0; k < kG; ++k) {
+          if (r + k >= r1) break;  // wave-uniform
+          const int64_t rr = r + k;
+          if constexpr (sizeof(IO) == 2) {
+            store_raw_nt<bf16, 8>(dx, rr * W + c, pack<bf16, 8>(gv[k]));
+          } else {
+            float t[4];
+            for (int i = 0; i < 4; ++i) t[i] = gv[k][i];
+            store_raw_nt<float, 4>(dx, rr * W + c, pack<float, 4>(t));
+            for (int i = 0; i < 4; ++i) t[i] = gv[k][4 + i];
+            store_raw_nt<float, 4>(dx, rr * W + c + 4, pack<float, 4>(t));
+          }
         }
       }
     }
-  }
+  }  // row blocks
   if (col_ok) {
     float* o0 = pd + static_cast<int64_t>(blockIdx.y) * W + c;
     float* o1 = pd + (static_cast<int64_t>(gridDim.y) + blockIdx.y) * W + c;
@@ -795,7 +800,7 @@ Layout layout(int64_t B, int64_t T, int64_t M, int direction) {
   l.V = mixer_v(B, M, direction);
   l.n_mb = static_cast<int>((M + 64 * l.V - 1) / (64 * l.V));
   l.R = B * T;
-  l.n_rb = static_cast<int>((l.R + kCtrlBwdRows - 1) / kCtrlBwdRows);
+  l.n_rb = static_cast<int>(std::min<int64_t>((l.R + kCtrlBwdRows - 1) / kCtrlBwdRows, kMaxRowBlocks));
   auto up = [](size_t n) { return (n + 255) / 256 * 256; };
   size_t off = 256;
   l.consts = off;
@@ -911,8 +916,10 @@ sparc_status scan_backward_impl(const Layout& l, int64_t batch, int64_t length, 
   } else {
     if (l.V == 2) launch_bwd<float, 2>(a, st); else launch_bwd<float, 1>(a, st);
   }
-  hipLaunchKernelGGL(token_sum_kernel, dim3(static_cast<unsigned>((l.R + 255) / 256)), dim3(256), 0, st, l.R, l.n_mb,
-                     part_tok, deta, ddelta);
+  // d eta, d delta per token: the sums over the mode blocks of part_tok [2][n_mb][R]
+  if (sparc_status s = sparc_column_sum(l.n_mb, l.R, part_tok, deta, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(l.n_mb, l.R, part_tok + static_cast<int64_t>(l.n_mb) * l.R, ddelta, 0, stream))
+    return s;
   for (int p = 0; p < 5; ++p)
     if (sparc_status s = sparc_column_sum(batch, modes, part_mode + static_cast<int64_t>(p) * batch * modes, outs[p], 0, stream))
       return s;
@@ -924,6 +931,36 @@ bool params_ok(const float* a, const float* b, const float* c, const float* d, c
   return a && b && c && d && e;
 }
 }  // namespace
+
+// The controls backward over rows of width W: n_cb column blocks of 2048
+// inputs, row blocks of `rows` rows (a multiple of 4 in [16, 128], chosen so
+// that the grid has about 1024 workgroups), and the partial direction
+// gradients pd [2][n_rb][W] and bias partials pbias [2][n_rb] in the workspace.
+struct ControlsLayout {
+  int n_cb = 0, n_rb = 0, rows = 0;
+  size_t pbias = 0, total = 0;
+};
+
+ControlsLayout controls_layout(int64_t R, int64_t W) {
+  ControlsLayout c;
+  c.n_cb = static_cast<int>((W + 2047) / 2048);
+  int64_t rows = (R * c.n_cb + 1023) / 1024;
+  rows = (rows + 3) / 4 * 4;
+  c.rows = static_cast<int>(rows < 16 ? 16 : (rows > kCtrlBwdRows ? kCtrlBwdRows : rows));
+  c.n_rb = static_cast<int>(std::min<int64_t>((R + c.rows - 1) / c.rows, kMaxRowBlocks));
+  auto up = [](size_t n) { return (n + 255) / 256 * 256; };
+  c.pbias = up(static_cast<size_t>(2) * c.n_rb * W * 4);
+  c.total = c.pbias + up(static_cast<size_t>(2) * (c.n_rb > 0 ? c.n_rb : 1) * 4);
+  return c;
+}
+
+sparc_status check_controls(int64_t rows, int64_t width, int32_t io_dtype) {
+  if (io_dtype != SPARC_BF16 && io_dtype != SPARC_F32) return fail(SPARC_EINVAL, "controls: io_dtype must be bf16 or f32");
+  if (rows < 0 || rows > (int64_t(1) << 40)) return fail(SPARC_EINVAL, "controls: rows out of range");
+  if (width < 8 || width % 8 || width > (int64_t(1) << 30))
+    return fail(SPARC_EINVAL, "controls: width must be a positive multiple of 8 (got %lld)", static_cast<long long>(width));
+  return SPARC_OK;
+}
 
 extern "C" {
 
@@ -977,11 +1014,10 @@ sparc_status sparc_mixer_forward(int64_t batch, int64_t length, int64_t modes, i
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int W = 2 * static_cast<int>(modes);
   if (length > 0) {
-    const dim3 gc(static_cast<unsigned>((l.R + kCtrlRows - 1) / kCtrlRows));
     if (io_dtype == SPARC_BF16)
-      hipLaunchKernelGGL(ctrl_fwd_kernel<sparc::bf16>, gc, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction, eta, delta);
+      launch_ctrl_fwd<sparc::bf16>(st, l.R, W, x, phase_direction, radial_direction, eta, delta);
     else
-      hipLaunchKernelGGL(ctrl_fwd_kernel<float>, gc, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction, eta, delta);
+      launch_ctrl_fwd<float>(st, l.R, W, x, phase_direction, radial_direction, eta, delta);
   }
   return scan_forward_impl(l, batch, length, modes, io_dtype, x, eta, delta, nu_log, theta_log, write_log_gain,
                            write_phase_response, write_radial_response, y, h_re, h_im, last_re, last_im,
@@ -1060,11 +1096,11 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
   float* pbias = reinterpret_cast<float*>(ws + l.pbias);
   const dim3 gb(static_cast<unsigned>((W + 2047) / 2048), static_cast<unsigned>(l.n_rb));
   if (io_dtype == SPARC_BF16)
-    hipLaunchKernelGGL(ctrl_bwd_kernel<sparc::bf16>, gb, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction,
-                       eta, delta, deta, ddelta, dx, pd, pbias);
+    hipLaunchKernelGGL(ctrl_bwd_kernel<sparc::bf16>, gb, dim3(256), 0, st, l.R, W, kCtrlBwdRows, x, phase_direction,
+                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias);
   else
-    hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, st, l.R, W, x, phase_direction, radial_direction,
-                       eta, delta, deta, ddelta, dx, pd, pbias);
+    hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, st, l.R, W, kCtrlBwdRows, x, phase_direction,
+                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias);
   // direction gradients: columns 0..W-1 from the row-block partials, the bias from pbias
   const int64_t plane = static_cast<int64_t>(l.n_rb) * W;
   if (sparc_status s = sparc_column_sum(l.n_rb, W, pd, dphase_direction, 0, stream)) return s;
@@ -1073,6 +1109,76 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
   if (sparc_status s = sparc_column_sum(l.n_rb, 1, pbias + l.n_rb, dradial_direction + W, 0, stream)) return s;
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(e));
+}
+
+// ---------------------------------------------------------------------------
+// the controls alone, over rows of any width that is a multiple of 8
+// ---------------------------------------------------------------------------
+size_t sparc_controls_workspace_bytes(int64_t rows, int64_t width) {
+  if (rows < 0 || width < 8 || width % 8 || width > (int64_t(1) << 30)) return 0;
+  const ControlsLayout c = controls_layout(rows, width);
+  return c.total;
+}
+
+sparc_status sparc_controls_forward(int64_t rows, int64_t width, int32_t io_dtype, const void* x,
+                                    const float* phase_direction, const float* radial_direction, float* eta,
+                                    float* delta, sparc_stream_t stream) {
+  if (sparc_status s = check_controls(rows, width, io_dtype)) return s;
+  if (rows == 0) return SPARC_OK;  // nothing to read or write (the pointers may be NULL)
+  if (!x || !phase_direction || !radial_direction || !eta || !delta)
+    return fail(SPARC_EINVAL, "controls forward: NULL pointer");
+  if (!al(x, 16) || !al(phase_direction, 16) || !al(radial_direction, 16))
+    return fail(SPARC_EINVAL, "controls forward: misaligned tensor");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int W = static_cast<int>(width);
+  if (io_dtype == SPARC_BF16)
+    launch_ctrl_fwd<sparc::bf16>(st, rows, W, x, phase_direction, radial_direction, eta, delta);
+  else
+    launch_ctrl_fwd<float>(st, rows, W, x, phase_direction, radial_direction, eta, delta);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "controls forward: %s", hipGetErrorString(e));
+}
+
+sparc_status sparc_controls_backward(int64_t rows, int64_t width, int32_t io_dtype, const void* x,
+                                     const float* phase_direction, const float* radial_direction, const float* eta,
+                                     const float* delta, const float* deta, const float* ddelta, void* dx,
+                                     float* dphase_direction, float* dradial_direction, void* workspace,
+                                     size_t workspace_bytes, sparc_stream_t stream) {
+  if (sparc_status s = check_controls(rows, width, io_dtype)) return s;
+  if (!dphase_direction || !dradial_direction) return fail(SPARC_EINVAL, "controls backward: NULL pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int W = static_cast<int>(width);
+  if (rows == 0) {  // zero direction gradients; the row tensors may be NULL
+    const dim3 gz(static_cast<unsigned>((W + 1 + 255) / 256));
+    for (float* o : {dphase_direction, dradial_direction})
+      hipLaunchKernelGGL(fill_zero_f32_kernel, gz, dim3(256), 0, st, o, static_cast<int64_t>(W + 1));
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "controls backward: %s", hipGetErrorString(e));
+  }
+  if (!x || !phase_direction || !radial_direction || !eta || !delta || !deta || !ddelta || !dx)
+    return fail(SPARC_EINVAL, "controls backward: NULL pointer");
+  const ControlsLayout c = controls_layout(rows, width);
+  if (!workspace || workspace_bytes < c.total)
+    return fail(SPARC_EWORKSPACE, "controls backward: workspace too small (%zu < %zu)", workspace_bytes, c.total);
+  if (!al(x, 16) || !al(dx, 16) || !al(phase_direction, 16) || !al(radial_direction, 16) || !al(workspace, 256))
+    return fail(SPARC_EINVAL, "controls backward: misaligned tensor");
+  char* ws = static_cast<char*>(workspace);
+  float* pd = reinterpret_cast<float*>(ws);
+  float* pbias = reinterpret_cast<float*>(ws + c.pbias);
+  const dim3 gb(static_cast<unsigned>(c.n_cb), static_cast<unsigned>(c.n_rb));
+  if (io_dtype == SPARC_BF16)
+    hipLaunchKernelGGL(ctrl_bwd_kernel<sparc::bf16>, gb, dim3(256), 0, st, rows, W, c.rows, x, phase_direction,
+                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias);
+  else
+    hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, st, rows, W, c.rows, x, phase_direction,
+                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias);
+  const int64_t plane = static_cast<int64_t>(c.n_rb) * W;
+  if (sparc_status s = sparc_column_sum(c.n_rb, W, pd, dphase_direction, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(c.n_rb, W, pd + plane, dradial_direction, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(c.n_rb, 1, pbias, dphase_direction + W, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(c.n_rb, 1, pbias + c.n_rb, dradial_direction + W, 0, stream)) return s;
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "controls backward: %s", hipGetErrorString(e));
 }
 
 }  // extern "C"

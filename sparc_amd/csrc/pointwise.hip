@@ -175,13 +175,46 @@ __global__ void row_sum_kernel(int64_t rows, int64_t cols, const float* in, floa
   out[r] = acc;
 }
 
-// out[c] (+)= sum_r in[r, c]; rows summed in order, one column per thread.
-__global__ void column_sum_kernel(int64_t rows, int64_t cols, const float* in, float* out, int accumulate) {
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
+// out[c] (+)= sum_r in[r, c].  A workgroup of 1024 threads takes cw columns
+// (64, or the power of two >= cols below that) and splits the rows into
+// S = 1024 / cw slices: slice s sums rows s, s + S, s + 2S, ... (four
+// interleaved partial sums, combined in a fixed order), and the slices
+// combine in a fixed binary tree in LDS: the result does not depend on
+// timing, and a long column is read by S threads at once.
+__global__ void __launch_bounds__(1024)
+column_sum_kernel(int64_t rows, int64_t cols, int cw, const float* in, float* out, int accumulate) {
+  __shared__ float red[1024];
+  const int t = threadIdx.x;
+  const int cl = t & (cw - 1), slice = t / cw;
+  const int S = 1024 / cw;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * cw + cl;
   float acc = 0.0f;
-  for (int64_t r = 0; r < rows; ++r) acc += in[r * cols + c];
-  out[c] = accumulate ? out[c] + acc : acc;
+  if (c < cols) {
+    float a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    int64_t r = slice;
+    for (; r + 3 * S < rows; r += 4 * S) {
+      acc += in[r * cols + c];
+      a1 += in[(r + S) * cols + c];
+      a2 += in[(r + 2 * S) * cols + c];
+      a3 += in[(r + 3 * S) * cols + c];
+    }
+    for (; r < rows; r += S) acc += in[r * cols + c];
+    acc = (acc + a1) + (a2 + a3);
+  }
+  red[t] = acc;
+  __syncthreads();
+  for (int h = S / 2; h > 0; h >>= 1) {
+    if (slice < h) red[t] += red[t + h * cw];
+    __syncthreads();
+  }
+  if (slice == 0 && c < cols) out[c] = accumulate ? out[c] + red[t] : red[t];
+}
+
+static void launch_column_sum(hipStream_t st, int64_t rows, int64_t cols, const float* in, float* out, int accumulate) {
+  int cw = 1;
+  while (cw < 64 && cw < cols) cw <<= 1;
+  hipLaunchKernelGGL(column_sum_kernel, dim3(static_cast<unsigned>((cols + cw - 1) / cw)), dim3(1024), 0, st, rows,
+                     cols, cw, in, out, accumulate);
 }
 
 // ---------------------------------------------------------------------------
@@ -671,11 +704,10 @@ sparc_status sparc_write_backward(int64_t rows, int64_t modes, int32_t io_dtype,
   hipLaunchKernelGGL(sparc::row_sum_kernel, gr, dim3(256), 0, st, rows, n_slices, pe, deta);
   hipLaunchKernelGGL(sparc::row_sum_kernel, gr, dim3(256), 0, st, rows, n_slices, pd, ddelta);
   const int64_t plane = n_rb * modes;
-  const dim3 gm(static_cast<unsigned>((modes + 255) / 256));
-  hipLaunchKernelGGL(sparc::column_sum_kernel, gm, dim3(256), 0, st, n_rb, modes, pp, dnu_log, 0);
-  hipLaunchKernelGGL(sparc::column_sum_kernel, gm, dim3(256), 0, st, n_rb, modes, pp + plane, dwrite_log_gain, 0);
-  hipLaunchKernelGGL(sparc::column_sum_kernel, gm, dim3(256), 0, st, n_rb, modes, pp + 2 * plane, dwrite_phase_response, 0);
-  hipLaunchKernelGGL(sparc::column_sum_kernel, gm, dim3(256), 0, st, n_rb, modes, pp + 3 * plane, dwrite_radial_response, 0);
+  sparc::launch_column_sum(st, n_rb, modes, pp, dnu_log, 0);
+  sparc::launch_column_sum(st, n_rb, modes, pp + plane, dwrite_log_gain, 0);
+  sparc::launch_column_sum(st, n_rb, modes, pp + 2 * plane, dwrite_phase_response, 0);
+  sparc::launch_column_sum(st, n_rb, modes, pp + 3 * plane, dwrite_radial_response, 0);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "write backward: %s", hipGetErrorString(e));
 }
@@ -684,8 +716,7 @@ sparc_status sparc_column_sum(int64_t rows, int64_t cols, const float* in, float
                               sparc_stream_t stream) {
   if (rows < 0 || cols <= 0 || !out || (rows > 0 && !in)) return fail2(SPARC_EINVAL, "column_sum: bad arguments");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(sparc::column_sum_kernel, dim3(static_cast<unsigned>((cols + 255) / 256)), dim3(256), 0, st,
-                     rows, cols, in, out, accumulate);
+  sparc::launch_column_sum(st, rows, cols, in, out, accumulate);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "column_sum: %s", hipGetErrorString(e));
 }

@@ -13,6 +13,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .control import aligned16
 
 _PATHS = ("auto", "fused", "composed")
 _path = "auto"
@@ -133,10 +134,6 @@ def fused_sequence(module, x: torch.Tensor):
 # ---------------------------------------------------------------------------
 # the mixer behind its input projection, with the controls folded into it
 # ---------------------------------------------------------------------------
-LOG16 = 2.772588722239781
-HALF_PI = 1.5707963267948966
-
-
 class _ProjectedMixer(torch.autograd.Function):
     """y = SPARCMixer(xn @ W^T) for xn [B, L, D] and the projection W [2M, D].
 
@@ -158,10 +155,17 @@ class _ProjectedMixer(torch.autograd.Function):
         M = W // 2
         x = torch.nn.functional.linear(xn, weight).contiguous()  # [B, T, 2M] in the activation dtype
         dirs = torch.stack((phase_direction, radial_direction)).detach().float()  # [2, 2M + 1]
-        v = dirs[:, :W] @ weight.detach().float()                                  # [2, D]
-        p = torch.addmm(dirs[:, W], xn.detach().reshape(-1, D).float(), v.t())     # [B*T, 2]
-        delta = (HALF_PI * torch.tanh(p[:, 0])).contiguous()
-        eta = (LOG16 * torch.tanh(p[:, 1])).contiguous()
+        # the folded directions [W^T u_phase, b_phase], [W^T u_radial, b_radial]
+        # in rows of a 16-byte multiple (each row a 16-byte aligned vector)
+        v = torch.zeros(2, (D + 4) // 4 * 4, dtype=torch.float32, device=dev)
+        torch.mm(dirs[:, :W], weight.detach().float(), out=v[:, :D])
+        v[:, D] = dirs[:, W]
+        xn2 = aligned16(xn.detach().reshape(-1, D))
+        eta = torch.empty(B * T, dtype=torch.float32, device=dev)
+        delta = torch.empty_like(eta)
+        P = _lib.ptr
+        _lib.check(lib.sparc_controls_forward(B * T, D, _lib.io_code(xn.dtype), P(xn2), P(v[0]), P(v[1]), P(eta),
+                                              P(delta), _lib.stream_of(dev)), "sparc_controls_forward")
         params = [t.detach().float().contiguous() for t in (
             nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response)]
         io = _lib.io_code(x.dtype)
@@ -174,11 +178,10 @@ class _ProjectedMixer(torch.autograd.Function):
         if ws_bytes == 0:
             raise ValueError("invalid shape for the fused mixer")
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-        P = _lib.ptr
         _lib.check(lib.sparc_mixer_scan_forward(
             B, T, M, io, P(x), P(eta), P(delta), *[P(t) for t in params], P(y), P(h_re), P(h_im),
             P(last_re), P(last_im), P(ws), ws.numel(), _lib.stream_of(dev)), "sparc_mixer_scan_forward")
-        ctx.save_for_backward(xn, weight, dirs, v, x, eta, delta, h_re, h_im, *params)
+        ctx.save_for_backward(xn2, weight, dirs, v, x, eta, delta, h_re, h_im, *params)
         ctx.dtypes = [t.dtype for t in (phase_direction, radial_direction, nu_log, theta_log,
                                         write_log_gain, write_phase_response, write_radial_response)]
         ctx.energy = (energy_response.shape, energy_response.dtype)
@@ -186,11 +189,11 @@ class _ProjectedMixer(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy, dlast_re, dlast_im):
-        xn, weight, dirs, v, x, eta, delta, h_re, h_im, *params = ctx.saved_tensors
+        xn2, weight, dirs, v, x, eta, delta, h_re, h_im, *params = ctx.saved_tensors
         lib = _lib.load()
         dev = x.device
         B, T, W = x.shape
-        D = xn.shape[-1]
+        D = xn2.shape[-1]
         M = W // 2
         if dy is None:
             dy = torch.zeros_like(x)
@@ -209,15 +212,20 @@ class _ProjectedMixer(torch.autograd.Function):
             B, T, M, _lib.io_code(x.dtype), P(x), P(eta), P(delta), *[P(t) for t in params],
             P(h_re), P(h_im), P(dy), P(dlast_re), P(dlast_im), P(dx), P(deta), P(ddelta),
             *[P(g) for g in grads], P(ws), ws.numel(), _lib.stream_of(dev)), "sparc_mixer_scan_backward")
-        # the controls: dp0 (phase), dp1 (radial) per token
-        dp = torch.stack((ddelta * HALF_PI * (1.0 - (delta / HALF_PI) ** 2),
-                          deta * LOG16 * (1.0 - (eta / LOG16) ** 2)), dim=1)          # [B*T, 2]
-        xn2 = xn.reshape(-1, D)
+        # the controls over xn: g_xn += dp (W^T u) in place and the folded
+        # directions' gradients dv = [dp^T xn, sum dp] (dp: the gradients of
+        # the two dot products per token)
         dx2 = dx.reshape(-1, W)
-        g_xn = (dx2 @ weight + (dp @ v).to(dx.dtype)).reshape(B, T, D)
-        dpx = dp.t() @ xn2.float()                                                      # [2, D]
+        g_xn = aligned16(dx2 @ weight)                                                 # [B*T, D]
+        dv = torch.empty(2, v.shape[1], dtype=torch.float32, device=dev)
+        cws = torch.empty(lib.sparc_controls_workspace_bytes(B * T, D), dtype=torch.uint8, device=dev)
+        _lib.check(lib.sparc_controls_backward(
+            B * T, D, _lib.io_code(x.dtype), P(xn2), P(v[0]), P(v[1]), P(eta), P(delta), P(deta), P(ddelta),
+            P(g_xn), P(dv[0]), P(dv[1]), P(cws), cws.numel(), _lib.stream_of(dev)), "sparc_controls_backward")
+        dpx = dv[:, :D]                                                                # [2, D]
         g_w = dx2.t() @ xn2 + (dirs[:, :W].t() @ dpx).to(weight.dtype)
-        g_dirs = torch.cat((dpx @ weight.float().t(), dp.sum(0)[:, None]), dim=1)      # [2, 2M + 1]
+        g_dirs = torch.cat((dpx @ weight.float().t(), dv[:, D:D + 1]), dim=1)          # [2, 2M + 1]
+        g_xn = g_xn.reshape(B, T, D)
         out = [g_dirs[0], g_dirs[1], *grads]
         out = [g.to(dt) for g, dt in zip(out, ctx.dtypes)]
         shape, dt = ctx.energy
@@ -226,7 +234,8 @@ class _ProjectedMixer(torch.autograd.Function):
 
 def projected_fused_supported(xn: torch.Tensor, weight: torch.Tensor) -> bool:
     return (xn.is_cuda and xn.dtype in (torch.float32, torch.bfloat16) and weight.dtype == xn.dtype
-            and weight.shape[0] % 8 == 0 and xn.ndim == 3 and xn.shape[0] > 0)
+            and weight.shape[0] % 8 == 0 and xn.ndim == 3 and xn.shape[0] > 0 and xn.shape[-1] % 8 == 0
+            and xn.shape[1] > 0)
 
 
 def projected_sequence(module, xn: torch.Tensor, weight: torch.Tensor):

@@ -133,3 +133,26 @@ def test_cpu_tensors_fail_loudly():
     br = torch.zeros(1, 16, 4)
     with pytest.raises(RuntimeError, match="need GPU tensors"):
         ops.sparc_scan(eta, eta, nu, nu, br, br)
+
+
+def test_controls_entry_points_validate_on_host():
+    """sparc_controls_*: width must be a positive multiple of 8, pointers
+    non-NULL, the workspace large enough; the workspace holds one row of
+    partial direction gradients per row block (at most 65535 row blocks)."""
+    lib = _lib.load()
+    assert lib.sparc_controls_workspace_bytes(10, 12) == 0
+    assert lib.sparc_controls_workspace_bytes(-1, 8) == 0
+    up = lambda n: (n + 255) // 256 * 256
+    # 1000 rows of width 8: 16-row blocks -> 63 blocks
+    assert lib.sparc_controls_workspace_bytes(1000, 8) == up(2 * 63 * 8 * 4) + up(2 * 63 * 4)
+    # 10M rows: 128-row blocks, capped at 65535 (the workgroups loop over the rest)
+    assert lib.sparc_controls_workspace_bytes(10_000_000, 8) == up(2 * 65535 * 8 * 4) + up(2 * 65535 * 4)
+    assert lib.sparc_controls_forward(4, 12, 0, *([None] * 5), None) == 1
+    assert b"multiple of 8" in lib.sparc_last_error()
+    assert lib.sparc_controls_forward(4, 16, 0, *([None] * 5), None) == 1
+    assert b"NULL" in lib.sparc_last_error()
+    assert lib.sparc_controls_forward(4, 16, 7, *([None] * 5), None) == 1
+    assert b"io_dtype" in lib.sparc_last_error()
+    fake = ctypes.c_void_p(256)  # never dereferenced: the size check fails first
+    st = lib.sparc_controls_backward(4, 16, 0, *([fake] * 10), fake, 0, None)
+    assert st == 4 and b"workspace" in lib.sparc_last_error()
