@@ -309,7 +309,9 @@ const char* sparc_version(void);
  * x [B,T,2M] (io_dtype; x[..., :M] feeds the real parts, x[..., M:] the
  * imaginary ones), directions [2M+1] fp32 (the last entry is the bias),
  * parameters [M] fp32.  M must be a multiple of 4; x, y, dy, dx and the
- * directions 16-byte aligned.
+ * directions 16-byte aligned.  With length 0 the per-token tensors (x, y,
+ * h_re, h_im, eta, delta, dy, dx, deta, ddelta) are neither read nor written
+ * and may be NULL; the last state is zero and every gradient is zero.
  * ------------------------------------------------------------------------- */
 /* Workspace bytes of sparc_mixer_forward (direction 0) or _backward (1); 0 if
  * the shape is invalid. */

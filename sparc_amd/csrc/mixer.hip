@@ -976,8 +976,10 @@ sparc_status sparc_mixer_scan_forward(int64_t batch, int64_t length, int64_t mod
                                       void* y, void* h_re, void* h_im, float* last_re, float* last_im,
                                       void* workspace, size_t workspace_bytes, sparc_stream_t stream) {
   if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
-  if (!x || !eta || !delta || !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response) ||
-      !y || !h_re || !h_im)
+  // per-token tensors may be NULL when length is 0 (nothing is read or written)
+  const bool rows = length > 0;
+  if ((rows && (!x || !eta || !delta || !y || !h_re || !h_im)) ||
+      !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response))
     return fail(SPARC_EINVAL, "mixer scan forward: NULL pointer");
   if ((last_re == nullptr) != (last_im == nullptr)) return fail(SPARC_EINVAL, "mixer scan forward: last_re/last_im");
   const Layout l = layout(batch, length, modes, 0);
@@ -999,9 +1001,9 @@ sparc_status sparc_mixer_forward(int64_t batch, int64_t length, int64_t modes, i
                                  float* last_re, float* last_im, void* workspace, size_t workspace_bytes,
                                  sparc_stream_t stream) {
   if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
-  if (!x || !phase_direction || !radial_direction ||
-      !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response) || !eta ||
-      !delta || !y || !h_re || !h_im)
+  const bool rows = length > 0;  // per-token tensors may be NULL when length is 0
+  if ((rows && (!x || !eta || !delta || !y || !h_re || !h_im)) || !phase_direction || !radial_direction ||
+      !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response))
     return fail(SPARC_EINVAL, "mixer forward: NULL pointer");
   if ((last_re == nullptr) != (last_im == nullptr)) return fail(SPARC_EINVAL, "mixer forward: last_re/last_im");
   const Layout l = layout(batch, length, modes, 0);
@@ -1034,8 +1036,9 @@ sparc_status sparc_mixer_scan_backward(int64_t batch, int64_t length, int64_t mo
                                        float* dwrite_radial_response, void* workspace, size_t workspace_bytes,
                                        sparc_stream_t stream) {
   if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
-  if (!x || !eta || !delta || !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response) ||
-      !h_re || !h_im || !dy || !dx || !deta || !ddelta ||
+  const bool rows = length > 0;  // per-token tensors may be NULL when length is 0
+  if ((rows && (!x || !eta || !delta || !h_re || !h_im || !dy || !dx || !deta || !ddelta)) ||
+      !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response) ||
       !params_ok(dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response))
     return fail(SPARC_EINVAL, "mixer scan backward: NULL pointer");
   if ((dlast_re == nullptr) != (dlast_im == nullptr)) return fail(SPARC_EINVAL, "mixer scan backward: dlast_re/dlast_im");
@@ -1062,9 +1065,10 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
                                   float* dwrite_radial_response, void* workspace, size_t workspace_bytes,
                                   sparc_stream_t stream) {
   if (sparc_status s = check_shape(batch, length, modes, io_dtype)) return s;
-  if (!x || !phase_direction || !radial_direction ||
-      !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response) || !eta ||
-      !delta || !h_re || !h_im || !dy || !dx || !dphase_direction || !dradial_direction ||
+  const bool rows = length > 0;  // per-token tensors may be NULL when length is 0
+  if ((rows && (!x || !eta || !delta || !h_re || !h_im || !dy || !dx)) || !phase_direction ||
+      !radial_direction || !dphase_direction || !dradial_direction ||
+      !params_ok(nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response) ||
       !params_ok(dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response))
     return fail(SPARC_EINVAL, "mixer backward: NULL pointer");
   if ((dlast_re == nullptr) != (dlast_im == nullptr)) return fail(SPARC_EINVAL, "mixer backward: dlast_re/dlast_im");

@@ -623,11 +623,11 @@ sparc_status sparc_write_forward(int64_t rows, int64_t modes, int32_t io_dtype, 
   if (rows < 0 || modes <= 0 || modes % 2 || modes > INT32_MAX / 4)
     return fail2(SPARC_EINVAL, "write: rows >= 0, modes > 0 and even required");
   if (io_dtype != SPARC_F32 && io_dtype != SPARC_BF16) return fail2(SPARC_EINVAL, "write: io_dtype");
+  if (rows == 0) return SPARC_OK;  // nothing to read or write (the row tensors may be NULL)
   if (!x || !eta || !delta || !nu_log || !write_log_gain || !write_phase_response || !write_radial_response || !w_re || !w_im)
     return fail2(SPARC_EINVAL, "write: NULL pointer");
   const size_t va = (io_dtype == SPARC_BF16 ? 2 : 4) * 2;
   if (!al(x, va) || !al(w_re, va) || !al(w_im, va)) return fail2(SPARC_EINVAL, "write: misaligned tensor");
-  if (rows == 0) return SPARC_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   dim3 g(static_cast<unsigned>((modes / 2 + 255) / 256), static_cast<unsigned>((rows + sparc::WR - 1) / sparc::WR));
   if (g.y > 65535u * 1024u) return fail2(SPARC_EINVAL, "write: too many rows");
@@ -668,9 +668,18 @@ sparc_status sparc_write_backward(int64_t rows, int64_t modes, int32_t io_dtype,
   if (rows < 0 || modes <= 0 || modes % 2 || modes > INT32_MAX / 4)
     return fail2(SPARC_EINVAL, "write backward: rows >= 0, modes > 0 and even required");
   if (io_dtype != SPARC_F32 && io_dtype != SPARC_BF16) return fail2(SPARC_EINVAL, "write backward: io_dtype");
-  if (!x || !eta || !delta || !nu_log || !write_log_gain || !write_phase_response || !write_radial_response ||
-      !dw_re || !dw_im || !dx || !deta || !ddelta || !dnu_log || !dwrite_log_gain || !dwrite_phase_response ||
-      !dwrite_radial_response)
+  if (!nu_log || !write_log_gain || !write_phase_response || !write_radial_response || !dnu_log ||
+      !dwrite_log_gain || !dwrite_phase_response || !dwrite_radial_response)
+    return fail2(SPARC_EINVAL, "write backward: NULL pointer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (rows == 0) {  // zero parameter gradients; the row tensors and the workspace may be NULL
+    const dim3 gz(static_cast<unsigned>((modes + 255) / 256));
+    for (float* o : {dnu_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response})
+      hipLaunchKernelGGL(sparc::fill_zero_kernel, gz, dim3(256), 0, st, o, modes);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "write backward: %s", hipGetErrorString(e));
+  }
+  if (!x || !eta || !delta || !dw_re || !dw_im || !dx || !deta || !ddelta)
     return fail2(SPARC_EINVAL, "write backward: NULL pointer");
   int64_t n_slices, n_rb;
   size_t need;
@@ -679,17 +688,9 @@ sparc_status sparc_write_backward(int64_t rows, int64_t modes, int32_t io_dtype,
   const size_t va = (io_dtype == SPARC_BF16 ? 2 : 4) * 2;
   if (!al(x, va) || !al(dw_re, va) || !al(dw_im, va) || !al(dx, va) || !al(workspace, 256))
     return fail2(SPARC_EINVAL, "write backward: misaligned tensor");
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   float* pe = static_cast<float*>(workspace);
   float* pd = pe + rows * n_slices;
   float* pp = pd + rows * n_slices;
-  if (rows == 0) {
-    const dim3 gz(static_cast<unsigned>((modes + 255) / 256));
-    for (float* o : {dnu_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response})
-      hipLaunchKernelGGL(sparc::fill_zero_kernel, gz, dim3(256), 0, st, o, modes);
-    hipError_t e = hipGetLastError();
-    return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "write backward: %s", hipGetErrorString(e));
-  }
   dim3 g(static_cast<unsigned>(n_slices), static_cast<unsigned>(n_rb));
   if (io_dtype == SPARC_BF16)
     hipLaunchKernelGGL(sparc::write_bwd_kernel<sparc::bf16>, g, dim3(256), 0, st, rows, static_cast<int>(modes),

@@ -290,3 +290,51 @@ def test_fused_mixer_deterministic():
             assert torch.equal(a, b)
     finally:
         sparc_amd.set_mixer_path("auto")
+
+
+def _module_vs_oracle(m, B, L, width, seed):
+    g = torch.Generator().manual_seed(seed)
+    x_in = torch.randn(B, L, width, generator=g, dtype=torch.float64)
+    p = oracle_params(m)
+    dy = _masked_dy(p, x_in, torch.randn(B, L, width, generator=g, dtype=torch.float64), band=1e-3)
+    dl = torch.randn(B, width // 2, generator=g, dtype=torch.float64)
+    x = x_in.float().cuda().requires_grad_()
+    y, cache = m(x, return_cache=True)
+    loss = (y * dy.cuda().float()).sum() + (cache[0] * dl.cuda().float()).sum()
+    grads = torch.autograd.grad(loss, [x] + [getattr(m, n) for n in NAMES])
+    xo = x_in.clone().requires_grad_()
+    yo, lasto = O.mixer_forward(p, xo, return_cache=True)
+    lo = (yo * dy).sum() + (lasto[0] * dl).sum()
+    grads_o = torch.autograd.grad(lo, [xo] + [getattr(p, n) for n in NAMES])
+    assert rel_err(y, yo) <= 1e-4
+    assert rel_err(cache[0], lasto[0]) <= 1e-4 and rel_err(cache[1], lasto[1]) <= 1e-4
+    for name, a, b in zip(["x"] + NAMES, grads, grads_o):
+        assert rel_err(a, b) <= 1e-4, f"grad {name}: {rel_err(a, b):.3g}"
+
+
+def test_module_single_step(mixer_path):
+    """L = 1: one step (a partial block in every kernel)."""
+    print(f"[case] module L=1 B=3 width=16 path={mixer_path}", flush=True)
+    _module_vs_oracle(make_module(16, seed=21).cuda(), 3, 1, 16, seed=22)
+
+
+def test_module_controls_width_not_multiple_of_8():
+    """width 12 (M = 6): the composed path, with the controls in their torch
+    formulation (the HIP controls need a width that is a multiple of 8)."""
+    print("[case] module width=12 B=2 L=19 (auto path)", flush=True)
+    _module_vs_oracle(make_module(12, seed=23).cuda(), 2, 19, 12, seed=24)
+
+
+def test_module_empty_sequence(mixer_path):
+    """L = 0: an empty output, the last state zero, every gradient zero."""
+    print(f"[case] module L=0 B=2 width=16 path={mixer_path}", flush=True)
+    m = make_module(16, seed=25).cuda()
+    x = torch.zeros(2, 0, 16, device="cuda", requires_grad=True)
+    y, cache = m(x, return_cache=True)
+    assert y.shape == (2, 0, 16)
+    assert cache[0].shape == (2, 8) and (cache[0] == 0).all() and (cache[1] == 0).all()
+    dl = torch.randn(2, 8, device="cuda")
+    loss = y.sum() + (cache[0] * dl).sum() + (cache[1] * dl).sum()
+    grads = torch.autograd.grad(loss, [getattr(m, n) for n in NAMES], allow_unused=True)
+    for n, gr in zip(NAMES, grads):
+        assert gr is None or (gr == 0).all(), n
