@@ -106,30 +106,70 @@ mixer_prepare_kernel(int M, const float* nu_log, const float* theta_log, const f
 // ---------------------------------------------------------------------------
 // wave reductions
 // ---------------------------------------------------------------------------
-// N values per lane -> the wave sums of all N: a reduce-scatter butterfly
-// (each xor step keeps half of the values and adds the partner's copy of
-// them), then plain xor steps.  On return lane l holds the sum of value
-// (l / (64 / N)) in v[0].
+// A DPP move of src with the given control; lanes outside BANKS (4-lane
+// banks of each 16-lane row, bit b = lanes 4b..4b+3) keep old.  Every lane of
+// the wave must be active: a DPP read from an inactive lane returns 0.
+template <int CTRL, int BANKS = 0xF>
+__device__ __forceinline__ float dpp_mov(float old, float src) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(src), CTRL, 0xF, BANKS,
+                                                    BANKS == 0xF));
+}
+constexpr int kDppIdentity = 0xE4;  // quad_perm [0, 1, 2, 3]
+constexpr int kDppRowShl = 0x100;   // + n: lane i reads lane i + n of its row
+constexpr int kDppRowShr = 0x110;   // + n: lane i reads lane i - n of its row
+constexpr int kDppRowRor = 0x120;   // + n: lane i reads lane (i - n) mod 16 of its row
+
+// N values per lane -> the wave sums of all N (a reduce-scatter butterfly:
+// each stage exchanges half of the values with the lane 32, 16, 8 or 4 away
+// and keeps the other half).  The 32- and 16-lane stages swap register
+// halves (v_permlane32_swap / v_permlane16_swap: one swap and one add per
+// pair, no selects); the 8- and 4-lane stages choose what to keep and send
+// with bank-masked DPP moves and read the partner through DPP, so nothing
+// goes through LDS and no value is selected by a lane-dependent index.  The
+// rest of each group of lanes is summed into its first lane.  On return the
+// lanes l with l % G == 0 hold in v[0..K-1] the sums of values
+// (l / G) * K ... (l / G) * K + K - 1, with K = max(1, N / 16) and
+// G = 64 K / N; the other lanes hold partial sums.  Fixed order: the result
+// does not depend on timing.
 template <int N>
-__device__ __forceinline__ void wave_reduce_scatter(float (&v)[N], int lane) {
-  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "power of two");
-  int n = N;
+__device__ __forceinline__ void wave_sums_to_leaders(float (&v)[N]) {
+  static_assert(N == 4 || N == 8 || N == 16 || N == 32, "4, 8, 16 or 32 values per lane");
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    if (n > 1) {
-      const bool lo = (lane & o) == 0;
+  for (int i = 0; i < N / 2; ++i) {  // lanes 32 apart: the lower half of the wave keeps values 0 .. N/2-1
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + N / 2]), false, false);
+    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
 #pragma unroll
-      for (int i = 0; i < N / 2; ++i) {
-        if (i < n / 2) {
-          const float send = lo ? v[i + n / 2] : v[i];
-          const float recv = __shfl_xor(send, o, 64);
-          v[i] = (lo ? v[i] : v[i + n / 2]) + recv;
-        }
-      }
-      n >>= 1;
-    } else {
-      v[0] += __shfl_xor(v[0], o, 64);
+  for (int i = 0; i < N / 4; ++i) {  // lanes 16 apart: even rows keep the lower half
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + N / 4]), false, false);
+    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (N >= 8) {
+#pragma unroll
+    for (int i = 0; i < N / 8; ++i) {  // lanes 8 apart: lanes 8-15 of a row (banks 2, 3) keep the upper half
+      const float keep = dpp_mov<kDppIdentity, 0xC>(v[i], v[i + N / 8]);
+      const float send = dpp_mov<kDppIdentity, 0xC>(v[i + N / 8], v[i]);
+      v[i] = keep + dpp_mov<kDppRowRor + 8>(0.0f, send);  // lane ^ 8
     }
+  }
+  if constexpr (N >= 16) {
+#pragma unroll
+    for (int i = 0; i < N / 16; ++i) {  // lanes 4 apart: banks 1, 3 keep the upper half
+      const float keep = dpp_mov<kDppIdentity, 0xA>(v[i], v[i + N / 16]);
+      const float send = dpp_mov<kDppIdentity, 0xA>(v[i + N / 16], v[i]);
+      float recv = dpp_mov<kDppRowShr + 4, 0xA>(0.0f, send);  // banks 1, 3 read lane - 4
+      recv = dpp_mov<kDppRowShl + 4, 0x5>(recv, send);        // banks 0, 2 read lane + 4
+      v[i] = keep + recv;
+    }
+  }
+  constexpr int K = N >= 16 ? N / 16 : 1;
+  constexpr int G = 64 * K / N;  // lanes per group, within one row
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    if constexpr (G >= 16) v[k] += dpp_mov<kDppRowShl + 8>(0.0f, v[k]);
+    if constexpr (G >= 8) v[k] += dpp_mov<kDppRowShl + 4>(0.0f, v[k]);
+    if constexpr (G >= 4) v[k] += dpp_mov<kDppRowShl + 2>(0.0f, v[k]);
+    if constexpr (G >= 2) v[k] += dpp_mov<kDppRowShl + 1>(0.0f, v[k]);
   }
 }
 
@@ -176,9 +216,12 @@ ctrl_fwd_kernel(int64_t R, int W, const void* x, const float* pdir, const float*
     }
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  wave_reduce_scatter<2 * kCtrlRows>(acc, lane);
-  constexpr int per = 64 / (2 * kCtrlRows);  // lanes holding one value
-  if (lane % per == 0) red[wave][lane / per] = acc[0];
+  static_assert(2 * kCtrlRows == 32, "two sums per leader lane below");
+  wave_sums_to_leaders<2 * kCtrlRows>(acc);  // lanes 4k: the sums of values 2k, 2k + 1
+  if (lane % 4 == 0) {
+    red[wave][lane / 2] = acc[0];
+    red[wave][lane / 2 + 1] = acc[1];
+  }
   __syncthreads();
   if (threadIdx.x < kCtrlRows) {
     const int r = threadIdx.x;
@@ -602,14 +645,18 @@ mixer_bwd_kernel(Args a) {
         buf_store<RawT, CPOL_NT>(pack<IO, V>(dxi[s]), rdx, lane_bytes, o + half_x);
       }
     }
-    // the lane sums of the block's 2*kS per-token values: lane l ends with
-    // value l / per
-    wave_reduce_scatter<2 * kS>(e, lane);
-    constexpr int per = 64 / (2 * kS);
-    const int i = lane / per;
-    const int t = t0 + (i >> 1);
-    if (lane % per == 0 && t < a.T)
-      a.part_tok[(static_cast<int64_t>(i & 1) * a.n_mb + mb) * R + row0 + t] = e[0];
+    // the wave sums of the block's 2*kS per-token values: the first lane of
+    // each group of G lanes holds K of them (values i = lane / G * K + k)
+    wave_sums_to_leaders<2 * kS>(e);
+    constexpr int K = 2 * kS >= 16 ? 2 * kS / 16 : 1, G = 64 * K / (2 * kS);
+    if (lane % G == 0) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int i = lane / G * K + k;
+        const int t = t0 + (i >> 1);
+        if (t < a.T) a.part_tok[(static_cast<int64_t>(i & 1) * a.n_mb + mb) * R + row0 + t] = e[k];
+      }
+    }
     unpack<IO, V>(pr[h][0], hcr);
     unpack<IO, V>(pi[h][0], hci);
   };
