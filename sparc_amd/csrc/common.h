@@ -331,6 +331,54 @@ __device__ __forceinline__ void sincos_half(float u, float& s, float& c) {
   c = fmaf(pc, u2, 1.0f);
 }
 
+// ---------------------------------------------------------------------------
+// cross-lane moves (every lane of the wave must be active: a DPP read from an
+// inactive lane returns 0)
+// ---------------------------------------------------------------------------
+// A DPP move of src with the given control; lanes outside BANKS (4-lane
+// banks of each 16-lane row, bit b = lanes 4b..4b+3) keep old.
+template <int CTRL, int BANKS = 0xF>
+__device__ __forceinline__ float dpp_mov(float old, float src) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(src), CTRL, 0xF, BANKS,
+                                                    BANKS == 0xF));
+}
+constexpr int kDppIdentity = 0xE4;     // quad_perm [0, 1, 2, 3]
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]: lane ^ 1
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]: lane ^ 2
+constexpr int kDppRowShl = 0x100;      // + n: lane i reads lane i + n of its row
+constexpr int kDppRowShr = 0x110;      // + n: lane i reads lane i - n of its row
+constexpr int kDppRowRor = 0x120;      // + n: lane i reads lane (i - n) mod 16 of its row
+constexpr int kDppRowMirror = 0x140;   // lane i reads lane 15 - i of its row
+constexpr int kDppHalfMirror = 0x141;  // lane i reads lane 7 - i of its half-row
+
+// x[l] + x[l ^ 16] (PAIR 16) or x[l] + x[l ^ 32] (PAIR 32) in every lane: a
+// swap of the register's row halves with itself (v_permlane16_swap /
+// v_permlane32_swap), no LDS.
+template <int PAIR>
+__device__ __forceinline__ float pair_sum(float x) {
+  const uint32_t u = __float_as_uint(x);
+  if constexpr (PAIR == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    static_assert(PAIR == 32, "16 or 32");
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
+// Sum over aligned groups of lpg lanes (a power of two up to 64, wave-
+// uniform), in every lane of the group.
+__device__ __forceinline__ float group_sum(float x, int lpg) {
+  if (lpg >= 2) x += dpp_mov<kDppXor1>(0.0f, x);
+  if (lpg >= 4) x += dpp_mov<kDppXor2>(0.0f, x);
+  if (lpg >= 8) x += dpp_mov<kDppHalfMirror>(0.0f, x);  // the other quad of the 8 lanes
+  if (lpg >= 16) x += dpp_mov<kDppRowMirror>(0.0f, x);  // the other half of the row
+  if (lpg >= 32) x = pair_sum<16>(x);
+  if (lpg >= 64) x = pair_sum<32>(x);
+  return x;
+}
+
 // tanh(x) = 1 - 2 / (1 + e^{2x}) through one hardware exponential and
 // reciprocal (absolute error ~1e-7; saturates to +-1 through e^{2x} = inf / 0)
 __device__ __forceinline__ float tanh_fast(float x) {

@@ -104,21 +104,8 @@ mixer_prepare_kernel(int M, const float* nu_log, const float* theta_log, const f
 }
 
 // ---------------------------------------------------------------------------
-// wave reductions
+// wave reductions (dpp_mov and the DPP controls: common.h)
 // ---------------------------------------------------------------------------
-// A DPP move of src with the given control; lanes outside BANKS (4-lane
-// banks of each 16-lane row, bit b = lanes 4b..4b+3) keep old.  Every lane of
-// the wave must be active: a DPP read from an inactive lane returns 0.
-template <int CTRL, int BANKS = 0xF>
-__device__ __forceinline__ float dpp_mov(float old, float src) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(src), CTRL, 0xF, BANKS,
-                                                    BANKS == 0xF));
-}
-constexpr int kDppIdentity = 0xE4;  // quad_perm [0, 1, 2, 3]
-constexpr int kDppRowShl = 0x100;   // + n: lane i reads lane i + n of its row
-constexpr int kDppRowShr = 0x110;   // + n: lane i reads lane i - n of its row
-constexpr int kDppRowRor = 0x120;   // + n: lane i reads lane (i - n) mod 16 of its row
-
 // N values per lane -> the wave sums of all N (a reduce-scatter butterfly:
 // each stage exchanges half of the values with the lane 32, 16, 8 or 4 away
 // and keeps the other half).  The 32- and 16-lane stages swap register

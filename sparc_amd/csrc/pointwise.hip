@@ -135,11 +135,8 @@ write_bwd_kernel(int64_t rows, int M, int n_slices, const void* x, const float* 
       store_raw<IO, WV>(dx, r * 2 * M + M + m0, pack<IO, WV>(oxi));
     }
     // block sum of (de, dd): wave butterfly, then the 4 waves in order
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      de += __shfl_xor(de, off, 64);
-      dd += __shfl_xor(dd, off, 64);
-    }
+    de = group_sum(de, 64);
+    dd = group_sum(dd, 64);
     if (lane == 0) { red[0][wave] = de; red[1][wave] = dd; }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -239,11 +236,8 @@ decode_kernel(int M, const void* x, const float* pdir, const float* rdir,
     p0 = fmaf(xv[0], pdir[i], fmaf(xv[1], pdir[i + 1], p0));
     p1 = fmaf(xv[0], rdir[i], fmaf(xv[1], rdir[i + 1], p1));
   }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    p0 += __shfl_xor(p0, off, 64);
-    p1 += __shfl_xor(p1, off, 64);
-  }
+  p0 = group_sum(p0, 64);
+  p1 = group_sum(p1, 64);
   if (lane == 0) { red[0][wave] = p0; red[1][wave] = p1; }
   __syncthreads();
   float s0 = pdir[W], s1 = rdir[W];
@@ -369,11 +363,8 @@ decode_dots_kernel(int B, int W, const void* x, const float* pdir, const float* 
   const int wave = threadIdx.x >> 6;
 #pragma unroll
   for (int r = 0; r < kDotRows; ++r) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      p0[r] += __shfl_xor(p0[r], off, 64);
-      p1[r] += __shfl_xor(p1[r], off, 64);
-    }
+    p0[r] = group_sum(p0[r], 64);
+    p1[r] = group_sum(p1[r], 64);
     if ((threadIdx.x & 63) == 0) { red[r][0][wave] = p0[r]; red[r][1][wave] = p1[r]; }
   }
   __syncthreads();

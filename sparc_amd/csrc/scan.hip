@@ -1185,6 +1185,8 @@ scan_bwd_kernel(ScanArgs p) {
         if constexpr (CPLX) store_raw<GT, V>(p.dg1, row * p.M + m0, pack<GT, V>(d1));
       }
     } else if constexpr (GM == GATE_LANE) {
+      // a runtime group width: one LDS permute per stage (at cfg3, one stage)
+      // is cheaper here than group_sum's branch chain
       float x0 = d0[0], x1 = d1[0];
       for (int off = 1; off < glanes; off <<= 1) {
         x0 += __shfl_xor(x0, off, 64);
@@ -1792,21 +1794,6 @@ chain_bwd_kernel(ScanArgs p) {
 // ---------------------------------------------------------------------------
 constexpr int kFastMaxGpw = 16;  // gate groups per wave handled by the fast kernels
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over aligned groups of lpg lanes (a power of two, uniform), in every lane.
-__device__ __forceinline__ float group_sum(float x, int lpg) {
-  if (lpg >= 2) x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
-  if (lpg >= 4) x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
-  if (lpg >= 8) x += dpp_mov<0x141>(x);  // row_half_mirror: the other quad of the 8 lanes
-  if (lpg >= 16) x += dpp_mov<0x140>(x); // row_mirror: the other half of the 16-lane row
-  if (lpg >= 32) x += __shfl_xor(x, 16, 64);
-  if (lpg >= 64) x += __shfl_xor(x, 32, 64);
-  return x;
-}
 
 constexpr int fast_rounds(int S) { return (S * kFastMaxGpw + 63) / 64; }
 
