@@ -18,6 +18,7 @@ constexpr float kLog16 = 2.772588722239781f;       // log(16)
 constexpr float kInvLog16 = 0.36067376022224085f;  // 1/log(16)
 constexpr float kHalfPi = 1.5707963267948966f;
 constexpr float kTwoOverPi = 0.6366197723675814f;
+constexpr float kLog2e = 1.4426950408889634f;     // log2(e)
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
@@ -313,7 +314,9 @@ constexpr int kDecodeRows = SPARC_DECODE_ROWS;  // rows per update workgroup (co
 #define SPARC_DECODE_PREFETCH 1
 #endif
 
-// consts[m] = (nu, cos theta, sin theta, gamma, 1/expm1(-2 nu), wpr, wrr, theta)
+// consts[m] = (nu, cos theta, sin theta, g2, -log2(e) wpr, -log2(e) wrr, theta, 0)
+// with g2 = 4 gamma^2 / expm1(-2 nu): the gain 2 gamma sqrt(expm1(-2 nu E) /
+// expm1(-2 nu)) sigmoid(q) is then sqrt(g2 expm1(-2 nu E)) / (1 + 2^(q'))
 __global__ void __launch_bounds__(256)
 decode_prepare_kernel(int M, const float* nu_log, const float* theta_log, const float* wlg,
                       const float* wpr, const float* wrr, float* consts) {
@@ -324,8 +327,8 @@ decode_prepare_kernel(int M, const float* nu_log, const float* theta_log, const 
   float sn, cs;
   sincosf(theta, &sn, &cs);
   float4* c = reinterpret_cast<float4*>(consts + static_cast<int64_t>(m) * kDecodeConsts);
-  c[0] = make_float4(nu, cs, sn, expf(wlg[m]));
-  c[1] = make_float4(1.0f / expm1f(-2.0f * nu), wpr[m], wrr[m], theta);
+  c[0] = make_float4(nu, cs, sn, 4.0f * expf(2.0f * wlg[m]) / expm1f(-2.0f * nu));
+  c[1] = make_float4(-kLog2e * wpr[m], -kLog2e * wrr[m], theta, 0.0f);
 }
 
 // part[b, k, 0..1] = partial dot products of row b's inputs with the phase and
@@ -400,13 +403,13 @@ decode_update_kernel(int B, int M, const void* x, const float* pbias, const floa
   }
   __syncthreads();
   if (m0 >= M) return;
-  float nu[SV], ct[SV], stt[SV], gam[SV], cinv[SV], wp[SV], wrr_[SV];
+  float nu[SV], ct[SV], stt[SV], g2[SV], wp[SV], wrr_[SV];
 #pragma unroll
   for (int v = 0; v < SV; ++v) {
     const float4* c = reinterpret_cast<const float4*>(consts + static_cast<int64_t>(m0 + v) * kDecodeConsts);
     const float4 c0 = c[0], c1 = c[1];
-    nu[v] = c0.x; ct[v] = c0.y; stt[v] = c0.z; gam[v] = c0.w;
-    cinv[v] = c1.x; wp[v] = c1.y; wrr_[v] = c1.z;
+    nu[v] = c0.x; ct[v] = c0.y; stt[v] = c0.z; g2[v] = c0.w;
+    wp[v] = c1.x; wrr_[v] = c1.y;
   }
   // Row loads are issued ahead of the stores of earlier rows (the new state
   // may be the old one, in place, so the compiler cannot hoist them itself):
@@ -469,11 +472,9 @@ decode_update_kernel(int B, int M, const void* x, const float* pbias, const floa
       sincos_half(-em * delta, su, cu);            // (1 - rho) * delta
       const float ar = rho * fmaf(ct[v], cu, -stt[v] * su);
       const float ai = rho * fmaf(stt[v], cu, ct[v] * su);
-      // expm1(-2 nu E) = em (2 + em); ratio = sqrt(expm1(-2 nu E) / expm1(-2 nu))
-      const float ratio = __builtin_sqrtf(em * (2.0f + em) * cinv[v]);
-      const float q = fmaf(ps, wp[v], rs * wrr_[v]);
-      const float gate = 2.0f * __builtin_amdgcn_rcpf(1.0f + fast_exp(-q));
-      const float gain = gam[v] * ratio * gate;
+      // expm1(-2 nu E) = em (2 + em); sigmoid(q) = 1 / (1 + 2^(-q log2 e))
+      const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(ps, wp[v], rs * wrr_[v])));
+      const float gain = __builtin_amdgcn_sqrtf(g2[v] * fmaf(em, em, em + em)) * sg;
       const float nr = fmaf(ar, hr[v], fmaf(-ai, hi[v], gain * tanh_fast(xr[v])));
       const float ni = fmaf(ai, hr[v], fmaf(ar, hi[v], gain * tanh_fast(xi[v])));
       hr[v] = nr;
