@@ -429,26 +429,6 @@ __device__ __forceinline__ void wait_stores_complete() {
 
 enum : uint32_t { FLAG_EMPTY = 0, FLAG_AGGREGATE = 1, FLAG_INCLUSIVE = 2 };
 
-// Bounded spin on a flag word (uniform across the wave).  Returns the flag, or
-// FLAG_INCLUSIVE after ``limit`` polls having set *error: a wait that could
-// never end (it cannot, by the ticket order, but the bound makes that a
-// property of the code rather than an assumption) turns into a reported error.
-__device__ __forceinline__ uint32_t poll_flag(const uint32_t* flag, uint32_t* error,
-                                              uint32_t limit) {
-  for (uint32_t it = 0; it < limit; ++it) {
-    uint32_t f = load_agent(flag);
-    f = __builtin_amdgcn_readfirstlane(f);
-    if (f != FLAG_EMPTY) {
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      return f;
-    }
-    // once any wait of this launch has failed, stop waiting at all
-    if ((it & 255u) == 255u && __builtin_amdgcn_readfirstlane(load_agent(error)) != 0u) break;
-    __builtin_amdgcn_s_sleep(2);
-  }
-  store_agent(error, 1u);
-  return FLAG_INCLUSIVE;
-}
 
 }  // namespace sparc
 

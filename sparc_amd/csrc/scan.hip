@@ -22,7 +22,7 @@
 //   4. every wave replays its S steps from its exact start state and stores.
 // Tiles are claimed through an atomic ticket in chunk-major order, so every
 // tile's predecessors were claimed earlier by running workgroups: the
-// look-back waits always end.  The waits are bounded anyway (poll_flag).
+// look-back waits always end.  The waits are bounded anyway (lb_window).
 //
 // The backward runs the same machinery on the adjoint in reverse time
 // (lambda_{t-1} = conj(a_t) lambda_t + dy_{t-1}) after recomputing the
@@ -214,6 +214,48 @@ __device__ __forceinline__ void store_agent_vec(float* p, const float (&v)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i) store_agent(reinterpret_cast<uint32_t*>(p) + i, __float_as_uint(v[i]));
   }
+}
+
+// The look-back walks its chain a window at a time.  Lane i reads the flag of
+// chunk j + i * dir (positions outside the chain read as inclusive: the
+// chain's end chunk always publishes an inclusive carry, so the walk never
+// reaches them).  Returned, wave-uniform: the number n of consecutive chunks
+// from j whose aggregates are published, and whether chunk j + n * dir holds
+// an inclusive carry that ends the walk.  A whole window of aggregates is
+// consumed per flag read, instead of one flag and one aggregate round trip
+// per chunk, so few long chains still move their carry frontier at the rate
+// their tiles finish.  Spins only while chunk j has published nothing, at most
+// `limit` polls: then it sets *error and reports {0, inclusive}, so that every
+// wave still finishes (the host reports the error).
+constexpr int kLbLoads = 4;  // aggregates in flight per composition step (forward)
+#ifndef SPARC_LB_BWD_LOADS
+#define SPARC_LB_BWD_LOADS 1
+#endif
+constexpr int kLbLoadsBwd = SPARC_LB_BWD_LOADS;  // the same, backward (register-bound)
+struct LbWindow {
+  int n;
+  bool incl;
+};
+__device__ __forceinline__ LbWindow lb_window(const uint32_t* flags, int j, int dir, int n_chunks, uint32_t* error,
+                                              uint32_t limit, int lane) {
+  const int jl = j + lane * dir;
+  const bool in_chain = jl >= 0 && jl < n_chunks;
+  for (uint32_t it = 0; it < limit; ++it) {
+    const uint32_t f = in_chain ? load_agent(flags + jl) : uint32_t(FLAG_INCLUSIVE);
+    const uint64_t incl = __ballot(f == FLAG_INCLUSIVE);
+    const uint64_t empty = __ballot(f == FLAG_EMPTY);
+    const int fi = incl ? __builtin_ctzll(incl) : 64;
+    const int fe = empty ? __builtin_ctzll(empty) : 64;
+    if (fi == 0 || fe > 0) {
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      return fi < fe ? LbWindow{fi, true} : LbWindow{fe, false};
+    }
+    // once any wait of this launch has failed, stop waiting at all
+    if ((it & 255u) == 255u && __builtin_amdgcn_readfirstlane(load_agent(error)) != 0u) break;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  store_agent(error, 1u);
+  return LbWindow{0, true};
 }
 
 // ---------------------------------------------------------------------------
@@ -498,11 +540,42 @@ scan_fwd_kernel(ScanArgs p) {
 #pragma unroll
       for (int v = 0; v < V; ++v) { Xpr[v] = 1.0f; Xpi[v] = 0.0f; Xqr[v] = 0.0f; Xqi[v] = 0.0f; }
       int j = chunk - 1;
+      const uint32_t* chain_flags = p.flagv + static_cast<int64_t>(chain) * p.n_chunks;
       while (true) {
-        const uint32_t f = poll_flag(p.flagv + static_cast<int64_t>(chain) * p.n_chunks + j, p.error, p.spin_limit);
-        if (f == FLAG_INCLUSIVE) {
+        const LbWindow w = lb_window(chain_flags, j, -1, p.n_chunks, p.error, p.spin_limit, lane);
+        // compose the aggregates of chunks j, j-1, ..., j-w.n+1 (nearest
+        // first), kLbLoads loads in flight at a time
+        for (int base = 0; base < w.n; base += kLbLoads) {
+          float q[kLbLoads][V * NQ];
+#pragma unroll
+          for (int u = 0; u < kLbLoads; ++u)
+            if (base + u < w.n)
+              agg_load<V * NQ>(p.agg + (static_cast<int64_t>(chain) * p.n_chunks + (j - base - u)) * MB * NQ, lane,
+                               q[u]);
+#pragma unroll
+          for (int u = 0; u < kLbLoads; ++u) {
+            if (base + u >= w.n) break;
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              if constexpr (CPLX) {
+                float nr, ni;
+                cmul(Xpr[v], Xpi[v], q[u][v * 4 + 2], q[u][v * 4 + 3], nr, ni);
+                Xqr[v] += nr;
+                Xqi[v] += ni;
+                cmul(Xpr[v], Xpi[v], q[u][v * 4 + 0], q[u][v * 4 + 1], nr, ni);
+                Xpr[v] = nr;
+                Xpi[v] = ni;
+              } else {
+                Xqr[v] += Xpr[v] * q[u][v * 2 + 1];
+                Xpr[v] *= q[u][v * 2 + 0];
+              }
+            }
+          }
+        }
+        j -= w.n;
+        if (w.incl) {
           float h[V * NH] = {};
-          if (lane_ok)
+          if (lane_ok && j >= 0)
             state_load<V * NH>(p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + j) * p.M + mb0) * NH, lane, h);
 #pragma unroll
           for (int v = 0; v < V; ++v) {
@@ -516,27 +589,6 @@ scan_fwd_kernel(ScanArgs p) {
               ci[v] = 0.0f;
             }
           }
-          break;
-        }
-        float q[V * NQ];
-        agg_load<V * NQ>(p.agg + (static_cast<int64_t>(chain) * p.n_chunks + j) * MB * NQ, lane, q);
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-          if constexpr (CPLX) {
-            float nr, ni;
-            cmul(Xpr[v], Xpi[v], q[v * 4 + 2], q[v * 4 + 3], nr, ni);
-            Xqr[v] += nr;
-            Xqi[v] += ni;
-            cmul(Xpr[v], Xpi[v], q[v * 4 + 0], q[v * 4 + 1], nr, ni);
-            Xpr[v] = nr;
-            Xpi[v] = ni;
-          } else {
-            Xqr[v] += Xpr[v] * q[v * 2 + 1];
-            Xpr[v] *= q[v * 2 + 0];
-          }
-        }
-        if (--j < 0) {  // unreachable: chunk 0 only ever publishes an inclusive carry
-          store_agent(p.error, 2u);
           break;
         }
       }
@@ -980,11 +1032,42 @@ scan_bwd_kernel(ScanArgs p) {
 #pragma unroll
       for (int v = 0; v < V; ++v) { Xpr[v] = 1.0f; Xpi[v] = 0.0f; Xqr[v] = 0.0f; Xqi[v] = 0.0f; }
       int j = chunk + 1;
+      const uint32_t* chain_flags = p.flagv + static_cast<int64_t>(chain) * p.n_chunks;
       while (true) {
-        const uint32_t f = poll_flag(p.flagv + static_cast<int64_t>(chain) * p.n_chunks + j, p.error, p.spin_limit);
-        if (f == FLAG_INCLUSIVE) {
+        const LbWindow w = lb_window(chain_flags, j, 1, p.n_chunks, p.error, p.spin_limit, lane);
+        // compose the aggregates of chunks j, j+1, ..., j+w.n-1 (nearest
+        // first), kLbLoadsBwd loads in flight at a time
+        for (int base = 0; base < w.n; base += kLbLoadsBwd) {
+          float q[kLbLoadsBwd][V * NQ];
+#pragma unroll
+          for (int u = 0; u < kLbLoadsBwd; ++u)
+            if (base + u < w.n)
+              load_agent_vec<V * NQ>(
+                  p.agg + ((static_cast<int64_t>(chain) * p.n_chunks + (j + base + u)) * MB + lane * V) * NQ, q[u]);
+#pragma unroll
+          for (int u = 0; u < kLbLoadsBwd; ++u) {
+            if (base + u >= w.n) break;
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              if constexpr (CPLX) {
+                float nr, ni;
+                cmul(Xpr[v], Xpi[v], q[u][v * 4 + 2], q[u][v * 4 + 3], nr, ni);
+                Xqr[v] += nr;
+                Xqi[v] += ni;
+                cmul(Xpr[v], Xpi[v], q[u][v * 4 + 0], q[u][v * 4 + 1], nr, ni);
+                Xpr[v] = nr;
+                Xpi[v] = ni;
+              } else {
+                Xqr[v] += Xpr[v] * q[u][v * 2 + 1];
+                Xpr[v] *= q[u][v * 2 + 0];
+              }
+            }
+          }
+        }
+        j += w.n;
+        if (w.incl) {
           float h[V * NH] = {};
-          if (lane_ok)
+          if (lane_ok && j < p.n_chunks)
             load_agent_vec<V * NH>(p.carry + ((static_cast<int64_t>(b) * p.n_chunks + j) * p.M + m0) * NH, h);
 #pragma unroll
           for (int v = 0; v < V; ++v) {
@@ -998,27 +1081,6 @@ scan_bwd_kernel(ScanArgs p) {
               ci[v] = 0.0f;
             }
           }
-          break;
-        }
-        float q[V * NQ];
-        load_agent_vec<V * NQ>(p.agg + ((static_cast<int64_t>(chain) * p.n_chunks + j) * MB + lane * V) * NQ, q);
-#pragma unroll
-        for (int v = 0; v < V; ++v) {
-          if constexpr (CPLX) {
-            float nr, ni;
-            cmul(Xpr[v], Xpi[v], q[v * 4 + 2], q[v * 4 + 3], nr, ni);
-            Xqr[v] += nr;
-            Xqi[v] += ni;
-            cmul(Xpr[v], Xpi[v], q[v * 4 + 0], q[v * 4 + 1], nr, ni);
-            Xpr[v] = nr;
-            Xpi[v] = ni;
-          } else {
-            Xqr[v] += Xpr[v] * q[v * 2 + 1];
-            Xpr[v] *= q[v * 2 + 0];
-          }
-        }
-        if (++j >= p.n_chunks) {  // unreachable: the last chunk only publishes an inclusive carry
-          store_agent(p.error, 2u);
           break;
         }
       }
@@ -1198,12 +1260,8 @@ scan_bwd_kernel(ScanArgs p) {
         if constexpr (CPLX) store1<GT>(p.dg1, gi, x1);
       }
     } else {  // GATE_CROSS: wave partial over its modes -> [B*T, n_mblocks]
-      float x0 = d0[0], x1 = d1[0];
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        x0 += __shfl_xor(x0, off, 64);
-        if constexpr (CPLX) x1 += __shfl_xor(x1, off, 64);
-      }
+      const float x0 = group_sum(d0[0], 64);
+      const float x1 = CPLX ? group_sum(d1[0], 64) : 0.0f;
       if (lane == 0 && t_ok) {
         p.part_g0[row * p.n_mblocks + mb] = x0;
         if constexpr (CPLX) p.part_g1[row * p.n_mblocks + mb] = x1;
@@ -1730,12 +1788,8 @@ chain_bwd_kernel(ScanArgs p) {
             if constexpr (CPLX) store1<GT>(p.dg1, gi, x1);
           }
         } else {
-          float x0 = d0[0], x1 = d1[0];
-#pragma unroll
-          for (int off = 1; off < 64; off <<= 1) {
-            x0 += __shfl_xor(x0, off, 64);
-            if constexpr (CPLX) x1 += __shfl_xor(x1, off, 64);
-          }
+          const float x0 = group_sum(d0[0], 64);
+          const float x1 = CPLX ? group_sum(d1[0], 64) : 0.0f;
           if (lane == 0 && t_ok) {
             p.part_g0[row * p.n_mblocks + mb] = x0;
             if constexpr (CPLX) p.part_g1[row * p.n_mblocks + mb] = x1;
