@@ -35,32 +35,35 @@ write_fwd_kernel(int64_t rows, int M, const void* x, const float* eta, const flo
                  void* w_re, void* w_im) {
   const int m0 = (blockIdx.x * 256 + threadIdx.x) * WV;
   if (m0 >= M) return;
-  float nu[WV], den[WV], g0[WV], pr[WV], rr[WV];
+  // per mode: g2 = 4 gamma^2 / (1 - e^{-2 nu}), so the gain 2 gamma
+  // sqrt((1 - e^{-2 nu E}) / (1 - e^{-2 nu})) sigmoid(q) is sqrt(g2 (1 -
+  // e^{-2 nu E})) / (1 + 2^(q')), with q' = -log2(e) q from the scaled
+  // responses ps, rs
+  float nu[WV], g2[WV], ps[WV], rs[WV];
 #pragma unroll
   for (int v = 0; v < WV; ++v) {
     nu[v] = expf(nu_log[m0 + v]);
-    den[v] = -expm1f(-2.0f * nu[v]);
-    g0[v] = expf(wlg[m0 + v]);
-    pr[v] = wpr[m0 + v];
-    rr[v] = wrr[m0 + v];
+    g2[v] = -4.0f * expf(2.0f * wlg[m0 + v]) / expm1f(-2.0f * nu[v]);
+    ps[v] = -kLog2e * kTwoOverPi * wpr[m0 + v];
+    rs[v] = -kLog2e * kInvLog16 * wrr[m0 + v];
   }
   const int64_t r0 = static_cast<int64_t>(blockIdx.y) * WR;
   for (int i = 0; i < WR; ++i) {
     const int64_t r = r0 + i;
     if (r >= rows) break;
     const float e = eta[r], dl = delta[r];
-    const float E = expf(e);
-    const float phase = dl * kTwoOverPi, radial = e * kInvLog16;
+    const float E = fast_exp(e);
     float xr[WV], xi[WV], outr[WV], outi[WV];
     unpack<IO, WV>(load_raw<IO, WV>(x, r * 2 * M + m0), xr);
     unpack<IO, WV>(load_raw<IO, WV>(x, r * 2 * M + M + m0), xi);
 #pragma unroll
     for (int v = 0; v < WV; ++v) {
-      const float ratio = sqrtf(-expm1f(-2.0f * nu[v] * E) / den[v]);
-      const float gate = 2.0f * sigmoidf_(phase * pr[v] + radial * rr[v]);
-      const float gain = g0[v] * ratio * gate;
-      outr[v] = gain * tanhf(xr[v]);
-      outi[v] = gain * tanhf(xi[v]);
+      const float em = expm1_nonpos(-nu[v] * E);  // e^{-nu E} - 1
+      const float num = -fmaf(em, em, em + em);    // 1 - e^{-2 nu E}
+      const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(dl, ps[v], e * rs[v])));
+      const float gain = __builtin_amdgcn_sqrtf(g2[v] * num) * sg;
+      outr[v] = gain * tanh_fast(xr[v]);
+      outi[v] = gain * tanh_fast(xi[v]);
     }
     store_raw<IO, WV>(w_re, r * M + m0, pack<IO, WV>(outr));
     store_raw<IO, WV>(w_im, r * M + m0, pack<IO, WV>(outi));
@@ -86,16 +89,20 @@ write_bwd_kernel(int64_t rows, int M, int n_slices, const void* x, const float* 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m0 = (blockIdx.x * 256 + threadIdx.x) * WV;
   const bool ok = m0 < M;
-  float nu[WV], den[WV], stat[WV], g0[WV], pr[WV], rr[WV];
+  // per mode: g2 and the scaled responses as in the forward; stat = nu
+  // e^{-2 nu} / (1 - e^{-2 nu}); prs, rrs: the responses times 2/pi, 1/log16
+  float nu[WV], stat[WV], g2[WV], ps[WV], rs[WV], prs[WV], rrs[WV];
 #pragma unroll
   for (int v = 0; v < WV; ++v) {
     const int m = ok ? m0 + v : 0;
     nu[v] = expf(nu_log[m]);
-    den[v] = -expm1f(-2.0f * nu[v]);
-    stat[v] = nu[v] * expf(-2.0f * nu[v]) / den[v];
-    g0[v] = expf(wlg[m]);
-    pr[v] = wpr[m];
-    rr[v] = wrr[m];
+    const float den = -expm1f(-2.0f * nu[v]);
+    stat[v] = nu[v] * expf(-2.0f * nu[v]) / den;
+    g2[v] = 4.0f * expf(2.0f * wlg[m]) / den;
+    prs[v] = kTwoOverPi * wpr[m];
+    rrs[v] = kInvLog16 * wrr[m];
+    ps[v] = -kLog2e * prs[v];
+    rs[v] = -kLog2e * rrs[v];
   }
   float acc_nu[WV] = {}, acc_g[WV] = {}, acc_p[WV] = {}, acc_r[WV] = {};
   const int64_t r0 = static_cast<int64_t>(blockIdx.y) * WB;
@@ -103,7 +110,7 @@ write_bwd_kernel(int64_t rows, int M, int n_slices, const void* x, const float* 
     const int64_t r = r0 + i;
     if (r >= rows) break;
     const float e = eta[r], dl = delta[r];
-    const float E = expf(e);
+    const float E = fast_exp(e);
     const float phase = dl * kTwoOverPi, radial = e * kInvLog16;
     float de = 0.0f, dd = 0.0f;
     if (ok) {
@@ -115,18 +122,21 @@ write_bwd_kernel(int64_t rows, int M, int n_slices, const void* x, const float* 
 #pragma unroll
       for (int v = 0; v < WV; ++v) {
         const float eff = nu[v] * E;
-        const float num = -expm1f(-2.0f * eff);
-        const float ratio = sqrtf(num / den[v]);
-        const float gate = 2.0f * sigmoidf_(phase * pr[v] + radial * rr[v]);
-        const float gain = g0[v] * ratio * gate;
-        const float cr = tanhf(xr[v]), ci = tanhf(xi[v]);
-        const float gain_grad = gain * (gr[v] * cr + gi[v] * ci);
-        const float gate_grad = gain_grad * (1.0f - 0.5f * gate);
-        const float dyn = eff * expf(-2.0f * eff) / num;
-        de += gain_grad * dyn + gate_grad * rr[v] * kInvLog16;
-        dd += gate_grad * pr[v] * kTwoOverPi;
-        oxr[v] = gr[v] * gain * (1.0f - cr * cr);
-        oxi[v] = gi[v] * gain * (1.0f - ci * ci);
+        const float em = expm1_nonpos(-eff);
+        const float num = -fmaf(em, em, em + em);  // 1 - e^{-2 eff}
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(dl, ps[v], e * rs[v])));
+        // one reciprocal square root of Y = g2 num gives sqrt(Y) = Y q and
+        // 1 / num = g2 q^2 (the floor keeps a zero gain at zero)
+        const float Y = g2[v] * num, q = __builtin_amdgcn_rsqf(fmaxf(Y, 1e-30f));
+        const float gain = Y * q * sg;
+        const float cr = tanh_fast(xr[v]), ci = tanh_fast(xi[v]);
+        const float gain_grad = gain * fmaf(gr[v], cr, gi[v] * ci);
+        const float gate_grad = gain_grad * (1.0f - sg);
+        const float dyn = eff * fmaf(g2[v], q * q, -1.0f);  // eff e^{-2 eff} / (1 - e^{-2 eff})
+        de += fmaf(gain_grad, dyn, gate_grad * rrs[v]);
+        dd += gate_grad * prs[v];
+        oxr[v] = gr[v] * gain * fmaf(-cr, cr, 1.0f);
+        oxi[v] = gi[v] * gain * fmaf(-ci, ci, 1.0f);
         acc_nu[v] += gain_grad * (dyn - stat[v]);
         acc_g[v] += gain_grad;
         acc_p[v] += gate_grad * phase;
