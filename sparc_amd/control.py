@@ -10,7 +10,6 @@ otherwise; the write ``gain * tanh(x)`` and its backward run as HIP kernels
 """
 from __future__ import annotations
 
-import ctypes
 import math
 
 import torch

@@ -13,7 +13,6 @@ fused into its store).
 from __future__ import annotations
 
 import math
-import re
 
 import torch
 from torch import nn

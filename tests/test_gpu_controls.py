@@ -2,7 +2,6 @@
 129-139) through the C ABI against autograd of the float64 oracle: eta and
 delta (fp32 outputs, tolerance 1e-4), the in-place input gradient (1e-4 fp32,
 2e-2 bf16) and the direction gradients (fp32, 1e-4)."""
-import ctypes
 
 import pytest
 import torch
