@@ -276,6 +276,52 @@ def bench_cfg5(args, dev):
             "model_tflops": round(flop / (ms * 1e-3) / 1e12, 1)}
 
 
+def bench_module(args, dev):
+    """The drop-in module at the headline shape: SPARCMixer(2 * D * N) forward
+    + backward on x [8, 4096, 32768] bf16 (fp32 parameters, initialised as the
+    reference does, controllers and write responses set to small random
+    values so that every term is active).  On this shape the module runs the
+    fused sequence path (controls, write, P1 scan, relu(cat) epilogue and their
+    backward); it is VALU-bound, so the report is time and tokens/s."""
+    import sparc_amd
+    from sparc_amd.mixer import use_fused
+    B, T, W = 8, 4096, 2 * 1024 * 16
+    torch.manual_seed(0)
+    m = sparc_amd.SPARCMixer(W).to(dev)
+    with torch.no_grad():
+        m.phase_direction.normal_(0, 1 / math.sqrt(W))
+        m.radial_direction.normal_(0, 1 / math.sqrt(W))
+        m.write_phase_response.normal_()
+        m.write_radial_response.normal_()
+    x = torch.randn(B, T, W, device=dev, dtype=torch.bfloat16).requires_grad_()
+    dy = torch.randn(B, T, W, device=dev, dtype=torch.bfloat16)
+    path = "fused" if use_fused(x, W // 2) else "composed"
+
+    def step():
+        x.grad = None
+        for p in m.parameters():
+            p.grad = None
+        y, _ = m(x)
+        y.backward(dy)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize(dev)
+    steps = 5
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / steps
+    del m, x, dy
+    torch.cuda.empty_cache()
+    return {"workload": "SPARCMixer forward + backward (the drop-in module), bf16 x, fp32 parameters",
+            "B": B, "T": T, "width": W, "path": path, "steps": steps, "ms_per_step": round(ms, 3),
+            "tokens_per_s": round(B * T / (ms * 1e-3), 1)}
+
+
 def _graph_time_us(dev, n_graph, reps, step_fn):
     """Captures reps HIP graphs of n_graph calls step_fn(i) (i = global step)
     after one eager call, replays them all once untimed and once timed;
@@ -414,6 +460,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cfg3", action="store_true", help="skip the cfg3 (real, T=65536) report")
     ap.add_argument("--no-cfg5", action="store_true", help="skip the cfg5 (12-layer stack) report")
+    ap.add_argument("--no-module", action="store_true", help="skip the module (SPARCMixer) report")
     ap.add_argument("--algo", default="auto", choices=["auto", "serial", "chain", "lookback"],
                     help="scan algorithm (auto picks the serial kernels at this shape)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -438,6 +485,7 @@ def main():
     res = bench_scan(args, dev)
     cfg3 = None if args.no_cfg3 else bench_cfg3(args, dev)
     cfg5 = None if args.no_cfg5 else bench_cfg5(args, dev)
+    module = None if args.no_module else bench_module(args, dev)
     core = None if args.no_decode else bench_decode_core(args, dev)
     dec = None if args.no_decode else bench_decode(args, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
@@ -487,6 +535,7 @@ def main():
                 "us_per_step": round(dec["us_per_step"], 2), "tokens_per_s": round(dec["tokens_per_s"], 1),
                 "steps": dec["steps"], "bytes_per_step": dec["bytes_per_step"], "GB_s": round(dec["gbs"], 1),
                 "form": "SPARCMixer.step (P1 controls and write from x), bf16 x/y, fp32 state in place"}},
+        "module": module,
         "cfg3": cfg3,
         "cfg5": cfg5,
         "cpu_baseline": cpu,
