@@ -185,7 +185,8 @@ int sparc_scan_workspace_error(const void* workspace, sparc_stream_t stream);
  * Replaces _latest_write_forward (sparc-kernal/forward/control.py:166-195).
  *   x [rows, 2M] io_dtype; eta, delta [rows] fp32; nu_log, write_log_gain,
  *   write_phase_response, write_radial_response [M] fp32;
- *   w_re, w_im [rows, M] io_dtype.
+ *   w_re, w_im [rows, M] io_dtype.  With rows = 0 nothing is read or
+ *   written and every pointer may be NULL.
  */
 sparc_status sparc_write_forward(int64_t rows, int64_t modes, int32_t io_dtype,
                                  const void* x, const float* eta, const float* delta,
@@ -202,6 +203,8 @@ size_t sparc_write_workspace_bytes(int64_t rows, int64_t modes);
  *   dw_re, dw_im [rows, M] io_dtype; dx [rows, 2M] io_dtype (written);
  *   deta, ddelta [rows] fp32 (written); dnu_log, dwrite_log_gain,
  *   dwrite_phase_response, dwrite_radial_response [M] fp32 (written).
+ *   With rows = 0 the parameter gradients are zeroed and the row tensors
+ *   and the workspace may be NULL.
  */
 sparc_status sparc_write_backward(int64_t rows, int64_t modes, int32_t io_dtype,
                                   const void* x, const float* eta, const float* delta,
@@ -390,7 +393,8 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
  * tanh(x.radial_direction), one fp32 value per row.  The mixer entry points
  * above run the same kernels over the module's input (width 2M); these take
  * any width, e.g. a normalised input whose projection the directions have
- * been folded into.  Replaces make_controls
+ * been folded into.  With rows = 0 nothing is read or written (the
+ * pointers may be NULL).  Replaces make_controls
  * (sparc-kernal/forward/control.py:129-139). */
 sparc_status sparc_controls_forward(int64_t rows, int64_t width, int32_t io_dtype, const void* x,
                                     const float* phase_direction, const float* radial_direction, float* eta,
@@ -402,7 +406,8 @@ size_t sparc_controls_workspace_bytes(int64_t rows, int64_t width);
 /* The backward of sparc_controls_forward given deta, ddelta [rows] fp32:
  * dx [rows, width] (io_dtype) += dp_phase * phase_direction + dp_radial *
  * radial_direction in place (dp: the gradients of the two dot products), and
- * the direction gradients [width + 1] fp32, bias last, overwritten.
+ * the direction gradients [width + 1] fp32, bias last, overwritten (zero
+ * with rows = 0; the row tensors and the workspace may then be NULL).
  * Deterministic.  Replaces the autograd of make_controls' tanh and F.linear
  * (sparc-kernal/forward/control.py:129-139). */
 sparc_status sparc_controls_backward(int64_t rows, int64_t width, int32_t io_dtype, const void* x,
