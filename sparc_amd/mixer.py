@@ -50,14 +50,18 @@ def use_fused(x: torch.Tensor, modes: int) -> bool:
         return True
     if not ok:
         return False
-    # One wave per chain (batch row x 64 modes) walks all of T in the fused
-    # kernels, so few chains leave most of the GPU idle; the composed path's
-    # look-back scan is parallel over T but makes more passes and launches.
-    # Measured (MI355X, bf16, forward + backward): fused wins from about 320
-    # chains at any T, and below that only for T <= 512 (launch-bound).
-    B, T = x.shape[0], x.shape[1]
-    chains = B * ((modes + 63) // 64)
-    return chains >= 320 or T <= 512
+    return fused_preferred(x.shape[0], x.shape[1], modes)
+
+
+def fused_preferred(batch: int, length: int, modes: int) -> bool:
+    """The "auto" rule.  One wave per chain (batch row x 64 modes) walks all
+    of T in the fused kernels, so few chains leave most of the GPU idle; the
+    composed path's look-back scan is parallel over T but makes more passes
+    and launches.  Measured (MI355X, bf16, forward + backward): fused wins
+    from about 320 chains at any T, and below that only for T <= 512
+    (launch-bound)."""
+    chains = batch * ((modes + 63) // 64)
+    return chains >= 320 or length <= 512
 
 
 _PARAMS = ("phase_direction", "radial_direction", "nu_log", "theta_log", "write_log_gain",
