@@ -242,6 +242,22 @@ def test_long_real_drift(algorithm):
     assert rel_err(y[:, -1], yo[:, -1]) <= 1e-4
 
 
+@pytest.mark.parametrize("transition,M,G,dtype", [
+    ("p1", 128, 1, F32), ("real", 256, 32, F32), ("polar", 128, 8, BF16)], ids=["p1_f32", "real_f32", "polar_bf16"])
+def test_lookback_single_long_chain(transition, M, G, dtype):
+    """One chain (one mode block) over 128 chunks: more of its tiles are
+    resident at once than one look-back window (64 predecessors) covers, so
+    tiles compose several windows of aggregates before they reach an
+    inclusive carry; forward and backward against the float64 oracle."""
+    print(f"[case] lookback single chain {transition} B=1 T=8192 M={M} G={G} {dtype}", flush=True)
+    ops.set_algorithm("lookback")
+    try:
+        case = make_case(transition, 1, 8192, M, G, dtype, seed=29, dlast=True)
+        check_case(case)
+    finally:
+        ops.set_algorithm("auto")
+
+
 def test_empty_sequence(algorithm):
     print("[case] empty T=0", flush=True)
     w = torch.zeros(2, 0, 64, device="cuda")
