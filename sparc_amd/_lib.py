@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "sparc_scan_forward",
     "sparc_scan_backward",
     "sparc_scan_workspace_error",
+    "sparc_set_wait_limit",
     "sparc_write_forward",
     "sparc_write_workspace_bytes",
     "sparc_write_backward",
@@ -100,6 +101,8 @@ def load() -> ctypes.CDLL:
         lib.sparc_scan_backward.restype = ctypes.c_int
         lib.sparc_scan_workspace_error.argtypes = [_P, _P]
         lib.sparc_scan_workspace_error.restype = ctypes.c_int
+        lib.sparc_set_wait_limit.argtypes = [ctypes.c_uint32]
+        lib.sparc_set_wait_limit.restype = ctypes.c_uint32
         lib.sparc_write_forward.argtypes = [_I64, _I64, _I32] + [_P] * 10
         lib.sparc_write_forward.restype = ctypes.c_int
         lib.sparc_write_workspace_bytes.argtypes = [_I64, _I64]

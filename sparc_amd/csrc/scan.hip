@@ -36,6 +36,7 @@
 // (forward/scan.py:724-854) and their reverse-time counterparts
 // (sparc-kernal/backward/scan.py:34-781).
 
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -3282,6 +3283,10 @@ constexpr int kWideV = 4;
 constexpr int kSerialWideMin = SPARC_SERIAL_WIDE_MIN;
 static_assert(kChunk == sparc::kStateChunk, "one saved-state chunk length");
 
+// Polls each cross-workgroup wait of the look-back kernels makes before it
+// gives up (sets the workspace error word and lets the workgroup finish).
+static std::atomic<uint32_t> g_wait_limit{1u << 20};
+
 struct Plan {
   int V = 1;
   int gm = sparc::GATE_LANE;
@@ -3634,7 +3639,7 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, con
   a.n_mblocks = pl.n_mblocks;
   a.n_chains = pl.n_chains;
   a.flags = static_cast<uint32_t>(d->flags);
-  a.spin_limit = 1u << 20;
+  a.spin_limit = g_wait_limit.load(std::memory_order_relaxed);
   a.g0 = gate0; a.g1 = gate1; a.nu_log = nu_log; a.theta_log = theta_log;
   a.w_re = w_re; a.w_im = w_im; a.h0_re = h0_re; a.h0_im = h0_im; a.segpos = segment_pos;
   a.y_re = y_re; a.y_im = y_im; a.chunk_state = chunk_state;
@@ -3724,7 +3729,7 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
   a.n_mblocks = pl.n_mblocks;
   a.n_chains = pl.n_chains;
   a.flags = static_cast<uint32_t>(d->flags);
-  a.spin_limit = 1u << 20;
+  a.spin_limit = g_wait_limit.load(std::memory_order_relaxed);
   a.g0 = gate0; a.g1 = gate1; a.nu_log = nu_log; a.theta_log = theta_log;
   a.w_re = w_re; a.w_im = w_im; a.h0_re = h0_re; a.h0_im = h0_im; a.segpos = segment_pos;
   a.chunk_state_in = chunk_state;
@@ -3763,6 +3768,10 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
   e = hipGetLastError();
   if (e != hipSuccess) return fail(SPARC_EHIP, "scan backward reductions: %s", hipGetErrorString(e));
   return SPARC_OK;
+}
+
+uint32_t sparc_set_wait_limit(uint32_t polls) {
+  return g_wait_limit.exchange(polls, std::memory_order_relaxed);
 }
 
 int sparc_scan_workspace_error(const void* workspace, sparc_stream_t stream) {

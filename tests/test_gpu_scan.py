@@ -292,6 +292,42 @@ def test_workspace_no_spin_errors(algo_flag):
     assert lib.sparc_scan_workspace_error(P(ws), st) == 0
 
 
+def test_wait_bound_reports_and_finishes():
+    """With every look-back wait bounded at 0 polls, a launch still finishes:
+    each tile that would wait gives up at once and reports through the
+    workspace error word (its results are invalid).  With the default bound
+    restored the same launch reports nothing and matches the oracle."""
+    import ctypes
+    from sparc_amd import _lib
+    print("[case] wait bound 0: real B=1 T=4096 M=256 (one chain, 64 chunks), look-back", flush=True)
+    case = make_case("real", 1, 4096, 256, 32, F32, seed=5)
+    L = _leaves(case, "cuda")
+    lib = _lib.load()
+    d = _lib.ScanDesc(1, 4096, 256, 32, 3, 0, 0, 4)  # real, fp32 I/O and gates, look-back
+    P = _lib.ptr
+    st = _lib.stream_of(torch.device("cuda"))
+    ws = torch.zeros(lib.sparc_scan_workspace_bytes(ctypes.byref(d), 0), dtype=torch.uint8, device="cuda")
+    y = torch.empty_like(L["w_re"])
+    cs = torch.zeros(1, lib.sparc_scan_chunk_count(ctypes.byref(d)), 256, 1, device="cuda")
+
+    def forward():
+        _lib.check(lib.sparc_scan_forward(ctypes.byref(d), P(L["g0"]), None, None, None, P(L["w_re"]), None,
+                                          None, None, None, P(y), None, P(cs), P(ws), ws.numel(), st), "fwd")
+        return lib.sparc_scan_workspace_error(P(ws), st)
+
+    prev = lib.sparc_set_wait_limit(0)
+    try:
+        assert forward() == 1
+    finally:
+        lib.sparc_set_wait_limit(prev)
+    assert forward() == 0
+    ops.set_algorithm("lookback")
+    try:
+        check_case(case)
+    finally:
+        ops.set_algorithm("auto")
+
+
 def test_deterministic_gradients(algorithm):
     """No float atomics anywhere: the chain and serial algorithms compose
     carries in a fixed order and give bit-identical results run to run.  The look-back
