@@ -191,12 +191,14 @@ def complex_scan(ar, ai, wr, wi, h0=None, resets=None):
     else:
         xr, xi = h0[0].to(wr.dtype), h0[1].to(wr.dtype)
     outr, outi = [], []
-    for t in range(length):
-        a_r, a_i = ar[:, t], ai[:, t]
+    # unbind, not per-step indexing: its backward stacks the step gradients
+    # once, where indexing would build a full-size gradient per step (O(T^2))
+    steps = zip(ar.unbind(1), ai.unbind(1), wr.unbind(1), wi.unbind(1))
+    for t, (a_r, a_i, w_r, w_i) in enumerate(steps):
         if resets is not None:
             keep = (~resets[:, t]).to(wr.dtype)[:, None]
             a_r, a_i = a_r * keep, a_i * keep
-        xr, xi = a_r * xr - a_i * xi + wr[:, t], a_i * xr + a_r * xi + wi[:, t]
+        xr, xi = a_r * xr - a_i * xi + w_r, a_i * xr + a_r * xi + w_i
         outr.append(xr)
         outi.append(xi)
     if length == 0:
@@ -210,11 +212,10 @@ def real_scan(a, b, h0=None, resets=None):
     batch, length, width = b.shape
     x = torch.zeros(batch, width, dtype=b.dtype) if h0 is None else h0.to(b.dtype)
     out = []
-    for t in range(length):
-        at = a[:, t]
+    for t, (at, bt) in enumerate(zip(a.unbind(1), b.unbind(1))):
         if resets is not None:
             at = at * (~resets[:, t]).to(b.dtype)[:, None]
-        x = at * x + b[:, t]
+        x = at * x + bt
         out.append(x)
     if length == 0:
         return b.new_zeros(batch, 0, width), x
