@@ -279,6 +279,23 @@ __device__ __forceinline__ float fast_exp(float x) {
   return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
 }
 
+// theta = exp(theta_log) and its cosine and sine (returned in c, s), each
+// evaluated in fp64 and rounded once to fp32.  A P1 transition turns the state
+// by theta plus a small gate-dependent angle at every step, so an error in
+// these per-mode constants is the same at every step and adds up over as many
+// steps as a mode remembers (about 1 / (1 - |a|), tens of thousands of steps
+// for slow modes).  fp32 evaluation (exp, then sincos of the rounded theta)
+// leaves a few ulps: about 1e-4 relative error after 2k steps of a slow mode,
+// against about 1e-5 with these constants.
+__device__ inline float theta_rotation(float theta_log, float& c, float& s) {
+  const double th = exp(static_cast<double>(theta_log));
+  double sd, cd;
+  sincos(th, &sd, &cd);
+  c = static_cast<float>(cd);
+  s = static_cast<float>(sd);
+  return static_cast<float>(th);
+}
+
 // sin and cos of |x| <= pi/4 by their Taylor series (truncation error below
 // 1e-9 on that interval, i.e. well under one fp32 ulp of the result).
 __device__ __forceinline__ void sincos_quarter(float x, float& s, float& c) {

@@ -92,9 +92,8 @@ mixer_prepare_kernel(int M, const float* nu_log, const float* theta_log, const f
   const int m = blockIdx.x * 256 + threadIdx.x;
   if (m >= M) return;
   const float nu = expf(nu_log[m]);
-  const float theta = expf(theta_log[m]);
   float sn, cs;
-  sincosf(theta, &sn, &cs);
+  const float theta = theta_rotation(theta_log[m], cs, sn);
   const float gam = expf(wlg[m]);
   const float cinv = 1.0f / expm1f(-2.0f * nu);
   float4* c = reinterpret_cast<float4*>(consts + static_cast<int64_t>(m) * kConsts);

@@ -271,12 +271,13 @@ decode_kernel(int M, const void* x, const float* pdir, const float* rdir,
     for (int v = 0; v < 2; ++v) {
       const int m = m0 + v;
       const float nu = expf(nu_log[m]);
-      const float theta = expf(theta_log[m]);
+      float ct, st;
+      theta_rotation(theta_log[m], ct, st);
       const float eff = nu * E;
       const float rho = expf(-eff);
       float sn, cs;
-      sincosf(theta + (1.0f - rho) * delta, &sn, &cs);
-      const float ar = rho * cs, ai = rho * sn;
+      sincosf((1.0f - rho) * delta, &sn, &cs);
+      const float ar = rho * (ct * cs - st * sn), ai = rho * (st * cs + ct * sn);
       const float ratio = sqrtf(expm1f(-2.0f * eff) / expm1f(-2.0f * nu));
       const float gate = 2.0f * sigmoidf_(phase_signal * wpr[m] + radial_signal * wrr[m]);
       const float gain = expf(wlg[m]) * ratio * gate;
@@ -333,9 +334,8 @@ decode_prepare_kernel(int M, const float* nu_log, const float* theta_log, const 
   const int m = blockIdx.x * 256 + threadIdx.x;
   if (m >= M) return;
   const float nu = expf(nu_log[m]);
-  const float theta = expf(theta_log[m]);
   float sn, cs;
-  sincosf(theta, &sn, &cs);
+  const float theta = theta_rotation(theta_log[m], cs, sn);
   float4* c = reinterpret_cast<float4*>(consts + static_cast<int64_t>(m) * kDecodeConsts);
   c[0] = make_float4(nu, cs, sn, 4.0f * expf(2.0f * wlg[m]) / expm1f(-2.0f * nu));
   c[1] = make_float4(-kLog2e * wpr[m], -kLog2e * wrr[m], theta, 0.0f);
@@ -549,12 +549,13 @@ scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* 
       const float eta = static_cast<const float*>(g0)[gi];
       const float delta = static_cast<const float*>(g1)[gi];
       const float nu = expf(nu_log[m + v]);
-      const float theta = expf(theta_log[m + v]);
+      float ct, st;
+      theta_rotation(theta_log[m + v], ct, st);
       const float rho = expf(-nu * expf(eta));
       float sn, cs;
-      sincosf(theta + (1.0f - rho) * delta, &sn, &cs);
-      ar[v] = rho * cs;
-      ai[v] = rho * sn;
+      sincosf((1.0f - rho) * delta, &sn, &cs);
+      ar[v] = rho * (ct * cs - st * sn);
+      ai[v] = rho * (st * cs + ct * sn);
     } else if constexpr (TR == TR_POLAR) {
       const float r = load1_nt<IO>(g0, gi);
       float sn, cs;

@@ -282,8 +282,7 @@ struct TransitionLane {
         const float nl = ok ? p.nu_log[m0 + v] : 0.0f;
         const float tl = ok ? p.theta_log[m0 + v] : 0.0f;
         nu[v] = expf(nl);
-        th[v] = expf(tl);
-        sincosf(th[v], &st[v], &ct[v]);
+        th[v] = theta_rotation(tl, ct[v], st[v]);
       }
     }
   }

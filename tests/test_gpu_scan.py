@@ -242,6 +242,46 @@ def test_long_real_drift(algorithm):
     assert rel_err(y[:, -1], yo[:, -1]) <= 1e-4
 
 
+# A P1 case whose slowest mode has |a| within 1.2e-5 of 1 over 2049 steps: the
+# rotation by theta repeats at every step, so fp32 rounding of cos(theta) and
+# sin(theta) adds up over the whole sequence (1.4e-4 relative error with
+# fp32-evaluated constants, 1.8e-5 with fp64-evaluated ones).
+LONG_P1 = dict(transition="p1", B=2, T=2049, M=32, G=1, dtype=F32, seed=548157)
+
+
+def test_long_p1_slow_modes(algorithm):
+    """P1 scan over 2049 steps with near-unit slow modes, relu output, forward
+    and backward against the float64 oracle; outputs within 4e-5."""
+    print(f"[case] long P1 slow modes {LONG_P1} algo={algorithm}", flush=True)
+    case = make_case(**LONG_P1, relu=True)
+    check_case(case)
+    y, _, _ = run_gpu(case)
+    yo, _, _ = run_oracle(case)
+    assert rel_err(y, yo) <= 4e-5, f"output rel err {rel_err(y, yo):.3g}"
+
+
+def test_long_p1_chained_steps():
+    """The same 2049 steps as single decode steps (sparc_scan_step), state
+    updated in place: the final state stays within 4e-5 of the float64
+    sequential recurrence."""
+    print(f"[case] long P1 chained steps {LONG_P1}", flush=True)
+    case = make_case(**LONG_P1)
+    B, T, M = LONG_P1["B"], LONG_P1["T"], LONG_P1["M"]
+    state = (torch.zeros(B, M, device="cuda"), torch.zeros(B, M, device="cuda"))
+    g0, g1 = case["g0"].cuda(), case["g1"].cuda()
+    w_re, w_im = case["w_re"].cuda(), case["w_im"].cuda()
+    nu, th = case["nu_log"].cuda(), case["theta_log"].cuda()
+    for t in range(T):
+        ops.scan_step("p1", g0[:, t].contiguous(), g1[:, t].contiguous(), w_re[:, t].contiguous(),
+                      w_im[:, t].contiguous(), state, nu, th)
+    torch.cuda.synchronize()
+    d = lambda x: x.double()  # noqa: E731
+    _, last = O.grouped_scan_forward("p1", d(case["g0"]), d(case["g1"]), d(case["w_re"]), d(case["w_im"]),
+                                     d(case["nu_log"]), d(case["theta_log"]))
+    for a, b in zip(state, last):
+        assert rel_err(a, b) <= 4e-5, f"final state rel err {rel_err(a, b):.3g}"
+
+
 @pytest.mark.parametrize("transition,M,G,dtype", [
     ("p1", 128, 1, F32), ("real", 256, 32, F32), ("polar", 128, 8, BF16)], ids=["p1_f32", "real_f32", "polar_bf16"])
 def test_lookback_single_long_chain(transition, M, G, dtype):
