@@ -327,12 +327,21 @@ def complex_scan_adjoint(ar, ai, hr, hi, dyr, dyi, dlast=None, h0=None, resets=N
 # module level
 # --------------------------------------------------------------------------
 def mixer_forward(p: MixerParams, x: torch.Tensor, return_cache=False,
-                  initial_state=None, segment_pos=None, reset_first=False):
+                  initial_state=None, segment_pos=None, reset_first=False,
+                  write_dtype=None):
     """``SPARCMixer.forward`` = ``run_sequence`` (forward/scan.py:1398-1603):
-    controls, P1 write, P1 transition, scan, ``relu(cat(h_r, h_i))``."""
+    controls, P1 write, P1 transition, scan, ``relu(cat(h_r, h_i))``.
+
+    ``write_dtype`` (e.g. torch.bfloat16) models the reference's cast of the
+    write to x's dtype (``write_r.to(x.dtype)``, forward/control.py:162-163):
+    the write's value is rounded to it, and autograd rounds the write's
+    gradient through the same cast.  The controls stay in the compute dtype
+    (``x.float()``, control.py:129-137)."""
     eta, delta = controls(x, p.phase_direction, p.radial_direction)
     wr, wi = write(x, eta, delta, p.nu_log, p.write_log_gain,
                    p.write_phase_response, p.write_radial_response)
+    if write_dtype is not None:
+        wr, wi = wr.to(write_dtype).to(wr.dtype), wi.to(write_dtype).to(wi.dtype)
     ar, ai = p1_transition(eta[..., None], delta[..., None], p.nu_log, p.theta_log)
     resets = None
     if segment_pos is not None or reset_first:

@@ -338,3 +338,68 @@ def test_module_empty_sequence(mixer_path):
     grads = torch.autograd.grad(loss, [getattr(m, n) for n in NAMES], allow_unused=True)
     for n, gr in zip(NAMES, grads):
         assert gr is None or (gr == 0).all(), n
+
+
+def _bf16_module_errors(B, L, width, seed, write_dtype):
+    """Relative errors of the module's bf16 outputs, last state and every
+    gradient against the float64 oracle (its write rounded to write_dtype,
+    None for exact arithmetic), with the output gradient rounded to bf16 as
+    the GPU receives it."""
+    m = make_module(width, seed=seed).cuda()
+    g = torch.Generator().manual_seed(seed + 7)
+    x_in = torch.randn(B, L, width, generator=g, dtype=torch.float64).to(torch.bfloat16)
+    p = oracle_params(m)
+    dy = _masked_dy(p, x_in.double(), torch.randn(B, L, width, generator=g, dtype=torch.float64), band=2e-2)
+    dy = dy.to(torch.bfloat16).double()
+    dl = (torch.randn(B, width // 2, generator=g, dtype=torch.float64),
+          torch.randn(B, width // 2, generator=g, dtype=torch.float64))
+    x = x_in.cuda().requires_grad_()
+    y, cache = m(x, return_cache=True)
+    loss = (y.float() * dy.cuda().float()).sum() + (cache[0] * dl[0].cuda().float()).sum() \
+        + (cache[1] * dl[1].cuda().float()).sum()
+    got = [y, cache[0], cache[1]] + list(torch.autograd.grad(loss, [x] + [getattr(m, n) for n in NAMES]))
+    xo = x_in.double().clone().requires_grad_()
+    yo, lasto = O.mixer_forward(p, xo, return_cache=True, write_dtype=write_dtype)
+    lo = (yo * dy).sum() + (lasto[0] * dl[0]).sum() + (lasto[1] * dl[1]).sum()
+    ref = [yo, lasto[0], lasto[1]] + list(torch.autograd.grad(lo, [xo] + [getattr(p, n) for n in NAMES]))
+    names = ["y", "last_re", "last_im", "dx"] + ["d" + n for n in NAMES]
+    return {n: rel_err(a, b) for n, a, b in zip(names, got, ref)}
+
+
+# bf16 shapes where the reference's own rounding of the write (value and
+# gradient) moves some gradient by more than 2e-2 from exact arithmetic (few
+# modes or few tokens: sums with cancellation), and two ordinary shapes
+BF16_SHAPES = [(1, 2, 256, 7459), (8, 4097, 8, 570786), (5, 200, 16, 398228), (2, 256, 128, 7),
+               (4, 513, 512, 3)]
+
+
+@pytest.mark.parametrize("B,L,width,seed", BF16_SHAPES)
+def test_composed_bf16_matches_reference_rounding(B, L, width, seed):
+    """The composed path rounds where the reference rounds: it stores the
+    write in x's dtype (forward/control.py:162-163), so its gradient is
+    rounded too.  Against the oracle with that rounding, every output and
+    gradient is within 1e-2 (half the bf16 tolerance), also where the same
+    rounding moves a gradient by more than 2e-2 from exact arithmetic."""
+    print(f"[case] composed bf16 vs reference rounding B={B} L={L} width={width}", flush=True)
+    sparc_amd.set_mixer_path("composed")
+    try:
+        errs = _bf16_module_errors(B, L, width, seed, torch.bfloat16)
+    finally:
+        sparc_amd.set_mixer_path("auto")
+    bad = {k: f"{v:.3g}" for k, v in errs.items() if v > 1e-2}
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("B,L,width,seed", [s for s in BF16_SHAPES if (s[2] // 2) % 4 == 0])
+def test_fused_bf16_tracks_exact_arithmetic(B, L, width, seed):
+    """The fused path keeps the write in fp32 inside its scan, so with bf16
+    x and y it stays within 1e-2 of exact arithmetic on every output and
+    gradient, including the shapes where the reference's bf16 write does not."""
+    print(f"[case] fused bf16 vs exact B={B} L={L} width={width}", flush=True)
+    sparc_amd.set_mixer_path("fused")
+    try:
+        errs = _bf16_module_errors(B, L, width, seed, None)
+    finally:
+        sparc_amd.set_mixer_path("auto")
+    bad = {k: f"{v:.3g}" for k, v in errs.items() if v > 1e-2}
+    assert not bad, bad

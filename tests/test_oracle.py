@@ -122,6 +122,49 @@ def test_mixer_gradcheck_finite_differences():
     assert torch.autograd.gradcheck(f, inputs, eps=1e-6, atol=1e-6, rtol=1e-5)
 
 
+def test_write_dtype_rounds_write_value_and_gradient():
+    """``mixer_forward(write_dtype=bf16)`` (the reference's cast of the write
+    to x's dtype): the outputs equal the scan of the write rounded to bf16 by
+    hand, and the parameter gradients equal the two-stage chain rule with the
+    scan's gradient of the write rounded to bf16 before the write's backward."""
+    g = torch.Generator().manual_seed(5)
+    M, names = 6, ["nu_log", "theta_log", "phase_direction", "radial_direction", "write_log_gain",
+                   "write_phase_response", "write_radial_response"]
+    p = O.init_params(2 * M, generator=g)
+    p.phase_direction = 0.3 * torch.randn(2 * M + 1, generator=g)
+    p.radial_direction = 0.3 * torch.randn(2 * M + 1, generator=g)
+    p.write_phase_response = torch.randn(M, generator=g)
+    p.write_radial_response = torch.randn(M, generator=g)
+    x = torch.randn(2, 9, 2 * M, generator=g)
+    dy = torch.randn(2, 9, 2 * M, generator=g)
+    params = [getattr(p, n).clone().requires_grad_() for n in names]
+    q = O.MixerParams(**dict(zip(names, params)))
+    y, _ = O.mixer_forward(q, x, write_dtype=torch.bfloat16)
+    got = torch.autograd.grad((y * dy).sum(), params)
+    # by hand: the write, its bf16 rounding as a fresh leaf, the scan
+    eta, delta = O.controls(x, q.phase_direction, q.radial_direction)
+    wr, wi = O.write(x, eta, delta, q.nu_log, q.write_log_gain, q.write_phase_response,
+                     q.write_radial_response)
+    lr = wr.detach().to(torch.bfloat16).double().requires_grad_()
+    li = wi.detach().to(torch.bfloat16).double().requires_grad_()
+    ar, ai = O.p1_transition(eta[..., None], delta[..., None], q.nu_log, q.theta_log)
+    (hr, hi), _ = O.complex_scan(ar, ai, lr, li)
+    y2 = torch.cat((hr, hi), -1).relu()
+    assert torch.equal(y.detach(), y2.detach())
+    loss = (y2 * dy).sum()
+    gw = torch.autograd.grad(loss, [lr, li], retain_graph=True)
+    direct = torch.autograd.grad(loss, params, allow_unused=True, retain_graph=True)  # transition, controls
+    via_write = torch.autograd.grad([wr, wi], params, [gw[0].to(torch.bfloat16).double(),
+                                                       gw[1].to(torch.bfloat16).double()], allow_unused=True)
+    for n, a, b, c in zip(names, got, direct, via_write):
+        ref = (b if b is not None else 0.0) + (c if c is not None else 0.0)
+        assert torch.allclose(a, ref, rtol=1e-12, atol=1e-12), n
+    # and the rounding changes the gradient (the model is not a no-op)
+    y0, _ = O.mixer_forward(q, x)
+    exact = torch.autograd.grad((y0 * dy).sum(), params)
+    assert (got[4] - exact[4]).abs().max() > 1e-6
+
+
 def test_controls_and_write_formulas_at_default_init():
     """Zero directions and responses (the module's init): eta = delta = 0,
     a_m = exp(-nu_m + i theta_m) and w = exp(wlg) tanh(x) exactly (ratio = 1,
