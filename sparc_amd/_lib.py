@@ -152,7 +152,34 @@ def check(status: int, what: str) -> None:
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
-    return None if t is None else t.data_ptr()
+    """The device address the C ABI reads: only for contiguous tensors (the
+    kernels index them as dense row-major arrays)."""
+    if t is None:
+        return None
+    if not t.is_contiguous():
+        raise ValueError("SPARC HIP kernels take contiguous tensors")
+    return t.data_ptr()
+
+
+def expect(t: torch.Tensor | None, shape: tuple, dtype: torch.dtype, name: str) -> None:
+    """Raise ValueError unless ``t`` has this shape and dtype (the sizes the
+    kernels assume: a tensor smaller than its descriptor would be read or
+    written past its end)."""
+    if t is None:
+        raise ValueError(f"{name} is required")
+    if tuple(t.shape) != tuple(shape) or t.dtype != dtype:
+        raise ValueError(f"{name} must be {list(shape)} {dtype}, got {list(t.shape)} {t.dtype}")
+
+
+def check_params(width: int, **named: torch.Tensor) -> None:
+    """Module parameters against the input width 2M they are used with:
+    ``*direction`` tensors hold width + 1 entries (bias last), every other
+    (per-mode) parameter width // 2.  ValueError otherwise: the kernels read
+    that many values from each."""
+    for name, t in named.items():
+        n = width + 1 if name.endswith("direction") else width // 2
+        if t.ndim != 1 or t.numel() != n:
+            raise ValueError(f"{name} must have {n} entries for inputs of width {width}, got {list(t.shape)}")
 
 
 def stream_of(device: torch.device) -> int:

@@ -34,8 +34,9 @@ class _Controls(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, phase_direction, radial_direction):
         lib = _lib.load()
-        dev = _lib.require_gpu(x, phase_direction, radial_direction)
         W = x.shape[-1]
+        _lib.check_params(W, phase_direction=phase_direction, radial_direction=radial_direction)
+        dev = _lib.require_gpu(x, phase_direction, radial_direction)
         rows = x.numel() // W
         x2 = aligned16(x)
         pd = aligned16(phase_direction.detach().float())
@@ -95,6 +96,10 @@ class _LatestSPARCWrite(torch.autograd.Function):
     @staticmethod
     def forward(ctx, raw_x, eta, delta, nu_log, write_log_gain, phase_response, radial_response):
         lib = _lib.load()
+        if raw_x.ndim != 3 or eta.shape != raw_x.shape[:2] or delta.shape != eta.shape:
+            raise ValueError("the write needs x [B, L, 2M] and eta, delta [B, L]")
+        _lib.check_params(raw_x.shape[-1], nu_log=nu_log, write_log_gain=write_log_gain,
+                          write_phase_response=phase_response, write_radial_response=radial_response)
         dev = _lib.require_gpu(raw_x, eta, delta, nu_log)
         raw_x = raw_x.contiguous()
         eta, delta = eta.float().contiguous(), delta.float().contiguous()

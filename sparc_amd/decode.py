@@ -32,9 +32,10 @@ def _decode_constants(module):
     if cache is not None and cache[0] == key:
         return cache[1]
     lib = _lib.load()
+    modes = module.nu_log.numel()
+    _lib.check_params(2 * modes, **{n: getattr(module, n) for n in _CONST_PARAMS})
     params = [getattr(module, n).detach().float().contiguous() for n in _CONST_PARAMS]
     dev = _lib.require_gpu(*params)
-    modes = params[0].numel()
     consts = torch.empty(modes, 8, dtype=torch.float32, device=dev)
     P = _lib.ptr
     _lib.check(lib.sparc_decode_prepare(modes, *[P(t) for t in params], P(consts), _lib.stream_of(dev)),
@@ -79,6 +80,8 @@ def latest_sparc_decode(module, x: torch.Tensor, state, out_state=None):
     state_r, state_i = state
     if state_r.shape != (batch, modes) or state_i.shape != state_r.shape:
         raise ValueError("SPARC decode state shape mismatch")
+    _lib.check_params(width, phase_direction=module.phase_direction, radial_direction=module.radial_direction,
+                      **{n: getattr(module, n) for n in _CONST_PARAMS})
     dev = _lib.require_gpu(x, state_r, state_i)
     state_r = state_r.float().contiguous()
     state_i = state_i.float().contiguous()

@@ -76,6 +76,9 @@ class _FusedMixer(torch.autograd.Function):
     def forward(ctx, x, phase_direction, radial_direction, nu_log, theta_log, write_log_gain,
                 write_phase_response, write_radial_response, energy_response):
         lib = _lib.load()
+        _lib.check_params(x.shape[-1], phase_direction=phase_direction, radial_direction=radial_direction,
+                          nu_log=nu_log, theta_log=theta_log, write_log_gain=write_log_gain,
+                          write_phase_response=write_phase_response, write_radial_response=write_radial_response)
         dev = _lib.require_gpu(x, phase_direction, nu_log)
         x = x.contiguous()
         params = [p.detach().float().contiguous() for p in (
@@ -159,9 +162,14 @@ class _ProjectedMixer(torch.autograd.Function):
     def forward(ctx, xn, weight, phase_direction, radial_direction, nu_log, theta_log, write_log_gain,
                 write_phase_response, write_radial_response, energy_response):
         lib = _lib.load()
-        dev = _lib.require_gpu(xn, weight, phase_direction)
         B, T, D = xn.shape
         W = weight.shape[0]
+        if weight.shape != (W, D):
+            raise ValueError(f"the projection must be [2M, {D}], got {list(weight.shape)}")
+        _lib.check_params(W, phase_direction=phase_direction, radial_direction=radial_direction,
+                          nu_log=nu_log, theta_log=theta_log, write_log_gain=write_log_gain,
+                          write_phase_response=write_phase_response, write_radial_response=write_radial_response)
+        dev = _lib.require_gpu(xn, weight, phase_direction)
         M = W // 2
         x = torch.nn.functional.linear(xn, weight).contiguous()  # [B, T, 2M] in the activation dtype
         dirs = torch.stack((phase_direction, radial_direction)).detach().float()  # [2, 2M + 1]

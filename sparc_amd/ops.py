@@ -55,12 +55,45 @@ def _workspace(n_bytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(n_bytes), 256), dtype=torch.uint8, device=device)
 
 
+def _check_scan_inputs(transition, g0, g1, w_re, w_im, nu_log, theta_log, h0_re, h0_im,
+                       segment_pos, step=False):
+    """Shapes and dtypes of a raw launch's inputs against its descriptor
+    (B, T, M from w_re, G from g0); ValueError on any mismatch.  ``step``:
+    the single-step layout (w [B, M], gates [B, G], no T axis)."""
+    if transition not in TRANSITIONS:
+        raise ValueError(f"unknown transition {transition!r}")
+    cplx, p1 = transition != "real", transition == "p1"
+    lead = tuple(w_re.shape[:-1])
+    if w_re.ndim != (2 if step else 3) or g0.ndim != w_re.ndim or tuple(g0.shape[:-1]) != lead:
+        raise ValueError("writes must be [B, T, M] and gates [B, T, G] ([B, M], [B, G] for a step)")
+    M, G, io = w_re.shape[-1], g0.shape[-1], w_re.dtype
+    if G <= 0 or M % G:
+        raise ValueError("the gate group count G must divide M")
+    gate_dtype = torch.float32 if p1 else io
+    _lib.expect(g0, lead + (G,), gate_dtype, "g0")
+    if cplx:
+        _lib.expect(g1, lead + (G,), gate_dtype, "g1")
+        _lib.expect(w_im, lead + (M,), io, "w_im")
+    if p1:
+        _lib.expect(nu_log, (M,), torch.float32, "nu_log")
+        _lib.expect(theta_log, (M,), torch.float32, "theta_log")
+    B = lead[0]
+    if h0_re is not None:
+        _lib.expect(h0_re, (B, M), torch.float32, "h0_re")
+    if h0_im is not None or (h0_re is not None and cplx):
+        _lib.expect(h0_im, (B, M), torch.float32, "h0_im")
+    if segment_pos is not None:
+        _lib.expect(segment_pos, lead, torch.int32, "segment_pos")
+
+
 def scan_forward_raw(transition, g0, g1, w_re, w_im, nu_log=None, theta_log=None,
                      h0_re=None, h0_im=None, segment_pos=None, reset_first=False,
                      relu_output=False):
     """One forward launch.  Inputs must be contiguous GPU tensors of the
-    dtypes the C ABI expects.  Returns (y_re, y_im, chunk_state)."""
+    dtypes the C ABI expects (ValueError otherwise).  Returns (y_re, y_im,
+    chunk_state)."""
     lib = _lib.load()
+    _check_scan_inputs(transition, g0, g1, w_re, w_im, nu_log, theta_log, h0_re, h0_im, segment_pos)
     dev = _lib.require_gpu(g0, g1, w_re, w_im, nu_log, theta_log, h0_re, h0_im, segment_pos)
     B, T, M = w_re.shape
     G = g0.shape[-1]
@@ -96,13 +129,25 @@ def scan_backward_raw(transition, g0, g1, w_re, w_im, chunk_state, dy_re, dy_im,
     epilogue), from which plans with lane-shared gates read the states instead
     of recomputing them.  Returns dict of gradients."""
     lib = _lib.load()
-    dev = _lib.require_gpu(g0, w_re, chunk_state, dy_re)
+    _check_scan_inputs(transition, g0, g1, w_re, w_im, nu_log, theta_log, h0_re, h0_im, segment_pos)
     B, T, M = w_re.shape
     G = g0.shape[-1]
     io = _lib.io_code(w_re.dtype)
     gate_io = _lib.io_code(g0.dtype)
     d = _desc(transition, B, T, M, G, io, gate_io, _flags(relu_output, reset_first))
     cplx = transition != "real"
+    n_chunks = lib.sparc_scan_chunk_count(ctypes.byref(d))
+    _lib.expect(chunk_state, (B, n_chunks, M, 2) if cplx else (B, n_chunks, M), torch.float32, "chunk_state")
+    _lib.expect(dy_re, (B, T, 2 * M if relu_output else M), w_re.dtype, "dy_re")
+    if cplx and not relu_output:
+        _lib.expect(dy_im, (B, T, M), w_re.dtype, "dy_im")
+    for name, t in (("y_re", y_re), ("y_im", y_im)):
+        if t is not None:
+            _lib.expect(t, (B, T, M), w_re.dtype, name)
+    for name, t in (("dlast_re", dlast_re), ("dlast_im", dlast_im)):
+        if t is not None:
+            _lib.expect(t, (B, M), torch.float32, name)
+    dev = _lib.require_gpu(g0, w_re, chunk_state, dy_re)
     dw_re = torch.empty_like(w_re)
     dw_im = torch.empty_like(w_im) if cplx else None
     dg0 = torch.empty_like(g0)
@@ -146,8 +191,8 @@ def scan_step(transition, g0, g1, w_re, w_im, state, nu_log=None, theta_log=None
         raise ValueError("scan_step expects w [B, M] and an fp32 state [B, M]")
     if not st_re.is_contiguous() or (st_im is not None and not st_im.is_contiguous()):
         raise ValueError("scan_step updates the state in place: it must be contiguous")
-    if cplx and (st_im is None or st_im.shape != st_re.shape or w_im is None):
-        raise ValueError("complex scan steps need (state_re, state_im) and w_im")
+    if cplx and (st_im is None or st_im.shape != st_re.shape or st_im.dtype != torch.float32 or w_im is None):
+        raise ValueError("complex scan steps need fp32 (state_re, state_im) and w_im")
     B, M = w_re.shape
     G = g0.shape[-1]
     if g0.shape != (B, G) or M % G or (cplx and (g1 is None or g1.shape != g0.shape)):
@@ -161,6 +206,7 @@ def scan_step(transition, g0, g1, w_re, w_im, state, nu_log=None, theta_log=None
         g0, g1 = g0.float(), g1.float()
     gate_io = _lib.io_code(g0.dtype)
     lib = _lib.load()
+    _check_scan_inputs(transition, g0, g1, w_re, w_im, nu_log, theta_log, None, None, None, step=True)
     dev = _lib.require_gpu(g0, w_re, st_re)
     y_re = y_im = None
     if want_output:

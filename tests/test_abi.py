@@ -156,3 +156,86 @@ def test_controls_entry_points_validate_on_host():
     fake = ctypes.c_void_p(256)  # never dereferenced: the size check fails first
     st = lib.sparc_controls_backward(4, 16, 0, *([fake] * 10), fake, 0, None)
     assert st == 4 and b"workspace" in lib.sparc_last_error()
+
+
+def _raw_inputs(transition="p1", B=2, T=5, M=8, G=2, io=torch.float32):
+    g = torch.float32 if transition == "p1" else io
+    d = dict(g0=torch.zeros(B, T, G, dtype=g), g1=torch.zeros(B, T, G, dtype=g),
+             w_re=torch.zeros(B, T, M, dtype=io), w_im=torch.zeros(B, T, M, dtype=io),
+             nu_log=torch.zeros(M), theta_log=torch.zeros(M))
+    if transition == "real":
+        d.update(g1=None, w_im=None, nu_log=None, theta_log=None)
+    elif transition != "p1":
+        d.update(nu_log=None, theta_log=None)
+    return d
+
+
+@pytest.mark.parametrize("change,msg", [
+    (dict(nu_log=torch.zeros(7)), "nu_log"),                          # shorter than M
+    (dict(theta_log=torch.zeros(8, dtype=torch.float64)), "theta_log"),
+    (dict(w_im=torch.zeros(2, 5, 4)), "w_im"),
+    (dict(g1=torch.zeros(2, 4, 2)), "g1"),
+    (dict(g0=torch.zeros(2, 5, 3)), "divide"),
+    (dict(h0_re=torch.zeros(2, 8)), "h0_im"),                         # complex h0 needs both halves
+    (dict(segment_pos=torch.ones(2, 5, dtype=torch.int64)), "segment_pos"),
+])
+def test_raw_scan_rejects_mismatched_tensors(change, msg):
+    """The raw launch wrappers check every tensor against the descriptor
+    before any pointer reaches the C ABI (on any device)."""
+    kw = _raw_inputs()
+    kw.update(change)
+    with pytest.raises(ValueError, match=msg):
+        ops.scan_forward_raw("p1", **kw)
+
+
+def test_raw_backward_and_step_reject_mismatched_tensors():
+    kw = _raw_inputs("polar", io=torch.bfloat16)
+    cs = torch.zeros(2, 1, 8, 2)
+    dy = torch.zeros(2, 5, 8, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="chunk_state"):
+        ops.scan_backward_raw("polar", kw["g0"], kw["g1"], kw["w_re"], kw["w_im"], cs[:, :, :4], dy, dy)
+    with pytest.raises(ValueError, match="dy_re"):
+        ops.scan_backward_raw("polar", kw["g0"], kw["g1"], kw["w_re"], kw["w_im"], cs, dy, dy, relu_output=True)
+    with pytest.raises(ValueError, match="g0"):
+        ops.scan_forward_raw("polar", **{**kw, "g0": kw["g0"].float()})  # gates in w's dtype
+    state = (torch.zeros(2, 8), torch.zeros(2, 8))
+    with pytest.raises(ValueError, match="nu_log"):
+        ops.scan_step("p1", torch.zeros(2, 1), torch.zeros(2, 1), torch.zeros(2, 8), torch.zeros(2, 8),
+                      state, torch.zeros(4), torch.zeros(8))
+    with pytest.raises(ValueError, match="w_im"):
+        ops.scan_step("polar", torch.zeros(2, 1), torch.zeros(2, 1), torch.zeros(2, 8), torch.zeros(2, 6),
+                      state)
+
+
+def test_pointer_helper_refuses_non_contiguous():
+    t = torch.zeros(4, 6)
+    assert _lib.ptr(t) == t.data_ptr() and _lib.ptr(None) is None
+    with pytest.raises(ValueError, match="contiguous"):
+        _lib.ptr(t.t())
+
+
+def test_module_paths_reject_wrong_parameter_shapes():
+    """Controls, write, fused and projected mixer and decode check every
+    parameter's length against the input width before any launch."""
+    from sparc_amd import control, mixer
+    from sparc_amd.decode import latest_sparc_decode
+    m = sparc_amd.SPARCMixer(16)  # M = 8
+    x = torch.zeros(2, 3, 16)
+    good = [getattr(m, n).detach() for n in ("phase_direction", "radial_direction", "nu_log", "theta_log",
+                                             "write_log_gain", "write_phase_response",
+                                             "write_radial_response")]
+    with pytest.raises(ValueError, match="phase_direction"):
+        control._Controls.apply(x, torch.zeros(16), good[1])
+    with pytest.raises(ValueError, match="nu_log"):
+        control._LatestSPARCWrite.apply(x, torch.zeros(2, 3), torch.zeros(2, 3), torch.zeros(7), *good[4:])
+    with pytest.raises(ValueError, match="theta_log"):
+        mixer._FusedMixer.apply(x, good[0], good[1], good[2], torch.zeros(9), *good[4:], m.energy_response)
+    with pytest.raises(ValueError, match="radial_direction"):
+        mixer._ProjectedMixer.apply(torch.zeros(2, 3, 4), torch.zeros(16, 4), good[0], torch.zeros(4),
+                                    *good[2:], m.energy_response)
+    with pytest.raises(ValueError, match="projection"):
+        mixer._ProjectedMixer.apply(torch.zeros(2, 3, 4), torch.zeros(16, 5), *good, m.energy_response)
+    with torch.no_grad():
+        m.write_log_gain = torch.nn.Parameter(torch.zeros(6))
+    with pytest.raises(ValueError, match="write_log_gain"):
+        latest_sparc_decode(m, torch.zeros(2, 16), (torch.zeros(2, 8), torch.zeros(2, 8)))
