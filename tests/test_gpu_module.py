@@ -403,3 +403,27 @@ def test_fused_bf16_tracks_exact_arithmetic(B, L, width, seed):
         sparc_amd.set_mixer_path("auto")
     bad = {k: f"{v:.3g}" for k, v in errs.items() if v > 1e-2}
     assert not bad, bad
+
+
+def test_module_decode_long_sequence():
+    """2049 chained SPARCMixer.step calls (prepared per-mode constants, fp32)
+    from a zero state: the final state and the last outputs stay within 4e-5
+    of the float64 sequence forward.  The rotation by theta repeats at every
+    step, so its per-mode constants must be exact to fp32 rounding."""
+    print("[case] module decode 2049 steps B=2 width=64 fp32", flush=True)
+    B, L, width = 2, 2049, 64
+    m = make_module(width, seed=31).cuda()
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(B, L, width, generator=g)
+    p = oracle_params(m, requires_grad=False)
+    y_full, last_full = O.mixer_forward(p, x.double(), return_cache=True)
+    xc = x.cuda()
+    state = (torch.zeros(B, width // 2, device="cuda"), torch.zeros(B, width // 2, device="cuda"))
+    with torch.no_grad():
+        m.prepare_inference()
+        for t in range(L):
+            yt, state = m.step(xc[:, t], state, segment_pos=None)
+    torch.cuda.synchronize()
+    assert rel_err(state[0], last_full[0]) <= 4e-5 and rel_err(state[1], last_full[1]) <= 4e-5, \
+        f"final state rel err {rel_err(state[0], last_full[0]):.3g}, {rel_err(state[1], last_full[1]):.3g}"
+    assert rel_err(yt, y_full[:, -1]) <= 4e-5
