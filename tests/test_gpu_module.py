@@ -408,8 +408,10 @@ def test_fused_bf16_tracks_exact_arithmetic(B, L, width, seed):
 def test_module_decode_long_sequence():
     """2049 chained SPARCMixer.step calls (prepared per-mode constants, fp32)
     from a zero state: the final state and the last outputs stay within 4e-5
-    of the float64 sequence forward.  The rotation by theta repeats at every
-    step, so its per-mode constants must be exact to fp32 rounding."""
+    of the float64 sequence forward (rounding does not build up over the
+    steps).  This case's slowest modes forget fast enough that fp32-evaluated
+    rotation constants alone would cost 1.2e-5 here; the scan-level long P1
+    tests are the ones sensitive to those constants."""
     print("[case] module decode 2049 steps B=2 width=64 fp32", flush=True)
     B, L, width = 2, 2049, 64
     m = make_module(width, seed=31).cuda()
