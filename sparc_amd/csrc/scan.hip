@@ -322,9 +322,12 @@ struct TransitionLane {
       const float delta = g1[0];
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        const float rho = fast_exp(-nu[v] * E);
+        // rho - 1 directly: for slow modes rho is within 1e-4 of 1, and
+        // 1 - fp32(rho) would keep only a few bits of the phase increment
+        const float em = expm1_nonpos(-nu[v] * E);
+        const float rho = 1.0f + em;
         float sd, cd;
-        sincos_quarter_or_half((1.0f - rho) * delta, sd, cd);
+        sincos_quarter_or_half(-em * delta, sd, cd);
         ar[v] = rho * (ct[v] * cd - st[v] * sd);
         ai[v] = rho * (st[v] * cd + ct[v] * sd);
       }
@@ -1208,7 +1211,8 @@ scan_bwd_kernel(ScanArgs p) {
         const float E = fast_exp(g0[s][0]);
         const float delta = g1[s][0];
         const float lrad = -tl.nu[v] * E;
-        const float rho = fast_exp(lrad);
+        const float em = expm1_nonpos(lrad);  // rho - 1 (as in the forward)
+        const float rho = 1.0f + em;
         const float ar = a_r[s][av], ai = a_i[s][av];
         float radial = lrad * (gar * ar + gai * ai);
         const float phase = -gar * ai + gai * ar;
@@ -1216,7 +1220,7 @@ scan_bwd_kernel(ScanArgs p) {
         radial += (-lrad) * rho * delta * phase;
         acc_nu[v] += radial;
         d0[gv] += radial;
-        d1[gv] += phase * (1.0f - rho);
+        d1[gv] -= phase * em;
       } else if constexpr (TR == TR_POLAR) {
         const float r = g0[s][gv];
         const float ar = a_r[s][av], ai = a_i[s][av];
@@ -1741,7 +1745,8 @@ chain_bwd_kernel(ScanArgs p) {
             const float E = fast_exp(buf[h].g0[s][0]);
             const float delta = buf[h].g1[s][0];
             const float lrad = -tl.nu[v] * E;
-            const float rho = fast_exp(lrad);
+            const float em = expm1_nonpos(lrad);  // rho - 1 (as in the forward)
+            const float rho = 1.0f + em;
             const float ar = a_r[s][av], ai = a_i[s][av];
             float radial = lrad * (gar * ar + gai * ai);
             const float phase = -gar * ai + gai * ar;
@@ -1749,7 +1754,7 @@ chain_bwd_kernel(ScanArgs p) {
             radial += (-lrad) * rho * delta * phase;
             acc_nu[v] += radial;
             d0[gv] += radial;
-            d1[gv] += phase * (1.0f - rho);
+            d1[gv] -= phase * em;
           } else if constexpr (TR == TR_POLAR) {
             const float ar = a_r[s][av], ai = a_i[s][av];
             float cphi, sphi;

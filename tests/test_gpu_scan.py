@@ -260,6 +260,15 @@ def test_long_p1_slow_modes(algorithm):
     assert rel_err(y, yo) <= 4e-5, f"output rel err {rel_err(y, yo):.3g}"
 
 
+def test_long_p1_8191_steps_last_state(algorithm):
+    """P1 fp32 over 8191 steps with four gate groups: the last state and every
+    gradient within 1e-4 of the float64 oracle.  The kernels form rho - 1 with
+    expm1 rather than as 1 - fp32(rho), which would lose most bits of the
+    phase increment (1 - rho) delta of slow modes (1.3e-4 on the last state)."""
+    print(f"[case] long P1 T=8191 M=256 G=4 algo={algorithm}", flush=True)
+    check_case(make_case("p1", 1, 8191, 256, 4, F32, seed=878652))
+
+
 def test_long_p1_chained_steps():
     """The same 2049 steps as single decode steps (sparc_scan_step), state
     updated in place: the final state stays within 4e-5 of the float64
