@@ -225,3 +225,225 @@ def test_grouped_gates_expand_per_mode():
     assert ar.shape == (2, 5, 12)
     for m in range(12):
         assert torch.equal(ar[..., m], r[..., m // 4] * torch.cos(phi[..., m // 4]))
+
+
+# --------------------------------------------------------------------------
+# reset, initial-state and init semantics, pinned by properties a misread
+# mask or state hand-off breaks (inverted, shifted or ignored resets; h0
+# applied twice or not at all; segment_pos and reset_first in the wrong order)
+# --------------------------------------------------------------------------
+def _real_inputs(B=2, T=31, W=5, seed=11):
+    g = torch.Generator().manual_seed(seed)
+    return 0.5 + 0.49 * torch.rand(B, T, W, generator=g), torch.randn(B, T, W, generator=g)
+
+
+@pytest.mark.parametrize("k", [1, 9, 36])
+def test_split_invariance_complex_scan(k):
+    """Scanning [0, T) equals scanning [0, k) and then [k, T) from the state
+    at k - 1 (the h0 hand-off of sparc-kernal/forward/scan.py:821-826)."""
+    ar, ai, wr, wi = _rand_complex_inputs(T=37, seed=21)
+    (hr, hi), last = O.complex_scan(ar, ai, wr, wi)
+    (pr, pi), plast = O.complex_scan(ar[:, :k], ai[:, :k], wr[:, :k], wi[:, :k])
+    (sr, si), slast = O.complex_scan(ar[:, k:], ai[:, k:], wr[:, k:], wi[:, k:], h0=plast)
+    assert torch.allclose(torch.cat((pr, sr), 1), hr, atol=1e-12)
+    assert torch.allclose(torch.cat((pi, si), 1), hi, atol=1e-12)
+    assert torch.allclose(slast[0], last[0], atol=1e-12) and torch.allclose(slast[1], last[1], atol=1e-12)
+
+
+@pytest.mark.parametrize("k", [1, 13, 30])
+def test_split_invariance_real_scan(k):
+    a, b = _real_inputs()
+    h, last = O.real_scan(a, b)
+    hp, lp = O.real_scan(a[:, :k], b[:, :k])
+    hs, ls = O.real_scan(a[:, k:], b[:, k:], h0=lp)
+    assert torch.allclose(torch.cat((hp, hs), 1), h, atol=1e-12)
+    assert torch.allclose(ls, last, atol=1e-12)
+
+
+@pytest.mark.parametrize("transition", ["p1", "polar", "cartesian", "real"])
+def test_split_invariance_grouped_scan(transition):
+    B, T, M, G, k = 2, 29, 8, 4, 12
+    g = torch.Generator().manual_seed(31)
+    if transition == "p1":
+        g0, g1 = 0.5 * torch.randn(B, T, G, generator=g), torch.randn(B, T, G, generator=g)
+    elif transition == "polar":
+        g0, g1 = 0.6 + 0.39 * torch.rand(B, T, G, generator=g), torch.randn(B, T, G, generator=g)
+    else:
+        g0, g1 = 0.6 * torch.rand(B, T, G, generator=g), 0.6 * torch.rand(B, T, G, generator=g)
+    wr, wi = torch.randn(B, T, M, generator=g), torch.randn(B, T, M, generator=g)
+    nu_log, theta_log = torch.randn(M, generator=g) - 2, torch.randn(M, generator=g)
+    kw = dict(nu_log=nu_log, theta_log=theta_log)
+    full, last = O.grouped_scan_forward(transition, g0, g1, wr, wi, **kw)
+    pre, plast = O.grouped_scan_forward(transition, g0[:, :k], g1[:, :k], wr[:, :k], wi[:, :k], **kw)
+    suf, slast = O.grouped_scan_forward(transition, g0[:, k:], g1[:, k:], wr[:, k:], wi[:, k:],
+                                        h0=plast, **kw)
+    if transition == "real":
+        assert torch.allclose(torch.cat((pre, suf), 1), full, atol=1e-12)
+        assert torch.allclose(slast, last, atol=1e-12)
+    else:
+        for p_, s_, f_ in zip(pre, suf, full):
+            assert torch.allclose(torch.cat((p_, s_), 1), f_, atol=1e-12)
+        assert torch.allclose(slast[0], last[0], atol=1e-12)
+
+
+def test_segment_reset_equals_fresh_suffix_scan():
+    """``segment_pos[b, t] == 0`` zeroes the transition at t
+    (sparc-kernal/forward/scan.py:838-845): from t on, the outputs are a scan
+    of the suffix from a zero state, and before t nothing changes.  A mask
+    that is inverted, shifted by one step or ignored fails this."""
+    ar, ai, wr, wi = _rand_complex_inputs(B=3, T=26, M=4, seed=41)
+    B, T, M = wr.shape
+    h0 = (torch.randn(B, M), torch.randn(B, M))
+    seg = torch.arange(T).repeat(B, 1) + 5          # no segment starts ...
+    seg[0, 10:] = torch.arange(T - 10)              # row 0: a segment starts at 10
+    seg[2, 3:] = torch.arange(T - 3)                # row 2: at 3
+    seg[2, 17:] = torch.arange(T - 17)              # ... and again at 17
+    resets = O.reset_mask(B, T, seg)
+    assert resets.sum() == 3 and resets[0, 10] and resets[2, 3] and resets[2, 17]
+    (hr, hi), last = O.complex_scan(ar, ai, wr, wi, h0=h0, resets=resets)
+    (nr, ni), _ = O.complex_scan(ar, ai, wr, wi, h0=h0)
+    starts = {0: [10], 1: [], 2: [3, 17]}
+    for b, ks in starts.items():
+        bounds = [0] + ks + [T]
+        for j, (s, e) in enumerate(zip(bounds[:-1], bounds[1:])):
+            sl = slice(b, b + 1)
+            if j == 0:   # before the first reset: the reset-free scan from h0
+                assert torch.allclose(hr[b, s:e], nr[b, s:e], atol=1e-12)
+                continue
+            (fr, fi), _ = O.complex_scan(ar[sl, s:e], ai[sl, s:e], wr[sl, s:e], wi[sl, s:e])
+            assert torch.allclose(hr[b, s:e], fr[0], atol=1e-12)
+            assert torch.allclose(hi[b, s:e], fi[0], atol=1e-12)
+    # row 1 has no reset: identical to the reset-free scan
+    assert torch.equal(hr[1], nr[1])
+    # the real scan and the module follow the same rule
+    a, bb = _real_inputs(B=1, T=20, W=3)
+    segr = torch.arange(20)[None] + 1
+    segr[0, 8:] = torch.arange(12)
+    h, _ = O.real_scan(a, bb, h0=torch.randn(1, 3), resets=O.reset_mask(1, 20, segr))
+    fresh, _ = O.real_scan(a[:, 8:], bb[:, 8:])
+    assert torch.allclose(h[:, 8:], fresh, atol=1e-12)
+
+
+def test_module_segment_reset_equals_fresh_suffix_forward():
+    """At module level (``mixer_forward(segment_pos=...)``) a segment start
+    at k makes the outputs from k those of the module run on x[:, k:] alone."""
+    g = torch.Generator().manual_seed(43)
+    p = O.init_params(8, generator=g)
+    p.phase_direction = 0.3 * torch.randn(9, generator=g)
+    p.radial_direction = 0.3 * torch.randn(9, generator=g)
+    x = torch.randn(1, 15, 8, generator=g)
+    seg = torch.arange(15)[None] + 2
+    seg[0, 6:] = torch.arange(9)
+    h0 = (torch.randn(1, 4, generator=g), torch.randn(1, 4, generator=g))
+    y, _ = O.mixer_forward(p, x, initial_state=h0, segment_pos=seg)
+    y_suffix, _ = O.mixer_forward(p, x[:, 6:])
+    y_prefix, _ = O.mixer_forward(p, x[:, :6], initial_state=h0)
+    assert torch.allclose(y[:, 6:], y_suffix, atol=1e-12)
+    assert torch.allclose(y[:, :6], y_prefix, atol=1e-12)
+
+
+def test_reset_first_discards_h0():
+    """``reset_first`` zeroes the first transition: with it, any h0 gives the
+    zero-state scan (forward/scan.py:840-841)."""
+    ar, ai, wr, wi = _rand_complex_inputs(T=12, seed=45)
+    B, T, M = wr.shape
+    h0 = (torch.randn(B, M), torch.randn(B, M))
+    zero, _ = O.grouped_scan_forward("cartesian", ar, ai, wr, wi)
+    with_h0, _ = O.grouped_scan_forward("cartesian", ar, ai, wr, wi, h0=h0, reset_first=True)
+    without, _ = O.grouped_scan_forward("cartesian", ar, ai, wr, wi, h0=h0)
+    assert torch.allclose(with_h0[0], zero[0], atol=1e-14) and torch.allclose(with_h0[1], zero[1], atol=1e-14)
+    assert (without[0] - zero[0]).abs().max() > 1e-3      # h0 matters without the reset
+    a, b = _real_inputs(T=9)
+    hz, _ = O.grouped_scan_forward("real", a, None, b, None)
+    hr, _ = O.grouped_scan_forward("real", a, None, b, None, h0=torch.randn(2, 5), reset_first=True)
+    assert torch.allclose(hr, hz, atol=1e-14)
+
+
+def test_segment_pos_wins_over_reset_first():
+    """With ``segment_pos`` given, ``reset_first`` is ignored: the reference
+    tests ``HAS_SEGMENTS`` before ``RESET_FIRST`` (forward/scan.py:838-843),
+    so a row whose t = 0 is not a segment start keeps its h0."""
+    ar, ai, wr, wi = _rand_complex_inputs(T=10, seed=47)
+    B, T, M = wr.shape
+    h0 = (torch.randn(B, M), torch.randn(B, M))
+    seg = torch.arange(T).repeat(B, 1) + 3     # no zeros: no segment starts
+    seg[1, 0] = 0                               # row 1 starts a segment at t = 0
+    mask = O.reset_mask(B, T, seg, reset_first=True)
+    assert not mask[0].any() and mask[1, 0] and mask[1].sum() == 1
+    out, _ = O.grouped_scan_forward("cartesian", ar, ai, wr, wi, h0=h0, segment_pos=seg,
+                                    reset_first=True)
+    keep, _ = O.grouped_scan_forward("cartesian", ar, ai, wr, wi, h0=h0)
+    zero, _ = O.grouped_scan_forward("cartesian", ar, ai, wr, wi)
+    assert torch.allclose(out[0][0], keep[0][0], atol=1e-14)   # row 0 keeps h0
+    assert torch.allclose(out[0][1], zero[0][1], atol=1e-14)   # row 1 was reset
+    assert O.reset_mask(B, T, None, reset_first=True)[:, 0].all()
+
+
+def test_adjoint_with_reset_splits_at_the_reset():
+    """No gradient crosses a reset: the explicit adjoint of a scan reset at k
+    equals, on [0, k), the adjoint of the prefix alone (no dlast) and, on
+    [k, T), the adjoint of the suffix from a zero state; dh0 is the prefix's."""
+    ar, ai, wr, wi = _rand_complex_inputs(B=1, T=19, M=3, seed=49)
+    B, T, M = wr.shape
+    k = 7
+    h0 = (torch.randn(B, M), torch.randn(B, M))
+    seg = torch.arange(T)[None] + 1
+    seg[0, k:] = torch.arange(T - k)
+    resets = O.reset_mask(B, T, seg)
+    (hr, hi), _ = O.complex_scan(ar, ai, wr, wi, h0=h0, resets=resets)
+    g = torch.Generator().manual_seed(50)
+    dyr, dyi = torch.randn(B, T, M, generator=g), torch.randn(B, T, M, generator=g)
+    dl = (torch.randn(B, M, generator=g), torch.randn(B, M, generator=g))
+    full = O.complex_scan_adjoint(ar, ai, hr, hi, dyr, dyi, dlast=dl, h0=h0, resets=resets)
+    pre = O.complex_scan_adjoint(ar[:, :k], ai[:, :k], hr[:, :k], hi[:, :k], dyr[:, :k],
+                                 dyi[:, :k], h0=h0)
+    suf = O.complex_scan_adjoint(ar[:, k:], ai[:, k:], hr[:, k:], hi[:, k:], dyr[:, k:],
+                                 dyi[:, k:], dlast=dl)
+    for j in range(4):
+        assert torch.allclose(full[j][:, :k], pre[j], atol=1e-12)
+        assert torch.allclose(full[j][:, k:], suf[j], atol=1e-12)
+    assert torch.allclose(full[4][0], pre[4][0], atol=1e-12)
+    assert full[0][:, k].abs().max() == 0 and full[1][:, k].abs().max() == 0
+
+
+def test_init_matches_reference_golden_under_seed_0():
+    """``torch.manual_seed(0); SPARCMixer(16)``: the golden fixture holds the
+    reference module's nu_log and theta_log made exactly so
+    (tests/golden/make_golden.py, sparc-kernal/sparc.py:65-73).  The oracle's
+    init reproduces them bit for bit, and so does the product module."""
+    import numpy as np
+    import os
+    import sparc_amd
+    path = os.path.join(os.path.dirname(__file__), "golden", "p1_eager_golden.npz")
+    with np.load(path, allow_pickle=False) as z:
+        nu_ref, theta_ref = torch.from_numpy(z["nu_log"]), torch.from_numpy(z["theta_log"])
+    torch.manual_seed(0)
+    p = O.init_params(16)
+    assert torch.equal(p.nu_log, nu_ref) and torch.equal(p.theta_log, theta_ref)
+    torch.set_default_dtype(torch.float32)      # the reference module was built so
+    torch.manual_seed(0)
+    m = sparc_amd.SPARCMixer(16)
+    assert m.nu_log.dtype == torch.float32
+    assert torch.equal(m.nu_log.detach().double(), nu_ref)
+    assert torch.equal(m.theta_log.detach().double(), theta_ref)
+    assert torch.equal(m.write_log_gain.detach().double(), p.write_log_gain)
+    # the spectrum's documented ranges: |a| = sqrt(U) in (0, 1), theta in (0, 2 pi)
+    radius = torch.exp(-torch.exp(nu_ref))
+    assert (radius > 0).all() and (radius < 1).all()
+    theta = torch.exp(theta_ref)
+    assert (theta > 0).all() and (theta < 2 * math.pi).all()
+
+
+def test_init_gain_normalises_stationary_energy():
+    """The initial write gain is the energy normaliser of the LTI system at
+    init: a unit-variance i.i.d. write scaled by gamma has stationary state
+    variance gamma^2 / (1 - |a|^2) = 1 (up to the 1e-8 guard), checked by
+    summing the impulse response's energy, not by the gain formula."""
+    torch.manual_seed(3)
+    p = O.init_params(12)
+    gamma = torch.exp(p.write_log_gain)
+    a = torch.exp(-torch.exp(p.nu_log))            # |a| at eta = 0
+    t = torch.arange(20000, dtype=torch.float64)[:, None]
+    energy = (gamma[None] * a[None] ** t).square().sum(0)
+    slow = a < 0.999                                 # series converged within 20000 terms
+    assert torch.allclose(energy[slow], torch.ones_like(energy[slow]), atol=1e-6)
