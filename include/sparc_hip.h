@@ -256,7 +256,8 @@ sparc_status sparc_decode_step(int64_t batch, int64_t modes, int32_t io_dtype,
  * Prepared decode: the per-mode constants of the P1 step are computed once
  * (consts [M, 8] fp32: nu, cos theta, sin theta, 4 exp(2 write_log_gain) /
  * expm1(-2 nu), -log2(e) write_phase_response, -log2(e)
- * write_radial_response, theta, 0) and reused by every step while the
+ * write_radial_response, and the fp64 remainders of cos theta and sin theta
+ * as fp32) and reused by every step while the
  * parameters do not change.  The step runs the
  * two control dot products split over several workgroups per row (partials in
  * the workspace) and then the per-(row, mode) update.  Same semantics and

@@ -30,6 +30,13 @@ __device__ __forceinline__ uint16_t pack_bf16(float v) {
 
 // transitions (values of sparc_transition)
 enum Transition : int { TR_P1 = 0, TR_POLAR = 1, TR_CART = 2, TR_REAL = 3 };
+// Kernel template argument TR = transition | TR_G32: TR_G32 marks fp32 gates
+// beside bf16 I/O for the polar, cartesian and real transitions (the
+// reference's generic scans load `a` in its own dtype, independently of the
+// writes).  P1 gates are always fp32.
+constexpr int TR_G32 = 4;
+constexpr int tr_kind(int tr) { return tr & 3; }
+constexpr bool tr_g32(int tr) { return (tr & TR_G32) != 0; }
 
 // Raw vector of V elements of type IO, loaded/stored with one instruction.
 template <typename IO, int V> struct Raw;
@@ -294,6 +301,34 @@ __device__ inline float theta_rotation(float theta_log, float& c, float& s) {
   c = static_cast<float>(cd);
   s = static_cast<float>(sd);
   return static_cast<float>(th);
+}
+
+// theta's cosine and sine as unevaluated fp32 sums hi + lo: hi is the fp64
+// value rounded to fp32 (what theta_rotation returns) and lo the remainder,
+// rounded.  Rotating by (hi + lo) removes the per-mode rounding of the
+// constants themselves, which is the same at every step: over 8k steps of a
+// slow mode it leaves about 1e-4 relative error with hi alone and under 1e-5
+// with the pair.  The single-step kernels use it (they are bound by memory,
+// so the two extra FMAs per rotation cost nothing there).
+__device__ inline void theta_rotation_split(float theta_log, float& c, float& s, float& c_lo,
+                                            float& s_lo) {
+  const double th = exp(static_cast<double>(theta_log));
+  double sd, cd;
+  sincos(th, &sd, &cd);
+  c = static_cast<float>(cd);
+  s = static_cast<float>(sd);
+  c_lo = static_cast<float>(cd - static_cast<double>(c));
+  s_lo = static_cast<float>(sd - static_cast<double>(s));
+}
+
+// (c + c_lo + i (s + s_lo)) (cd + i sd) with the small products added first,
+// so the result is rounded once
+__device__ __forceinline__ void rotate_split(float c, float s, float c_lo, float s_lo, float cd,
+                                             float sd, float& re, float& im) {
+  const float lo_r = fmaf(c_lo, cd, -s_lo * sd);
+  const float lo_i = fmaf(s_lo, cd, c_lo * sd);
+  re = fmaf(c, cd, fmaf(-s, sd, lo_r));
+  im = fmaf(s, cd, fmaf(c, sd, lo_i));
 }
 
 // sin and cos of |x| <= pi/4 by their Taylor series (truncation error below

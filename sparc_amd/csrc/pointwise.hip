@@ -271,14 +271,20 @@ decode_kernel(int M, const void* x, const float* pdir, const float* rdir,
     for (int v = 0; v < 2; ++v) {
       const int m = m0 + v;
       const float nu = expf(nu_log[m]);
-      float ct, st;
-      theta_rotation(theta_log[m], ct, st);
+      float ct, st, ctl, stl;
+      theta_rotation_split(theta_log[m], ct, st, ctl, stl);
       const float eff = nu * E;
-      const float rho = expf(-eff);
+      // rho - 1 directly, as the scans form it: for slow modes rho is within
+      // 1e-4 of 1, and 1 - fp32(rho) would keep only a few bits of the phase
+      // increment (1 - rho) delta; expm1(-2 eff) = em (2 + em)
+      const float em = expm1_nonpos(-eff);
+      const float rho = 1.0f + em;
       float sn, cs;
-      sincosf((1.0f - rho) * delta, &sn, &cs);
-      const float ar = rho * (ct * cs - st * sn), ai = rho * (st * cs + ct * sn);
-      const float ratio = sqrtf(expm1f(-2.0f * eff) / expm1f(-2.0f * nu));
+      sincosf(-em * delta, &sn, &cs);
+      float cr, ci;
+      rotate_split(ct, st, ctl, stl, cs, sn, cr, ci);
+      const float ar = rho * cr, ai = rho * ci;
+      const float ratio = sqrtf(em * (2.0f + em) / expm1f(-2.0f * nu));
       const float gate = 2.0f * sigmoidf_(phase_signal * wpr[m] + radial_signal * wrr[m]);
       const float gain = expf(wlg[m]) * ratio * gate;
       n_r[v] = ar * o_r[v] - ai * o_i[v] + gain * tanhf(xr[v]);
@@ -325,7 +331,9 @@ constexpr int kDecodeRows = SPARC_DECODE_ROWS;  // rows per update workgroup (co
 #define SPARC_DECODE_PREFETCH 1
 #endif
 
-// consts[m] = (nu, cos theta, sin theta, g2, -log2(e) wpr, -log2(e) wrr, theta, 0)
+// consts[m] = (nu, cos theta, sin theta, g2, -log2(e) wpr, -log2(e) wrr, cos_lo, sin_lo)
+// where cos theta + cos_lo and sin theta + sin_lo are the fp64 values as
+// fp32 pairs (theta_rotation_split)
 // with g2 = 4 gamma^2 / expm1(-2 nu): the gain 2 gamma sqrt(expm1(-2 nu E) /
 // expm1(-2 nu)) sigmoid(q) is then sqrt(g2 expm1(-2 nu E)) / (1 + 2^(q'))
 __global__ void __launch_bounds__(256)
@@ -334,11 +342,11 @@ decode_prepare_kernel(int M, const float* nu_log, const float* theta_log, const 
   const int m = blockIdx.x * 256 + threadIdx.x;
   if (m >= M) return;
   const float nu = expf(nu_log[m]);
-  float sn, cs;
-  const float theta = theta_rotation(theta_log[m], cs, sn);
+  float sn, cs, cs_lo, sn_lo;
+  theta_rotation_split(theta_log[m], cs, sn, cs_lo, sn_lo);
   float4* c = reinterpret_cast<float4*>(consts + static_cast<int64_t>(m) * kDecodeConsts);
   c[0] = make_float4(nu, cs, sn, 4.0f * expf(2.0f * wlg[m]) / expm1f(-2.0f * nu));
-  c[1] = make_float4(-kLog2e * wpr[m], -kLog2e * wrr[m], theta, 0.0f);
+  c[1] = make_float4(-kLog2e * wpr[m], -kLog2e * wrr[m], cs_lo, sn_lo);
 }
 
 // part[b, k, 0..1] = partial dot products of row b's inputs with the phase and
@@ -413,13 +421,13 @@ decode_update_kernel(int B, int M, const void* x, const float* pbias, const floa
   }
   __syncthreads();
   if (m0 >= M) return;
-  float nu[SV], ct[SV], stt[SV], g2[SV], wp[SV], wrr_[SV];
+  float nu[SV], ct[SV], stt[SV], g2[SV], wp[SV], wrr_[SV], ctl[SV], stl[SV];
 #pragma unroll
   for (int v = 0; v < SV; ++v) {
     const float4* c = reinterpret_cast<const float4*>(consts + static_cast<int64_t>(m0 + v) * kDecodeConsts);
     const float4 c0 = c[0], c1 = c[1];
     nu[v] = c0.x; ct[v] = c0.y; stt[v] = c0.z; g2[v] = c0.w;
-    wp[v] = c1.x; wrr_[v] = c1.y;
+    wp[v] = c1.x; wrr_[v] = c1.y; ctl[v] = c1.z; stl[v] = c1.w;
   }
   // Row loads are issued ahead of the stores of earlier rows (the new state
   // may be the old one, in place, so the compiler cannot hoist them itself):
@@ -480,8 +488,9 @@ decode_update_kernel(int B, int M, const void* x, const float* pbias, const floa
       const float rho = 1.0f + em;
       float su, cu;
       sincos_half(-em * delta, su, cu);            // (1 - rho) * delta
-      const float ar = rho * fmaf(ct[v], cu, -stt[v] * su);
-      const float ai = rho * fmaf(stt[v], cu, ct[v] * su);
+      float cr, ci;
+      rotate_split(ct[v], stt[v], ctl[v], stl[v], cu, su, cr, ci);
+      const float ar = rho * cr, ai = rho * ci;
       // expm1(-2 nu E) = em (2 + em); sigmoid(q) = 1 / (1 + 2^(-q log2 e))
       const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(ps, wp[v], rs * wrr_[v])));
       const float gain = __builtin_amdgcn_sqrtf(g2[v] * fmaf(em, em, em + em)) * sg;
@@ -549,13 +558,15 @@ scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* 
       const float eta = static_cast<const float*>(g0)[gi];
       const float delta = static_cast<const float*>(g1)[gi];
       const float nu = expf(nu_log[m + v]);
-      float ct, st;
-      theta_rotation(theta_log[m + v], ct, st);
-      const float rho = expf(-nu * expf(eta));
-      float sn, cs;
-      sincosf((1.0f - rho) * delta, &sn, &cs);
-      ar[v] = rho * (ct * cs - st * sn);
-      ai[v] = rho * (st * cs + ct * sn);
+      float ct, st, ctl, stl;
+      theta_rotation_split(theta_log[m + v], ct, st, ctl, stl);
+      const float em = expm1_nonpos(-nu * expf(eta));  // rho - 1, as in the scans
+      const float rho = 1.0f + em;
+      float sn, cs, cr, ci;
+      sincosf(-em * delta, &sn, &cs);                    // (1 - rho) delta
+      rotate_split(ct, st, ctl, stl, cs, sn, cr, ci);
+      ar[v] = rho * cr;
+      ai[v] = rho * ci;
     } else if constexpr (TR == TR_POLAR) {
       const float r = load1_nt<IO>(g0, gi);
       float sn, cs;

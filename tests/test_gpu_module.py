@@ -429,3 +429,33 @@ def test_module_decode_long_sequence():
     assert rel_err(state[0], last_full[0]) <= 4e-5 and rel_err(state[1], last_full[1]) <= 4e-5, \
         f"final state rel err {rel_err(state[0], last_full[0]):.3g}, {rel_err(state[1], last_full[1]):.3g}"
     assert rel_err(yt, y_full[:, -1]) <= 4e-5
+
+
+def test_module_decode_8191_steps_single_kernel():
+    """8191 chained SPARCMixer.step calls on the single-kernel decode
+    (sparc_decode_step: the mode count 130 is not a multiple of 4), fp32,
+    with slow modes (nu down to 1e-5, |a| within 1e-5 of 1) and active phase
+    controls: the final state within 1e-4 of the float64 sequence forward.
+    There the phase increment (1 - rho) delta needs rho - 1 from expm1;
+    1 - fp32(rho) keeps a few bits of it and the error grows with the steps."""
+    print("[case] module decode 8191 steps B=2 width=260 fp32 (single kernel)", flush=True)
+    B, L, width = 2, 8191, 260
+    m = make_module(width, seed=41)
+    with torch.no_grad():
+        m.nu_log[:16].copy_(torch.log(torch.logspace(-5, -3, 16)))
+        m.phase_direction.mul_(4.0)
+    m = m.cuda()
+    g = torch.Generator().manual_seed(42)
+    x = torch.randn(B, L, width, generator=g)
+    p = oracle_params(m, requires_grad=False)
+    with torch.no_grad():
+        _, last_full = O.mixer_forward(p, x.double(), return_cache=True)
+    xc = x.cuda()
+    state = (torch.zeros(B, width // 2, device="cuda"), torch.zeros(B, width // 2, device="cuda"))
+    with torch.no_grad():
+        m.prepare_inference()
+        for t in range(L):
+            _, state = m.step(xc[:, t], state, segment_pos=None)
+    torch.cuda.synchronize()
+    e = (rel_err(state[0], last_full[0]), rel_err(state[1], last_full[1]))
+    assert max(e) <= 1e-4, f"final state rel err {e[0]:.3g}, {e[1]:.3g}"

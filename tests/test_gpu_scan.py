@@ -291,6 +291,31 @@ def test_long_p1_chained_steps():
         assert rel_err(a, b) <= 4e-5, f"final state rel err {rel_err(a, b):.3g}"
 
 
+def test_long_p1_8191_chained_steps():
+    """The 8191-step P1 case of test_long_p1_8191_steps_last_state as 8191
+    single steps (sparc_scan_step, P1 branch, state in place): the final
+    state within 1e-4 of the float64 recurrence.  The step kernel forms
+    rho - 1 with expm1 as the scans do; 1 - fp32(rho) costs this case
+    about 1.3e-4 over the sequence."""
+    print("[case] P1 chained steps B=1 T=8191 M=256 G=4 f32", flush=True)
+    case = make_case("p1", 1, 8191, 256, 4, F32, seed=878652)
+    B, T, M = 1, 8191, 256
+    state = (torch.zeros(B, M, device="cuda"), torch.zeros(B, M, device="cuda"))
+    g0, g1 = case["g0"].cuda(), case["g1"].cuda()
+    w_re, w_im = case["w_re"].cuda(), case["w_im"].cuda()
+    nu, th = case["nu_log"].cuda(), case["theta_log"].cuda()
+    for t in range(T):
+        ops.scan_step("p1", g0[:, t].contiguous(), g1[:, t].contiguous(), w_re[:, t].contiguous(),
+                      w_im[:, t].contiguous(), state, nu, th)
+    torch.cuda.synchronize()
+    d = lambda x: x.double()  # noqa: E731
+    with torch.no_grad():
+        _, last = O.grouped_scan_forward("p1", d(case["g0"]), d(case["g1"]), d(case["w_re"]),
+                                         d(case["w_im"]), d(case["nu_log"]), d(case["theta_log"]))
+    for a, b in zip(state, last):
+        assert rel_err(a, b) <= 1e-4, f"final state rel err {rel_err(a, b):.3g}"
+
+
 @pytest.mark.parametrize("transition,M,G,dtype", [
     ("p1", 128, 1, F32), ("real", 256, 32, F32), ("polar", 128, 8, BF16)], ids=["p1_f32", "real_f32", "polar_bf16"])
 def test_lookback_single_long_chain(transition, M, G, dtype):
