@@ -83,7 +83,10 @@ typedef struct sparc_scan_desc {
   int64_t groups;     /* G, divides M */
   int32_t transition; /* sparc_transition */
   int32_t io_dtype;   /* sparc_dtype of w, y, dy, dw */
-  int32_t gate_dtype; /* sparc_dtype of gate0/gate1/dgate*: F32 for P1, io_dtype otherwise */
+  int32_t gate_dtype; /* sparc_dtype of gate0/gate1/dgate*: F32 for P1; for the other
+                       * transitions io_dtype, or F32 beside BF16 I/O (the reference's
+                       * generic scans load `a` in its own dtype and upcast it:
+                       * sparc-kernal/forward/scan.py:629-630, :707-710) */
   int32_t flags;      /* SPARC_FLAG_* */
 } sparc_scan_desc;
 

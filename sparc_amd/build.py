@@ -1,7 +1,8 @@
 """Builds libsparc_hip.so (gfx950) in-tree with hipcc.
 
 ``python -m sparc_amd.build`` or ``sparc_amd.build.build()``.  Every call
-recompiles.  The objects are compiled in parallel, one process per source.
+recompiles.  The objects are compiled in parallel, one process per source
+(scan.hip in several parts, one per (transition, I/O dtype) launcher).
 """
 from __future__ import annotations
 
@@ -18,6 +19,9 @@ INCLUDE = os.path.join(ROOT, "include")
 LIB_NAME = "libsparc_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 SOURCES = ["scan.hip", "pointwise.hip", "mixer.hip"]
+# scan.hip compiles as SCAN_PARTS translation units (SPARC_SCAN_PART = 0..11:
+# the C ABI, then one per (transition, I/O dtype) launcher), in parallel
+SCAN_PARTS = 12
 ARCH = os.environ.get("SPARC_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -40,9 +44,12 @@ def _hipcc() -> str:
     return path
 
 
-def _compile(src: str, build_dir: str, extra: list[str]) -> str:
-    obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, *extra, "-I", INCLUDE, "-I", CSRC, "-c",
+def _compile(job: tuple[str, int | None], build_dir: str, extra: list[str]) -> str:
+    src, part = job
+    stem = os.path.splitext(src)[0] + ("" if part is None else f"_part{part}")
+    obj = os.path.join(build_dir, stem + ".o")
+    defs = [] if part is None else [f"-DSPARC_SCAN_PART={part}"]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *defs, *extra, "-I", INCLUDE, "-I", CSRC, "-c",
            os.path.join(CSRC, src), "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
@@ -54,8 +61,11 @@ def build(verbose: bool = False, extra: list[str] | None = None) -> str:
     extra = list(extra or [])
     build_dir = os.path.join(HERE, "_build")
     os.makedirs(build_dir, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
-        objs = list(pool.map(lambda s: _compile(s, build_dir, extra), SOURCES))
+    jobs = [(src, part) for src in SOURCES
+            for part in (range(SCAN_PARTS) if src == "scan.hip" else [None])]
+    # the scan parts are the long ones: start them first
+    with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 4)) as pool:
+        objs = list(pool.map(lambda j: _compile(j, build_dir, extra), jobs))
     tmp = LIB_PATH + ".tmp"
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     proc = subprocess.run(cmd, capture_output=True, text=True)

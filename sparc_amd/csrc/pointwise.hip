@@ -9,6 +9,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "sparc_hip.h"
 
@@ -524,7 +526,8 @@ __global__ void __launch_bounds__(256)
 scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* g0, const void* g1,
                  const float* nu_log, const float* theta_log, const void* w_re, const void* w_im,
                  float* st_re, float* st_im, void* y_re, void* y_im) {
-  constexpr bool CPLX = TR != TR_REAL;
+  constexpr bool CPLX = tr_kind(TR) != TR_REAL;
+  using GT = std::conditional_t<tr_g32(TR), float, IO>;  // gate dtype (P1: fp32 loads)
   const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   // this workgroup's slice of the state planes, addressed through buffer
   // resources (32-bit offsets from a per-workgroup base)
@@ -548,13 +551,13 @@ scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* 
     if constexpr (CPLX) unpack<IO, SV>(load_raw<IO, SV>(w_im, i), wi);
   }
   // P1 transitions also depend on each mode's nu and theta
-  const bool shared = TR != TR_P1 && gs % SV == 0;  // uniform over the launch
+  const bool shared = tr_kind(TR) != TR_P1 && gs % SV == 0;  // uniform over the launch
   float ar[SV], ai[SV];
 #pragma unroll
   for (int v = 0; v < SV; ++v) {
     if (v > 0 && shared) { ar[v] = ar[0]; ai[v] = ai[0]; continue; }
     const int64_t gi = static_cast<int64_t>(b) * G + (m + v) / gs;
-    if constexpr (TR == TR_P1) {
+    if constexpr (tr_kind(TR) == TR_P1) {
       const float eta = static_cast<const float*>(g0)[gi];
       const float delta = static_cast<const float*>(g1)[gi];
       const float nu = expf(nu_log[m + v]);
@@ -567,17 +570,17 @@ scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* 
       rotate_split(ct, st, ctl, stl, cs, sn, cr, ci);
       ar[v] = rho * cr;
       ai[v] = rho * ci;
-    } else if constexpr (TR == TR_POLAR) {
-      const float r = load1_nt<IO>(g0, gi);
+    } else if constexpr (tr_kind(TR) == TR_POLAR) {
+      const float r = load1_nt<GT>(g0, gi);
       float sn, cs;
-      sincos_moderate(load1_nt<IO>(g1, gi), sn, cs);
+      sincos_moderate(load1_nt<GT>(g1, gi), sn, cs);
       ar[v] = r * cs;
       ai[v] = r * sn;
-    } else if constexpr (TR == TR_CART) {
-      ar[v] = load1<IO>(g0, gi);
-      ai[v] = load1<IO>(g1, gi);
+    } else if constexpr (tr_kind(TR) == TR_CART) {
+      ar[v] = load1<GT>(g0, gi);
+      ai[v] = load1<GT>(g1, gi);
     } else {
-      ar[v] = load1<IO>(g0, gi);
+      ar[v] = load1<GT>(g0, gi);
       ai[v] = 0.0f;
     }
     if (reset) { ar[v] = 0.0f; ai[v] = 0.0f; }
@@ -778,7 +781,7 @@ void launch_step(bool v4, bool relu, int64_t B, int M, int G, bool reset, const 
 #define SPARC_STEP(SVV, RR)                                                                         \
   hipLaunchKernelGGL((sparc::scan_step_kernel<TR, IO, SVV, RR>), grid, dim3(256), 0, st, n, M, G, gs, \
                      reset, g0, g1, nu_log, theta_log, w_re, w_im, st_re, st_im, y_re, y_im)
-  if constexpr (TR == sparc::TR_REAL) {
+  if constexpr (sparc::tr_kind(TR) == sparc::TR_REAL) {
     if (v4) SPARC_STEP(4, false); else SPARC_STEP(1, false);
   } else {
     if (v4 && relu) SPARC_STEP(4, true);
@@ -863,8 +866,11 @@ sparc_status sparc_scan_step(const sparc_scan_desc* d, const void* gate0, const 
   const bool p1 = d->transition == SPARC_TRANSITION_P1;
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
   const bool relu = (d->flags & SPARC_FLAG_RELU_OUTPUT) != 0;
+  if (d->gate_dtype != SPARC_F32 && d->gate_dtype != SPARC_BF16) return fail2(SPARC_EINVAL, "step: unknown gate_dtype");
   if (p1 && d->gate_dtype != SPARC_F32) return fail2(SPARC_EINVAL, "step: P1 gates must be fp32");
-  if (!p1 && d->gate_dtype != d->io_dtype) return fail2(SPARC_EINVAL, "step: gate_dtype must equal io_dtype");
+  // fp32 gates beside bf16 I/O (polar, cartesian, real)
+  const bool g32 = !p1 && d->gate_dtype == SPARC_F32 && d->io_dtype == SPARC_BF16;
+  if (!p1 && d->gate_dtype != d->io_dtype && !g32) return fail2(SPARC_EINVAL, "step: bf16 gates need bf16 I/O");
   if (relu && !cplx) return fail2(SPARC_EINVAL, "step: RELU_OUTPUT needs a complex transition");
   if (!gate0 || !w_re || !state_re) return fail2(SPARC_EINVAL, "step: gate0, w_re, state_re are required");
   if (cplx && (!gate1 || !w_im || !state_im)) return fail2(SPARC_EINVAL, "step: complex transitions need gate1, w_im, state_im");
@@ -887,12 +893,22 @@ sparc_status sparc_scan_step(const sparc_scan_desc* d, const void* gate0, const 
                                       w_im, state_re, state_im, y_re, y_im, st)                          \
       : launch_step<TRV, float>(v4, relu, B, m, g, reset, gate0, gate1, nu_log, theta_log, w_re, w_im,    \
                                 state_re, state_im, y_re, y_im, st))
+#define SPARC_STEP_G32(TRV)                                                                                     \
+  launch_step<TRV | sparc::TR_G32, sparc::bf16>(v4, relu, B, m, g, reset, gate0, gate1, nu_log, theta_log, w_re, \
+                                                w_im, state_re, state_im, y_re, y_im, st)
   switch (d->transition) {
     case SPARC_TRANSITION_P1: SPARC_STEP_TR(sparc::TR_P1); break;
-    case SPARC_TRANSITION_POLAR: SPARC_STEP_TR(sparc::TR_POLAR); break;
-    case SPARC_TRANSITION_CARTESIAN: SPARC_STEP_TR(sparc::TR_CART); break;
-    default: SPARC_STEP_TR(sparc::TR_REAL); break;
+    case SPARC_TRANSITION_POLAR:
+      if (g32) SPARC_STEP_G32(sparc::TR_POLAR); else SPARC_STEP_TR(sparc::TR_POLAR);
+      break;
+    case SPARC_TRANSITION_CARTESIAN:
+      if (g32) SPARC_STEP_G32(sparc::TR_CART); else SPARC_STEP_TR(sparc::TR_CART);
+      break;
+    default:
+      if (g32) SPARC_STEP_G32(sparc::TR_REAL); else SPARC_STEP_TR(sparc::TR_REAL);
+      break;
   }
+#undef SPARC_STEP_G32
 #undef SPARC_STEP_TR
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "scan step: %s", hipGetErrorString(e));

@@ -42,6 +42,12 @@
 #include "common.h"
 #include "sparc_hip.h"
 
+// SPARC_SCAN_PART: which part of a split build this is (see the host side)
+#ifndef SPARC_SCAN_PART
+#define SPARC_SCAN_PART -1
+#endif
+#define SPARC_SCAN_OWNS(k) (SPARC_SCAN_PART < 0 || SPARC_SCAN_PART == (k))
+
 namespace sparc {
 
 
@@ -264,13 +270,13 @@ __device__ __forceinline__ LbWindow lb_window(const uint32_t* flags, int j, int 
 // ---------------------------------------------------------------------------
 template <int TR, typename IO, int V, int GM>
 struct TransitionLane {
-  static constexpr bool CPLX = TR != TR_REAL;
-  static constexpr bool P1 = TR == TR_P1;
+  static constexpr bool CPLX = tr_kind(TR) != TR_REAL;
+  static constexpr bool P1 = tr_kind(TR) == TR_P1;
   // number of distinct gate values per lane and step
   static constexpr int GV = (GM == GATE_MODE) ? V : 1;
   // number of distinct transition values per lane and step
   static constexpr int AV = (P1 || GM == GATE_MODE) ? V : 1;
-  using GT = std::conditional_t<P1, float, IO>;
+  using GT = std::conditional_t<P1 || tr_g32(TR), float, IO>;  // gate dtype
 
   // P1 per-mode constants
   float nu[P1 ? V : 1], th[P1 ? V : 1], ct[P1 ? V : 1], st[P1 ? V : 1];
@@ -331,7 +337,7 @@ struct TransitionLane {
         ar[v] = rho * (ct[v] * cd - st[v] * sd);
         ai[v] = rho * (st[v] * cd + ct[v] * sd);
       }
-    } else if constexpr (TR == TR_POLAR) {
+    } else if constexpr (tr_kind(TR) == TR_POLAR) {
 #pragma unroll
       for (int v = 0; v < AV; ++v) {
         float s, c;
@@ -339,7 +345,7 @@ struct TransitionLane {
         ar[v] = g0[v] * c;
         ai[v] = g0[v] * s;
       }
-    } else if constexpr (TR == TR_CART) {
+    } else if constexpr (tr_kind(TR) == TR_CART) {
 #pragma unroll
       for (int v = 0; v < AV; ++v) {
         ar[v] = g0[v];
@@ -690,12 +696,12 @@ scan_fwd_kernel(ScanArgs p) {
 #define SPARC_LB_BWD_WAVES 4
 #endif
 template <int TR, typename IO, int V, int GM, int S, int NW, bool SAVED>
-__global__ void __launch_bounds__(NW * 64, (SAVED && TR == TR_REAL) ? SPARC_LB_BWD_WAVES : 1)
+__global__ void __launch_bounds__(NW * 64, (SAVED && tr_kind(TR) == TR_REAL) ? SPARC_LB_BWD_WAVES : 1)
 scan_bwd_kernel(ScanArgs p) {
   using TL = TransitionLane<TR, IO, V, GM>;
   using GT = typename TL::GT;
   constexpr bool CPLX = TL::CPLX;
-  constexpr bool P1 = TR == TR_P1;
+  constexpr bool P1 = tr_kind(TR) == TR_P1;
   constexpr int AV = TL::AV;
   constexpr int GV = TL::GV;
   constexpr int C = S * NW;
@@ -1221,7 +1227,7 @@ scan_bwd_kernel(ScanArgs p) {
         acc_nu[v] += radial;
         d0[gv] += radial;
         d1[gv] -= phase * em;
-      } else if constexpr (TR == TR_POLAR) {
+      } else if constexpr (tr_kind(TR) == TR_POLAR) {
         const float r = g0[s][gv];
         const float ar = a_r[s][av], ai = a_i[s][av];
         // d|a|: (gar cos phi + gai sin phi); with a = r (cos, sin)
@@ -1230,7 +1236,7 @@ scan_bwd_kernel(ScanArgs p) {
         d0[gv] += gar * cphi + gai * sphi;
         d1[gv] += -gar * ai + gai * ar;
         (void)r;
-      } else if constexpr (TR == TR_CART) {
+      } else if constexpr (tr_kind(TR) == TR_CART) {
         d0[gv] += gar;
         d1[gv] += gai;
       } else {
@@ -1548,7 +1554,7 @@ chain_bwd_kernel(ScanArgs p) {
   using GT = typename TL::GT;
   using RawT = typename Raw<IO, V>::T;
   constexpr bool CPLX = TL::CPLX;
-  constexpr bool P1 = TR == TR_P1;
+  constexpr bool P1 = tr_kind(TR) == TR_P1;
   constexpr int AV = TL::AV;
   constexpr int GV = TL::GV;
   constexpr int C = S * NW;
@@ -1755,13 +1761,13 @@ chain_bwd_kernel(ScanArgs p) {
             acc_nu[v] += radial;
             d0[gv] += radial;
             d1[gv] -= phase * em;
-          } else if constexpr (TR == TR_POLAR) {
+          } else if constexpr (tr_kind(TR) == TR_POLAR) {
             const float ar = a_r[s][av], ai = a_i[s][av];
             float cphi, sphi;
             sincos_moderate(buf[h].g1[s][gv], sphi, cphi);
             d0[gv] += gar * cphi + gai * sphi;
             d1[gv] += -gar * ai + gai * ar;
-          } else if constexpr (TR == TR_CART) {
+          } else if constexpr (tr_kind(TR) == TR_CART) {
             d0[gv] += gar;
             d1[gv] += gai;
           } else {
@@ -1946,6 +1952,7 @@ __device__ __forceinline__ uint32_t fill_tab(const ScanArgs& p, int t0, int g_ba
 template <int TR, typename IO, int V, int S, int NW, bool RELU>
 __global__ void __launch_bounds__(NW * 64, 4)
 chain_fwd_fast_kernel(ScanArgs p) {
+  static_assert(!tr_g32(TR), "lane-shared kernels read gates in the I/O dtype");
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
   constexpr bool CPLX = TR != TR_REAL;
   constexpr int C = S * NW;
@@ -2145,6 +2152,7 @@ chain_fwd_fast_kernel(ScanArgs p) {
 template <int TR, typename IO, int V, int S, int NW, bool RELU>
 __global__ void __launch_bounds__(NW * 64, 2)
 chain_bwd_fast_kernel(ScanArgs p) {
+  static_assert(!tr_g32(TR), "lane-shared kernels read gates in the I/O dtype");
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
   constexpr bool CPLX = TR != TR_REAL;
   constexpr int C = S * NW;
@@ -2541,6 +2549,7 @@ chain_bwd_fast_kernel(ScanArgs p) {
 template <int TR, typename IO, int V, int S, int NW>
 __global__ void __launch_bounds__(NW * 64, 2)
 chain_bwd_saved_kernel(ScanArgs p) {
+  static_assert(!tr_g32(TR), "lane-shared kernels read gates in the I/O dtype");
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
   constexpr bool CPLX = TR != TR_REAL;
   constexpr int C = S * NW;
@@ -2846,6 +2855,7 @@ static_assert(kGateDepth % 2 == 0 && kGateDepth >= 2, "the loops pair plane buff
 template <int TR, typename IO, int V, int S, bool RELU>
 __global__ void __launch_bounds__(128, 1)
 chain_fwd_serial_kernel(ScanArgs p) {
+  static_assert(!tr_g32(TR), "lane-shared kernels read gates in the I/O dtype");
   static_assert(kStateChunk % S == 0, "blocks must tile the saved-state chunks");
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
   constexpr bool CPLX = TR != TR_REAL;
@@ -3010,6 +3020,7 @@ chain_fwd_serial_kernel(ScanArgs p) {
 template <int TR, typename IO, int V, int S>
 __global__ void __launch_bounds__(128, 1)
 chain_bwd_serial_kernel(ScanArgs p) {
+  static_assert(!tr_g32(TR), "lane-shared kernels read gates in the I/O dtype");
   if (blockIdx.x == 0 && threadIdx.x == 0) *p.error = 0u;  // no waits here: never an error
   constexpr bool CPLX = TR != TR_REAL;
   constexpr int MB = 64 * V;
@@ -3232,10 +3243,12 @@ chain_bwd_serial_kernel(ScanArgs p) {
 // ---------------------------------------------------------------------------
 // helpers: workspace clear, partial reductions
 // ---------------------------------------------------------------------------
+#if SPARC_SCAN_OWNS(0)
 __global__ void clear_u32_kernel(uint32_t* p, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0u;
 }
+#endif
 
 // out[r, g] = sum_{j < per} part[r, g*per + j] for G columns; fixed order.
 template <typename GT>
@@ -3254,21 +3267,18 @@ __global__ void reduce_groups_kernel(const float* part, int64_t rows, int n_mblo
 }  // namespace sparc
 
 // ===========================================================================
-// C ABI
+// host side: plans, launchers, C ABI
 // ===========================================================================
+// This file compiles as one translation unit or, with SPARC_SCAN_PART = k, as
+// part k of kScanParts (the build compiles the parts in parallel): part 0
+// holds the plan logic and the C ABI, part k >= 1 the launcher of one
+// (transition, I/O dtype) pair and every kernel it launches.  Each part sees
+// every template; an `extern template` declaration keeps the parts that do
+// not own a launcher from instantiating it.
 #include <stdio.h>
 #include <string.h>
 
-namespace {
-
-sparc_status fail(sparc_status s, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-sparc_status fail(sparc_status s, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(sparc::error_buffer(), 512, fmt, ap);
-  va_end(ap);
-  return s;
-}
+namespace sparc_host {
 
 constexpr int kChunk = 64;  // C = S * NW for every instantiation
 
@@ -3287,108 +3297,18 @@ constexpr int kWideV = 4;
 constexpr int kSerialWideMin = SPARC_SERIAL_WIDE_MIN;
 static_assert(kChunk == sparc::kStateChunk, "one saved-state chunk length");
 
-// Polls each cross-workgroup wait of the look-back kernels makes before it
-// gives up (sets the workspace error word and lets the workgroup finish).
-static std::atomic<uint32_t> g_wait_limit{1u << 20};
-
 struct Plan {
   int V = 1;
   int gm = sparc::GATE_LANE;
   bool chain = false;
   bool fast = false;  // chain kernels specialised for lane-shared gates
   bool serial = false;  // one wave per chain (lane-shared gates, many chains)
+  bool g32 = false;  // fp32 gates beside bf16 I/O (general kernels only)
   int n_chunks = 0, n_mblocks = 0, n_chains = 0;
   int64_t n_tiles = 0;
   size_t flags_off = 0, agg_off = 0, carry_off = 0, part_off = 0, total = 0;
   int64_t part_g_elems = 0, part_p_elems = 0;
 };
-
-bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
-
-// Chooses V and the gate mode; fills sizes.  Returns an error message or NULL.
-// allow_wide: the caller can use the 4-mode serial kernels (their pointers are
-// 8-byte aligned and, backward, the states come from the saved output).
-const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl, bool allow_wide = true) {
-  if (!d) return "desc is NULL";
-  if (d->batch <= 0 || d->length < 0 || d->modes <= 0 || d->groups <= 0) return "B, M, G must be > 0 and T >= 0";
-  if (d->modes % d->groups) return "groups must divide modes";
-  if (d->transition < 0 || d->transition > 3) return "unknown transition";
-  if (d->io_dtype != SPARC_F32 && d->io_dtype != SPARC_BF16) return "unknown io_dtype";
-  const bool p1 = d->transition == SPARC_TRANSITION_P1;
-  if (p1 && d->gate_dtype != SPARC_F32) return "P1 gates (eta, delta) must be fp32";
-  if (!p1 && d->gate_dtype != d->io_dtype) return "gate_dtype must equal io_dtype for this transition";
-  if ((d->flags & SPARC_FLAG_RELU_OUTPUT) && d->transition == SPARC_TRANSITION_REAL)
-    return "RELU_OUTPUT needs a complex transition";
-  if (d->batch * d->length * d->modes * 2 >= (int64_t(1) << 62)) return "tensor too large";
-  if (d->modes > INT32_MAX / 2 || d->length > INT32_MAX - kChunk || d->batch > INT32_MAX) return "dimension too large";
-  const int64_t M = d->modes, G = d->groups, gs = M / G;
-  const int vmax = (d->transition == SPARC_TRANSITION_REAL) ? 4 : 2;
-  int V = 0, gm = 0;
-  auto try_v = [&](int v) -> bool {
-    if (M % v) return false;
-    if (gs == 1 && (d->transition == SPARC_TRANSITION_CARTESIAN || d->transition == SPARC_TRANSITION_REAL)) {
-      V = v; gm = sparc::GATE_MODE; return true;
-    }
-    if (gs % v) return false;
-    const int64_t mbm = 64 * v;
-    if (G == 1 || gs % mbm == 0) { V = v; gm = sparc::GATE_CROSS; return true; }
-    if (mbm % gs == 0 && is_pow2(gs / v)) { V = v; gm = sparc::GATE_LANE; return true; }
-    return false;
-  };
-  const bool force_l = (d->flags & SPARC_FLAG_ALGO_LOOKBACK) != 0;
-  const bool force_c = (d->flags & SPARC_FLAG_ALGO_CHAIN) != 0;
-  const bool force_s = (d->flags & SPARC_FLAG_ALGO_SERIAL) != 0;
-  if (int(force_l) + int(force_c) + int(force_s) > 1)
-    return "ALGO_LOOKBACK, ALGO_CHAIN and ALGO_SERIAL are exclusive";
-  // Complex bf16 with lane-shared gates: the serial kernels stream 8 bytes
-  // per lane and plane (4 modes) when that still leaves enough chains.
-  bool wide = false;
-  if (!p1 && d->transition != SPARC_TRANSITION_REAL && d->io_dtype == SPARC_BF16 && M % kWideV == 0 &&
-      gs % kWideV == 0 && (64 * kWideV) % gs == 0 && is_pow2(gs / kWideV) &&
-      (64 * kWideV) / gs <= sparc::kFastMaxGpw && !force_l && !force_c && allow_wide) {
-    const int64_t chains = d->batch * ((M + 64 * kWideV - 1) / (64 * kWideV));
-    wide = force_s || chains >= kSerialWideMin;
-  }
-  if (wide) {
-    V = kWideV;
-    gm = sparc::GATE_LANE;
-  } else if (!try_v(vmax) && !try_v(1)) {
-    return "unsupported gate group size (need G == 1, M/G == 1, M/G dividing 64*V or a multiple of it)";
-  }
-  pl->V = V;
-  pl->gm = gm;
-  pl->n_chunks = static_cast<int>((d->length + kChunk - 1) / kChunk);
-  pl->n_mblocks = static_cast<int>((M + 64 * V - 1) / (64 * V));
-  pl->n_chains = static_cast<int>(d->batch * pl->n_mblocks);
-  pl->n_tiles = static_cast<int64_t>(pl->n_chains) * pl->n_chunks;
-  const bool lane_shared = !p1 && gm == sparc::GATE_LANE && (64 * V) / gs <= sparc::kFastMaxGpw;
-  pl->serial = wide || (lane_shared && (force_s || (!force_l && !force_c && pl->n_chains >= kSerialMin)));
-  pl->chain = pl->serial || force_c || force_s || (!force_l && pl->n_chains >= kChainMin);
-  pl->fast = pl->chain && lane_shared;
-  const bool cplx = d->transition != SPARC_TRANSITION_REAL;
-  const int NQ = cplx ? 4 : 2, NH = cplx ? 2 : 1;
-  // [0] ticket, [1] error; then, for look-back only, one flag and one
-  // aggregate per tile and (backward) the carries; then gradient partials.
-  size_t off = 256;
-  pl->flags_off = off;
-  if (!pl->chain) off += ((static_cast<size_t>(pl->n_tiles) * 4 + 255) / 256) * 256;
-  pl->agg_off = off;
-  if (!pl->chain) off += ((static_cast<size_t>(pl->n_tiles) * 64 * V * NQ * 4 + 255) / 256) * 256;
-  pl->carry_off = off;
-  if (direction == 1 && !pl->chain)
-    off += ((static_cast<size_t>(d->batch) * pl->n_chunks * M * NH * 4 + 255) / 256) * 256;
-  pl->part_off = off;
-  pl->part_g_elems = 0;
-  pl->part_p_elems = 0;
-  if (direction == 1) {
-    if (gm == sparc::GATE_CROSS) pl->part_g_elems = d->batch * d->length * pl->n_mblocks;
-    // P1 nu/theta partials: one row per tile (look-back) or per batch row (chain)
-    if (p1) pl->part_p_elems = d->batch * static_cast<int64_t>(pl->chain ? 1 : pl->n_chunks) * M;
-    off += ((static_cast<size_t>(2 * pl->part_g_elems + 2 * pl->part_p_elems) * 4 + 255) / 256) * 256;
-  }
-  pl->total = off;
-  return nullptr;
-}
 
 // steps per prefetched block of the serial kernels (compile-time tunable)
 #ifndef SPARC_SERIAL_FWD_S
@@ -3409,10 +3329,10 @@ struct Kernels {
   static constexpr int CS_F = 8, CNW_F = kChunk / CS_F;
   static constexpr int CS_B = 4, CNW_B = kChunk / CS_B;
   static void run(int dir, bool chain, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
-    if constexpr (TR != sparc::TR_P1 && GM == sparc::GATE_LANE) {
+    if constexpr (sparc::tr_kind(TR) != sparc::TR_P1 && GM == sparc::GATE_LANE && !sparc::tr_g32(TR)) {
       if (pl.serial && dir == 0) {
         const dim3 g(static_cast<unsigned>(pl.n_chains));
-        if ((a.flags & SPARC_FLAG_RELU_OUTPUT) && TR != sparc::TR_REAL)
+        if ((a.flags & SPARC_FLAG_RELU_OUTPUT) && sparc::tr_kind(TR) != sparc::TR_REAL)
           hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, true>), g, dim3(128), 0, st, a);
         else
           hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, false>), g, dim3(128), 0, st, a);
@@ -3422,7 +3342,7 @@ struct Kernels {
         constexpr int FS = 8, FNW = kChunk / FS;
         const dim3 g(static_cast<unsigned>(pl.n_chains));
         const bool relu = (a.flags & SPARC_FLAG_RELU_OUTPUT) != 0;
-        if constexpr (TR == sparc::TR_REAL) {
+        if constexpr (sparc::tr_kind(TR) == sparc::TR_REAL) {
           if (dir == 0) hipLaunchKernelGGL((sparc::chain_fwd_fast_kernel<TR, IO, V, FS, FNW, false>), g, dim3(FNW * 64), 0, st, a);
           else hipLaunchKernelGGL((sparc::chain_bwd_fast_kernel<TR, IO, V, FS, FNW, false>), g, dim3(FNW * 64), 0, st, a);
         } else if (relu) {
@@ -3445,7 +3365,7 @@ struct Kernels {
       hipLaunchKernelGGL((sparc::scan_bwd_kernel<TR, IO, V, GM, S, NW, true>), g, dim3(NW * 64), 0, st, a);
       return true;
     }
-    if constexpr (TR != sparc::TR_P1 && GM == sparc::GATE_LANE) {
+    if constexpr (sparc::tr_kind(TR) != sparc::TR_P1 && GM == sparc::GATE_LANE && !sparc::tr_g32(TR)) {
       if (pl.serial) {
         const dim3 g(static_cast<unsigned>(pl.n_chains));
         hipLaunchKernelGGL((sparc::chain_bwd_serial_kernel<TR, IO, V, kSerialBwdS>), g, dim3(128), 0, st, a);
@@ -3480,7 +3400,7 @@ struct Kernels {
 // without launching anything otherwise)
 template <int TR, typename IO>
 bool launch_v(int dir, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
-  constexpr int VM = (TR == sparc::TR_REAL) ? 4 : 2;
+  constexpr int VM = (sparc::tr_kind(TR) == sparc::TR_REAL) ? 4 : 2;
   const int V = pl.V, gm = pl.gm;
 #define SPARC_LAUNCH(VV, GG)                                                            \
   if (V == VV && gm == GG) {                                                           \
@@ -3488,7 +3408,8 @@ bool launch_v(int dir, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a)
     Kernels<TR, IO, VV, GG>::run(dir, pl.chain, pl, st, a);                              \
     return true;                                                                        \
   }
-  if constexpr ((TR == sparc::TR_POLAR || TR == sparc::TR_CART) && sparc::IsBf16<IO>::value) {
+  if constexpr ((sparc::tr_kind(TR) == sparc::TR_POLAR || sparc::tr_kind(TR) == sparc::TR_CART) &&
+                sparc::IsBf16<IO>::value && !sparc::tr_g32(TR)) {
     if (V == kWideV) {
       if (!pl.serial || gm != sparc::GATE_LANE) return false;
       if (dir == 1) return false;  // no recomputing kernel: wide plans need the saved output
@@ -3509,12 +3430,182 @@ bool launch_v(int dir, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a)
   SPARC_LAUNCH(VM, sparc::GATE_CROSS)
   SPARC_LAUNCH(1, sparc::GATE_LANE)
   SPARC_LAUNCH(1, sparc::GATE_CROSS)
-  if constexpr (TR == sparc::TR_CART || TR == sparc::TR_REAL) {
+  if constexpr (sparc::tr_kind(TR) == sparc::TR_CART || sparc::tr_kind(TR) == sparc::TR_REAL) {
     SPARC_LAUNCH(VM, sparc::GATE_MODE)
     SPARC_LAUNCH(1, sparc::GATE_MODE)
   }
 #undef SPARC_LAUNCH
   return false;
+}
+
+// Launchers by part.  TR | TR_G32: fp32 gates beside bf16 I/O.
+#define SPARC_LV(TRV, IOT) bool launch_v<TRV, IOT>(int, const Plan&, hipStream_t, const sparc::ScanArgs&)
+#if SPARC_SCAN_OWNS(1)
+template SPARC_LV(sparc::TR_P1, float);
+#else
+extern template SPARC_LV(sparc::TR_P1, float);
+#endif
+#if SPARC_SCAN_OWNS(2)
+template SPARC_LV(sparc::TR_P1, sparc::bf16);
+#else
+extern template SPARC_LV(sparc::TR_P1, sparc::bf16);
+#endif
+#if SPARC_SCAN_OWNS(3)
+template SPARC_LV(sparc::TR_POLAR, float);
+#else
+extern template SPARC_LV(sparc::TR_POLAR, float);
+#endif
+#if SPARC_SCAN_OWNS(4)
+template SPARC_LV(sparc::TR_POLAR, sparc::bf16);
+#else
+extern template SPARC_LV(sparc::TR_POLAR, sparc::bf16);
+#endif
+#if SPARC_SCAN_OWNS(5)
+template SPARC_LV(sparc::TR_CART, float);
+#else
+extern template SPARC_LV(sparc::TR_CART, float);
+#endif
+#if SPARC_SCAN_OWNS(6)
+template SPARC_LV(sparc::TR_CART, sparc::bf16);
+#else
+extern template SPARC_LV(sparc::TR_CART, sparc::bf16);
+#endif
+#if SPARC_SCAN_OWNS(7)
+template SPARC_LV(sparc::TR_REAL, float);
+#else
+extern template SPARC_LV(sparc::TR_REAL, float);
+#endif
+#if SPARC_SCAN_OWNS(8)
+template SPARC_LV(sparc::TR_REAL, sparc::bf16);
+#else
+extern template SPARC_LV(sparc::TR_REAL, sparc::bf16);
+#endif
+#if SPARC_SCAN_OWNS(9)
+template SPARC_LV(sparc::TR_POLAR | sparc::TR_G32, sparc::bf16);
+#else
+extern template SPARC_LV(sparc::TR_POLAR | sparc::TR_G32, sparc::bf16);
+#endif
+#if SPARC_SCAN_OWNS(10)
+template SPARC_LV(sparc::TR_CART | sparc::TR_G32, sparc::bf16);
+#else
+extern template SPARC_LV(sparc::TR_CART | sparc::TR_G32, sparc::bf16);
+#endif
+#if SPARC_SCAN_OWNS(11)
+template SPARC_LV(sparc::TR_REAL | sparc::TR_G32, sparc::bf16);
+#else
+extern template SPARC_LV(sparc::TR_REAL | sparc::TR_G32, sparc::bf16);
+#endif
+#undef SPARC_LV
+
+}  // namespace sparc_host
+
+#if SPARC_SCAN_OWNS(0)
+namespace {
+
+using namespace sparc_host;
+
+sparc_status fail(sparc_status s, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+sparc_status fail(sparc_status s, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(sparc::error_buffer(), 512, fmt, ap);
+  va_end(ap);
+  return s;
+}
+
+// Polls each cross-workgroup wait of the look-back kernels makes before it
+// gives up (sets the workspace error word and lets the workgroup finish).
+static std::atomic<uint32_t> g_wait_limit{1u << 20};
+
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// Chooses V and the gate mode; fills sizes.  Returns an error message or NULL.
+// allow_wide: the caller can use the 4-mode serial kernels (their pointers are
+// 8-byte aligned and, backward, the states come from the saved output).
+const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl, bool allow_wide = true) {
+  if (!d) return "desc is NULL";
+  if (d->batch <= 0 || d->length < 0 || d->modes <= 0 || d->groups <= 0) return "B, M, G must be > 0 and T >= 0";
+  if (d->modes % d->groups) return "groups must divide modes";
+  if (d->transition < 0 || d->transition > 3) return "unknown transition";
+  if (d->io_dtype != SPARC_F32 && d->io_dtype != SPARC_BF16) return "unknown io_dtype";
+  const bool p1 = d->transition == SPARC_TRANSITION_P1;
+  if (d->gate_dtype != SPARC_F32 && d->gate_dtype != SPARC_BF16) return "unknown gate_dtype";
+  if (p1 && d->gate_dtype != SPARC_F32) return "P1 gates (eta, delta) must be fp32";
+  // fp32 gates beside bf16 I/O: the general (per-lane transition) kernels
+  const bool g32 = !p1 && d->gate_dtype == SPARC_F32 && d->io_dtype == SPARC_BF16;
+  if (!p1 && d->gate_dtype != d->io_dtype && !g32) return "bf16 gates need bf16 I/O";
+  if ((d->flags & SPARC_FLAG_RELU_OUTPUT) && d->transition == SPARC_TRANSITION_REAL)
+    return "RELU_OUTPUT needs a complex transition";
+  if (d->batch * d->length * d->modes * 2 >= (int64_t(1) << 62)) return "tensor too large";
+  if (d->modes > INT32_MAX / 2 || d->length > INT32_MAX - kChunk || d->batch > INT32_MAX) return "dimension too large";
+  const int64_t M = d->modes, G = d->groups, gs = M / G;
+  const int vmax = (d->transition == SPARC_TRANSITION_REAL) ? 4 : 2;
+  int V = 0, gm = 0;
+  auto try_v = [&](int v) -> bool {
+    if (M % v) return false;
+    if (gs == 1 && (d->transition == SPARC_TRANSITION_CARTESIAN || d->transition == SPARC_TRANSITION_REAL)) {
+      V = v; gm = sparc::GATE_MODE; return true;
+    }
+    if (gs % v) return false;
+    const int64_t mbm = 64 * v;
+    if (G == 1 || gs % mbm == 0) { V = v; gm = sparc::GATE_CROSS; return true; }
+    if (mbm % gs == 0 && is_pow2(gs / v)) { V = v; gm = sparc::GATE_LANE; return true; }
+    return false;
+  };
+  const bool force_l = (d->flags & SPARC_FLAG_ALGO_LOOKBACK) != 0;
+  const bool force_c = (d->flags & SPARC_FLAG_ALGO_CHAIN) != 0;
+  const bool force_s = (d->flags & SPARC_FLAG_ALGO_SERIAL) != 0;
+  if (int(force_l) + int(force_c) + int(force_s) > 1)
+    return "ALGO_LOOKBACK, ALGO_CHAIN and ALGO_SERIAL are exclusive";
+  // Complex bf16 with lane-shared gates: the serial kernels stream 8 bytes
+  // per lane and plane (4 modes) when that still leaves enough chains.
+  bool wide = false;
+  if (!p1 && !g32 && d->transition != SPARC_TRANSITION_REAL && d->io_dtype == SPARC_BF16 && M % kWideV == 0 &&
+      gs % kWideV == 0 && (64 * kWideV) % gs == 0 && is_pow2(gs / kWideV) &&
+      (64 * kWideV) / gs <= sparc::kFastMaxGpw && !force_l && !force_c && allow_wide) {
+    const int64_t chains = d->batch * ((M + 64 * kWideV - 1) / (64 * kWideV));
+    wide = force_s || chains >= kSerialWideMin;
+  }
+  if (wide) {
+    V = kWideV;
+    gm = sparc::GATE_LANE;
+  } else if (!try_v(vmax) && !try_v(1)) {
+    return "unsupported gate group size (need G == 1, M/G == 1, M/G dividing 64*V or a multiple of it)";
+  }
+  pl->V = V;
+  pl->gm = gm;
+  pl->g32 = g32;
+  pl->n_chunks = static_cast<int>((d->length + kChunk - 1) / kChunk);
+  pl->n_mblocks = static_cast<int>((M + 64 * V - 1) / (64 * V));
+  pl->n_chains = static_cast<int>(d->batch * pl->n_mblocks);
+  pl->n_tiles = static_cast<int64_t>(pl->n_chains) * pl->n_chunks;
+  const bool lane_shared = !p1 && !g32 && gm == sparc::GATE_LANE && (64 * V) / gs <= sparc::kFastMaxGpw;
+  pl->serial = wide || (lane_shared && (force_s || (!force_l && !force_c && pl->n_chains >= kSerialMin)));
+  pl->chain = pl->serial || force_c || force_s || (!force_l && pl->n_chains >= kChainMin);
+  pl->fast = pl->chain && lane_shared;
+  const bool cplx = d->transition != SPARC_TRANSITION_REAL;
+  const int NQ = cplx ? 4 : 2, NH = cplx ? 2 : 1;
+  // [0] ticket, [1] error; then, for look-back only, one flag and one
+  // aggregate per tile and (backward) the carries; then gradient partials.
+  size_t off = 256;
+  pl->flags_off = off;
+  if (!pl->chain) off += ((static_cast<size_t>(pl->n_tiles) * 4 + 255) / 256) * 256;
+  pl->agg_off = off;
+  if (!pl->chain) off += ((static_cast<size_t>(pl->n_tiles) * 64 * V * NQ * 4 + 255) / 256) * 256;
+  pl->carry_off = off;
+  if (direction == 1 && !pl->chain)
+    off += ((static_cast<size_t>(d->batch) * pl->n_chunks * M * NH * 4 + 255) / 256) * 256;
+  pl->part_off = off;
+  pl->part_g_elems = 0;
+  pl->part_p_elems = 0;
+  if (direction == 1) {
+    if (gm == sparc::GATE_CROSS) pl->part_g_elems = d->batch * d->length * pl->n_mblocks;
+    // P1 nu/theta partials: one row per tile (look-back) or per batch row (chain)
+    if (p1) pl->part_p_elems = d->batch * static_cast<int64_t>(pl->chain ? 1 : pl->n_chunks) * M;
+    off += ((static_cast<size_t>(2 * pl->part_g_elems + 2 * pl->part_p_elems) * 4 + 255) / 256) * 256;
+  }
+  pl->total = off;
+  return nullptr;
 }
 
 bool launch(int dir, const sparc_scan_desc* d, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
@@ -3524,12 +3615,15 @@ bool launch(int dir, const sparc_scan_desc* d, const Plan& pl, hipStream_t st, c
       return bf ? launch_v<sparc::TR_P1, sparc::bf16>(dir, pl, st, a)
                 : launch_v<sparc::TR_P1, float>(dir, pl, st, a);
     case SPARC_TRANSITION_POLAR:
+      if (pl.g32) return launch_v<sparc::TR_POLAR | sparc::TR_G32, sparc::bf16>(dir, pl, st, a);
       return bf ? launch_v<sparc::TR_POLAR, sparc::bf16>(dir, pl, st, a)
                 : launch_v<sparc::TR_POLAR, float>(dir, pl, st, a);
     case SPARC_TRANSITION_CARTESIAN:
+      if (pl.g32) return launch_v<sparc::TR_CART | sparc::TR_G32, sparc::bf16>(dir, pl, st, a);
       return bf ? launch_v<sparc::TR_CART, sparc::bf16>(dir, pl, st, a)
                 : launch_v<sparc::TR_CART, float>(dir, pl, st, a);
     default:
+      if (pl.g32) return launch_v<sparc::TR_REAL | sparc::TR_G32, sparc::bf16>(dir, pl, st, a);
       return bf ? launch_v<sparc::TR_REAL, sparc::bf16>(dir, pl, st, a)
                 : launch_v<sparc::TR_REAL, float>(dir, pl, st, a);
   }
@@ -3597,12 +3691,19 @@ static sparc_status clear_ws(const Plan& pl, void* ws, hipStream_t st) {
   return SPARC_OK;
 }
 
-static sparc_status check_io_ptrs(const sparc_scan_desc* d, const Plan& pl, const void* const* ptrs, int n) {
-  const size_t esz = d->io_dtype == SPARC_BF16 ? 2 : 4;
+static sparc_status check_ptrs(size_t esz, const Plan& pl, const void* const* ptrs, int n) {
   for (int i = 0; i < n; ++i)
     if (ptrs[i] && !aligned(ptrs[i], esz * pl.V))
       return fail(SPARC_EINVAL, "tensor %d not aligned to %zu bytes", i, esz * pl.V);
   return SPARC_OK;
+}
+
+static sparc_status check_io_ptrs(const sparc_scan_desc* d, const Plan& pl, const void* const* ptrs, int n) {
+  return check_ptrs(d->io_dtype == SPARC_BF16 ? 2 : 4, pl, ptrs, n);
+}
+
+static sparc_status check_gate_ptrs(const sparc_scan_desc* d, const Plan& pl, const void* const* ptrs, int n) {
+  return check_ptrs(d->gate_dtype == SPARC_BF16 ? 2 : 4, pl, ptrs, n);
 }
 
 sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, const void* gate1,
@@ -3627,7 +3728,7 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, con
   if (sparc_status s = check_io_ptrs(d, pl, ptrs, 4)) return s;
   if (pl.gm == sparc::GATE_MODE) {
     const void* gp[] = {gate0, gate1};
-    if (sparc_status s = check_io_ptrs(d, pl, gp, 2)) return s;
+    if (sparc_status s = check_gate_ptrs(d, pl, gp, 2)) return s;
   }
   if (!aligned(chunk_state, 8 * pl.V)) return fail(SPARC_EINVAL, "chunk_state must be %d-byte aligned", 8 * pl.V);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -3718,7 +3819,7 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
   if (sparc_status s = check_io_ptrs(d, pl, ptrs, 8)) return s;
   if (pl.gm == sparc::GATE_MODE) {
     const void* gp[] = {gate0, gate1, dgate0, dgate1};
-    if (sparc_status s = check_io_ptrs(d, pl, gp, 4)) return s;
+    if (sparc_status s = check_gate_ptrs(d, pl, gp, 4)) return s;
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (!pl.chain)
@@ -3787,3 +3888,4 @@ int sparc_scan_workspace_error(const void* workspace, sparc_stream_t stream) {
 }
 
 }  // extern "C"
+#endif  // SPARC_SCAN_OWNS(0)

@@ -69,7 +69,9 @@ def _check_scan_inputs(transition, g0, g1, w_re, w_im, nu_log, theta_log, h0_re,
     M, G, io = w_re.shape[-1], g0.shape[-1], w_re.dtype
     if G <= 0 or M % G:
         raise ValueError("the gate group count G must divide M")
-    gate_dtype = torch.float32 if p1 else io
+    gate_dtype = torch.float32 if p1 else g0.dtype
+    if not p1 and gate_dtype != io and not (gate_dtype == torch.float32 and io == torch.bfloat16):
+        raise ValueError("gates must be in the writes' dtype, or fp32 beside bf16 writes")
     _lib.expect(g0, lead + (G,), gate_dtype, "g0")
     if cplx:
         _lib.expect(g1, lead + (G,), gate_dtype, "g1")
@@ -178,7 +180,8 @@ def scan_step(transition, g0, g1, w_re, w_im, state, nu_log=None, theta_log=None
     (the scan-core decode step): h <- a h + w, the same as ``chunk_scan`` with
     T = 1 and the state as initial state.
 
-    g0, g1: gates [B, G] (fp32 eta, delta for "p1"; w's dtype otherwise);
+    g0, g1: gates [B, G] (fp32 eta, delta for "p1"; otherwise bf16 beside bf16
+    w, else passed as fp32);
     w_re, w_im: [B, M]; state: (state_re, state_im) fp32 [B, M] contiguous
     (a single tensor for "real"), modified in place.  Returns the new state in
     w's dtype (``relu(cat)`` [B, 2M] with ``relu_output``) when
@@ -200,8 +203,7 @@ def scan_step(transition, g0, g1, w_re, w_im, state, nu_log=None, theta_log=None
     p1 = transition == "p1"
     io = _lib.io_code(w_re.dtype)
     if not p1:
-        g0 = g0.to(w_re.dtype)
-        g1 = None if g1 is None else g1.to(w_re.dtype)
+        g0, g1 = _gate_dtype(g0, g1, w_re.dtype)
     else:
         g0, g1 = g0.float(), g1.float()
     gate_io = _lib.io_code(g0.dtype)
@@ -230,6 +232,16 @@ def scan_step(transition, g0, g1, w_re, w_im, state, nu_log=None, theta_log=None
 # ---------------------------------------------------------------------------
 def _c(t):
     return None if t is None else t.contiguous()
+
+
+def _gate_dtype(g0, g1, io_dtype):
+    """Gates of the polar, cartesian and real transitions keep bf16 only
+    beside bf16 writes; otherwise they go to the library as fp32 (exact for
+    bf16 gates).  The reference loads ``a`` in its own dtype and computes in
+    fp32 whatever the writes' dtype (forward/scan.py:629-630, 707-710)."""
+    both_bf16 = g0.dtype == torch.bfloat16 and (g1 is None or g1.dtype == torch.bfloat16)
+    dt = torch.bfloat16 if (both_bf16 and io_dtype == torch.bfloat16) else torch.float32
+    return g0.to(dt), (None if g1 is None else g1.to(dt))
 
 
 class _ChunkScan(torch.autograd.Function):
@@ -301,7 +313,9 @@ def chunk_scan(transition: str, g0, g1, w_re, w_im=None, nu_log=None, theta_log=
 
     transition: "p1" (g0 = eta, g1 = delta, fp32 [B,T,G]; nu_log/theta_log [M]),
     "polar" (g0 = r, g1 = phi), "cartesian" (g0 + i g1), "real" (g0 = a).
-    Gates of non-P1 transitions are cast to the dtype of w.
+    Gates of non-P1 transitions keep their dtype: bf16 gates with bf16 w run
+    in bf16 I/O, anything else passes fp32 gates (bf16 gates beside fp32 w are
+    widened exactly); their gradients come back in the gates' dtype.
     Returns (y, last): y = (h_re, h_im) [B,T,M] each, or relu(cat) [B,T,2M]
     with relu_output, or h [B,T,M] for "real"; last = (last_re, last_im) fp32
     [B,M] (a single tensor for "real")."""
@@ -326,8 +340,7 @@ def chunk_scan(transition: str, g0, g1, w_re, w_im=None, nu_log=None, theta_log=
         g0, g1 = g0.float(), g1.float()
         nu_log, theta_log = nu_log.float(), theta_log.float()
     else:
-        g0 = g0.to(w_re.dtype)
-        g1 = g1.to(w_re.dtype) if g1 is not None else None
+        g0, g1 = _gate_dtype(g0, g1, w_re.dtype)
         nu_log = theta_log = None
     h0_re = h0_im = None
     if initial_state is not None:

@@ -56,7 +56,8 @@ def test_workspace_and_chunk_queries():
     (dict(transition=7), b"unknown transition"),
     (dict(io_dtype=5), b"io_dtype"),
     (dict(transition=0, gate_dtype=1), b"P1 gates"),
-    (dict(gate_dtype=0), b"gate_dtype must equal"),
+    (dict(io_dtype=0, gate_dtype=1), b"bf16 gates need bf16 I/O"),
+    (dict(gate_dtype=3), b"unknown gate_dtype"),
     (dict(transition=3, flags=1), b"RELU_OUTPUT"),
     (dict(batch=0), b"must be > 0"),
     (dict(groups=256 // 3 * 0 + 64, modes=192), b"unsupported gate group"),
@@ -68,6 +69,17 @@ def test_invalid_descriptors_rejected_on_host(kw, msg):
     st = lib.sparc_scan_forward(ctypes.byref(d), *([None] * 13), 0, None)
     assert st == 1
     assert msg in lib.sparc_last_error()
+
+
+@pytest.mark.parametrize("transition,groups", [(1, 16), (2, 256), (3, 256), (3, 16)])
+def test_fp32_gates_with_bf16_io_plan(transition, groups):
+    """fp32 gates beside bf16 writes (the reference's generic scans upcast
+    `a` from its own dtype) are a valid plan for the polar, cartesian and real
+    transitions, per-element or grouped."""
+    lib = _lib.load()
+    d = _desc(transition=transition, groups=groups, io_dtype=1, gate_dtype=0)
+    assert lib.sparc_scan_workspace_bytes(ctypes.byref(d), 0) > 0
+    assert lib.sparc_scan_workspace_bytes(ctypes.byref(d), 1) > 0
 
 
 def test_forward_requires_workspace():
@@ -196,8 +208,11 @@ def test_raw_backward_and_step_reject_mismatched_tensors():
         ops.scan_backward_raw("polar", kw["g0"], kw["g1"], kw["w_re"], kw["w_im"], cs[:, :, :4], dy, dy)
     with pytest.raises(ValueError, match="dy_re"):
         ops.scan_backward_raw("polar", kw["g0"], kw["g1"], kw["w_re"], kw["w_im"], cs, dy, dy, relu_output=True)
-    with pytest.raises(ValueError, match="g0"):
-        ops.scan_forward_raw("polar", **{**kw, "g0": kw["g0"].float()})  # gates in w's dtype
+    with pytest.raises(ValueError, match="g1"):   # the two gates in one dtype
+        ops.scan_forward_raw("polar", **{**kw, "g0": kw["g0"].float()})
+    kw32 = _raw_inputs("polar", io=torch.float32)
+    with pytest.raises(ValueError, match="writes' dtype"):   # bf16 gates need bf16 writes
+        ops.scan_forward_raw("polar", **{**kw32, "g0": kw32["g0"].bfloat16(), "g1": kw32["g1"].bfloat16()})
     state = (torch.zeros(2, 8), torch.zeros(2, 8))
     with pytest.raises(ValueError, match="nu_log"):
         ops.scan_step("p1", torch.zeros(2, 1), torch.zeros(2, 1), torch.zeros(2, 8), torch.zeros(2, 8),
