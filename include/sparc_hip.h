@@ -285,6 +285,26 @@ sparc_status sparc_decode_step_prepared(int64_t batch, int64_t modes, int32_t io
                                         sparc_stream_t stream);
 
 /*
+ * sparc_decode_step_prepared without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference.  The
+ * partial sums live in a library-owned device array of 512 KiB + 256 B per
+ * GPU (batch <= 4096 rows; larger batches return SPARC_EINVAL), kept until
+ * the process ends; nothing is allocated.  Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (concurrent streams, threads)
+ * race and must be ordered by the caller.  The stream must belong to the
+ * current device.  Same arguments and results as sparc_decode_step_prepared.
+ */
+sparc_status sparc_decode_step_prepared_noalloc(int64_t batch, int64_t modes, int32_t io_dtype,
+                                                const void* x,
+                                                const float* phase_direction,
+                                                const float* radial_direction,
+                                                const float* consts,
+                                                const float* state_re, const float* state_im,
+                                                float* new_re, float* new_im, void* y,
+                                                sparc_stream_t stream);
+
+/*
  * One step of the scan for B independent rows, with the state carried by the
  * caller: h <- a h + w, fp32 state updated in place (the scan-core decode
  * step).  The same as sparc_scan_forward with T = 1 and h0 = state: the

@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "sparc_decode_workspace_bytes",
     "sparc_decode_prepare",
     "sparc_decode_step_prepared",
+    "sparc_decode_step_prepared_noalloc",
     "sparc_scan_step",
     "sparc_column_sum",
     "sparc_mixer_workspace_bytes",
@@ -117,6 +118,8 @@ def load() -> ctypes.CDLL:
         lib.sparc_decode_prepare.restype = ctypes.c_int
         lib.sparc_decode_step_prepared.argtypes = [_I64, _I64, _I32] + [_P] * 9 + [_P, _SZ, _P]
         lib.sparc_decode_step_prepared.restype = ctypes.c_int
+        lib.sparc_decode_step_prepared_noalloc.argtypes = [_I64, _I64, _I32] + [_P] * 9 + [_P]
+        lib.sparc_decode_step_prepared_noalloc.restype = ctypes.c_int
         lib.sparc_scan_step.argtypes = [D] + [_P] * 10 + [_P]
         lib.sparc_scan_step.restype = ctypes.c_int
         lib.sparc_column_sum.argtypes = [_I64, _I64, _P, _P, ctypes.c_int, _P]

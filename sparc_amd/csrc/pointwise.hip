@@ -14,6 +14,18 @@
 #include "common.h"
 #include "sparc_hip.h"
 
+#include <atomic>
+
+// Scratch of sparc_decode_step_prepared_noalloc: the control dot products'
+// partial sums (kDotSplit pairs of floats per row) for up to
+// kNoallocDecodeRows rows.  Library-owned device memory: each GPU the library
+// runs on holds its own copy until the process ends.  In host code the name
+// is a stand-in, not a device address: host code uses the address that
+// hipGetSymbolAddress returns for the current device (noalloc_scratch below).
+constexpr int64_t kNoallocDecodeRows = 4096;
+constexpr size_t kNoallocScratchBytes = 256 + static_cast<size_t>(kNoallocDecodeRows) * 16 * 2 * sizeof(float);
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
 namespace sparc {
 
 constexpr float kLog16 = 2.772588722239781f;       // log(16)
@@ -628,6 +640,33 @@ sparc_status fail2(sparc_status s, const char* fmt, ...) {
   return s;
 }
 bool al(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Device address of the current GPU's copy of `scratch`, looked up once per
+// device with that device current (the stream must belong to it) and kept.
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+
+sparc_status noalloc_scratch(sparc_stream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail2(SPARC_EHIP, "no-alloc decode: hipGetDevice: %s", hipGetErrorString(e));
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) return fail2(SPARC_EHIP, "no-alloc decode: hipStreamGetDevice: %s", hipGetErrorString(e));
+    if (sdev != dev) return fail2(SPARC_EINVAL, "no-alloc decode: the stream's device (%d) is not the current one (%d)", sdev, dev);
+  }
+  if (dev < 0 || dev >= kMaxDevices) return fail2(SPARC_EUNSUPPORTED, "no-alloc decode: device %d", dev);
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail2(SPARC_EHIP, "no-alloc decode: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    g_scratch_addr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return SPARC_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -850,6 +889,24 @@ sparc_status sparc_decode_step_prepared(int64_t batch, int64_t modes, int32_t io
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "decode: %s", hipGetErrorString(e));
+}
+
+sparc_status sparc_decode_step_prepared_noalloc(int64_t batch, int64_t modes, int32_t io_dtype,
+                                                const void* x, const float* phase_direction,
+                                                const float* radial_direction, const float* consts,
+                                                const float* state_re, const float* state_im,
+                                                float* new_re, float* new_im, void* y,
+                                                sparc_stream_t stream) {
+  static_assert(sparc::kDotSplit == 16, "kNoallocScratchBytes counts 16 partial pairs per row");
+  if (batch > kNoallocDecodeRows)
+    return fail2(SPARC_EINVAL, "no-alloc decode: batch %lld exceeds its scratch limit of %lld rows",
+                 static_cast<long long>(batch), static_cast<long long>(kNoallocDecodeRows));
+  if (batch >= 0 && modes > 0 && sparc_decode_workspace_bytes(batch, modes) > kNoallocScratchBytes)
+    return fail2(SPARC_EINVAL, "no-alloc decode: scratch too small");
+  void* ws = nullptr;
+  if (sparc_status s = noalloc_scratch(stream, &ws)) return s;
+  return sparc_decode_step_prepared(batch, modes, io_dtype, x, phase_direction, radial_direction, consts,
+                                    state_re, state_im, new_re, new_im, y, ws, kNoallocScratchBytes, stream);
 }
 
 sparc_status sparc_scan_step(const sparc_scan_desc* d, const void* gate0, const void* gate1,
