@@ -232,8 +232,10 @@ __device__ __forceinline__ void store_agent_vec(float* p, const float (&v)[N]) {
 // consumed per flag read, instead of one flag and one aggregate round trip
 // per chunk, so few long chains still move their carry frontier at the rate
 // their tiles finish.  Spins only while chunk j has published nothing, at most
-// `limit` polls: then it sets *error and reports {0, inclusive}, so that every
-// wave still finishes (the host reports the error).
+// `limit` polls: then it sets *error and reports {0, inclusive, failed}, so
+// that every wave still finishes; the caller then poisons its carry with NaN,
+// so the failure shows in the outputs and gradients as well as in the error
+// word.
 constexpr int kLbLoads = 4;  // aggregates in flight per composition step (forward)
 #ifndef SPARC_LB_BWD_LOADS
 #define SPARC_LB_BWD_LOADS 1
@@ -242,6 +244,7 @@ constexpr int kLbLoadsBwd = SPARC_LB_BWD_LOADS;  // the same, backward (register
 struct LbWindow {
   int n;
   bool incl;
+  bool failed;  // the wait gave up: the carry it ends on is not valid
 };
 __device__ __forceinline__ LbWindow lb_window(const uint32_t* flags, int j, int dir, int n_chunks, uint32_t* error,
                                               uint32_t limit, int lane) {
@@ -255,14 +258,14 @@ __device__ __forceinline__ LbWindow lb_window(const uint32_t* flags, int j, int 
     const int fe = empty ? __builtin_ctzll(empty) : 64;
     if (fi == 0 || fe > 0) {
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      return fi < fe ? LbWindow{fi, true} : LbWindow{fe, false};
+      return fi < fe ? LbWindow{fi, true, false} : LbWindow{fe, false, false};
     }
     // once any wait of this launch has failed, stop waiting at all
     if ((it & 255u) == 255u && __builtin_amdgcn_readfirstlane(load_agent(error)) != 0u) break;
     __builtin_amdgcn_s_sleep(2);
   }
   store_agent(error, 1u);
-  return LbWindow{0, true};
+  return LbWindow{0, true, true};
 }
 
 // ---------------------------------------------------------------------------
@@ -596,6 +599,13 @@ scan_fwd_kernel(ScanArgs p) {
             } else {
               cr[v] = Xpr[v] * h[v] + Xqr[v];
               ci[v] = 0.0f;
+            }
+          }
+          if (w.failed) {  // gave up waiting: make the failure visible downstream
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              cr[v] = __builtin_nanf("");
+              if constexpr (CPLX) ci[v] = __builtin_nanf("");
             }
           }
           break;
@@ -1088,6 +1098,13 @@ scan_bwd_kernel(ScanArgs p) {
             } else {
               cr[v] = Xpr[v] * h[v] + Xqr[v];
               ci[v] = 0.0f;
+            }
+          }
+          if (w.failed) {  // gave up waiting: make the failure visible downstream
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              cr[v] = __builtin_nanf("");
+              if constexpr (CPLX) ci[v] = __builtin_nanf("");
             }
           }
           break;

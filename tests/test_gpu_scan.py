@@ -369,7 +369,8 @@ def test_workspace_no_spin_errors(algo_flag):
 def test_wait_bound_reports_and_finishes():
     """With every look-back wait bounded at 0 polls, a launch still finishes:
     each tile that would wait gives up at once and reports through the
-    workspace error word (its results are invalid).  With the default bound
+    workspace error word, and poisons its carry with NaN, so the outputs (and,
+    backward, the gradients) show the failure too.  With the default bound
     restored the same launch reports nothing and matches the oracle."""
     import ctypes
     from sparc_amd import _lib
@@ -392,8 +393,27 @@ def test_wait_bound_reports_and_finishes():
     prev = lib.sparc_set_wait_limit(0)
     try:
         assert forward() == 1
+        # the tiles that gave up poison their carries: the failure shows in
+        # the outputs and in the final state, not only in the error word
+        torch.cuda.synchronize()
+        assert torch.isnan(y).any() and torch.isnan(cs[:, -1]).all()
     finally:
         lib.sparc_set_wait_limit(prev)
+    # a valid look-back forward, then a backward whose waits all give up
+    ops.set_algorithm("lookback")
+    try:
+        xw = L["w_re"].detach().clone().requires_grad_()
+        hw, _ = ops.chunk_scan("real", L["g0"].detach(), None, xw, None)
+        assert not torch.isnan(hw).any()
+        lib.sparc_set_wait_limit(0)
+        try:
+            hw.backward(torch.ones_like(hw))
+            torch.cuda.synchronize()
+        finally:
+            lib.sparc_set_wait_limit(prev)
+        assert torch.isnan(xw.grad).any()
+    finally:
+        ops.set_algorithm("auto")
     assert forward() == 0
     ops.set_algorithm("lookback")
     try:
