@@ -38,6 +38,7 @@ HBM_PEAK_GBS = 8000.0
 ROOT = os.path.dirname(os.path.abspath(__file__))
 TRAFFIC_FILE = os.path.join("profiles", "scan_cfg2_hbm_traffic.md")
 TRAFFIC_FILE_CFG3 = os.path.join("profiles", "scan_cfg3_hbm_traffic.md")
+COUNTERS_FILE = os.path.join("profiles", "counters_bench_kernels.md")
 # kernels each algorithm runs at this shape (backward, forward)
 ALGO_KERNELS = {"auto": ("chain_bwd_serial_kernel", "chain_fwd_serial_kernel"),
                 "serial": ("chain_bwd_serial_kernel", "chain_fwd_serial_kernel"),
@@ -56,6 +57,21 @@ def measured_traffic(path: str = TRAFFIC_FILE) -> dict:
                 parts = line.split()
                 if len(parts) == 3 and parts[0] == "traffic":
                     out[parts[1]] = int(parts[2])
+    except OSError:
+        pass
+    return out
+
+
+def measured_valu_busy(path: str = COUNTERS_FILE) -> dict:
+    """VALU-busy percentage by kernel name from the committed counter summary
+    (rocprofv3 VALUBusy); empty if the file is absent."""
+    out = {}
+    try:
+        with open(os.path.join(ROOT, path)) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "valu_busy":
+                    out[parts[1]] = float(parts[2])
     except OSError:
         pass
     return out
@@ -282,7 +298,9 @@ def bench_module(args, dev):
     reference does, controllers and write responses set to small random
     values so that every term is active).  On this shape the module runs the
     fused sequence path (controls, write, P1 scan, relu(cat) epilogue and their
-    backward); it is VALU-bound, so the report is time and tokens/s."""
+    backward).  Its kernels are VALU-bound (the counter summary's VALU busy),
+    so its roofline object reports the HBM rate of its algorithmic bytes
+    beside the measured traffic and VALU-busy figures."""
     import sparc_amd
     from sparc_amd.mixer import use_fused
     B, T, W = 8, 4096, 2 * 1024 * 16
@@ -317,9 +335,22 @@ def bench_module(args, dev):
     ms = e0.elapsed_time(e1) / steps
     del m, x, dy
     torch.cuda.empty_cache()
+    # algorithmic bytes of the drop-in (G = 1) form: per token 10 bf16 planes
+    # of M (x in, y out; dy in, x in, dx out) and 6 fp32 control values
+    M = W // 2
+    algo_bytes = B * T * (M * 10 * 2 + 6 * 4)
+    kernels = ("ctrl_fwd_kernel", "mixer_fwd_kernel", "mixer_bwd_kernel", "ctrl_bwd_kernel")
+    traffic = measured_traffic(COUNTERS_FILE)
+    valu = measured_valu_busy()
+    measured = sum(traffic[k] for k in kernels) if path == "fused" and all(k in traffic for k in kernels) else None
+    gbs = algo_bytes / (ms * 1e-3) / 1e9
+    roof = {"bound": "valu", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_step": algo_bytes,
+            "traffic": measured, "traffic_source": COUNTERS_FILE if measured else None,
+            "valu_busy_pct": {k: valu[k] for k in kernels if k in valu} or None}
     return {"workload": "SPARCMixer forward + backward (the drop-in module), bf16 x, fp32 parameters",
             "B": B, "T": T, "width": W, "path": path, "steps": steps, "ms_per_step": round(ms, 3),
-            "tokens_per_s": round(B * T / (ms * 1e-3), 1)}
+            "tokens_per_s": round(B * T / (ms * 1e-3), 1), "roofline": roof}
 
 
 def _graph_time_us(dev, n_graph, reps, step_fn):
