@@ -103,63 +103,6 @@ mixer_prepare_kernel(int M, const float* nu_log, const float* theta_log, const f
 }
 
 // ---------------------------------------------------------------------------
-// wave reductions (dpp_mov and the DPP controls: common.h)
-// ---------------------------------------------------------------------------
-// N values per lane -> the wave sums of all N (a reduce-scatter butterfly:
-// each stage exchanges half of the values with the lane 32, 16, 8 or 4 away
-// and keeps the other half).  The 32- and 16-lane stages swap register
-// halves (v_permlane32_swap / v_permlane16_swap: one swap and one add per
-// pair, no selects); the 8- and 4-lane stages choose what to keep and send
-// with bank-masked DPP moves and read the partner through DPP, so nothing
-// goes through LDS and no value is selected by a lane-dependent index.  The
-// rest of each group of lanes is summed into its first lane.  On return the
-// lanes l with l % G == 0 hold in v[0..K-1] the sums of values
-// (l / G) * K ... (l / G) * K + K - 1, with K = max(1, N / 16) and
-// G = 64 K / N; the other lanes hold partial sums.  Fixed order: the result
-// does not depend on timing.
-template <int N>
-__device__ __forceinline__ void wave_sums_to_leaders(float (&v)[N]) {
-  static_assert(N == 4 || N == 8 || N == 16 || N == 32, "4, 8, 16 or 32 values per lane");
-#pragma unroll
-  for (int i = 0; i < N / 2; ++i) {  // lanes 32 apart: the lower half of the wave keeps values 0 .. N/2-1
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + N / 2]), false, false);
-    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-#pragma unroll
-  for (int i = 0; i < N / 4; ++i) {  // lanes 16 apart: even rows keep the lower half
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + N / 4]), false, false);
-    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-  if constexpr (N >= 8) {
-#pragma unroll
-    for (int i = 0; i < N / 8; ++i) {  // lanes 8 apart: lanes 8-15 of a row (banks 2, 3) keep the upper half
-      const float keep = dpp_mov<kDppIdentity, 0xC>(v[i], v[i + N / 8]);
-      const float send = dpp_mov<kDppIdentity, 0xC>(v[i + N / 8], v[i]);
-      v[i] = keep + dpp_mov<kDppRowRor + 8>(0.0f, send);  // lane ^ 8
-    }
-  }
-  if constexpr (N >= 16) {
-#pragma unroll
-    for (int i = 0; i < N / 16; ++i) {  // lanes 4 apart: banks 1, 3 keep the upper half
-      const float keep = dpp_mov<kDppIdentity, 0xA>(v[i], v[i + N / 16]);
-      const float send = dpp_mov<kDppIdentity, 0xA>(v[i + N / 16], v[i]);
-      float recv = dpp_mov<kDppRowShr + 4, 0xA>(0.0f, send);  // banks 1, 3 read lane - 4
-      recv = dpp_mov<kDppRowShl + 4, 0x5>(recv, send);        // banks 0, 2 read lane + 4
-      v[i] = keep + recv;
-    }
-  }
-  constexpr int K = N >= 16 ? N / 16 : 1;
-  constexpr int G = 64 * K / N;  // lanes per group, within one row
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    if constexpr (G >= 16) v[k] += dpp_mov<kDppRowShl + 8>(0.0f, v[k]);
-    if constexpr (G >= 8) v[k] += dpp_mov<kDppRowShl + 4>(0.0f, v[k]);
-    if constexpr (G >= 4) v[k] += dpp_mov<kDppRowShl + 2>(0.0f, v[k]);
-    if constexpr (G >= 2) v[k] += dpp_mov<kDppRowShl + 1>(0.0f, v[k]);
-  }
-}
-
-// ---------------------------------------------------------------------------
 // controls forward: eta = log16 tanh(x.u_r + b_r), delta = pi/2 tanh(x.u_p + b_p)
 // ---------------------------------------------------------------------------
 // A workgroup of NW waves takes kCtrlRows rows; each thread 8 consecutive

@@ -303,8 +303,8 @@ decode_kernel(int M, const void* x, const float* pdir, const float* rdir,
       const float gain = expf(wlg[m]) * ratio * gate;
       n_r[v] = ar * o_r[v] - ai * o_i[v] + gain * tanhf(xr[v]);
       n_i[v] = ai * o_r[v] + ar * o_i[v] + gain * tanhf(xi[v]);
-      yr[v] = fmaxf(n_r[v], 0.0f);
-      yi[v] = fmaxf(n_i[v], 0.0f);
+      yr[v] = relu_keep_nan(n_r[v]);
+      yi[v] = relu_keep_nan(n_i[v]);
     }
     *reinterpret_cast<float2*>(new_re + srow + m0) = make_float2(n_r[0], n_r[1]);
     *reinterpret_cast<float2*>(new_im + srow + m0) = make_float2(n_i[0], n_i[1]);
@@ -512,8 +512,8 @@ decode_update_kernel(int B, int M, const void* x, const float* pbias, const floa
       const float ni = fmaf(ai, hr[v], fmaf(ar, hi[v], gain * tanh_fast(xi[v])));
       hr[v] = nr;
       hi[v] = ni;
-      yr[v] = fmaxf(nr, 0.0f);
-      yi[v] = fmaxf(ni, 0.0f);
+      yr[v] = relu_keep_nan(nr);
+      yi[v] = relu_keep_nan(ni);
     }
     buffer_store_f32<SV, SPARC_STEP_STATE_CPOL>(make_rsrc(new_re + srow - m0 + mb, row_bytes), soff, hr);
     buffer_store_f32<SV, SPARC_STEP_STATE_CPOL>(make_rsrc(new_im + srow - m0 + mb, row_bytes), soff, hi);
@@ -614,7 +614,7 @@ scan_step_kernel(int64_t n_items, int M, int G, int gs, bool reset, const void* 
     if constexpr (RELU) {
       float rr[SV], ri[SV];
 #pragma unroll
-      for (int v = 0; v < SV; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
+      for (int v = 0; v < SV; ++v) { rr[v] = relu_keep_nan(hr[v]); ri[v] = relu_keep_nan(hi[v]); }
       const int64_t yrow = static_cast<int64_t>(b) * 2 * M + m;
       store_raw<IO, SV>(y_re, yrow, pack<IO, SV>(rr));
       store_raw<IO, SV>(y_re, yrow + M, pack<IO, SV>(ri));

@@ -236,6 +236,77 @@ def test_prepared_decode_matches_single_kernel_and_tracks_updates(dtype):
         assert rel_err(y1, y2) <= (1e-5 if dtype == torch.float32 else 2.0 ** -7)
 
 
+@pytest.mark.parametrize("B,modes,dtype", [
+    (19, 1028, torch.bfloat16),     # a ragged row group, a last mode block of 4 modes
+    (19, 1028, torch.float32),      # the fp32 row groups (8 rows)
+    (40, 4096, torch.bfloat16),     # several row groups and mode blocks
+    (3, 131076, torch.float32),     # a wide row: 129 blocks of 1024 modes
+], ids=["ragged_bf16", "ragged_f32", "groups_bf16", "wide_f32"])
+def test_prepared_decode_shapes(B, modes, dtype):
+    """The prepared step (control dots split over workgroups, then the
+    update) against the single-kernel decode and the float64 oracle, updating
+    the state in place: ragged row groups, a partial last block of modes."""
+    from sparc_amd.decode import latest_sparc_decode
+    print(f"[case] prepared decode B={B} M={modes} {dtype}", flush=True)
+    width = 2 * modes
+    m = make_module(width, seed=23).cuda()
+    m.prepare_inference()
+    g = torch.Generator().manual_seed(24)
+    x = torch.randn(B, width, generator=g).to(dtype).cuda()
+    s0 = ((0.1 * torch.randn(B, modes, generator=g)).cuda(), (0.1 * torch.randn(B, modes, generator=g)).cuda())
+    y2, s2 = _single_kernel_decode(m, x, s0)
+    state = (s0[0].clone(), s0[1].clone())
+    y1, s1 = latest_sparc_decode(m, x, state, out_state=state)
+    assert s1[0].data_ptr() == state[0].data_ptr()
+    assert rel_err(s1[0], s2[0]) <= 1e-5 and rel_err(s1[1], s2[1]) <= 1e-5
+    assert rel_err(y1, y2) <= (1e-5 if dtype == torch.float32 else 2.0 ** -7)
+    p = oracle_params(m, requires_grad=False)
+    yo, so = O.decode_step(p, x.double().cpu(), (s0[0].double().cpu(), s0[1].double().cpu()))
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert rel_err(y1, yo) <= tol and rel_err(s1[0], so[0]) <= tol and rel_err(s1[1], so[1]) <= tol
+
+
+def test_prepared_decode_graph_replays_match_eager():
+    """Prepared decode steps captured in a HIP graph and replayed several
+    times give the eager steps' results bit for bit, with eager work and
+    synchronisations between the replays (the serving-loop use)."""
+    from sparc_amd.decode import latest_sparc_decode
+    print("[case] prepared decode graph replays: B=64 M=4096 bf16, 5 steps", flush=True)
+    B, modes, n = 64, 4096, 5
+    m = make_module(2 * modes, seed=27).cuda()
+    m.prepare_inference()
+    g = torch.Generator().manual_seed(28)
+    xs = torch.randn(n, B, 2 * modes, generator=g).bfloat16().cuda()
+    s0 = ((0.1 * torch.randn(B, modes, generator=g)).cuda(), (0.1 * torch.randn(B, modes, generator=g)).cuda())
+    state = (s0[0].clone(), s0[1].clone())
+    ys_eager = []
+    for i in range(n):
+        y, _ = latest_sparc_decode(m, xs[i], state, out_state=state)
+        ys_eager.append(y.clone())
+    eager_state = (state[0].clone(), state[1].clone())
+    state[0].copy_(s0[0]); state[1].copy_(s0[1])
+    ys = []
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(n):
+                y, _ = latest_sparc_decode(m, xs[i], state, out_state=state)
+                ys.append(y)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        state[0].copy_(s0[0]); state[1].copy_(s0[1])
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i in range(n):
+            assert torch.equal(ys[i], ys_eager[i]), f"replay {rep}, step {i}"
+        assert torch.equal(state[0], eager_state[0]) and torch.equal(state[1], eager_state[1])
+        _ = (xs[0].float() * 2).sum().item()   # eager work between replays
+
+
 @pytest.mark.parametrize("B,L,width,dtype,tol", [
     (16, 21, 16384, torch.bfloat16, 2e-2),   # two modes per lane in the forward (>= 1024 chains)
     (3, 45, 200, torch.float32, 1e-4),       # a partial mode block (M = 100), ragged L
