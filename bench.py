@@ -348,9 +348,55 @@ def bench_module(args, dev):
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_step": algo_bytes,
             "traffic": measured, "traffic_source": COUNTERS_FILE if measured else None,
             "valu_busy_pct": {k: valu[k] for k in kernels if k in valu} or None}
-    return {"workload": "SPARCMixer forward + backward (the drop-in module), bf16 x, fp32 parameters",
-            "B": B, "T": T, "width": W, "path": path, "steps": steps, "ms_per_step": round(ms, 3),
-            "tokens_per_s": round(B * T / (ms * 1e-3), 1), "roofline": roof}
+    out = {"workload": "SPARCMixer forward + backward (the drop-in module), bf16 x, fp32 parameters",
+           "B": B, "T": T, "width": W, "path": path, "steps": steps, "ms_per_step": round(ms, 3),
+           "tokens_per_s": round(B * T / (ms * 1e-3), 1), "roofline": roof}
+    out["few_chains"] = bench_module_few_chains(dev)
+    return out
+
+
+def bench_module_few_chains(dev):
+    """The module on few long chains: B=1, T=65536, width 2048 (16 chains of
+    64 modes).  The fused kernels split the sequence into time segments
+    (summary pass, carry across segments, replay).  Algorithmic bytes of the
+    drop-in form as for the headline module report."""
+    import sparc_amd
+    B, T, W = 1, 65536, 2048
+    torch.manual_seed(0)
+    m = sparc_amd.SPARCMixer(W).to(dev)
+    with torch.no_grad():
+        m.phase_direction.normal_(0, 1 / math.sqrt(W))
+        m.radial_direction.normal_(0, 1 / math.sqrt(W))
+        m.write_phase_response.normal_()
+        m.write_radial_response.normal_()
+    x = torch.randn(B, T, W, device=dev, dtype=torch.bfloat16).requires_grad_()
+    dy = torch.randn(B, T, W, device=dev, dtype=torch.bfloat16)
+
+    def step():
+        x.grad = None
+        for p in m.parameters():
+            p.grad = None
+        y, _ = m(x)
+        y.backward(dy)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize(dev)
+    steps = 10
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / steps
+    M = W // 2
+    algo_bytes = B * T * (M * 10 * 2 + 6 * 4)
+    gbs = algo_bytes / (ms * 1e-3) / 1e9
+    del m, x, dy
+    return {"workload": "SPARCMixer forward + backward, few long chains (time segments)", "B": B, "T": T,
+            "width": W, "steps": steps, "ms_per_step": round(ms, 3), "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+            "bytes_per_step": algo_bytes, "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def _graph_time_us(dev, n_graph, reps, step_fn):

@@ -75,8 +75,30 @@ struct Args {
   const float* dlast_im;
   void* dx;
   float* part_tok;   // [2][n_mb][B*T]: d eta, d delta partials per mode block
-  float* part_mode;  // [5][B][M]: nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response
+  float* part_mode;  // [5][B*n_seg][M]: nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response
+  // time segments: the chains of segment s cover steps [s*t_seg, min(T, (s+1)*t_seg));
+  // a launch runs segments seg_lo, seg_lo+1, ... (grid = B * n_mb * segments)
+  int n_seg, t_seg, seg_lo;
+  float* seg_sum;    // [B][n_seg][M][4]: each segment's map (P, Q): h_out = P h_in + Q (complex)
+  float* seg_state;  // [B][n_seg][M][2]: the state (forward) or adjoint (backward) entering each segment
 };
+
+// Chain index of this workgroup -> (batch row, mode block, segment, steps).
+struct ChainPos {
+  int b, mb, seg, t_begin, t_end;
+};
+__device__ __forceinline__ ChainPos chain_pos(const Args& a) {
+  const int idx = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int n_chains = a.B * a.n_mb;
+  const int sj = idx / n_chains, chain = idx - sj * n_chains;
+  ChainPos c;
+  c.b = chain / a.n_mb;
+  c.mb = chain - c.b * a.n_mb;
+  c.seg = a.seg_lo + sj;
+  c.t_begin = c.seg * a.t_seg;
+  c.t_end = min(a.T, c.t_begin + a.t_seg);
+  return c;
+}
 
 // Per-mode constants, folded so that the per-step arithmetic is short:
 //   c0 = (nu, cos theta, sin theta, g2 = 4 gamma^2 / expm1(-2 nu))
@@ -223,21 +245,40 @@ __device__ __forceinline__ StepMode p1_step(float nu, float ct, float st, float 
 // row T-1; lanes past M read their block's first element) and the next
 // block is always prefetched (the last block re-reads itself), so that the
 // wait before a block never covers the prefetch of the next one.
-template <typename IO, int V>
+template <typename IO, int V, bool SUMMARY>
 __global__ void __launch_bounds__(64, 1)
 mixer_fwd_kernel(Args a) {
   using RawT = typename Raw<IO, V>::T;
   constexpr int ESZ = sizeof(IO);
   constexpr int MB = 64 * V;
   const int lane = threadIdx.x;
-  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
-  const int b = chain / a.n_mb;
-  const int mb = chain - b * a.n_mb;
+  const ChainPos cp = chain_pos(a);
+  const int b = cp.b, mb = cp.mb, t_begin = cp.t_begin, t_end = cp.t_end;
   const int m0 = mb * MB + lane * V;
   const bool lane_ok = m0 < a.M;
-  const int n_blocks = (a.T + kS - 1) / kS;
+  const int n_blocks = (t_end - t_begin + kS - 1) / kS;
   ModeConsts<V, false> mc;
   mc.load(a.consts, m0, lane_ok);
+  // the state entering this segment: a buffer load over an empty range (which
+  // reads zeros) for the first segment and for summaries.  Not a global load
+  // under a branch: that made the compiler restructure the block loop (1.5x
+  // slower at B=8, T=4096, width 32768)
+  float hr[V], hi[V];
+  {
+    const bool from_seg = !SUMMARY && a.n_seg > 1;
+    const float* base = a.seg_state + (static_cast<int64_t>(b) * a.n_seg + cp.seg) * a.M * 2;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(from_seg ? base : a.consts, from_seg ? a.M * 8u : 0u);
+    float h0[2 * V];
+    buffer_load_f32<2 * V, CPOL_DEFAULT>(rs, static_cast<uint32_t>(lane_ok ? m0 * 8 : 0), h0);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      hr[v] = h0[2 * v];
+      hi[v] = h0[2 * v + 1];
+    }
+  }
+  float Pr[V], Pi[V];  // SUMMARY: the product of the segment's transitions
+#pragma unroll
+  for (int v = 0; v < V; ++v) { Pr[v] = 1.0f; Pi[v] = 0.0f; }
   const int64_t row0 = static_cast<int64_t>(b) * a.T;
   const int64_t mbase = static_cast<int64_t>(mb) * MB;
   const int64_t W = 2 * static_cast<int64_t>(a.M);
@@ -255,8 +296,8 @@ mixer_fwd_kernel(Args a) {
   float ev[2], dv[2];  // lane s < kS: eta, delta of step s of the block
   auto load_block = [&](auto h_tag, int k) {
     constexpr int h = decltype(h_tag)::value;
-    const int t0 = k * kS;
-    const int last = a.T - 1 - t0;
+    const int t0 = t_begin + k * kS;
+    const int last = t_end - 1 - t0;
     // the block's rows of x through one buffer resource: row offsets in
     // scalar registers, no per-lane address arithmetic
     const int64_t off = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
@@ -273,9 +314,6 @@ mixer_fwd_kernel(Args a) {
     dv[h] = a.delta[ti];
   };
 
-  float hr[V], hi[V];
-#pragma unroll
-  for (int v = 0; v < V; ++v) { hr[v] = 0.0f; hi[v] = 0.0f; }
   // One block of kS steps in two phases: (A) every step's transition and
   // write, independent of the state, as one straight-line region the
   // compiler can interleave; (B) the recurrence and the stores.  TAIL: the
@@ -309,14 +347,20 @@ mixer_fwd_kernel(Args a) {
     const __amdgpu_buffer_rsrc_t rhi = make_rsrc(static_cast<char*>(a.h_im) + hoff, blk_h);
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
-      if (TAIL && t0 + s >= a.T) break;  // wave-uniform
+      if (TAIL && t0 + s >= t_end) break;  // wave-uniform
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         const float nr = fmaf(ar[s][v], hr[v], fmaf(-ai[s][v], hi[v], wr[s][v]));
         const float ni = fmaf(ai[s][v], hr[v], fmaf(ar[s][v], hi[v], wi[s][v]));
         hr[v] = nr;
         hi[v] = ni;
+        if constexpr (SUMMARY) {
+          const float pr = fmaf(ar[s][v], Pr[v], -ai[s][v] * Pi[v]);
+          Pi[v] = fmaf(ai[s][v], Pr[v], ar[s][v] * Pi[v]);
+          Pr[v] = pr;
+        }
       }
+      if constexpr (SUMMARY) continue;
       float rr[V], ri[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
@@ -336,8 +380,8 @@ mixer_fwd_kernel(Args a) {
   auto step_block = [&](auto h_tag, int k) {
     constexpr int h = decltype(h_tag)::value;
     load_block(std::integral_constant<int, 1 - h>{}, k + 1 < n_blocks ? k + 1 : k);
-    const int t0 = k * kS;
-    if (t0 + kS <= a.T) run_block(h_tag, t0, std::false_type{});
+    const int t0 = t_begin + k * kS;
+    if (t0 + kS <= t_end) run_block(h_tag, t0, std::false_type{});
     else run_block(h_tag, t0, std::true_type{});
   };
   load_block(std::integral_constant<int, 0>{}, 0);
@@ -345,7 +389,14 @@ mixer_fwd_kernel(Args a) {
     step_block(std::integral_constant<int, 0>{}, k);
     if (k + 1 < n_blocks) step_block(std::integral_constant<int, 1>{}, k + 1);
   }
-  if (lane_ok && a.last_re) {
+  if constexpr (SUMMARY) {
+    if (lane_ok) {
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        *reinterpret_cast<float4*>(a.seg_sum + ((static_cast<int64_t>(b) * a.n_seg + cp.seg) * a.M + m0 + v) * 4) =
+            make_float4(Pr[v], Pi[v], hr[v], hi[v]);
+    }
+  } else if (lane_ok && a.last_re && cp.seg == a.n_seg - 1) {
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       a.last_re[static_cast<int64_t>(b) * a.M + m0 + v] = hr[v];
@@ -371,19 +422,18 @@ mixer_fwd_kernel(Args a) {
 //   d wlg += g, d wpr += g (1 - sig) delta 2/pi, d wrr += g (1 - sig) eta / log16
 // (the P1 chain rule of sparc-kernal/backward/scan.py:593-644 and the write
 // gradients of sparc-kernal/backward/control.py:10-89).
-template <typename IO, int V, int kS>
+template <typename IO, int V, int kS, bool SUMMARY>
 __global__ void __launch_bounds__(64, 2)
 mixer_bwd_kernel(Args a) {
   using RawT = typename Raw<IO, V>::T;
   constexpr int ESZ = sizeof(IO);
   constexpr int MB = 64 * V;
   const int lane = threadIdx.x;
-  const int chain = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
-  const int b = chain / a.n_mb;
-  const int mb = chain - b * a.n_mb;
+  const ChainPos cp = chain_pos(a);
+  const int b = cp.b, mb = cp.mb, t_begin = cp.t_begin, t_end = cp.t_end;
   const int m0 = mb * MB + lane * V;
   const bool lane_ok = m0 < a.M;
-  const int n_blocks = (a.T + kS - 1) / kS;
+  const int n_blocks = (t_end - t_begin + kS - 1) / kS;
   const int64_t R = static_cast<int64_t>(a.B) * a.T;
   const int64_t row0 = static_cast<int64_t>(b) * a.T;
   const int64_t mbase = static_cast<int64_t>(mb) * MB;
@@ -400,16 +450,30 @@ mixer_bwd_kernel(Args a) {
   float Xr[V], Xi[V];    // conj(a_{t+1}) lambda_{t+1}
   float hcr[V], hci[V];  // h at the last step of the next block to process
   float acc[5][V];       // nu_log, theta_log, wlg, wpr, wrr
+  float Pr[V], Pi[V];    // SUMMARY: the product of the segment's conj(a)
 #pragma unroll
   for (int v = 0; v < V; ++v) {
+    // the adjoint entering this segment from the right (summaries start at zero)
     const int64_t i0 = static_cast<int64_t>(b) * a.M + (lane_ok ? m0 + v : 0);
-    Xr[v] = a.dlast_re ? a.dlast_re[i0] : 0.0f;
-    Xi[v] = a.dlast_im ? a.dlast_im[i0] : 0.0f;
+    if (SUMMARY) {
+      Xr[v] = 0.0f;
+      Xi[v] = 0.0f;
+    } else if (a.n_seg > 1) {
+      const float2 x0 = *reinterpret_cast<const float2*>(
+          a.seg_state + ((static_cast<int64_t>(b) * a.n_seg + cp.seg) * a.M + (lane_ok ? m0 + v : 0)) * 2);
+      Xr[v] = x0.x;
+      Xi[v] = x0.y;
+    } else {
+      Xr[v] = a.dlast_re ? a.dlast_re[i0] : 0.0f;
+      Xi[v] = a.dlast_im ? a.dlast_im[i0] : 0.0f;
+    }
+    Pr[v] = 1.0f;
+    Pi[v] = 0.0f;
 #pragma unroll
     for (int p = 0; p < 5; ++p) acc[p][v] = 0.0f;
   }
-  {  // h_{T-1}: the relu mask of step T-1
-    const int64_t ho = wave_uniform(((row0 + a.T - 1) * a.M + mbase) * ESZ);
+  {  // h at the segment's last step: its relu mask
+    const int64_t ho = wave_uniform(((row0 + t_end - 1) * a.M + mbase) * ESZ);
     unpack<IO, V>(ldb<RawT>(a.h_re, ho, lane_ld), hcr);
     unpack<IO, V>(ldb<RawT>(a.h_im, ho, lane_ld), hci);
   }
@@ -421,8 +485,8 @@ mixer_bwd_kernel(Args a) {
   // for t = 0, zeroed in the step)
   auto load_block = [&](auto h_tag, int k) {
     constexpr int h = decltype(h_tag)::value;
-    const int t0 = k * kS;
-    const int last = a.T - 1 - t0;
+    const int t0 = t_begin + k * kS;
+    const int last = t_end - 1 - t0;
     // buffer resources over the block's rows (row offsets in scalar
     // registers); the previous states start at row t0-1 (row 0 when t0 = 0)
     const int hb = t0 > 0 ? t0 - 1 : 0;
@@ -438,8 +502,10 @@ mixer_bwd_kernel(Args a) {
       const uint32_t o = static_cast<uint32_t>(sc) * row_x;
       dr[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o);
       di[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o + half_x);
-      xr[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
-      xi[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
+      if constexpr (!SUMMARY) {  // summaries need no write path
+        xr[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
+        xi[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
+      }
       // row t-1 (t >= 1), else row 0, relative to hb
       const int rel = t0 > 0 ? sc : (sc > 0 ? sc - 1 : 0);
       const uint32_t q = static_cast<uint32_t>(rel) * half_x;
@@ -486,7 +552,7 @@ mixer_bwd_kernel(Args a) {
 #pragma unroll
     for (int s = kS - 1; s >= 0; --s) {
       const int t = t0 + s;
-      if (TAIL && t >= a.T) {
+      if (TAIL && t >= t_end) {
 #pragma unroll
         for (int v = 0; v < V; ++v) { lr[s][v] = 0.0f; li[s][v] = 0.0f; }
         continue;
@@ -494,7 +560,7 @@ mixer_bwd_kernel(Args a) {
       float gyr[V], gyi[V], mr[V], mi[V];
       unpack<IO, V>(dr[h][s], gyr);
       unpack<IO, V>(di[h][s], gyi);
-      const bool carry = s == kS - 1 || (TAIL && t == a.T - 1);  // wave-uniform
+      const bool carry = s == kS - 1 || (TAIL && t == t_end - 1);  // wave-uniform
       if (carry) {
 #pragma unroll
         for (int v = 0; v < V; ++v) { mr[v] = hcr[v]; mi[v] = hci[v]; }
@@ -508,7 +574,17 @@ mixer_bwd_kernel(Args a) {
         li[s][v] = (mi[v] > 0.0f ? gyi[v] : 0.0f) + Xi[v];
         Xr[v] = fmaf(qar[s][v], lr[s][v], qai[s][v] * li[s][v]);
         Xi[v] = fmaf(qar[s][v], li[s][v], -qai[s][v] * lr[s][v]);
+        if constexpr (SUMMARY) {  // P <- conj(a) P
+          const float pr = fmaf(qar[s][v], Pr[v], qai[s][v] * Pi[v]);
+          Pi[v] = fmaf(qar[s][v], Pi[v], -qai[s][v] * Pr[v]);
+          Pr[v] = pr;
+        }
       }
+    }
+    if constexpr (SUMMARY) {  // the adjoint alone: no gradients, no stores
+      unpack<IO, V>(pr[h][0], hcr);
+      unpack<IO, V>(pi[h][0], hci);
+      return;
     }
     // (C) gradients; e[2s], e[2s+1]: this lane's d eta, d delta of step s
     float dxr[kS][V], dxi[kS][V], e[2 * kS];
@@ -525,7 +601,7 @@ mixer_bwd_kernel(Args a) {
       unpack<IO, V>(xr[h][s], cxr);
       unpack<IO, V>(xi[h][s], cxi);
       float se = 0.0f, sd = 0.0f;
-      const bool live = !TAIL || t < a.T;  // steps past T contribute nothing (wave-uniform)
+      const bool live = !TAIL || t < t_end;  // steps past the segment contribute nothing (wave-uniform)
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         if (t == 0) { hpr[v] = 0.0f; hpi[v] = 0.0f; }
@@ -567,7 +643,7 @@ mixer_bwd_kernel(Args a) {
     const __amdgpu_buffer_rsrc_t rdx = make_rsrc(static_cast<char*>(a.dx) + xoff, blk_x);
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
-      if (TAIL && t0 + s >= a.T) break;
+      if (TAIL && t0 + s >= t_end) break;
       if (lane_ok) {
         const uint32_t o = static_cast<uint32_t>(s) * row_x;
         buf_store<RawT, CPOL_NT>(pack<IO, V>(dxr[s]), rdx, lane_bytes, o);
@@ -583,7 +659,7 @@ mixer_bwd_kernel(Args a) {
       for (int k = 0; k < K; ++k) {
         const int i = lane / G * K + k;
         const int t = t0 + (i >> 1);
-        if (t < a.T) a.part_tok[(static_cast<int64_t>(i & 1) * a.n_mb + mb) * R + row0 + t] = e[k];
+        if (t < t_end) a.part_tok[(static_cast<int64_t>(i & 1) * a.n_mb + mb) * R + row0 + t] = e[k];
       }
     }
     unpack<IO, V>(pr[h][0], hcr);
@@ -594,8 +670,8 @@ mixer_bwd_kernel(Args a) {
   auto step_block = [&](auto h_tag, int k) {
     constexpr int h = decltype(h_tag)::value;
     load_block(std::integral_constant<int, 1 - h>{}, k > 0 ? k - 1 : k);
-    const int t0 = k * kS;
-    if (t0 + kS <= a.T) run_block(h_tag, t0, std::false_type{});
+    const int t0 = t_begin + k * kS;
+    if (t0 + kS <= t_end) run_block(h_tag, t0, std::false_type{});
     else run_block(h_tag, t0, std::true_type{});
   };
   int k = n_blocks - 1;
@@ -610,12 +686,76 @@ mixer_bwd_kernel(Args a) {
     step_block(std::integral_constant<int, 0>{}, k);
     if (k >= 1) step_block(std::integral_constant<int, 1>{}, k - 1);
   }
-  if (lane_ok) {
+  if constexpr (SUMMARY) {
+    if (lane_ok) {
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        *reinterpret_cast<float4*>(a.seg_sum + ((static_cast<int64_t>(b) * a.n_seg + cp.seg) * a.M + m0 + v) * 4) =
+            make_float4(Pr[v], Pi[v], Xr[v], Xi[v]);
+    }
+  } else if (lane_ok) {
+    const int64_t rows = static_cast<int64_t>(a.B) * a.n_seg, row = static_cast<int64_t>(b) * a.n_seg + cp.seg;
 #pragma unroll
     for (int p = 0; p < 5; ++p)
 #pragma unroll
       for (int v = 0; v < V; ++v)
-        a.part_mode[(static_cast<int64_t>(p) * a.B + b) * a.M + m0 + v] = acc[p][v];
+        a.part_mode[(p * rows + row) * a.M + m0 + v] = acc[p][v];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// carries across time segments
+// ---------------------------------------------------------------------------
+// Each segment maps the state entering it to the state leaving it, h -> P h + Q
+// (forward: P the product of its transitions, Q its end state from zero;
+// backward: the same for the adjoint with conj(a), in reverse time).  The
+// state entering segment s is the composition of the maps of the segments
+// processed before it (forward 0 .. s-1 applied to zero; backward n-1 .. s+1
+// applied to dlast).  One wave per (batch row, mode): lane j takes the j-th
+// segment in processing order of each group of 64, a Hillis-Steele scan over
+// the lanes composes the maps, and each group's composition carries into the
+// next.  The last segment processed has no map (its summary is not needed).
+__global__ void __launch_bounds__(64)
+mixer_seg_carry_kernel(int B, int M, int n_seg, int reverse, const float* seg_sum, const float* init_re,
+                       const float* init_im, float* seg_state) {
+  const int i = blockIdx.x, lane = threadIdx.x;  // i = b * M + m
+  const int b = i / M, m = i - b * M;
+  float cr = init_re ? init_re[i] : 0.0f, ci = init_im ? init_im[i] : 0.0f;
+  for (int g0 = 0; g0 < n_seg; g0 += 64) {
+    const int j = g0 + lane;                      // position in processing order
+    const int sg = reverse ? n_seg - 1 - j : j;   // the segment
+    float pr = 1.0f, pi = 0.0f, qr = 0.0f, qi = 0.0f;  // identity past the end / for the last segment
+    if (j < n_seg - 1) {
+      const float4 e = *reinterpret_cast<const float4*>(seg_sum + ((static_cast<int64_t>(b) * n_seg + sg) * M + m) * 4);
+      pr = e.x; pi = e.y; qr = e.z; qi = e.w;
+    }
+    // inclusive scan: lane j holds map_j o ... o map_g0
+#pragma unroll
+    for (int d = 1; d < 64; d *= 2) {
+      const float ppr = __shfl_up(pr, d), ppi = __shfl_up(pi, d);
+      const float pqr = __shfl_up(qr, d), pqi = __shfl_up(qi, d);
+      if (lane >= d) {  // (P, Q) o (Pp, Qp) = (P Pp, P Qp + Q)
+        const float nqr = fmaf(pr, pqr, fmaf(-pi, pqi, qr));
+        const float nqi = fmaf(pr, pqi, fmaf(pi, pqr, qi));
+        const float npr = fmaf(pr, ppr, -pi * ppi);
+        const float npi = fmaf(pr, ppi, pi * ppr);
+        pr = npr; pi = npi; qr = nqr; qi = nqi;
+      }
+    }
+    // the state entering segment sg: the maps before it (exclusive) applied to the carry
+    const float epr = __shfl_up(pr, 1), epi = __shfl_up(pi, 1), eqr = __shfl_up(qr, 1), eqi = __shfl_up(qi, 1);
+    float hr = cr, hi = ci;
+    if (lane > 0) {
+      hr = fmaf(epr, cr, fmaf(-epi, ci, eqr));
+      hi = fmaf(epr, ci, fmaf(epi, cr, eqi));
+    }
+    if (j < n_seg)
+      *reinterpret_cast<float2*>(seg_state + ((static_cast<int64_t>(b) * n_seg + sg) * M + m) * 2) = make_float2(hr, hi);
+    // the carry into the next group: the whole group's composition
+    const float lpr = __shfl(pr, 63), lpi = __shfl(pi, 63), lqr = __shfl(qr, 63), lqi = __shfl(qi, 63);
+    const float ncr = fmaf(lpr, cr, fmaf(-lpi, ci, lqr));
+    ci = fmaf(lpr, ci, fmaf(lpi, cr, lqi));
+    cr = ncr;
   }
 }
 
@@ -765,29 +905,71 @@ int mixer_v(int64_t B, int64_t M, int direction) {
   return chains2 >= 1280 ? 2 : 1;
 }
 
+// Time segments.  One wave per chain (batch row x 64 V modes) walks its
+// whole sequence, so with fewer chains than SIMDs most of the GPU idles.
+// Then the sequence is split into n_seg segments of t_seg steps (a multiple
+// of 8, at least kMinSegSteps) so that about two waves per SIMD run: a
+// summary pass gives each segment's map (P, Q), a carry kernel composes them
+// into the state entering every segment, and the full pass replays each
+// segment from its entering state.  This costs a second pass over the
+// transitions (and, forward, the writes), paid for by the occupancy.
+#ifndef SPARC_MIXER_SEG_CHAINS
+#define SPARC_MIXER_SEG_CHAINS 1024
+#endif
+constexpr int64_t kSegChains = SPARC_MIXER_SEG_CHAINS;  // segment below this many chains
+#ifndef SPARC_MIXER_SEG_TARGET
+#define SPARC_MIXER_SEG_TARGET 4096
+#endif
+#ifndef SPARC_MIXER_SEG_MIN
+#define SPARC_MIXER_SEG_MIN 128
+#endif
+constexpr int64_t kSegTarget = SPARC_MIXER_SEG_TARGET;  // waves to aim for
+constexpr int64_t kMinSegSteps = SPARC_MIXER_SEG_MIN;
+void choose_segments(int64_t B, int64_t T, int n_mb, int& n_seg, int& t_seg) {
+  n_seg = 1;
+  t_seg = static_cast<int>(T > 0 ? T : 1);
+  const int64_t chains = B * n_mb;
+  if (chains >= kSegChains || T < 2 * kMinSegSteps) return;
+  int64_t n = std::min((kSegTarget + chains - 1) / chains, T / kMinSegSteps);
+  if (n < 2) return;
+  int64_t len = (T + n - 1) / n;
+  len = (len + 7) / 8 * 8;
+  n = (T + len - 1) / len;
+  if (n < 2) return;
+  n_seg = static_cast<int>(n);
+  t_seg = static_cast<int>(len);
+}
+
 struct Layout {
-  int V = 1, n_mb = 0, n_rb = 0;
+  int V = 1, n_mb = 0, n_rb = 0, n_seg = 1, t_seg = 1;
   int64_t R = 0;
-  size_t consts = 0, part_tok = 0, tok = 0, part_mode = 0, pd = 0, pbias = 0, total = 0;
+  size_t consts = 0, part_tok = 0, tok = 0, part_mode = 0, pd = 0, pbias = 0, seg_sum = 0, seg_state = 0, total = 0;
 };
 
 Layout layout(int64_t B, int64_t T, int64_t M, int direction) {
   Layout l;
   l.V = mixer_v(B, M, direction);
   l.n_mb = static_cast<int>((M + 64 * l.V - 1) / (64 * l.V));
+  choose_segments(B, T, l.n_mb, l.n_seg, l.t_seg);
   l.R = B * T;
   l.n_rb = static_cast<int>(std::min<int64_t>((l.R + kCtrlBwdRows - 1) / kCtrlBwdRows, kMaxRowBlocks));
   auto up = [](size_t n) { return (n + 255) / 256 * 256; };
   size_t off = 256;
   l.consts = off;
   off += up(static_cast<size_t>(M) * kConsts * 4);
+  if (l.n_seg > 1) {
+    l.seg_sum = off;
+    off += up(static_cast<size_t>(B) * l.n_seg * M * 4 * 4);
+    l.seg_state = off;
+    off += up(static_cast<size_t>(B) * l.n_seg * M * 2 * 4);
+  }
   if (direction == 1) {
     l.part_tok = off;
     off += up(static_cast<size_t>(2) * l.n_mb * l.R * 4);
     l.tok = off;
     off += up(static_cast<size_t>(2) * l.R * 4);
     l.part_mode = off;
-    off += up(static_cast<size_t>(5) * B * M * 4);
+    off += up(static_cast<size_t>(5) * B * l.n_seg * M * 4);
     l.pd = off;
     off += up(static_cast<size_t>(2) * l.n_rb * 2 * M * 4);
     l.pbias = off;
@@ -807,16 +989,39 @@ sparc_status check_shape(int64_t B, int64_t T, int64_t M, int32_t io) {
   return SPARC_OK;
 }
 
+// the forward over n_segs segments from a.seg_lo (SUMMARY: the maps only)
+template <typename IO, int V, bool SUMMARY>
+void launch_fwd(const Args& a, int n_segs, hipStream_t st) {
+  const dim3 g(static_cast<unsigned>(a.B) * a.n_mb * static_cast<unsigned>(n_segs));
+  hipLaunchKernelGGL((mixer_fwd_kernel<IO, V, SUMMARY>), g, dim3(64), 0, st, a);
+}
 template <typename IO, int V>
-void launch_fwd(const Args& a, hipStream_t st) {
-  hipLaunchKernelGGL((mixer_fwd_kernel<IO, V>), dim3(static_cast<unsigned>(a.B) * a.n_mb), dim3(64), 0, st, a);
+void run_fwd(const Args& a, hipStream_t st) {
+  if (a.n_seg > 1) {  // maps of segments 0 .. n-2, then the entering states
+    launch_fwd<IO, V, true>(a, a.n_seg - 1, st);
+    hipLaunchKernelGGL(mixer_seg_carry_kernel, dim3(static_cast<unsigned>(a.B) * a.M), dim3(64), 0, st, a.B, a.M,
+                       a.n_seg, 0, a.seg_sum, nullptr, nullptr, a.seg_state);
+  }
+  launch_fwd<IO, V, false>(a, a.n_seg, st);
 }
 #ifndef SPARC_MIXER_BWD_S
 #define SPARC_MIXER_BWD_S 4
 #endif
+template <typename IO, int V, bool SUMMARY>
+void launch_bwd(const Args& a, int n_segs, hipStream_t st) {
+  const dim3 g(static_cast<unsigned>(a.B) * a.n_mb * static_cast<unsigned>(n_segs));
+  hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, SPARC_MIXER_BWD_S, SUMMARY>), g, dim3(64), 0, st, a);
+}
 template <typename IO, int V>
-void launch_bwd(const Args& a, hipStream_t st) {
-  hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, SPARC_MIXER_BWD_S>), dim3(static_cast<unsigned>(a.B) * a.n_mb), dim3(64), 0, st, a);
+void run_bwd(const Args& a, hipStream_t st) {
+  if (a.n_seg > 1) {  // maps of segments n-1 .. 1 (reverse time), then the entering adjoints
+    Args s = a;
+    s.seg_lo = 1;
+    launch_bwd<IO, V, true>(s, a.n_seg - 1, st);
+    hipLaunchKernelGGL(mixer_seg_carry_kernel, dim3(static_cast<unsigned>(a.B) * a.M), dim3(64), 0, st, a.B, a.M,
+                       a.n_seg, 1, a.seg_sum, a.dlast_re, a.dlast_im, a.seg_state);
+  }
+  launch_bwd<IO, V, false>(a, a.n_seg, st);
 }
 
 // The scan and its backward with the controls given; the per-mode constants
@@ -846,10 +1051,13 @@ sparc_status scan_forward_impl(const Layout& l, int64_t batch, int64_t length, i
     a.n_mb = l.n_mb;
     a.x = x; a.consts = consts; a.eta = eta; a.delta = delta;
     a.y = y; a.h_re = h_re; a.h_im = h_im; a.last_re = last_re; a.last_im = last_im;
+    a.n_seg = l.n_seg; a.t_seg = l.t_seg; a.seg_lo = 0;
+    a.seg_sum = reinterpret_cast<float*>(ws + l.seg_sum);
+    a.seg_state = reinterpret_cast<float*>(ws + l.seg_state);
     if (io_dtype == SPARC_BF16) {
-      if (l.V == 2) launch_fwd<sparc::bf16, 2>(a, st); else launch_fwd<sparc::bf16, 1>(a, st);
+      if (l.V == 2) run_fwd<sparc::bf16, 2>(a, st); else run_fwd<sparc::bf16, 1>(a, st);
     } else {
-      if (l.V == 2) launch_fwd<float, 2>(a, st); else launch_fwd<float, 1>(a, st);
+      if (l.V == 2) run_fwd<float, 2>(a, st); else run_fwd<float, 1>(a, st);
     }
   }
   hipError_t e = hipGetLastError();
@@ -887,17 +1095,21 @@ sparc_status scan_backward_impl(const Layout& l, int64_t batch, int64_t length, 
   a.h_re = const_cast<void*>(h_re); a.h_im = const_cast<void*>(h_im);
   a.dy = dy; a.dlast_re = dlast_re; a.dlast_im = dlast_im; a.dx = dx;
   a.part_tok = part_tok; a.part_mode = part_mode;
+  a.n_seg = l.n_seg; a.t_seg = l.t_seg; a.seg_lo = 0;
+  a.seg_sum = reinterpret_cast<float*>(ws + l.seg_sum);
+  a.seg_state = reinterpret_cast<float*>(ws + l.seg_state);
   if (io_dtype == SPARC_BF16) {
-    if (l.V == 2) launch_bwd<sparc::bf16, 2>(a, st); else launch_bwd<sparc::bf16, 1>(a, st);
+    if (l.V == 2) run_bwd<sparc::bf16, 2>(a, st); else run_bwd<sparc::bf16, 1>(a, st);
   } else {
-    if (l.V == 2) launch_bwd<float, 2>(a, st); else launch_bwd<float, 1>(a, st);
+    if (l.V == 2) run_bwd<float, 2>(a, st); else run_bwd<float, 1>(a, st);
   }
   // d eta, d delta per token: the sums over the mode blocks of part_tok [2][n_mb][R]
   if (sparc_status s = sparc_column_sum(l.n_mb, l.R, part_tok, deta, 0, stream)) return s;
   if (sparc_status s = sparc_column_sum(l.n_mb, l.R, part_tok + static_cast<int64_t>(l.n_mb) * l.R, ddelta, 0, stream))
     return s;
+  const int64_t prow = batch * l.n_seg;  // one partial row per (batch row, segment)
   for (int p = 0; p < 5; ++p)
-    if (sparc_status s = sparc_column_sum(batch, modes, part_mode + static_cast<int64_t>(p) * batch * modes, outs[p], 0, stream))
+    if (sparc_status s = sparc_column_sum(prow, modes, part_mode + static_cast<int64_t>(p) * prow * modes, outs[p], 0, stream))
       return s;
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer scan backward: %s", hipGetErrorString(e));

@@ -22,9 +22,7 @@ _path = "auto"
 def set_mixer_path(name: str) -> None:
     """Sequence path of ``SPARCMixer.forward``: "fused" (sparc_mixer_*),
     "composed" (controls, write, chunked scan as separate operators) or
-    "auto" (fused from 320 chains of 64 modes, or for sequences of at most
-    512 steps; below that the composed path, whose look-back scan
-    parallelises over time)."""
+    "auto" (the fused path whenever it supports the input)."""
     global _path
     if name not in _PATHS:
         raise ValueError(f"unknown mixer path {name!r}")
@@ -54,14 +52,18 @@ def use_fused(x: torch.Tensor, modes: int) -> bool:
 
 
 def fused_preferred(batch: int, length: int, modes: int) -> bool:
-    """The "auto" rule.  One wave per chain (batch row x 64 modes) walks all
-    of T in the fused kernels, so few chains leave most of the GPU idle; the
-    composed path's look-back scan is parallel over T but makes more passes
-    and launches.  Measured (MI355X, bf16, forward + backward): fused wins
-    from about 320 chains at any T, and below that only for T <= 512
-    (launch-bound)."""
-    chains = batch * ((modes + 63) // 64)
-    return chains >= 320 or length <= 512
+    """The "auto" rule: the fused path at every shape.  Its kernels run one
+    wave per chain (batch row x 64 modes); with fewer chains than SIMDs they
+    split the sequence into segments (a summary pass, a carry across
+    segments, then the replay), so they parallelise over time as the composed
+    path's look-back scan does, with fewer passes.  Measured on MI355X (bf16,
+    forward + backward, fused against composed): B=1 T=65536 width 2048
+    1.12 against 1.96 ms; B=1 T=4096 width 4096 0.30 against 0.60 ms; B=4
+    T=2048 width 8192 0.63 against 0.99 ms; B=8 T=4096 width 8192 1.94
+    against 3.50 ms; widths down to 8 and sequences down to 300 steps about
+    0.25 against 0.42 ms."""
+    del batch, length, modes
+    return True
 
 
 _PARAMS = ("phase_direction", "radial_direction", "nu_log", "theta_log", "write_log_gain",

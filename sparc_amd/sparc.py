@@ -6,9 +6,10 @@ keep the reference's signatures, defaults and ``ValueError``s.  The sequence
 forward is ``run_sequence`` below (reference: sparc-kernal/forward/scan.py:
 1398-1603): by default the fused HIP path (controls, write, P1 scan and
 ``relu(cat(h_re, h_im))`` epilogue in two C-ABI calls forward and backward,
-``sparc_amd.mixer``); for few chains over long sequences the composed path
-(torch controls, HIP write prologue, HIP chunked P1 scan with the epilogue
-fused into its store).
+``sparc_amd.mixer``; few chains over long sequences split time into
+segments there).  ``set_mixer_path("composed")`` selects the composed path
+instead (controls, HIP write prologue and HIP chunked P1 scan with the
+epilogue fused into its store, as separate operators).
 """
 from __future__ import annotations
 

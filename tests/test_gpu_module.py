@@ -97,6 +97,45 @@ def test_mixer_forward_backward_parity(dtype, tol, B, L, width, mixer_path):
         assert e <= tol, f"grad {name}: {e:.3g}"
 
 
+@pytest.mark.parametrize("B,L,width,dtype,tol", [
+    (1, 3001, 128, torch.float32, 1e-4),    # 2 chains: 23 segments of 136 steps, a ragged last one
+    (3, 1024, 512, torch.bfloat16, 2e-2),   # 12 chains: 8 segments of 128
+    (2, 777, 64, torch.float32, 1e-4),      # 2 chains: 6 segments of 136, the last of 97 steps
+])
+def test_fused_time_segments(B, L, width, dtype, tol):
+    """Few chains over long sequences: the fused kernels split time into
+    segments (a summary pass, a carry across segments, then the replay),
+    forward and backward; outputs, last state and every gradient against the
+    float64 oracle, with a gradient through the last state."""
+    print(f"[case] fused segments B={B} L={L} width={width} {dtype}", flush=True)
+    sparc_amd.set_mixer_path("fused")
+    try:
+        m = make_module(width, seed=9).cuda()
+        g = torch.Generator().manual_seed(4)
+        x_in = torch.randn(B, L, width, generator=g, dtype=torch.float64).to(dtype)
+        p = oracle_params(m)
+        dy = _masked_dy(p, x_in.double(), torch.randn(B, L, width, generator=g, dtype=torch.float64),
+                        band=1e-3 if dtype == torch.float32 else 2e-2)
+        dl = (torch.randn(B, width // 2, generator=g, dtype=torch.float64),
+              torch.randn(B, width // 2, generator=g, dtype=torch.float64))
+        x = x_in.cuda().requires_grad_()
+        y, cache = m(x, return_cache=True)
+        loss = (y.float() * dy.cuda().float()).sum() + (cache[0] * dl[0].cuda().float()).sum() \
+            + (cache[1] * dl[1].cuda().float()).sum()
+        grads = torch.autograd.grad(loss, [x] + [getattr(m, n) for n in NAMES])
+    finally:
+        sparc_amd.set_mixer_path("auto")
+    xo = x_in.double().clone().requires_grad_()
+    yo, lasto = O.mixer_forward(p, xo, return_cache=True)
+    lo = (yo * dy).sum() + (lasto[0] * dl[0]).sum() + (lasto[1] * dl[1]).sum()
+    grads_o = torch.autograd.grad(lo, [xo] + [getattr(p, n) for n in NAMES])
+    assert rel_err(y, yo) <= tol
+    assert rel_err(cache[0], lasto[0]) <= tol and rel_err(cache[1], lasto[1]) <= tol
+    for name, a, b in zip(["x"] + NAMES, grads, grads_o):
+        e = rel_err(a, b)
+        assert e <= tol, f"grad {name}: {e:.3g}"
+
+
 def test_mixer_matches_reference_golden(mixer_path):
     """The HIP module on the reference's own golden inputs (fp32 I/O)."""
     print(f"[case] golden path={mixer_path}", flush=True)
