@@ -27,6 +27,12 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ uint16_t pack_bf16(float v) {
   return (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffffu);
 }
+// Both values rounded to bf16 (nearest even) and widened back to fp32.
+__device__ __forceinline__ void round_bf16x2(float& a, float& b) {
+  const uint32_t u = pack_bf16x2(a, b);
+  a = __uint_as_float(u << 16);
+  b = __uint_as_float(u & 0xffff0000u);
+}
 
 // transitions (values of sparc_transition)
 enum Transition : int { TR_P1 = 0, TR_POLAR = 1, TR_CART = 2, TR_REAL = 3 };

@@ -57,6 +57,15 @@ constexpr int kS = SPARC_MIXER_FWD_S;  // steps per prefetched block of the forw
 constexpr int kCtrlRows = 16;  // rows per workgroup of the controls forward
 constexpr int kCtrlBwdRows = 128;  // rows per workgroup of the controls backward
 constexpr int kMaxRowBlocks = 65535;  // grid.y limit: more row blocks loop in the workgroups
+// bf16 x: the write is rounded to bf16 before the scan, as the reference
+// stores it in x's dtype (write_r.to(x.dtype), sparc-kernal/forward/
+// control.py:162-163), and its gradient reaches the write's backward rounded
+// to bf16 (the scan returns grad_br in the writes' dtype); the transition
+// gradients keep the fp32 adjoint, as inside the reference's scan kernel.
+#ifndef SPARC_MIXER_ROUND_WRITE
+#define SPARC_MIXER_ROUND_WRITE 1
+#endif
+template <typename IO> constexpr bool kRoundWrite = SPARC_MIXER_ROUND_WRITE && sizeof(IO) == 2;
 
 struct Args {
   int B, T, M, n_mb;
@@ -338,6 +347,7 @@ mixer_fwd_kernel(Args a) {
         ai[s][v] = q.ai;
         wr[s][v] = q.gain * tanh_fast(cr[v]);
         wi[s][v] = q.gain * tanh_fast(ci[v]);
+        if constexpr (kRoundWrite<IO>) round_bf16x2(wr[s][v], wi[s][v]);
       }
     }
     const int64_t yoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
@@ -615,9 +625,11 @@ mixer_bwd_kernel(Args a) {
         const float Y = mc.g2[v] * e2, r = __builtin_amdgcn_rsqf(fmaxf(Y, 1e-30f));
         const float gain = Y * r * sg;
         const float tr = tanh_fast(cxr[v]), ti = tanh_fast(cxi[v]);
-        dxr[s][v] = l_r * gain * fmaf(-tr, tr, 1.0f);
-        dxi[s][v] = l_i * gain * fmaf(-ti, ti, 1.0f);
-        const float g = fmaf(l_r, tr, l_i * ti) * gain;
+        float w_r = l_r, w_i = l_i;  // the write's gradient
+        if constexpr (kRoundWrite<IO>) round_bf16x2(w_r, w_i);
+        dxr[s][v] = w_r * gain * fmaf(-tr, tr, 1.0f);
+        dxi[s][v] = w_i * gain * fmaf(-ti, ti, 1.0f);
+        const float g = fmaf(w_r, tr, w_i * ti) * gain;
         const float gar = fmaf(l_r, hpr[v], l_i * hpi[v]);
         const float gai = fmaf(l_i, hpr[v], -l_r * hpi[v]);
         const float dphi = fmaf(-gar, ai, gai * ar);

@@ -501,14 +501,16 @@ def test_composed_bf16_matches_reference_rounding(B, L, width, seed):
 
 
 @pytest.mark.parametrize("B,L,width,seed", [s for s in BF16_SHAPES if (s[2] // 2) % 4 == 0])
-def test_fused_bf16_tracks_exact_arithmetic(B, L, width, seed):
-    """The fused path keeps the write in fp32 inside its scan, so with bf16
-    x and y it stays within 1e-2 of exact arithmetic on every output and
-    gradient, including the shapes where the reference's bf16 write does not."""
-    print(f"[case] fused bf16 vs exact B={B} L={L} width={width}", flush=True)
+def test_fused_bf16_matches_reference_rounding(B, L, width, seed):
+    """The fused path rounds where the reference rounds too: the write to
+    bf16 before the scan and the write's gradient to bf16 before the write's
+    backward.  Against the oracle with that rounding, every output and
+    gradient is within 1e-2, also on the shapes where the rounding moves a
+    gradient by more than 2e-2 from exact arithmetic."""
+    print(f"[case] fused bf16 vs reference rounding B={B} L={L} width={width}", flush=True)
     sparc_amd.set_mixer_path("fused")
     try:
-        errs = _bf16_module_errors(B, L, width, seed, None)
+        errs = _bf16_module_errors(B, L, width, seed, torch.bfloat16)
     finally:
         sparc_amd.set_mixer_path("auto")
     bad = {k: f"{v:.3g}" for k, v in errs.items() if v > 1e-2}
