@@ -39,6 +39,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "p1_fused.h"
 #include "sparc_hip.h"
 
 namespace sparc {
@@ -67,6 +68,17 @@ constexpr int kMaxRowBlocks = 65535;  // grid.y limit: more row blocks loop in t
 #endif
 template <typename IO> constexpr bool kRoundWrite = SPARC_MIXER_ROUND_WRITE && sizeof(IO) == 2;
 
+// What a chain of the scan kernels reads and writes.
+//   kModule: x in (the write is gain * tanh x); y = relu(cat(h_re, h_im))
+//            and the saved states h_re, h_im out; backward dx out.
+//   kPlanes: the writes w_re, w_im in; the states y_re, y_im (through h_re,
+//            h_im) and the chunk states out; backward dw out (the P1 scan of
+//            sparc_scan_forward / _backward with one gate pair per token).
+//   kRelu:   as kPlanes, but y = relu(cat(h_re, h_im)) out instead of the
+//            states (forward only).
+enum : int { kModule = 0, kPlanes = 1, kRelu = 2 };
+constexpr int kStateChunk = 64;  // steps per saved chunk state (sparc_scan_chunk_length)
+
 struct Args {
   int B, T, M, n_mb;
   const void* x;
@@ -90,6 +102,19 @@ struct Args {
   int n_seg, t_seg, seg_lo;
   float* seg_sum;    // [B][n_seg][M][4]: each segment's map (P, Q): h_out = P h_in + Q (complex)
   float* seg_state;  // [B][n_seg][M][2]: the state (forward) or adjoint (backward) entering each segment
+  // kPlanes / kRelu: the writes (forward) or their gradients (backward,
+  // through dy = dy_re and dx = dw_re), [B,T,M] each; the initial state and
+  // its gradient [B,M] fp32 (NULL: zero / not wanted); the chunk states
+  // [B][ceil(T/64)][M][2] fp32
+  const void* w_re;
+  const void* w_im;
+  const void* dy_im;
+  void* dw_im;
+  const float* h0_re;
+  const float* h0_im;
+  float* dh0_re;
+  float* dh0_im;
+  float* chunk_state;
 };
 
 // Chain index of this workgroup -> (batch row, mode block, segment, steps).
@@ -117,6 +142,8 @@ __device__ __forceinline__ ChainPos chain_pos(const Args& a) {
 //        pl = -wpr log2(e) 2/pi, rl = -wrr log2(e) / log16;
 //        kappa = nu e^{-2 nu} / (1 - e^{-2 nu})
 //   c2 = (wrr / log16, wpr 2/pi, 0, 0)
+// With no write parameters (wlg NULL: the P1 scan with the writes given) the
+// write constants are those of gamma = 1, wpr = wrr = 0, which nothing reads.
 __global__ void __launch_bounds__(256)
 mixer_prepare_kernel(int M, const float* nu_log, const float* theta_log, const float* wlg,
                      const float* wpr, const float* wrr, float* consts) {
@@ -125,12 +152,13 @@ mixer_prepare_kernel(int M, const float* nu_log, const float* theta_log, const f
   const float nu = expf(nu_log[m]);
   float sn, cs;
   const float theta = theta_rotation(theta_log[m], cs, sn);
-  const float gam = expf(wlg[m]);
+  const bool wp = wlg != nullptr;
+  const float gam = wp ? expf(wlg[m]) : 1.0f, pr = wp ? wpr[m] : 0.0f, rr = wp ? wrr[m] : 0.0f;
   const float cinv = 1.0f / expm1f(-2.0f * nu);
   float4* c = reinterpret_cast<float4*>(consts + static_cast<int64_t>(m) * kConsts);
   c[0] = make_float4(nu, cs, sn, 4.0f * gam * gam * cinv);
-  c[1] = make_float4(-wpr[m] * kLog2e * kTwoOverPi, -wrr[m] * kLog2e * kInvLog16, theta, -nu * (1.0f + cinv));
-  c[2] = make_float4(wrr[m] * kInvLog16, wpr[m] * kTwoOverPi, 0.0f, 0.0f);
+  c[1] = make_float4(-pr * kLog2e * kTwoOverPi, -rr * kLog2e * kInvLog16, theta, -nu * (1.0f + cinv));
+  c[2] = make_float4(rr * kInvLog16, pr * kTwoOverPi, 0.0f, 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -228,6 +256,18 @@ struct ModeConsts {
   }
 };
 
+// The P1 transition of one mode and step: a = rho e^{i (theta + (1 - rho) delta)},
+// rho = exp(-nu E), E = e^eta, with rho - 1 formed by expm1.
+__device__ __forceinline__ void p1_transition(float nu, float ct, float st, float E, float delta, float& ar,
+                                              float& ai) {
+  const float em = expm1_nonpos(-nu * E);
+  const float rho = 1.0f + em;
+  float su, cu;
+  sincos_half(-em * delta, su, cu);  // phase (1 - rho) delta, |.| <= pi/2
+  ar = rho * fmaf(ct, cu, -st * su);
+  ai = rho * fmaf(st, cu, ct * su);
+}
+
 // Per-step values of the P1 transition and write of one mode.
 struct StepMode {
   float em, rho, ar, ai, gain, sg;
@@ -254,12 +294,14 @@ __device__ __forceinline__ StepMode p1_step(float nu, float ct, float st, float 
 // row T-1; lanes past M read their block's first element) and the next
 // block is always prefetched (the last block re-reads itself), so that the
 // wait before a block never covers the prefetch of the next one.
-template <typename IO, int V, bool SUMMARY>
+template <typename IO, int V, bool SUMMARY, int MODE>
 __global__ void __launch_bounds__(64, 1)
 mixer_fwd_kernel(Args a) {
   using RawT = typename Raw<IO, V>::T;
   constexpr int ESZ = sizeof(IO);
   constexpr int MB = 64 * V;
+  constexpr bool GW = MODE != kModule;  // the writes are given
+  static_assert(kStateChunk % kS == 0, "blocks must tile the saved-state chunks");
   const int lane = threadIdx.x;
   const ChainPos cp = chain_pos(a);
   const int b = cp.b, mb = cp.mb, t_begin = cp.t_begin, t_end = cp.t_end;
@@ -283,6 +325,22 @@ mixer_fwd_kernel(Args a) {
     for (int v = 0; v < V; ++v) {
       hr[v] = h0[2 * v];
       hi[v] = h0[2 * v + 1];
+    }
+    if constexpr (GW && !SUMMARY) {
+      // the caller's initial state, for a single segment (with segments the
+      // carry kernel has folded it into the entering state of segment 0)
+      const bool from_h0 = a.n_seg == 1 && a.h0_re != nullptr;
+      const int64_t hb = static_cast<int64_t>(b) * a.M;
+      const __amdgpu_buffer_rsrc_t rr = make_rsrc(from_h0 ? a.h0_re + hb : a.consts, from_h0 ? a.M * 4u : 0u);
+      const __amdgpu_buffer_rsrc_t ri = make_rsrc(from_h0 ? a.h0_im + hb : a.consts, from_h0 ? a.M * 4u : 0u);
+      float qr[V], qi[V];
+      buffer_load_f32<V, CPOL_DEFAULT>(rr, static_cast<uint32_t>(lane_ok ? m0 * 4 : 0), qr);
+      buffer_load_f32<V, CPOL_DEFAULT>(ri, static_cast<uint32_t>(lane_ok ? m0 * 4 : 0), qi);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        hr[v] += qr[v];
+        hi[v] += qi[v];
+      }
     }
   }
   float Pr[V], Pi[V];  // SUMMARY: the product of the segment's transitions
@@ -309,13 +367,25 @@ mixer_fwd_kernel(Args a) {
     const int last = t_end - 1 - t0;
     // the block's rows of x through one buffer resource: row offsets in
     // scalar registers, no per-lane address arithmetic
-    const int64_t off = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const char*>(a.x) + off, blk_x);
+    if constexpr (GW) {  // the writes: rows of the w_re and w_im planes
+      const int64_t off = wave_uniform(((row0 + t0) * a.M + mbase) * ESZ);
+      const __amdgpu_buffer_rsrc_t rwr = make_rsrc(static_cast<const char*>(a.w_re) + off, blk_h);
+      const __amdgpu_buffer_rsrc_t rwi = make_rsrc(static_cast<const char*>(a.w_im) + off, blk_h);
 #pragma unroll
-    for (int s = 0; s < kS; ++s) {
-      const uint32_t o = static_cast<uint32_t>(s <= last ? s : last) * row_x;
-      xr[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
-      xi[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
+      for (int s = 0; s < kS; ++s) {
+        const uint32_t o = static_cast<uint32_t>(s <= last ? s : last) * half_x;
+        xr[h][s] = buf_load<RawT, CPOL_NT>(rwr, lane_ld, o);
+        xi[h][s] = buf_load<RawT, CPOL_NT>(rwi, lane_ld, o);
+      }
+    } else {
+      const int64_t off = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
+      const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const char*>(a.x) + off, blk_x);
+#pragma unroll
+      for (int s = 0; s < kS; ++s) {
+        const uint32_t o = static_cast<uint32_t>(s <= last ? s : last) * row_x;
+        xr[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
+        xi[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
+      }
     }
     const int sl = lane & (kS - 1);
     const int64_t ti = row0 + t0 + (sl <= last ? sl : last);
@@ -342,12 +412,18 @@ mixer_fwd_kernel(Args a) {
       unpack<IO, V>(xi[h][s], ci);
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        const StepMode q = p1_step(mc.nu[v], mc.ct[v], mc.st[v], mc.g2[v], mc.pl[v], mc.rl[v], E, eta, delta);
-        ar[s][v] = q.ar;
-        ai[s][v] = q.ai;
-        wr[s][v] = q.gain * tanh_fast(cr[v]);
-        wi[s][v] = q.gain * tanh_fast(ci[v]);
-        if constexpr (kRoundWrite<IO>) round_bf16x2(wr[s][v], wi[s][v]);
+        if constexpr (GW) {
+          p1_transition(mc.nu[v], mc.ct[v], mc.st[v], E, delta, ar[s][v], ai[s][v]);
+          wr[s][v] = cr[v];
+          wi[s][v] = ci[v];
+        } else {
+          const StepMode q = p1_step(mc.nu[v], mc.ct[v], mc.st[v], mc.g2[v], mc.pl[v], mc.rl[v], E, eta, delta);
+          ar[s][v] = q.ar;
+          ai[s][v] = q.ai;
+          wr[s][v] = q.gain * tanh_fast(cr[v]);
+          wi[s][v] = q.gain * tanh_fast(ci[v]);
+          if constexpr (kRoundWrite<IO>) round_bf16x2(wr[s][v], wi[s][v]);
+        }
       }
     }
     const int64_t yoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
@@ -371,16 +447,33 @@ mixer_fwd_kernel(Args a) {
         }
       }
       if constexpr (SUMMARY) continue;
-      float rr[V], ri[V];
-#pragma unroll
-      for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
       if (lane_ok) {
-        const uint32_t yo = static_cast<uint32_t>(s) * row_x;
-        buf_store<RawT, CPOL_NT>(pack<IO, V>(rr), ry, lane_bytes, yo);
-        buf_store<RawT, CPOL_NT>(pack<IO, V>(ri), ry, lane_bytes, yo + half_x);
-        const uint32_t ho = static_cast<uint32_t>(s) * half_x;
-        buf_store<RawT, CPOL_NT>(pack<IO, V>(hr), rhr, lane_bytes, ho);
-        buf_store<RawT, CPOL_NT>(pack<IO, V>(hi), rhi, lane_bytes, ho);
+        if constexpr (MODE != kPlanes) {  // y = relu(cat(h_re, h_im))
+          float rr[V], ri[V];
+#pragma unroll
+          for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
+          const uint32_t yo = static_cast<uint32_t>(s) * row_x;
+          buf_store<RawT, CPOL_NT>(pack<IO, V>(rr), ry, lane_bytes, yo);
+          buf_store<RawT, CPOL_NT>(pack<IO, V>(ri), ry, lane_bytes, yo + half_x);
+        }
+        if constexpr (MODE != kRelu) {  // the states
+          const uint32_t ho = static_cast<uint32_t>(s) * half_x;
+          buf_store<RawT, CPOL_NT>(pack<IO, V>(hr), rhr, lane_bytes, ho);
+          buf_store<RawT, CPOL_NT>(pack<IO, V>(hi), rhi, lane_bytes, ho);
+        }
+      }
+    }
+    if constexpr (GW && !SUMMARY) {
+      // the state after the last step of every 64-step chunk and after T-1
+      const int t_last = (TAIL ? t_end : t0 + kS) - 1;
+      if (lane_ok && ((t_last + 1) % kStateChunk == 0 || t_last == a.T - 1)) {
+        const int64_t n_chunks = (a.T + kStateChunk - 1) / kStateChunk;
+        float* cs = a.chunk_state + ((static_cast<int64_t>(b) * n_chunks + t_last / kStateChunk) * a.M + m0) * 2;
+        float o[2 * V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) { o[2 * v] = hr[v]; o[2 * v + 1] = hi[v]; }
+        if constexpr (V == 2) *reinterpret_cast<float4*>(cs) = make_float4(o[0], o[1], o[2], o[3]);
+        else *reinterpret_cast<float2*>(cs) = make_float2(o[0], o[1]);
       }
     }
   };
@@ -432,12 +525,14 @@ mixer_fwd_kernel(Args a) {
 //   d wlg += g, d wpr += g (1 - sig) delta 2/pi, d wrr += g (1 - sig) eta / log16
 // (the P1 chain rule of sparc-kernal/backward/scan.py:593-644 and the write
 // gradients of sparc-kernal/backward/control.py:10-89).
-template <typename IO, int V, int kS, bool SUMMARY>
+template <typename IO, int V, int kS, bool SUMMARY, int MODE>
 __global__ void __launch_bounds__(64, 2)
 mixer_bwd_kernel(Args a) {
   using RawT = typename Raw<IO, V>::T;
   constexpr int ESZ = sizeof(IO);
   constexpr int MB = 64 * V;
+  constexpr bool GW = MODE == kPlanes;  // the writes are given: dw out, no relu mask
+  static_assert(MODE != kRelu, "the backward of the relu output recomputes states (scan.hip)");
   const int lane = threadIdx.x;
   const ChainPos cp = chain_pos(a);
   const int b = cp.b, mb = cp.mb, t_begin = cp.t_begin, t_end = cp.t_end;
@@ -482,10 +577,25 @@ mixer_bwd_kernel(Args a) {
 #pragma unroll
     for (int p = 0; p < 5; ++p) acc[p][v] = 0.0f;
   }
-  {  // h at the segment's last step: its relu mask
+  if constexpr (!GW) {  // h at the segment's last step: its relu mask
     const int64_t ho = wave_uniform(((row0 + t_end - 1) * a.M + mbase) * ESZ);
     unpack<IO, V>(ldb<RawT>(a.h_re, ho, lane_ld), hcr);
     unpack<IO, V>(ldb<RawT>(a.h_im, ho, lane_ld), hci);
+  }
+  // GW: the state before step 0 (the caller's initial state, else zero), for
+  // the transition gradient of step 0; a buffer load over an empty range
+  // reads the zeros
+  float h0r[V], h0i[V];
+  if constexpr (GW && !SUMMARY) {
+    const bool use = t_begin == 0 && a.h0_re != nullptr;
+    const int64_t hb = static_cast<int64_t>(b) * a.M;
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(use ? a.h0_re + hb : a.consts, use ? a.M * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t ri = make_rsrc(use ? a.h0_im + hb : a.consts, use ? a.M * 4u : 0u);
+    buffer_load_f32<V, CPOL_DEFAULT>(rr, static_cast<uint32_t>(lane_ok ? m0 * 4 : 0), h0r);
+    buffer_load_f32<V, CPOL_DEFAULT>(ri, static_cast<uint32_t>(lane_ok ? m0 * 4 : 0), h0i);
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) { h0r[v] = 0.0f; h0i[v] = 0.0f; }
   }
   wait_vm_all();  // the loop-carried values above, before the first prefetch
 
@@ -501,26 +611,38 @@ mixer_bwd_kernel(Args a) {
     // registers); the previous states start at row t0-1 (row 0 when t0 = 0)
     const int hb = t0 > 0 ? t0 - 1 : 0;
     const int64_t xoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
+    const int64_t woff = wave_uniform(((row0 + t0) * a.M + mbase) * ESZ);
     const int64_t poff = wave_uniform(((row0 + hb) * a.M + mbase) * ESZ);
-    const __amdgpu_buffer_rsrc_t rdy = make_rsrc(static_cast<const char*>(a.dy) + xoff, blk_x);
+    // module: dy [B,T,2M] and x; GW: the dy_re and dy_im planes [B,T,M]
+    const __amdgpu_buffer_rsrc_t rdy = GW ? make_rsrc(static_cast<const char*>(a.dy) + woff, blk_h)
+                                          : make_rsrc(static_cast<const char*>(a.dy) + xoff, blk_x);
+    const __amdgpu_buffer_rsrc_t rdi = GW ? make_rsrc(static_cast<const char*>(a.dy_im) + woff, blk_h) : rdy;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const char*>(a.x) + xoff, blk_x);
     const __amdgpu_buffer_rsrc_t rpr = make_rsrc(static_cast<const char*>(a.h_re) + poff, blk_h);
     const __amdgpu_buffer_rsrc_t rpi = make_rsrc(static_cast<const char*>(a.h_im) + poff, blk_h);
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
       const int sc = s <= last ? s : last;
-      const uint32_t o = static_cast<uint32_t>(sc) * row_x;
-      dr[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o);
-      di[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o + half_x);
-      if constexpr (!SUMMARY) {  // summaries need no write path
-        xr[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
-        xi[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
+      if constexpr (GW) {
+        const uint32_t o = static_cast<uint32_t>(sc) * half_x;
+        dr[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o);
+        di[h][s] = buf_load<RawT, CPOL_NT>(rdi, lane_ld, o);
+      } else {
+        const uint32_t o = static_cast<uint32_t>(sc) * row_x;
+        dr[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o);
+        di[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o + half_x);
+        if constexpr (!SUMMARY) {  // summaries need no write path
+          xr[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
+          xi[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
+        }
       }
-      // row t-1 (t >= 1), else row 0, relative to hb
-      const int rel = t0 > 0 ? sc : (sc > 0 ? sc - 1 : 0);
-      const uint32_t q = static_cast<uint32_t>(rel) * half_x;
-      pr[h][s] = buf_load<RawT, CPOL_NT>(rpr, lane_ld, q);
-      pi[h][s] = buf_load<RawT, CPOL_NT>(rpi, lane_ld, q);
+      if constexpr (!(GW && SUMMARY)) {  // GW summaries need no states (no relu mask)
+        // row t-1 (t >= 1), else row 0, relative to hb
+        const int rel = t0 > 0 ? sc : (sc > 0 ? sc - 1 : 0);
+        const uint32_t q = static_cast<uint32_t>(rel) * half_x;
+        pr[h][s] = buf_load<RawT, CPOL_NT>(rpr, lane_ld, q);
+        pi[h][s] = buf_load<RawT, CPOL_NT>(rpi, lane_ld, q);
+      }
     }
     const int sl = lane & (kS - 1);
     const int64_t ti = row0 + t0 + (sl <= last ? sl : last);
@@ -567,21 +689,29 @@ mixer_bwd_kernel(Args a) {
         for (int v = 0; v < V; ++v) { lr[s][v] = 0.0f; li[s][v] = 0.0f; }
         continue;
       }
-      float gyr[V], gyi[V], mr[V], mi[V];
+      float gyr[V], gyi[V];
       unpack<IO, V>(dr[h][s], gyr);
       unpack<IO, V>(di[h][s], gyi);
-      const bool carry = s == kS - 1 || (TAIL && t == t_end - 1);  // wave-uniform
-      if (carry) {
+      if constexpr (!GW) {  // the relu mask: h_t > 0
+        float mr[V], mi[V];
+        const bool carry = s == kS - 1 || (TAIL && t == t_end - 1);  // wave-uniform
+        if (carry) {
 #pragma unroll
-        for (int v = 0; v < V; ++v) { mr[v] = hcr[v]; mi[v] = hci[v]; }
-      } else {
-        unpack<IO, V>(pr[h][s + 1 < kS ? s + 1 : s], mr);
-        unpack<IO, V>(pi[h][s + 1 < kS ? s + 1 : s], mi);
+          for (int v = 0; v < V; ++v) { mr[v] = hcr[v]; mi[v] = hci[v]; }
+        } else {
+          unpack<IO, V>(pr[h][s + 1 < kS ? s + 1 : s], mr);
+          unpack<IO, V>(pi[h][s + 1 < kS ? s + 1 : s], mi);
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          gyr[v] = mr[v] > 0.0f ? gyr[v] : 0.0f;
+          gyi[v] = mi[v] > 0.0f ? gyi[v] : 0.0f;
+        }
       }
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        lr[s][v] = (mr[v] > 0.0f ? gyr[v] : 0.0f) + Xr[v];
-        li[s][v] = (mi[v] > 0.0f ? gyi[v] : 0.0f) + Xi[v];
+        lr[s][v] = gyr[v] + Xr[v];
+        li[s][v] = gyi[v] + Xi[v];
         Xr[v] = fmaf(qar[s][v], lr[s][v], qai[s][v] * li[s][v]);
         Xi[v] = fmaf(qar[s][v], li[s][v], -qai[s][v] * lr[s][v]);
         if constexpr (SUMMARY) {  // P <- conj(a) P
@@ -592,8 +722,10 @@ mixer_bwd_kernel(Args a) {
       }
     }
     if constexpr (SUMMARY) {  // the adjoint alone: no gradients, no stores
-      unpack<IO, V>(pr[h][0], hcr);
-      unpack<IO, V>(pi[h][0], hci);
+      if constexpr (!GW) {
+        unpack<IO, V>(pr[h][0], hcr);
+        unpack<IO, V>(pi[h][0], hci);
+      }
       return;
     }
     // (C) gradients; e[2s], e[2s+1]: this lane's d eta, d delta of step s
@@ -608,58 +740,93 @@ mixer_bwd_kernel(Args a) {
       float hpr[V], hpi[V], cxr[V], cxi[V];
       unpack<IO, V>(pr[h][s], hpr);
       unpack<IO, V>(pi[h][s], hpi);
-      unpack<IO, V>(xr[h][s], cxr);
-      unpack<IO, V>(xi[h][s], cxi);
+      if constexpr (!GW) {
+        unpack<IO, V>(xr[h][s], cxr);
+        unpack<IO, V>(xi[h][s], cxi);
+      }
       float se = 0.0f, sd = 0.0f;
       const bool live = !TAIL || t < t_end;  // steps past the segment contribute nothing (wave-uniform)
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        if (t == 0) { hpr[v] = 0.0f; hpi[v] = 0.0f; }
+        if (t == 0) { hpr[v] = h0r[v]; hpi[v] = h0i[v]; }
         const float l_r = lr[s][v], l_i = li[s][v];
-        const float em = qem[s][v], rho = 1.0f + em;
-        const float ar = qar[s][v], ai = qai[s][v];
-        const float e2 = fmaf(em, em, em + em);  // em (2 + em) = expm1(-2 nu E) = rho^2 - 1
-        const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(delta, mc.pl[v], eta * mc.rl[v])));
-        // one reciprocal square root gives both sqrt(Y) = Y r and 1/e2 = g2 r^2
-        // (Y >= 0; the floor keeps a zero gain at zero instead of 0 * inf)
-        const float Y = mc.g2[v] * e2, r = __builtin_amdgcn_rsqf(fmaxf(Y, 1e-30f));
-        const float gain = Y * r * sg;
-        const float tr = tanh_fast(cxr[v]), ti = tanh_fast(cxi[v]);
-        float w_r = l_r, w_i = l_i;  // the write's gradient
-        if constexpr (kRoundWrite<IO>) round_bf16x2(w_r, w_i);
-        dxr[s][v] = w_r * gain * fmaf(-tr, tr, 1.0f);
-        dxi[s][v] = w_i * gain * fmaf(-ti, ti, 1.0f);
-        const float g = fmaf(w_r, tr, w_i * ti) * gain;
-        const float gar = fmaf(l_r, hpr[v], l_i * hpi[v]);
-        const float gai = fmaf(l_i, hpr[v], -l_r * hpi[v]);
-        const float dphi = fmaf(-gar, ai, gai * ar);
-        const float z = mc.nu[v] * E;  // -log(rho)
-        const float radial = z * fmaf(rho * delta, dphi, -fmaf(gar, ar, gai * ai));
-        const float wterm = -z * fmaf(mc.g2[v], r * r, 1.0f);  // -z rho^2 / e2 = -z (1 + 1/e2)
-        const float gs = g * (1.0f - sg);
-        se += radial + fmaf(g, wterm, gs * mc.wrr_s[v]);
-        sd += fmaf(dphi, -em, gs * mc.wpr_s[v]);
-        if (live) {
-          acc[0][v] += radial + g * (wterm - mc.kappa[v]);
-          acc[1][v] = fmaf(mc.th[v], dphi, acc[1][v]);
-          acc[2][v] += g;
-          acc[3][v] = fmaf(gs, ps, acc[3][v]);
-          acc[4][v] = fmaf(gs, rs, acc[4][v]);
+        if constexpr (GW) {  // dw = lambda; the transition gradients alone
+          const float em = qem[s][v], rho = 1.0f + em;
+          const float ar = qar[s][v], ai = qai[s][v];
+          dxr[s][v] = l_r;
+          dxi[s][v] = l_i;
+          const float gar = fmaf(l_r, hpr[v], l_i * hpi[v]);
+          const float gai = fmaf(l_i, hpr[v], -l_r * hpi[v]);
+          const float dphi = fmaf(-gar, ai, gai * ar);
+          const float z = mc.nu[v] * E;  // -log(rho)
+          const float radial = z * fmaf(rho * delta, dphi, -fmaf(gar, ar, gai * ai));
+          se += radial;
+          sd = fmaf(dphi, -em, sd);
+          if (live) {
+            acc[0][v] += radial;
+            acc[1][v] = fmaf(mc.th[v], dphi, acc[1][v]);
+          }
+        } else {  // module: the write path too
+          const float em = qem[s][v], rho = 1.0f + em;
+          const float ar = qar[s][v], ai = qai[s][v];
+          const float e2 = fmaf(em, em, em + em);  // em (2 + em) = expm1(-2 nu E) = rho^2 - 1
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(delta, mc.pl[v], eta * mc.rl[v])));
+          // one reciprocal square root gives both sqrt(Y) = Y r and 1/e2 = g2 r^2
+          // (Y >= 0; the floor keeps a zero gain at zero instead of 0 * inf)
+          const float Y = mc.g2[v] * e2, r = __builtin_amdgcn_rsqf(fmaxf(Y, 1e-30f));
+          const float gain = Y * r * sg;
+          const float tr = tanh_fast(cxr[v]), ti = tanh_fast(cxi[v]);
+          float w_r = l_r, w_i = l_i;  // the write's gradient
+          if constexpr (kRoundWrite<IO>) round_bf16x2(w_r, w_i);
+          dxr[s][v] = w_r * gain * fmaf(-tr, tr, 1.0f);
+          dxi[s][v] = w_i * gain * fmaf(-ti, ti, 1.0f);
+          const float g = fmaf(w_r, tr, w_i * ti) * gain;
+          const float gar = fmaf(l_r, hpr[v], l_i * hpi[v]);
+          const float gai = fmaf(l_i, hpr[v], -l_r * hpi[v]);
+          const float dphi = fmaf(-gar, ai, gai * ar);
+          const float z = mc.nu[v] * E;  // -log(rho)
+          const float radial = z * fmaf(rho * delta, dphi, -fmaf(gar, ar, gai * ai));
+          const float wterm = -z * fmaf(mc.g2[v], r * r, 1.0f);  // -z rho^2 / e2 = -z (1 + 1/e2)
+          const float gs = g * (1.0f - sg);
+          se += radial + fmaf(g, wterm, gs * mc.wrr_s[v]);
+          sd += fmaf(dphi, -em, gs * mc.wpr_s[v]);
+          if (live) {
+            acc[0][v] += radial + g * (wterm - mc.kappa[v]);
+            acc[1][v] = fmaf(mc.th[v], dphi, acc[1][v]);
+            acc[2][v] += g;
+            acc[3][v] = fmaf(gs, ps, acc[3][v]);
+            acc[4][v] = fmaf(gs, rs, acc[4][v]);
+          }
         }
       }
       e[2 * s] = lane_ok ? se : 0.0f;
       e[2 * s + 1] = lane_ok ? sd : 0.0f;
     }
     // (D) stores; the carry for the next block (in reverse time) is h_{t0-1}
-    const int64_t xoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
-    const __amdgpu_buffer_rsrc_t rdx = make_rsrc(static_cast<char*>(a.dx) + xoff, blk_x);
+    if constexpr (GW) {  // dw_re, dw_im planes
+      const int64_t woff = wave_uniform(((row0 + t0) * a.M + mbase) * ESZ);
+      const __amdgpu_buffer_rsrc_t rwr = make_rsrc(static_cast<char*>(a.dx) + woff, blk_h);
+      const __amdgpu_buffer_rsrc_t rwi = make_rsrc(static_cast<char*>(a.dw_im) + woff, blk_h);
 #pragma unroll
-    for (int s = 0; s < kS; ++s) {
-      if (TAIL && t0 + s >= t_end) break;
-      if (lane_ok) {
-        const uint32_t o = static_cast<uint32_t>(s) * row_x;
-        buf_store<RawT, CPOL_NT>(pack<IO, V>(dxr[s]), rdx, lane_bytes, o);
-        buf_store<RawT, CPOL_NT>(pack<IO, V>(dxi[s]), rdx, lane_bytes, o + half_x);
+      for (int s = 0; s < kS; ++s) {
+        if (TAIL && t0 + s >= t_end) break;
+        if (lane_ok) {
+          const uint32_t o = static_cast<uint32_t>(s) * half_x;
+          buf_store<RawT, CPOL_NT>(pack<IO, V>(dxr[s]), rwr, lane_bytes, o);
+          buf_store<RawT, CPOL_NT>(pack<IO, V>(dxi[s]), rwi, lane_bytes, o);
+        }
+      }
+    } else {
+      const int64_t xoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
+      const __amdgpu_buffer_rsrc_t rdx = make_rsrc(static_cast<char*>(a.dx) + xoff, blk_x);
+#pragma unroll
+      for (int s = 0; s < kS; ++s) {
+        if (TAIL && t0 + s >= t_end) break;
+        if (lane_ok) {
+          const uint32_t o = static_cast<uint32_t>(s) * row_x;
+          buf_store<RawT, CPOL_NT>(pack<IO, V>(dxr[s]), rdx, lane_bytes, o);
+          buf_store<RawT, CPOL_NT>(pack<IO, V>(dxi[s]), rdx, lane_bytes, o + half_x);
+        }
       }
     }
     // the wave sums of the block's 2*kS per-token values: the first lane of
@@ -674,8 +841,10 @@ mixer_bwd_kernel(Args a) {
         if (t < t_end) a.part_tok[(static_cast<int64_t>(i & 1) * a.n_mb + mb) * R + row0 + t] = e[k];
       }
     }
-    unpack<IO, V>(pr[h][0], hcr);
-    unpack<IO, V>(pi[h][0], hci);
+    if constexpr (!GW) {
+      unpack<IO, V>(pr[h][0], hcr);
+      unpack<IO, V>(pi[h][0], hci);
+    }
   };
 
   // block k uses register buffer k & 1 (compile-time in each call, see the forward)
@@ -707,11 +876,21 @@ mixer_bwd_kernel(Args a) {
     }
   } else if (lane_ok) {
     const int64_t rows = static_cast<int64_t>(a.B) * a.n_seg, row = static_cast<int64_t>(b) * a.n_seg + cp.seg;
+    constexpr int NP = GW ? 2 : 5;  // GW: nu_log and theta_log only
 #pragma unroll
-    for (int p = 0; p < 5; ++p)
+    for (int p = 0; p < NP; ++p)
 #pragma unroll
       for (int v = 0; v < V; ++v)
         a.part_mode[(p * rows + row) * a.M + m0 + v] = acc[p][v];
+    if constexpr (GW) {  // the gradient of the initial state: conj(a_0) lambda_0
+      if (t_begin == 0 && a.dh0_re) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          a.dh0_re[static_cast<int64_t>(b) * a.M + m0 + v] = Xr[v];
+          a.dh0_im[static_cast<int64_t>(b) * a.M + m0 + v] = Xi[v];
+        }
+      }
+    }
   }
 }
 
@@ -958,7 +1137,8 @@ struct Layout {
   size_t consts = 0, part_tok = 0, tok = 0, part_mode = 0, pd = 0, pbias = 0, seg_sum = 0, seg_state = 0, total = 0;
 };
 
-Layout layout(int64_t B, int64_t T, int64_t M, int direction) {
+// gw: the P1 scan with the writes given (no controls, two per-mode gradients)
+Layout layout(int64_t B, int64_t T, int64_t M, int direction, bool gw = false) {
   Layout l;
   l.V = mixer_v(B, M, direction);
   l.n_mb = static_cast<int>((M + 64 * l.V - 1) / (64 * l.V));
@@ -975,7 +1155,12 @@ Layout layout(int64_t B, int64_t T, int64_t M, int direction) {
     l.seg_state = off;
     off += up(static_cast<size_t>(B) * l.n_seg * M * 2 * 4);
   }
-  if (direction == 1) {
+  if (direction == 1 && gw) {
+    l.part_tok = off;
+    off += up(static_cast<size_t>(2) * l.n_mb * l.R * 4);
+    l.part_mode = off;
+    off += up(static_cast<size_t>(2) * B * l.n_seg * M * 4);
+  } else if (direction == 1) {
     l.part_tok = off;
     off += up(static_cast<size_t>(2) * l.n_mb * l.R * 4);
     l.tok = off;
@@ -1002,38 +1187,39 @@ sparc_status check_shape(int64_t B, int64_t T, int64_t M, int32_t io) {
 }
 
 // the forward over n_segs segments from a.seg_lo (SUMMARY: the maps only)
-template <typename IO, int V, bool SUMMARY>
+template <typename IO, int V, bool SUMMARY, int MODE>
 void launch_fwd(const Args& a, int n_segs, hipStream_t st) {
   const dim3 g(static_cast<unsigned>(a.B) * a.n_mb * static_cast<unsigned>(n_segs));
-  hipLaunchKernelGGL((mixer_fwd_kernel<IO, V, SUMMARY>), g, dim3(64), 0, st, a);
+  hipLaunchKernelGGL((mixer_fwd_kernel<IO, V, SUMMARY, MODE>), g, dim3(64), 0, st, a);
 }
-template <typename IO, int V>
+template <typename IO, int V, int MODE = kModule>
 void run_fwd(const Args& a, hipStream_t st) {
-  if (a.n_seg > 1) {  // maps of segments 0 .. n-2, then the entering states
-    launch_fwd<IO, V, true>(a, a.n_seg - 1, st);
+  if (a.n_seg > 1) {  // maps of segments 0 .. n-2, then the entering states (from h0, if any)
+    // (the summaries read the writes only: kRelu shares the kPlanes kernel)
+    launch_fwd<IO, V, true, MODE == kModule ? kModule : kPlanes>(a, a.n_seg - 1, st);
     hipLaunchKernelGGL(mixer_seg_carry_kernel, dim3(static_cast<unsigned>(a.B) * a.M), dim3(64), 0, st, a.B, a.M,
-                       a.n_seg, 0, a.seg_sum, nullptr, nullptr, a.seg_state);
+                       a.n_seg, 0, a.seg_sum, a.h0_re, a.h0_im, a.seg_state);
   }
-  launch_fwd<IO, V, false>(a, a.n_seg, st);
+  launch_fwd<IO, V, false, MODE>(a, a.n_seg, st);
 }
 #ifndef SPARC_MIXER_BWD_S
 #define SPARC_MIXER_BWD_S 4
 #endif
-template <typename IO, int V, bool SUMMARY>
+template <typename IO, int V, bool SUMMARY, int MODE>
 void launch_bwd(const Args& a, int n_segs, hipStream_t st) {
   const dim3 g(static_cast<unsigned>(a.B) * a.n_mb * static_cast<unsigned>(n_segs));
-  hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, SPARC_MIXER_BWD_S, SUMMARY>), g, dim3(64), 0, st, a);
+  hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, SPARC_MIXER_BWD_S, SUMMARY, MODE>), g, dim3(64), 0, st, a);
 }
-template <typename IO, int V>
+template <typename IO, int V, int MODE = kModule>
 void run_bwd(const Args& a, hipStream_t st) {
   if (a.n_seg > 1) {  // maps of segments n-1 .. 1 (reverse time), then the entering adjoints
     Args s = a;
     s.seg_lo = 1;
-    launch_bwd<IO, V, true>(s, a.n_seg - 1, st);
+    launch_bwd<IO, V, true, MODE>(s, a.n_seg - 1, st);
     hipLaunchKernelGGL(mixer_seg_carry_kernel, dim3(static_cast<unsigned>(a.B) * a.M), dim3(64), 0, st, a.B, a.M,
                        a.n_seg, 1, a.seg_sum, a.dlast_re, a.dlast_im, a.seg_state);
   }
-  launch_bwd<IO, V, false>(a, a.n_seg, st);
+  launch_bwd<IO, V, false, MODE>(a, a.n_seg, st);
 }
 
 // The scan and its backward with the controls given; the per-mode constants
@@ -1130,7 +1316,124 @@ sparc_status scan_backward_impl(const Layout& l, int64_t batch, int64_t length, 
 bool params_ok(const float* a, const float* b, const float* c, const float* d, const float* e) {
   return a && b && c && d && e;
 }
+
+#ifndef SPARC_P1_FUSED
+#define SPARC_P1_FUSED 1
+#endif
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// the P1 scan with the writes given (sparc_scan_forward / _backward, G = 1)
+// ---------------------------------------------------------------------------
+namespace sparc {
+using namespace sparc::mix;
+
+bool p1_fused_shape(const sparc_scan_desc* d) {
+  constexpr int32_t forced = SPARC_FLAG_ALGO_LOOKBACK | SPARC_FLAG_ALGO_CHAIN | SPARC_FLAG_ALGO_SERIAL;
+  if (!SPARC_P1_FUSED || !d || d->transition != SPARC_TRANSITION_P1 || d->groups != 1) return false;
+  if (d->flags & (SPARC_FLAG_RESET_FIRST | forced)) return false;
+  if (d->gate_dtype != SPARC_F32) return false;
+  return check_shape(d->batch, d->length, d->modes, d->io_dtype) == SPARC_OK;
+}
+
+size_t p1_fused_workspace_bytes(const sparc_scan_desc* d, int direction) {
+  if (!p1_fused_shape(d)) return 0;
+  return layout(d->batch, d->length, d->modes, direction, true).total;
+}
+
+sparc_status p1_fused_forward(const sparc_scan_desc* d, const float* eta, const float* delta,
+                              const float* nu_log, const float* theta_log, const void* w_re, const void* w_im,
+                              const float* h0_re, const float* h0_im, void* y_re, void* y_im,
+                              float* chunk_state, void* workspace, size_t workspace_bytes,
+                              sparc_stream_t stream) {
+  if (!p1_fused_shape(d) || d->length <= 0) return fail(SPARC_EINVAL, "p1 fused forward: shape");
+  const Layout l = layout(d->batch, d->length, d->modes, 0, true);
+  if (workspace_bytes < l.total) return fail(SPARC_EWORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, l.total);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const int M = static_cast<int>(d->modes);
+  float* consts = reinterpret_cast<float*>(ws + l.consts);
+  hipLaunchKernelGGL(mixer_prepare_kernel, dim3(static_cast<unsigned>((M + 255) / 256)), dim3(256), 0, st, M, nu_log,
+                     theta_log, nullptr, nullptr, nullptr, consts);
+  const bool relu = (d->flags & SPARC_FLAG_RELU_OUTPUT) != 0;
+  Args a{};
+  a.B = static_cast<int>(d->batch);
+  a.T = static_cast<int>(d->length);
+  a.M = M;
+  a.n_mb = l.n_mb;
+  a.consts = consts; a.eta = eta; a.delta = delta;
+  a.w_re = w_re; a.w_im = w_im; a.h0_re = h0_re; a.h0_im = h0_im; a.chunk_state = chunk_state;
+  if (relu) {
+    a.y = y_re;
+  } else {
+    a.h_re = y_re;
+    a.h_im = y_im;
+  }
+  a.n_seg = l.n_seg; a.t_seg = l.t_seg; a.seg_lo = 0;
+  a.seg_sum = reinterpret_cast<float*>(ws + l.seg_sum);
+  a.seg_state = reinterpret_cast<float*>(ws + l.seg_state);
+  const bool bf = d->io_dtype == SPARC_BF16;
+  if (relu) {
+    if (bf) { if (l.V == 2) run_fwd<sparc::bf16, 2, kRelu>(a, st); else run_fwd<sparc::bf16, 1, kRelu>(a, st); }
+    else { if (l.V == 2) run_fwd<float, 2, kRelu>(a, st); else run_fwd<float, 1, kRelu>(a, st); }
+  } else {
+    if (bf) { if (l.V == 2) run_fwd<sparc::bf16, 2, kPlanes>(a, st); else run_fwd<sparc::bf16, 1, kPlanes>(a, st); }
+    else { if (l.V == 2) run_fwd<float, 2, kPlanes>(a, st); else run_fwd<float, 1, kPlanes>(a, st); }
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "p1 fused forward: %s", hipGetErrorString(e));
+}
+
+sparc_status p1_fused_backward(const sparc_scan_desc* d, const float* eta, const float* delta,
+                               const float* nu_log, const float* theta_log, const void* y_re, const void* y_im,
+                               const float* h0_re, const float* h0_im, const void* dy_re, const void* dy_im,
+                               const float* dlast_re, const float* dlast_im, void* dw_re, void* dw_im,
+                               float* deta, float* ddelta, float* dnu_log, float* dtheta_log, float* dh0_re,
+                               float* dh0_im, void* workspace, size_t workspace_bytes, sparc_stream_t stream) {
+  if (!p1_fused_shape(d) || d->length <= 0 || (d->flags & SPARC_FLAG_RELU_OUTPUT))
+    return fail(SPARC_EINVAL, "p1 fused backward: shape");
+  const Layout l = layout(d->batch, d->length, d->modes, 1, true);
+  if (workspace_bytes < l.total) return fail(SPARC_EWORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, l.total);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const int M = static_cast<int>(d->modes);
+  float* consts = reinterpret_cast<float*>(ws + l.consts);
+  float* part_tok = reinterpret_cast<float*>(ws + l.part_tok);
+  float* part_mode = reinterpret_cast<float*>(ws + l.part_mode);
+  hipLaunchKernelGGL(mixer_prepare_kernel, dim3(static_cast<unsigned>((M + 255) / 256)), dim3(256), 0, st, M, nu_log,
+                     theta_log, nullptr, nullptr, nullptr, consts);
+  Args a{};
+  a.B = static_cast<int>(d->batch);
+  a.T = static_cast<int>(d->length);
+  a.M = M;
+  a.n_mb = l.n_mb;
+  a.consts = consts; a.eta = eta; a.delta = delta;
+  a.h_re = const_cast<void*>(y_re); a.h_im = const_cast<void*>(y_im);
+  a.dy = dy_re; a.dy_im = dy_im; a.dlast_re = dlast_re; a.dlast_im = dlast_im;
+  a.dx = dw_re; a.dw_im = dw_im;
+  a.h0_re = h0_re; a.h0_im = h0_im; a.dh0_re = dh0_re; a.dh0_im = dh0_im;
+  a.part_tok = part_tok; a.part_mode = part_mode;
+  a.n_seg = l.n_seg; a.t_seg = l.t_seg; a.seg_lo = 0;
+  a.seg_sum = reinterpret_cast<float*>(ws + l.seg_sum);
+  a.seg_state = reinterpret_cast<float*>(ws + l.seg_state);
+  if (d->io_dtype == SPARC_BF16) {
+    if (l.V == 2) run_bwd<sparc::bf16, 2, kPlanes>(a, st); else run_bwd<sparc::bf16, 1, kPlanes>(a, st);
+  } else {
+    if (l.V == 2) run_bwd<float, 2, kPlanes>(a, st); else run_bwd<float, 1, kPlanes>(a, st);
+  }
+  // d eta, d delta per token over the mode blocks; d nu_log, d theta_log per
+  // mode over the (batch row, segment) partial rows
+  if (sparc_status s = sparc_column_sum(l.n_mb, l.R, part_tok, deta, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(l.n_mb, l.R, part_tok + static_cast<int64_t>(l.n_mb) * l.R, ddelta, 0, stream))
+    return s;
+  const int64_t prow = d->batch * l.n_seg;
+  if (sparc_status s = sparc_column_sum(prow, d->modes, part_mode, dnu_log, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(prow, d->modes, part_mode + prow * d->modes, dtheta_log, 0, stream)) return s;
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "p1 fused backward: %s", hipGetErrorString(e));
+}
+
+}  // namespace sparc
 
 // The controls backward over rows of width W: n_cb column blocks of 2048
 // inputs, row blocks of `rows` rows (a multiple of 4 in [16, 128], chosen so

@@ -40,6 +40,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "p1_fused.h"
 #include "sparc_hip.h"
 
 // SPARC_SCAN_PART: which part of a split build this is (see the host side)
@@ -3664,10 +3665,26 @@ int64_t sparc_scan_chunk_count(const sparc_scan_desc* d) {
 }
 
 size_t sparc_scan_workspace_bytes(const sparc_scan_desc* d, int direction) {
-  // enough for either plan: the call decides from its pointers
+  // enough for every plan: the call decides from its pointers
   Plan pw, pn;
   if (make_plan(d, direction, &pw, true) || make_plan(d, direction, &pn, false)) return 0;
-  return pw.total > pn.total ? pw.total : pn.total;
+  size_t n = pw.total > pn.total ? pw.total : pn.total;
+  const size_t f = sparc::p1_fused_workspace_bytes(d, direction);
+  return f > n ? f : n;
+}
+
+// The P1 scan with one gate pair per token takes the one-wave-per-chain
+// kernels of the fused module path (p1_fused.h) when nothing needs the
+// general kernels: no segment resets, aligned planes, a large enough
+// workspace.  Otherwise the general kernels run.
+static bool p1_fused_route(const sparc_scan_desc* d, int direction, const int32_t* segment_pos,
+                           const void* const* planes, int n_planes, const float* chunk_state,
+                           size_t workspace_bytes) {
+  if (segment_pos || !sparc::p1_fused_shape(d)) return false;
+  if (workspace_bytes < sparc::p1_fused_workspace_bytes(d, direction)) return false;
+  for (int i = 0; i < n_planes; ++i)
+    if (!aligned(planes[i], 8)) return false;
+  return aligned(chunk_state, 16);
 }
 
 static sparc_status common_checks(const sparc_scan_desc* d, int dir, Plan* pl,
@@ -3748,6 +3765,13 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, con
     if (sparc_status s = check_gate_ptrs(d, pl, gp, 2)) return s;
   }
   if (!aligned(chunk_state, 8 * pl.V)) return fail(SPARC_EINVAL, "chunk_state must be %d-byte aligned", 8 * pl.V);
+  {
+    const void* fp[] = {w_re, w_im, y_re, y_im, h0_re, h0_im};
+    if (p1_fused_route(d, 0, segment_pos, fp, 6, chunk_state, workspace_bytes))
+      return sparc::p1_fused_forward(d, static_cast<const float*>(gate0), static_cast<const float*>(gate1), nu_log,
+                                     theta_log, w_re, w_im, h0_re, h0_im, y_re, relu ? nullptr : y_im, chunk_state,
+                                     workspace, workspace_bytes, stream);
+  }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (!pl.chain)
     if (sparc_status s = clear_ws(pl, workspace, st)) return s;
@@ -3837,6 +3861,14 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
   if (pl.gm == sparc::GATE_MODE) {
     const void* gp[] = {gate0, gate1, dgate0, dgate1};
     if (sparc_status s = check_gate_ptrs(d, pl, gp, 4)) return s;
+  }
+  if (saved) {  // P1 from the saved states: the fused kernels, when they apply
+    const void* fp[] = {y_re, y_im, dy_re, dy_im, dw_re, dw_im, h0_re, h0_im, dh0_re, dh0_im};
+    if (p1_fused_route(d, 1, segment_pos, fp, 10, chunk_state, workspace_bytes))
+      return sparc::p1_fused_backward(d, static_cast<const float*>(gate0), static_cast<const float*>(gate1), nu_log,
+                                      theta_log, y_re, y_im, h0_re, h0_im, dy_re, dy_im, dlast_re, dlast_im, dw_re,
+                                      dw_im, static_cast<float*>(dgate0), static_cast<float*>(dgate1), dnu_log,
+                                      dtheta_log, dh0_re, dh0_im, workspace, workspace_bytes, stream);
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (!pl.chain)

@@ -1,0 +1,75 @@
+"""GPU parity of the P1 scan with one gate pair per token (G = 1), which
+sparc_scan_forward / sparc_scan_backward run on the one-wave-per-chain
+kernels of the fused module path (writes given, states or relu(cat) out,
+chunk states every 64 steps; few chains split time into segments).
+
+Values, final states and every gradient (eta, delta, nu_log, theta_log, the
+writes, h0) against the float64 oracle, to 1e-4 (fp32 I/O) or 2e-2 (bf16
+I/O) of max |oracle|; the chunk states against the general chain kernels'
+(the same recurrence, other kernels).  The relu cases take the fused forward
+and the general backward (which recomputes the states from the chunk states
+the fused forward wrote)."""
+import pytest
+import torch
+
+from sparc_amd import ops
+from test_gpu_scan import BF16, F32, check_case, make_case, rel_err
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # (id, B, T, M, dtype, extra)
+    ("ragged_f32", 2, 200, 256, F32, {}),
+    ("bf16", 2, 192, 256, BF16, {}),
+    ("lanes_past_M_h0_f32", 3, 77, 132, F32, dict(h0=True, dlast=True)),
+    ("h0_dlast_bf16", 2, 150, 128, BF16, dict(h0=True, dlast=True)),
+    ("T1_h0_f32", 3, 1, 128, F32, dict(h0=True, dlast=True)),
+    ("relu_bf16", 2, 96, 256, BF16, dict(relu=True)),
+    ("relu_h0_f32", 2, 130, 128, F32, dict(relu=True, h0=True, dlast=True)),
+    # one or two chains: time segments (23 of 136 steps; 20 of 128)
+    ("segments_h0_f32", 1, 3000, 64, F32, dict(h0=True, dlast=True)),
+    ("segments_bf16", 2, 2500, 128, BF16, dict(dlast=True)),
+    ("segments_relu_h0_f32", 1, 1100, 64, F32, dict(relu=True, h0=True)),
+    # 1280 chains of 2 modes per lane in the forward
+    ("two_modes_per_lane_bf16", 10, 9, 16384, BF16, dict(h0=True, dlast=True)),
+]
+
+
+@pytest.mark.parametrize("cid,B,T,M,dtype,extra", CASES, ids=[c[0] for c in CASES])
+def test_p1_fused_parity(cid, B, T, M, dtype, extra):
+    ops.set_algorithm("auto")
+    print(f"[case] p1 fused {cid} B={B} T={T} M={M} {dtype}", flush=True)
+    case = make_case("p1", B, T, M, 1, dtype, seed=sum(map(ord, cid)) % 1000, **extra)
+    check_case(case)
+
+
+def _forward_raw(case, algorithm):
+    ops.set_algorithm(algorithm)
+    try:
+        init = case["init"]
+        h0 = (None, None) if init is None else tuple(t.cuda() for t in init)
+        y_re, y_im, cs = ops.scan_forward_raw(
+            "p1", case["g0"].cuda(), case["g1"].cuda(), case["w_re"].cuda(), case["w_im"].cuda(),
+            case["nu_log"].cuda(), case["theta_log"].cuda(), h0[0], h0[1], None, False, case["relu"])
+        torch.cuda.synchronize()
+        return y_re, y_im, cs
+    finally:
+        ops.set_algorithm("auto")
+
+
+@pytest.mark.parametrize("B,T,M,relu", [(2, 200, 256, False), (1, 3000, 64, False), (2, 130, 128, True)],
+                         ids=["ragged", "segments", "relu"])
+def test_p1_fused_chunk_states(B, T, M, relu):
+    """Every saved chunk state (the state after steps 63, 127, ... and T-1)
+    of the fused forward against the general chain forward's."""
+    print(f"[case] p1 fused chunk states B={B} T={T} M={M} relu={relu}", flush=True)
+    case = make_case("p1", B, T, M, 1, F32, seed=B * 7 + T, h0=True, relu=relu)
+    yf_re, yf_im, csf = _forward_raw(case, "auto")
+    yc_re, yc_im, csc = _forward_raw(case, "chain")
+    assert csf.shape == csc.shape == (B, (T + 63) // 64, M, 2)
+    for c in range(csf.shape[1]):
+        e = rel_err(csf[:, c], csc[:, c])
+        assert e <= 1e-4, f"chunk {c}: rel err {e:.3g}"
+    assert rel_err(yf_re, yc_re) <= 1e-4
+    if not relu:
+        assert rel_err(yf_im, yc_im) <= 1e-4
