@@ -389,6 +389,55 @@ __device__ __forceinline__ void sincos_half(float u, float& s, float& c) {
   c = fmaf(pc, u2, 1.0f);
 }
 
+// expm1_nonpos and sincos_half over N independent arguments, written one
+// polynomial level at a time across all N: the N dependency chains then
+// interleave in the instruction stream (the compiler keeps this order), so
+// a wave has independent work between dependent instructions.
+template <int N>
+__device__ __forceinline__ void expm1_nonpos_n(const float (&x)[N], float (&o)[N]) {
+  float p[N], e[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) p[i] = fmaf(1.0f / 24.0f, x[i], 1.0f / 6.0f);
+#pragma unroll
+  for (int i = 0; i < N; ++i) e[i] = __builtin_amdgcn_exp2f(x[i] * 1.4426950408889634f);
+#pragma unroll
+  for (int i = 0; i < N; ++i) p[i] = fmaf(p[i], x[i], 0.5f);
+#pragma unroll
+  for (int i = 0; i < N; ++i) p[i] = fmaf(p[i], x[i], 1.0f);
+#pragma unroll
+  for (int i = 0; i < N; ++i) p[i] *= x[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) o[i] = x[i] > -0.0625f ? p[i] : e[i] - 1.0f;
+}
+template <int N>
+__device__ __forceinline__ void sincos_half_n(const float (&u)[N], float (&s)[N], float (&c)[N]) {
+  float u2[N], ps[N], pc[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) u2[i] = u[i] * u[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    ps[i] = fmaf(2.6057807644974673e-6f, u2[i], -1.9809603691101074e-4f);
+    pc[i] = fmaf(-2.607710598567792e-7f, u2[i], 2.4761886379565112e-5f);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    ps[i] = fmaf(ps[i], u2[i], 8.33306647837162e-3f);
+    pc[i] = fmaf(pc[i], u2[i], -1.38884037733078e-3f);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    ps[i] = fmaf(ps[i], u2[i], -1.6666659712791443e-1f);
+    pc[i] = fmaf(pc[i], u2[i], 4.166664183139801e-2f);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    s[i] = fmaf(ps[i] * u2[i], u[i], u[i]);
+    pc[i] = fmaf(pc[i], u2[i], -0.5f);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) c[i] = fmaf(pc[i], u2[i], 1.0f);
+}
+
 // ---------------------------------------------------------------------------
 // cross-lane moves (every lane of the wave must be active: a DPP read from an
 // inactive lane returns 0)

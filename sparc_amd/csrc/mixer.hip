@@ -78,6 +78,14 @@ template <typename IO> constexpr bool kRoundWrite = SPARC_MIXER_ROUND_WRITE && s
 //            states (forward only).
 enum : int { kModule = 0, kPlanes = 1, kRelu = 2 };
 constexpr int kStateChunk = 64;  // steps per saved chunk state (sparc_scan_chunk_length)
+// A lane byte offset past every buffer resource of these kernels (each spans
+// less than 2^31 bytes): the hardware range check drops a store through it.
+// Lanes that must not store (past M) store through it, so that no store
+// sits under a branch: a branch per step splits the block's straight-line
+// code, and the compiler's wait for the prefetched loads then also covers
+// every store issued before them (the path that skips the stores has fewer
+// memory operations in flight).
+constexpr uint32_t kDropOffset = 0x80000000u;
 
 struct Args {
   int B, T, M, n_mb;
@@ -256,16 +264,40 @@ struct ModeConsts {
   }
 };
 
-// The P1 transition of one mode and step: a = rho e^{i (theta + (1 - rho) delta)},
-// rho = exp(-nu E), E = e^eta, with rho - 1 formed by expm1.
-__device__ __forceinline__ void p1_transition(float nu, float ct, float st, float E, float delta, float& ar,
-                                              float& ai) {
-  const float em = expm1_nonpos(-nu * E);
-  const float rho = 1.0f + em;
-  float su, cu;
-  sincos_half(-em * delta, su, cu);  // phase (1 - rho) delta, |.| <= pi/2
-  ar = rho * fmaf(ct, cu, -st * su);
-  ai = rho * fmaf(st, cu, ct * su);
+// The P1 transitions of a block of S steps (lane s of ee, dv: e^eta and
+// delta of step s) for the lane's V modes, written one polynomial level at a
+// time across the S*V values so that their dependency chains interleave.
+// The transition of p1_step, value for value: a = rho e^{i (theta + (1 - rho)
+// delta)}, rho = exp(-nu E), E = e^eta, with rho - 1 (em) formed by expm1.
+template <int S, int V, bool BWD>
+__device__ __forceinline__ void p1_block_transitions(const ModeConsts<V, BWD>& mc, float ee, float dv,
+                                                     float (&ar)[S][V], float (&ai)[S][V],
+                                                     float (*em_out)[V] = nullptr) {
+  constexpr int N = S * V;
+  float q[N], em[N], u[N], su[N], cu[N], dl[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const float E = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), s));
+    dl[s] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv), s));
+#pragma unroll
+    for (int v = 0; v < V; ++v) q[s * V + v] = -mc.nu[v] * E;
+  }
+  expm1_nonpos_n<N>(q, em);
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int v = 0; v < V; ++v) u[s * V + v] = -em[s * V + v] * dl[s];
+  sincos_half_n<N>(u, su, cu);
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int i = s * V + v;
+      const float rho = 1.0f + em[i];
+      ar[s][v] = rho * fmaf(mc.ct[v], cu[i], -mc.st[v] * su[i]);
+      ai[s][v] = rho * fmaf(mc.st[v], cu[i], mc.ct[v] * su[i]);
+      if (em_out) em_out[s][v] = em[i];
+    }
 }
 
 // Per-step values of the P1 transition and write of one mode.
@@ -351,6 +383,7 @@ mixer_fwd_kernel(Args a) {
   const int64_t W = 2 * static_cast<int64_t>(a.M);
   const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
   const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
+  const uint32_t lane_st = lane_ok ? lane_bytes : kDropOffset;
   // bytes of one row of x (2M) and of h (M), and of kS rows (< 2^31: the host
   // limits M to 2^24)
   const uint32_t row_x = static_cast<uint32_t>(W * ESZ), half_x = static_cast<uint32_t>(a.M * ESZ);
@@ -402,6 +435,7 @@ mixer_fwd_kernel(Args a) {
     constexpr bool TAIL = decltype(tail_tag)::value;
     float ar[kS][V], ai[kS][V], wr[kS][V], wi[kS][V];
     const float ee = fast_exp(ev[h]);  // lane s: e^eta of step s
+    if constexpr (GW) p1_block_transitions<kS, V>(mc, ee, dv[h], ar, ai);
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
       const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
@@ -412,8 +446,7 @@ mixer_fwd_kernel(Args a) {
       unpack<IO, V>(xi[h][s], ci);
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        if constexpr (GW) {
-          p1_transition(mc.nu[v], mc.ct[v], mc.st[v], E, delta, ar[s][v], ai[s][v]);
+        if constexpr (GW) {  // the transitions above
           wr[s][v] = cr[v];
           wi[s][v] = ci[v];
         } else {
@@ -447,33 +480,31 @@ mixer_fwd_kernel(Args a) {
         }
       }
       if constexpr (SUMMARY) continue;
-      if (lane_ok) {
-        if constexpr (MODE != kPlanes) {  // y = relu(cat(h_re, h_im))
-          float rr[V], ri[V];
+      if constexpr (MODE != kPlanes) {  // y = relu(cat(h_re, h_im))
+        float rr[V], ri[V];
 #pragma unroll
-          for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
-          const uint32_t yo = static_cast<uint32_t>(s) * row_x;
-          buf_store<RawT, CPOL_NT>(pack<IO, V>(rr), ry, lane_bytes, yo);
-          buf_store<RawT, CPOL_NT>(pack<IO, V>(ri), ry, lane_bytes, yo + half_x);
-        }
-        if constexpr (MODE != kRelu) {  // the states
-          const uint32_t ho = static_cast<uint32_t>(s) * half_x;
-          buf_store<RawT, CPOL_NT>(pack<IO, V>(hr), rhr, lane_bytes, ho);
-          buf_store<RawT, CPOL_NT>(pack<IO, V>(hi), rhi, lane_bytes, ho);
-        }
+        for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
+        const uint32_t yo = static_cast<uint32_t>(s) * row_x;
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(rr), ry, lane_st, yo);
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(ri), ry, lane_st, yo + half_x);
+      }
+      if constexpr (MODE != kRelu) {  // the states
+        const uint32_t ho = static_cast<uint32_t>(s) * half_x;
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(hr), rhr, lane_st, ho);
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(hi), rhi, lane_st, ho);
       }
     }
     if constexpr (GW && !SUMMARY) {
       // the state after the last step of every 64-step chunk and after T-1
       const int t_last = (TAIL ? t_end : t0 + kS) - 1;
-      if (lane_ok && ((t_last + 1) % kStateChunk == 0 || t_last == a.T - 1)) {
+      if ((t_last + 1) % kStateChunk == 0 || t_last == a.T - 1) {  // wave-uniform
         const int64_t n_chunks = (a.T + kStateChunk - 1) / kStateChunk;
-        float* cs = a.chunk_state + ((static_cast<int64_t>(b) * n_chunks + t_last / kStateChunk) * a.M + m0) * 2;
+        const int64_t off = wave_uniform(((static_cast<int64_t>(b) * n_chunks + t_last / kStateChunk) * a.M + mbase) * 8);
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(reinterpret_cast<char*>(a.chunk_state) + off, MB * 8u);
         float o[2 * V];
 #pragma unroll
         for (int v = 0; v < V; ++v) { o[2 * v] = hr[v]; o[2 * v + 1] = hi[v]; }
-        if constexpr (V == 2) *reinterpret_cast<float4*>(cs) = make_float4(o[0], o[1], o[2], o[3]);
-        else *reinterpret_cast<float2*>(cs) = make_float2(o[0], o[1]);
+        buffer_store_f32<2 * V, CPOL_DEFAULT>(rc, lane_ok ? static_cast<uint32_t>(lane * V * 8) : kDropOffset, o);
       }
     }
   };
@@ -545,6 +576,7 @@ mixer_bwd_kernel(Args a) {
   const int64_t W = 2 * static_cast<int64_t>(a.M);
   const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
   const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
+  const uint32_t lane_st = lane_ok ? lane_bytes : kDropOffset;
   // bytes of one row of x / dy / dx (2M) and of h (M), and of kS rows (the host
   // limits M to 2^24, so these fit in 32 bits)
   const uint32_t row_x = static_cast<uint32_t>(W * ESZ), half_x = static_cast<uint32_t>(a.M * ESZ);
@@ -664,21 +696,7 @@ mixer_bwd_kernel(Args a) {
     constexpr bool TAIL = decltype(tail_tag)::value;
     float qar[kS][V], qai[kS][V], qem[kS][V];
     const float ee = fast_exp(ev[h]);  // lane s: e^eta of step s
-#pragma unroll
-    for (int s = 0; s < kS; ++s) {
-      const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), s));
-      const float E = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), s));
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        const float em = expm1_nonpos(-mc.nu[v] * E);
-        const float rho = 1.0f + em;
-        float su, cu;
-        sincos_half(-em * delta, su, cu);
-        qar[s][v] = rho * fmaf(mc.ct[v], cu, -mc.st[v] * su);
-        qai[s][v] = rho * fmaf(mc.st[v], cu, mc.ct[v] * su);
-        qem[s][v] = em;
-      }
-    }
+    p1_block_transitions<kS, V>(mc, ee, dv[h], qar, qai, qem);
     // (B) the adjoint
     float lr[kS][V], li[kS][V];
 #pragma unroll
@@ -810,11 +828,9 @@ mixer_bwd_kernel(Args a) {
 #pragma unroll
       for (int s = 0; s < kS; ++s) {
         if (TAIL && t0 + s >= t_end) break;
-        if (lane_ok) {
-          const uint32_t o = static_cast<uint32_t>(s) * half_x;
-          buf_store<RawT, CPOL_NT>(pack<IO, V>(dxr[s]), rwr, lane_bytes, o);
-          buf_store<RawT, CPOL_NT>(pack<IO, V>(dxi[s]), rwi, lane_bytes, o);
-        }
+        const uint32_t o = static_cast<uint32_t>(s) * half_x;
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(dxr[s]), rwr, lane_st, o);
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(dxi[s]), rwi, lane_st, o);
       }
     } else {
       const int64_t xoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
@@ -822,23 +838,33 @@ mixer_bwd_kernel(Args a) {
 #pragma unroll
       for (int s = 0; s < kS; ++s) {
         if (TAIL && t0 + s >= t_end) break;
-        if (lane_ok) {
-          const uint32_t o = static_cast<uint32_t>(s) * row_x;
-          buf_store<RawT, CPOL_NT>(pack<IO, V>(dxr[s]), rdx, lane_bytes, o);
-          buf_store<RawT, CPOL_NT>(pack<IO, V>(dxi[s]), rdx, lane_bytes, o + half_x);
-        }
+        const uint32_t o = static_cast<uint32_t>(s) * row_x;
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(dxr[s]), rdx, lane_st, o);
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(dxi[s]), rdx, lane_st, o + half_x);
       }
     }
     // the wave sums of the block's 2*kS per-token values: the first lane of
     // each group of G lanes holds K of them (values i = lane / G * K + k)
     wave_sums_to_leaders<2 * kS>(e);
     constexpr int K = 2 * kS >= 16 ? 2 * kS / 16 : 1, G = 64 * K / (2 * kS);
-    if (lane % G == 0) {
+    {
+      // value i (d eta for even i, d delta for odd i, of step t0 + i/2) goes
+      // through the resource of its plane, which covers the block's steps
+      // inside the segment; the other plane's store, non-leader lanes and
+      // steps past the segment are dropped (no store under a branch)
+      const uint32_t nb = static_cast<uint32_t>(min(kS, t_end - t0)) * 4u;
+      const int64_t o0 = wave_uniform(((static_cast<int64_t>(0) * a.n_mb + mb) * R + row0 + t0) * 4);
+      const int64_t o1 = wave_uniform(((static_cast<int64_t>(1) * a.n_mb + mb) * R + row0 + t0) * 4);
+      const __amdgpu_buffer_rsrc_t rt0 = make_rsrc(reinterpret_cast<char*>(a.part_tok) + o0, nb);
+      const __amdgpu_buffer_rsrc_t rt1 = make_rsrc(reinterpret_cast<char*>(a.part_tok) + o1, nb);
+      const bool lead = lane % G == 0;
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         const int i = lane / G * K + k;
-        const int t = t0 + (i >> 1);
-        if (t < t_end) a.part_tok[(static_cast<int64_t>(i & 1) * a.n_mb + mb) * R + row0 + t] = e[k];
+        const uint32_t off = static_cast<uint32_t>(i >> 1) * 4u;
+        const float v[1] = {e[k]};
+        buffer_store_f32<1, CPOL_DEFAULT>(rt0, lead && !(i & 1) ? off : kDropOffset, v);
+        buffer_store_f32<1, CPOL_DEFAULT>(rt1, lead && (i & 1) ? off : kDropOffset, v);
       }
     }
     if constexpr (!GW) {
