@@ -243,6 +243,89 @@ def bench_cfg3(args, dev):
     }
 
 
+def bench_p1(args, dev):
+    """The reference's own scan operator (sparc_chunk_scan: the P1 transition
+    from per-token eta, delta and per-mode nu_log, theta_log; writes given) at
+    the headline shape: B=8, T=4096, M=16384, one gate pair per token (G = 1),
+    bf16 writes, fp32 eta/delta, fp32 state.  Forward and backward through the
+    C ABI; at G = 1 they run the one-wave-per-chain fused kernels
+    (mixer_fwd_kernel / mixer_bwd_kernel with the writes given), the backward
+    reading the states from the forward's output.
+
+    Algorithmic bytes: forward B*T*(8*M + 8) (read w, write y; read eta,
+    delta), backward B*T*(12*M + 16) (read dy and y, write dw; read eta,
+    delta, write their gradients)."""
+    from sparc_amd import _lib
+    lib = _lib.load()
+    B, T, M = 8, 4096, 16384
+    g = torch.Generator(device=dev).manual_seed(0)
+    eta = 2.772588722239781 * torch.tanh(0.5 * torch.randn(B, T, 1, device=dev, generator=g))
+    delta = 1.5707963267948966 * torch.tanh(torch.randn(B, T, 1, device=dev, generator=g))
+    nu_log = torch.log(-0.5 * torch.log(torch.rand(M, device=dev, generator=g).clamp_min(1e-30)))
+    theta_log = torch.log((2 * math.pi * torch.rand(M, device=dev, generator=g)).clamp_min(1e-30))
+    w_re, w_im, dy_re, dy_im = (torch.randn(B, T, M, device=dev, generator=g).bfloat16() for _ in range(4))
+    y_re, y_im, dw_re, dw_im = (torch.empty_like(w_re) for _ in range(4))
+    deta, ddelta = torch.empty_like(eta), torch.empty_like(delta)
+    dnu, dth = torch.empty_like(nu_log), torch.empty_like(theta_log)
+    d = _lib.ScanDesc(B, T, M, 1, _lib.TRANSITIONS["p1"], _lib.SPARC_BF16, _lib.SPARC_F32, 0)
+    cs = torch.empty(B, lib.sparc_scan_chunk_count(ctypes.byref(d)), M, 2, device=dev)
+    ws_f = torch.empty(lib.sparc_scan_workspace_bytes(ctypes.byref(d), 0), dtype=torch.uint8, device=dev)
+    ws_b = torch.empty(lib.sparc_scan_workspace_bytes(ctypes.byref(d), 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    st = stream.cuda_stream
+    P = _lib.ptr
+
+    def fwd():
+        _lib.check(lib.sparc_scan_forward(ctypes.byref(d), P(eta), P(delta), P(nu_log), P(theta_log), P(w_re),
+                                          P(w_im), None, None, None, P(y_re), P(y_im), P(cs), P(ws_f),
+                                          ws_f.numel(), st), "forward")
+
+    def bwd():
+        _lib.check(lib.sparc_scan_backward(
+            ctypes.byref(d), P(eta), P(delta), P(nu_log), P(theta_log), P(w_re), P(w_im), P(y_re), P(y_im),
+            None, None, None, P(cs), P(dy_re), P(dy_im), None, None, P(dw_re), P(dw_im), P(deta), P(ddelta),
+            P(dnu), P(dth), None, None, P(ws_b), ws_b.numel(), st), "backward")
+
+    for _ in range(2):
+        fwd()
+        bwd()
+    steps = max(3, args.steps // 2)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for e0, e1, e2 in ev:
+        e0.record(stream)
+        fwd()
+        e1.record(stream)
+        bwd()
+        e2.record(stream)
+    torch.cuda.synchronize(dev)
+    elapsed = time.perf_counter() - t0
+    fwd_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in ev) / steps
+    bwd_ms = sum(e1.elapsed_time(e2) for _, e1, e2 in ev) / steps
+    bytes_fwd = B * T * (8 * M + 8)
+    bytes_bwd = B * T * (12 * M + 16)
+    ms_step = elapsed * 1e3 / steps
+    del w_re, w_im, dy_re, dy_im, y_re, y_im, dw_re, dw_im, cs
+    torch.cuda.empty_cache()
+    traffic = measured_traffic(COUNTERS_FILE)
+    valu = measured_valu_busy()
+    kf, kb = "mixer_fwd_kernel (writes given)", "mixer_bwd_kernel (writes given)"
+    return {
+        "workload": "P1 chunk scan fwd+bwd (the reference's sparc_chunk_scan), one (eta, delta) per token",
+        "B": B, "T": T, "M": M, "G": 1, "io_dtype": "bf16", "steps": steps,
+        "tokens_per_s": round(B * T * steps / elapsed, 1), "ms_per_step": round(ms_step, 4),
+        "step_frac": round((bytes_fwd + bytes_bwd) / ms_step / 1e6 / HBM_PEAK_GBS, 4),
+        "forward": {"kernel": kf, "avg_launch_ms": round(fwd_ms, 4), "bytes_per_launch": bytes_fwd,
+                    "traffic": traffic.get("mixer_fwd_kernel_p1"), "valu_busy_pct": valu.get("mixer_fwd_kernel_p1"),
+                    "frac": round(bytes_fwd / fwd_ms / 1e6 / HBM_PEAK_GBS, 4)},
+        "backward": {"kernel": kb, "avg_launch_ms": round(bwd_ms, 4), "bytes_per_launch": bytes_bwd,
+                     "traffic": traffic.get("mixer_bwd_kernel_p1"), "valu_busy_pct": valu.get("mixer_bwd_kernel_p1"),
+                     "frac": round(bytes_bwd / bwd_ms / 1e6 / HBM_PEAK_GBS, 4)},
+        "counters_source": COUNTERS_FILE if "mixer_fwd_kernel_p1" in traffic else None,
+    }
+
+
 def bench_cfg5(args, dev):
     """cfg5: a 12-layer stack of SPARC blocks (RMSNorm -> Linear(768 -> 2M) ->
     SPARCMixer -> Linear(2M -> 768), residual; M = 768*16 = 12288), bf16
@@ -538,6 +621,7 @@ def main():
     ap.add_argument("--no-cfg3", action="store_true", help="skip the cfg3 (real, T=65536) report")
     ap.add_argument("--no-cfg5", action="store_true", help="skip the cfg5 (12-layer stack) report")
     ap.add_argument("--no-module", action="store_true", help="skip the module (SPARCMixer) report")
+    ap.add_argument("--no-p1", action="store_true", help="skip the P1 operator (sparc_chunk_scan) report")
     ap.add_argument("--algo", default="auto", choices=["auto", "serial", "chain", "lookback"],
                     help="scan algorithm (auto picks the serial kernels at this shape)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -560,6 +644,7 @@ def main():
         torch.cuda.synchronize(dev)
         del src, dst
     res = bench_scan(args, dev)
+    p1 = None if args.no_p1 else bench_p1(args, dev)
     cfg3 = None if args.no_cfg3 else bench_cfg3(args, dev)
     cfg5 = None if args.no_cfg5 else bench_cfg5(args, dev)
     module = None if args.no_module else bench_module(args, dev)
@@ -613,6 +698,7 @@ def main():
                 "steps": dec["steps"], "bytes_per_step": dec["bytes_per_step"], "GB_s": round(dec["gbs"], 1),
                 "form": "SPARCMixer.step (P1 controls and write from x), bf16 x/y, fp32 state in place"}},
         "module": module,
+        "p1": p1,
         "cfg3": cfg3,
         "cfg5": cfg5,
         "cpu_baseline": cpu,
