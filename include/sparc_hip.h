@@ -70,8 +70,8 @@ enum {
    * a whole chain step by step (no sub-chunk maps, no barriers); for gates
    * shared by the lanes of a group (polar, cartesian, real) and enough chains
    * to give every SIMD a wave; other shapes fall back to CHAIN.  Without a
-   * flag, a P1 scan with G = 1, no segment_pos, no RESET_FIRST, M a multiple
-   * of 4 and 8-byte aligned planes runs on the one-wave-per-chain fused
+   * flag, a P1 scan with G = 1 (resets included), M a multiple of 4 and
+   * 8-byte aligned planes runs on the one-wave-per-chain fused
    * kernels of the module path (time segments for few chains); its backward
    * too when y_re/y_im are given without RELU_OUTPUT.  Same results up to
    * float rounding; the saved chunk states of any feed any backward. */

@@ -76,7 +76,9 @@ template <typename IO> constexpr bool kRoundWrite = SPARC_MIXER_ROUND_WRITE && s
 //            sparc_scan_forward / _backward with one gate pair per token).
 //   kRelu:   as kPlanes, but y = relu(cat(h_re, h_im)) out instead of the
 //            states (forward only).
-enum : int { kModule = 0, kPlanes = 1, kRelu = 2 };
+//   | kReset: kPlanes or kRelu with reset steps (segment_pos[b, t] == 0, or
+//            step 0 with reset_first): the transition there is 0.
+enum : int { kModule = 0, kPlanes = 1, kRelu = 2, kReset = 4 };
 constexpr int kStateChunk = 64;  // steps per saved chunk state (sparc_scan_chunk_length)
 // A lane byte offset past every buffer resource of these kernels (each spans
 // less than 2^31 bytes): the hardware range check drops a store through it.
@@ -123,7 +125,20 @@ struct Args {
   float* dh0_re;
   float* dh0_im;
   float* chunk_state;
+  const int32_t* segpos;  // [B,T] or NULL (kReset)
+  int reset_first;        // kReset without segpos: step 0 resets
 };
+
+// kReset: whether step t of batch row b keeps its transition (1) or resets
+// (0).  segment_pos is read through a buffer resource that is empty without
+// it (no load under a branch); segment_pos wins over reset_first.
+__device__ __forceinline__ int p1_keep(const Args& a, int b, int t) {
+  const bool sp = a.segpos != nullptr;
+  const __amdgpu_buffer_rsrc_t r =
+      make_rsrc(sp ? static_cast<const void*>(a.segpos + static_cast<int64_t>(b) * a.T) : a.consts, sp ? a.T * 4u : 0u);
+  const int v = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(r, static_cast<uint32_t>(t) * 4u, 0, CPOL_DEFAULT));
+  return sp ? (v != 0) : !(a.reset_first && t == 0);
+}
 
 // Chain index of this workgroup -> (batch row, mode block, segment, steps).
 struct ChainPos {
@@ -300,6 +315,22 @@ __device__ __forceinline__ void p1_block_transitions(const ModeConsts<V, BWD>& m
     }
 }
 
+// Reset steps of a block (lane s of kv: 0 where step s resets): a := 0.  The
+// transition gradients at such a step then vanish with it, and so does the
+// adjoint carried past it.
+template <int S, int V>
+__device__ __forceinline__ void p1_block_resets(int kv, float (&ar)[S][V], float (&ai)[S][V]) {
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const bool keep = __builtin_amdgcn_readlane(kv, s) != 0;  // wave-uniform
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      ar[s][v] = keep ? ar[s][v] : 0.0f;
+      ai[s][v] = keep ? ai[s][v] : 0.0f;
+    }
+  }
+}
+
 // Per-step values of the P1 transition and write of one mode.
 struct StepMode {
   float em, rho, ar, ai, gain, sg;
@@ -332,8 +363,11 @@ mixer_fwd_kernel(Args a) {
   using RawT = typename Raw<IO, V>::T;
   constexpr int ESZ = sizeof(IO);
   constexpr int MB = 64 * V;
-  constexpr bool GW = MODE != kModule;  // the writes are given
+  constexpr int CM = MODE & 3;             // the chain mode without kReset
+  constexpr bool RST = (MODE & kReset) != 0;
+  constexpr bool GW = CM != kModule;  // the writes are given
   static_assert(kStateChunk % kS == 0, "blocks must tile the saved-state chunks");
+  static_assert(GW || !RST, "resets in the P1 scan only");
   const int lane = threadIdx.x;
   const ChainPos cp = chain_pos(a);
   const int b = cp.b, mb = cp.mb, t_begin = cp.t_begin, t_end = cp.t_end;
@@ -394,6 +428,7 @@ mixer_fwd_kernel(Args a) {
 
   RawT xr[2][kS], xi[2][kS];
   float ev[2], dv[2];  // lane s < kS: eta, delta of step s of the block
+  int kv[2];           // RST: lane s < kS: whether step s keeps its transition
   auto load_block = [&](auto h_tag, int k) {
     constexpr int h = decltype(h_tag)::value;
     const int t0 = t_begin + k * kS;
@@ -424,6 +459,7 @@ mixer_fwd_kernel(Args a) {
     const int64_t ti = row0 + t0 + (sl <= last ? sl : last);
     ev[h] = a.eta[ti];
     dv[h] = a.delta[ti];
+    if constexpr (RST) kv[h] = p1_keep(a, b, t0 + (sl <= last ? sl : last));
   };
 
   // One block of kS steps in two phases: (A) every step's transition and
@@ -436,6 +472,7 @@ mixer_fwd_kernel(Args a) {
     float ar[kS][V], ai[kS][V], wr[kS][V], wi[kS][V];
     const float ee = fast_exp(ev[h]);  // lane s: e^eta of step s
     if constexpr (GW) p1_block_transitions<kS, V>(mc, ee, dv[h], ar, ai);
+    if constexpr (RST) p1_block_resets<kS, V>(kv[h], ar, ai);
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
       const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
@@ -480,7 +517,7 @@ mixer_fwd_kernel(Args a) {
         }
       }
       if constexpr (SUMMARY) continue;
-      if constexpr (MODE != kPlanes) {  // y = relu(cat(h_re, h_im))
+      if constexpr (CM != kPlanes) {  // y = relu(cat(h_re, h_im))
         float rr[V], ri[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) { rr[v] = fmaxf(hr[v], 0.0f); ri[v] = fmaxf(hi[v], 0.0f); }
@@ -488,7 +525,7 @@ mixer_fwd_kernel(Args a) {
         buf_store<RawT, CPOL_NT>(pack<IO, V>(rr), ry, lane_st, yo);
         buf_store<RawT, CPOL_NT>(pack<IO, V>(ri), ry, lane_st, yo + half_x);
       }
-      if constexpr (MODE != kRelu) {  // the states
+      if constexpr (CM != kRelu) {  // the states
         const uint32_t ho = static_cast<uint32_t>(s) * half_x;
         buf_store<RawT, CPOL_NT>(pack<IO, V>(hr), rhr, lane_st, ho);
         buf_store<RawT, CPOL_NT>(pack<IO, V>(hi), rhi, lane_st, ho);
@@ -562,8 +599,11 @@ mixer_bwd_kernel(Args a) {
   using RawT = typename Raw<IO, V>::T;
   constexpr int ESZ = sizeof(IO);
   constexpr int MB = 64 * V;
-  constexpr bool GW = MODE == kPlanes;  // the writes are given: dw out, no relu mask
-  static_assert(MODE != kRelu, "the backward of the relu output recomputes states (scan.hip)");
+  constexpr int CM = MODE & 3;             // the chain mode without kReset
+  constexpr bool RST = (MODE & kReset) != 0;
+  constexpr bool GW = CM == kPlanes;  // the writes are given: dw out, no relu mask
+  static_assert(CM != kRelu, "the backward of the relu output recomputes states (scan.hip)");
+  static_assert(GW || !RST, "resets in the P1 scan only");
   const int lane = threadIdx.x;
   const ChainPos cp = chain_pos(a);
   const int b = cp.b, mb = cp.mb, t_begin = cp.t_begin, t_end = cp.t_end;
@@ -633,6 +673,7 @@ mixer_bwd_kernel(Args a) {
 
   RawT dr[2][kS], di[2][kS], xr[2][kS], xi[2][kS], pr[2][kS], pi[2][kS];
   float ev[2], dv[2];
+  int kv[2];  // RST: lane s < kS: whether step s keeps its transition
   // block k: steps t0 .. t0+kS-1; the previous states are rows t-1 (row 0
   // for t = 0, zeroed in the step)
   auto load_block = [&](auto h_tag, int k) {
@@ -680,6 +721,7 @@ mixer_bwd_kernel(Args a) {
     const int64_t ti = row0 + t0 + (sl <= last ? sl : last);
     ev[h] = a.eta[ti];
     dv[h] = a.delta[ti];
+    if constexpr (RST) kv[h] = p1_keep(a, b, t0 + (sl <= last ? sl : last));
   };
 
   // One block of kS steps, in phases: (A) every step's transition
@@ -697,6 +739,7 @@ mixer_bwd_kernel(Args a) {
     float qar[kS][V], qai[kS][V], qem[kS][V];
     const float ee = fast_exp(ev[h]);  // lane s: e^eta of step s
     p1_block_transitions<kS, V>(mc, ee, dv[h], qar, qai, qem);
+    if constexpr (RST) p1_block_resets<kS, V>(kv[h], qar, qai);
     // (B) the adjoint
     float lr[kS][V], li[kS][V];
 #pragma unroll
@@ -1222,7 +1265,7 @@ template <typename IO, int V, int MODE = kModule>
 void run_fwd(const Args& a, hipStream_t st) {
   if (a.n_seg > 1) {  // maps of segments 0 .. n-2, then the entering states (from h0, if any)
     // (the summaries read the writes only: kRelu shares the kPlanes kernel)
-    launch_fwd<IO, V, true, MODE == kModule ? kModule : kPlanes>(a, a.n_seg - 1, st);
+    launch_fwd<IO, V, true, (MODE & 3) == kModule ? kModule : (kPlanes | (MODE & kReset))>(a, a.n_seg - 1, st);
     hipLaunchKernelGGL(mixer_seg_carry_kernel, dim3(static_cast<unsigned>(a.B) * a.M), dim3(64), 0, st, a.B, a.M,
                        a.n_seg, 0, a.seg_sum, a.h0_re, a.h0_im, a.seg_state);
   }
@@ -1357,7 +1400,7 @@ using namespace sparc::mix;
 bool p1_fused_shape(const sparc_scan_desc* d) {
   constexpr int32_t forced = SPARC_FLAG_ALGO_LOOKBACK | SPARC_FLAG_ALGO_CHAIN | SPARC_FLAG_ALGO_SERIAL;
   if (!SPARC_P1_FUSED || !d || d->transition != SPARC_TRANSITION_P1 || d->groups != 1) return false;
-  if (d->flags & (SPARC_FLAG_RESET_FIRST | forced)) return false;
+  if (d->flags & forced) return false;
   if (d->gate_dtype != SPARC_F32) return false;
   return check_shape(d->batch, d->length, d->modes, d->io_dtype) == SPARC_OK;
 }
@@ -1367,10 +1410,28 @@ size_t p1_fused_workspace_bytes(const sparc_scan_desc* d, int direction) {
   return layout(d->batch, d->length, d->modes, direction, true).total;
 }
 
+// the launches of one chain mode for the I/O type and modes per lane
+template <int MODE>
+void run_fwd_mode(const Args& a, bool bf, int V, hipStream_t st) {
+  if (bf) {
+    if (V == 2) run_fwd<sparc::bf16, 2, MODE>(a, st); else run_fwd<sparc::bf16, 1, MODE>(a, st);
+  } else {
+    if (V == 2) run_fwd<float, 2, MODE>(a, st); else run_fwd<float, 1, MODE>(a, st);
+  }
+}
+template <int MODE>
+void run_bwd_mode(const Args& a, bool bf, int V, hipStream_t st) {
+  if (bf) {
+    if (V == 2) run_bwd<sparc::bf16, 2, MODE>(a, st); else run_bwd<sparc::bf16, 1, MODE>(a, st);
+  } else {
+    if (V == 2) run_bwd<float, 2, MODE>(a, st); else run_bwd<float, 1, MODE>(a, st);
+  }
+}
+
 sparc_status p1_fused_forward(const sparc_scan_desc* d, const float* eta, const float* delta,
                               const float* nu_log, const float* theta_log, const void* w_re, const void* w_im,
-                              const float* h0_re, const float* h0_im, void* y_re, void* y_im,
-                              float* chunk_state, void* workspace, size_t workspace_bytes,
+                              const float* h0_re, const float* h0_im, const int32_t* segment_pos, void* y_re,
+                              void* y_im, float* chunk_state, void* workspace, size_t workspace_bytes,
                               sparc_stream_t stream) {
   if (!p1_fused_shape(d) || d->length <= 0) return fail(SPARC_EINVAL, "p1 fused forward: shape");
   const Layout l = layout(d->batch, d->length, d->modes, 0, true);
@@ -1389,6 +1450,9 @@ sparc_status p1_fused_forward(const sparc_scan_desc* d, const float* eta, const 
   a.n_mb = l.n_mb;
   a.consts = consts; a.eta = eta; a.delta = delta;
   a.w_re = w_re; a.w_im = w_im; a.h0_re = h0_re; a.h0_im = h0_im; a.chunk_state = chunk_state;
+  a.segpos = segment_pos;
+  a.reset_first = (d->flags & SPARC_FLAG_RESET_FIRST) != 0;
+  const bool reset = segment_pos != nullptr || a.reset_first;
   if (relu) {
     a.y = y_re;
   } else {
@@ -1399,23 +1463,21 @@ sparc_status p1_fused_forward(const sparc_scan_desc* d, const float* eta, const 
   a.seg_sum = reinterpret_cast<float*>(ws + l.seg_sum);
   a.seg_state = reinterpret_cast<float*>(ws + l.seg_state);
   const bool bf = d->io_dtype == SPARC_BF16;
-  if (relu) {
-    if (bf) { if (l.V == 2) run_fwd<sparc::bf16, 2, kRelu>(a, st); else run_fwd<sparc::bf16, 1, kRelu>(a, st); }
-    else { if (l.V == 2) run_fwd<float, 2, kRelu>(a, st); else run_fwd<float, 1, kRelu>(a, st); }
-  } else {
-    if (bf) { if (l.V == 2) run_fwd<sparc::bf16, 2, kPlanes>(a, st); else run_fwd<sparc::bf16, 1, kPlanes>(a, st); }
-    else { if (l.V == 2) run_fwd<float, 2, kPlanes>(a, st); else run_fwd<float, 1, kPlanes>(a, st); }
-  }
+  if (relu && reset) run_fwd_mode<kRelu | kReset>(a, bf, l.V, st);
+  else if (relu) run_fwd_mode<kRelu>(a, bf, l.V, st);
+  else if (reset) run_fwd_mode<kPlanes | kReset>(a, bf, l.V, st);
+  else run_fwd_mode<kPlanes>(a, bf, l.V, st);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "p1 fused forward: %s", hipGetErrorString(e));
 }
 
 sparc_status p1_fused_backward(const sparc_scan_desc* d, const float* eta, const float* delta,
                                const float* nu_log, const float* theta_log, const void* y_re, const void* y_im,
-                               const float* h0_re, const float* h0_im, const void* dy_re, const void* dy_im,
-                               const float* dlast_re, const float* dlast_im, void* dw_re, void* dw_im,
-                               float* deta, float* ddelta, float* dnu_log, float* dtheta_log, float* dh0_re,
-                               float* dh0_im, void* workspace, size_t workspace_bytes, sparc_stream_t stream) {
+                               const float* h0_re, const float* h0_im, const int32_t* segment_pos,
+                               const void* dy_re, const void* dy_im, const float* dlast_re, const float* dlast_im,
+                               void* dw_re, void* dw_im, float* deta, float* ddelta, float* dnu_log,
+                               float* dtheta_log, float* dh0_re, float* dh0_im, void* workspace,
+                               size_t workspace_bytes, sparc_stream_t stream) {
   if (!p1_fused_shape(d) || d->length <= 0 || (d->flags & SPARC_FLAG_RELU_OUTPUT))
     return fail(SPARC_EINVAL, "p1 fused backward: shape");
   const Layout l = layout(d->batch, d->length, d->modes, 1, true);
@@ -1442,11 +1504,11 @@ sparc_status p1_fused_backward(const sparc_scan_desc* d, const float* eta, const
   a.n_seg = l.n_seg; a.t_seg = l.t_seg; a.seg_lo = 0;
   a.seg_sum = reinterpret_cast<float*>(ws + l.seg_sum);
   a.seg_state = reinterpret_cast<float*>(ws + l.seg_state);
-  if (d->io_dtype == SPARC_BF16) {
-    if (l.V == 2) run_bwd<sparc::bf16, 2, kPlanes>(a, st); else run_bwd<sparc::bf16, 1, kPlanes>(a, st);
-  } else {
-    if (l.V == 2) run_bwd<float, 2, kPlanes>(a, st); else run_bwd<float, 1, kPlanes>(a, st);
-  }
+  a.segpos = segment_pos;
+  a.reset_first = (d->flags & SPARC_FLAG_RESET_FIRST) != 0;
+  const bool bf = d->io_dtype == SPARC_BF16;
+  if (segment_pos || a.reset_first) run_bwd_mode<kPlanes | kReset>(a, bf, l.V, st);
+  else run_bwd_mode<kPlanes>(a, bf, l.V, st);
   // d eta, d delta per token over the mode blocks; d nu_log, d theta_log per
   // mode over the (batch row, segment) partial rows
   if (sparc_status s = sparc_column_sum(l.n_mb, l.R, part_tok, deta, 0, stream)) return s;

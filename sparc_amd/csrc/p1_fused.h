@@ -12,9 +12,10 @@
 
 namespace sparc {
 
-// Whether a descriptor can take these kernels: P1, G = 1, no reset_first,
-// no forced algorithm, M a multiple of 4, sizes within the kernels' limits.
-// Segment resets and pointer alignment are checked by the caller.
+// Whether a descriptor can take these kernels: P1, G = 1, no forced
+// algorithm, M a multiple of 4, sizes within the kernels' limits (segment
+// resets and reset_first included).  Pointer alignment is checked by the
+// caller.
 bool p1_fused_shape(const sparc_scan_desc* d);
 
 // Workspace bytes of p1_fused_forward (direction 0) / _backward (1).
@@ -25,17 +26,18 @@ size_t p1_fused_workspace_bytes(const sparc_scan_desc* d, int direction);
 // [B][ceil(T/64)][M][2], as sparc_scan_forward.  T > 0.
 sparc_status p1_fused_forward(const sparc_scan_desc* d, const float* eta, const float* delta,
                               const float* nu_log, const float* theta_log, const void* w_re, const void* w_im,
-                              const float* h0_re, const float* h0_im, void* y_re, void* y_im,
-                              float* chunk_state, void* workspace, size_t workspace_bytes,
+                              const float* h0_re, const float* h0_im, const int32_t* segment_pos, void* y_re,
+                              void* y_im, float* chunk_state, void* workspace, size_t workspace_bytes,
                               sparc_stream_t stream);
 
 // Backward from the forward's states y_re, y_im (no relu output).  T > 0.
 sparc_status p1_fused_backward(const sparc_scan_desc* d, const float* eta, const float* delta,
                                const float* nu_log, const float* theta_log, const void* y_re, const void* y_im,
-                               const float* h0_re, const float* h0_im, const void* dy_re, const void* dy_im,
-                               const float* dlast_re, const float* dlast_im, void* dw_re, void* dw_im,
-                               float* deta, float* ddelta, float* dnu_log, float* dtheta_log, float* dh0_re,
-                               float* dh0_im, void* workspace, size_t workspace_bytes, sparc_stream_t stream);
+                               const float* h0_re, const float* h0_im, const int32_t* segment_pos,
+                               const void* dy_re, const void* dy_im, const float* dlast_re, const float* dlast_im,
+                               void* dw_re, void* dw_im, float* deta, float* ddelta, float* dnu_log,
+                               float* dtheta_log, float* dh0_re, float* dh0_im, void* workspace,
+                               size_t workspace_bytes, sparc_stream_t stream);
 
 }  // namespace sparc
 

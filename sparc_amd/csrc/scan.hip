@@ -3675,12 +3675,11 @@ size_t sparc_scan_workspace_bytes(const sparc_scan_desc* d, int direction) {
 
 // The P1 scan with one gate pair per token takes the one-wave-per-chain
 // kernels of the fused module path (p1_fused.h) when nothing needs the
-// general kernels: no segment resets, aligned planes, a large enough
-// workspace.  Otherwise the general kernels run.
-static bool p1_fused_route(const sparc_scan_desc* d, int direction, const int32_t* segment_pos,
-                           const void* const* planes, int n_planes, const float* chunk_state,
-                           size_t workspace_bytes) {
-  if (segment_pos || !sparc::p1_fused_shape(d)) return false;
+// general kernels: aligned planes, a large enough workspace.  Otherwise the
+// general kernels run.
+static bool p1_fused_route(const sparc_scan_desc* d, int direction, const void* const* planes, int n_planes,
+                           const float* chunk_state, size_t workspace_bytes) {
+  if (!sparc::p1_fused_shape(d)) return false;
   if (workspace_bytes < sparc::p1_fused_workspace_bytes(d, direction)) return false;
   for (int i = 0; i < n_planes; ++i)
     if (!aligned(planes[i], 8)) return false;
@@ -3767,10 +3766,10 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, con
   if (!aligned(chunk_state, 8 * pl.V)) return fail(SPARC_EINVAL, "chunk_state must be %d-byte aligned", 8 * pl.V);
   {
     const void* fp[] = {w_re, w_im, y_re, y_im, h0_re, h0_im};
-    if (p1_fused_route(d, 0, segment_pos, fp, 6, chunk_state, workspace_bytes))
+    if (p1_fused_route(d, 0, fp, 6, chunk_state, workspace_bytes))
       return sparc::p1_fused_forward(d, static_cast<const float*>(gate0), static_cast<const float*>(gate1), nu_log,
-                                     theta_log, w_re, w_im, h0_re, h0_im, y_re, relu ? nullptr : y_im, chunk_state,
-                                     workspace, workspace_bytes, stream);
+                                     theta_log, w_re, w_im, h0_re, h0_im, segment_pos, y_re, relu ? nullptr : y_im,
+                                     chunk_state, workspace, workspace_bytes, stream);
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (!pl.chain)
@@ -3864,11 +3863,12 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
   }
   if (saved) {  // P1 from the saved states: the fused kernels, when they apply
     const void* fp[] = {y_re, y_im, dy_re, dy_im, dw_re, dw_im, h0_re, h0_im, dh0_re, dh0_im};
-    if (p1_fused_route(d, 1, segment_pos, fp, 10, chunk_state, workspace_bytes))
+    if (p1_fused_route(d, 1, fp, 10, chunk_state, workspace_bytes))
       return sparc::p1_fused_backward(d, static_cast<const float*>(gate0), static_cast<const float*>(gate1), nu_log,
-                                      theta_log, y_re, y_im, h0_re, h0_im, dy_re, dy_im, dlast_re, dlast_im, dw_re,
-                                      dw_im, static_cast<float*>(dgate0), static_cast<float*>(dgate1), dnu_log,
-                                      dtheta_log, dh0_re, dh0_im, workspace, workspace_bytes, stream);
+                                      theta_log, y_re, y_im, h0_re, h0_im, segment_pos, dy_re, dy_im, dlast_re,
+                                      dlast_im, dw_re, dw_im, static_cast<float*>(dgate0),
+                                      static_cast<float*>(dgate1), dnu_log, dtheta_log, dh0_re, dh0_im, workspace,
+                                      workspace_bytes, stream);
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (!pl.chain)

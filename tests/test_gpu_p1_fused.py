@@ -1,7 +1,8 @@
 """GPU parity of the P1 scan with one gate pair per token (G = 1), which
 sparc_scan_forward / sparc_scan_backward run on the one-wave-per-chain
 kernels of the fused module path (writes given, states or relu(cat) out,
-chunk states every 64 steps; few chains split time into segments).
+chunk states every 64 steps; segment resets and reset_first; few chains
+split time into segments).
 
 Values, final states and every gradient (eta, delta, nu_log, theta_log, the
 writes, h0) against the float64 oracle, to 1e-4 (fp32 I/O) or 2e-2 (bf16
@@ -32,6 +33,14 @@ CASES = [
     ("segments_relu_h0_f32", 1, 1100, 64, F32, dict(relu=True, h0=True)),
     # 1280 chains of 2 modes per lane in the forward
     ("two_modes_per_lane_bf16", 10, 9, 16384, BF16, dict(h0=True, dlast=True)),
+    # reset steps (segment_pos == 0: a := 0), reset_first, and both (segment_pos wins)
+    ("resets_h0_f32", 2, 200, 256, F32, dict(h0=True, dlast=True, seg=True)),
+    ("resets_bf16", 2, 150, 128, BF16, dict(seg=True)),
+    ("reset_first_h0_f32", 2, 80, 128, F32, dict(h0=True, dlast=True, reset_first=True)),
+    ("resets_and_reset_first_f32", 2, 90, 256, F32, dict(h0=True, seg=True, reset_first=True)),
+    ("resets_relu_f32", 2, 130, 128, F32, dict(h0=True, seg=True, relu=True)),
+    ("resets_segments_h0_f32", 1, 3000, 64, F32, dict(h0=True, dlast=True, seg=True)),
+    ("reset_first_segments_bf16", 2, 2500, 128, BF16, dict(h0=True, dlast=True, reset_first=True)),
 ]
 
 
