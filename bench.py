@@ -625,7 +625,7 @@ def main():
     ap.add_argument("--algo", default="auto", choices=["auto", "serial", "chain", "lookback"],
                     help="scan algorithm (auto picks the serial kernels at this shape)")
     ap.add_argument("--copy-probe", action="store_true",
-                    help="first copy 1 GiB device-to-device (a kernel of known traffic, "
+                    help="first copy, sum and fill 1 GiB (kernels of known traffic, "
                          "to calibrate the FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -638,11 +638,17 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda", 0)
     if args.copy_probe:
+        # kernels of known traffic for the FETCH_SIZE / WRITE_SIZE factors:
+        # a 1 GiB copy (1 GiB read, 1 GiB written), a 1 GiB sum (read only)
+        # and a 1 GiB fill (written only)
         src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)  # 1 GiB
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize(dev)
-        del src, dst
+        total = src.sum(dtype=torch.float32)
+        dst.fill_(2.0)
+        torch.cuda.synchronize(dev)
+        del src, dst, total
     res = bench_scan(args, dev)
     p1 = None if args.no_p1 else bench_p1(args, dev)
     cfg3 = None if args.no_cfg3 else bench_cfg3(args, dev)
