@@ -133,6 +133,63 @@ def test_cfg2_full_size_sampled_groups():
     assert rel_err(pick(gr["dg1"], gsel), d_phi) <= tol
 
 
+def test_cfg2_shape_p1_operator_full_size():
+    """The reference's own operator (P1, one (eta, delta) per token) at the
+    cfg2 shape, bf16 writes: the fused route (the automatic choice) against
+    the float64 oracle on three blocks of 16 modes over every row and step
+    (outputs, final states, write gradients and the nu_log / theta_log
+    gradients, which are complete sums per mode), and against the general
+    chain kernels (ALGO_CHAIN) on the per-token eta / delta gradients, which
+    sum over all 16384 modes."""
+    print("[case] P1 operator full size B=8 T=4096 M=16384 G=1 bf16", flush=True)
+    B, T, M = 8, 4096, 16384
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(3)
+    eta = (O.LOG16 * torch.tanh(0.5 * torch.randn(B, T, 1, device=dev, generator=g))).float()
+    delta = (O.HALF_PI * torch.tanh(torch.randn(B, T, 1, device=dev, generator=g))).float()
+    p = O.init_params(2 * M, generator=torch.Generator().manual_seed(3))
+    nu_log, theta_log = p.nu_log.float().to(dev), p.theta_log.float().to(dev)
+    w_re, w_im, dy_re, dy_im = (torch.randn(B, T, M, device=dev, generator=g, dtype=torch.bfloat16)
+                                for _ in range(4))
+
+    def run(algorithm):
+        ops.set_algorithm(algorithm)
+        try:
+            y_re, y_im, cs = ops.scan_forward_raw("p1", eta, delta, w_re, w_im, nu_log, theta_log)
+            gr = ops.scan_backward_raw("p1", eta, delta, w_re, w_im, cs, dy_re, dy_im, nu_log, theta_log,
+                                       y_re=y_re, y_im=y_im)
+            torch.cuda.synchronize()
+            return y_re, y_im, cs, gr
+        finally:
+            ops.set_algorithm("auto")
+
+    y_re, y_im, cs, gr = run("auto")
+    gc = run("chain")[3]
+    tol = 2e-2
+    assert rel_err(gr["dg0"], gc["dg0"]) <= tol, "d eta against the chain kernels"
+    assert rel_err(gr["dg1"], gc["dg1"]) <= tol, "d delta against the chain kernels"
+    del gc
+    modes = torch.cat([torch.arange(0, 16), torch.arange(8192, 8208), torch.arange(M - 16, M)]).to(dev)
+
+    def pick(t):
+        return t[:, :, modes].double().cpu()
+
+    leaves = [eta.double().cpu(), delta.double().cpu(), pick(w_re), pick(w_im),
+              nu_log[modes].double().cpu(), theta_log[modes].double().cpu()]
+    leaves = [v.clone().requires_grad_() for v in leaves]
+    (hr, hi), last = O.grouped_scan_forward("p1", leaves[0], leaves[1], leaves[2], leaves[3], leaves[4], leaves[5])
+    loss = (hr * pick(dy_re)).sum() + (hi * pick(dy_im)).sum()
+    _, _, d_wr, d_wi, d_nu, d_th = torch.autograd.grad(loss, leaves)
+    assert rel_err(pick(y_re), hr) <= tol
+    assert rel_err(pick(y_im), hi) <= tol
+    assert rel_err(cs[:, -1][:, modes, 0], last[0]) <= 1e-4  # fp32 state after T steps
+    assert rel_err(cs[:, -1][:, modes, 1], last[1]) <= 1e-4
+    assert rel_err(pick(gr["dw_re"]), d_wr) <= tol
+    assert rel_err(pick(gr["dw_im"]), d_wi) <= tol
+    assert rel_err(gr["dnu"][modes], d_nu) <= tol
+    assert rel_err(gr["dth"][modes], d_th) <= tol
+
+
 # ---------------------------------------------------------------------------
 # cfg3: real scan, B=4, T=65536, D=512, N=8, fp32, |a| in [0.95, 0.9999]
 # ---------------------------------------------------------------------------
