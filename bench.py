@@ -99,11 +99,13 @@ def scan_case(B, T, M, G, dev, seed=0):
     return r, phi, w_re, w_im, dy_re, dy_im
 
 
-def bench_scan(args, dev):
+def bench_scan(args, dev, B=8, T=4096, D=1024, N=16, steps=None):
+    """Polar scan fwd+bwd (bf16 I/O, gates shared per channel) at one shape:
+    the headline cfg2 shape by default."""
     from sparc_amd import _lib
     lib = _lib.load()
-    B, T, D, N = 8, 4096, 1024, 16
     M, G = D * N, D
+    n_steps = steps or args.steps
     r, phi, w_re, w_im, dy_re, dy_im = scan_case(B, T, M, G, dev)
     d = _lib.ScanDesc(B, T, M, G, _lib.TRANSITIONS["polar"], _lib.SPARC_BF16, _lib.SPARC_BF16,
                       _lib.ALGO_FLAGS[args.algo])
@@ -137,7 +139,7 @@ def bench_scan(args, dev):
         raise RuntimeError("a look-back wait hit its bound during warmup")
 
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-           torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+           torch.cuda.Event(enable_timing=True)) for _ in range(n_steps)]
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
     for e0, e1, e2 in ev:
@@ -148,8 +150,8 @@ def bench_scan(args, dev):
         e2.record(stream)
     torch.cuda.synchronize(dev)
     elapsed = time.perf_counter() - t0
-    fwd_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in ev) / args.steps
-    bwd_ms = sum(e1.elapsed_time(e2) for _, e1, e2 in ev) / args.steps
+    fwd_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in ev) / n_steps
+    bwd_ms = sum(e1.elapsed_time(e2) for _, e1, e2 in ev) / n_steps
     if lib.sparc_scan_workspace_error(P(ws_f), st) or lib.sparc_scan_workspace_error(P(ws_b), st):
         raise RuntimeError("a look-back wait hit its bound during the timed region")
 
@@ -157,10 +159,10 @@ def bench_scan(args, dev):
     mode_steps, group_steps = B * T * M, B * T * G
     bytes_fwd = mode_steps * 8 + group_steps * 4
     bytes_bwd = mode_steps * 12 + group_steps * 8
-    ms_step = elapsed * 1e3 / args.steps
+    ms_step = elapsed * 1e3 / n_steps
     return dict(
         B=B, T=T, D=D, N=N, M=M, G=G, ms_step=ms_step,
-        tokens_per_s=tokens * args.steps / elapsed,
+        tokens_per_s=tokens * n_steps / elapsed,
         fwd_ms=fwd_ms, bwd_ms=bwd_ms,
         bytes_fwd=bytes_fwd, bytes_bwd=bytes_bwd,
         fwd_gbs=bytes_fwd / fwd_ms / 1e6, bwd_gbs=bytes_bwd / bwd_ms / 1e6,
@@ -650,6 +652,9 @@ def main():
         torch.cuda.synchronize(dev)
         del src, dst, total
     res = bench_scan(args, dev)
+    # few long chains: 8 chains of 256 modes, which the serial kernels split
+    # into time segments (the reference's long-context regime)
+    few = bench_scan(args, dev, B=1, T=65536, D=128, N=16, steps=10)
     p1 = None if args.no_p1 else bench_p1(args, dev)
     cfg3 = None if args.no_cfg3 else bench_cfg3(args, dev)
     cfg5 = None if args.no_cfg5 else bench_cfg5(args, dev)
@@ -703,6 +708,16 @@ def main():
                 "us_per_step": round(dec["us_per_step"], 2), "tokens_per_s": round(dec["tokens_per_s"], 1),
                 "steps": dec["steps"], "bytes_per_step": dec["bytes_per_step"], "GB_s": round(dec["gbs"], 1),
                 "form": "SPARCMixer.step (P1 controls and write from x), bf16 x/y, fp32 state in place"}},
+        "few_chains_scan": {
+            "workload": "complex chunked scan fwd+bwd, few long chains (polar, bf16 I/O, fp32 state)",
+            "B": few["B"], "T": few["T"], "D": few["D"], "N": few["N"], "M": few["M"], "G": few["G"],
+            "ms_per_step": round(few["ms_step"], 4), "tokens_per_s": round(few["tokens_per_s"], 1),
+            "bytes_per_step": few["bytes_fwd"] + few["bytes_bwd"],
+            "forward": {"avg_launch_ms": round(few["fwd_ms"], 4), "bytes_per_launch": few["bytes_fwd"],
+                        "frac": round(few["fwd_gbs"] / HBM_PEAK_GBS, 4)},
+            "backward": {"avg_launch_ms": round(few["bwd_ms"], 4), "bytes_per_launch": few["bytes_bwd"],
+                         "frac": round(few["bwd_gbs"] / HBM_PEAK_GBS, 4)},
+            "step_frac": round(few["step_gbs"] / HBM_PEAK_GBS, 4)},
         "module": module,
         "p1": p1,
         "cfg3": cfg3,

@@ -26,10 +26,17 @@
 // sparc_mixer_scan_forward / _backward run 1 + 3 / 4 + 5 (the controls are
 // the caller's); sparc_controls_forward / _backward run 2 / 6 alone over rows
 // of any width that is a multiple of 8.
+// The P1 scan of sparc_scan_forward / _backward with one (eta, delta) per
+// token runs 1 + 3 / 4 + 5 in another chain mode (p1_fused.h): the writes
+// given instead of x, the states (or relu(cat)) and the chunk states out,
+// reset steps; backward dw instead of dx and the transition gradients only.
+// Few chains split time into segments (summary pass, carry, replay) in
+// every mode.
 //
 // Reference replaced: make_controls / make_scan_inputs / _latest_write_forward
 // (sparc-kernal/forward/control.py:129-195), _SPARCChunkScan forward and
-// backward (sparc-kernal/backward/scan.py:1126-1640), the output epilogue
+// backward (sparc-kernal/backward/scan.py:1126-1640) and, with resets,
+// _SPARCTiledSerialScan (:971-1070), the output epilogue
 // (sparc-kernal/forward/scan.py:1598-1603), _latest_write_backward and
 // _LatestSPARCWrite (sparc-kernal/backward/control.py:10-137).
 
@@ -1396,6 +1403,15 @@ bool params_ok(const float* a, const float* b, const float* c, const float* d, c
 // ---------------------------------------------------------------------------
 namespace sparc {
 using namespace sparc::mix;
+
+sparc_status seg_carry(int64_t B, int64_t M, int n_seg, int reverse, const float* seg_sum, const float* init_re,
+                       const float* init_im, float* seg_state, sparc_stream_t stream) {
+  if (B <= 0 || M <= 0 || n_seg < 1 || B * M > INT32_MAX) return fail(SPARC_EINVAL, "seg_carry: shape");
+  hipLaunchKernelGGL(mixer_seg_carry_kernel, dim3(static_cast<unsigned>(B * M)), dim3(64), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<int>(B), static_cast<int>(M), n_seg, reverse,
+                     seg_sum, init_re, init_im, seg_state);
+  return SPARC_OK;  // a launch error stays for the caller's hipGetLastError
+}
 
 bool p1_fused_shape(const sparc_scan_desc* d) {
   constexpr int32_t forced = SPARC_FLAG_ALGO_LOOKBACK | SPARC_FLAG_ALGO_CHAIN | SPARC_FLAG_ALGO_SERIAL;

@@ -1,7 +1,8 @@
 // The P1 scan of sparc_scan_forward / sparc_scan_backward with one gate pair
 // (eta, delta) per token, run on the one-wave-per-chain kernels of the fused
-// module path (mixer.hip) with the writes given instead of computed from x.
-// Declared here for scan.hip (the C ABI), defined in mixer.hip.
+// module path (mixer.hip) with the writes given instead of computed from x;
+// and the carry across time segments that the serial scan kernels share with
+// them.  Declared here for scan.hip (the C ABI), defined in mixer.hip.
 #ifndef SPARC_P1_FUSED_H
 #define SPARC_P1_FUSED_H
 
@@ -38,6 +39,16 @@ sparc_status p1_fused_backward(const sparc_scan_desc* d, const float* eta, const
                                void* dw_re, void* dw_im, float* deta, float* ddelta, float* dnu_log,
                                float* dtheta_log, float* dh0_re, float* dh0_im, void* workspace,
                                size_t workspace_bytes, sparc_stream_t stream);
+
+// The carry across time segments of the scan kernels (mixer.hip's
+// mixer_seg_carry_kernel): from each segment's map (P, Q) in seg_sum
+// [B][n_seg][M][4], the state (reverse = 0, from init = h0 or zero) or the
+// adjoint (reverse = 1, from init = dlast or zero) entering every segment,
+// into seg_state [B][n_seg][M][2].  Real scans pass maps with zero imaginary
+// parts and init_im = NULL.  Launch errors are left for the caller's
+// hipGetLastError.
+sparc_status seg_carry(int64_t B, int64_t M, int n_seg, int reverse, const float* seg_sum, const float* init_re,
+                       const float* init_im, float* seg_state, sparc_stream_t stream);
 
 }  // namespace sparc
 

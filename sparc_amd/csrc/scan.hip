@@ -98,6 +98,11 @@ struct ScanArgs {
   uint32_t* flagv;    // [n_chains, n_chunks]
   float* agg;         // [n_chains, n_chunks, 64*V, NQ]
   float* carry;       // backward inclusive adjoint carries [B, n_chunks, M, NH]
+  // time segments of the serial kernels (n_seg > 1): a launch runs segments
+  // seg_lo, seg_lo + 1, ... of t_seg steps each (grid = n_chains * segments)
+  int n_seg, t_seg, seg_lo;
+  float* seg_sum;     // [B][n_seg][M][4]: each segment's map (P, Q) of the state or adjoint
+  float* seg_state;   // [B][n_seg][M][2]: the state (forward) or adjoint (backward) entering it
 };
 
 // Cache policy of the serial kernels' plane loads and stores: bit 0 loads,
@@ -2870,7 +2875,30 @@ static_assert(kGateDepth % 2 == 0 && kGateDepth >= 2, "the loops pair plane buff
 #define SPARC_SERIAL_SWIZZLE 1
 #endif
 
-template <int TR, typename IO, int V, int S, bool RELU>
+// A serial workgroup's chain and steps: segment seg_lo + blockIdx / n_chains
+// of t_seg steps with time segments, else the whole sequence.
+struct SerialPos {
+  int b, mb, seg, t_begin, t_end;
+};
+__device__ __forceinline__ SerialPos serial_pos(const ScanArgs& p) {
+  const int idx = SPARC_SERIAL_SWIZZLE ? xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x))
+                                       : static_cast<int>(blockIdx.x);
+  const int sj = idx / p.n_chains, chain = idx - sj * p.n_chains;
+  SerialPos c;
+  c.b = chain / p.n_mblocks;
+  c.mb = chain - c.b * p.n_mblocks;
+  const bool segs = p.n_seg > 1;
+  c.seg = segs ? p.seg_lo + sj : 0;
+  c.t_begin = segs ? c.seg * p.t_seg : 0;
+  c.t_end = segs ? min(p.T, c.t_begin + p.t_seg) : p.T;
+  return c;
+}
+
+// SUMMARY (time segments): the segment's map from a zero state, h_out = P h_in
+// + Q, into seg_sum; no stores of y or of the chunk states.  Otherwise the
+// segment starts from its entering state in seg_state (h0 for the first
+// segment is folded in there by the carry kernel).
+template <int TR, typename IO, int V, int S, bool RELU, bool SUMMARY = false>
 __global__ void __launch_bounds__(128, 1)
 chain_fwd_serial_kernel(ScanArgs p) {
   static_assert(!tr_g32(TR), "lane-shared kernels read gates in the I/O dtype");
@@ -2884,14 +2912,12 @@ chain_fwd_serial_kernel(ScanArgs p) {
   using RawT = typename Raw<IO, V>::T;
   __shared__ float tab[2][S * kFastMaxGpw * TW];
 
-  const int n_blocks = (p.T + S - 1) / S;
-  if (n_blocks == 0) return;  // the whole workgroup: no barrier is skipped by one wave only
+  const SerialPos cp = serial_pos(p);
+  const int n_blocks = (cp.t_end - cp.t_begin + S - 1) / S;
+  if (n_blocks <= 0) return;  // the whole workgroup: no barrier is skipped by one wave only
   const int lane = threadIdx.x & 63;
   const bool streamer = threadIdx.x < 64;  // wave-uniform
-  const int chain = SPARC_SERIAL_SWIZZLE ? xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x))
-                                         : static_cast<int>(blockIdx.x);
-  const int b = chain / p.n_mblocks;
-  const int mb = chain - b * p.n_mblocks;
+  const int b = cp.b, mb = cp.mb, t_begin = cp.t_begin;
   const int m0 = mb * MB + lane * V;
   const bool lane_ok = m0 < p.M;
   const int gpw = MB / p.gs;
@@ -2906,11 +2932,24 @@ chain_fwd_serial_kernel(ScanArgs p) {
   const int64_t ostride = (RELU ? 2 : 1) * stride;          // bytes per step of y
 
   float hr[V], hi[V];
+  float Pr[V], Pi[V];  // SUMMARY: the product of the segment's transitions
+  const bool from_seg = !SUMMARY && p.n_seg > 1;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
-    hr[v] = (streamer && p.h0_re && lane_ok) ? p.h0_re[i0] : 0.0f;
-    hi[v] = (streamer && CPLX && p.h0_im && lane_ok) ? p.h0_im[i0] : 0.0f;
+    const int64_t si = ((static_cast<int64_t>(b) * p.n_seg + cp.seg) * p.M + m0 + v) * 2;
+    if (SUMMARY) {
+      hr[v] = 0.0f;
+      hi[v] = 0.0f;
+    } else if (from_seg) {
+      hr[v] = (streamer && lane_ok) ? p.seg_state[si] : 0.0f;
+      hi[v] = (streamer && CPLX && lane_ok) ? p.seg_state[si + 1] : 0.0f;
+    } else {
+      hr[v] = (streamer && p.h0_re && lane_ok) ? p.h0_re[i0] : 0.0f;
+      hi[v] = (streamer && CPLX && p.h0_im && lane_ok) ? p.h0_im[i0] : 0.0f;
+    }
+    Pr[v] = 1.0f;
+    Pi[v] = 0.0f;
   }
   // The initial state is loop-carried: complete its loads here, or the
   // compiler, unsure at the loop head whether they are still pending, waits
@@ -2925,7 +2964,7 @@ chain_fwd_serial_kernel(ScanArgs p) {
   // prefetch before every block.)
   const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
   auto load_block = [&](int hb, int k) {
-    const int t0 = k * S;
+    const int t0 = t_begin + k * S;
     const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
     const int last = p.T - 1 - t0;  // the block's last step inside T (wave-uniform)
 #pragma unroll
@@ -2962,10 +3001,17 @@ chain_fwd_serial_kernel(ScanArgs p) {
           const float ni = fmaf(ai[s], hr[v], fmaf(ar[s], hi[v], xi[v]));
           hr[v] = nr;
           hi[v] = ni;
+          if constexpr (SUMMARY) {  // P <- a P (the identity past T)
+            const float pr = fmaf(ar[s], Pr[v], -ai[s] * Pi[v]);
+            Pi[v] = fmaf(ai[s], Pr[v], ar[s] * Pi[v]);
+            Pr[v] = pr;
+          }
         } else {
           hr[v] = fmaf(ar[s], hr[v], xr[v]);
+          if constexpr (SUMMARY) Pr[v] *= ar[s];
         }
       }
+      if constexpr (SUMMARY) continue;
       if (lane_ok && t0 + s < p.T) {
         const int64_t o = yoff + s * ostride;
         if constexpr (RELU) {
@@ -2987,8 +3033,8 @@ chain_fwd_serial_kernel(ScanArgs p) {
   } else {
 #pragma unroll
     for (int d = 0; d < kGateDepth - 1; ++d)
-      if (d < n_blocks) load_gate_pairs<TR, IO, S>(p, b, d * S, g_base, gpw, lane, gb[d]);
-    fill_tab<TR, IO, S, TW>(p, 0, g_base, gpw, lane, reset_first, gb[0], tab[0]);
+      if (d < n_blocks) load_gate_pairs<TR, IO, S>(p, b, t_begin + d * S, g_base, gpw, lane, gb[d]);
+    fill_tab<TR, IO, S, TW>(p, t_begin, g_base, gpw, lane, reset_first, gb[0], tab[0]);
   }
   __syncthreads();
   // block k = k0 + h: planes and table in buffers k & 1 = h & 1, gates in
@@ -2998,7 +3044,7 @@ chain_fwd_serial_kernel(ScanArgs p) {
     for (int h = 0; h < kGateDepth; ++h) {
       const int k = k0 + h;
       if (k >= n_blocks) break;
-      const int t0 = k * S;
+      const int t0 = t_begin + k * S;
       const int x = h & 1;
       if (streamer) {
         // unconditional (the last block re-reads itself): a path without the
@@ -3008,7 +3054,7 @@ chain_fwd_serial_kernel(ScanArgs p) {
         // the state after the last step of a saved-state chunk (steps past T
         // are the identity, so the last block ends on the state after T-1)
         const int t_end = t0 + S;
-        if (lane_ok && (t_end % kStateChunk == 0 || t_end >= p.T)) {
+        if (!SUMMARY && lane_ok && (t_end % kStateChunk == 0 || t_end >= p.T)) {
           const int c = (min(t_end, p.T) - 1) / kStateChunk;
           float* dst = p.chunk_state + ((static_cast<int64_t>(b) * p.n_chunks + c) * p.M + m0) * NH;
 #pragma unroll
@@ -3026,6 +3072,14 @@ chain_fwd_serial_kernel(ScanArgs p) {
       __syncthreads();
     }
   }
+  if constexpr (SUMMARY) {
+    if (streamer && lane_ok) {
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        *reinterpret_cast<float4*>(p.seg_sum + ((static_cast<int64_t>(b) * p.n_seg + cp.seg) * p.M + m0 + v) * 4) =
+            make_float4(Pr[v], CPLX ? Pi[v] : 0.0f, hr[v], CPLX ? hi[v] : 0.0f);
+    }
+  }
 }
 
 // Backward from the saved forward output (no relu epilogue), one chain per
@@ -3034,8 +3088,12 @@ chain_fwd_serial_kernel(ScanArgs p) {
 // from row t-1 of y (h0 at t = 0).  Wave 0 runs the adjoint and leaves each
 // lane's per-step transition gradients in LDS; wave 1 sums them over the
 // lanes of each group one block later, applies the polar chain rule (dr,
-// dphi) to the group sums and stores the gate gradients.
-template <int TR, typename IO, int V, int S>
+// dphi) to the group sums and stores the gate gradients.  SUMMARY (time
+// segments): the segment's map of the adjoint from zero (P the product of
+// conj(a), Q the adjoint leaving its first step) into seg_sum, nothing else;
+// otherwise the segment starts from its entering adjoint in seg_state (dlast
+// for the last segment, folded in there by the carry kernel).
+template <int TR, typename IO, int V, int S, bool SUMMARY = false>
 __global__ void __launch_bounds__(128, 1)
 chain_bwd_serial_kernel(ScanArgs p) {
   static_assert(!tr_g32(TR), "lane-shared kernels read gates in the I/O dtype");
@@ -3051,14 +3109,12 @@ chain_bwd_serial_kernel(ScanArgs p) {
   __shared__ float tab[2][S * kFastMaxGpw * TW];
   __shared__ float red[2][64 * RED];
 
-  const int n_blocks = (p.T + S - 1) / S;
-  if (n_blocks == 0) return;  // the whole workgroup
+  const SerialPos cp = serial_pos(p);
+  const int n_blocks = (cp.t_end - cp.t_begin + S - 1) / S;
+  if (n_blocks <= 0) return;  // the whole workgroup
   const int lane = threadIdx.x & 63;
   const bool streamer = threadIdx.x < 64;  // wave-uniform
-  const int chain = SPARC_SERIAL_SWIZZLE ? xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x))
-                                         : static_cast<int>(blockIdx.x);
-  const int b = chain / p.n_mblocks;
-  const int mb = chain - b * p.n_mblocks;
+  const int b = cp.b, mb = cp.mb, t_begin = cp.t_begin;
   const int m0 = mb * MB + lane * V;
   const bool lane_ok = m0 < p.M;
   const int gpw = MB / p.gs;
@@ -3072,11 +3128,24 @@ chain_bwd_serial_kernel(ScanArgs p) {
   const int64_t stride = static_cast<int64_t>(p.M) * ESZ;
 
   float xr[V], xi[V];  // conj(a_{t+1}) lambda_{t+1}: the adjoint flowing into step t
+  float Pr[V], Pi[V];  // SUMMARY: the product of the segment's conj(a)
+  const bool from_seg = !SUMMARY && p.n_seg > 1;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
-    xr[v] = (streamer && p.dlast_re && lane_ok) ? p.dlast_re[i0] : 0.0f;
-    xi[v] = (streamer && CPLX && p.dlast_im && lane_ok) ? p.dlast_im[i0] : 0.0f;
+    const int64_t si = ((static_cast<int64_t>(b) * p.n_seg + cp.seg) * p.M + m0 + v) * 2;
+    if (SUMMARY) {
+      xr[v] = 0.0f;
+      xi[v] = 0.0f;
+    } else if (from_seg) {
+      xr[v] = (streamer && lane_ok) ? p.seg_state[si] : 0.0f;
+      xi[v] = (streamer && CPLX && lane_ok) ? p.seg_state[si + 1] : 0.0f;
+    } else {
+      xr[v] = (streamer && p.dlast_re && lane_ok) ? p.dlast_re[i0] : 0.0f;
+      xi[v] = (streamer && CPLX && p.dlast_im && lane_ok) ? p.dlast_im[i0] : 0.0f;
+    }
+    Pr[v] = 1.0f;
+    Pi[v] = 0.0f;
   }
 
   // wave 0: dy rows t0 .. t0+S-1 and y rows t0-1 .. t0+S-2 (the state before each step)
@@ -3087,7 +3156,7 @@ chain_bwd_serial_kernel(ScanArgs p) {
   // discards what lies outside (dy past T, y before step 0, lanes past M).
   const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
   auto load_block = [&](int hb, int k) {
-    const int t0 = k * S;
+    const int t0 = t_begin + k * S;
     const int64_t off = wave_uniform(((row0 + t0) * p.M + mbase) * ESZ);
     const int last = p.T - 1 - t0;  // the block's last step inside T (wave-uniform)
 #pragma unroll
@@ -3097,10 +3166,10 @@ chain_bwd_serial_kernel(ScanArgs p) {
       const int64_t od = off + static_cast<int64_t>(sd) * stride;
       const int64_t oy = off + static_cast<int64_t>(sy) * stride;
       dr[hb][s] = ldn<RawT, (SPARC_BWD_NT & 1) != 0>(p.dy_re, od, lane_ld);
-      yr[hb][s] = ldn<RawT, (SPARC_BWD_NT & 1) != 0>(p.y_re, oy, lane_ld);
+      if constexpr (!SUMMARY) yr[hb][s] = ldn<RawT, (SPARC_BWD_NT & 1) != 0>(p.y_re, oy, lane_ld);
       if constexpr (CPLX) {
         di[hb][s] = ldn<RawT, (SPARC_BWD_NT & 1) != 0>(p.dy_im, od, lane_ld);
-        yi[hb][s] = ldn<RawT, (SPARC_BWD_NT & 1) != 0>(p.y_im, oy, lane_ld);
+        if constexpr (!SUMMARY) yi[hb][s] = ldn<RawT, (SPARC_BWD_NT & 1) != 0>(p.y_im, oy, lane_ld);
       }
     }
   };
@@ -3128,10 +3197,10 @@ chain_bwd_serial_kernel(ScanArgs p) {
     for (int s = S - 1; s >= 0; --s) {
       float gy_r[V], gy_i[V], hr[V], hi[V], lr[V], li[V];
       unpack<IO, V>(dr[h][s], gy_r);
-      unpack<IO, V>(yr[h][s], hr);
+      if constexpr (!SUMMARY) unpack<IO, V>(yr[h][s], hr);
       if constexpr (CPLX) {
         unpack<IO, V>(di[h][s], gy_i);
-        unpack<IO, V>(yi[h][s], hi);
+        if constexpr (!SUMMARY) unpack<IO, V>(yi[h][s], hi);
       }
       if (edge) {
         if (t0 + s >= p.T) {  // past T: no incoming gradient (the transition is the identity)
@@ -3147,6 +3216,22 @@ chain_bwd_serial_kernel(ScanArgs p) {
       for (int v = 0; v < V; ++v) {
         lr[v] = gy_r[v] + xr[v];
         if constexpr (CPLX) li[v] = gy_i[v] + xi[v];
+      }
+      if constexpr (SUMMARY) {  // the adjoint alone; P <- conj(a) P (the identity past T)
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (CPLX) {
+            xr[v] = fmaf(ar[s], lr[v], ai[s] * li[v]);
+            xi[v] = fmaf(ar[s], li[v], -ai[s] * lr[v]);
+            const float pr = fmaf(ar[s], Pr[v], ai[s] * Pi[v]);
+            Pi[v] = fmaf(ar[s], Pi[v], -ai[s] * Pr[v]);
+            Pr[v] = pr;
+          } else {
+            xr[v] = ar[s] * lr[v];
+            Pr[v] *= ar[s];
+          }
+        }
+        continue;
       }
       if (lane_ok && t0 + s < p.T) {
         stn<RawT, (SPARC_BWD_NT & 2) != 0>(p.dw_re, off + s * stride, lane_bytes, pack<IO, V>(lr));
@@ -3213,8 +3298,9 @@ chain_bwd_serial_kernel(ScanArgs p) {
   } else {
 #pragma unroll
     for (int d = 0; d < kGateDepth - 1; ++d)
-      if (d < n_blocks) load_gate_pairs<TR, IO, S>(p, b, (n_blocks - 1 - d) * S, g_base, gpw, lane, gb[d]);
-    rm_mid = fill_tab<TR, IO, S, TW>(p, (n_blocks - 1) * S, g_base, gpw, lane, reset_first, gb[0], tab[0]);
+      if (d < n_blocks)
+        load_gate_pairs<TR, IO, S>(p, b, t_begin + (n_blocks - 1 - d) * S, g_base, gpw, lane, gb[d]);
+    rm_mid = fill_tab<TR, IO, S, TW>(p, t_begin + (n_blocks - 1) * S, g_base, gpw, lane, reset_first, gb[0], tab[0]);
   }
   __syncthreads();
   for (int j0 = 0; j0 < n_blocks; j0 += kGateDepth) {
@@ -3223,13 +3309,13 @@ chain_bwd_serial_kernel(ScanArgs p) {
       const int j = j0 + h;
       if (j >= n_blocks) break;
       const int k = n_blocks - 1 - j;
-      const int t0 = k * S;
+      const int t0 = t_begin + k * S;
       const int x = h & 1;
       if (streamer) {
         load_block(1 - x, k >= 1 ? k - 1 : 0);  // unconditional, as in the forward
         run_block(x, t0, tab[x], red[x]);
       } else {
-        if (j >= 1) store_block_grads(t0 + S, tab[1 - x], red[1 - x], rm_old);
+        if (!SUMMARY && j >= 1) store_block_grads(t0 + S, tab[1 - x], red[1 - x], rm_old);
         rm_old = rm_mid;
         rm_mid = 0u;
         if (k >= 1) {
@@ -3243,8 +3329,15 @@ chain_bwd_serial_kernel(ScanArgs p) {
       __syncthreads();
     }
   }
-  if (streamer) {
-    if (lane_ok && p.dh0_re) {
+  if constexpr (SUMMARY) {
+    if (streamer && lane_ok) {
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        *reinterpret_cast<float4*>(p.seg_sum + ((static_cast<int64_t>(b) * p.n_seg + cp.seg) * p.M + m0 + v) * 4) =
+            make_float4(Pr[v], CPLX ? Pi[v] : 0.0f, xr[v], CPLX ? xi[v] : 0.0f);
+    }
+  } else if (streamer) {
+    if (lane_ok && p.dh0_re && t_begin == 0) {
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         const int64_t i0 = static_cast<int64_t>(b) * p.M + m0 + v;
@@ -3254,7 +3347,7 @@ chain_bwd_serial_kernel(ScanArgs p) {
     }
   } else {
     const int hl = (n_blocks - 1) & 1;  // buffers of the last iteration (block 0)
-    store_block_grads(0, tab[hl], red[hl], rm_old);
+    store_block_grads(t_begin, tab[hl], red[hl], rm_old);
   }
 }
 
@@ -3323,8 +3416,9 @@ struct Plan {
   bool serial = false;  // one wave per chain (lane-shared gates, many chains)
   bool g32 = false;  // fp32 gates beside bf16 I/O (general kernels only)
   int n_chunks = 0, n_mblocks = 0, n_chains = 0;
+  int n_seg = 1, t_seg = 0;  // time segments of the serial kernels (n_seg > 1: few chains)
   int64_t n_tiles = 0;
-  size_t flags_off = 0, agg_off = 0, carry_off = 0, part_off = 0, total = 0;
+  size_t flags_off = 0, agg_off = 0, carry_off = 0, part_off = 0, seg_sum_off = 0, seg_state_off = 0, total = 0;
   int64_t part_g_elems = 0, part_p_elems = 0;
 };
 
@@ -3338,6 +3432,38 @@ struct Plan {
 constexpr int kSerialFwdS = SPARC_SERIAL_FWD_S;
 constexpr int kSerialBwdS = SPARC_SERIAL_BWD_S;
 
+// The serial kernels over a plan's chains.  With time segments: the maps of
+// every segment but the last one processed (forward 0 .. n-2, backward
+// n-1 .. 1), the carry into every segment (from h0 / dlast), then every
+// segment from its entering state.
+template <int TR, typename IO, int V>
+void serial_fwd(const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
+  const auto ss = reinterpret_cast<sparc_stream_t>(st);
+  if (pl.n_seg > 1) {
+    const dim3 gs(static_cast<unsigned>(pl.n_chains) * static_cast<unsigned>(pl.n_seg - 1));
+    hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, false, true>), gs, dim3(128), 0, st, a);
+    (void)sparc::seg_carry(a.B, a.M, pl.n_seg, 0, a.seg_sum, a.h0_re, a.h0_im, a.seg_state, ss);
+  }
+  const dim3 g(static_cast<unsigned>(pl.n_chains) * static_cast<unsigned>(pl.n_seg));
+  if ((a.flags & SPARC_FLAG_RELU_OUTPUT) && sparc::tr_kind(TR) != sparc::TR_REAL)
+    hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, true>), g, dim3(128), 0, st, a);
+  else
+    hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, false>), g, dim3(128), 0, st, a);
+}
+template <int TR, typename IO, int V>
+void serial_bwd(const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
+  const auto ss = reinterpret_cast<sparc_stream_t>(st);
+  if (pl.n_seg > 1) {
+    sparc::ScanArgs s = a;
+    s.seg_lo = 1;
+    const dim3 gs(static_cast<unsigned>(pl.n_chains) * static_cast<unsigned>(pl.n_seg - 1));
+    hipLaunchKernelGGL((sparc::chain_bwd_serial_kernel<TR, IO, V, kSerialBwdS, true>), gs, dim3(128), 0, st, s);
+    (void)sparc::seg_carry(a.B, a.M, pl.n_seg, 1, a.seg_sum, a.dlast_re, a.dlast_im, a.seg_state, ss);
+  }
+  const dim3 g(static_cast<unsigned>(pl.n_chains) * static_cast<unsigned>(pl.n_seg));
+  hipLaunchKernelGGL((sparc::chain_bwd_serial_kernel<TR, IO, V, kSerialBwdS>), g, dim3(128), 0, st, a);
+}
+
 template <int TR, typename IO, int V, int GM>
 struct Kernels {
   // look-back kernels: 8 waves x 8 steps
@@ -3349,11 +3475,7 @@ struct Kernels {
   static void run(int dir, bool chain, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
     if constexpr (sparc::tr_kind(TR) != sparc::TR_P1 && GM == sparc::GATE_LANE && !sparc::tr_g32(TR)) {
       if (pl.serial && dir == 0) {
-        const dim3 g(static_cast<unsigned>(pl.n_chains));
-        if ((a.flags & SPARC_FLAG_RELU_OUTPUT) && sparc::tr_kind(TR) != sparc::TR_REAL)
-          hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, true>), g, dim3(128), 0, st, a);
-        else
-          hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, false>), g, dim3(128), 0, st, a);
+        serial_fwd<TR, IO, V>(pl, st, a);
         return;
       }
       if (chain && pl.fast) {
@@ -3385,8 +3507,7 @@ struct Kernels {
     }
     if constexpr (sparc::tr_kind(TR) != sparc::TR_P1 && GM == sparc::GATE_LANE && !sparc::tr_g32(TR)) {
       if (pl.serial) {
-        const dim3 g(static_cast<unsigned>(pl.n_chains));
-        hipLaunchKernelGGL((sparc::chain_bwd_serial_kernel<TR, IO, V, kSerialBwdS>), g, dim3(128), 0, st, a);
+        serial_bwd<TR, IO, V>(pl, st, a);
         return true;
       }
       if (pl.chain && pl.fast) {
@@ -3431,16 +3552,8 @@ bool launch_v(int dir, const Plan& pl, hipStream_t st, const sparc::ScanArgs& a)
     if (V == kWideV) {
       if (!pl.serial || gm != sparc::GATE_LANE) return false;
       if (dir == 1) return false;  // no recomputing kernel: wide plans need the saved output
-      if (dir == 2) {
-        const dim3 g(static_cast<unsigned>(pl.n_chains));
-        hipLaunchKernelGGL((sparc::chain_bwd_serial_kernel<TR, IO, kWideV, kSerialBwdS>), g, dim3(128), 0, st, a);
-        return true;
-      }
-      const dim3 g(static_cast<unsigned>(pl.n_chains));
-      if (a.flags & SPARC_FLAG_RELU_OUTPUT)
-        hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, kWideV, kSerialFwdS, true>), g, dim3(128), 0, st, a);
-      else
-        hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, kWideV, kSerialFwdS, false>), g, dim3(128), 0, st, a);
+      if (dir == 2) serial_bwd<TR, IO, kWideV>(pl, st, a);
+      else serial_fwd<TR, IO, kWideV>(pl, st, a);
       return true;
     }
   }
@@ -3537,10 +3650,55 @@ static std::atomic<uint32_t> g_wait_limit{1u << 20};
 
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
+// Time segments of the serial kernels: below kSegChains chains (where the
+// look-back kernels would run), T splits into segments of a multiple of 64
+// steps, at least kSegMinSteps long, enough for about kSegTarget workgroups
+// (per direction: at B=1, T=65536, M=2048 the forward took 0.376 / 0.397 /
+// 0.426 ms with 512 / 1024 / 2048 workgroups, the backward 0.524 / 0.479 /
+// 0.489 ms).
+#ifndef SPARC_SERIAL_SEG_CHAINS
+#define SPARC_SERIAL_SEG_CHAINS 512
+#endif
+#ifndef SPARC_SERIAL_SEG_TARGET_FWD
+#define SPARC_SERIAL_SEG_TARGET_FWD 512
+#endif
+#ifndef SPARC_SERIAL_SEG_TARGET_BWD
+#define SPARC_SERIAL_SEG_TARGET_BWD 1024
+#endif
+#ifndef SPARC_SERIAL_SEG_MIN
+#define SPARC_SERIAL_SEG_MIN 256
+#endif
+constexpr int64_t kSegChains = SPARC_SERIAL_SEG_CHAINS;
+constexpr int64_t kSegTarget[2] = {SPARC_SERIAL_SEG_TARGET_FWD, SPARC_SERIAL_SEG_TARGET_BWD};
+constexpr int64_t kSegMinSteps = SPARC_SERIAL_SEG_MIN;
+static_assert(kSegMinSteps % 64 == 0 && kSegChains <= kSegTarget[0] && kSegChains <= kSegTarget[1],
+              "segments of whole chunks, at least two");
+
+bool want_segments(int64_t chains, int64_t T) { return chains < kSegChains && T >= 2 * kSegMinSteps; }
+
+// n >= 2 segments of t_seg steps (a multiple of the saved-state chunk), or 1
+void choose_serial_segments(int direction, int64_t chains, int64_t T, int& n_seg, int& t_seg) {
+  n_seg = 1;
+  t_seg = static_cast<int>(T);
+  if (!want_segments(chains, T)) return;
+  const int64_t target = kSegTarget[direction ? 1 : 0];
+  int64_t n = std::min((target + chains - 1) / chains, T / kSegMinSteps);
+  if (n < 2) return;
+  int64_t len = (T + n - 1) / n;
+  len = (len + kChunk - 1) / kChunk * kChunk;
+  n = (T + len - 1) / len;
+  if (n < 2) return;
+  n_seg = static_cast<int>(n);
+  t_seg = static_cast<int>(len);
+}
+
 // Chooses V and the gate mode; fills sizes.  Returns an error message or NULL.
 // allow_wide: the caller can use the 4-mode serial kernels (their pointers are
 // 8-byte aligned and, backward, the states come from the saved output).
-const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl, bool allow_wide = true) {
+// allow_seg: the serial kernels may split time into segments (backward: the
+// states come from the saved output).
+const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl, bool allow_wide = true,
+                      bool allow_seg = true) {
   if (!d) return "desc is NULL";
   if (d->batch <= 0 || d->length < 0 || d->modes <= 0 || d->groups <= 0) return "B, M, G must be > 0 and T >= 0";
   if (d->modes % d->groups) return "groups must divide modes";
@@ -3582,7 +3740,7 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl, bool al
       gs % kWideV == 0 && (64 * kWideV) % gs == 0 && is_pow2(gs / kWideV) &&
       (64 * kWideV) / gs <= sparc::kFastMaxGpw && !force_l && !force_c && allow_wide) {
     const int64_t chains = d->batch * ((M + 64 * kWideV - 1) / (64 * kWideV));
-    wide = force_s || chains >= kSerialWideMin;
+    wide = force_s || chains >= kSerialWideMin || (allow_seg && want_segments(chains, d->length));
   }
   if (wide) {
     V = kWideV;
@@ -3598,7 +3756,12 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl, bool al
   pl->n_chains = static_cast<int>(d->batch * pl->n_mblocks);
   pl->n_tiles = static_cast<int64_t>(pl->n_chains) * pl->n_chunks;
   const bool lane_shared = !p1 && !g32 && gm == sparc::GATE_LANE && (64 * V) / gs <= sparc::kFastMaxGpw;
-  pl->serial = wide || (lane_shared && (force_s || (!force_l && !force_c && pl->n_chains >= kSerialMin)));
+  pl->n_seg = 1;
+  pl->t_seg = static_cast<int>(d->length);
+  if (allow_seg && lane_shared && !force_l && !force_c)
+    choose_serial_segments(direction, pl->n_chains, d->length, pl->n_seg, pl->t_seg);
+  pl->serial = wide || pl->n_seg > 1 ||
+               (lane_shared && (force_s || (!force_l && !force_c && pl->n_chains >= kSerialMin)));
   pl->chain = pl->serial || force_c || force_s || (!force_l && pl->n_chains >= kChainMin);
   pl->fast = pl->chain && lane_shared;
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
@@ -3621,6 +3784,12 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl, bool al
     // P1 nu/theta partials: one row per tile (look-back) or per batch row (chain)
     if (p1) pl->part_p_elems = d->batch * static_cast<int64_t>(pl->chain ? 1 : pl->n_chunks) * M;
     off += ((static_cast<size_t>(2 * pl->part_g_elems + 2 * pl->part_p_elems) * 4 + 255) / 256) * 256;
+  }
+  if (pl->n_seg > 1) {  // each segment's map [B][n_seg][M][4], its entering state [B][n_seg][M][2]
+    pl->seg_sum_off = off;
+    off += ((static_cast<size_t>(d->batch) * pl->n_seg * M * 16 + 255) / 256) * 256;
+    pl->seg_state_off = off;
+    off += ((static_cast<size_t>(d->batch) * pl->n_seg * M * 8 + 255) / 256) * 256;
   }
   pl->total = off;
   return nullptr;
@@ -3666,9 +3835,12 @@ int64_t sparc_scan_chunk_count(const sparc_scan_desc* d) {
 
 size_t sparc_scan_workspace_bytes(const sparc_scan_desc* d, int direction) {
   // enough for every plan: the call decides from its pointers
-  Plan pw, pn;
-  if (make_plan(d, direction, &pw, true) || make_plan(d, direction, &pn, false)) return 0;
-  size_t n = pw.total > pn.total ? pw.total : pn.total;
+  size_t n = 0;
+  for (int k = 0; k < 4; ++k) {
+    Plan pk;
+    if (make_plan(d, direction, &pk, (k & 1) != 0, (k & 2) != 0)) return 0;
+    n = pk.total > n ? pk.total : n;
+  }
   const size_t f = sparc::p1_fused_workspace_bytes(d, direction);
   return f > n ? f : n;
 }
@@ -3687,8 +3859,8 @@ static bool p1_fused_route(const sparc_scan_desc* d, int direction, const void* 
 }
 
 static sparc_status common_checks(const sparc_scan_desc* d, int dir, Plan* pl,
-                                  void* workspace, size_t workspace_bytes, bool allow_wide) {
-  if (const char* e = make_plan(d, dir, pl, allow_wide)) return fail(SPARC_EINVAL, "%s", e);
+                                  void* workspace, size_t workspace_bytes, bool allow_wide, bool allow_seg) {
+  if (const char* e = make_plan(d, dir, pl, allow_wide, allow_seg)) return fail(SPARC_EINVAL, "%s", e);
   if (!workspace) return fail(SPARC_EWORKSPACE, "workspace is NULL");
   if (workspace_bytes < pl->total)
     return fail(SPARC_EWORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, pl->total);
@@ -3708,6 +3880,11 @@ static void fill_ws(sparc::ScanArgs& a, const Plan& pl, void* ws) {
   a.part_g1 = part + pl.part_g_elems;
   a.part_nu = part + 2 * pl.part_g_elems;
   a.part_theta = part + 2 * pl.part_g_elems + pl.part_p_elems;
+  a.n_seg = pl.n_seg;
+  a.t_seg = pl.t_seg;
+  a.seg_lo = 0;
+  a.seg_sum = pl.n_seg > 1 ? reinterpret_cast<float*>(base + pl.seg_sum_off) : nullptr;
+  a.seg_state = pl.n_seg > 1 ? reinterpret_cast<float*>(base + pl.seg_state_off) : nullptr;
 }
 
 static sparc_status clear_ws(const Plan& pl, void* ws, hipStream_t st) {
@@ -3748,7 +3925,7 @@ sparc_status sparc_scan_forward(const sparc_scan_desc* d, const void* gate0, con
                                 void* workspace, size_t workspace_bytes, sparc_stream_t stream) {
   Plan pl;
   const bool wide_ok = aligned8(w_re) && aligned8(w_im) && aligned8(y_re) && aligned8(y_im);
-  if (sparc_status s = common_checks(d, 0, &pl, workspace, workspace_bytes, wide_ok)) return s;
+  if (sparc_status s = common_checks(d, 0, &pl, workspace, workspace_bytes, wide_ok, true)) return s;
   if (d->length == 0) return SPARC_OK;  // nothing to read or write
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
   const bool relu = (d->flags & SPARC_FLAG_RELU_OUTPUT) != 0;
@@ -3836,7 +4013,7 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
   const bool wide_ok = y_re && !relu && aligned8(w_re) && aligned8(w_im) && aligned8(y_re) &&
                        aligned8(y_im) && aligned8(dy_re) && aligned8(dy_im) && aligned8(dw_re) &&
                        aligned8(dw_im);
-  if (sparc_status s = common_checks(d, 1, &pl, workspace, workspace_bytes, wide_ok)) return s;
+  if (sparc_status s = common_checks(d, 1, &pl, workspace, workspace_bytes, wide_ok, y_re && !relu)) return s;
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
   const bool p1 = d->transition == SPARC_TRANSITION_P1;
   if (d->length == 0) {

@@ -133,6 +133,68 @@ def test_cfg2_full_size_sampled_groups():
     assert rel_err(pick(gr["dg1"], gsel), d_phi) <= tol
 
 
+def test_few_chains_time_segments_full_size():
+    """B=1, T=32768, D=128, N=16 polar bf16: 8 chains of 256 modes, which the
+    serial kernels split into 128 time segments (two groups of 64 in the
+    carry).  Outputs, final state and gradients against the look-back
+    kernels everywhere, and against the float64 oracle on three whole gate
+    groups over every step."""
+    print("[case] few chains B=1 T=32768 M=2048 G=128 bf16 polar, segments vs look-back", flush=True)
+    B, T, D, N = 1, 32768, 128, 16
+    M, G = D * N, D
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(7)
+    r = torch.sigmoid(torch.randn(B, T, G, device=dev, generator=g) + 2.0).to(torch.bfloat16)
+    phi = ((torch.rand(B, T, G, device=dev, generator=g) * 2 - 1) * math.pi).to(torch.bfloat16)
+    w_re, w_im, dy_re, dy_im = (torch.randn(B, T, M, device=dev, generator=g, dtype=torch.bfloat16)
+                                for _ in range(4))
+    h0_re, h0_im, dl_re, dl_im = (torch.randn(B, M, device=dev, generator=g) for _ in range(4))
+
+    def run(algorithm):
+        ops.set_algorithm(algorithm)
+        try:
+            y_re, y_im, cs = ops.scan_forward_raw("polar", r, phi, w_re, w_im, h0_re=h0_re, h0_im=h0_im)
+            gr = ops.scan_backward_raw("polar", r, phi, w_re, w_im, cs, dy_re, dy_im, h0_re=h0_re, h0_im=h0_im,
+                                       dlast_re=dl_re, dlast_im=dl_im, want_dh0=True, y_re=y_re, y_im=y_im)
+            torch.cuda.synchronize()
+            return y_re, y_im, cs, gr
+        finally:
+            ops.set_algorithm("auto")
+
+    y_re, y_im, cs, gr = run("auto")
+    ly_re, ly_im, lcs, lgr = run("lookback")
+    tol = 2e-2
+    assert rel_err(y_re, ly_re) <= tol and rel_err(y_im, ly_im) <= tol
+    assert rel_err(cs[:, -1], lcs[:, -1]) <= 1e-4
+    for k in ("dw_re", "dw_im", "dg0", "dg1", "dh0_re", "dh0_im"):
+        assert rel_err(gr[k], lgr[k]) <= tol, k
+    del ly_re, ly_im, lcs, lgr
+    groups = [0, 77, G - 1]
+    modes = group_modes(groups, N).to(dev)
+    gsel = torch.tensor(groups, device=dev)
+
+    def pick(t, idx):
+        return t[:, :, idx].double().cpu()
+
+    leaves = [pick(r, gsel), pick(phi, gsel), pick(w_re, modes), pick(w_im, modes),
+              h0_re[:, modes].double().cpu(), h0_im[:, modes].double().cpu()]
+    leaves = [v.clone().requires_grad_() for v in leaves]
+    (hr, hi), last = O.grouped_scan_forward("polar", *leaves[:4], h0=(leaves[4], leaves[5]))
+    loss = (hr * pick(dy_re, modes)).sum() + (hi * pick(dy_im, modes)).sum() \
+        + (last[0] * dl_re[:, modes].double().cpu()).sum() + (last[1] * dl_im[:, modes].double().cpu()).sum()
+    d_r, d_phi, d_wr, d_wi, d_h0r, d_h0i = torch.autograd.grad(loss, leaves)
+    assert rel_err(pick(y_re, modes), hr) <= tol
+    assert rel_err(pick(y_im, modes), hi) <= tol
+    assert rel_err(cs[:, -1][:, modes, 0], last[0]) <= 1e-4
+    assert rel_err(cs[:, -1][:, modes, 1], last[1]) <= 1e-4
+    assert rel_err(pick(gr["dw_re"], modes), d_wr) <= tol
+    assert rel_err(pick(gr["dw_im"], modes), d_wi) <= tol
+    assert rel_err(pick(gr["dg0"], gsel), d_r) <= tol
+    assert rel_err(pick(gr["dg1"], gsel), d_phi) <= tol
+    assert rel_err(gr["dh0_re"][:, modes], d_h0r) <= tol
+    assert rel_err(gr["dh0_im"][:, modes], d_h0i) <= tol
+
+
 def test_cfg2_shape_p1_operator_full_size():
     """The reference's own operator (P1, one (eta, delta) per token) at the
     cfg2 shape, bf16 writes: the fused route (the automatic choice) against

@@ -230,6 +230,40 @@ def test_scan_parity(cid, transition, B, T, M, G, dtype, extra, algorithm):
     check_case(case)
 
 
+# Few chains and long enough sequences: the serial kernels split time into
+# segments (the maps of all segments but the last, a carry across them, then
+# every segment from its entering state).  Each case has fewer than 512
+# chains and T >= 512; gate groups of 16 modes keep the gates lane-shared.
+# The segment lengths are multiples of 64 steps, so ragged T leaves a short
+# last segment.
+SEG_CASES = [
+    ("seg_polar_bf16_wide", "polar", 1, 1500, 512, 32, BF16, dict(h0=True, dlast=True, seg=True)),
+    ("seg_polar_f32_reset_first", "polar", 2, 1100, 256, 16, F32, dict(h0=True, reset_first=True, dlast=True)),
+    ("seg_cart_bf16_relu", "cartesian", 1, 700, 256, 16, BF16, dict(relu=True, h0=True)),
+    ("seg_cart_f32_segments", "cartesian", 1, 900, 128, 8, F32, dict(h0=True, dlast=True, seg=True)),
+    ("seg_real_f32", "real", 2, 1030, 512, 32, F32, dict(h0=True, dlast=True, seg=True)),
+    ("seg_real_bf16", "real", 1, 2000, 256, 16, BF16, {}),
+    ("seg_polar_bf16_16segs", "polar", 3, 4096, 256, 16, BF16, dict(dlast=True)),
+]
+
+
+@pytest.mark.parametrize("algo", ["auto", "serial"])
+@pytest.mark.parametrize("cid,transition,B,T,M,G,dtype,extra", SEG_CASES, ids=[c[0] for c in SEG_CASES])
+def test_scan_time_segments(cid, transition, B, T, M, G, dtype, extra, algo):
+    """Serial kernels over time segments (few chains), forward and backward
+    from the saved output, against the float64 oracle: h0 folded into the
+    first segment's entering state, dlast into the last one's, resets and
+    reset_first inside segments, relu output (its backward recomputes states
+    on the look-back or chain kernels)."""
+    print(f"[case] {cid} B={B} T={T} M={M} G={G} {dtype} algo={algo}", flush=True)
+    ops.set_algorithm(algo)
+    try:
+        case = make_case(transition, B, T, M, G, dtype, seed=sum(map(ord, cid)) % 1000, **extra)
+        check_case(case)
+    finally:
+        ops.set_algorithm("auto")
+
+
 def test_long_real_drift(algorithm):
     """Long real scan with |a| up to 0.9999: chunk carries over 64 chunks keep
     fp32 within 1e-4 of the float64 sequential recurrence, including the last
