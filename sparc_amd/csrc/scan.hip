@@ -397,7 +397,7 @@ scan_fwd_kernel(ScanArgs p) {
   __shared__ uint32_t s_tile;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));  // wave-uniform (scalar branches)
   if (threadIdx.x == 0) s_tile = atomicAdd(p.ticket, 1u);
   __syncthreads();
   const uint32_t tile = s_tile;
@@ -732,7 +732,7 @@ scan_bwd_kernel(ScanArgs p) {
   __shared__ uint32_t s_tile;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));  // wave-uniform (scalar branches)
   if (threadIdx.x == 0) s_tile = atomicAdd(p.ticket, 1u);
   __syncthreads();
   const uint32_t tile = s_tile;
