@@ -703,16 +703,23 @@ scan_fwd_kernel(ScanArgs p) {
 #ifndef SPARC_LB_SAVED_LATE
 #define SPARC_LB_SAVED_LATE 1
 #endif
-// Waves per SIMD the SAVED backward of real scans is compiled for: 4 (two
-// workgroups per CU) spills 8-21 registers but, at B=4, T=65536, M=4096
-// (fp32), runs in 2.42 ms against 2.87 ms at the unconstrained 172 registers
-// (one workgroup per CU).  Complex transitions would spill 40-150 registers
-// under the same bound and keep the compiler's choice.
+// Waves per SIMD the SAVED backward is compiled for: 4, two workgroups per
+// CU.  Real scans fit it without spills (90 registers; B=4, T=65536, M=4096
+// fp32: 2.37 ms, against 2.87 ms at one workgroup per CU).  Polar and
+// cartesian scans spill 6-12 registers under it and still gain (polar bf16,
+// B=1, T=65536, M=2048: 1.00 -> 0.70 ms); P1 with two modes per lane would
+// spill 68-118 and keeps the compiler's choice.
 #ifndef SPARC_LB_BWD_WAVES
 #define SPARC_LB_BWD_WAVES 4
 #endif
+#ifndef SPARC_LB_BWD_WAVES_CPLX
+#define SPARC_LB_BWD_WAVES_CPLX 4
+#endif
 template <int TR, typename IO, int V, int GM, int S, int NW, bool SAVED>
-__global__ void __launch_bounds__(NW * 64, (SAVED && tr_kind(TR) == TR_REAL) ? SPARC_LB_BWD_WAVES : 1)
+__global__ void __launch_bounds__(NW * 64, !SAVED                      ? 1
+                                           : tr_kind(TR) == TR_REAL ? SPARC_LB_BWD_WAVES
+                                           : tr_kind(TR) == TR_P1   ? 1
+                                                                    : SPARC_LB_BWD_WAVES_CPLX)
 scan_bwd_kernel(ScanArgs p) {
   using TL = TransitionLane<TR, IO, V, GM>;
   using GT = typename TL::GT;
