@@ -3681,13 +3681,15 @@ constexpr int64_t kSegMinSteps = SPARC_SERIAL_SEG_MIN;
 static_assert(kSegMinSteps % 64 == 0 && kSegChains <= kSegTarget[0] && kSegChains <= kSegTarget[1],
               "segments of whole chunks, at least two");
 
-bool want_segments(int64_t chains, int64_t T) { return chains < kSegChains && T >= 2 * kSegMinSteps; }
+bool want_segments(int64_t chains, int64_t T, int64_t below = kSegChains) {
+  return chains < below && T >= 2 * kSegMinSteps;
+}
 
 // n >= 2 segments of t_seg steps (a multiple of the saved-state chunk), or 1
-void choose_serial_segments(int direction, int64_t chains, int64_t T, int& n_seg, int& t_seg) {
+void choose_serial_segments(int direction, int64_t below, int64_t chains, int64_t T, int& n_seg, int& t_seg) {
   n_seg = 1;
   t_seg = static_cast<int>(T);
-  if (!want_segments(chains, T)) return;
+  if (!want_segments(chains, T, below)) return;
   const int64_t target = kSegTarget[direction ? 1 : 0];
   int64_t n = std::min((target + chains - 1) / chains, T / kSegMinSteps);
   if (n < 2) return;
@@ -3697,6 +3699,35 @@ void choose_serial_segments(int direction, int64_t chains, int64_t T, int& n_seg
   if (n < 2) return;
   n_seg = static_cast<int>(n);
   t_seg = static_cast<int>(len);
+}
+
+// Chain-count thresholds of the automatic plan for lane-shared gates (chains
+// at the plan's modes per lane).  Measured fwd+bwd, polar and real, G = M/16,
+// B*T*M = 2^28, chains 8 .. 1024:
+//   bf16 complex: wide (4 modes) serial from 512 wide chains (69-72 % of 8
+//     TB/s), the 8-wave chain kernels at 2 modes from 128 wide chains (53-54 %
+//     against 46-48 % segmented), segments below (43-48 %; look-back 29-33 %);
+//   bf16 real (4 modes): serial from 1024 chains (75 %), chain kernels from
+//     256 (59-61 %; segments 41 %), segments below (41-44 %; look-back 31-39 %);
+//   fp32 complex (2 modes): serial from 512 chains (63-65 %), look-back below
+//     (53-62 %; segments 46-52 %, chain kernels 29-54 %);
+//   fp32 real (4 modes): look-back everywhere (60-77 %; serial 53-75 %).
+// A backward without the saved output (recompute) has no serial kernel of its
+// own: fp32 then keeps the look-back.
+constexpr int64_t kSegBelowCplx = 128;  // bf16 complex: segments below this many wide chains
+constexpr int64_t kSegBelowReal = 256;  // bf16 real
+constexpr int64_t kNever = INT64_MAX;
+void plan_lane_shared(bool cplx, bool bf16, bool wide, bool recompute_bwd, int64_t& seg_below, int64_t& serial_min,
+                      int64_t& chain_min) {
+  if (bf16) {
+    seg_below = cplx ? kSegBelowCplx : kSegBelowReal;
+    serial_min = cplx && wide ? kSerialWideMin : kSerialMin;
+    chain_min = 256;
+  } else {
+    seg_below = 0;
+    serial_min = cplx && !recompute_bwd ? 512 : kNever;
+    chain_min = kNever;
+  }
 }
 
 // Chooses V and the gate mode; fills sizes.  Returns an error message or NULL.
@@ -3740,14 +3771,18 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl, bool al
   const bool force_s = (d->flags & SPARC_FLAG_ALGO_SERIAL) != 0;
   if (int(force_l) + int(force_c) + int(force_s) > 1)
     return "ALGO_LOOKBACK, ALGO_CHAIN and ALGO_SERIAL are exclusive";
+  const bool auto_plan = !force_l && !force_c && !force_s;
+  const bool cplx_tr = d->transition != SPARC_TRANSITION_REAL;
+  const bool bf16_io = d->io_dtype == SPARC_BF16;
   // Complex bf16 with lane-shared gates: the serial kernels stream 8 bytes
-  // per lane and plane (4 modes) when that still leaves enough chains.
+  // per lane and plane (4 modes) when that still leaves enough chains, or
+  // over time segments when the chains are few.
   bool wide = false;
-  if (!p1 && !g32 && d->transition != SPARC_TRANSITION_REAL && d->io_dtype == SPARC_BF16 && M % kWideV == 0 &&
+  if (!p1 && !g32 && cplx_tr && bf16_io && M % kWideV == 0 &&
       gs % kWideV == 0 && (64 * kWideV) % gs == 0 && is_pow2(gs / kWideV) &&
       (64 * kWideV) / gs <= sparc::kFastMaxGpw && !force_l && !force_c && allow_wide) {
     const int64_t chains = d->batch * ((M + 64 * kWideV - 1) / (64 * kWideV));
-    wide = force_s || chains >= kSerialWideMin || (allow_seg && want_segments(chains, d->length));
+    wide = force_s || chains >= kSerialWideMin || (allow_seg && want_segments(chains, d->length, kSegBelowCplx));
   }
   if (wide) {
     V = kWideV;
@@ -3763,13 +3798,24 @@ const char* make_plan(const sparc_scan_desc* d, int direction, Plan* pl, bool al
   pl->n_chains = static_cast<int>(d->batch * pl->n_mblocks);
   pl->n_tiles = static_cast<int64_t>(pl->n_chains) * pl->n_chunks;
   const bool lane_shared = !p1 && !g32 && gm == sparc::GATE_LANE && (64 * V) / gs <= sparc::kFastMaxGpw;
+  // The automatic plan for lane-shared gates, by I/O dtype and transition
+  // (MI355X, fwd+bwd at B*T*M = 2^28, G = M/16; `plan_lane_shared` below):
+  // bf16 streams half the bytes per tile, so the look-back's per-tile cost
+  // weighs twice and the chain, serial and segmented serial kernels win;
+  // fp32 tiles carry enough bytes for the look-back to win below the serial
+  // kernels' chain count, and for real scans everywhere.
+  int64_t seg_below = 0, serial_min = kSerialMin, chain_min = kChainMin;
+  if (force_s) {
+    seg_below = kSegChains;
+  } else if (auto_plan && lane_shared) {
+    plan_lane_shared(cplx_tr, bf16_io, wide, direction == 1 && !allow_seg, seg_below, serial_min, chain_min);
+  }
   pl->n_seg = 1;
   pl->t_seg = static_cast<int>(d->length);
-  if (allow_seg && lane_shared && !force_l && !force_c)
-    choose_serial_segments(direction, pl->n_chains, d->length, pl->n_seg, pl->t_seg);
-  pl->serial = wide || pl->n_seg > 1 ||
-               (lane_shared && (force_s || (!force_l && !force_c && pl->n_chains >= kSerialMin)));
-  pl->chain = pl->serial || force_c || force_s || (!force_l && pl->n_chains >= kChainMin);
+  if (allow_seg && lane_shared && seg_below > 0 && (wide || !cplx_tr || force_s))
+    choose_serial_segments(direction, seg_below, pl->n_chains, d->length, pl->n_seg, pl->t_seg);
+  pl->serial = wide || pl->n_seg > 1 || (lane_shared && (force_s || (auto_plan && pl->n_chains >= serial_min)));
+  pl->chain = pl->serial || force_c || force_s || (auto_plan && pl->n_chains >= chain_min);
   pl->fast = pl->chain && lane_shared;
   const bool cplx = d->transition != SPARC_TRANSITION_REAL;
   const int NQ = cplx ? 4 : 2, NH = cplx ? 2 : 1;

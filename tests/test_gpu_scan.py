@@ -250,11 +250,12 @@ SEG_CASES = [
 @pytest.mark.parametrize("algo", ["auto", "serial"])
 @pytest.mark.parametrize("cid,transition,B,T,M,G,dtype,extra", SEG_CASES, ids=[c[0] for c in SEG_CASES])
 def test_scan_time_segments(cid, transition, B, T, M, G, dtype, extra, algo):
-    """Serial kernels over time segments (few chains), forward and backward
-    from the saved output, against the float64 oracle: h0 folded into the
-    first segment's entering state, dlast into the last one's, resets and
-    reset_first inside segments, relu output (its backward recomputes states
-    on the look-back or chain kernels)."""
+    """Serial kernels over time segments (few chains; forced with "serial",
+    the automatic choice for bf16, while fp32 takes the look-back), forward
+    and backward from the saved output, against the float64 oracle: h0
+    folded into the first segment's entering state, dlast into the last
+    one's, resets and reset_first inside segments, relu output (its backward
+    recomputes states on the look-back or chain kernels)."""
     print(f"[case] {cid} B={B} T={T} M={M} G={G} {dtype} algo={algo}", flush=True)
     ops.set_algorithm(algo)
     try:
@@ -262,6 +263,18 @@ def test_scan_time_segments(cid, transition, B, T, M, G, dtype, extra, algo):
         check_case(case)
     finally:
         ops.set_algorithm("auto")
+
+
+def test_time_segments_deterministic():
+    """The segmented serial plan (few chains) has no float atomics either:
+    outputs, final states and gradients are bit-identical run to run."""
+    print("[case] determinism of time segments: polar bf16 B=1 T=2048 M=512 G=32", flush=True)
+    case = make_case("polar", 1, 2048, 512, 32, BF16, seed=33, h0=True, dlast=True, seg=True)
+    y1, l1, g1 = run_gpu(case)
+    y2, l2, g2 = run_gpu(case)
+    for a, b in zip(list(y1) + list(l1) + list(g1), list(y2) + list(l2) + list(g2)):
+        if a is not None:
+            assert torch.equal(a, b)
 
 
 def test_long_real_drift(algorithm):
