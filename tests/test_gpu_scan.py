@@ -244,6 +244,9 @@ SEG_CASES = [
     ("seg_real_f32", "real", 2, 1030, 512, 32, F32, dict(h0=True, dlast=True, seg=True)),
     ("seg_real_bf16", "real", 1, 2000, 256, 16, BF16, {}),
     ("seg_polar_bf16_16segs", "polar", 3, 4096, 256, 16, BF16, dict(dlast=True)),
+    # a partial mode block: 320 modes are a block of 256 and one of 64
+    ("seg_polar_bf16_partial_block", "polar", 1, 1100, 320, 20, BF16, dict(h0=True, dlast=True)),
+    ("seg_real_bf16_partial_block", "real", 2, 700, 320, 20, BF16, dict(seg=True, dlast=True)),
 ]
 
 
