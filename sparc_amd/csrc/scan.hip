@@ -3449,6 +3449,8 @@ void serial_fwd(const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
   if (pl.n_seg > 1) {
     const dim3 gs(static_cast<unsigned>(pl.n_chains) * static_cast<unsigned>(pl.n_seg - 1));
     hipLaunchKernelGGL((sparc::chain_fwd_serial_kernel<TR, IO, V, kSerialFwdS, false, true>), gs, dim3(128), 0, st, a);
+    // seg_carry refuses B*M > INT32_MAX only; segmented plans have fewer than
+    // 512 chains of at most 256 modes, so B*M < 2^17 here
     (void)sparc::seg_carry(a.B, a.M, pl.n_seg, 0, a.seg_sum, a.h0_re, a.h0_im, a.seg_state, ss);
   }
   const dim3 g(static_cast<unsigned>(pl.n_chains) * static_cast<unsigned>(pl.n_seg));
@@ -3465,7 +3467,7 @@ void serial_bwd(const Plan& pl, hipStream_t st, const sparc::ScanArgs& a) {
     s.seg_lo = 1;
     const dim3 gs(static_cast<unsigned>(pl.n_chains) * static_cast<unsigned>(pl.n_seg - 1));
     hipLaunchKernelGGL((sparc::chain_bwd_serial_kernel<TR, IO, V, kSerialBwdS, true>), gs, dim3(128), 0, st, s);
-    (void)sparc::seg_carry(a.B, a.M, pl.n_seg, 1, a.seg_sum, a.dlast_re, a.dlast_im, a.seg_state, ss);
+    (void)sparc::seg_carry(a.B, a.M, pl.n_seg, 1, a.seg_sum, a.dlast_re, a.dlast_im, a.seg_state, ss);  // as above
   }
   const dim3 g(static_cast<unsigned>(pl.n_chains) * static_cast<unsigned>(pl.n_seg));
   hipLaunchKernelGGL((sparc::chain_bwd_serial_kernel<TR, IO, V, kSerialBwdS>), g, dim3(128), 0, st, a);
