@@ -245,21 +245,11 @@ def bench_cfg3(args, dev):
     }
 
 
-def bench_p1(args, dev):
-    """The reference's own scan operator (sparc_chunk_scan: the P1 transition
-    from per-token eta, delta and per-mode nu_log, theta_log; writes given) at
-    the headline shape: B=8, T=4096, M=16384, one gate pair per token (G = 1),
-    bf16 writes, fp32 eta/delta, fp32 state.  Forward and backward through the
-    C ABI; at G = 1 they run the one-wave-per-chain fused kernels
-    (mixer_fwd_kernel / mixer_bwd_kernel with the writes given), the backward
-    reading the states from the forward's output.
-
-    Algorithmic bytes: forward B*T*(8*M + 8) (read w, write y; read eta,
-    delta), backward B*T*(12*M + 16) (read dy and y, write dw; read eta,
-    delta, write their gradients)."""
+def _p1_timed(dev, B, T, M, steps):
+    """Forward and backward of the P1 scan through the C ABI (bf16 writes, fp32
+    eta/delta, G = 1) over `steps` timed pairs: (fwd ms, bwd ms, wall s)."""
     from sparc_amd import _lib
     lib = _lib.load()
-    B, T, M = 8, 4096, 16384
     g = torch.Generator(device=dev).manual_seed(0)
     eta = 2.772588722239781 * torch.tanh(0.5 * torch.randn(B, T, 1, device=dev, generator=g))
     delta = 1.5707963267948966 * torch.tanh(torch.randn(B, T, 1, device=dev, generator=g))
@@ -291,7 +281,6 @@ def bench_p1(args, dev):
     for _ in range(2):
         fwd()
         bwd()
-    steps = max(3, args.steps // 2)
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
@@ -305,14 +294,40 @@ def bench_p1(args, dev):
     elapsed = time.perf_counter() - t0
     fwd_ms = sum(e0.elapsed_time(e1) for e0, e1, _ in ev) / steps
     bwd_ms = sum(e1.elapsed_time(e2) for _, e1, e2 in ev) / steps
-    bytes_fwd = B * T * (8 * M + 8)
-    bytes_bwd = B * T * (12 * M + 16)
-    ms_step = elapsed * 1e3 / steps
     del w_re, w_im, dy_re, dy_im, y_re, y_im, dw_re, dw_im, cs
     torch.cuda.empty_cache()
+    return fwd_ms, bwd_ms, elapsed
+
+
+def _p1_bytes(B, T, M):
+    """Algorithmic bytes of the P1 scan: forward B*T*(8*M + 8) (read w, write
+    y; read eta, delta), backward B*T*(12*M + 16) (read dy and y, write dw;
+    read eta, delta, write their gradients)."""
+    return B * T * (8 * M + 8), B * T * (12 * M + 16)
+
+
+def bench_p1(args, dev):
+    """The reference's own scan operator (sparc_chunk_scan: the P1 transition
+    from per-token eta, delta and per-mode nu_log, theta_log; writes given) at
+    the headline shape: B=8, T=4096, M=16384, one gate pair per token (G = 1),
+    bf16 writes, fp32 eta/delta, fp32 state.  Forward and backward through the
+    C ABI; at G = 1 they run the one-wave-per-chain fused kernels
+    (mixer_fwd_kernel / mixer_bwd_kernel with the writes given), the backward
+    reading the states from the forward's output.  Beside it the few-chain
+    form, B=1, T=65536, M=2048 (32 chains of 64 modes, split into time
+    segments: a summary pass, the carry, a replay)."""
+    B, T, M = 8, 4096, 16384
+    steps = max(3, args.steps // 2)
+    fwd_ms, bwd_ms, elapsed = _p1_timed(dev, B, T, M, steps)
+    bytes_fwd, bytes_bwd = _p1_bytes(B, T, M)
+    ms_step = elapsed * 1e3 / steps
     traffic = measured_traffic(COUNTERS_FILE)
     valu = measured_valu_busy()
     kf, kb = "mixer_fwd_kernel (writes given)", "mixer_bwd_kernel (writes given)"
+    Bf, Tf, Mf, sf = 1, 65536, 2048, 10
+    ff_ms, fb_ms, fel = _p1_timed(dev, Bf, Tf, Mf, sf)
+    fbf, fbb = _p1_bytes(Bf, Tf, Mf)
+    fms = fel * 1e3 / sf
     return {
         "workload": "P1 chunk scan fwd+bwd (the reference's sparc_chunk_scan), one (eta, delta) per token",
         "B": B, "T": T, "M": M, "G": 1, "io_dtype": "bf16", "steps": steps,
@@ -325,6 +340,16 @@ def bench_p1(args, dev):
                      "traffic": traffic.get("mixer_bwd_kernel_p1"), "valu_busy_pct": valu.get("mixer_bwd_kernel_p1"),
                      "frac": round(bytes_bwd / bwd_ms / 1e6 / HBM_PEAK_GBS, 4)},
         "counters_source": COUNTERS_FILE if "mixer_fwd_kernel_p1" in traffic else None,
+        "few_chains": {
+            "workload": "P1 chunk scan fwd+bwd, few long chains (time segments)",
+            "B": Bf, "T": Tf, "M": Mf, "G": 1, "steps": sf, "ms_per_step": round(fms, 4),
+            "tokens_per_s": round(Bf * Tf * sf / fel, 1), "bytes_per_step": fbf + fbb,
+            "step_frac": round((fbf + fbb) / fms / 1e6 / HBM_PEAK_GBS, 4),
+            "forward": {"avg_launch_ms": round(ff_ms, 4), "bytes_per_launch": fbf,
+                        "frac": round(fbf / ff_ms / 1e6 / HBM_PEAK_GBS, 4)},
+            "backward": {"avg_launch_ms": round(fb_ms, 4), "bytes_per_launch": fbb,
+                         "frac": round(fbb / fb_ms / 1e6 / HBM_PEAK_GBS, 4)},
+        },
     }
 
 
