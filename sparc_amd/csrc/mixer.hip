@@ -1278,13 +1278,32 @@ void run_fwd(const Args& a, hipStream_t st) {
   }
   launch_fwd<IO, V, false, MODE>(a, a.n_seg, st);
 }
+// Steps per block of the backward.  8-step blocks prefetch twice as far
+// ahead; the module backward then needs about 240 VGPRs (two waves per SIMD
+// instead of three at 4 steps), so it takes them only when its grid leaves
+// at most two waves per SIMD of the 1024 (B=8, T=4096, width 32768: 3.85 ->
+// 3.75 ms; B=16, T=2048, width 24576, 3072 waves: 2.77 -> 2.81 ms with 8).
+// The P1 scan (writes given) fits 8-step blocks in about 147 VGPRs: 1.61 ->
+// 1.52 ms at B=8, T=4096, M=16384, and faster with time segments too.
 #ifndef SPARC_MIXER_BWD_S
 #define SPARC_MIXER_BWD_S 4
 #endif
+#ifndef SPARC_MIXER_BWD_LONG_S
+#define SPARC_MIXER_BWD_LONG_S 8
+#endif
+constexpr unsigned kBwdLongWaves = 2048;  // the module's 8-step blocks up to this grid
 template <typename IO, int V, bool SUMMARY, int MODE>
 void launch_bwd(const Args& a, int n_segs, hipStream_t st) {
-  const dim3 g(static_cast<unsigned>(a.B) * a.n_mb * static_cast<unsigned>(n_segs));
-  hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, SPARC_MIXER_BWD_S, SUMMARY, MODE>), g, dim3(64), 0, st, a);
+  const unsigned waves = static_cast<unsigned>(a.B) * a.n_mb * static_cast<unsigned>(n_segs);
+  const dim3 g(waves);
+  if constexpr ((MODE & 3) == kModule && V == 1) {
+    if (waves <= kBwdLongWaves) {
+      hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, SPARC_MIXER_BWD_LONG_S, SUMMARY, MODE>), g, dim3(64), 0, st, a);
+      return;
+    }
+  }
+  constexpr int S = (MODE & 3) == kModule ? SPARC_MIXER_BWD_S : SPARC_MIXER_BWD_LONG_S;
+  hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, S, SUMMARY, MODE>), g, dim3(64), 0, st, a);
 }
 template <typename IO, int V, int MODE = kModule>
 void run_bwd(const Args& a, hipStream_t st) {
