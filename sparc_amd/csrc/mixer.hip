@@ -584,6 +584,189 @@ mixer_fwd_kernel(Args a) {
 }
 
 // ---------------------------------------------------------------------------
+// module forward over wide chains: one streaming wave and NH helper waves
+// ---------------------------------------------------------------------------
+// A chain is a batch row and 256 modes (4 per lane), so that every load and
+// store moves a 512-byte piece of a row (1 KB for fp32) instead of the
+// 128-byte pieces of one mode per lane.  Wave 0 runs the recurrence and
+// stores y and the saved states; waves 1 .. NH load x and compute each
+// step's transition and write (the transcendental part of a step, SPH = S/NH
+// steps of a block each) into an LDS table one block ahead of wave 0,
+// double-buffered, with one workgroup barrier per block.  The arithmetic is
+// that of mixer_fwd_kernel in kModule, value for value, so both give the
+// same bits.  No time segments: the host takes this kernel only with enough
+// chains to fill the GPU.
+template <typename IO, int NH, int S>
+__global__ void __launch_bounds__(64 * (NH + 1))
+mixer_fwd_wide_kernel(Args a) {
+  constexpr int V = 4;
+  constexpr int MB = 64 * V;
+  constexpr int ESZ = sizeof(IO);
+  constexpr int SPH = S / NH;  // steps of a block per helper wave
+  static_assert(S % NH == 0 && SPH <= 64, "whole steps per helper");
+  constexpr bool PACKW = kRoundWrite<IO>;  // the writes rounded to bf16: one dword (re | im << 16) per mode
+  constexpr int NPL = PACKW ? 3 : 4;       // table planes per step: ar, ai, then w or wr, wi
+  using RawT = typename Raw<IO, V>::T;
+  __shared__ float4 tab[2][S][NPL][64];  // [buffer][step][plane][lane]: the lane's 4 modes
+
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));  // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const int idx = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int b = idx / a.n_mb, mb = idx - b * a.n_mb;
+  const int m0 = mb * MB + lane * V;
+  const bool lane_ok = m0 < a.M;  // the host requires M % 4 == 0: a lane's modes are all in or all out
+  const int T = a.T;
+  const int n_blocks = (T + S - 1) / S;
+  const int64_t row0 = static_cast<int64_t>(b) * T;
+  const int64_t mbase = static_cast<int64_t>(mb) * MB;
+  const int64_t W = 2 * static_cast<int64_t>(a.M);
+  const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
+  const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
+  const uint32_t lane_st = lane_ok ? lane_bytes : kDropOffset;
+  // bytes of one row of x / y (2M) and of h (M) (< 2^31: the host limits M to 2^24)
+  const uint32_t row_x = static_cast<uint32_t>(W * ESZ), half_x = static_cast<uint32_t>(a.M * ESZ);
+
+  // helpers: the per-mode constants and, double-buffered in registers, the
+  // x rows and (lane j < SPH) eta, delta of their steps of a block
+  const int hw = wave > 0 ? wave - 1 : 0;
+  ModeConsts<V, false> mc;
+  mc.load(a.consts, m0, lane_ok);
+  RawT xr[2][SPH], xi[2][SPH];
+  float ev[2], dv[2];
+  float hr[V], hi[V];  // wave 0: the state
+#pragma unroll
+  for (int v = 0; v < V; ++v) { hr[v] = 0.0f; hi[v] = 0.0f; }
+  wait_vm_all();  // the loop-carried constants, before the first prefetch
+
+  // rows past T re-read row T-1 (no loads under a branch)
+  auto load_block = [&](auto h_tag, int k) __attribute__((always_inline)) {
+    constexpr int h = decltype(h_tag)::value;
+    const int t0 = k * S + hw * SPH;
+    const int tb = min(t0, T - 1);
+    const int64_t off = wave_uniform(((row0 + tb) * W + mbase) * ESZ);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const char*>(a.x) + off, SPH * row_x);
+#pragma unroll
+    for (int j = 0; j < SPH; ++j) {
+      const uint32_t o = static_cast<uint32_t>(min(t0 + j, T - 1) - tb) * row_x;
+      xr[h][j] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
+      xi[h][j] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
+    }
+    const int64_t ti = row0 + min(t0 + lane % SPH, T - 1);
+    ev[h] = a.eta[ti];
+    dv[h] = a.delta[ti];
+  };
+  // a helper's steps of one block into table buffer kb
+  auto compute_block = [&](auto h_tag, int kb) __attribute__((always_inline)) {
+    constexpr int h = decltype(h_tag)::value;
+    const float ee = fast_exp(ev[h]);  // lane j: e^eta of step j
+#pragma unroll
+    for (int j = 0; j < SPH; ++j) {
+      const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), j));
+      const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), j));
+      const float E = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), j));
+      float cr[V], ci[V], ar[V], ai[V], wr[V], wi[V];
+      unpack<IO, V>(xr[h][j], cr);
+      unpack<IO, V>(xi[h][j], ci);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const StepMode q = p1_step(mc.nu[v], mc.ct[v], mc.st[v], mc.g2[v], mc.pl[v], mc.rl[v], E, eta, delta);
+        ar[v] = q.ar;
+        ai[v] = q.ai;
+        wr[v] = q.gain * tanh_fast(cr[v]);
+        wi[v] = q.gain * tanh_fast(ci[v]);
+      }
+      const int s = hw * SPH + j;
+      tab[kb][s][0][lane] = make_float4(ar[0], ar[1], ar[2], ar[3]);
+      tab[kb][s][1][lane] = make_float4(ai[0], ai[1], ai[2], ai[3]);
+      if constexpr (PACKW) {
+        float4 w;
+        w.x = __uint_as_float(pack_bf16x2(wr[0], wi[0]));
+        w.y = __uint_as_float(pack_bf16x2(wr[1], wi[1]));
+        w.z = __uint_as_float(pack_bf16x2(wr[2], wi[2]));
+        w.w = __uint_as_float(pack_bf16x2(wr[3], wi[3]));
+        tab[kb][s][2][lane] = w;
+      } else {
+        tab[kb][s][2][lane] = make_float4(wr[0], wr[1], wr[2], wr[3]);
+        tab[kb][s][NPL - 1][lane] = make_float4(wi[0], wi[1], wi[2], wi[3]);
+      }
+    }
+  };
+  // wave 0: block k from table buffer k & 1
+  auto stream_block = [&](int k) __attribute__((always_inline)) {
+    const int t0 = k * S, kb = k & 1;
+    const int64_t yoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
+    const int64_t hoff = wave_uniform(((row0 + t0) * a.M + mbase) * ESZ);
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<char*>(a.y) + yoff, S * row_x);
+    const __amdgpu_buffer_rsrc_t rhr = make_rsrc(static_cast<char*>(a.h_re) + hoff, S * half_x);
+    const __amdgpu_buffer_rsrc_t rhi = make_rsrc(static_cast<char*>(a.h_im) + hoff, S * half_x);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if (t0 + s >= T) break;  // wave-uniform
+      const float4 A = tab[kb][s][0][lane], Bv = tab[kb][s][1][lane], C = tab[kb][s][2][lane];
+      const float ar[V] = {A.x, A.y, A.z, A.w}, ai[V] = {Bv.x, Bv.y, Bv.z, Bv.w};
+      float wr[V], wi[V];
+      if constexpr (PACKW) {
+        const float c4[V] = {C.x, C.y, C.z, C.w};
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const uint32_t u = __float_as_uint(c4[v]);
+          wr[v] = __uint_as_float(u << 16);
+          wi[v] = __uint_as_float(u & 0xffff0000u);
+        }
+      } else {
+        const float4 D = tab[kb][s][NPL - 1][lane];
+        wr[0] = C.x; wr[1] = C.y; wr[2] = C.z; wr[3] = C.w;
+        wi[0] = D.x; wi[1] = D.y; wi[2] = D.z; wi[3] = D.w;
+      }
+      float rr[V], ri[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float nr = fmaf(ar[v], hr[v], fmaf(-ai[v], hi[v], wr[v]));
+        const float ni = fmaf(ai[v], hr[v], fmaf(ar[v], hi[v], wi[v]));
+        hr[v] = nr;
+        hi[v] = ni;
+        rr[v] = fmaxf(nr, 0.0f);
+        ri[v] = fmaxf(ni, 0.0f);
+      }
+      const uint32_t yo = static_cast<uint32_t>(s) * row_x, ho = static_cast<uint32_t>(s) * half_x;
+      buf_store<RawT, CPOL_NT>(pack<IO, V>(rr), ry, lane_st, yo);
+      buf_store<RawT, CPOL_NT>(pack<IO, V>(ri), ry, lane_st, yo + half_x);
+      buf_store<RawT, CPOL_NT>(pack<IO, V>(hr), rhr, lane_st, ho);
+      buf_store<RawT, CPOL_NT>(pack<IO, V>(hi), rhi, lane_st, ho);
+    }
+  };
+  // iteration k: wave 0 streams block k; the helpers prefetch block k + 2
+  // into the registers block k used and build block k + 1's table
+  auto iteration = [&](auto h_tag, int k) __attribute__((always_inline)) {
+    constexpr int h = decltype(h_tag)::value;  // k & 1
+    if (wave == 0) {
+      stream_block(k);
+    } else if (k + 1 < n_blocks) {
+      load_block(h_tag, min(k + 2, n_blocks - 1));
+      compute_block(std::integral_constant<int, 1 - h>{}, 1 - h);
+    }
+    __syncthreads();
+  };
+  if (wave > 0) {
+    load_block(std::integral_constant<int, 0>{}, 0);
+    load_block(std::integral_constant<int, 1>{}, min(1, n_blocks - 1));
+    compute_block(std::integral_constant<int, 0>{}, 0);
+  }
+  __syncthreads();
+  for (int k = 0; k < n_blocks; k += 2) {
+    iteration(std::integral_constant<int, 0>{}, k);
+    if (k + 1 < n_blocks) iteration(std::integral_constant<int, 1>{}, k + 1);
+  }
+  if (wave == 0 && lane_ok && a.last_re) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      a.last_re[static_cast<int64_t>(b) * a.M + m0 + v] = hr[v];
+      a.last_im[static_cast<int64_t>(b) * a.M + m0 + v] = hi[v];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // backward scan: one chain per workgroup of two waves, reverse time
 // ---------------------------------------------------------------------------
 // Per step t and mode, with lambda the adjoint of h_t and h' = h_{t-1}:
@@ -1317,6 +1500,35 @@ void run_bwd(const Args& a, hipStream_t st) {
   launch_bwd<IO, V, false, MODE>(a, a.n_seg, st);
 }
 
+// The module forward takes the wide kernel (4 modes per lane, four helper
+// waves, 8-step blocks) with at least kWideChains chains of 256 modes and no
+// time segments.  Forward + backward, measured against the one- and two-mode
+// kernels (bf16): B=8 T=4096 width 32768 (512 chains) 5.89 -> 5.46 ms;
+// B=16 T=2048 width 24576 (768) 4.19 -> 4.04 ms; B=32 T=1024 width 16384
+// (1024) 2.80 -> 2.81 ms; below 512 chains mixed (B=8 T=2048 width 16384 1.68
+// -> 1.64 ms, B=4 T=4096 width 32768 3.73 -> 3.91 ms, B=6 4.88 -> 4.94 ms):
+// the forward itself is faster at every one of these shapes, the backward
+// launched after it is not always as fast.  2 helper waves were slower, 8
+// helper waves or 4-step blocks the same.
+#ifndef SPARC_MIXER_WIDE
+#define SPARC_MIXER_WIDE 1
+#endif
+#ifndef SPARC_MIXER_WIDE_HELPERS
+#define SPARC_MIXER_WIDE_HELPERS 4
+#endif
+#ifndef SPARC_MIXER_WIDE_S
+#define SPARC_MIXER_WIDE_S 8
+#endif
+#ifndef SPARC_MIXER_WIDE_CHAINS
+#define SPARC_MIXER_WIDE_CHAINS 512
+#endif
+constexpr int kWideHelpers = SPARC_MIXER_WIDE_HELPERS;
+constexpr int kWideS = SPARC_MIXER_WIDE_S;
+constexpr int64_t kWideChains = SPARC_MIXER_WIDE_CHAINS;
+bool fwd_wide(const Layout& l, int64_t batch, int64_t modes) {
+  return SPARC_MIXER_WIDE && l.n_seg == 1 && modes % 4 == 0 && batch * ((modes + 255) / 256) >= kWideChains;
+}
+
 // The scan and its backward with the controls given; the per-mode constants
 // are built in the workspace first.  Shapes, pointers and the workspace are
 // checked by the callers.
@@ -1347,7 +1559,16 @@ sparc_status scan_forward_impl(const Layout& l, int64_t batch, int64_t length, i
     a.n_seg = l.n_seg; a.t_seg = l.t_seg; a.seg_lo = 0;
     a.seg_sum = reinterpret_cast<float*>(ws + l.seg_sum);
     a.seg_state = reinterpret_cast<float*>(ws + l.seg_state);
-    if (io_dtype == SPARC_BF16) {
+    if (fwd_wide(l, batch, modes)) {
+      a.n_mb = static_cast<int>((modes + 255) / 256);
+      const dim3 g(static_cast<unsigned>(batch) * static_cast<unsigned>(a.n_mb));
+      if (io_dtype == SPARC_BF16)
+        hipLaunchKernelGGL((mixer_fwd_wide_kernel<sparc::bf16, kWideHelpers, kWideS>), g, dim3(64 * (kWideHelpers + 1)),
+                           0, st, a);
+      else
+        hipLaunchKernelGGL((mixer_fwd_wide_kernel<float, kWideHelpers, kWideS>), g, dim3(64 * (kWideHelpers + 1)), 0,
+                           st, a);
+    } else if (io_dtype == SPARC_BF16) {
       if (l.V == 2) run_fwd<sparc::bf16, 2>(a, st); else run_fwd<sparc::bf16, 1>(a, st);
     } else {
       if (l.V == 2) run_fwd<float, 2>(a, st); else run_fwd<float, 1>(a, st);

@@ -402,6 +402,38 @@ def test_fused_mixer_deterministic():
         sparc_amd.set_mixer_path("auto")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_wide_forward_matches_one_mode_per_lane(dtype):
+    """With at least 512 chains of 256 modes the module forward runs the wide
+    kernel (4 modes per lane, helper waves building the step table in LDS);
+    one batch row alone has too few chains and runs the one-mode-per-lane
+    kernel.  Both compute each step value for value, so the batched outputs,
+    last states and input gradients equal the row-by-row ones bit for bit.
+    M = 16380 leaves a partial last block of modes; L = 70 a partial last
+    block of steps."""
+    B, L, width = 8, 70, 32760
+    print(f"[case] wide forward B={B} L={L} width={width} {dtype}", flush=True)
+    sparc_amd.set_mixer_path("fused")
+    try:
+        m = make_module(width, seed=21).cuda()
+        g = torch.Generator(device="cuda").manual_seed(22)
+        x = torch.randn(B, L, width, device="cuda", generator=g).to(dtype)
+        dy = torch.randn(B, L, width, device="cuda", generator=g).to(dtype)
+        dl = torch.randn(B, width // 2, device="cuda", generator=g)
+        xx = x.clone().requires_grad_()
+        y, cache = m(xx, return_cache=True)
+        (gx,) = torch.autograd.grad((y.float() * dy.float()).sum() + (cache[0] * dl).sum(), [xx])
+        for b in range(B):
+            xb = x[b:b + 1].clone().requires_grad_()
+            yb, cb = m(xb, return_cache=True)
+            (gb,) = torch.autograd.grad((yb.float() * dy[b:b + 1].float()).sum() + (cb[0] * dl[b:b + 1]).sum(), [xb])
+            assert torch.equal(y[b:b + 1], yb), f"row {b}: y"
+            assert torch.equal(cache[0][b:b + 1], cb[0]) and torch.equal(cache[1][b:b + 1], cb[1]), f"row {b}: cache"
+            assert torch.equal(gx[b:b + 1], gb), f"row {b}: dx"
+    finally:
+        sparc_amd.set_mixer_path("auto")
+
+
 def _module_vs_oracle(m, B, L, width, seed):
     g = torch.Generator().manual_seed(seed)
     x_in = torch.randn(B, L, width, generator=g, dtype=torch.float64)
