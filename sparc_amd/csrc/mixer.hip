@@ -584,27 +584,32 @@ mixer_fwd_kernel(Args a) {
 }
 
 // ---------------------------------------------------------------------------
-// module forward over wide chains: one streaming wave and NH helper waves
+// forward over wide chains: one streaming wave and NH helper waves
 // ---------------------------------------------------------------------------
 // A chain is a batch row and 256 modes (4 per lane), so that every load and
 // store moves a 512-byte piece of a row (1 KB for fp32) instead of the
-// 128-byte pieces of one mode per lane.  Wave 0 runs the recurrence and
-// stores y and the saved states; waves 1 .. NH load x and compute each
-// step's transition and write (the transcendental part of a step, SPH = S/NH
-// steps of a block each) into an LDS table one block ahead of wave 0,
-// double-buffered, with one workgroup barrier per block.  The arithmetic is
-// that of mixer_fwd_kernel in kModule, value for value, so both give the
-// same bits.  No time segments: the host takes this kernel only with enough
-// chains to fill the GPU.
-template <typename IO, int NH, int S>
+// 128-byte pieces of one mode per lane.  Wave 0 runs the recurrence and the
+// stores; waves 1 .. NH load x (kModule) or the writes (kPlanes, kRelu) and
+// compute each step's transition and write (the transcendental part of a
+// step, SPH = S/NH steps of a block each) into an LDS table one block ahead
+// of wave 0, double-buffered, with one workgroup barrier per block.  The
+// arithmetic is that of mixer_fwd_kernel in the same chain mode, value for
+// value, so both give the same bits.  No time segments: the host takes this
+// kernel only with enough chains to fill the GPU.
+template <typename IO, int NH, int S, int MODE>
 __global__ void __launch_bounds__(64 * (NH + 1))
 mixer_fwd_wide_kernel(Args a) {
   constexpr int V = 4;
   constexpr int MB = 64 * V;
   constexpr int ESZ = sizeof(IO);
   constexpr int SPH = S / NH;  // steps of a block per helper wave
-  static_assert(S % NH == 0 && SPH <= 64, "whole steps per helper");
-  constexpr bool PACKW = kRoundWrite<IO>;  // the writes rounded to bf16: one dword (re | im << 16) per mode
+  static_assert(S % NH == 0 && SPH <= 64 && kStateChunk % S == 0, "whole steps per helper, blocks tile the chunks");
+  constexpr int CM = MODE & 3;             // the chain mode without kReset
+  constexpr bool RST = (MODE & kReset) != 0;
+  constexpr bool GW = CM != kModule;       // the writes are given
+  static_assert(GW || !RST, "resets in the P1 scan only");
+  constexpr bool PACKW = sizeof(IO) == 2;  // bf16 writes: one dword (re | im << 16) per mode
+  static_assert(GW || PACKW == kRoundWrite<IO>, "the module's bf16 writes are rounded to bf16");
   constexpr int NPL = PACKW ? 3 : 4;       // table planes per step: ar, ai, then w or wr, wi
   using RawT = typename Raw<IO, V>::T;
   __shared__ float4 tab[2][S][NPL][64];  // [buffer][step][plane][lane]: the lane's 4 modes
@@ -623,37 +628,57 @@ mixer_fwd_wide_kernel(Args a) {
   const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
   const uint32_t lane_ld = lane_ok ? lane_bytes : 0u;
   const uint32_t lane_st = lane_ok ? lane_bytes : kDropOffset;
-  // bytes of one row of x / y (2M) and of h (M) (< 2^31: the host limits M to 2^24)
+  // bytes of one row of x / y (2M) and of h / w (M) (< 2^31: the host limits M to 2^24)
   const uint32_t row_x = static_cast<uint32_t>(W * ESZ), half_x = static_cast<uint32_t>(a.M * ESZ);
 
   // helpers: the per-mode constants and, double-buffered in registers, the
-  // x rows and (lane j < SPH) eta, delta of their steps of a block
+  // rows of x or of the writes and (lane j < SPH) eta, delta (and whether the
+  // step keeps its transition) of their steps of a block
   const int hw = wave > 0 ? wave - 1 : 0;
   ModeConsts<V, false> mc;
   mc.load(a.consts, m0, lane_ok);
   RawT xr[2][SPH], xi[2][SPH];
   float ev[2], dv[2];
-  float hr[V], hi[V];  // wave 0: the state
+  int kv[2];
+  // wave 0: the state, from the caller's initial state (the P1 scan) or zero
+  float hr[V], hi[V];
 #pragma unroll
-  for (int v = 0; v < V; ++v) { hr[v] = 0.0f; hi[v] = 0.0f; }
-  wait_vm_all();  // the loop-carried constants, before the first prefetch
+  for (int v = 0; v < V; ++v) {
+    const bool h0 = GW && wave == 0 && lane_ok && a.h0_re != nullptr;
+    hr[v] = h0 ? a.h0_re[static_cast<int64_t>(b) * a.M + m0 + v] : 0.0f;
+    hi[v] = h0 ? a.h0_im[static_cast<int64_t>(b) * a.M + m0 + v] : 0.0f;
+  }
+  wait_vm_all();  // the loop-carried constants and state, before the first prefetch
 
   // rows past T re-read row T-1 (no loads under a branch)
   auto load_block = [&](auto h_tag, int k) __attribute__((always_inline)) {
     constexpr int h = decltype(h_tag)::value;
     const int t0 = k * S + hw * SPH;
     const int tb = min(t0, T - 1);
-    const int64_t off = wave_uniform(((row0 + tb) * W + mbase) * ESZ);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const char*>(a.x) + off, SPH * row_x);
+    if constexpr (GW) {
+      const int64_t off = wave_uniform(((row0 + tb) * a.M + mbase) * ESZ);
+      const __amdgpu_buffer_rsrc_t rwr = make_rsrc(static_cast<const char*>(a.w_re) + off, SPH * half_x);
+      const __amdgpu_buffer_rsrc_t rwi = make_rsrc(static_cast<const char*>(a.w_im) + off, SPH * half_x);
 #pragma unroll
-    for (int j = 0; j < SPH; ++j) {
-      const uint32_t o = static_cast<uint32_t>(min(t0 + j, T - 1) - tb) * row_x;
-      xr[h][j] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
-      xi[h][j] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
+      for (int j = 0; j < SPH; ++j) {
+        const uint32_t o = static_cast<uint32_t>(min(t0 + j, T - 1) - tb) * half_x;
+        xr[h][j] = buf_load<RawT, CPOL_NT>(rwr, lane_ld, o);
+        xi[h][j] = buf_load<RawT, CPOL_NT>(rwi, lane_ld, o);
+      }
+    } else {
+      const int64_t off = wave_uniform(((row0 + tb) * W + mbase) * ESZ);
+      const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const char*>(a.x) + off, SPH * row_x);
+#pragma unroll
+      for (int j = 0; j < SPH; ++j) {
+        const uint32_t o = static_cast<uint32_t>(min(t0 + j, T - 1) - tb) * row_x;
+        xr[h][j] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
+        xi[h][j] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
+      }
     }
-    const int64_t ti = row0 + min(t0 + lane % SPH, T - 1);
-    ev[h] = a.eta[ti];
-    dv[h] = a.delta[ti];
+    const int tl = min(t0 + lane % SPH, T - 1);
+    ev[h] = a.eta[row0 + tl];
+    dv[h] = a.delta[row0 + tl];
+    if constexpr (RST) kv[h] = p1_keep(a, b, tl);
   };
   // a helper's steps of one block into table buffer kb
   auto compute_block = [&](auto h_tag, int kb) __attribute__((always_inline)) {
@@ -664,31 +689,65 @@ mixer_fwd_wide_kernel(Args a) {
       const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), j));
       const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), j));
       const float E = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), j));
-      float cr[V], ci[V], ar[V], ai[V], wr[V], wi[V];
-      unpack<IO, V>(xr[h][j], cr);
-      unpack<IO, V>(xi[h][j], ci);
+      float ar[V], ai[V];
+      float4 w0, w1;  // the table's write plane(s)
+      if constexpr (GW) {
+        // the transition of p1_step (p1_block_transitions), a := 0 at a reset step
+        const bool keep = !RST || __builtin_amdgcn_readlane(kv[h], j) != 0;  // wave-uniform
+        float q[V], em[V], u[V], su[V], cu[V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        const StepMode q = p1_step(mc.nu[v], mc.ct[v], mc.st[v], mc.g2[v], mc.pl[v], mc.rl[v], E, eta, delta);
-        ar[v] = q.ar;
-        ai[v] = q.ai;
-        wr[v] = q.gain * tanh_fast(cr[v]);
-        wi[v] = q.gain * tanh_fast(ci[v]);
+        for (int v = 0; v < V; ++v) q[v] = -mc.nu[v] * E;
+        expm1_nonpos_n<V>(q, em);
+#pragma unroll
+        for (int v = 0; v < V; ++v) u[v] = -em[v] * delta;
+        sincos_half_n<V>(u, su, cu);
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const float rho = 1.0f + em[v];
+          ar[v] = keep ? rho * fmaf(mc.ct[v], cu[v], -mc.st[v] * su[v]) : 0.0f;
+          ai[v] = keep ? rho * fmaf(mc.st[v], cu[v], mc.ct[v] * su[v]) : 0.0f;
+        }
+        if constexpr (PACKW) {  // the raw bf16 writes, re in the low half of each dword
+          const uint32_t* r = reinterpret_cast<const uint32_t*>(&xr[h][j]);
+          const uint32_t* i = reinterpret_cast<const uint32_t*>(&xi[h][j]);
+          w0.x = __uint_as_float((r[0] & 0xffffu) | (i[0] << 16));
+          w0.y = __uint_as_float((r[0] >> 16) | (i[0] & 0xffff0000u));
+          w0.z = __uint_as_float((r[1] & 0xffffu) | (i[1] << 16));
+          w0.w = __uint_as_float((r[1] >> 16) | (i[1] & 0xffff0000u));
+        } else {
+          float wr[V], wi[V];
+          unpack<IO, V>(xr[h][j], wr);
+          unpack<IO, V>(xi[h][j], wi);
+          w0 = make_float4(wr[0], wr[1], wr[2], wr[3]);
+          w1 = make_float4(wi[0], wi[1], wi[2], wi[3]);
+        }
+      } else {
+        float cr[V], ci[V], wr[V], wi[V];
+        unpack<IO, V>(xr[h][j], cr);
+        unpack<IO, V>(xi[h][j], ci);
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const StepMode q = p1_step(mc.nu[v], mc.ct[v], mc.st[v], mc.g2[v], mc.pl[v], mc.rl[v], E, eta, delta);
+          ar[v] = q.ar;
+          ai[v] = q.ai;
+          wr[v] = q.gain * tanh_fast(cr[v]);
+          wi[v] = q.gain * tanh_fast(ci[v]);
+        }
+        if constexpr (PACKW) {  // rounded to bf16, as round_bf16x2
+          w0.x = __uint_as_float(pack_bf16x2(wr[0], wi[0]));
+          w0.y = __uint_as_float(pack_bf16x2(wr[1], wi[1]));
+          w0.z = __uint_as_float(pack_bf16x2(wr[2], wi[2]));
+          w0.w = __uint_as_float(pack_bf16x2(wr[3], wi[3]));
+        } else {
+          w0 = make_float4(wr[0], wr[1], wr[2], wr[3]);
+          w1 = make_float4(wi[0], wi[1], wi[2], wi[3]);
+        }
       }
       const int s = hw * SPH + j;
       tab[kb][s][0][lane] = make_float4(ar[0], ar[1], ar[2], ar[3]);
       tab[kb][s][1][lane] = make_float4(ai[0], ai[1], ai[2], ai[3]);
-      if constexpr (PACKW) {
-        float4 w;
-        w.x = __uint_as_float(pack_bf16x2(wr[0], wi[0]));
-        w.y = __uint_as_float(pack_bf16x2(wr[1], wi[1]));
-        w.z = __uint_as_float(pack_bf16x2(wr[2], wi[2]));
-        w.w = __uint_as_float(pack_bf16x2(wr[3], wi[3]));
-        tab[kb][s][2][lane] = w;
-      } else {
-        tab[kb][s][2][lane] = make_float4(wr[0], wr[1], wr[2], wr[3]);
-        tab[kb][s][NPL - 1][lane] = make_float4(wi[0], wi[1], wi[2], wi[3]);
-      }
+      tab[kb][s][2][lane] = w0;
+      if constexpr (!PACKW) tab[kb][s][NPL - 1][lane] = w1;
     }
   };
   // wave 0: block k from table buffer k & 1
@@ -696,9 +755,9 @@ mixer_fwd_wide_kernel(Args a) {
     const int t0 = k * S, kb = k & 1;
     const int64_t yoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
     const int64_t hoff = wave_uniform(((row0 + t0) * a.M + mbase) * ESZ);
-    const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<char*>(a.y) + yoff, S * row_x);
-    const __amdgpu_buffer_rsrc_t rhr = make_rsrc(static_cast<char*>(a.h_re) + hoff, S * half_x);
-    const __amdgpu_buffer_rsrc_t rhi = make_rsrc(static_cast<char*>(a.h_im) + hoff, S * half_x);
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<char*>(a.y) + yoff, CM != kPlanes ? S * row_x : 0u);
+    const __amdgpu_buffer_rsrc_t rhr = make_rsrc(static_cast<char*>(a.h_re) + hoff, CM != kRelu ? S * half_x : 0u);
+    const __amdgpu_buffer_rsrc_t rhi = make_rsrc(static_cast<char*>(a.h_im) + hoff, CM != kRelu ? S * half_x : 0u);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       if (t0 + s >= T) break;  // wave-uniform
@@ -728,11 +787,29 @@ mixer_fwd_wide_kernel(Args a) {
         rr[v] = fmaxf(nr, 0.0f);
         ri[v] = fmaxf(ni, 0.0f);
       }
-      const uint32_t yo = static_cast<uint32_t>(s) * row_x, ho = static_cast<uint32_t>(s) * half_x;
-      buf_store<RawT, CPOL_NT>(pack<IO, V>(rr), ry, lane_st, yo);
-      buf_store<RawT, CPOL_NT>(pack<IO, V>(ri), ry, lane_st, yo + half_x);
-      buf_store<RawT, CPOL_NT>(pack<IO, V>(hr), rhr, lane_st, ho);
-      buf_store<RawT, CPOL_NT>(pack<IO, V>(hi), rhi, lane_st, ho);
+      if constexpr (CM != kPlanes) {  // y = relu(cat(h_re, h_im))
+        const uint32_t yo = static_cast<uint32_t>(s) * row_x;
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(rr), ry, lane_st, yo);
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(ri), ry, lane_st, yo + half_x);
+      }
+      if constexpr (CM != kRelu) {  // the states
+        const uint32_t ho = static_cast<uint32_t>(s) * half_x;
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(hr), rhr, lane_st, ho);
+        buf_store<RawT, CPOL_NT>(pack<IO, V>(hi), rhi, lane_st, ho);
+      }
+    }
+    if constexpr (GW) {
+      // the state after the last step of every 64-step chunk and after T-1
+      const int t_last = min(t0 + S, T) - 1;
+      if ((t_last + 1) % kStateChunk == 0 || t_last == T - 1) {  // wave-uniform
+        const int64_t n_chunks = (T + kStateChunk - 1) / kStateChunk;
+        const int64_t off = wave_uniform(((static_cast<int64_t>(b) * n_chunks + t_last / kStateChunk) * a.M + mbase) * 8);
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(reinterpret_cast<char*>(a.chunk_state) + off, MB * 8u);
+        const float o0[4] = {hr[0], hi[0], hr[1], hi[1]}, o1[4] = {hr[2], hi[2], hr[3], hi[3]};
+        const uint32_t co = static_cast<uint32_t>(lane * V * 8);
+        buffer_store_f32<4, CPOL_DEFAULT>(rc, lane_ok ? co : kDropOffset, o0);
+        buffer_store_f32<4, CPOL_DEFAULT>(rc, lane_ok ? co + 16u : kDropOffset, o1);
+      }
     }
   };
   // iteration k: wave 0 streams block k; the helpers prefetch block k + 2
@@ -1529,6 +1606,14 @@ bool fwd_wide(const Layout& l, int64_t batch, int64_t modes) {
   return SPARC_MIXER_WIDE && l.n_seg == 1 && modes % 4 == 0 && batch * ((modes + 255) / 256) >= kWideChains;
 }
 
+// the wide forward (a.n_mb: blocks of 256 modes)
+template <int MODE>
+void run_fwd_wide(const Args& a, bool bf, hipStream_t st) {
+  const dim3 g(static_cast<unsigned>(a.B) * static_cast<unsigned>(a.n_mb)), blk(64 * (kWideHelpers + 1));
+  if (bf) hipLaunchKernelGGL((mixer_fwd_wide_kernel<sparc::bf16, kWideHelpers, kWideS, MODE>), g, blk, 0, st, a);
+  else hipLaunchKernelGGL((mixer_fwd_wide_kernel<float, kWideHelpers, kWideS, MODE>), g, blk, 0, st, a);
+}
+
 // The scan and its backward with the controls given; the per-mode constants
 // are built in the workspace first.  Shapes, pointers and the workspace are
 // checked by the callers.
@@ -1561,13 +1646,7 @@ sparc_status scan_forward_impl(const Layout& l, int64_t batch, int64_t length, i
     a.seg_state = reinterpret_cast<float*>(ws + l.seg_state);
     if (fwd_wide(l, batch, modes)) {
       a.n_mb = static_cast<int>((modes + 255) / 256);
-      const dim3 g(static_cast<unsigned>(batch) * static_cast<unsigned>(a.n_mb));
-      if (io_dtype == SPARC_BF16)
-        hipLaunchKernelGGL((mixer_fwd_wide_kernel<sparc::bf16, kWideHelpers, kWideS>), g, dim3(64 * (kWideHelpers + 1)),
-                           0, st, a);
-      else
-        hipLaunchKernelGGL((mixer_fwd_wide_kernel<float, kWideHelpers, kWideS>), g, dim3(64 * (kWideHelpers + 1)), 0,
-                           st, a);
+      run_fwd_wide<kModule>(a, io_dtype == SPARC_BF16, st);
     } else if (io_dtype == SPARC_BF16) {
       if (l.V == 2) run_fwd<sparc::bf16, 2>(a, st); else run_fwd<sparc::bf16, 1>(a, st);
     } else {
@@ -1719,7 +1798,13 @@ sparc_status p1_fused_forward(const sparc_scan_desc* d, const float* eta, const 
   a.seg_sum = reinterpret_cast<float*>(ws + l.seg_sum);
   a.seg_state = reinterpret_cast<float*>(ws + l.seg_state);
   const bool bf = d->io_dtype == SPARC_BF16;
-  if (relu && reset) run_fwd_mode<kRelu | kReset>(a, bf, l.V, st);
+  if (fwd_wide(l, d->batch, d->modes)) {
+    a.n_mb = static_cast<int>((d->modes + 255) / 256);
+    if (relu && reset) run_fwd_wide<kRelu | kReset>(a, bf, st);
+    else if (relu) run_fwd_wide<kRelu>(a, bf, st);
+    else if (reset) run_fwd_wide<kPlanes | kReset>(a, bf, st);
+    else run_fwd_wide<kPlanes>(a, bf, st);
+  } else if (relu && reset) run_fwd_mode<kRelu | kReset>(a, bf, l.V, st);
   else if (relu) run_fwd_mode<kRelu>(a, bf, l.V, st);
   else if (reset) run_fwd_mode<kPlanes | kReset>(a, bf, l.V, st);
   else run_fwd_mode<kPlanes>(a, bf, l.V, st);

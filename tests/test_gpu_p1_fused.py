@@ -82,3 +82,40 @@ def test_p1_fused_chunk_states(B, T, M, relu):
     assert rel_err(yf_re, yc_re) <= 1e-4
     if not relu:
         assert rel_err(yf_im, yc_im) <= 1e-4
+
+
+@pytest.mark.parametrize("dtype,extra", [
+    (BF16, dict(h0=True)),
+    (F32, dict(h0=True)),
+    (BF16, dict(relu=True)),
+    (F32, dict(h0=True, seg=True, reset_first=True)),
+], ids=["planes_h0_bf16", "planes_h0_f32", "relu_bf16", "resets_h0_f32"])
+def test_p1_wide_forward_matches_one_mode_per_lane(dtype, extra):
+    """With at least 512 chains of 256 modes the P1 forward runs the wide
+    kernel (4 modes per lane, helper waves building the transitions in LDS);
+    one batch row alone has too few chains and runs the one-mode-per-lane
+    kernel.  Both compute each step value for value: the batched outputs and
+    chunk states equal the row-by-row ones bit for bit.  M = 16380 leaves a
+    partial last block of modes, T = 70 a partial last block of steps and a
+    partial last chunk."""
+    B, T, M = 8, 70, 16380
+    print(f"[case] p1 wide forward B={B} T={T} M={M} {dtype} {extra}", flush=True)
+    case = make_case("p1", B, T, M, 1, dtype, seed=31, **extra)
+    segpos = None if case["segpos"] is None else case["segpos"].cuda()
+    init = case["init"]
+
+    def fwd(rows):
+        h0 = (None, None) if init is None else tuple(t[rows].cuda() for t in init)
+        sp = None if segpos is None else segpos[rows]
+        return ops.scan_forward_raw(
+            "p1", case["g0"][rows].cuda(), case["g1"][rows].cuda(), case["w_re"][rows].cuda(),
+            case["w_im"][rows].cuda(), case["nu_log"].cuda(), case["theta_log"].cuda(), h0[0], h0[1], sp,
+            case["reset_first"], case["relu"])
+
+    y_re, y_im, cs = fwd(slice(0, B))
+    for b in range(B):
+        r_re, r_im, rc = fwd(slice(b, b + 1))
+        assert torch.equal(y_re[b:b + 1], r_re), f"row {b}: y_re"
+        if not case["relu"]:
+            assert torch.equal(y_im[b:b + 1], r_im), f"row {b}: y_im"
+        assert torch.equal(cs[b:b + 1], rc), f"row {b}: chunk states"
