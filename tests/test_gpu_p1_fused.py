@@ -41,6 +41,11 @@ CASES = [
     ("resets_relu_f32", 2, 130, 128, F32, dict(h0=True, seg=True, relu=True)),
     ("resets_segments_h0_f32", 1, 3000, 64, F32, dict(h0=True, dlast=True, seg=True)),
     ("reset_first_segments_bf16", 2, 2500, 128, BF16, dict(h0=True, dlast=True, reset_first=True)),
+    # 512 chains of 256 modes: the wide forward; a partial last block of modes
+    # and of steps
+    ("wide_h0_dlast_bf16", 8, 70, 16380, BF16, dict(h0=True, dlast=True)),
+    ("wide_resets_reset_first_bf16", 8, 70, 16380, BF16, dict(h0=True, dlast=True, seg=True, reset_first=True)),
+    ("wide_h0_f32", 8, 37, 16384, F32, dict(h0=True, dlast=True)),
 ]
 
 
