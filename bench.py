@@ -311,9 +311,10 @@ def bench_p1(args, dev):
     from per-token eta, delta and per-mode nu_log, theta_log; writes given) at
     the headline shape: B=8, T=4096, M=16384, one gate pair per token (G = 1),
     bf16 writes, fp32 eta/delta, fp32 state.  Forward and backward through the
-    C ABI; at G = 1 they run the one-wave-per-chain fused kernels
-    (mixer_fwd_kernel / mixer_bwd_kernel with the writes given), the backward
-    reading the states from the forward's output.  Beside it the few-chain
+    C ABI; at G = 1 they run the fused kernels with the writes given (the
+    forward on chains of 256 modes with helper waves, mixer_fwd_wide_kernel;
+    the backward one wave per chain of 64 modes, mixer_bwd_kernel), the
+    backward reading the states from the forward's output.  Beside it the few-chain
     form, B=1, T=65536, M=2048 (32 chains of 64 modes, split into time
     segments: a summary pass, the carry, a replay)."""
     B, T, M = 8, 4096, 16384
@@ -323,7 +324,7 @@ def bench_p1(args, dev):
     ms_step = elapsed * 1e3 / steps
     traffic = measured_traffic(COUNTERS_FILE)
     valu = measured_valu_busy()
-    kf, kb = "mixer_fwd_kernel (writes given)", "mixer_bwd_kernel (writes given)"
+    kf, kb = "mixer_fwd_wide_kernel (writes given)", "mixer_bwd_kernel (writes given)"
     Bf, Tf, Mf, sf = 1, 65536, 2048, 10
     ff_ms, fb_ms, fel = _p1_timed(dev, Bf, Tf, Mf, sf)
     fbf, fbb = _p1_bytes(Bf, Tf, Mf)
@@ -334,12 +335,12 @@ def bench_p1(args, dev):
         "tokens_per_s": round(B * T * steps / elapsed, 1), "ms_per_step": round(ms_step, 4),
         "step_frac": round((bytes_fwd + bytes_bwd) / ms_step / 1e6 / HBM_PEAK_GBS, 4),
         "forward": {"kernel": kf, "avg_launch_ms": round(fwd_ms, 4), "bytes_per_launch": bytes_fwd,
-                    "traffic": traffic.get("mixer_fwd_kernel_p1"), "valu_busy_pct": valu.get("mixer_fwd_kernel_p1"),
+                    "traffic": traffic.get("mixer_fwd_wide_kernel_p1"), "valu_busy_pct": valu.get("mixer_fwd_wide_kernel_p1"),
                     "frac": round(bytes_fwd / fwd_ms / 1e6 / HBM_PEAK_GBS, 4)},
         "backward": {"kernel": kb, "avg_launch_ms": round(bwd_ms, 4), "bytes_per_launch": bytes_bwd,
                      "traffic": traffic.get("mixer_bwd_kernel_p1"), "valu_busy_pct": valu.get("mixer_bwd_kernel_p1"),
                      "frac": round(bytes_bwd / bwd_ms / 1e6 / HBM_PEAK_GBS, 4)},
-        "counters_source": COUNTERS_FILE if "mixer_fwd_kernel_p1" in traffic else None,
+        "counters_source": COUNTERS_FILE if "mixer_fwd_wide_kernel_p1" in traffic else None,
         "few_chains": {
             "workload": "P1 chunk scan fwd+bwd, few long chains (time segments)",
             "B": Bf, "T": Tf, "M": Mf, "G": 1, "steps": sf, "ms_per_step": round(fms, 4),
@@ -449,7 +450,7 @@ def bench_module(args, dev):
     # of M (x in, y out; dy in, x in, dx out) and 6 fp32 control values
     M = W // 2
     algo_bytes = B * T * (M * 10 * 2 + 6 * 4)
-    kernels = ("ctrl_fwd_kernel", "mixer_fwd_kernel", "mixer_bwd_kernel", "ctrl_bwd_kernel")
+    kernels = ("ctrl_fwd_kernel", "mixer_fwd_wide_kernel", "mixer_bwd_kernel", "ctrl_bwd_kernel")
     traffic = measured_traffic(COUNTERS_FILE)
     valu = measured_valu_busy()
     measured = sum(traffic[k] for k in kernels) if path == "fused" and all(k in traffic for k in kernels) else None
