@@ -2877,7 +2877,11 @@ constexpr int kStateChunk = 64;  // steps per saved chunk state
 #define SPARC_GATE_DEPTH 4
 #endif
 constexpr int kGateDepth = SPARC_GATE_DEPTH;
-static_assert(kGateDepth % 2 == 0 && kGateDepth >= 2, "the loops pair plane buffers with even depths");
+// At least 4: a block's gates are loaded kGateDepth-1 blocks ahead and its
+// table is built from them one block ahead, so the load must come at least two
+// iterations before the build (the loops issue an iteration's load after its
+// build).
+static_assert(kGateDepth % 2 == 0 && kGateDepth >= 4, "the loops pair plane buffers with even depths, 4 or more");
 #ifndef SPARC_SERIAL_SWIZZLE
 #define SPARC_SERIAL_SWIZZLE 1
 #endif
