@@ -1436,8 +1436,15 @@ bool al(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) =
 // more resident waves hide the latency of its dependent arithmetic.
 // Backward: the fixed choice (its per-step working set is twice the
 // forward's).
-int mixer_v(int64_t B, int64_t M, int direction) {
-  const int fixed = direction == 0 ? SPARC_MIXER_FWD_V : SPARC_MIXER_BWD_V;
+// The P1 scan's backward (writes given) with two modes per lane: 1.58-1.59 ->
+// 1.46-1.49 ms at B=8, T=4096, M=16384 (1024 waves); the module's backward
+// was slower with two (3.75 -> 3.87-3.95 ms at width 32768, 2.80 -> 3.08 ms at
+// B=16, width 24576).
+#ifndef SPARC_P1_BWD_V
+#define SPARC_P1_BWD_V 2
+#endif
+int mixer_v(int64_t B, int64_t M, int direction, bool gw) {
+  const int fixed = direction == 0 ? SPARC_MIXER_FWD_V : gw ? SPARC_P1_BWD_V : SPARC_MIXER_BWD_V;
   if (fixed == 1 || M % 2) return 1;
   if (fixed == 2) return 2;
   const int64_t chains2 = B * ((M + 127) / 128);
@@ -1488,7 +1495,7 @@ struct Layout {
 // gw: the P1 scan with the writes given (no controls, two per-mode gradients)
 Layout layout(int64_t B, int64_t T, int64_t M, int direction, bool gw = false) {
   Layout l;
-  l.V = mixer_v(B, M, direction);
+  l.V = mixer_v(B, M, direction, gw);
   l.n_mb = static_cast<int>((M + 64 * l.V - 1) / (64 * l.V));
   choose_segments(B, T, l.n_mb, l.n_seg, l.t_seg);
   l.R = B * T;
