@@ -1433,7 +1433,11 @@ bool al(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) =
 // 256-CU MI355X), else 1 (twice the chains).  Measured at B=8, M=16384 (1024
 // chains of 2): 1 mode per lane 2.3 ms against 2.8 ms; at B=16, M=12288 (1536
 // chains of 2): 2 modes 1.4 ms against 1.5 ms.  The forward is VALU-bound:
-// more resident waves hide the latency of its dependent arithmetic.
+// more resident waves hide the latency of its dependent arithmetic.  (Both
+// shapes now take the wide kernel.)  Also 2 when one mode per lane would be
+// split into time segments anyway: the P1 forward at B=1, T=65536, M=2048
+// 0.443 -> 0.405 ms, at B=2, T=16384, M=8192 0.84 -> 0.77 ms, the module
+// step at B=1, T=65536, width 2048 1.11 -> 1.08 ms.
 // Backward: the fixed choice (its per-step working set is twice the
 // forward's).
 // The P1 scan's backward (writes given) with two modes per lane: 1.58-1.59 ->
@@ -1443,13 +1447,7 @@ bool al(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) =
 #ifndef SPARC_P1_BWD_V
 #define SPARC_P1_BWD_V 2
 #endif
-int mixer_v(int64_t B, int64_t M, int direction, bool gw) {
-  const int fixed = direction == 0 ? SPARC_MIXER_FWD_V : gw ? SPARC_P1_BWD_V : SPARC_MIXER_BWD_V;
-  if (fixed == 1 || M % 2) return 1;
-  if (fixed == 2) return 2;
-  const int64_t chains2 = B * ((M + 127) / 128);
-  return chains2 >= 1280 ? 2 : 1;
-}
+int mixer_v(int64_t B, int64_t T, int64_t M, int direction, bool gw);
 
 // Time segments.  One wave per chain (batch row x 64 V modes) walks its
 // whole sequence, so with fewer chains than SIMDs most of the GPU idles.
@@ -1471,6 +1469,14 @@ constexpr int64_t kSegChains = SPARC_MIXER_SEG_CHAINS;  // segment below this ma
 #endif
 constexpr int64_t kSegTarget = SPARC_MIXER_SEG_TARGET;  // waves to aim for
 constexpr int64_t kMinSegSteps = SPARC_MIXER_SEG_MIN;
+int mixer_v(int64_t B, int64_t T, int64_t M, int direction, bool gw) {
+  const int fixed = direction == 0 ? SPARC_MIXER_FWD_V : gw ? SPARC_P1_BWD_V : SPARC_MIXER_BWD_V;
+  if (fixed == 1 || M % 2) return 1;
+  if (fixed == 2) return 2;
+  const int64_t chains1 = B * ((M + 63) / 64), chains2 = B * ((M + 127) / 128);
+  const bool segmented = chains1 < kSegChains && T >= 2 * kMinSegSteps;  // with one mode per lane
+  return chains2 >= 1280 || segmented ? 2 : 1;
+}
 void choose_segments(int64_t B, int64_t T, int n_mb, int& n_seg, int& t_seg) {
   n_seg = 1;
   t_seg = static_cast<int>(T > 0 ? T : 1);
@@ -1495,7 +1501,7 @@ struct Layout {
 // gw: the P1 scan with the writes given (no controls, two per-mode gradients)
 Layout layout(int64_t B, int64_t T, int64_t M, int direction, bool gw = false) {
   Layout l;
-  l.V = mixer_v(B, M, direction, gw);
+  l.V = mixer_v(B, T, M, direction, gw);
   l.n_mb = static_cast<int>((M + 64 * l.V - 1) / (64 * l.V));
   choose_segments(B, T, l.n_mb, l.n_seg, l.t_seg);
   l.R = B * T;
