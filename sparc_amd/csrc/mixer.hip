@@ -1427,7 +1427,7 @@ bool al(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) =
 #define SPARC_MIXER_FWD_V 0
 #endif
 #ifndef SPARC_MIXER_BWD_V
-#define SPARC_MIXER_BWD_V 1
+#define SPARC_MIXER_BWD_V 0
 #endif
 // Forward: 2 when that leaves at least 1280 chains (1.25 waves per SIMD of the
 // 256-CU MI355X), else 1 (twice the chains).  Measured at B=8, M=16384 (1024
@@ -1438,12 +1438,12 @@ bool al(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) =
 // split into time segments anyway: the P1 forward at B=1, T=65536, M=2048
 // 0.443 -> 0.405 ms, at B=2, T=16384, M=8192 0.84 -> 0.77 ms, the module
 // step at B=1, T=65536, width 2048 1.11 -> 1.08 ms.
-// Backward: the fixed choice (its per-step working set is twice the
-// forward's).
+// Backward (module): 1, or 2 when one mode per lane would be split into time
+// segments anyway (B=1, T=65536, width 2048: 1.08 -> 1.05-1.06 ms per step);
+// with many chains 2 was slower (3.75 -> 3.87-3.95 ms at B=8, width 32768).
 // The P1 scan's backward (writes given) with two modes per lane: 1.58-1.59 ->
-// 1.46-1.49 ms at B=8, T=4096, M=16384 (1024 waves); the module's backward
-// was slower with two (3.75 -> 3.87-3.95 ms at width 32768, 2.80 -> 3.08 ms at
-// B=16, width 24576).
+// 1.46-1.49 ms at B=8, T=4096, M=16384 (1024 waves), faster at every shape
+// measured.
 #ifndef SPARC_P1_BWD_V
 #define SPARC_P1_BWD_V 2
 #endif
@@ -1475,6 +1475,7 @@ int mixer_v(int64_t B, int64_t T, int64_t M, int direction, bool gw) {
   if (fixed == 2) return 2;
   const int64_t chains1 = B * ((M + 63) / 64), chains2 = B * ((M + 127) / 128);
   const bool segmented = chains1 < kSegChains && T >= 2 * kMinSegSteps;  // with one mode per lane
+  if (direction == 1) return segmented ? 2 : 1;
   return chains2 >= 1280 || segmented ? 2 : 1;
 }
 void choose_segments(int64_t B, int64_t T, int n_mb, int& n_seg, int& t_seg) {
