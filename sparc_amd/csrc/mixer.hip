@@ -862,8 +862,9 @@ mixer_fwd_wide_kernel(Args a) {
 //   d wlg += g, d wpr += g (1 - sig) delta 2/pi, d wrr += g (1 - sig) eta / log16
 // (the P1 chain rule of sparc-kernal/backward/scan.py:593-644 and the write
 // gradients of sparc-kernal/backward/control.py:10-89).
+// two waves per SIMD; one for the P1 scan's 16-step blocks (about 256 VGPRs)
 template <typename IO, int V, int kS, bool SUMMARY, int MODE>
-__global__ void __launch_bounds__(64, 2)
+__global__ void __launch_bounds__(64, (MODE & 3) == kPlanes && kS >= 16 ? 1 : 2)
 mixer_bwd_kernel(Args a) {
   using RawT = typename Raw<IO, V>::T;
   constexpr int ESZ = sizeof(IO);
@@ -1570,7 +1571,14 @@ void run_fwd(const Args& a, hipStream_t st) {
 // at most two waves per SIMD of the 1024 (B=8, T=4096, width 32768: 3.85 ->
 // 3.75 ms; B=16, T=2048, width 24576, 3072 waves: 2.77 -> 2.81 ms with 8).
 // The P1 scan (writes given) fits 8-step blocks in about 147 VGPRs: 1.61 ->
-// 1.52 ms at B=8, T=4096, M=16384, and faster with time segments too.
+// 1.52 ms at B=8, T=4096, M=16384, and faster with time segments too.  At two
+// modes per lane and without time segments it takes 16-step blocks at one
+// wave per SIMD (B=8, T=4096, M=16384: 1.43 -> 1.39 ms; B=16, T=2048: 1.42 ->
+// 1.34 ms); with time segments (4096 waves) those were slower (0.52 -> 0.58
+// ms at B=1, T=65536, M=2048).
+#ifndef SPARC_MIXER_BWD_P1_S
+#define SPARC_MIXER_BWD_P1_S 16
+#endif
 #ifndef SPARC_MIXER_BWD_S
 #define SPARC_MIXER_BWD_S 4
 #endif
@@ -1585,6 +1593,12 @@ void launch_bwd(const Args& a, int n_segs, hipStream_t st) {
   if constexpr ((MODE & 3) == kModule && V == 1) {
     if (waves <= kBwdLongWaves) {
       hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, SPARC_MIXER_BWD_LONG_S, SUMMARY, MODE>), g, dim3(64), 0, st, a);
+      return;
+    }
+  }
+  if constexpr ((MODE & 3) != kModule) {
+    if (a.n_seg == 1) {  // no time segments: 16-step blocks, one wave per SIMD
+      hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, SPARC_MIXER_BWD_P1_S, SUMMARY, MODE>), g, dim3(64), 0, st, a);
       return;
     }
   }
