@@ -1642,8 +1642,15 @@ void run_bwd(const Args& a, hipStream_t st) {
 constexpr int kWideHelpers = SPARC_MIXER_WIDE_HELPERS;
 constexpr int kWideS = SPARC_MIXER_WIDE_S;
 constexpr int64_t kWideChains = SPARC_MIXER_WIDE_CHAINS;
-bool fwd_wide(const Layout& l, int64_t batch, int64_t modes) {
-  return SPARC_MIXER_WIDE && l.n_seg == 1 && modes % 4 == 0 && batch * ((modes + 255) / 256) >= kWideChains;
+// The module forward above 1024 such chains keeps the two-mode kernel (B=32,
+// T=1024, width 32768, 2048 chains: 5.21-5.23 against 5.30-5.43 ms per step;
+// at 1024 chains the two are even); the P1 forward takes the wide kernel at
+// every count measured (up to 2048 chains).
+constexpr int64_t kWideChainsMaxModule = 1024;
+bool fwd_wide(const Layout& l, int64_t batch, int64_t modes, bool module = false) {
+  const int64_t chains = batch * ((modes + 255) / 256);
+  return SPARC_MIXER_WIDE && l.n_seg == 1 && modes % 4 == 0 && chains >= kWideChains &&
+         (!module || chains <= kWideChainsMaxModule);
 }
 
 // the wide forward (a.n_mb: blocks of 256 modes)
@@ -1684,7 +1691,7 @@ sparc_status scan_forward_impl(const Layout& l, int64_t batch, int64_t length, i
     a.n_seg = l.n_seg; a.t_seg = l.t_seg; a.seg_lo = 0;
     a.seg_sum = reinterpret_cast<float*>(ws + l.seg_sum);
     a.seg_state = reinterpret_cast<float*>(ws + l.seg_state);
-    if (fwd_wide(l, batch, modes)) {
+    if (fwd_wide(l, batch, modes, true)) {
       a.n_mb = static_cast<int>((modes + 255) / 256);
       run_fwd_wide<kModule>(a, io_dtype == SPARC_BF16, st);
     } else if (io_dtype == SPARC_BF16) {
