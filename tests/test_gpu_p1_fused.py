@@ -46,6 +46,10 @@ CASES = [
     ("wide_h0_dlast_bf16", 8, 70, 16380, BF16, dict(h0=True, dlast=True)),
     ("wide_resets_reset_first_bf16", 8, 70, 16380, BF16, dict(h0=True, dlast=True, seg=True, reset_first=True)),
     ("wide_h0_f32", 8, 37, 16384, F32, dict(h0=True, dlast=True)),
+    # an odd number of modes: one mode per lane in both directions (two
+    # otherwise), with and without time segments
+    ("odd_M_h0_f32", 2, 90, 131, F32, dict(h0=True, dlast=True)),
+    ("odd_M_segments_bf16", 1, 1500, 131, BF16, dict(h0=True, dlast=True, seg=True)),
 ]
 
 
