@@ -43,6 +43,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -119,6 +120,11 @@ struct Args {
   int n_seg, t_seg, seg_lo;
   float* seg_sum;    // [B][n_seg][M][4]: each segment's map (P, Q): h_out = P h_in + Q (complex)
   float* seg_state;  // [B][n_seg][M][2]: the state (forward) or adjoint (backward) entering each segment
+  // backward in time pieces (segments without the summary pass): one launch
+  // per piece, the last first; a piece leaves the adjoint entering the piece
+  // before it in seg_state, the last piece starts from dlast; piece s keeps
+  // its per-token partials in part_tok + s*2*n_mb*B*t_seg as [2][n_mb][B][t_seg]
+  int piped;
   // kPlanes / kRelu: the writes (forward) or their gradients (backward,
   // through dy = dy_re and dx = dw_re), [B,T,M] each; the initial state and
   // its gradient [B,M] fp32 (NULL: zero / not wanted); the chunk states
@@ -882,6 +888,11 @@ mixer_bwd_kernel(Args a) {
   const int n_blocks = (t_end - t_begin + kS - 1) / kS;
   const int64_t R = static_cast<int64_t>(a.B) * a.T;
   const int64_t row0 = static_cast<int64_t>(b) * a.T;
+  // per-token partials: columns b*T + t of [2][n_mb][B*T], or, in time
+  // pieces, columns b*t_seg + t - t_begin of piece s's [2][n_mb][B*t_seg]
+  const int64_t Rp = a.piped ? static_cast<int64_t>(a.B) * a.t_seg : R;
+  const int64_t tok0 =
+      a.piped ? static_cast<int64_t>(cp.seg) * 2 * a.n_mb * Rp + static_cast<int64_t>(b) * a.t_seg - t_begin : row0;
   const int64_t mbase = static_cast<int64_t>(mb) * MB;
   const int64_t W = 2 * static_cast<int64_t>(a.M);
   const uint32_t lane_bytes = static_cast<uint32_t>(lane * V * ESZ);
@@ -905,7 +916,7 @@ mixer_bwd_kernel(Args a) {
     if (SUMMARY) {
       Xr[v] = 0.0f;
       Xi[v] = 0.0f;
-    } else if (a.n_seg > 1) {
+    } else if (a.n_seg > 1 && !(a.piped && cp.seg == a.n_seg - 1)) {
       const float2 x0 = *reinterpret_cast<const float2*>(
           a.seg_state + ((static_cast<int64_t>(b) * a.n_seg + cp.seg) * a.M + (lane_ok ? m0 + v : 0)) * 2);
       Xr[v] = x0.x;
@@ -1176,8 +1187,8 @@ mixer_bwd_kernel(Args a) {
       // inside the segment; the other plane's store, non-leader lanes and
       // steps past the segment are dropped (no store under a branch)
       const uint32_t nb = static_cast<uint32_t>(min(kS, t_end - t0)) * 4u;
-      const int64_t o0 = wave_uniform(((static_cast<int64_t>(0) * a.n_mb + mb) * R + row0 + t0) * 4);
-      const int64_t o1 = wave_uniform(((static_cast<int64_t>(1) * a.n_mb + mb) * R + row0 + t0) * 4);
+      const int64_t o0 = wave_uniform(((static_cast<int64_t>(0) * a.n_mb + mb) * Rp + tok0 + t0) * 4);
+      const int64_t o1 = wave_uniform(((static_cast<int64_t>(1) * a.n_mb + mb) * Rp + tok0 + t0) * 4);
       const __amdgpu_buffer_rsrc_t rt0 = make_rsrc(reinterpret_cast<char*>(a.part_tok) + o0, nb);
       const __amdgpu_buffer_rsrc_t rt1 = make_rsrc(reinterpret_cast<char*>(a.part_tok) + o1, nb);
       const bool lead = lane % G == 0;
@@ -1231,6 +1242,13 @@ mixer_bwd_kernel(Args a) {
 #pragma unroll
       for (int v = 0; v < V; ++v)
         a.part_mode[(p * rows + row) * a.M + m0 + v] = acc[p][v];
+    if (a.piped && cp.seg > 0) {  // the adjoint entering the piece before this one
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        *reinterpret_cast<float2*>(a.seg_state +
+                                   ((static_cast<int64_t>(b) * a.n_seg + cp.seg - 1) * a.M + m0 + v) * 2) =
+            make_float2(Xr[v], Xi[v]);
+    }
     if constexpr (GW) {  // the gradient of the initial state: conj(a_0) lambda_0
       if (t_begin == 0 && a.dh0_re) {
 #pragma unroll
@@ -1317,7 +1335,7 @@ template <typename IO>
 __global__ void __launch_bounds__(256)
 ctrl_bwd_kernel(int64_t R, int W, int rows, const void* x, const float* pdir, const float* rdir,
                 const float* eta, const float* delta, const float* deta, const float* ddelta,
-                void* dx, float* pd, float* pbias) {
+                void* dx, float* pd, float* pbias, int64_t T, int64_t t0, int64_t L, int rb0, int n_rb) {
   const int c = (blockIdx.x * 256 + threadIdx.x) * 8;
   const bool col_ok = c < W;
   const int cc = col_ok ? c : 0;
@@ -1334,6 +1352,11 @@ ctrl_bwd_kernel(int64_t R, int W, int rows, const void* x, const float* pdir, co
   constexpr int kG = 4;
   for (int64_t r0 = static_cast<int64_t>(blockIdx.y) * rows; r0 < R; r0 += static_cast<int64_t>(gridDim.y) * rows) {
     const int64_t r1 = r0 + rows < R ? r0 + rows : R;
+    // row r of deta, ddelta is row r + da of x, dx, eta, delta: a time piece
+    // is B runs of L rows from step t0 of each batch row (L a multiple of
+    // `rows`, so a workgroup's rows stay in one run); otherwise L = T = R,
+    // t0 = 0 and da = 0
+    const int64_t da = (r0 / L) * T + t0 + (r0 % L) - r0;
     auto load8 = [&](const void* base, int64_t row, float (&o)[8]) {
       if constexpr (sizeof(IO) == 2) {
         unpack<bf16, 8>(load_raw_nt<bf16, 8>(base, row * W + cc), o);
@@ -1350,13 +1373,13 @@ ctrl_bwd_kernel(int64_t R, int W, int rows, const void* x, const float* pdir, co
 #pragma unroll
       for (int k = 0; k < kG; ++k) {
         const int64_t rr = r + k < r1 ? r + k : r1 - 1;
-        load8(x, rr, xv[k]);
-        load8(dx, rr, gv[k]);
+        load8(x, rr + da, xv[k]);
+        load8(dx, rr + da, gv[k]);
       }
 #pragma unroll
       for (int k = 0; k < kG; ++k) {
         const int64_t rr = r + k < r1 ? r + k : r1 - 1;
-        const float e = eta[rr] * kInvLog16, d = delta[rr] * kTwoOverPi;
+        const float e = eta[rr + da] * kInvLog16, d = delta[rr + da] * kTwoOverPi;
         const bool live = r + k < r1;
         dp1[k] = live ? deta[rr] * kLog16 * fmaf(-e, e, 1.0f) : 0.0f;
         dp0[k] = live ? ddelta[rr] * kHalfPi * fmaf(-d, d, 1.0f) : 0.0f;
@@ -1376,7 +1399,7 @@ ctrl_bwd_kernel(int64_t R, int W, int rows, const void* x, const float* pdir, co
 #pragma unroll
         for (int k = 0; k < kG; ++k) {
           if (r + k >= r1) break;  // wave-uniform
-          const int64_t rr = r + k;
+          const int64_t rr = r + k + da;
           if constexpr (sizeof(IO) == 2) {
             store_raw_nt<bf16, 8>(dx, rr * W + c, pack<bf16, 8>(gv[k]));
           } else {
@@ -1391,16 +1414,17 @@ ctrl_bwd_kernel(int64_t R, int W, int rows, const void* x, const float* pdir, co
     }
   }  // row blocks
   if (col_ok) {
-    float* o0 = pd + static_cast<int64_t>(blockIdx.y) * W + c;
-    float* o1 = pd + (static_cast<int64_t>(gridDim.y) + blockIdx.y) * W + c;
+    // partial row rb0 + blockIdx.y of the [2][n_rb][W] partials
+    float* o0 = pd + (static_cast<int64_t>(rb0) + blockIdx.y) * W + c;
+    float* o1 = pd + (static_cast<int64_t>(n_rb) + rb0 + blockIdx.y) * W + c;
     *reinterpret_cast<float4*>(o0) = *reinterpret_cast<const float4*>(a0);
     *reinterpret_cast<float4*>(o0 + 4) = *reinterpret_cast<const float4*>(a0 + 4);
     *reinterpret_cast<float4*>(o1) = *reinterpret_cast<const float4*>(a1);
     *reinterpret_cast<float4*>(o1 + 4) = *reinterpret_cast<const float4*>(a1 + 4);
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
-    pbias[blockIdx.y] = b0;
-    pbias[gridDim.y + blockIdx.y] = b1;
+    pbias[rb0 + blockIdx.y] = b0;
+    pbias[n_rb + rb0 + blockIdx.y] = b1;
   }
 }
 
@@ -1494,27 +1518,50 @@ void choose_segments(int64_t B, int64_t T, int n_mb, int& n_seg, int& t_seg) {
   t_seg = static_cast<int>(len);
 }
 
+// The module backward without time segments runs in time pieces: the
+// controls backward of piece p then runs on a second stream while the mixer
+// backward works on piece p - 1.  The most pieces, up to kPieces, whose
+// length is a multiple of kCtrlBwdRows (no pieces when T allows none).
+// Module fwd+bwd, bf16, against no pieces: B=8 T=4096 width 32768 5.59 ->
+// 5.38 ms with at most 4 pieces, 5.24 with 8, 5.35 with 16; B=16 T=2048
+// width 24576 4.21 -> 3.92 (4), 3.96 (8), 4.15 (16, pieces of 128 steps).
+#ifndef SPARC_MIXER_BWD_PIECES
+#define SPARC_MIXER_BWD_PIECES 8
+#endif
+constexpr int kPieces = SPARC_MIXER_BWD_PIECES;
+
 struct Layout {
-  int V = 1, n_mb = 0, n_rb = 0, n_seg = 1, t_seg = 1;
+  bool piped = false;
+  int V = 1, n_mb = 0, n_rb = 0, n_rb_piece = 0, n_seg = 1, t_seg = 1;
   int64_t R = 0;
   size_t consts = 0, part_tok = 0, tok = 0, part_mode = 0, pd = 0, pbias = 0, seg_sum = 0, seg_state = 0, total = 0;
 };
 
-// gw: the P1 scan with the writes given (no controls, two per-mode gradients)
-Layout layout(int64_t B, int64_t T, int64_t M, int direction, bool gw = false) {
+// gw: the P1 scan with the writes given (no controls, two per-mode gradients);
+// pieces: the module backward in time pieces where the shape allows
+Layout layout(int64_t B, int64_t T, int64_t M, int direction, bool gw = false, bool pieces = false) {
   Layout l;
   l.V = mixer_v(B, T, M, direction, gw);
   l.n_mb = static_cast<int>((M + 64 * l.V - 1) / (64 * l.V));
   choose_segments(B, T, l.n_mb, l.n_seg, l.t_seg);
   l.R = B * T;
   l.n_rb = static_cast<int>(std::min<int64_t>((l.R + kCtrlBwdRows - 1) / kCtrlBwdRows, kMaxRowBlocks));
+  int np = kPieces;
+  while (np > 1 && T % (static_cast<int64_t>(np) * kCtrlBwdRows) != 0) np /= 2;
+  if (pieces && np > 1 && T > 0 && direction == 1 && !gw && l.n_seg == 1 && l.V == 1) {
+    l.piped = true;
+    l.n_seg = np;
+    l.t_seg = static_cast<int>(T / np);
+    l.n_rb_piece = static_cast<int>(std::min<int64_t>(B * l.t_seg / kCtrlBwdRows, kMaxRowBlocks));
+    l.n_rb = np * l.n_rb_piece;
+  }
   auto up = [](size_t n) { return (n + 255) / 256 * 256; };
   size_t off = 256;
   l.consts = off;
   off += up(static_cast<size_t>(M) * kConsts * 4);
   if (l.n_seg > 1) {
     l.seg_sum = off;
-    off += up(static_cast<size_t>(B) * l.n_seg * M * 4 * 4);
+    if (!l.piped) off += up(static_cast<size_t>(B) * l.n_seg * M * 4 * 4);
     l.seg_state = off;
     off += up(static_cast<size_t>(B) * l.n_seg * M * 2 * 4);
   }
@@ -1941,11 +1988,136 @@ sparc_status check_controls(int64_t rows, int64_t width, int32_t io_dtype) {
   return SPARC_OK;
 }
 
+// The second stream and events of the module backward in time pieces, one set
+// per device, created on first use (default priority, non-blocking) and kept
+// until the process ends.  The mutex is held while a call enqueues its work,
+// so calls from several host threads do not share an event between a record
+// and its wait.
+struct PipeStreams {
+  hipStream_t aux = nullptr;
+  hipEvent_t ev[kPieces + 1] = {};
+};
+std::mutex& pipe_mutex() {
+  static std::mutex mu;
+  return mu;
+}
+sparc_status pipe_streams(PipeStreams** out) {  // the caller holds pipe_mutex()
+  static PipeStreams sets[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64) return fail(SPARC_EHIP, "mixer backward: hipGetDevice (%d)", dev);
+  PipeStreams& ps = sets[dev];
+  if (!ps.aux) {
+    for (hipEvent_t& v : ps.ev) {
+      if (v) continue;
+      e = hipEventCreateWithFlags(&v, hipEventDisableTiming);
+      if (e != hipSuccess) {
+        v = nullptr;
+        return fail(SPARC_EHIP, "mixer backward: hipEventCreate: %s", hipGetErrorString(e));
+      }
+    }
+    e = hipStreamCreateWithFlags(&ps.aux, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      ps.aux = nullptr;
+      return fail(SPARC_EHIP, "mixer backward: hipStreamCreate: %s", hipGetErrorString(e));
+    }
+  }
+  *out = &ps;
+  return SPARC_OK;
+}
+
+// The module backward in l.n_seg time pieces, the last first.  On the caller's
+// stream: the mixer backward of piece p (entering adjoint from piece p + 1),
+// then the sums of its per-token partials into d eta, d delta of its rows; on
+// the second stream, after an event: the controls backward of piece p (dx of
+// its rows in place, the direction partials of its row blocks), which so runs
+// beside the mixer backward of piece p - 1.  The caller's stream waits for
+// the second stream before the per-mode and direction sums.
+sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
+                            const void* x, const float* phase_direction, const float* radial_direction,
+                            const float* eta, const float* delta, const float* nu_log, const float* theta_log,
+                            const float* write_log_gain, const float* write_phase_response,
+                            const float* write_radial_response, const void* h_re, const void* h_im, const void* dy,
+                            const float* dlast_re, const float* dlast_im, void* dx, float* dphase_direction,
+                            float* dradial_direction, float* dnu_log, float* dtheta_log, float* dwrite_log_gain,
+                            float* dwrite_phase_response, float* dwrite_radial_response, char* ws, hipStream_t st) {
+  std::lock_guard<std::mutex> lock(pipe_mutex());
+  PipeStreams* ps = nullptr;
+  if (sparc_status s = pipe_streams(&ps)) return s;
+  const sparc_stream_t stream = reinterpret_cast<sparc_stream_t>(st);
+  const int M = static_cast<int>(modes), W = 2 * M;
+  float* consts = reinterpret_cast<float*>(ws + l.consts);
+  float* part_tok = reinterpret_cast<float*>(ws + l.part_tok);
+  float* part_mode = reinterpret_cast<float*>(ws + l.part_mode);
+  float* deta = reinterpret_cast<float*>(ws + l.tok);
+  float* ddelta = deta + l.R;
+  float* pd = reinterpret_cast<float*>(ws + l.pd);
+  float* pbias = reinterpret_cast<float*>(ws + l.pbias);
+  hipLaunchKernelGGL(mixer_prepare_kernel, dim3(static_cast<unsigned>((M + 255) / 256)), dim3(256), 0, st, M, nu_log,
+                     theta_log, write_log_gain, write_phase_response, write_radial_response, consts);
+  Args a{};
+  a.B = static_cast<int>(batch);
+  a.T = static_cast<int>(length);
+  a.M = M;
+  a.n_mb = l.n_mb;
+  a.x = x; a.consts = consts; a.eta = eta; a.delta = delta;
+  a.h_re = const_cast<void*>(h_re); a.h_im = const_cast<void*>(h_im);
+  a.dy = dy; a.dlast_re = dlast_re; a.dlast_im = dlast_im; a.dx = dx;
+  a.part_tok = part_tok; a.part_mode = part_mode;
+  a.n_seg = l.n_seg; a.t_seg = l.t_seg;
+  a.seg_state = reinterpret_cast<float*>(ws + l.seg_state);
+  a.piped = 1;
+  const int64_t L = l.t_seg, rows_p = batch * L;
+  const dim3 gb(static_cast<unsigned>((W + 2047) / 2048), static_cast<unsigned>(l.n_rb_piece));
+  hipEvent_t fork = ps->ev[kPieces];
+  (void)hipEventRecord(fork, st);
+  (void)hipStreamWaitEvent(ps->aux, fork, 0);
+  for (int p = l.n_seg - 1; p >= 0; --p) {
+    a.seg_lo = p;
+    if (io_dtype == SPARC_BF16) launch_bwd<sparc::bf16, 1, false, kModule>(a, 1, st);
+    else launch_bwd<float, 1, false, kModule>(a, 1, st);
+    const float* pt = part_tok + static_cast<int64_t>(p) * 2 * l.n_mb * rows_p;
+    float* de = deta + static_cast<int64_t>(p) * rows_p;
+    float* dd = ddelta + static_cast<int64_t>(p) * rows_p;
+    if (sparc_status s = sparc_column_sum(l.n_mb, rows_p, pt, de, 0, stream)) return s;
+    if (sparc_status s = sparc_column_sum(l.n_mb, rows_p, pt + static_cast<int64_t>(l.n_mb) * rows_p, dd, 0, stream))
+      return s;
+    (void)hipEventRecord(ps->ev[p], st);
+    (void)hipStreamWaitEvent(ps->aux, ps->ev[p], 0);
+    const int64_t t0 = static_cast<int64_t>(p) * L;
+    const int rb0 = p * l.n_rb_piece;
+    if (io_dtype == SPARC_BF16)
+      hipLaunchKernelGGL(ctrl_bwd_kernel<sparc::bf16>, gb, dim3(256), 0, ps->aux, rows_p, W, kCtrlBwdRows, x,
+                         phase_direction, radial_direction, eta, delta, de, dd, dx, pd, pbias, length, t0, L, rb0,
+                         l.n_rb);
+    else
+      hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, ps->aux, rows_p, W, kCtrlBwdRows, x,
+                         phase_direction, radial_direction, eta, delta, de, dd, dx, pd, pbias, length, t0, L, rb0,
+                         l.n_rb);
+  }
+  (void)hipEventRecord(fork, ps->aux);  // join (the fork's wait is already enqueued)
+  hipError_t e = hipStreamWaitEvent(st, fork, 0);
+  if (e != hipSuccess) return fail(SPARC_EHIP, "mixer backward: stream join: %s", hipGetErrorString(e));
+  float* outs[5] = {dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response};
+  const int64_t prow = batch * l.n_seg;  // one partial row per (batch row, piece)
+  for (int p = 0; p < 5; ++p)
+    if (sparc_status s = sparc_column_sum(prow, modes, part_mode + static_cast<int64_t>(p) * prow * modes, outs[p], 0, stream))
+      return s;
+  const int64_t plane = static_cast<int64_t>(l.n_rb) * W;
+  if (sparc_status s = sparc_column_sum(l.n_rb, W, pd, dphase_direction, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(l.n_rb, W, pd + plane, dradial_direction, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(l.n_rb, 1, pbias, dphase_direction + W, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(l.n_rb, 1, pbias + l.n_rb, dradial_direction + W, 0, stream)) return s;
+  e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(e));
+}
+
 extern "C" {
 
 size_t sparc_mixer_workspace_bytes(int64_t batch, int64_t length, int64_t modes, int direction) {
   if (batch <= 0 || length < 0 || modes <= 0 || modes % 4 || (direction != 0 && direction != 1)) return 0;
-  return layout(batch, length, modes, direction).total;
+  // the module backward may run in time pieces (a larger workspace)
+  return std::max(layout(batch, length, modes, direction).total, layout(batch, length, modes, direction, false, true).total);
 }
 
 sparc_status sparc_mixer_scan_forward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
@@ -2051,7 +2223,7 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
       !params_ok(dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response))
     return fail(SPARC_EINVAL, "mixer backward: NULL pointer");
   if ((dlast_re == nullptr) != (dlast_im == nullptr)) return fail(SPARC_EINVAL, "mixer backward: dlast_re/dlast_im");
-  const Layout l = layout(batch, length, modes, 1);
+  const Layout l = layout(batch, length, modes, 1, false, true);
   if (!workspace || workspace_bytes < l.total)
     return fail(SPARC_EWORKSPACE, "mixer backward: workspace too small (%zu < %zu)", workspace_bytes, l.total);
   const size_t esz = io_dtype == SPARC_BF16 ? 2 : 4;
@@ -2063,6 +2235,11 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
   char* ws = static_cast<char*>(workspace);
   float* deta = reinterpret_cast<float*>(ws + l.tok);
   float* ddelta = deta + l.R;
+  if (l.piped)
+    return piped_backward(l, batch, length, modes, io_dtype, x, phase_direction, radial_direction, eta, delta,
+                          nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response, h_re, h_im,
+                          dy, dlast_re, dlast_im, dx, dphase_direction, dradial_direction, dnu_log, dtheta_log,
+                          dwrite_log_gain, dwrite_phase_response, dwrite_radial_response, ws, st);
   if (sparc_status s = scan_backward_impl(l, batch, length, modes, io_dtype, x, eta, delta, nu_log, theta_log,
                                           write_log_gain, write_phase_response, write_radial_response, h_re, h_im,
                                           dy, dlast_re, dlast_im, dx, deta, ddelta, dnu_log, dtheta_log,
@@ -2080,10 +2257,10 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
   const dim3 gb(static_cast<unsigned>((W + 2047) / 2048), static_cast<unsigned>(l.n_rb));
   if (io_dtype == SPARC_BF16)
     hipLaunchKernelGGL(ctrl_bwd_kernel<sparc::bf16>, gb, dim3(256), 0, st, l.R, W, kCtrlBwdRows, x, phase_direction,
-                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias);
+                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias, l.R, int64_t(0), l.R, 0, l.n_rb);
   else
     hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, st, l.R, W, kCtrlBwdRows, x, phase_direction,
-                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias);
+                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias, l.R, int64_t(0), l.R, 0, l.n_rb);
   // direction gradients: columns 0..W-1 from the row-block partials, the bias from pbias
   const int64_t plane = static_cast<int64_t>(l.n_rb) * W;
   if (sparc_status s = sparc_column_sum(l.n_rb, W, pd, dphase_direction, 0, stream)) return s;
@@ -2151,10 +2328,10 @@ sparc_status sparc_controls_backward(int64_t rows, int64_t width, int32_t io_dty
   const dim3 gb(static_cast<unsigned>(c.n_cb), static_cast<unsigned>(c.n_rb));
   if (io_dtype == SPARC_BF16)
     hipLaunchKernelGGL(ctrl_bwd_kernel<sparc::bf16>, gb, dim3(256), 0, st, rows, W, c.rows, x, phase_direction,
-                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias);
+                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias, rows, int64_t(0), rows, 0, c.n_rb);
   else
     hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, st, rows, W, c.rows, x, phase_direction,
-                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias);
+                       radial_direction, eta, delta, deta, ddelta, dx, pd, pbias, rows, int64_t(0), rows, 0, c.n_rb);
   const int64_t plane = static_cast<int64_t>(c.n_rb) * W;
   if (sparc_status s = sparc_column_sum(c.n_rb, W, pd, dphase_direction, 0, stream)) return s;
   if (sparc_status s = sparc_column_sum(c.n_rb, W, pd + plane, dradial_direction, 0, stream)) return s;

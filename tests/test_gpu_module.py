@@ -97,6 +97,22 @@ def test_mixer_forward_backward_parity(dtype, tol, B, L, width, mixer_path):
         assert e <= tol, f"grad {name}: {e:.3g}"
 
 
+@pytest.mark.parametrize("L,dtype,tol", [(512, torch.float32, 1e-4), (512, torch.bfloat16, 2e-2),
+                                         (1024, torch.float32, 1e-4)])
+def test_fused_backward_time_pieces(L, dtype, tol):
+    """1024 chains of 64 modes and T a multiple of 512 (1024): the fused module
+    backward runs in four (eight) time pieces, the last first, with the controls
+    backward of each piece on a second stream beside the mixer backward of
+    the piece before it.  The adjoint crosses the pieces, dx is updated piece
+    by piece and the direction gradients sum the pieces' partials; all of it
+    against the float64 oracle, with a gradient through the last state."""
+    sparc_amd.set_mixer_path("fused")
+    try:
+        test_mixer_forward_backward_parity(dtype, tol, 2, L, 65536, "fused")
+    finally:
+        sparc_amd.set_mixer_path("auto")
+
+
 @pytest.mark.parametrize("B,L,width,dtype,tol", [
     (1, 3001, 128, torch.float32, 1e-4),    # 2 chains: 23 segments of 136 steps, a ragged last one
     (3, 1024, 512, torch.bfloat16, 2e-2),   # 12 chains: 8 segments of 128
