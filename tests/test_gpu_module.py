@@ -397,14 +397,17 @@ def test_fused_mixer_shapes(B, L, width, dtype, tol):
         sparc_amd.set_mixer_path("auto")
 
 
-def test_fused_mixer_deterministic():
+@pytest.mark.parametrize("B,L,width", [(4, 77, 512), (2, 4096, 65536)])
+def test_fused_mixer_deterministic(B, L, width):
     """Two fused forward+backward passes give bit-identical outputs and
-    gradients (fixed-order reductions, no atomics)."""
-    print("[case] fused mixer determinism", flush=True)
+    gradients (fixed-order reductions, no atomics); the second shape runs the
+    backward in eight time pieces on two streams, whose result must not
+    depend on how the streams interleave."""
+    print(f"[case] fused mixer determinism B={B} L={L} width={width}", flush=True)
     sparc_amd.set_mixer_path("fused")
     try:
-        m = make_module(512, seed=3).cuda()
-        x = torch.randn(4, 77, 512, device="cuda", dtype=torch.bfloat16)
+        m = make_module(width, seed=3).cuda()
+        x = torch.randn(B, L, width, device="cuda", dtype=torch.bfloat16)
         dy = torch.randn_like(x)
         outs = []
         for _ in range(2):
