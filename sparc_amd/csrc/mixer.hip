@@ -2069,9 +2069,12 @@ sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int6
   a.piped = 1;
   const int64_t L = l.t_seg, rows_p = batch * L;
   const dim3 gb(static_cast<unsigned>((W + 2047) / 2048), static_cast<unsigned>(l.n_rb_piece));
+  // the controls go to the second stream while every event call succeeds,
+  // else (from then on) to the caller's stream, in order after the mixer
   hipEvent_t fork = ps->ev[kPieces];
-  (void)hipEventRecord(fork, st);
-  (void)hipStreamWaitEvent(ps->aux, fork, 0);
+  hipStream_t cs = hipEventRecord(fork, st) == hipSuccess && hipStreamWaitEvent(ps->aux, fork, 0) == hipSuccess
+                       ? ps->aux
+                       : st;
   for (int p = l.n_seg - 1; p >= 0; --p) {
     a.seg_lo = p;
     if (io_dtype == SPARC_BF16) launch_bwd<sparc::bf16, 1, false, kModule>(a, 1, st);
@@ -2082,22 +2085,28 @@ sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int6
     if (sparc_status s = sparc_column_sum(l.n_mb, rows_p, pt, de, 0, stream)) return s;
     if (sparc_status s = sparc_column_sum(l.n_mb, rows_p, pt + static_cast<int64_t>(l.n_mb) * rows_p, dd, 0, stream))
       return s;
-    (void)hipEventRecord(ps->ev[p], st);
-    (void)hipStreamWaitEvent(ps->aux, ps->ev[p], 0);
+    if (cs != st && (hipEventRecord(ps->ev[p], st) != hipSuccess || hipStreamWaitEvent(cs, ps->ev[p], 0) != hipSuccess))
+      cs = st;
     const int64_t t0 = static_cast<int64_t>(p) * L;
     const int rb0 = p * l.n_rb_piece;
     if (io_dtype == SPARC_BF16)
-      hipLaunchKernelGGL(ctrl_bwd_kernel<sparc::bf16>, gb, dim3(256), 0, ps->aux, rows_p, W, kCtrlBwdRows, x,
+      hipLaunchKernelGGL(ctrl_bwd_kernel<sparc::bf16>, gb, dim3(256), 0, cs, rows_p, W, kCtrlBwdRows, x,
                          phase_direction, radial_direction, eta, delta, de, dd, dx, pd, pbias, length, t0, L, rb0,
                          l.n_rb);
     else
-      hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, ps->aux, rows_p, W, kCtrlBwdRows, x,
+      hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, cs, rows_p, W, kCtrlBwdRows, x,
                          phase_direction, radial_direction, eta, delta, de, dd, dx, pd, pbias, length, t0, L, rb0,
                          l.n_rb);
   }
-  (void)hipEventRecord(fork, ps->aux);  // join (the fork's wait is already enqueued)
-  hipError_t e = hipStreamWaitEvent(st, fork, 0);
-  if (e != hipSuccess) return fail(SPARC_EHIP, "mixer backward: stream join: %s", hipGetErrorString(e));
+  // join (the fork's wait is already enqueued); if the join cannot be
+  // enqueued, wait on the host so that nothing after this call races the
+  // second stream
+  hipError_t e = hipEventRecord(fork, ps->aux);
+  if (e == hipSuccess) e = hipStreamWaitEvent(st, fork, 0);
+  if (e != hipSuccess) {
+    (void)hipStreamSynchronize(ps->aux);
+    return fail(SPARC_EHIP, "mixer backward: stream join: %s", hipGetErrorString(e));
+  }
   float* outs[5] = {dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response};
   const int64_t prow = batch * l.n_seg;  // one partial row per (batch row, piece)
   for (int p = 0; p < 5; ++p)
