@@ -717,11 +717,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16",
         "data": "synthetic: w, dy ~ N(0,1); r = sigmoid(N(2,1)); phi ~ U(-pi,pi)",
         "config": {"workload": "complex chunked scan fwd+bwd (polar gates shared per channel)",
                    "B": res["B"], "T": res["T"], "D": res["D"], "N": res["N"], "M": res["M"],
-                   "G": res["G"], "io_dtype": "bf16", "state_dtype": "f32", "algorithm": args.algo,
+                   "G": res["G"], "io_dtype": "bf16", "gate_dtype": "bf16", "state_dtype": "f32",
+                   "accumulate_dtype": "f32", "algorithm": args.algo,
                    "parallelism": "single GPU"},
         "roofline": roof,
         "decode": None if core is None else {

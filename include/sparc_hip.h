@@ -4,7 +4,9 @@
  *
  * Plain pointers and sizes only.  Every tensor is caller-allocated device
  * memory, row-major and contiguous; every call is enqueued on the caller's
- * HIP stream and returns without synchronising.  Scratch memory comes in
+ * HIP stream and returns without synchronising (sparc_mixer_backward may also
+ * fork work onto a library-owned stream and joins it back before it returns:
+ * see there).  Scratch memory comes in
  * through ``workspace`` (size from the matching *_workspace_bytes query,
  * contents undefined on entry); calls that share one workspace must be
  * ordered on one stream.  No entry point allocates device memory.
@@ -409,6 +411,25 @@ sparc_status sparc_mixer_scan_backward(int64_t batch, int64_t length, int64_t mo
  * forward wrote them.  Writes dx [B,T,2M] (io_dtype) and, overwriting, the
  * direction gradients [2M+1] and the parameter gradients [M] (fp32).
  * Deterministic (fixed-order reductions, no atomics).
+ *
+ * Streams: when T splits into time pieces (T a multiple of 256, and at least
+ * 1024 chains of 64 modes, so that no time segments are needed; the
+ * workspace query covers both layouts), the call runs the
+ * pieces last first and launches each piece's controls backward on a second
+ * stream, so that it overlaps the next piece's scan.  That stream is owned by
+ * the library: one per device, non-blocking, default priority, created with
+ * its events on the first such call that is not under graph capture and kept
+ * until the process ends.  Every use of it is bracketed by events: it first
+ * waits for the given stream, and the given stream waits for it before the
+ * call's last reductions and before any error return after that fork, so
+ * work enqueued afterwards on the given stream sees every result.  If the
+ * stream or an event call is unavailable (the first call is under capture, a
+ * HIP call fails), the same launches go to the given stream alone, with the
+ * same results.  Under capture the fork and join become graph edges and
+ * nothing waits on the host.  A process-wide mutex is held while a call
+ * enqueues, so calls from several host threads do not share an event between
+ * a record and its wait.
+ *
  * Replaces _SPARCChunkScan.backward (sparc-kernal/backward/scan.py:1375-1640),
  * _LatestSPARCWrite.backward (sparc-kernal/backward/control.py:92-129, kernel
  * :10-89) and the autograd of make_controls' F.linear

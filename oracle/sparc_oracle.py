@@ -351,12 +351,16 @@ def mixer_forward(p: MixerParams, x: torch.Tensor, return_cache=False,
     return y, (last if return_cache else None)
 
 
-def decode_step(p: MixerParams, x: torch.Tensor, state):
-    """Eager ``run_decode_step`` (forward/decode.py:296-306); x is [B, 2M]."""
+def decode_step(p: MixerParams, x: torch.Tensor, state, write_dtype=None):
+    """Eager ``run_decode_step`` (forward/decode.py:296-306); x is [B, 2M].
+    ``write_dtype`` models the cast of the write to x's dtype inside
+    ``make_scan_inputs`` (forward/control.py:162-163), as in ``mixer_forward``."""
     eta, delta = controls(x, p.phase_direction, p.radial_direction)
     wr, wi = write(x[:, None], eta[:, None], delta[:, None], p.nu_log,
                    p.write_log_gain, p.write_phase_response,
                    p.write_radial_response)
+    if write_dtype is not None:
+        wr, wi = wr.to(write_dtype).to(wr.dtype), wi.to(write_dtype).to(wi.dtype)
     ar, ai = p1_transition(eta[:, None, None], delta[:, None, None], p.nu_log, p.theta_log)
     ar, ai, wr, wi = ar[:, 0], ai[:, 0], wr[:, 0], wi[:, 0]
     old_r, old_i = state

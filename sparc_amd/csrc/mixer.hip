@@ -1989,10 +1989,10 @@ sparc_status check_controls(int64_t rows, int64_t width, int32_t io_dtype) {
 }
 
 // The second stream and events of the module backward in time pieces, one set
-// per device, created on first use (default priority, non-blocking) and kept
-// until the process ends.  The mutex is held while a call enqueues its work,
-// so calls from several host threads do not share an event between a record
-// and its wait.
+// per device, created on first use outside graph capture (default priority,
+// non-blocking) and kept until the process ends.  The mutex is held while a
+// call enqueues its work, so calls from several host threads do not share an
+// event between a record and its wait.
 struct PipeStreams {
   hipStream_t aux = nullptr;
   hipEvent_t ev[kPieces + 1] = {};
@@ -2001,29 +2001,45 @@ std::mutex& pipe_mutex() {
   static std::mutex mu;
   return mu;
 }
-sparc_status pipe_streams(PipeStreams** out) {  // the caller holds pipe_mutex()
+// The current device's set, or NULL when it does not exist and may not be
+// created (create false: the caller's stream is capturing) or when a HIP call
+// fails; the error such a failure leaves is cleared, since the caller then
+// runs on its own stream alone.  The caller holds pipe_mutex().
+PipeStreams* pipe_streams(bool create) {
   static PipeStreams sets[64];
   int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess || dev < 0 || dev >= 64) return fail(SPARC_EHIP, "mixer backward: hipGetDevice (%d)", dev);
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
   PipeStreams& ps = sets[dev];
-  if (!ps.aux) {
-    for (hipEvent_t& v : ps.ev) {
-      if (v) continue;
-      e = hipEventCreateWithFlags(&v, hipEventDisableTiming);
-      if (e != hipSuccess) {
-        v = nullptr;
-        return fail(SPARC_EHIP, "mixer backward: hipEventCreate: %s", hipGetErrorString(e));
-      }
-    }
-    e = hipStreamCreateWithFlags(&ps.aux, hipStreamNonBlocking);
-    if (e != hipSuccess) {
-      ps.aux = nullptr;
-      return fail(SPARC_EHIP, "mixer backward: hipStreamCreate: %s", hipGetErrorString(e));
+  if (ps.aux) return &ps;
+  if (!create) return nullptr;
+  for (hipEvent_t& v : ps.ev) {
+    if (v) continue;
+    if (hipEventCreateWithFlags(&v, hipEventDisableTiming) != hipSuccess) {
+      v = nullptr;
+      (void)hipGetLastError();
+      return nullptr;
     }
   }
-  *out = &ps;
-  return SPARC_OK;
+  if (hipStreamCreateWithFlags(&ps.aux, hipStreamNonBlocking) != hipSuccess) {
+    ps.aux = nullptr;
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return &ps;
+}
+
+// Whether st is capturing into a graph (a failed query counts as capturing:
+// then nothing is created and nothing waits on the host).
+bool stream_capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;
+  }
+  return cs != hipStreamCaptureStatusNone;
 }
 
 // The module backward in l.n_seg time pieces, the last first.  On the caller's
@@ -2032,7 +2048,11 @@ sparc_status pipe_streams(PipeStreams** out) {  // the caller holds pipe_mutex()
 // the second stream, after an event: the controls backward of piece p (dx of
 // its rows in place, the direction partials of its row blocks), which so runs
 // beside the mixer backward of piece p - 1.  The caller's stream waits for
-// the second stream before the per-mode and direction sums.
+// the second stream before the per-mode and direction sums, and before any
+// error return once the second stream has been forked.  Without the second
+// stream (a capture that reaches the first call, a failed stream or event
+// call) every launch goes to the caller's stream, in the same order and with
+// the same workspace layout.
 sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
                             const void* x, const float* phase_direction, const float* radial_direction,
                             const float* eta, const float* delta, const float* nu_log, const float* theta_log,
@@ -2042,8 +2062,8 @@ sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int6
                             float* dradial_direction, float* dnu_log, float* dtheta_log, float* dwrite_log_gain,
                             float* dwrite_phase_response, float* dwrite_radial_response, char* ws, hipStream_t st) {
   std::lock_guard<std::mutex> lock(pipe_mutex());
-  PipeStreams* ps = nullptr;
-  if (sparc_status s = pipe_streams(&ps)) return s;
+  const bool capturing = stream_capturing(st);
+  PipeStreams* ps = pipe_streams(!capturing);
   const sparc_stream_t stream = reinterpret_cast<sparc_stream_t>(st);
   const int M = static_cast<int>(modes), W = 2 * M;
   float* consts = reinterpret_cast<float*>(ws + l.consts);
@@ -2053,8 +2073,6 @@ sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int6
   float* ddelta = deta + l.R;
   float* pd = reinterpret_cast<float*>(ws + l.pd);
   float* pbias = reinterpret_cast<float*>(ws + l.pbias);
-  hipLaunchKernelGGL(mixer_prepare_kernel, dim3(static_cast<unsigned>((M + 255) / 256)), dim3(256), 0, st, M, nu_log,
-                     theta_log, write_log_gain, write_phase_response, write_radial_response, consts);
   Args a{};
   a.B = static_cast<int>(batch);
   a.T = static_cast<int>(length);
@@ -2071,10 +2089,27 @@ sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int6
   const dim3 gb(static_cast<unsigned>((W + 2047) / 2048), static_cast<unsigned>(l.n_rb_piece));
   // the controls go to the second stream while every event call succeeds,
   // else (from then on) to the caller's stream, in order after the mixer
-  hipEvent_t fork = ps->ev[kPieces];
-  hipStream_t cs = hipEventRecord(fork, st) == hipSuccess && hipStreamWaitEvent(ps->aux, fork, 0) == hipSuccess
-                       ? ps->aux
-                       : st;
+  hipEvent_t fork = ps ? ps->ev[kPieces] : nullptr;
+  bool forked = false;  // the second stream waits on the fork and must be joined
+  if (ps) {
+    if (hipEventRecord(fork, st) == hipSuccess && hipStreamWaitEvent(ps->aux, fork, 0) == hipSuccess) forked = true;
+    else (void)hipGetLastError();
+  }
+  hipStream_t cs = forked ? ps->aux : st;
+  hipLaunchKernelGGL(mixer_prepare_kernel, dim3(static_cast<unsigned>((M + 255) / 256)), dim3(256), 0, st, M, nu_log,
+                     theta_log, write_log_gain, write_phase_response, write_radial_response, consts);
+  // the caller's stream waits for everything enqueued on the second stream;
+  // if that cannot be enqueued, the host waits for the second stream (never
+  // while capturing: a capture with an unjoined stream fails at its end)
+  auto join = [&]() -> hipError_t {
+    if (!forked) return hipSuccess;
+    forked = false;
+    cs = st;
+    hipError_t e = hipEventRecord(fork, ps->aux);
+    if (e == hipSuccess) e = hipStreamWaitEvent(st, fork, 0);
+    if (e != hipSuccess && !capturing) (void)hipStreamSynchronize(ps->aux);
+    return e;
+  };
   for (int p = l.n_seg - 1; p >= 0; --p) {
     a.seg_lo = p;
     if (io_dtype == SPARC_BF16) launch_bwd<sparc::bf16, 1, false, kModule>(a, 1, st);
@@ -2082,11 +2117,16 @@ sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int6
     const float* pt = part_tok + static_cast<int64_t>(p) * 2 * l.n_mb * rows_p;
     float* de = deta + static_cast<int64_t>(p) * rows_p;
     float* dd = ddelta + static_cast<int64_t>(p) * rows_p;
-    if (sparc_status s = sparc_column_sum(l.n_mb, rows_p, pt, de, 0, stream)) return s;
-    if (sparc_status s = sparc_column_sum(l.n_mb, rows_p, pt + static_cast<int64_t>(l.n_mb) * rows_p, dd, 0, stream))
+    sparc_status s = sparc_column_sum(l.n_mb, rows_p, pt, de, 0, stream);
+    if (!s) s = sparc_column_sum(l.n_mb, rows_p, pt + static_cast<int64_t>(l.n_mb) * rows_p, dd, 0, stream);
+    if (s) {
+      (void)join();
       return s;
-    if (cs != st && (hipEventRecord(ps->ev[p], st) != hipSuccess || hipStreamWaitEvent(cs, ps->ev[p], 0) != hipSuccess))
-      cs = st;
+    }
+    if (cs != st && (hipEventRecord(ps->ev[p], st) != hipSuccess || hipStreamWaitEvent(cs, ps->ev[p], 0) != hipSuccess)) {
+      (void)hipGetLastError();
+      cs = st;  // the second stream stays forked until the join
+    }
     const int64_t t0 = static_cast<int64_t>(p) * L;
     const int rb0 = p * l.n_rb_piece;
     if (io_dtype == SPARC_BF16)
@@ -2097,16 +2137,13 @@ sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int6
       hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, cs, rows_p, W, kCtrlBwdRows, x,
                          phase_direction, radial_direction, eta, delta, de, dd, dx, pd, pbias, length, t0, L, rb0,
                          l.n_rb);
+    if (hipError_t le = hipGetLastError()) {
+      (void)join();
+      return fail(SPARC_EHIP, "mixer backward: controls launch: %s", hipGetErrorString(le));
+    }
   }
-  // join (the fork's wait is already enqueued); if the join cannot be
-  // enqueued, wait on the host so that nothing after this call races the
-  // second stream
-  hipError_t e = hipEventRecord(fork, ps->aux);
-  if (e == hipSuccess) e = hipStreamWaitEvent(st, fork, 0);
-  if (e != hipSuccess) {
-    (void)hipStreamSynchronize(ps->aux);
-    return fail(SPARC_EHIP, "mixer backward: stream join: %s", hipGetErrorString(e));
-  }
+  hipError_t e = join();
+  if (e != hipSuccess) return fail(SPARC_EHIP, "mixer backward: stream join: %s", hipGetErrorString(e));
   float* outs[5] = {dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response};
   const int64_t prow = batch * l.n_seg;  // one partial row per (batch row, piece)
   for (int p = 0; p < 5; ++p)

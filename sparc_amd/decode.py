@@ -3,7 +3,9 @@
 ``_latest_sparc_decode`` (decode.py:10-75): ``sparc_decode_step_prepared``
 (per-mode constants cached on the module, controls split over workgroups)
 when the mode count is a multiple of 4, else the single-kernel
-``sparc_decode_step``.
+``sparc_decode_step``.  Before ``prepare_inference`` a step follows the
+reference's eager branch (decode.py:296-306) instead: the write is stored in
+x's dtype, then one ``sparc_scan_step``.
 """
 from __future__ import annotations
 
@@ -113,13 +115,57 @@ def latest_sparc_decode(module, x: torch.Tensor, state, out_state=None):
     return y, (new_r, new_i)
 
 
+@torch.no_grad()
+def eager_decode_step(module, x: torch.Tensor, state, out_state=None):
+    """The step before ``prepare_inference``: the reference's eager branch of
+    ``run_decode_step`` (forward/decode.py:296-306).  ``make_scan_inputs`` on
+    the single token stores the write in x's dtype (``write_r.to(x.dtype)``,
+    forward/control.py:162-163; bf16 x rounds it), then h' = a h + w in fp32
+    and y = relu(cat(h'_r, h'_i)) in x's dtype.  HIP throughout: the controls
+    and write kernels of the composed sequence path, then
+    ``sparc_scan_step``.  ``out_state`` as in ``latest_sparc_decode``."""
+    from .control import make_scan_inputs
+    from .ops import scan_step
+    if x.ndim != 2 or x.shape[-1] % 2:
+        raise ValueError("SPARC decode expects [B, 2M]")
+    batch, width = x.shape
+    modes = width // 2
+    state_r, state_i = state
+    if state_r.shape != (batch, modes) or state_i.shape != state_r.shape:
+        raise ValueError("SPARC decode state shape mismatch")
+    _lib.require_gpu(x, state_r, state_i)
+    eta, delta, write_r, write_i = make_scan_inputs(module, x[:, None])
+    if out_state is None:
+        new_r = state_r.float().clone(memory_format=torch.contiguous_format)
+        new_i = state_i.float().clone(memory_format=torch.contiguous_format)
+    else:
+        new_r, new_i = out_state
+        if (new_r.dtype != torch.float32 or new_i.dtype != torch.float32 or not new_r.is_contiguous()
+                or not new_i.is_contiguous() or new_r.shape != (batch, modes) or new_i.shape != (batch, modes)):
+            raise ValueError("out_state must be contiguous fp32 [B, M] tensors")
+        if new_r.data_ptr() != state_r.data_ptr():
+            new_r.copy_(state_r)
+        if new_i.data_ptr() != state_i.data_ptr():
+            new_i.copy_(state_i)
+    y = scan_step("p1", eta, delta, write_r[:, 0], write_i[:, 0], (new_r, new_i),
+                  nu_log=module.nu_log.detach().float().contiguous(),
+                  theta_log=module.theta_log.detach().float().contiguous(),
+                  relu_output=True, want_output=True)
+    return y, (new_r, new_i)
+
+
 def run_decode_step(module, x: torch.Tensor, state, segment_pos):
     """``run_decode_step`` (forward/decode.py:273-306); ``segment_pos`` is
-    ignored as in the reference.  With ``module.decode_in_place`` the new state
-    overwrites ``state`` (same tensors returned)."""
+    ignored as in the reference.  After ``prepare_inference`` the fused step
+    (``latest_sparc_decode``, the write kept in fp32); before it the
+    reference's eager step (``eager_decode_step``, the write stored in x's
+    dtype).  With ``module.decode_in_place`` the new state overwrites
+    ``state`` (same tensors returned)."""
     del segment_pos
     out = state if getattr(module, "decode_in_place", False) else None
+    if not getattr(module, "_inference_fused", False):
+        return eager_decode_step(module, x, state, out_state=out)
     return latest_sparc_decode(module, x, state, out_state=out)
 
 
-__all__ = ["prepare_decode", "run_decode_step", "latest_sparc_decode"]
+__all__ = ["prepare_decode", "run_decode_step", "latest_sparc_decode", "eager_decode_step"]

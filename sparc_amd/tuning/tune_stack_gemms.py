@@ -1,6 +1,9 @@
-"""Writes a TunableOp results file for the GEMMs of one training step of the
-12-layer block stack (d_model 768, N=16, B=16, T=2048, bf16, AdamW) on the
-current GPU:
+"""The recipe of ``gemm_stack_gfx950.csv`` beside it: writes a TunableOp
+results file for the GEMMs of one training step of the 12-layer block stack
+(d_model 768, N=16, B=16, T=2048, bf16, AdamW) on the current GPU.  It is
+kept in the package so that the committed file can be regenerated for
+another ROCm, torch or GPU (the reader rejects files whose validator lines do
+not match); nothing imports it at run time:
 
     python -m sparc_amd.tuning.tune_stack_gemms [OUT.csv]
 

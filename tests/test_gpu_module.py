@@ -249,6 +249,45 @@ def test_decode_in_place_state():
     assert torch.equal(y, y_ref) and torch.equal(sr, nr) and torch.equal(si, ni)
 
 
+@pytest.mark.parametrize("in_place", [False, True])
+def test_step_before_prepare_rounds_the_write_as_the_reference(in_place):
+    """Before prepare_inference, step() is the reference's eager step
+    (forward/decode.py:296-306): the write stored in x's dtype, then h' = a h
+    + w in fp32.  Against the float64 oracle with that rounding modelled the
+    new state agrees to fp32 arithmetic; the unrounded model is off by the
+    write's bf16 rounding, which the fused (prepared) step keeps instead."""
+    print(f"[case] step before prepare_inference, bf16, in_place={in_place}", flush=True)
+    B, modes = 8, 256
+    m = make_module(2 * modes, seed=29).cuda()
+    m.decode_in_place = in_place
+    g = torch.Generator().manual_seed(30)
+    x = torch.randn(B, 2 * modes, generator=g).bfloat16().cuda()
+    s0 = ((0.1 * torch.randn(B, modes, generator=g)).cuda(), (0.1 * torch.randn(B, modes, generator=g)).cuda())
+    state = (s0[0].clone(), s0[1].clone())
+    y, (nr, ni) = m.step(x, state, None)
+    assert (nr.data_ptr() == state[0].data_ptr()) == in_place
+    if not in_place:
+        assert torch.equal(state[0], s0[0]) and torch.equal(state[1], s0[1])
+    p = oracle_params(m, requires_grad=False)
+    xd, sd = x.double().cpu(), (s0[0].double().cpu(), s0[1].double().cpu())
+    yr, (rr, ri) = O.decode_step(p, xd, sd, write_dtype=torch.bfloat16)
+    _, (er, ei) = O.decode_step(p, xd, sd)
+    scale = max(rr.abs().max().item(), ri.abs().max().item())
+    err_round = max((nr.double().cpu() - rr).abs().max().item(), (ni.double().cpu() - ri).abs().max().item())
+    err_exact = max((nr.double().cpu() - er).abs().max().item(), (ni.double().cpu() - ei).abs().max().item())
+    # the controls see bf16 x exactly; a write within fp32 rounding of a bf16
+    # tie may round the other way (one bf16 step of w), hence the median too
+    diff = torch.cat([(nr.double().cpu() - rr).abs().flatten(), (ni.double().cpu() - ri).abs().flatten()])
+    assert diff.median().item() <= 1e-6 * scale, diff.median().item()
+    assert err_round <= 2.0 ** -8 * scale and err_exact > 10 * diff.median().item()
+    assert rel_err(y, yr) <= 2e-2
+    # after prepare_inference the fused step takes over (the write in fp32)
+    m.decode_in_place = False
+    m.prepare_inference()
+    _, (fr, fi) = m.step(x, (s0[0].clone(), s0[1].clone()), None)
+    assert rel_err(fr, er) <= 1e-4 and rel_err(fi, ei) <= 1e-4
+
+
 def _single_kernel_decode(m, x, state):
     """The unprepared one-kernel decode (sparc_decode_step) through the C ABI."""
     from sparc_amd import _lib

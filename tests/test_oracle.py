@@ -217,6 +217,32 @@ def test_decode_steps_match_sequence_forward():
     assert torch.allclose(y_seq, y_full[:, :4], atol=1e-14)
 
 
+def test_decode_step_write_dtype_rounds_only_the_write():
+    """decode_step(write_dtype=bf16) is the sequence forward with the same
+    write rounding, step by step; the write is the only rounded quantity (the
+    new state differs from the unrounded one by exactly the rounding of w)."""
+    g = torch.Generator().manual_seed(63)
+    p = O.init_params(12, generator=g)
+    p.phase_direction = 0.3 * torch.randn(13, generator=g)
+    p.radial_direction = 0.3 * torch.randn(13, generator=g)
+    x = torch.randn(2, 5, 12, generator=g, dtype=torch.float64)
+    _, last = O.mixer_forward(p, x[:, :3], return_cache=True, write_dtype=torch.bfloat16)
+    state = last
+    for t in range(3, 5):
+        y, state = O.decode_step(p, x[:, t], state, write_dtype=torch.bfloat16)
+    y_full, last_full = O.mixer_forward(p, x, return_cache=True, write_dtype=torch.bfloat16)
+    assert torch.allclose(y, y_full[:, 4], atol=1e-12) and torch.allclose(state[0], last_full[0], atol=1e-12)
+    s0 = (torch.randn(2, 6, generator=g, dtype=torch.float64), torch.randn(2, 6, generator=g, dtype=torch.float64))
+    _, (rr, ri) = O.decode_step(p, x[:, 0], s0, write_dtype=torch.bfloat16)
+    _, (er, ei) = O.decode_step(p, x[:, 0], s0)
+    eta, delta = O.controls(x[:, :1], p.phase_direction, p.radial_direction)
+    wr, wi = O.write(x[:, :1], eta, delta, p.nu_log, p.write_log_gain, p.write_phase_response,
+                     p.write_radial_response)
+    assert torch.allclose(rr - er, wr[:, 0].bfloat16().double() - wr[:, 0], atol=1e-14)
+    assert torch.allclose(ri - ei, wi[:, 0].bfloat16().double() - wi[:, 0], atol=1e-14)
+    assert (rr - er).abs().max() > 0
+
+
 def test_grouped_gates_expand_per_mode():
     g = torch.Generator().manual_seed(6)
     r = torch.rand(2, 5, 3, generator=g)
@@ -225,6 +251,42 @@ def test_grouped_gates_expand_per_mode():
     assert ar.shape == (2, 5, 12)
     for m in range(12):
         assert torch.equal(ar[..., m], r[..., m // 4] * torch.cos(phi[..., m // 4]))
+
+
+def test_polar_transition_is_r_exp_i_phi():
+    """polar_transition(r, phi) = r e^{+i phi} in both parts: torch.polar, the
+    quarter turns (phi = +-pi/2 puts r on the +-imaginary axis), and
+    r e^{i phi} e^{-i phi} = r.  A conjugate-sign or swapped-part slip fails."""
+    g = torch.Generator().manual_seed(61)
+    r = torch.rand(2, 7, 5, generator=g, dtype=torch.float64) * 0.9 + 0.05
+    phi = (torch.rand(2, 7, 5, generator=g, dtype=torch.float64) * 2 - 1) * math.pi
+    ar, ai = O.polar_transition(r, phi, 5)
+    ref = torch.polar(r, phi)
+    assert torch.allclose(ar, ref.real, atol=1e-15) and torch.allclose(ai, ref.imag, atol=1e-15)
+    quarter = torch.tensor([[[math.pi / 2, -math.pi / 2, 0.0, math.pi]]], dtype=torch.float64)
+    rr = torch.full_like(quarter, 0.5)
+    qr, qi = O.polar_transition(rr, quarter, 4)
+    assert torch.allclose(qr, torch.tensor([[[0.0, 0.0, 0.5, -0.5]]], dtype=torch.float64), atol=1e-15)
+    assert torch.allclose(qi, torch.tensor([[[0.5, -0.5, 0.0, 0.0]]], dtype=torch.float64), atol=1e-15)
+    back = torch.complex(ar, ai) * torch.exp(-1j * phi)
+    assert torch.allclose(back.real, r, atol=1e-15) and back.imag.abs().max() < 1e-15
+
+
+def test_polar_transition_matches_p1_at_equal_radius_and_phase():
+    """At eta = 0 the P1 radius is exp(-nu) and its phase theta + (1 - rho)
+    delta: with nu = -log r and the phase phi = theta + (1 - r) delta, the
+    P1 transition is the polar one of (r, phi), part for part."""
+    g = torch.Generator().manual_seed(62)
+    M, B, T = 6, 2, 9
+    r = torch.rand(M, generator=g, dtype=torch.float64) * 0.5 + 0.45
+    theta = torch.rand(M, generator=g, dtype=torch.float64) * 5.0 + 0.2
+    delta = (torch.rand(B, T, 1, generator=g, dtype=torch.float64) * 2 - 1) * (math.pi / 2)
+    eta = torch.zeros(B, T, 1, dtype=torch.float64)
+    pr, pi = O.p1_transition(eta, delta, torch.log(-torch.log(r)), torch.log(theta))
+    phi = theta + (1.0 - r) * delta                       # [B, T, M]
+    ar, ai = O.polar_transition(r.expand(B, T, M), phi, M)
+    assert torch.allclose(pr, ar, atol=1e-14) and torch.allclose(pi, ai, atol=1e-14)
+    assert (ai * torch.sin(phi) >= 0).all()               # the imaginary part follows +sin(phi)
 
 
 # --------------------------------------------------------------------------
