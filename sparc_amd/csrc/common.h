@@ -173,11 +173,19 @@ __device__ __forceinline__ void buf_store(T x, __amdgpu_buffer_rsrc_t r, uint32_
     __builtin_memcpy(&v, &x, 8);
     __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, soff, CPOL);
   } else {
+    // A store of more than 8 bytes reads its data registers after it issues:
+    // a VALU write to them right behind it needs wait states.  The compiler
+    // inserts them only for stores without a register soffset, and on gfx950
+    // a 16-byte buffer store with an SGPR soffset measurably stored the
+    // next step's value into its first dword now and then (the wide P1
+    // backward in fp32, before this).  So the uniform offset joins the lane
+    // offset (one add; the sum stays below 2^32 and past the resource for
+    // dropped lanes) and soffset is the constant 0.
     static_assert(sizeof(T) == 16, "2, 4, 8 or 16 bytes");
     typedef uint32_t u4 __attribute__((ext_vector_type(4)));
     u4 v;
     __builtin_memcpy(&v, &x, 16);
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, CPOL);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, voff + soff, 0, CPOL);
   }
 }
 
@@ -436,6 +444,29 @@ __device__ __forceinline__ void sincos_half_n(const float (&u)[N], float (&s)[N]
   }
 #pragma unroll
   for (int i = 0; i < N; ++i) c[i] = fmaf(pc[i], u2[i], 1.0f);
+}
+
+// sin and cos of 2 pi r through the hardware (v_sin_f32, v_cos_f32 take the
+// angle in revolutions).  Measured on MI355X over |2 pi r| <= pi/2 against
+// fp64: max abs error 1.4e-7 (sin) and 1.7e-7 (cos), mean error below 1e-8
+// (no bias that adds up over steps); each instruction issues at about half the
+// FMA rate, against 6 FMAs per function for the polynomials above.  Used for
+// bf16 I/O only: fp32 I/O keeps sincos_half (1.3e-7 / 0.9e-7, about 1 ulp).
+__device__ __forceinline__ void sincos_rev_hw(float r, float& s, float& c) {
+  s = __builtin_amdgcn_sinf(r);
+  c = __builtin_amdgcn_cosf(r);
+}
+constexpr float kNegInv2Pi = -0.15915494309189535f;  // -1 / (2 pi): a phase in radians -> revolutions, negated
+
+// Keeps the compiler from moving this wave's LDS accesses across it.  A
+// wave's own LDS reads and writes are performed in issue order, so a value
+// one lane writes is seen by a later read of another lane of the same wave
+// without a workgroup barrier (which would also wait for every outstanding
+// global load); no instruction is emitted.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // ---------------------------------------------------------------------------

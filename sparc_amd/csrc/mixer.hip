@@ -274,7 +274,7 @@ void launch_ctrl_fwd(hipStream_t st, int64_t R, int W, const void* x, const floa
 // ---------------------------------------------------------------------------
 template <int V, bool BWD>
 struct ModeConsts {
-  float nu[V], ct[V], st[V], g2[V], pl[V], rl[V], th[V], kappa[V], wrr_s[V], wpr_s[V];
+  float nu[V], nul[V], ct[V], st[V], g2[V], pl[V], rl[V], th[V], kappa[V], wrr_s[V], wpr_s[V];
   __device__ __forceinline__ void load(const float* consts, int m0, bool ok) {
 #pragma unroll
     for (int v = 0; v < V; ++v) {
@@ -286,6 +286,7 @@ struct ModeConsts {
       const float4 c1 = *reinterpret_cast<const float4*>(c + 4);
       nu[v] = ok ? c0.x : 0.0f; ct[v] = ok ? c0.y : 0.0f; st[v] = ok ? c0.z : 0.0f; g2[v] = ok ? c0.w : 0.0f;
       pl[v] = ok ? c1.x : 0.0f; rl[v] = ok ? c1.y : 0.0f; th[v] = ok ? c1.z : 0.0f; kappa[v] = ok ? c1.w : 0.0f;
+      nul[v] = nu[v] * kLog2e;
       if constexpr (BWD) {
         const float4 c2 = *reinterpret_cast<const float4*>(c + 8);
         wrr_s[v] = ok ? c2.x : 0.0f; wpr_s[v] = ok ? c2.y : 0.0f;
@@ -294,40 +295,88 @@ struct ModeConsts {
   }
 };
 
-// The P1 transitions of a block of S steps (lane s of ee, dv: e^eta and
-// delta of step s) for the lane's V modes, written one polynomial level at a
-// time across the S*V values so that their dependency chains interleave.
-// The transition of p1_step, value for value: a = rho e^{i (theta + (1 - rho)
-// delta)}, rho = exp(-nu E), E = e^eta, with rho - 1 (em) formed by expm1.
-template <int S, int V, bool BWD>
-__device__ __forceinline__ void p1_block_transitions(const ModeConsts<V, BWD>& mc, float ee, float dv,
+// How the kernels of one I/O type and chain mode evaluate the P1 transition
+// (every kernel of the pair the same way, so that forward, backward and the
+// summary passes of time segments see the same a):
+//   HW   (bf16 I/O): the sine and cosine of the phase step from the hardware
+//        (sincos_rev_hw) instead of the degree-9/10 polynomials;
+//   FAST (bf16 I/O, writes given): rho = 2^{-nu log2(e) E} and em = rho - 1
+//        from the hardware exponential alone, without expm1's series for
+//        |nu E| < 1/16.  em then carries the exponential's absolute error
+//        (~6e-8, the size of rho's own fp32 rounding) rather than a relative
+//        one; with the writes given, em only turns the phase (by em delta)
+//        and weighs the d delta terms, where that error is below the fp32
+//        rounding of rho.  The module keeps the series: its write gain goes
+//        as sqrt(em) for slow modes.
+// fp32 I/O keeps the polynomials and the series.
+template <typename IO, int MODE>
+struct P1Math {
+  static constexpr bool HW = sizeof(IO) == 2;
+  static constexpr bool FAST = HW && (MODE & 3) != kModule;
+};
+
+// The P1 transitions of a block of S steps for the lane's V modes, from each
+// step's E = e^eta, delta and (HW) dr = -delta / (2 pi), written one level at
+// a time across the S*V values so that their dependency chains interleave.
+// a = rho e^{i (theta + (1 - rho) delta)}, rho = exp(-nu E), with rho - 1
+// (em) formed as P1Math says; the value of p1_step, value for value.
+template <typename IO, int MODE, int S, int V, bool BWD>
+__device__ __forceinline__ void p1_block_transitions(const ModeConsts<V, BWD>& mc, const float (&E)[S],
+                                                     const float (&dl)[S], const float (&dr)[S],
                                                      float (&ar)[S][V], float (&ai)[S][V],
-                                                     float (*em_out)[V] = nullptr) {
+                                                     float (&em_out)[S][V]) {
+  using PM = P1Math<IO, MODE>;
   constexpr int N = S * V;
-  float q[N], em[N], u[N], su[N], cu[N], dl[S];
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    const float E = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), s));
-    dl[s] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv), s));
-#pragma unroll
-    for (int v = 0; v < V; ++v) q[s * V + v] = -mc.nu[v] * E;
-  }
-  expm1_nonpos_n<N>(q, em);
+  float q[N], em[N], rho[N], su[N], cu[N];
 #pragma unroll
   for (int s = 0; s < S; ++s)
 #pragma unroll
-    for (int v = 0; v < V; ++v) u[s * V + v] = -em[s * V + v] * dl[s];
-  sincos_half_n<N>(u, su, cu);
+    for (int v = 0; v < V; ++v) q[s * V + v] = PM::FAST ? -mc.nul[v] * E[s] : -mc.nu[v] * E[s];
+  if constexpr (PM::FAST) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) rho[i] = __builtin_amdgcn_exp2f(q[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) em[i] = rho[i] - 1.0f;
+  } else {
+    expm1_nonpos_n<N>(q, em);
+#pragma unroll
+    for (int i = 0; i < N; ++i) rho[i] = 1.0f + em[i];
+  }
+  if constexpr (PM::HW) {
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int v = 0; v < V; ++v) sincos_rev_hw(em[s * V + v] * dr[s], su[s * V + v], cu[s * V + v]);
+  } else {
+    float u[N];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int v = 0; v < V; ++v) u[s * V + v] = -em[s * V + v] * dl[s];
+    sincos_half_n<N>(u, su, cu);
+  }
 #pragma unroll
   for (int s = 0; s < S; ++s)
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       const int i = s * V + v;
-      const float rho = 1.0f + em[i];
-      ar[s][v] = rho * fmaf(mc.ct[v], cu[i], -mc.st[v] * su[i]);
-      ai[s][v] = rho * fmaf(mc.st[v], cu[i], mc.ct[v] * su[i]);
-      if (em_out) em_out[s][v] = em[i];
+      ar[s][v] = rho[i] * fmaf(mc.ct[v], cu[i], -mc.st[v] * su[i]);
+      ai[s][v] = rho[i] * fmaf(mc.st[v], cu[i], mc.ct[v] * su[i]);
+      em_out[s][v] = em[i];
     }
+}
+
+// The block's per-step values from lanes s of ee (e^eta), dv (delta), as
+// read by p1_block_transitions.
+template <int S>
+__device__ __forceinline__ void p1_block_steps(float ee, float dv, float (&E)[S], float (&dl)[S], float (&dr)[S]) {
+  const float drv = dv * kNegInv2Pi;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    E[s] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), s));
+    dl[s] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv), s));
+    dr[s] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(drv), s));
+  }
 }
 
 // Reset steps of a block (lane s of kv: 0 where step s resets): a := 0.  The
@@ -350,13 +399,17 @@ __device__ __forceinline__ void p1_block_resets(int kv, float (&ar)[S][V], float
 struct StepMode {
   float em, rho, ar, ai, gain, sg;
 };
+// HW: the phase step's sine and cosine from the hardware (P1Math), dr =
+// -delta / (2 pi).
+template <bool HW>
 __device__ __forceinline__ StepMode p1_step(float nu, float ct, float st, float g2, float pl, float rl,
-                                             float E, float eta, float delta) {
+                                             float E, float eta, float delta, float dr) {
   StepMode o;
   o.em = expm1_nonpos(-nu * E);  // rho - 1
   o.rho = 1.0f + o.em;
   float su, cu;
-  sincos_half(-o.em * delta, su, cu);  // phase (1 - rho) delta, |.| <= pi/2
+  if constexpr (HW) sincos_rev_hw(o.em * dr, su, cu);
+  else sincos_half(-o.em * delta, su, cu);  // phase (1 - rho) delta, |.| <= pi/2
   o.ar = o.rho * fmaf(ct, cu, -st * su);
   o.ai = o.rho * fmaf(st, cu, ct * su);
   // em (2 + em) = expm1(-2 nu E)
@@ -486,13 +539,15 @@ mixer_fwd_kernel(Args a) {
     constexpr bool TAIL = decltype(tail_tag)::value;
     float ar[kS][V], ai[kS][V], wr[kS][V], wi[kS][V];
     const float ee = fast_exp(ev[h]);  // lane s: e^eta of step s
-    if constexpr (GW) p1_block_transitions<kS, V>(mc, ee, dv[h], ar, ai);
+    float Es[kS], Ds[kS], Rs[kS];
+    p1_block_steps<kS>(ee, dv[h], Es, Ds, Rs);
+    if constexpr (GW) {
+      float em[kS][V];
+      p1_block_transitions<IO, MODE, kS, V>(mc, Es, Ds, Rs, ar, ai, em);
+    }
     if constexpr (RST) p1_block_resets<kS, V>(kv[h], ar, ai);
 #pragma unroll
     for (int s = 0; s < kS; ++s) {
-      const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
-      const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), s));
-      const float E = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), s));
       float cr[V], ci[V];
       unpack<IO, V>(xr[h][s], cr);
       unpack<IO, V>(xi[h][s], ci);
@@ -502,7 +557,9 @@ mixer_fwd_kernel(Args a) {
           wr[s][v] = cr[v];
           wi[s][v] = ci[v];
         } else {
-          const StepMode q = p1_step(mc.nu[v], mc.ct[v], mc.st[v], mc.g2[v], mc.pl[v], mc.rl[v], E, eta, delta);
+          const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
+          const StepMode q = p1_step<P1Math<IO, MODE>::HW>(mc.nu[v], mc.ct[v], mc.st[v], mc.g2[v], mc.pl[v],
+                                                           mc.rl[v], Es[s], eta, Ds[s], Rs[s]);
           ar[s][v] = q.ar;
           ai[s][v] = q.ai;
           wr[s][v] = q.gain * tanh_fast(cr[v]);
@@ -692,28 +749,22 @@ mixer_fwd_wide_kernel(Args a) {
   auto compute_block = [&](auto h_tag, int kb) __attribute__((always_inline)) {
     constexpr int h = decltype(h_tag)::value;
     const float ee = fast_exp(ev[h]);  // lane j: e^eta of step j
+    float Es[SPH], Ds[SPH], Rs[SPH];
+    p1_block_steps<SPH>(ee, dv[h], Es, Ds, Rs);
 #pragma unroll
     for (int j = 0; j < SPH; ++j) {
-      const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), j));
-      const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), j));
-      const float E = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), j));
       float ar[V], ai[V];
       float4 w0, w1;  // the table's write plane(s)
       if constexpr (GW) {
-        // the transition of p1_step (p1_block_transitions), a := 0 at a reset step
+        // the transition of p1_block_transitions, a := 0 at a reset step
         const bool keep = !RST || __builtin_amdgcn_readlane(kv[h], j) != 0;  // wave-uniform
-        float q[V], em[V], u[V], su[V], cu[V];
-#pragma unroll
-        for (int v = 0; v < V; ++v) q[v] = -mc.nu[v] * E;
-        expm1_nonpos_n<V>(q, em);
-#pragma unroll
-        for (int v = 0; v < V; ++v) u[v] = -em[v] * delta;
-        sincos_half_n<V>(u, su, cu);
+        float a1r[1][V], a1i[1][V], em[1][V];
+        const float E1[1] = {Es[j]}, D1[1] = {Ds[j]}, R1[1] = {Rs[j]};
+        p1_block_transitions<IO, MODE, 1, V>(mc, E1, D1, R1, a1r, a1i, em);
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-          const float rho = 1.0f + em[v];
-          ar[v] = keep ? rho * fmaf(mc.ct[v], cu[v], -mc.st[v] * su[v]) : 0.0f;
-          ai[v] = keep ? rho * fmaf(mc.st[v], cu[v], mc.ct[v] * su[v]) : 0.0f;
+          ar[v] = keep ? a1r[0][v] : 0.0f;
+          ai[v] = keep ? a1i[0][v] : 0.0f;
         }
         if constexpr (PACKW) {  // the raw bf16 writes, re in the low half of each dword
           const uint32_t* r = reinterpret_cast<const uint32_t*>(&xr[h][j]);
@@ -733,9 +784,11 @@ mixer_fwd_wide_kernel(Args a) {
         float cr[V], ci[V], wr[V], wi[V];
         unpack<IO, V>(xr[h][j], cr);
         unpack<IO, V>(xi[h][j], ci);
+        const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), j));
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-          const StepMode q = p1_step(mc.nu[v], mc.ct[v], mc.st[v], mc.g2[v], mc.pl[v], mc.rl[v], E, eta, delta);
+          const StepMode q = p1_step<P1Math<IO, MODE>::HW>(mc.nu[v], mc.ct[v], mc.st[v], mc.g2[v], mc.pl[v],
+                                                           mc.rl[v], Es[j], eta, Ds[j], Rs[j]);
           ar[v] = q.ar;
           ai[v] = q.ai;
           wr[v] = q.gain * tanh_fast(cr[v]);
@@ -880,6 +933,7 @@ mixer_bwd_kernel(Args a) {
   constexpr bool GW = CM == kPlanes;  // the writes are given: dw out, no relu mask
   static_assert(CM != kRelu, "the backward of the relu output recomputes states (scan.hip)");
   static_assert(GW || !RST, "resets in the P1 scan only");
+  __shared__ float4 tok[64];  // the block's per-step values (run_block)
   const int lane = threadIdx.x;
   const ChainPos cp = chain_pos(a);
   const int b = cp.b, mb = cp.mb, t_begin = cp.t_begin, t_end = cp.t_end;
@@ -1005,11 +1059,16 @@ mixer_bwd_kernel(Args a) {
     if constexpr (RST) kv[h] = p1_keep(a, b, t0 + (sl <= last ? sl : last));
   };
 
-  // One block of kS steps, in phases: (A) every step's transition
-  // (independent of the adjoint); (B) the adjoint, a short serial chain over
-  // the steps in reverse; (C) every step's write gain, tanh and gradients;
-  // (D) the stores and the wave sums of the per-token gradients.  The phases
-  // are straight-line code the compiler can interleave across steps.
+  // One block of kS steps: (A) every step's transition (independent of the
+  // adjoint), then (B) one pass over the steps in reverse: the adjoint
+  // lambda = dy (relu-masked in the module) + X, the write's gradient,
+  // X = conj(a) lambda (carried to the step before), and the transition
+  // gradients from Z = X conj(h'): for dA = lambda conj(h'), conj(a) dA = Z,
+  // so Re Z = gar a_re + gai a_im and Im Z = dphi, and radial = -log(rho)
+  // (rho delta Im Z - Re Z) = E nu (rho delta Im Z - Re Z) with the factor E
+  // of the step taken out of the per-mode products; then (C) the stores and
+  // the wave sums of the per-token gradients.  Straight-line code the
+  // compiler can interleave across steps.
   // TAIL: the block holding T-1 when T is not a multiple of kS.  The relu
   // mask of step t needs h_t: row t of the saved states, which is the
   // previous state of step t+1, or (last step of a block, and T-1) the carry
@@ -1017,18 +1076,35 @@ mixer_bwd_kernel(Args a) {
   auto run_block = [&](auto h_tag, int t0, auto tail_tag) {
     constexpr int h = decltype(h_tag)::value;
     constexpr bool TAIL = decltype(tail_tag)::value;
+    // the block's per-step values through LDS: lane s (< kS, the lanes above
+    // repeat them) writes step s's (E = e^eta, delta, -delta / (2 pi), eta),
+    // every lane reads them back (a broadcast read)
+    wave_lds_fence();
+    tok[lane] = make_float4(fast_exp(ev[h]), dv[h], dv[h] * kNegInv2Pi, ev[h]);
+    wave_lds_fence();
+    float Es[kS], Ds[kS], Rs[kS], Hs[kS];
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      const float4 t4 = tok[s];
+      Es[s] = t4.x;
+      Ds[s] = t4.y;
+      Rs[s] = t4.z;
+      Hs[s] = t4.w;
+    }
     float qar[kS][V], qai[kS][V], qem[kS][V];
-    const float ee = fast_exp(ev[h]);  // lane s: e^eta of step s
-    p1_block_transitions<kS, V>(mc, ee, dv[h], qar, qai, qem);
+    p1_block_transitions<IO, MODE, kS, V>(mc, Es, Ds, Rs, qar, qai, qem);
     if constexpr (RST) p1_block_resets<kS, V>(kv[h], qar, qai);
-    // (B) the adjoint
-    float lr[kS][V], li[kS][V];
+    RawT dwr[kS], dwi[kS];          // GW: the packed dw rows
+    float dxr[kS][V], dxi[kS][V];   // module: dx
+    float e[2 * kS];                // e[2s], e[2s+1]: this lane's d eta, d delta of step s
 #pragma unroll
     for (int s = kS - 1; s >= 0; --s) {
       const int t = t0 + s;
-      if (TAIL && t >= t_end) {
+      if (TAIL && t >= t_end) {  // wave-uniform: no such step
+        e[2 * s] = 0.0f;
+        e[2 * s + 1] = 0.0f;
 #pragma unroll
-        for (int v = 0; v < V; ++v) { lr[s][v] = 0.0f; li[s][v] = 0.0f; }
+        for (int v = 0; v < V; ++v) { dxr[s][v] = 0.0f; dxi[s][v] = 0.0f; }
         continue;
       }
       float gyr[V], gyi[V];
@@ -1050,38 +1126,22 @@ mixer_bwd_kernel(Args a) {
           gyi[v] = mi[v] > 0.0f ? gyi[v] : 0.0f;
         }
       }
+      if constexpr (SUMMARY) {  // the adjoint alone: no gradients, no stores
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        lr[s][v] = gyr[v] + Xr[v];
-        li[s][v] = gyi[v] + Xi[v];
-        Xr[v] = fmaf(qar[s][v], lr[s][v], qai[s][v] * li[s][v]);
-        Xi[v] = fmaf(qar[s][v], li[s][v], -qai[s][v] * lr[s][v]);
-        if constexpr (SUMMARY) {  // P <- conj(a) P
-          const float pr = fmaf(qar[s][v], Pr[v], qai[s][v] * Pi[v]);
+        for (int v = 0; v < V; ++v) {
+          const float l_r = gyr[v] + Xr[v], l_i = gyi[v] + Xi[v];
+          Xr[v] = fmaf(qar[s][v], l_r, qai[s][v] * l_i);
+          Xi[v] = fmaf(qar[s][v], l_i, -qai[s][v] * l_r);
+          const float pr2 = fmaf(qar[s][v], Pr[v], qai[s][v] * Pi[v]);  // P <- conj(a) P
           Pi[v] = fmaf(qar[s][v], Pi[v], -qai[s][v] * Pr[v]);
-          Pr[v] = pr;
+          Pr[v] = pr2;
         }
+        continue;
       }
-    }
-    if constexpr (SUMMARY) {  // the adjoint alone: no gradients, no stores
-      if constexpr (!GW) {
-        unpack<IO, V>(pr[h][0], hcr);
-        unpack<IO, V>(pi[h][0], hci);
-      }
-      return;
-    }
-    // (C) gradients; e[2s], e[2s+1]: this lane's d eta, d delta of step s
-    float dxr[kS][V], dxi[kS][V], e[2 * kS];
-#pragma unroll
-    for (int s = 0; s < kS; ++s) {
-      const int t = t0 + s;
-      const float eta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ev[h]), s));
-      const float delta = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(dv[h]), s));
-      const float E = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(ee), s));
       float hpr[V], hpi[V], cxr[V], cxi[V];
       unpack<IO, V>(pr[h][s], hpr);
       unpack<IO, V>(pi[h][s], hpi);
-      if (GW && s == 0) {  // the state before step 0 (t = 0 only at s = 0): selects, not a branch in the block
+      if (s == 0) {  // the state before step 0 (t = 0 only at s = 0): selects, not a branch in the block
         const bool first = t0 == 0;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
@@ -1093,35 +1153,31 @@ mixer_bwd_kernel(Args a) {
         unpack<IO, V>(xr[h][s], cxr);
         unpack<IO, V>(xi[h][s], cxi);
       }
+      const float E = Es[s], delta = Ds[s];
       float se = 0.0f, sd = 0.0f;
-      const bool live = !TAIL || t < t_end;  // steps past the segment contribute nothing (wave-uniform)
+      float lrv[V], liv[V];
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        // module: the state before step 0 per step (the per-block form above,
-        // and the trimmed forms below, measured 4 % slower in the module)
-        if (!GW && t == 0) { hpr[v] = h0r[v]; hpi[v] = h0i[v]; }
-        const float l_r = lr[s][v], l_i = li[s][v];
+        const float l_r = gyr[v] + Xr[v], l_i = gyi[v] + Xi[v];
+        const float xr1 = fmaf(qar[s][v], l_r, qai[s][v] * l_i);
+        const float xi1 = fmaf(qar[s][v], l_i, -qai[s][v] * l_r);
+        Xr[v] = xr1;
+        Xi[v] = xi1;
+        const float zr = fmaf(xr1, hpr[v], xi1 * hpi[v]);   // Re Z
+        const float zi = fmaf(xi1, hpr[v], -xr1 * hpi[v]);  // Im Z = dphi
+        const float em = qem[s][v];
+        const float tt = fmaf(fmaf(em, delta, delta), zi, -zr);  // rho delta dphi - Re Z
         if constexpr (GW) {  // dw = lambda; the transition gradients alone
-          const float em = qem[s][v], rho = 1.0f + em;
-          const float ar = qar[s][v], ai = qai[s][v];
-          dxr[s][v] = l_r;
-          dxi[s][v] = l_i;
-          const float gar = fmaf(l_r, hpr[v], l_i * hpi[v]);
-          const float gai = fmaf(l_i, hpr[v], -l_r * hpi[v]);
-          const float dphi = fmaf(-gar, ai, gai * ar);
-          const float z = mc.nu[v] * E;  // -log(rho)
-          const float radial = z * fmaf(rho * delta, dphi, -fmaf(gar, ar, gai * ai));
-          se += radial;
-          sd = fmaf(dphi, -em, sd);
-          if (live) {
-            acc[0][v] += radial;
-            acc[1][v] = fmaf(mc.th[v], dphi, acc[1][v]);
-          }
+          lrv[v] = l_r;
+          liv[v] = l_i;
+          const float u = mc.nu[v] * tt;  // radial / E
+          se += u;
+          sd = fmaf(-em, zi, sd);
+          acc[0][v] = fmaf(E, u, acc[0][v]);
+          acc[1][v] += zi;
         } else {  // module: the write path too
-          const float em = qem[s][v], rho = 1.0f + em;
-          const float ar = qar[s][v], ai = qai[s][v];
           const float e2 = fmaf(em, em, em + em);  // em (2 + em) = expm1(-2 nu E) = rho^2 - 1
-          const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(delta, mc.pl[v], eta * mc.rl[v])));
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(delta, mc.pl[v], Hs[s] * mc.rl[v])));
           // one reciprocal square root gives both sqrt(Y) = Y r and 1/e2 = g2 r^2
           // (Y >= 0; the floor keeps a zero gain at zero instead of 0 * inf)
           const float Y = mc.g2[v] * e2, r = __builtin_amdgcn_rsqf(fmaxf(Y, 1e-30f));
@@ -1132,29 +1188,35 @@ mixer_bwd_kernel(Args a) {
           dxr[s][v] = w_r * gain * fmaf(-tr, tr, 1.0f);
           dxi[s][v] = w_i * gain * fmaf(-ti, ti, 1.0f);
           const float g = fmaf(w_r, tr, w_i * ti) * gain;
-          const float gar = fmaf(l_r, hpr[v], l_i * hpi[v]);
-          const float gai = fmaf(l_i, hpr[v], -l_r * hpi[v]);
-          const float dphi = fmaf(-gar, ai, gai * ar);
-          const float z = mc.nu[v] * E;  // -log(rho)
-          const float radial = z * fmaf(rho * delta, dphi, -fmaf(gar, ar, gai * ai));
-          const float wterm = -z * fmaf(mc.g2[v], r * r, 1.0f);  // -z rho^2 / e2 = -z (1 + 1/e2)
+          // radial + g wterm = E nu (tt - g rho^2 / e2) with rho^2 / e2 = 1 + g2 r^2
+          const float u = mc.nu[v] * fmaf(-g, fmaf(mc.g2[v], r * r, 1.0f), tt);
           const float gs = g * (1.0f - sg);
-          se += radial + fmaf(g, wterm, gs * mc.wrr_s[v]);
-          sd += fmaf(dphi, -em, gs * mc.wpr_s[v]);
-          if (live) {
-            acc[0][v] += radial + g * (wterm - mc.kappa[v]);
-            acc[1][v] = fmaf(mc.th[v], dphi, acc[1][v]);
-            acc[2][v] += g;
-            acc[3][v] = fmaf(gs, delta * kTwoOverPi, acc[3][v]);
-            acc[4][v] = fmaf(gs, eta * kInvLog16, acc[4][v]);
-          }
+          se = fmaf(E, u, fmaf(gs, mc.wrr_s[v], se));
+          sd = fmaf(-em, zi, fmaf(gs, mc.wpr_s[v], sd));
+          acc[0][v] = fmaf(E, u, fmaf(-g, mc.kappa[v], acc[0][v]));
+          acc[1][v] += zi;
+          acc[2][v] += g;
+          acc[3][v] = fmaf(gs, delta * kTwoOverPi, acc[3][v]);
+          acc[4][v] = fmaf(gs, Hs[s] * kInvLog16, acc[4][v]);
         }
       }
-      // P1: lanes past M contribute 0, their constants being zero (ModeConsts)
-      e[2 * s] = GW || lane_ok ? se : 0.0f;
+      if constexpr (GW) {
+        dwr[s] = pack<IO, V>(lrv);
+        dwi[s] = pack<IO, V>(liv);
+        e[2 * s] = se * E;
+      } else {
+        e[2 * s] = lane_ok ? se : 0.0f;  // lanes past M: finite zeros from their zero constants, kept exact
+      }
       e[2 * s + 1] = GW || lane_ok ? sd : 0.0f;
     }
-    // (D) stores; the carry for the next block (in reverse time) is h_{t0-1}
+    if constexpr (SUMMARY) {
+      if constexpr (!GW) {
+        unpack<IO, V>(pr[h][0], hcr);
+        unpack<IO, V>(pi[h][0], hci);
+      }
+      return;
+    }
+    // (C) stores; the carry for the next block (in reverse time) is h_{t0-1}
     if constexpr (GW) {  // dw_re, dw_im planes
       const int64_t woff = wave_uniform(((row0 + t0) * a.M + mbase) * ESZ);
       const __amdgpu_buffer_rsrc_t rwr = make_rsrc(static_cast<char*>(a.dx) + woff, blk_h);
@@ -1163,8 +1225,8 @@ mixer_bwd_kernel(Args a) {
       for (int s = 0; s < kS; ++s) {
         if (TAIL && t0 + s >= t_end) break;
         const uint32_t o = static_cast<uint32_t>(s) * half_x;
-        buf_store<RawT, CPOL_NT>(pack<IO, V>(dxr[s]), rwr, lane_st, o);
-        buf_store<RawT, CPOL_NT>(pack<IO, V>(dxi[s]), rwi, lane_st, o);
+        buf_store<RawT, CPOL_NT>(dwr[s], rwr, lane_st, o);
+        buf_store<RawT, CPOL_NT>(dwi[s], rwi, lane_st, o);
       }
     } else {
       const int64_t xoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
@@ -1237,6 +1299,8 @@ mixer_bwd_kernel(Args a) {
   } else if (lane_ok) {
     const int64_t rows = static_cast<int64_t>(a.B) * a.n_seg, row = static_cast<int64_t>(b) * a.n_seg + cp.seg;
     constexpr int NP = GW ? 2 : 5;  // GW: nu_log and theta_log only
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[1][v] *= mc.th[v];  // d theta_log = theta sum dphi
 #pragma unroll
     for (int p = 0; p < NP; ++p)
 #pragma unroll
@@ -1619,12 +1683,14 @@ void run_fwd(const Args& a, hipStream_t st) {
 // 3.75 ms; B=16, T=2048, width 24576, 3072 waves: 2.77 -> 2.81 ms with 8).
 // The P1 scan (writes given) fits 8-step blocks in about 147 VGPRs: 1.61 ->
 // 1.52 ms at B=8, T=4096, M=16384, and faster with time segments too.  At two
-// modes per lane and without time segments it takes 16-step blocks at one
-// wave per SIMD (B=8, T=4096, M=16384: 1.43 -> 1.39 ms; B=16, T=2048: 1.42 ->
-// 1.34 ms); with time segments (4096 waves) those were slower (0.52 -> 0.58
-// ms at B=1, T=65536, M=2048).
+// modes per lane and without time segments, 16-step blocks at one wave per
+// SIMD were faster while the kernel was bound by its VALU work (B=8, T=4096,
+// M=16384: 1.43 -> 1.39 ms); with the transitions' hardware sine and cosine
+// and the transition gradients taken from conj(a) lambda it streams at its
+// access pattern's rate (the same time with the arithmetic stubbed out), and
+// 8-step blocks at two waves per SIMD are 2 % faster (1.29 -> 1.26 ms).
 #ifndef SPARC_MIXER_BWD_P1_S
-#define SPARC_MIXER_BWD_P1_S 16
+#define SPARC_MIXER_BWD_P1_S 8
 #endif
 #ifndef SPARC_MIXER_BWD_S
 #define SPARC_MIXER_BWD_S 4
@@ -1644,8 +1710,9 @@ void launch_bwd(const Args& a, int n_segs, hipStream_t st) {
     }
   }
   if constexpr ((MODE & 3) != kModule) {
-    if (a.n_seg == 1) {  // no time segments: 16-step blocks, one wave per SIMD
-      hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, SPARC_MIXER_BWD_P1_S, SUMMARY, MODE>), g, dim3(64), 0, st, a);
+    if (a.n_seg == 1) {  // no time segments; fp32 keeps 16-step blocks at one wave per SIMD (8 would spill)
+      constexpr int S = sizeof(IO) == 2 ? SPARC_MIXER_BWD_P1_S : 16;
+      hipLaunchKernelGGL((mixer_bwd_kernel<IO, V, S, SUMMARY, MODE>), g, dim3(64), 0, st, a);
       return;
     }
   }

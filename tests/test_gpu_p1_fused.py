@@ -128,3 +128,52 @@ def test_p1_wide_forward_matches_one_mode_per_lane(dtype, extra):
         if not case["relu"]:
             assert torch.equal(y_im[b:b + 1], r_im), f"row {b}: y_im"
         assert torch.equal(cs[b:b + 1], rc), f"row {b}: chunk states"
+
+
+@pytest.mark.parametrize("dtype,extra", [
+    (BF16, dict(h0=True, dlast=True)),
+    (F32, dict(h0=True, dlast=True)),
+    (BF16, dict(h0=True, dlast=True, seg=True, reset_first=True)),
+], ids=["h0_dlast_bf16", "h0_dlast_f32", "resets_bf16"])
+def test_p1_backward_batched_matches_row_by_row(dtype, extra):
+    """The P1 backward of a batch against each of its rows alone: every
+    (row, mode) chain runs the same adjoint recurrence value for value
+    whatever the batch around it (the batch's forward runs on wide chains,
+    one row's on the one-wave kernel; the backward takes the batch in 128-mode
+    chains), so dw and dh0 match bit for bit, as does every row's sum over
+    time of the per-mode terms; the per-token gradients (sums over the modes,
+    grouped otherwise) agree to fp32 rounding.  M = 16380 leaves a partial
+    last block of modes, T = 70 a partial last block of steps."""
+    B, T, M = 8, 70, 16380
+    print(f"[case] p1 backward batched vs rows B={B} T={T} M={M} {dtype} {extra}", flush=True)
+    case = make_case("p1", B, T, M, 1, dtype, seed=37, **extra)
+    segpos = None if case["segpos"] is None else case["segpos"].cuda()
+    init, dl = case["init"], case["dlast"]
+
+    def run(rows):
+        h0 = (None, None) if init is None else tuple(t[rows].cuda() for t in init)
+        sp = None if segpos is None else segpos[rows]
+        args = [case["g0"][rows].cuda(), case["g1"][rows].cuda(), case["w_re"][rows].cuda(),
+                case["w_im"][rows].cuda(), case["nu_log"].cuda(), case["theta_log"].cuda()]
+        y_re, y_im, cs = ops.scan_forward_raw("p1", *args, h0[0], h0[1], sp, case["reset_first"], False)
+        g = ops.scan_backward_raw("p1", args[0], args[1], args[2], args[3], cs, case["dy_re"][rows].cuda(),
+                                  case["dy_im"][rows].cuda(), args[4], args[5], h0[0], h0[1], sp,
+                                  case["reset_first"], False, dl[0][rows].cuda(), dl[1][rows].cuda(),
+                                  want_dh0=init is not None, y_re=y_re, y_im=y_im)
+        torch.cuda.synchronize()
+        return g
+
+    gb = run(slice(0, B))
+    dnu = torch.zeros_like(gb["dnu"])
+    dth = torch.zeros_like(gb["dth"])
+    for b in range(B):
+        gr = run(slice(b, b + 1))
+        for k in ("dw_re", "dw_im", "dh0_re", "dh0_im"):
+            if gb[k] is not None:
+                assert torch.equal(gb[k][b:b + 1], gr[k]), f"row {b}: {k}"
+        for k in ("dg0", "dg1"):
+            e = rel_err(gb[k][b:b + 1], gr[k])
+            assert e <= 1e-5, f"row {b}: {k} rel err {e:.3g}"
+        dnu += gr["dnu"]
+        dth += gr["dth"]
+    assert rel_err(gb["dnu"], dnu) <= 1e-5 and rel_err(gb["dth"], dth) <= 1e-5
