@@ -411,6 +411,35 @@ decode_dots_kernel(int B, int W, const void* x, const float* pdir, const float* 
   }
 }
 
+// One P1 decode step of 4 modes of a row: the transition a and the write
+// gain * tanh x from the per-mode constants c0 = (nu, cos theta, sin theta,
+// g2), c1 = (-log2(e) wpr, -log2(e) wrr, cos_lo, sin_lo) and the row's
+// phase and radial signals ps, rs with E = e^eta, delta; h <- a h + w in
+// place, y = relu(h) (NaN kept).
+__device__ __forceinline__ void decode_modes(const float4 (&c0)[4], const float4 (&c1)[4], float ps, float rs,
+                                             float E, float delta, const float (&xr)[4], const float (&xi)[4],
+                                             float (&hr)[4], float (&hi)[4], float (&yr)[4], float (&yi)[4]) {
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const float em = expm1_nonpos(-c0[v].x * E);  // rho - 1
+    const float rho = 1.0f + em;
+    float su, cu;
+    sincos_half(-em * delta, su, cu);            // (1 - rho) * delta
+    float cr, ci;
+    rotate_split(c0[v].y, c0[v].z, c1[v].z, c1[v].w, cu, su, cr, ci);
+    const float ar = rho * cr, ai = rho * ci;
+    // expm1(-2 nu E) = em (2 + em); sigmoid(q) = 1 / (1 + 2^(-q log2 e))
+    const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(ps, c1[v].x, rs * c1[v].y)));
+    const float gain = __builtin_amdgcn_sqrtf(c0[v].w * fmaf(em, em, em + em)) * sg;
+    const float nr = fmaf(ar, hr[v], fmaf(-ai, hi[v], gain * tanh_fast(xr[v])));
+    const float ni = fmaf(ai, hr[v], fmaf(ar, hi[v], gain * tanh_fast(xi[v])));
+    hr[v] = nr;
+    hi[v] = ni;
+    yr[v] = relu_keep_nan(nr);
+    yi[v] = relu_keep_nan(ni);
+  }
+}
+
 template <typename IO>
 __global__ void __launch_bounds__(256)
 decode_update_kernel(int B, int M, const void* x, const float* pbias, const float* rbias, const float* part,
@@ -435,13 +464,13 @@ decode_update_kernel(int B, int M, const void* x, const float* pbias, const floa
   }
   __syncthreads();
   if (m0 >= M) return;
-  float nu[SV], ct[SV], stt[SV], g2[SV], wp[SV], wrr_[SV], ctl[SV], stl[SV];
+  static_assert(SV == 4, "decode_modes takes 4 modes");
+  float4 c0[SV], c1[SV];
 #pragma unroll
   for (int v = 0; v < SV; ++v) {
     const float4* c = reinterpret_cast<const float4*>(consts + static_cast<int64_t>(m0 + v) * kDecodeConsts);
-    const float4 c0 = c[0], c1 = c[1];
-    nu[v] = c0.x; ct[v] = c0.y; stt[v] = c0.z; g2[v] = c0.w;
-    wp[v] = c1.x; wrr_[v] = c1.y; ctl[v] = c1.z; stl[v] = c1.w;
+    c0[v] = c[0];
+    c1[v] = c[1];
   }
   // Row loads are issued ahead of the stores of earlier rows (the new state
   // may be the old one, in place, so the compiler cannot hoist them itself):
@@ -496,25 +525,7 @@ decode_update_kernel(int B, int M, const void* x, const float* pbias, const floa
     unpack<float, SV>(hr_raw[slot], hr);
     unpack<float, SV>(hi_raw[slot], hi);
     float yr[SV], yi[SV];
-#pragma unroll
-    for (int v = 0; v < SV; ++v) {
-      const float em = expm1_nonpos(-nu[v] * E);  // rho - 1
-      const float rho = 1.0f + em;
-      float su, cu;
-      sincos_half(-em * delta, su, cu);            // (1 - rho) * delta
-      float cr, ci;
-      rotate_split(ct[v], stt[v], ctl[v], stl[v], cu, su, cr, ci);
-      const float ar = rho * cr, ai = rho * ci;
-      // expm1(-2 nu E) = em (2 + em); sigmoid(q) = 1 / (1 + 2^(-q log2 e))
-      const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(ps, wp[v], rs * wrr_[v])));
-      const float gain = __builtin_amdgcn_sqrtf(g2[v] * fmaf(em, em, em + em)) * sg;
-      const float nr = fmaf(ar, hr[v], fmaf(-ai, hi[v], gain * tanh_fast(xr[v])));
-      const float ni = fmaf(ai, hr[v], fmaf(ar, hi[v], gain * tanh_fast(xi[v])));
-      hr[v] = nr;
-      hi[v] = ni;
-      yr[v] = relu_keep_nan(nr);
-      yi[v] = relu_keep_nan(ni);
-    }
+    decode_modes(c0, c1, ps, rs, E, delta, xr, xi, hr, hi, yr, yi);
     buffer_store_f32<SV, SPARC_STEP_STATE_CPOL>(make_rsrc(new_re + srow - m0 + mb, row_bytes), soff, hr);
     buffer_store_f32<SV, SPARC_STEP_STATE_CPOL>(make_rsrc(new_im + srow - m0 + mb, row_bytes), soff, hi);
     store_raw_nt<IO, SV>(y, xrow, pack<IO, SV>(yr));
