@@ -410,7 +410,19 @@ sparc_status sparc_mixer_scan_backward(int64_t batch, int64_t length, int64_t mo
  * of the last state (both NULL: zero).  eta, delta, h_re, h_im as the
  * forward wrote them.  Writes dx [B,T,2M] (io_dtype) and, overwriting, the
  * direction gradients [2M+1] and the parameter gradients [M] (fp32).
- * Deterministic (fixed-order reductions, no atomics).
+ * Deterministic (fixed-order reductions).
+ *
+ * Forms (sparc_mixer_backward_form): where no time segments are needed (at
+ * least 1024 chains of 64 modes), T > 0 and every chain fits on the GPU at
+ * once at the kernel's occupancy, the call runs in ONE launch that also
+ * completes dx and the direction gradients: the chains of a batch row
+ * exchange per-block sums through the workspace (the last chain to arrive
+ * reduces them in a fixed order) and each chain completes a block two blocks
+ * after computing it.  Its waits are bounded (sparc_set_wait_limit): a wait
+ * that reaches the bound sets the workspace error word
+ * (sparc_scan_workspace_error) and leaves NaN gradients for that block, and
+ * every workgroup still finishes.  Otherwise the time pieces below, else one
+ * scan launch followed by the controls' backward.
  *
  * Streams: when T splits into time pieces (T a multiple of 256, and at least
  * 1024 chains of 64 modes, so that no time segments are needed; the
@@ -444,6 +456,18 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
                                   float* dtheta_log, float* dwrite_log_gain, float* dwrite_phase_response,
                                   float* dwrite_radial_response, void* workspace, size_t workspace_bytes,
                                   sparc_stream_t stream);
+
+/* The form sparc_mixer_backward takes for this shape on the current device:
+ * 2 (one launch), 1 (time pieces), 0 (one scan launch, then the controls'
+ * backward), -1 (invalid shape).  No counterpart in the reference (one Triton
+ * launch sequence). */
+int sparc_mixer_backward_form(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype);
+
+/* Process-wide: 0 (default) lets sparc_mixer_backward take the one-launch
+ * form wherever it applies, 1 never.  Returns the previous setting (-1 for
+ * an invalid argument).  For tests and A/B measurements; no counterpart in
+ * the reference. */
+int sparc_mixer_backward_plan(int plan);
 
 /* ---- the controls alone (make_controls) ----------------------------------
  * Rows x [rows, width] (io_dtype, width a positive multiple of 8, 16-byte

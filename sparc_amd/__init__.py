@@ -22,7 +22,7 @@ from .ops import (
     sparc_tiled_serial_scan,
     sparc_training_scan_dispatch,
 )
-from .mixer import get_mixer_path, set_mixer_path
+from .mixer import backward_form, get_mixer_path, set_backward_plan, set_mixer_path
 from .sparc import SPARCMixer, run_sequence
 
 __all__ = [
@@ -31,5 +31,5 @@ __all__ = [
     "complex_scan_with_last", "real_scan", "real_chunk_scan", "real_scan_with_last",
     "sparc_scan", "sparc_scan_with_last", "sparc_chunk_scan", "sparc_tiled_serial_scan",
     "sparc_training_scan_dispatch", "polar_chunk_scan", "grouped_real_scan", "scan_step",
-    "set_mixer_path", "get_mixer_path",
+    "set_mixer_path", "get_mixer_path", "set_backward_plan", "backward_form",
 ]

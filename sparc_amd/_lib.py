@@ -46,6 +46,8 @@ EXPORTED_SYMBOLS = (
     "sparc_mixer_workspace_bytes",
     "sparc_mixer_forward",
     "sparc_mixer_backward",
+    "sparc_mixer_backward_form",
+    "sparc_mixer_backward_plan",
     "sparc_mixer_scan_forward",
     "sparc_mixer_scan_backward",
     "sparc_controls_forward",
@@ -130,6 +132,10 @@ def load() -> ctypes.CDLL:
         lib.sparc_mixer_forward.restype = ctypes.c_int
         lib.sparc_mixer_backward.argtypes = [_I64, _I64, _I64, _I32] + [_P] * 24 + [_SZ, _P]
         lib.sparc_mixer_backward.restype = ctypes.c_int
+        lib.sparc_mixer_backward_form.argtypes = [_I64, _I64, _I64, _I32]
+        lib.sparc_mixer_backward_form.restype = ctypes.c_int
+        lib.sparc_mixer_backward_plan.argtypes = [ctypes.c_int]
+        lib.sparc_mixer_backward_plan.restype = ctypes.c_int
         lib.sparc_mixer_scan_forward.argtypes = [_I64, _I64, _I64, _I32] + [_P] * 14 + [_SZ, _P]
         lib.sparc_mixer_scan_forward.restype = ctypes.c_int
         lib.sparc_mixer_scan_backward.argtypes = [_I64, _I64, _I64, _I32] + [_P] * 22 + [_SZ, _P]

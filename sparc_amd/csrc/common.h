@@ -640,4 +640,6 @@ inline char* error_buffer() {
   static thread_local char buf[512] = "";
   return buf;
 }
+// The bound on each cross-workgroup wait, in polls (sparc_set_wait_limit).
+uint32_t wait_limit();
 }  // namespace sparc

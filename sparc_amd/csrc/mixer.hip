@@ -43,6 +43,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -86,7 +87,10 @@ template <typename IO> constexpr bool kRoundWrite = SPARC_MIXER_ROUND_WRITE && s
 //            states (forward only).
 //   | kReset: kPlanes or kRelu with reset steps (segment_pos[b, t] == 0, or
 //            step 0 with reset_first): the transition there is 0.
-enum : int { kModule = 0, kPlanes = 1, kRelu = 2, kReset = 4 };
+//   | kCoop: the module backward in one launch that also runs the controls'
+//            backward (dx completed, direction gradients): see
+//            mixer_bwd_kernel.
+enum : int { kModule = 0, kPlanes = 1, kRelu = 2, kReset = 4, kCoop = 8 };
 constexpr int kStateChunk = 64;  // steps per saved chunk state (sparc_scan_chunk_length)
 // A lane byte offset past every buffer resource of these kernels (each spans
 // less than 2^31 bytes): the hardware range check drops a store through it.
@@ -140,7 +144,57 @@ struct Args {
   float* chunk_state;
   const int32_t* segpos;  // [B,T] or NULL (kReset)
   int reset_first;        // kReset without segpos: step 0 resets
+  // kCoop: the directions [2M + 1] (phase, radial); the error word; every
+  // chain's wave sums of every block [B*n_blk][n_mb][2 kS] and the blocks'
+  // controls gradients [B*n_blk][2 kS] (both kCoopEmpty at launch), the same
+  // gradients per token [2][B*T] (phase, radial projection); the direction
+  // gradients per batch row [2][B][2M]; blocks per chain; polls before a
+  // wait gives up
+  const float* pdir;
+  const float* rdir;
+  uint32_t* coop_error;
+  float* coop_part;
+  float* coop_sum;
+  float* coop_dtok;
+  float* coop_pd;
+  int coop_nblk;
+  uint32_t coop_spin;
 };
+
+// kCoop ring entry (LDS): one step's dx of one mode, rounded to the I/O type
+// (the value the controls' backward adds its rank-2 term to), and its x.
+template <typename IO> struct CoopRing;
+template <> struct CoopRing<bf16> {
+  using T = uint2;  // bf16 pairs, re in the low half: dx, x
+  static __device__ __forceinline__ T put(float dr, float di, uint16_t xr, uint16_t xi) {
+    return make_uint2(pack_bf16x2(dr, di), static_cast<uint32_t>(xr) | (static_cast<uint32_t>(xi) << 16));
+  }
+  static __device__ __forceinline__ void get(const T& v, float& dr, float& di, float& xr, float& xi) {
+    dr = __uint_as_float(v.x << 16);
+    di = __uint_as_float(v.x & 0xffff0000u);
+    xr = __uint_as_float(v.y << 16);
+    xi = __uint_as_float(v.y & 0xffff0000u);
+  }
+};
+template <> struct CoopRing<float> {
+  using T = float4;  // dx re, dx im, x re, x im
+  static __device__ __forceinline__ T put(float dr, float di, float xr, float xi) { return make_float4(dr, di, xr, xi); }
+  static __device__ __forceinline__ void get(const T& v, float& dr, float& di, float& xr, float& xi) {
+    dr = v.x;
+    di = v.y;
+    xr = v.z;
+    xi = v.w;
+  }
+};
+// Blocks a chain keeps before completing them (its ring slots, 16 KB of LDS
+// per wave): a block's controls gradient is ready about two blocks after the
+// block (the records stored at its end, reduced at a later block's end);
+// the rest absorbs the chains' skew.
+template <typename IO> constexpr int kCoopLag = sizeof(IO) == 2 ? 8 : 4;
+// The records and the blocks' controls gradients start as this value, a
+// signalling NaN (arithmetic quiets those, so no computed value has this bit
+// pattern): a value that differs from it is final.
+constexpr uint32_t kCoopEmpty = 0x7fa00001u;
 
 // kReset: whether step t of batch row b keeps its transition (1) or resets
 // (0).  segment_pos is read through a buffer resource that is empty without
@@ -922,6 +976,27 @@ mixer_fwd_wide_kernel(Args a) {
 // (the P1 chain rule of sparc-kernal/backward/scan.py:593-644 and the write
 // gradients of sparc-kernal/backward/control.py:10-89).
 // two waves per SIMD; one for the P1 scan's 16-step blocks (about 256 VGPRs)
+//
+// kCoop (the module, one launch over all T, every chain resident at once):
+// the controls' backward runs inside.  d eta_t and d delta_t are sums over
+// all mode blocks of a batch row, known only once every chain of the row has
+// passed step t; dx_t needs them (dx += dp_phase u_phase + dp_radial
+// u_radial, dp the projections' gradients from d eta, d delta), and so do
+// the direction gradients (sum_t dp_t x_t).  So each chain stores its wave
+// sums of each block (its record) and counts itself in with an atomic; the
+// chain that arrives last sums the row's records in a fixed order (the
+// result does not depend on timing), turns them into dp and stores them.  A
+// chain keeps each block's dx (rounded to the I/O type) and x in an LDS ring
+// and completes the block kCoopLag blocks later, once dp differs from the
+// value it starts as.  Every step of this exchange waits only on memory
+// operations issued a block earlier, so the blocks' compute hides it.  A wait
+// depends only on blocks every chain passes before it waits itself, so it
+// ends once all chains of the row are resident (the host launches this form
+// only when the grid fits the GPU at the kernel's occupancy); it is bounded
+// anyway (coop_spin polls), after which the error word is set and the
+// block's gradients are NaN.  Replaces the controls-backward launches and
+// the dx round trip between them (sparc-kernal/backward/control.py:10-89 for
+// the controls' chain rule).
 template <typename IO, int V, int kS, bool SUMMARY, int MODE>
 __global__ void __launch_bounds__(64, (MODE & 3) == kPlanes && kS >= 16 ? 1 : 2)
 mixer_bwd_kernel(Args a) {
@@ -930,9 +1005,11 @@ mixer_bwd_kernel(Args a) {
   constexpr int MB = 64 * V;
   constexpr int CM = MODE & 3;             // the chain mode without kReset
   constexpr bool RST = (MODE & kReset) != 0;
+  constexpr bool COOP = (MODE & kCoop) != 0;
   constexpr bool GW = CM == kPlanes;  // the writes are given: dw out, no relu mask
   static_assert(CM != kRelu, "the backward of the relu output recomputes states (scan.hip)");
   static_assert(GW || !RST, "resets in the P1 scan only");
+  static_assert(!COOP || (CM == kModule && V == 1 && !SUMMARY), "one-launch form: the module, one mode per lane");
   __shared__ float4 tok[64];  // the block's per-step values (run_block)
   const int lane = threadIdx.x;
   const ChainPos cp = chain_pos(a);
@@ -959,6 +1036,26 @@ mixer_bwd_kernel(Args a) {
 
   ModeConsts<V, true> mc;
   mc.load(a.consts, m0, lane_ok);
+  // kCoop: the directions at this lane's channels (phase re, radial re, phase
+  // im, radial im), the direction-gradient sums in the same order, the ring
+  // of the blocks waiting for their controls gradient (block k in slot
+  // k % L), the next such gradient to use (loaded one block ahead) and the
+  // block this chain is to reduce and has not yet (-1: none)
+  constexpr int L = COOP ? kCoopLag<IO> : 1;
+  __shared__ typename CoopRing<IO>::T cring[L][COOP ? kS : 1][64];
+  float cu[4], ad[4], dpn[COOP ? 2 * kS : 1];
+  int pend = -1;
+  if constexpr (COOP) {
+    const int mm = lane_ok ? m0 : 0;
+    cu[0] = lane_ok ? a.pdir[mm] : 0.0f;
+    cu[1] = lane_ok ? a.rdir[mm] : 0.0f;
+    cu[2] = lane_ok ? a.pdir[a.M + mm] : 0.0f;
+    cu[3] = lane_ok ? a.rdir[a.M + mm] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ad[i] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2 * kS; ++i) dpn[i] = __uint_as_float(kCoopEmpty);
+  }
   float Xr[V], Xi[V];    // conj(a_{t+1}) lambda_{t+1}
   float hcr[V], hci[V];  // h at the last step of the next block to process
   float acc[5][V];       // nu_log, theta_log, wlg, wpr, wrr
@@ -1057,6 +1154,148 @@ mixer_bwd_kernel(Args a) {
     ev[h] = a.eta[ti];
     dv[h] = a.delta[ti];
     if constexpr (RST) kv[h] = p1_keep(a, b, t0 + (sl <= last ? sl : last));
+  };
+
+  // kCoop helpers.  Records, gradients and counts travel between chains
+  // (possibly on different XCDs) through agent-scope (sc1) accesses.
+  const int nblk = COOP ? a.coop_nblk : 1;
+  const int64_t slot0 = static_cast<int64_t>(b) * nblk;  // this batch row's first block
+  constexpr int NV = 2 * kS;                             // per-token values of a block
+  constexpr int KV = NV >= 16 ? NV / 16 : 1, GV = 64 * KV / NV;
+  // this chain's record of block kb: the leaders' wave sums (value i: d eta
+  // of step i/2 for even i, d delta for odd i)
+  auto coop_store_record = [&](int kb, const float (&sums)[NV]) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(a.coop_part + wave_uniform(((slot0 + kb) * a.n_mb + mb) * NV), static_cast<uint32_t>(NV * 4));
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+      const float v[1] = {sums[k]};
+      buffer_store_f32<1, CPOL_SC1>(rp, lane % GV == 0 ? static_cast<uint32_t>((lane / GV * KV + k) * 4) : kDropOffset,
+                                    v);
+    }
+  };
+  // block kc's controls gradient, every lane the same values
+  auto coop_load_grad = [&](int kc, float (&v)[NV]) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.coop_sum + wave_uniform((slot0 + kc) * NV), static_cast<uint32_t>(NV * 4));
+#pragma unroll
+    for (int j = 0; j < NV / 4; ++j) {
+      float t[4];
+      buffer_load_f32<4, CPOL_SC1>(rs, static_cast<uint32_t>(16 * j), t);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[4 * j + q] = t[q];
+    }
+  };
+  auto coop_final = [&](const float (&v)[NV]) -> bool {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) ok = ok && __float_as_uint(v[i]) != kCoopEmpty;
+    return __builtin_amdgcn_readfirstlane(static_cast<int>(ok)) != 0;
+  };
+  // The reduction of block kr by its chain (mode block kr % n_mb of the
+  // row): the row's records, once none is kCoopEmpty (else false, or with
+  // `wait` loads again, at most coop_spin polls: then the error word), summed
+  // in a fixed order (lane l the records l, l + 64, ..., then the wave's
+  // sums), turned into the projections' gradients as the controls' backward
+  // does (dp_radial = d eta log16 (1 - (eta/log16)^2), dp_phase = d delta
+  // pi/2 (1 - (2 delta/pi)^2)) and stored for the row's chains and per token.
+  auto coop_reduce = [&](int kr, bool wait) -> bool {
+    float r[NV];
+    const __amdgpu_buffer_rsrc_t rr =
+        make_rsrc(a.coop_part + wave_uniform((slot0 + kr) * a.n_mb * NV), static_cast<uint32_t>(a.n_mb * NV * 4));
+    for (uint32_t it = 0;; ++it) {
+      bool full = true;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) r[i] = 0.0f;
+      for (int c = lane; c < a.n_mb; c += 64) {
+#pragma unroll
+        for (int j = 0; j < NV / 4; ++j) {
+          float t[4];
+          buffer_load_f32<4, CPOL_SC1>(rr, static_cast<uint32_t>((c * NV + 4 * j) * 4), t);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            full = full && __float_as_uint(t[q]) != kCoopEmpty;
+            r[4 * j + q] += t[q];
+          }
+        }
+      }
+      if (__builtin_amdgcn_ballot_w64(!full) == 0) break;  // every record complete
+      if (!wait) return false;
+      const bool failed = it >= a.coop_spin ||
+                          ((it & 255u) == 255u && __builtin_amdgcn_readfirstlane(load_agent(a.coop_error)) != 0u);
+      if (failed) {
+        if (lane == 0) store_agent(a.coop_error, 1u);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) r[i] = __builtin_nanf("");
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    wave_sums_to_leaders<NV>(r);
+    const int t0r = t_begin + kr * kS;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.coop_sum + wave_uniform((slot0 + kr) * NV), static_cast<uint32_t>(NV * 4));
+    const bool lead = lane % GV == 0;
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+      const int i = lane / GV * KV + k, t = t0r + (i >> 1);
+      const bool live = t < t_end;
+      const float ee = (live ? a.eta[row0 + t] : 0.0f) * kInvLog16;
+      const float dd = (live ? a.delta[row0 + t] : 0.0f) * kTwoOverPi;
+      const float dp = (i & 1) ? r[k] * kHalfPi * fmaf(-dd, dd, 1.0f) : r[k] * kLog16 * fmaf(-ee, ee, 1.0f);
+      const float v[1] = {dp};
+      buffer_store_f32<1, CPOL_SC1>(rs, lead ? static_cast<uint32_t>(i * 4) : kDropOffset, v);
+      if (lead && live) a.coop_dtok[((i & 1) ? 0 : R) + row0 + t] = dp;  // [0] phase, [1] radial
+    }
+    return true;
+  };
+  // v holds block kc's gradient as loaded earlier; until it is final, load
+  // it again (at most coop_spin polls: then the error word, and NaN).  Its
+  // own chain reduces it first if it has not yet.
+  auto coop_await = [&](int kc, float (&v)[NV]) __attribute__((always_inline)) {
+    if (coop_final(v)) return;
+    if (kc % a.n_mb == mb) {  // this chain's block: reduce it now unless it has
+      coop_load_grad(kc, v);
+      if (!coop_final(v)) {
+        (void)coop_reduce(kc, true);
+        wait_stores_complete();
+      }
+      if (pend == kc) pend = -1;
+      coop_load_grad(kc, v);
+      if (coop_final(v)) return;
+    }
+    for (uint32_t it = 0; it < a.coop_spin; ++it) {
+      if ((it & 255u) == 255u && __builtin_amdgcn_readfirstlane(load_agent(a.coop_error)) != 0u) break;
+      __builtin_amdgcn_s_sleep(2);
+      coop_load_grad(kc, v);
+      if (coop_final(v)) return;
+    }
+    if (lane == 0) store_agent(a.coop_error, 1u);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = __builtin_nanf("");
+  };
+  // Block kc from its ring slot with its controls gradient dp: dx += dp_phase
+  // u_phase + dp_radial u_radial per channel (the controls' backward's order
+  // of operations), the direction sums dp x, the dx stores.
+  auto coop_finish = [&](int kc, const float (&dp)[NV]) __attribute__((always_inline)) {
+    const int sl = kc % L;
+    const int t0c = t_begin + kc * kS;
+    const int64_t xoff = wave_uniform(((row0 + t0c) * W + mbase) * ESZ);
+    const __amdgpu_buffer_rsrc_t rdx = make_rsrc(static_cast<char*>(a.dx) + xoff, blk_x);
+#pragma unroll
+    for (int s = 0; s < kS; ++s) {
+      if (t0c + s >= t_end) break;  // wave-uniform: the block holding T-1
+      float dr, di, xr1, xi1;
+      CoopRing<IO>::get(cring[sl][s][lane], dr, di, xr1, xi1);
+      const float p1 = dp[2 * s], p0 = dp[2 * s + 1];
+      const float gr[1] = {fmaf(p0, cu[0], fmaf(p1, cu[1], dr))};
+      const float gi[1] = {fmaf(p0, cu[2], fmaf(p1, cu[3], di))};
+      ad[0] = fmaf(p0, xr1, ad[0]);
+      ad[1] = fmaf(p1, xr1, ad[1]);
+      ad[2] = fmaf(p0, xi1, ad[2]);
+      ad[3] = fmaf(p1, xi1, ad[3]);
+      const uint32_t o = static_cast<uint32_t>(s) * row_x;
+      buf_store<typename Raw<IO, 1>::T, CPOL_NT>(pack<IO, 1>(gr), rdx, lane_st, o);
+      buf_store<typename Raw<IO, 1>::T, CPOL_NT>(pack<IO, 1>(gi), rdx, lane_st, o + half_x);
+    }
   };
 
   // One block of kS steps: (A) every step's transition (independent of the
@@ -1228,7 +1467,7 @@ mixer_bwd_kernel(Args a) {
         buf_store<RawT, CPOL_NT>(dwr[s], rwr, lane_st, o);
         buf_store<RawT, CPOL_NT>(dwi[s], rwi, lane_st, o);
       }
-    } else {
+    } else if constexpr (!COOP) {
       const int64_t xoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
       const __amdgpu_buffer_rsrc_t rdx = make_rsrc(static_cast<char*>(a.dx) + xoff, blk_x);
 #pragma unroll
@@ -1243,7 +1482,26 @@ mixer_bwd_kernel(Args a) {
     // each group of G lanes holds K of them (values i = lane / G * K + k)
     wave_sums_to_leaders<2 * kS>(e);
     constexpr int K = 2 * kS >= 16 ? 2 * kS / 16 : 1, G = 64 * K / (2 * kS);
-    {
+    if constexpr (COOP) {
+      // Blocks go nblk-1 .. 0.  Each step below waits on memory operations
+      // issued at least a block earlier, so that a block's compute hides them.
+      const int kb = (t0 - t_begin) / kS;
+      // reduce the block this chain owns once its records are in (tried at
+      // each block's end from two blocks after it)
+      if (pend < 0 && kb + 2 < nblk && (kb + 2) % a.n_mb == mb) pend = kb + 2;
+      if (pend >= 0 && coop_reduce(pend, false)) pend = -1;
+      coop_store_record(kb, e);
+      // complete block kb + L (this block's slot) with the gradient loaded at
+      // the previous block's end; load the one the next block completes
+      if (kb + L < nblk) {
+        coop_await(kb + L, dpn);
+        coop_finish(kb + L, dpn);
+      }
+      if (kb >= 1 && kb + L - 1 < nblk) coop_load_grad(kb + L - 1, dpn);
+      const int sl = kb % L;
+#pragma unroll
+      for (int s = 0; s < kS; ++s) cring[sl][s][lane] = CoopRing<IO>::put(dxr[s][0], dxi[s][0], xr[h][s], xi[h][s]);
+    } else {
       // value i (d eta for even i, d delta for odd i, of step t0 + i/2) goes
       // through the resource of its plane, which covers the block's steps
       // inside the segment; the other plane's store, non-leader lanes and
@@ -1288,6 +1546,24 @@ mixer_bwd_kernel(Args a) {
   for (; k >= 0; k -= 2) {  // k even here
     step_block(std::integral_constant<int, 0>{}, k);
     if (k >= 1) step_block(std::integral_constant<int, 1>{}, k - 1);
+  }
+  if constexpr (COOP) {
+    // complete the blocks still in the ring (reducing the ones this chain
+    // owns on the way), then store this chain's direction sums
+    for (int kc = min(L, nblk) - 1; kc >= 0; --kc) {
+      float v[NV];
+      coop_load_grad(kc, v);
+      coop_await(kc, v);
+      coop_finish(kc, v);
+    }
+    if (lane_ok) {
+      float* p0 = a.coop_pd + static_cast<int64_t>(b) * W;                 // [0][b]: phase
+      float* p1 = a.coop_pd + (static_cast<int64_t>(a.B) + b) * W;         // [1][b]: radial
+      p0[m0] = ad[0];
+      p1[m0] = ad[1];
+      p0[a.M + m0] = ad[2];
+      p1[a.M + m0] = ad[3];
+    }
   }
   if constexpr (SUMMARY) {
     if (lane_ok) {
@@ -1384,6 +1660,10 @@ mixer_seg_carry_kernel(int B, int M, int n_seg, int reverse, const float* seg_su
 __global__ void fill_zero_f32_kernel(float* p, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i < n) p[i] = 0.0f;
+}
+__global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
 }
 
 // ---------------------------------------------------------------------------
@@ -2225,12 +2505,166 @@ sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int6
   return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(e));
 }
 
+// ---------------------------------------------------------------------------
+// the module backward in one launch (kCoop)
+// ---------------------------------------------------------------------------
+// Which form sparc_mixer_backward takes: 0 the one-launch form wherever it
+// fits (below), 1 never (time pieces or the separate controls backward).
+std::atomic<int> g_bwd_plan{0};
+
+// Steps per block of the one-launch form: 4 (with 8 the ring and the
+// reduction's registers spill under the two-waves-per-SIMD bound).
+constexpr int kCoopS = 4;
+template <typename IO, int kS>
+const void* coop_kernel() {
+  return reinterpret_cast<const void*>(&mixer_bwd_kernel<IO, 1, kS, false, kModule | kCoop>);
+}
+// Workgroups of the kernel that the current device holds at once (0 on any
+// failure), cached per device.
+template <typename IO, int kS>
+int64_t coop_capacity() {
+  static std::atomic<int64_t> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  int64_t c = cache[dev].load(std::memory_order_relaxed);
+  if (c > 0) return c;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, coop_kernel<IO, kS>(), 64, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  c = static_cast<int64_t>(per_cu) * cus;
+  cache[dev].store(c, std::memory_order_relaxed);
+  return c;
+}
+
+struct CoopLayout {
+  int kS = 0, nblk = 0, n_mb = 0;
+  size_t consts = 0, part_mode = 0, part = 0, sum = 0, dtok = 0, pd = 0, total = 0;
+};
+// Byte 4 of the workspace is the error word (as for the scans, so that
+// sparc_scan_workspace_error reads it).
+CoopLayout coop_layout(int64_t B, int64_t T, int64_t M, int kS) {
+  CoopLayout c;
+  c.kS = kS;
+  c.n_mb = static_cast<int>((M + 63) / 64);
+  c.nblk = static_cast<int>((T + kS - 1) / kS);
+  auto up = [](size_t n) { return (n + 255) / 256 * 256; };
+  size_t off = 256;
+  c.consts = off;
+  off += up(static_cast<size_t>(M) * kConsts * 4);
+  c.part_mode = off;
+  off += up(static_cast<size_t>(5) * B * M * 4);
+  c.part = off;
+  off += up(static_cast<size_t>(B) * c.nblk * c.n_mb * 2 * kS * 4);
+  c.sum = off;
+  off += up(static_cast<size_t>(B) * c.nblk * 2 * kS * 4);
+  c.dtok = off;
+  off += up(static_cast<size_t>(2) * B * T * 4);
+  c.pd = off;
+  off += up(static_cast<size_t>(2) * B * 2 * M * 4);
+  c.total = off;
+  return c;
+}
+
+// The steps per block of the one-launch form for this call, or 0 where it
+// does not apply: the plan allows it, T > 0, one mode per lane and no time
+// segments (the chains fill the GPU), and every chain resident at once.
+int coop_steps(int64_t B, int64_t T, int64_t M, int32_t io) {
+  if (g_bwd_plan.load(std::memory_order_relaxed) != 0 || T <= 0) return 0;
+  const Layout l = layout(B, T, M, 1);
+  if (l.V != 1 || l.n_seg != 1) return 0;
+  const int64_t grid = B * l.n_mb;
+  const int64_t cap = io == SPARC_BF16 ? coop_capacity<sparc::bf16, kCoopS>() : coop_capacity<float, kCoopS>();
+  return grid <= cap ? kCoopS : 0;
+}
+
+sparc_status coop_backward(int kS, int64_t batch, int64_t length, int64_t modes, int32_t io_dtype, const void* x,
+                           const float* phase_direction, const float* radial_direction, const float* eta,
+                           const float* delta, const float* nu_log, const float* theta_log,
+                           const float* write_log_gain, const float* write_phase_response,
+                           const float* write_radial_response, const void* h_re, const void* h_im, const void* dy,
+                           const float* dlast_re, const float* dlast_im, void* dx, float* dphase_direction,
+                           float* dradial_direction, float* dnu_log, float* dtheta_log, float* dwrite_log_gain,
+                           float* dwrite_phase_response, float* dwrite_radial_response, char* ws, hipStream_t st) {
+  const CoopLayout c = coop_layout(batch, length, modes, kS);
+  const sparc_stream_t stream = reinterpret_cast<sparc_stream_t>(st);
+  const int M = static_cast<int>(modes), W = 2 * M;
+  float* consts = reinterpret_cast<float*>(ws + c.consts);
+  hipLaunchKernelGGL(mixer_prepare_kernel, dim3(static_cast<unsigned>((M + 255) / 256)), dim3(256), 0, st, M, nu_log,
+                     theta_log, write_log_gain, write_phase_response, write_radial_response, consts);
+  // the error word starts at zero, the records and the blocks' gradients as
+  // kCoopEmpty (fill kernels, not memsets: the call may be captured into a
+  // graph; the records and gradients are adjacent)
+  const int64_t nfill = static_cast<int64_t>(c.dtok - c.part) / 4;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(256), 0, st, reinterpret_cast<uint32_t*>(ws), int64_t(2), 0u);
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>((nfill + 255) / 256)), dim3(256), 0, st,
+                     reinterpret_cast<uint32_t*>(ws + c.part), nfill, kCoopEmpty);
+  Args a{};
+  a.B = static_cast<int>(batch);
+  a.T = static_cast<int>(length);
+  a.M = M;
+  a.n_mb = c.n_mb;
+  a.x = x; a.consts = consts; a.eta = eta; a.delta = delta;
+  a.h_re = const_cast<void*>(h_re); a.h_im = const_cast<void*>(h_im);
+  a.dy = dy; a.dlast_re = dlast_re; a.dlast_im = dlast_im; a.dx = dx;
+  a.part_mode = reinterpret_cast<float*>(ws + c.part_mode);
+  a.n_seg = 1; a.t_seg = static_cast<int>(length); a.seg_lo = 0;
+  a.pdir = phase_direction;
+  a.rdir = radial_direction;
+  a.coop_part = reinterpret_cast<float*>(ws + c.part);
+  a.coop_sum = reinterpret_cast<float*>(ws + c.sum);
+  a.coop_dtok = reinterpret_cast<float*>(ws + c.dtok);
+  a.coop_pd = reinterpret_cast<float*>(ws + c.pd);
+  a.coop_nblk = c.nblk;
+  a.coop_error = reinterpret_cast<uint32_t*>(ws) + 1;
+  a.coop_spin = sparc::wait_limit();
+  const dim3 g(static_cast<unsigned>(batch * c.n_mb));
+  constexpr int kC = kModule | kCoop;
+  static_assert(kCoopS == 4, "one instantiation per I/O type");
+  if (kS != kCoopS) return fail(SPARC_EINVAL, "mixer backward: steps per block");
+  if (io_dtype == SPARC_BF16)
+    hipLaunchKernelGGL((mixer_bwd_kernel<sparc::bf16, 1, kCoopS, false, kC>), g, dim3(64), 0, st, a);
+  else
+    hipLaunchKernelGGL((mixer_bwd_kernel<float, 1, kCoopS, false, kC>), g, dim3(64), 0, st, a);
+  if (hipError_t le = hipGetLastError()) return fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(le));
+  float* outs[5] = {dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response};
+  for (int p = 0; p < 5; ++p)
+    if (sparc_status s = sparc_column_sum(batch, modes, a.part_mode + static_cast<int64_t>(p) * batch * modes, outs[p],
+                                          0, stream))
+      return s;
+  const int64_t R = batch * length;
+  if (sparc_status s = sparc_column_sum(batch, W, a.coop_pd, dphase_direction, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(batch, W, a.coop_pd + batch * W, dradial_direction, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(R, 1, a.coop_dtok, dphase_direction + W, 0, stream)) return s;
+  if (sparc_status s = sparc_column_sum(R, 1, a.coop_dtok + R, dradial_direction + W, 0, stream)) return s;
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(e));
+}
+
 extern "C" {
 
 size_t sparc_mixer_workspace_bytes(int64_t batch, int64_t length, int64_t modes, int direction) {
   if (batch <= 0 || length < 0 || modes <= 0 || modes % 4 || (direction != 0 && direction != 1)) return 0;
-  // the module backward may run in time pieces (a larger workspace)
-  return std::max(layout(batch, length, modes, direction).total, layout(batch, length, modes, direction, false, true).total);
+  // the module backward may run in time pieces or in one launch (larger workspaces)
+  size_t n = std::max(layout(batch, length, modes, direction).total, layout(batch, length, modes, direction, false, true).total);
+  if (direction == 1) n = std::max(n, coop_layout(batch, length, modes, kCoopS).total);
+  return n;
+}
+
+int sparc_mixer_backward_plan(int plan) {
+  if (plan != 0 && plan != 1) return -1;
+  return g_bwd_plan.exchange(plan, std::memory_order_relaxed);
+}
+
+int sparc_mixer_backward_form(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype) {
+  if (check_shape(batch, length, modes, io_dtype)) return -1;
+  if (coop_steps(batch, length, modes, io_dtype)) return 2;
+  return layout(batch, length, modes, 1, false, true).piped ? 1 : 0;
 }
 
 sparc_status sparc_mixer_scan_forward(int64_t batch, int64_t length, int64_t modes, int32_t io_dtype,
@@ -2337,8 +2771,10 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
     return fail(SPARC_EINVAL, "mixer backward: NULL pointer");
   if ((dlast_re == nullptr) != (dlast_im == nullptr)) return fail(SPARC_EINVAL, "mixer backward: dlast_re/dlast_im");
   const Layout l = layout(batch, length, modes, 1, false, true);
-  if (!workspace || workspace_bytes < l.total)
-    return fail(SPARC_EWORKSPACE, "mixer backward: workspace too small (%zu < %zu)", workspace_bytes, l.total);
+  const int cs = coop_steps(batch, length, modes, io_dtype);
+  const size_t need = cs ? coop_layout(batch, length, modes, cs).total : l.total;
+  if (!workspace || workspace_bytes < need)
+    return fail(SPARC_EWORKSPACE, "mixer backward: workspace too small (%zu < %zu)", workspace_bytes, need);
   const size_t esz = io_dtype == SPARC_BF16 ? 2 : 4;
   if (!al(x, 16) || !al(dy, 16) || !al(dx, 16) || !al(h_re, esz * l.V) || !al(h_im, esz * l.V) ||
       !al(phase_direction, 16) || !al(radial_direction, 16) || !al(workspace, 256))
@@ -2346,6 +2782,11 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int M = static_cast<int>(modes), W = 2 * M;
   char* ws = static_cast<char*>(workspace);
+  if (cs)
+    return coop_backward(cs, batch, length, modes, io_dtype, x, phase_direction, radial_direction, eta, delta, nu_log,
+                         theta_log, write_log_gain, write_phase_response, write_radial_response, h_re, h_im, dy,
+                         dlast_re, dlast_im, dx, dphase_direction, dradial_direction, dnu_log, dtheta_log,
+                         dwrite_log_gain, dwrite_phase_response, dwrite_radial_response, ws, st);
   float* deta = reinterpret_cast<float*>(ws + l.tok);
   float* ddelta = deta + l.R;
   if (l.piped)

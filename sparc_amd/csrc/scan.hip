@@ -3660,6 +3660,13 @@ sparc_status fail(sparc_status s, const char* fmt, ...) {
 // Polls each cross-workgroup wait of the look-back kernels makes before it
 // gives up (sets the workspace error word and lets the workgroup finish).
 static std::atomic<uint32_t> g_wait_limit{1u << 20};
+}  // namespace
+
+namespace sparc {
+uint32_t wait_limit() { return g_wait_limit.load(std::memory_order_relaxed); }
+}  // namespace sparc
+
+namespace {
 
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 

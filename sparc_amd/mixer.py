@@ -33,6 +33,30 @@ def get_mixer_path() -> str:
     return _path
 
 
+_BWD_PLANS = ("auto", "pieces")
+
+
+def set_backward_plan(name: str) -> str:
+    """Form of the fused module backward (sparc_mixer_backward_plan):
+    "auto" runs it in one launch wherever every chain fits on the GPU at once
+    (the controls' backward inside), else in time pieces or as a scan launch
+    followed by the controls' backward; "pieces" never takes the one-launch
+    form.  Process-wide; returns the previous setting."""
+    if name not in _BWD_PLANS:
+        raise ValueError(f"unknown backward plan {name!r}")
+    prev = _lib.load().sparc_mixer_backward_plan(_BWD_PLANS.index(name))
+    return _BWD_PLANS[prev]
+
+
+def backward_form(batch: int, length: int, modes: int, dtype: torch.dtype) -> str:
+    """The form sparc_mixer_backward takes for this shape on the current GPU:
+    "one_launch", "pieces" or "separate" (sparc_mixer_backward_form)."""
+    f = _lib.load().sparc_mixer_backward_form(batch, length, modes, _lib.io_code(dtype))
+    if f < 0:
+        raise ValueError(_lib.load().sparc_last_error().decode(errors="replace"))
+    return ("separate", "pieces", "one_launch")[f]
+
+
 def fused_supported(x: torch.Tensor, modes: int) -> bool:
     return (x.is_cuda and x.dtype in (torch.float32, torch.bfloat16) and modes % 4 == 0
             and x.ndim == 3 and x.shape[0] > 0)
@@ -105,6 +129,7 @@ class _FusedMixer(torch.autograd.Function):
             B, T, M, io, P(x), *[P(p) for p in params], P(eta), P(delta), P(y), P(h_re), P(h_im),
             P(last_re), P(last_im), P(ws), ws.numel(), _lib.stream_of(dev)), "sparc_mixer_forward")
         ctx.save_for_backward(x, *params, eta, delta, h_re, h_im)
+        ctx.set_materialize_grads(False)  # unused last-state outputs: NULL, not zero tensors
         ctx.dtypes = [p.dtype for p in (phase_direction, radial_direction, nu_log, theta_log,
                                         write_log_gain, write_phase_response, write_radial_response)]
         ctx.energy = (energy_response.shape, energy_response.dtype)

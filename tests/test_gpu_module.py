@@ -97,19 +97,84 @@ def test_mixer_forward_backward_parity(dtype, tol, B, L, width, mixer_path):
         assert e <= tol, f"grad {name}: {e:.3g}"
 
 
+@pytest.mark.parametrize("plan", ["auto", "pieces"])
 @pytest.mark.parametrize("L,dtype,tol", [(512, torch.float32, 1e-4), (512, torch.bfloat16, 2e-2),
                                          (1024, torch.float32, 1e-4)])
-def test_fused_backward_time_pieces(L, dtype, tol):
-    """1024 chains of 64 modes and T a multiple of 512 (1024): the fused module
-    backward runs in four (eight) time pieces, the last first, with the controls
-    backward of each piece on a second stream beside the mixer backward of
-    the piece before it.  The adjoint crosses the pieces, dx is updated piece
-    by piece and the direction gradients sum the pieces' partials; all of it
+def test_fused_backward_time_pieces(L, dtype, tol, plan):
+    """1024 chains of 64 modes and T a multiple of 512 (1024).  "pieces": the
+    fused module backward runs in four (eight) time pieces, the last first,
+    with the controls backward of each piece on a second stream beside the
+    mixer backward of the piece before it; the adjoint crosses the pieces, dx
+    is updated piece by piece and the direction gradients sum the pieces'
+    partials.  "auto": every chain fits on the GPU at once, so it runs in one
+    launch that completes dx and the direction gradients itself.  Both
     against the float64 oracle, with a gradient through the last state."""
     sparc_amd.set_mixer_path("fused")
+    prev = sparc_amd.set_backward_plan(plan)
     try:
+        form = sparc_amd.backward_form(2, L, 32768, dtype)
+        print(f"[case] backward form {form}", flush=True)
+        assert form == ("one_launch" if plan == "auto" else "pieces")
         test_mixer_forward_backward_parity(dtype, tol, 2, L, 65536, "fused")
     finally:
+        sparc_amd.set_backward_plan(prev)
+        sparc_amd.set_mixer_path("auto")
+
+
+@pytest.mark.parametrize("L", [1, 3, 4, 6, 13])
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_one_launch_backward_short_sequences(L, dtype, tol):
+    """The one-launch module backward (B=16, width 8192: 1024 chains of 64
+    modes) on sequences of one block of four steps or less, a whole block,
+    and ragged tails (the chains complete each block two blocks after it, and
+    the last two at the end): against the float64 oracle."""
+    sparc_amd.set_mixer_path("fused")
+    try:
+        assert sparc_amd.backward_form(16, L, 4096, dtype) == "one_launch"
+        test_mixer_forward_backward_parity(dtype, tol, 16, L, 8192, "fused")
+    finally:
+        sparc_amd.set_mixer_path("auto")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_one_launch_backward_matches_pieces(dtype):
+    """At B=8, width 32768 (2048 chains: every SIMD holds two) the one-launch
+    backward against the time pieces on the same inputs: dx within two units
+    in the last place of its dtype plus 1e-6 of its largest value (both add
+    the same rank-2 term to the same rounded partial dx; d eta and d delta
+    are summed in different orders), every parameter gradient within 1e-5
+    relative."""
+    B, L, width = 8, 512, 32768
+    print(f"[case] one launch vs pieces B={B} L={L} width={width} {dtype}", flush=True)
+    sparc_amd.set_mixer_path("fused")
+    prev = sparc_amd.set_backward_plan("auto")
+    try:
+        assert sparc_amd.backward_form(B, L, width // 2, dtype) == "one_launch"
+        m = make_module(width, seed=31).cuda()
+        g = torch.Generator().manual_seed(32)
+        x = torch.randn(B, L, width, generator=g).to(dtype).cuda()
+        dy = torch.randn(B, L, width, generator=g).to(dtype).cuda()
+        outs = {}
+        for plan in ("auto", "pieces"):
+            sparc_amd.set_backward_plan(plan)
+            xx = x.clone().requires_grad_()
+            y, _ = m(xx)
+            outs[plan] = torch.autograd.grad((y.float() * dy.float()).sum(), [xx] + [getattr(m, n) for n in NAMES])
+        a, b = outs["auto"], outs["pieces"]
+        assert torch.isfinite(a[0]).all()
+        ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -23
+        ref = b[0].float().abs()
+        lim = 2 * ulp * ref + 1e-6 * ref.max()
+        bad = ((a[0].float() - b[0].float()).abs() > lim).sum().item()
+        print(f"[case] dx elements beyond the bound: {bad}; equal: {(a[0] == b[0]).float().mean().item():.4f}",
+              flush=True)
+        assert bad == 0
+        for name, ga, gb in zip(NAMES, a[1:], b[1:]):
+            e = rel_err(ga, gb)
+            print(f"[case] {name} rel {e:.2e}", flush=True)
+            assert e <= 1e-5, name
+    finally:
+        sparc_amd.set_backward_plan(prev)
         sparc_amd.set_mixer_path("auto")
 
 
