@@ -409,9 +409,10 @@ def bench_module(args, dev):
     reference does, controllers and write responses set to small random
     values so that every term is active).  On this shape the module runs the
     fused sequence path (controls, write, P1 scan, relu(cat) epilogue and their
-    backward).  Its kernels are VALU-bound (the counter summary's VALU busy),
-    so its roofline object reports the HBM rate of its algorithmic bytes
-    beside the measured traffic and VALU-busy figures."""
+    backward; the backward in one launch with the controls' backward inside,
+    `backward_form`).  Its kernels are VALU-bound (the counter summary's VALU
+    busy), so its roofline object reports the HBM rate of its algorithmic
+    bytes beside the measured traffic and VALU-busy figures."""
     import sparc_amd
     from sparc_amd.mixer import use_fused
     B, T, W = 8, 4096, 2 * 1024 * 16
@@ -450,7 +451,10 @@ def bench_module(args, dev):
     # of M (x in, y out; dy in, x in, dx out) and 6 fp32 control values
     M = W // 2
     algo_bytes = B * T * (M * 10 * 2 + 6 * 4)
-    kernels = ("ctrl_fwd_kernel", "mixer_fwd_wide_kernel", "mixer_bwd_kernel", "ctrl_bwd_kernel")
+    form = sparc_amd.backward_form(B, T, M, torch.bfloat16)
+    kernels = ("ctrl_fwd_kernel", "mixer_fwd_wide_kernel", "mixer_bwd_kernel")
+    if form != "one_launch":
+        kernels += ("ctrl_bwd_kernel",)
     traffic = measured_traffic(COUNTERS_FILE)
     valu = measured_valu_busy()
     measured = sum(traffic[k] for k in kernels) if path == "fused" and all(k in traffic for k in kernels) else None
@@ -460,7 +464,8 @@ def bench_module(args, dev):
             "traffic": measured, "traffic_source": COUNTERS_FILE if measured else None,
             "valu_busy_pct": {k: valu[k] for k in kernels if k in valu} or None}
     out = {"workload": "SPARCMixer forward + backward (the drop-in module), bf16 x, fp32 parameters",
-           "B": B, "T": T, "width": W, "path": path, "steps": steps, "ms_per_step": round(ms, 3),
+           "B": B, "T": T, "width": W, "path": path, "backward_form": form, "steps": steps,
+           "ms_per_step": round(ms, 3),
            "tokens_per_s": round(B * T / (ms * 1e-3), 1), "roofline": roof}
     out["few_chains"] = bench_module_few_chains(dev)
     return out
