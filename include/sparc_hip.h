@@ -187,10 +187,12 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d,
  * no cross-workgroup wait exceeded its bound, else 1.  For tests. */
 int sparc_scan_workspace_error(const void* workspace, sparc_stream_t stream);
 
-/* The bound on each cross-workgroup wait of the look-back kernels, in polls
- * (default 2^20, about a second).  A wait that reaches it sets the workspace
- * error word (sparc_scan_workspace_error) and its workgroup carries on, so
- * every launch finishes; the results of such a launch are invalid.  Applies
+/* The bound on each cross-workgroup wait of the look-back kernels and of the
+ * one-launch module backward (sparc_mixer_backward), in polls (default 2^20,
+ * about a second).  A wait that reaches it sets the workspace error word
+ * (sparc_scan_workspace_error, which reads either workspace) and its
+ * workgroup carries on, so every launch finishes; the results of such a
+ * launch are invalid (NaN where they depend on the missing value).  Applies
  * to launches issued after the call, process-wide; returns the previous
  * bound.  For tests and diagnostics (0: every wait fails at once).  No
  * counterpart in the reference, whose Triton scans have no cross-workgroup
