@@ -1,18 +1,20 @@
 """Graph capture of the drop-in module's forward and backward.
 
-At a shape whose backward runs in time pieces (the controls backward of each
-piece on the library's second stream), SPARCMixer forward + backward is
-captured into a HIP graph with torch.cuda.graph and replayed several times,
-with eager work and synchronisations between the replays; every replay must
-give the eager run's output and gradients bit for bit.  The reference launches
-every kernel on torch's current stream with no host synchronisation
+SPARCMixer forward + backward is captured into a HIP graph with
+torch.cuda.graph and replayed several times, with eager work and
+synchronisations between the replays; every replay must give the eager run's
+output and gradients bit for bit.  The reference launches every kernel on
+torch's current stream with no host synchronisation
 (sparc-kernal/backward/scan.py:1375-1640), so its path can be captured; so
-must this one.
+must this one.  Both forms of the backward at this shape: the one launch
+(the chains exchange per-block sums through the workspace; fill kernels, not
+memsets, reset it) and, with the one-launch form switched off, the time
+pieces (the controls backward of each piece on the library's second stream).
 
-Two orders: eager first (the second stream exists when the capture starts, so
-the fork and join become graph edges), and capture first in a fresh process
-(the library must not create a stream under capture: the pieces then run on
-the capturing stream alone, with the same results)."""
+Two orders for the pieces: eager first (the second stream exists when the
+capture starts, so the fork and join become graph edges), and capture first
+in a fresh process (the library must not create a stream under capture: the
+pieces then run on the capturing stream alone, with the same results)."""
 import math
 import os
 import subprocess
@@ -97,23 +99,33 @@ def _capture_and_replay(m, x, dy, dlast, expect, reps=3):
         _ = (x.float() * 2).sum().item()  # eager work between replays
 
 
-def test_module_fwd_bwd_graph_replays_match_eager():
+@pytest.mark.parametrize("plan", ["auto", "pieces"])
+def test_module_fwd_bwd_graph_replays_match_eager(plan):
     B, T, width = SHAPE
-    print(f"[case] module fwd+bwd graph capture after eager: B={B} T={T} width={width} bf16", flush=True)
-    m = _module(width, seed=41)
-    x, dy, dlast = _inputs(B, T, width, seed=42)
-    x.requires_grad_(True)
-    expect = _eager(m, x, dy, dlast)       # creates the library's second stream
-    again = _eager(m, x, dy, dlast)
-    for a, b in zip(expect, again):
-        assert torch.equal(a, b)           # the eager path is deterministic
-    _capture_and_replay(m, x, dy, dlast, expect)
+    print(f"[case] module fwd+bwd graph capture after eager: B={B} T={T} width={width} bf16 plan={plan}",
+          flush=True)
+    prev = sparc_amd.set_backward_plan(plan)
+    try:
+        form = sparc_amd.backward_form(B, T, width // 2, torch.bfloat16)
+        assert form == ("one_launch" if plan == "auto" else "pieces")
+        m = _module(width, seed=41)
+        x, dy, dlast = _inputs(B, T, width, seed=42)
+        x.requires_grad_(True)
+        expect = _eager(m, x, dy, dlast)       # pieces: creates the library's second stream
+        again = _eager(m, x, dy, dlast)
+        for a, b in zip(expect, again):
+            assert torch.equal(a, b)           # the eager path is deterministic
+        _capture_and_replay(m, x, dy, dlast, expect)
+    finally:
+        sparc_amd.set_backward_plan(prev)
 
 
 def _capture_first_main():
-    """Body of the fresh-process case: warm up at a shape without time
-    pieces (which creates no stream), capture at the pieced shape, then
-    compare with eager runs made after the capture."""
+    """Body of the fresh-process case, with the one-launch backward switched
+    off: warm up at a shape without time pieces (which creates no stream),
+    capture at the pieced shape, then compare with eager runs made after the
+    capture."""
+    sparc_amd.set_backward_plan("pieces")
     B, T, width = SHAPE
     m = _module(width, seed=43)
     x, dy, dlast = _inputs(B, T, width, seed=44)
