@@ -490,6 +490,9 @@ mixer_fwd_kernel(Args a) {
   constexpr bool GW = CM != kModule;  // the writes are given
   static_assert(kStateChunk % kS == 0, "blocks must tile the saved-state chunks");
   static_assert(GW || !RST, "resets in the P1 scan only");
+  // a summary's loads keep their lines in the caches (the replay that follows
+  // reads the same rows again); the replay's loads are their last use
+  constexpr int kSumLoad = SUMMARY ? CPOL_DEFAULT : CPOL_NT;
   const int lane = threadIdx.x;
   const ChainPos cp = chain_pos(a);
   const int b = cp.b, mb = cp.mb, t_begin = cp.t_begin, t_end = cp.t_end;
@@ -564,8 +567,8 @@ mixer_fwd_kernel(Args a) {
 #pragma unroll
       for (int s = 0; s < kS; ++s) {
         const uint32_t o = static_cast<uint32_t>(s <= last ? s : last) * half_x;
-        xr[h][s] = buf_load<RawT, CPOL_NT>(rwr, lane_ld, o);
-        xi[h][s] = buf_load<RawT, CPOL_NT>(rwi, lane_ld, o);
+        xr[h][s] = buf_load<RawT, kSumLoad>(rwr, lane_ld, o);
+        xi[h][s] = buf_load<RawT, kSumLoad>(rwi, lane_ld, o);
       }
     } else {
       const int64_t off = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
@@ -622,6 +625,25 @@ mixer_fwd_kernel(Args a) {
         }
       }
     }
+    if constexpr (SUMMARY) {
+      // the segment's map from a zero state, last step first: with P the
+      // product of the transitions after step t, the end state is the sum of
+      // P w_t (hr, hi += P w_t, then P <- P a_t); at the end P is the
+      // product over the whole segment
+#pragma unroll
+      for (int s = kS - 1; s >= 0; --s) {
+        if (TAIL && t0 + s >= t_end) continue;  // wave-uniform
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          hr[v] = fmaf(Pr[v], wr[s][v], fmaf(-Pi[v], wi[s][v], hr[v]));
+          hi[v] = fmaf(Pr[v], wi[s][v], fmaf(Pi[v], wr[s][v], hi[v]));
+          const float pr = fmaf(ar[s][v], Pr[v], -ai[s][v] * Pi[v]);
+          Pi[v] = fmaf(ai[s][v], Pr[v], ar[s][v] * Pi[v]);
+          Pr[v] = pr;
+        }
+      }
+      return;
+    }
     const int64_t yoff = wave_uniform(((row0 + t0) * W + mbase) * ESZ);
     const int64_t hoff = wave_uniform(((row0 + t0) * a.M + mbase) * ESZ);
     const __amdgpu_buffer_rsrc_t ry = make_rsrc(static_cast<char*>(a.y) + yoff, blk_x);
@@ -636,13 +658,7 @@ mixer_fwd_kernel(Args a) {
         const float ni = fmaf(ai[s][v], hr[v], fmaf(ar[s][v], hi[v], wi[s][v]));
         hr[v] = nr;
         hi[v] = ni;
-        if constexpr (SUMMARY) {
-          const float pr = fmaf(ar[s][v], Pr[v], -ai[s][v] * Pi[v]);
-          Pi[v] = fmaf(ai[s][v], Pr[v], ar[s][v] * Pi[v]);
-          Pr[v] = pr;
-        }
       }
-      if constexpr (SUMMARY) continue;
       if constexpr (CM != kPlanes) {  // y = relu(cat(h_re, h_im))
         float rr[V], ri[V];
 #pragma unroll
@@ -674,14 +690,18 @@ mixer_fwd_kernel(Args a) {
   // block k uses register buffer k & 1; the loop runs over pairs of blocks so
   // that every buffer index is a compile-time constant (a runtime index into
   // register arrays becomes indexed register access)
+  // A summary walks its segment last block first (blk), so that the rows it
+  // read last, still in the caches when the replay starts, are the ones the
+  // replay reads first.
+  auto blk = [&](int k) { return SUMMARY ? n_blocks - 1 - k : k; };
   auto step_block = [&](auto h_tag, int k) {
     constexpr int h = decltype(h_tag)::value;
-    load_block(std::integral_constant<int, 1 - h>{}, k + 1 < n_blocks ? k + 1 : k);
-    const int t0 = t_begin + k * kS;
+    load_block(std::integral_constant<int, 1 - h>{}, blk(k + 1 < n_blocks ? k + 1 : k));
+    const int t0 = t_begin + blk(k) * kS;
     if (t0 + kS <= t_end) run_block(h_tag, t0, std::false_type{});
     else run_block(h_tag, t0, std::true_type{});
   };
-  load_block(std::integral_constant<int, 0>{}, 0);
+  load_block(std::integral_constant<int, 0>{}, blk(0));
   for (int k = 0; k < n_blocks; k += 2) {
     step_block(std::integral_constant<int, 0>{}, k);
     if (k + 1 < n_blocks) step_block(std::integral_constant<int, 1>{}, k + 1);
@@ -983,12 +1003,15 @@ mixer_fwd_wide_kernel(Args a) {
 // passed step t; dx_t needs them (dx += dp_phase u_phase + dp_radial
 // u_radial, dp the projections' gradients from d eta, d delta), and so do
 // the direction gradients (sum_t dp_t x_t).  So each chain stores its wave
-// sums of each block (its record) and counts itself in with an atomic; the
-// chain that arrives last sums the row's records in a fixed order (the
-// result does not depend on timing), turns them into dp and stores them.  A
-// chain keeps each block's dx (rounded to the I/O type) and x in an LDS ring
-// and completes the block kCoopLag blocks later, once dp differs from the
-// value it starts as.  Every step of this exchange waits only on memory
+// sums of each block (its record, agent-scope stores, no atomics).  Each
+// block has one owner, the chain whose mode block is the block index mod
+// n_mb: from two blocks later it polls the row's records at its block ends
+// and, once none holds the empty marker they start as, sums them in a fixed
+// order (the result does not depend on timing), turns them into dp and
+// stores them.  A chain keeps each block's dx (rounded to the I/O type) and
+// x in an LDS ring and completes the block kCoopLag blocks later, once dp
+// differs from the marker (reducing it first if it owns the block and has
+// not yet).  Every step of this exchange waits only on memory
 // operations issued a block earlier, so the blocks' compute hides it.  A wait
 // depends only on blocks every chain passes before it waits itself, so it
 // ends once all chains of the row are resident (the host launches this form
@@ -1010,6 +1033,7 @@ mixer_bwd_kernel(Args a) {
   static_assert(CM != kRelu, "the backward of the relu output recomputes states (scan.hip)");
   static_assert(GW || !RST, "resets in the P1 scan only");
   static_assert(!COOP || (CM == kModule && V == 1 && !SUMMARY), "one-launch form: the module, one mode per lane");
+  constexpr int kSumLoad = SUMMARY ? CPOL_DEFAULT : CPOL_NT;  // as in mixer_fwd_kernel
   __shared__ float4 tok[64];  // the block's per-step values (run_block)
   const int lane = threadIdx.x;
   const ChainPos cp = chain_pos(a);
@@ -1130,12 +1154,12 @@ mixer_bwd_kernel(Args a) {
       const int sc = s <= last ? s : last;
       if constexpr (GW) {
         const uint32_t o = static_cast<uint32_t>(sc) * half_x;
-        dr[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o);
-        di[h][s] = buf_load<RawT, CPOL_NT>(rdi, lane_ld, o);
+        dr[h][s] = buf_load<RawT, kSumLoad>(rdy, lane_ld, o);
+        di[h][s] = buf_load<RawT, kSumLoad>(rdi, lane_ld, o);
       } else {
         const uint32_t o = static_cast<uint32_t>(sc) * row_x;
-        dr[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o);
-        di[h][s] = buf_load<RawT, CPOL_NT>(rdy, lane_ld, o + half_x);
+        dr[h][s] = buf_load<RawT, kSumLoad>(rdy, lane_ld, o);
+        di[h][s] = buf_load<RawT, kSumLoad>(rdy, lane_ld, o + half_x);
         if constexpr (!SUMMARY) {  // summaries need no write path
           xr[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o);
           xi[h][s] = buf_load<RawT, CPOL_NT>(rx, lane_ld, o + half_x);
@@ -1333,6 +1357,28 @@ mixer_bwd_kernel(Args a) {
     float qar[kS][V], qai[kS][V], qem[kS][V];
     p1_block_transitions<IO, MODE, kS, V>(mc, Es, Ds, Rs, qar, qai, qem);
     if constexpr (RST) p1_block_resets<kS, V>(kv[h], qar, qai);
+    if constexpr (GW && SUMMARY) {
+      // the adjoint's map over the segment from a zero adjoint after it,
+      // first step first: with P the product of conj(a) up to step t, the
+      // adjoint leaving the segment is the sum of P dy_t (P <- P conj(a_t),
+      // then Xr, Xi += P dy_t)
+#pragma unroll
+      for (int s = 0; s < kS; ++s) {
+        if (TAIL && t0 + s >= t_end) break;  // wave-uniform
+        float gyr[V], gyi[V];
+        unpack<IO, V>(dr[h][s], gyr);
+        unpack<IO, V>(di[h][s], gyi);
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const float pr2 = fmaf(qar[s][v], Pr[v], qai[s][v] * Pi[v]);
+          Pi[v] = fmaf(qar[s][v], Pi[v], -qai[s][v] * Pr[v]);
+          Pr[v] = pr2;
+          Xr[v] = fmaf(Pr[v], gyr[v], fmaf(-Pi[v], gyi[v], Xr[v]));
+          Xi[v] = fmaf(Pr[v], gyi[v], fmaf(Pi[v], gyr[v], Xi[v]));
+        }
+      }
+      return;
+    }
     RawT dwr[kS], dwi[kS];          // GW: the packed dw rows
     float dxr[kS][V], dxi[kS][V];   // module: dx
     float e[2 * kS];                // e[2s], e[2s+1]: this lane's d eta, d delta of step s
@@ -1527,21 +1573,25 @@ mixer_bwd_kernel(Args a) {
     }
   };
 
-  // block k uses register buffer k & 1 (compile-time in each call, see the forward)
+  // block k uses register buffer k & 1 (compile-time in each call, see the
+  // forward).  A summary of given writes walks its segment first block first
+  // (blk): the rows it read last, still in the caches when the replay starts,
+  // are then the ones the replay (in reverse time) reads first.
+  auto blk = [&](int k) { return GW && SUMMARY ? n_blocks - 1 - k : k; };
   auto step_block = [&](auto h_tag, int k) {
     constexpr int h = decltype(h_tag)::value;
-    load_block(std::integral_constant<int, 1 - h>{}, k > 0 ? k - 1 : k);
-    const int t0 = t_begin + k * kS;
+    load_block(std::integral_constant<int, 1 - h>{}, blk(k > 0 ? k - 1 : k));
+    const int t0 = t_begin + blk(k) * kS;
     if (t0 + kS <= t_end) run_block(h_tag, t0, std::false_type{});
     else run_block(h_tag, t0, std::true_type{});
   };
   int k = n_blocks - 1;
   if (k & 1) {
-    load_block(std::integral_constant<int, 1>{}, k);
+    load_block(std::integral_constant<int, 1>{}, blk(k));
     step_block(std::integral_constant<int, 1>{}, k);
     --k;
   } else {
-    load_block(std::integral_constant<int, 0>{}, k);
+    load_block(std::integral_constant<int, 0>{}, blk(k));
   }
   for (; k >= 0; k -= 2) {  // k even here
     step_block(std::integral_constant<int, 0>{}, k);
