@@ -418,8 +418,9 @@ sparc_status sparc_mixer_scan_backward(int64_t batch, int64_t length, int64_t mo
  * least 1024 chains of 64 modes), T > 0 and every chain fits on the GPU at
  * once at the kernel's occupancy, the call runs in ONE launch that also
  * completes dx and the direction gradients: the chains of a batch row
- * exchange per-block sums through the workspace (the last chain to arrive
- * reduces them in a fixed order) and each chain completes a block two blocks
+ * exchange per-block sums through the workspace (no atomics: each block has
+ * one owner chain, which sums the row's records in a fixed order once all
+ * are stored) and each chain completes a block eight blocks (fp32: four)
  * after computing it.  Its waits are bounded (sparc_set_wait_limit): a wait
  * that reaches the bound sets the workspace error word
  * (sparc_scan_workspace_error) and leaves NaN gradients for that block, and
@@ -467,8 +468,10 @@ int sparc_mixer_backward_form(int64_t batch, int64_t length, int64_t modes, int3
 
 /* Process-wide: 0 (default) lets sparc_mixer_backward take the one-launch
  * form wherever it applies, 1 never.  Returns the previous setting (-1 for
- * an invalid argument).  For tests and A/B measurements; no counterpart in
- * the reference. */
+ * an invalid argument).  For tests and A/B measurements, and for callers
+ * that keep other kernels running on the same GPU beside the backward (the
+ * one-launch form's waits last until all of its chains are resident); no
+ * counterpart in the reference. */
 int sparc_mixer_backward_plan(int plan);
 
 /* ---- the controls alone (make_controls) ----------------------------------
