@@ -504,6 +504,28 @@ sparc_status sparc_controls_backward(int64_t rows, int64_t width, int32_t io_dty
                                      float* dphase_direction, float* dradial_direction, void* workspace,
                                      size_t workspace_bytes, sparc_stream_t stream);
 
+/* ---- RMSNorm (the block stack's pre-norm and final norm) -----------------
+ * x, y [rows, cols] and weight [cols] in io_dtype (cols a positive multiple
+ * of 8 up to 4096; x, y and weight 16-byte aligned); rstd [rows] fp32.
+ * Forward: rstd = 1 / sqrt(mean over the row of x^2 + eps), y = (x rstd)
+ * weight, in fp32 arithmetic.  No counterpart in the reference, which ships
+ * the layer, not a network: torch.nn.RMSNorm's formula for the 12-layer
+ * stack that runs the layer in its training configuration. */
+sparc_status sparc_rms_norm_forward(int64_t rows, int64_t cols, int32_t io_dtype, const void* x, const void* weight,
+                                    float eps, void* y, float* rstd, sparc_stream_t stream);
+
+/* Workspace bytes of sparc_rms_norm_backward (0: invalid shape). */
+size_t sparc_rms_norm_workspace_bytes(int64_t rows, int64_t cols);
+
+/* Backward of sparc_rms_norm_forward given rstd from it and dy [rows, cols]
+ * (io_dtype): dx = rstd (g - xhat mean(g xhat)) with xhat = x rstd, g = dy
+ * weight (io_dtype, 16-byte aligned), and dweight [cols] fp32 = the sum over
+ * rows of dy xhat, overwritten, in a fixed order (zero with rows = 0; the row
+ * tensors and the workspace may then be NULL). */
+sparc_status sparc_rms_norm_backward(int64_t rows, int64_t cols, int32_t io_dtype, const void* x, const void* weight,
+                                     const float* rstd, const void* dy, void* dx, float* dweight, void* workspace,
+                                     size_t workspace_bytes, sparc_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
