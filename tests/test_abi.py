@@ -170,6 +170,26 @@ def test_controls_entry_points_validate_on_host():
     assert st == 4 and b"workspace" in lib.sparc_last_error()
 
 
+def test_rms_norm_entry_points_validate_on_host():
+    """sparc_rms_norm_*: cols a positive multiple of 8 up to 4096, a known
+    I/O type, non-NULL pointers, a large enough workspace (one fp32 partial
+    row of dweight per 8 rows)."""
+    lib = _lib.load()
+    assert lib.sparc_rms_norm_workspace_bytes(-1, 768) == 0
+    assert lib.sparc_rms_norm_workspace_bytes(1000, 768) == 125 * 768 * 4 + 256
+    eps = ctypes.c_float(1e-6)
+    assert lib.sparc_rms_norm_forward(4, 12, 0, None, None, eps, None, None, None) == 1
+    assert b"multiple of 8" in lib.sparc_last_error()
+    assert lib.sparc_rms_norm_forward(4, 8192, 0, None, None, eps, None, None, None) == 1
+    assert lib.sparc_rms_norm_forward(4, 16, 7, None, None, eps, None, None, None) == 1
+    assert b"io_dtype" in lib.sparc_last_error()
+    assert lib.sparc_rms_norm_forward(4, 16, 0, None, None, eps, None, None, None) == 1
+    assert b"NULL" in lib.sparc_last_error()
+    fake = ctypes.c_void_p(256)  # never dereferenced: the size check fails first
+    st = lib.sparc_rms_norm_backward(4, 16, 0, *([fake] * 7), 0, None)
+    assert st == 4 and b"workspace" in lib.sparc_last_error()
+
+
 def _raw_inputs(transition="p1", B=2, T=5, M=8, G=2, io=torch.float32):
     g = torch.float32 if transition == "p1" else io
     d = dict(g0=torch.zeros(B, T, G, dtype=g), g1=torch.zeros(B, T, G, dtype=g),
