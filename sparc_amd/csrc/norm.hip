@@ -182,7 +182,8 @@ sparc_status check_norm(int64_t rows, int64_t cols, int32_t io) {
   if (rows < 0 || cols <= 0 || cols % 8 || cols > kNormMaxCols)
     return norm_fail(SPARC_EINVAL, "rms norm: rows >= 0 and cols a positive multiple of 8 up to 4096 required");
   if (io != SPARC_F32 && io != SPARC_BF16) return norm_fail(SPARC_EINVAL, "rms norm: io_dtype");
-  if (rows > (int64_t(1) << 40) / cols) return norm_fail(SPARC_EINVAL, "rms norm: too large");
+  // grids of rows / 4 and rows / 8 workgroups; 64-bit element offsets
+  if (rows > INT32_MAX || rows > (int64_t(1) << 40) / cols) return norm_fail(SPARC_EINVAL, "rms norm: too large");
   return SPARC_OK;
 }
 
