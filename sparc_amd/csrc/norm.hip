@@ -218,7 +218,7 @@ sparc_status sparc_rms_norm_forward(int64_t rows, int64_t cols, int32_t io_dtype
 
 size_t sparc_rms_norm_workspace_bytes(int64_t rows, int64_t cols) {
   using namespace sparc;
-  if (rows < 0 || cols <= 0) return 0;
+  if (rows < 0 || rows > INT32_MAX || cols <= 0 || cols % 8 || cols > kNormMaxCols) return 0;
   const int64_t blocks = (rows + kNormBwdRows - 1) / kNormBwdRows;
   return static_cast<size_t>(blocks) * static_cast<size_t>(cols) * sizeof(float) + 256;
 }

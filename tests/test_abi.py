@@ -176,6 +176,7 @@ def test_rms_norm_entry_points_validate_on_host():
     row of dweight per 8 rows)."""
     lib = _lib.load()
     assert lib.sparc_rms_norm_workspace_bytes(-1, 768) == 0
+    assert lib.sparc_rms_norm_workspace_bytes(10, 12) == 0
     assert lib.sparc_rms_norm_workspace_bytes(1000, 768) == 125 * 768 * 4 + 256
     eps = ctypes.c_float(1e-6)
     assert lib.sparc_rms_norm_forward(4, 12, 0, None, None, eps, None, None, None) == 1
