@@ -6,9 +6,9 @@
 //             dx = rstd (g - xhat mean(g xhat)),  dw = sum over rows of dy xhat
 // in fp32 arithmetic with x, w, y, dy, dx in the I/O type.  Forward: one wave
 // per row, 8 consecutive columns per lane and chunk; backward: one wave per
-// block of kNormBwdRows rows, whose per-column sums of dy xhat form one
-// partial row of dw; the partial rows are summed in a fixed order
-// (sparc_column_sum), so dw does not depend on timing.  The reference ships
+// kNormBwdRows rows, and the per-column sums of dy xhat of a workgroup's
+// waves form one partial row of dw; the partial rows are summed in a fixed
+// order (sparc_column_sum), so dw does not depend on timing.  The reference ships
 // the layer, not a network; the stack is this library's harness for the
 // 12-layer training configuration.
 
@@ -20,7 +20,15 @@ namespace {
 
 constexpr int kNormWaves = 4;      // rows per forward workgroup, one per wave
 constexpr int kNormMaxCols = 4096; // 8 chunks of 64 lanes x 8 columns
-constexpr int kNormBwdRows = 8;    // rows per backward wave (one dw partial row)
+constexpr int kNormBwdRows = 8;    // rows per backward wave
+// waves per backward workgroup (one dw partial row each): 16, fewer where a
+// lane holds more columns (the register bound of 64 NW threads per workgroup)
+constexpr int bwd_waves(int nch) { return nch <= 2 ? 16 : (nch <= 4 ? 8 : 4); }
+constexpr int nch_of(int64_t cols) { return cols <= 512 ? 1 : cols <= 1024 ? 2 : cols <= 2048 ? 4 : 8; }
+int64_t bwd_blocks(int64_t rows, int64_t cols) {
+  const int64_t block_rows = static_cast<int64_t>(kNormBwdRows) * bwd_waves(nch_of(cols));
+  return (rows + block_rows - 1) / block_rows;
+}
 
 template <typename IO>
 __device__ __forceinline__ void load8(const void* base, int64_t index, float (&o)[8]) {
@@ -82,13 +90,18 @@ rms_norm_fwd_kernel(int64_t R, int D, const void* x, const void* w, float eps, v
   }
 }
 
-// one wave per kNormBwdRows rows; dw_part [n_blocks, D] fp32
+// kNormBwdRows rows per wave, bwd_waves(NCH) waves per workgroup; the
+// waves' per-column sums of dy xhat are added in LDS in a fixed order (wave 0,
+// 1, 2, ...) into one partial row per workgroup: dw_part [n_blocks, D] fp32
 template <typename IO, int NCH>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(64 * bwd_waves(NCH))
 rms_norm_bwd_kernel(int64_t R, int D, const void* x, const void* w, const float* rstd, const void* dy, void* dx,
                     float* dw_part) {
-  const int lane = threadIdx.x;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kNormBwdRows;
+  constexpr int kNormBwdWaves = bwd_waves(NCH);
+  __shared__ float4 red[kNormBwdWaves - 1][2][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));  // wave-uniform
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * kNormBwdWaves + wave) * kNormBwdRows;
   float wv[NCH][8], acc[NCH][8];
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
@@ -100,7 +113,7 @@ rms_norm_bwd_kernel(int64_t R, int D, const void* x, const void* w, const float*
   const float inv_d = 1.0f / static_cast<float>(D);
   for (int j = 0; j < kNormBwdRows; ++j) {
     const int64_t row = r0 + j;
-    if (row >= R) break;  // wave-uniform
+    if (row >= R) break;  // wave-uniform; every wave still reaches the barriers below
     const int64_t base = row * D;
     const float r = rstd[row];
     float xh[NCH][8], g[NCH][8];
@@ -138,11 +151,25 @@ rms_norm_bwd_kernel(int64_t R, int D, const void* x, const void* w, const float*
   float* out = dw_part + static_cast<int64_t>(blockIdx.x) * D;
 #pragma unroll
   for (int k = 0; k < NCH; ++k) {
-    const int c = (k * 64 + lane) * 8;
-    if (c < D) {
-      *reinterpret_cast<float4*>(out + c) = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
-      *reinterpret_cast<float4*>(out + c + 4) = make_float4(acc[k][4], acc[k][5], acc[k][6], acc[k][7]);
+    if (wave > 0) {
+      red[wave - 1][0][lane] = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+      red[wave - 1][1][lane] = make_float4(acc[k][4], acc[k][5], acc[k][6], acc[k][7]);
     }
+    __syncthreads();
+    const int c = (k * 64 + lane) * 8;
+    if (wave == 0 && c < D) {
+      float t[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) t[i] = acc[k][i];
+      for (int v = 0; v < kNormBwdWaves - 1; ++v) {
+        const float4 a = red[v][0][lane], b = red[v][1][lane];
+        t[0] += a.x; t[1] += a.y; t[2] += a.z; t[3] += a.w;
+        t[4] += b.x; t[5] += b.y; t[6] += b.z; t[7] += b.w;
+      }
+      *reinterpret_cast<float4*>(out + c) = make_float4(t[0], t[1], t[2], t[3]);
+      *reinterpret_cast<float4*>(out + c + 4) = make_float4(t[4], t[5], t[6], t[7]);
+    }
+    __syncthreads();
   }
 }
 
@@ -163,8 +190,8 @@ void launch_fwd(hipStream_t st, int64_t R, int D, const void* x, const void* w, 
 template <typename IO>
 void launch_bwd(hipStream_t st, int64_t R, int D, const void* x, const void* w, const float* rstd, const void* dy,
                 void* dx, float* part) {
-  const dim3 g(static_cast<unsigned>((R + kNormBwdRows - 1) / kNormBwdRows)), b(64);
-  const int nch = (D + 511) / 512;
+  const int nch = nch_of(D);
+  const dim3 g(static_cast<unsigned>(bwd_blocks(R, D))), b(64 * bwd_waves(nch));
   if (nch <= 1) hipLaunchKernelGGL((rms_norm_bwd_kernel<IO, 1>), g, b, 0, st, R, D, x, w, rstd, dy, dx, part);
   else if (nch <= 2) hipLaunchKernelGGL((rms_norm_bwd_kernel<IO, 2>), g, b, 0, st, R, D, x, w, rstd, dy, dx, part);
   else if (nch <= 4) hipLaunchKernelGGL((rms_norm_bwd_kernel<IO, 4>), g, b, 0, st, R, D, x, w, rstd, dy, dx, part);
@@ -219,7 +246,7 @@ sparc_status sparc_rms_norm_forward(int64_t rows, int64_t cols, int32_t io_dtype
 size_t sparc_rms_norm_workspace_bytes(int64_t rows, int64_t cols) {
   using namespace sparc;
   if (rows < 0 || rows > INT32_MAX || cols <= 0 || cols % 8 || cols > kNormMaxCols) return 0;
-  const int64_t blocks = (rows + kNormBwdRows - 1) / kNormBwdRows;
+  const int64_t blocks = bwd_blocks(rows, cols);
   return static_cast<size_t>(blocks) * static_cast<size_t>(cols) * sizeof(float) + 256;
 }
 
@@ -253,8 +280,7 @@ sparc_status sparc_rms_norm_backward(int64_t rows, int64_t cols, int32_t io_dtyp
     snprintf(error_buffer(), 512, "rms norm backward: %s", hipGetErrorString(e));
     return SPARC_EHIP;
   }
-  const int64_t blocks = (rows + kNormBwdRows - 1) / kNormBwdRows;
-  return sparc_column_sum(blocks, cols, part, dweight, 0, stream);
+  return sparc_column_sum(bwd_blocks(rows, cols), cols, part, dweight, 0, stream);
 }
 
 }  // extern "C"

@@ -173,11 +173,11 @@ def test_controls_entry_points_validate_on_host():
 def test_rms_norm_entry_points_validate_on_host():
     """sparc_rms_norm_*: cols a positive multiple of 8 up to 4096, a known
     I/O type, non-NULL pointers, a large enough workspace (one fp32 partial
-    row of dweight per 8 rows)."""
+    row of dweight per 128 rows at these widths)."""
     lib = _lib.load()
     assert lib.sparc_rms_norm_workspace_bytes(-1, 768) == 0
     assert lib.sparc_rms_norm_workspace_bytes(10, 12) == 0
-    assert lib.sparc_rms_norm_workspace_bytes(1000, 768) == 125 * 768 * 4 + 256
+    assert lib.sparc_rms_norm_workspace_bytes(1000, 768) == 8 * 768 * 4 + 256
     eps = ctypes.c_float(1e-6)
     assert lib.sparc_rms_norm_forward(4, 12, 0, None, None, eps, None, None, None) == 1
     assert b"multiple of 8" in lib.sparc_last_error()
