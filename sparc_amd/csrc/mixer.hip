@@ -2023,9 +2023,12 @@ void run_fwd(const Args& a, hipStream_t st) {
 // M=16384: 1.43 -> 1.39 ms); with the transitions' hardware sine and cosine
 // and the transition gradients taken from conj(a) lambda it streams at its
 // access pattern's rate (the same time with the arithmetic stubbed out), and
-// 8-step blocks at two waves per SIMD are 2 % faster (1.29 -> 1.26 ms).
+// 8-step blocks at two waves per SIMD are 2 % faster (1.29 -> 1.26 ms); with
+// the later cuts 4-step blocks are faster again (1.29-1.31 -> 1.24-1.26 ms;
+// 2 steps 1.58-1.62, 16 steps 1.31-1.33).  With time segments the P1
+// backward keeps 8-step blocks (4 measured the same).
 #ifndef SPARC_MIXER_BWD_P1_S
-#define SPARC_MIXER_BWD_P1_S 8
+#define SPARC_MIXER_BWD_P1_S 4
 #endif
 #ifndef SPARC_MIXER_BWD_S
 #define SPARC_MIXER_BWD_S 4
