@@ -504,6 +504,27 @@ sparc_status sparc_controls_backward(int64_t rows, int64_t width, int32_t io_dty
                                      float* dphase_direction, float* dradial_direction, void* workspace,
                                      size_t workspace_bytes, sparc_stream_t stream);
 
+/* ---- the controls folded into an input projection ------------------------
+ * weight [width, dim] (io_dtype, 16-byte aligned, dim a positive multiple of
+ * 8 up to 4096) is the projection W with x = x_n W^T; the directions [width
+ * + 1] fp32 (bias last).  sparc_controls_fold writes the folded directions
+ * [dim + 1] fp32: folded[d] = sum_w direction[w] W[w, d], folded[dim] =
+ * direction[width], the sums in a fixed order, so that sparc_controls_forward
+ * over x_n with them gives the controls of x.  sparc_controls_fold_backward
+ * maps the gradients of the folded directions [dim + 1] back:
+ * ddirection[w] = sum_d dfolded[d] W[w, d], ddirection[width] =
+ * dfolded[dim].  No counterpart in the reference, which ships the layer, not
+ * a network: the 12-layer stack that runs the layer in its training
+ * configuration folds its controls this way. */
+size_t sparc_controls_fold_workspace_bytes(int64_t width, int64_t dim);
+sparc_status sparc_controls_fold(int64_t width, int64_t dim, int32_t io_dtype, const void* weight,
+                                 const float* phase_direction, const float* radial_direction, float* folded_phase,
+                                 float* folded_radial, void* workspace, size_t workspace_bytes,
+                                 sparc_stream_t stream);
+sparc_status sparc_controls_fold_backward(int64_t width, int64_t dim, int32_t io_dtype, const void* weight,
+                                          const float* dfolded_phase, const float* dfolded_radial,
+                                          float* dphase_direction, float* dradial_direction, sparc_stream_t stream);
+
 /* ---- RMSNorm (the block stack's pre-norm and final norm) -----------------
  * x, y [rows, cols] and weight [cols] in io_dtype (cols a positive multiple
  * of 8 up to 4096; x, y and weight 16-byte aligned); rstd [rows] fp32.

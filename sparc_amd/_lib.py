@@ -53,6 +53,9 @@ EXPORTED_SYMBOLS = (
     "sparc_controls_forward",
     "sparc_controls_workspace_bytes",
     "sparc_controls_backward",
+    "sparc_controls_fold_workspace_bytes",
+    "sparc_controls_fold",
+    "sparc_controls_fold_backward",
     "sparc_rms_norm_forward",
     "sparc_rms_norm_workspace_bytes",
     "sparc_rms_norm_backward",
@@ -149,6 +152,12 @@ def load() -> ctypes.CDLL:
         lib.sparc_controls_workspace_bytes.restype = _SZ
         lib.sparc_controls_backward.argtypes = [_I64, _I64, _I32] + [_P] * 11 + [_SZ, _P]
         lib.sparc_controls_backward.restype = ctypes.c_int
+        lib.sparc_controls_fold_workspace_bytes.argtypes = [_I64, _I64]
+        lib.sparc_controls_fold_workspace_bytes.restype = _SZ
+        lib.sparc_controls_fold.argtypes = [_I64, _I64, _I32] + [_P] * 6 + [_SZ, _P]
+        lib.sparc_controls_fold.restype = ctypes.c_int
+        lib.sparc_controls_fold_backward.argtypes = [_I64, _I64, _I32] + [_P] * 5 + [_P]
+        lib.sparc_controls_fold_backward.restype = ctypes.c_int
         lib.sparc_rms_norm_forward.argtypes = [_I64, _I64, _I32, _P, _P, ctypes.c_float, _P, _P, _P]
         lib.sparc_rms_norm_forward.restype = ctypes.c_int
         lib.sparc_rms_norm_workspace_bytes.argtypes = [_I64, _I64]

@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_NAME = "libsparc_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["scan.hip", "pointwise.hip", "mixer.hip", "norm.hip"]
+SOURCES = ["scan.hip", "pointwise.hip", "mixer.hip", "norm.hip", "fold.hip"]
 # scan.hip compiles as SCAN_PARTS translation units (SPARC_SCAN_PART = 0..11:
 # the C ABI, then one per (transition, I/O dtype) launcher), in parallel
 SCAN_PARTS = 12

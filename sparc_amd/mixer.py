@@ -174,6 +174,9 @@ def fused_sequence(module, x: torch.Tensor):
 # ---------------------------------------------------------------------------
 # the mixer behind its input projection, with the controls folded into it
 # ---------------------------------------------------------------------------
+_FOLD_MAX_DIM = 4096  # sparc_controls_fold's widest model dimension
+
+
 class _ProjectedMixer(torch.autograd.Function):
     """y = SPARCMixer(xn @ W^T) for xn [B, L, D] and the projection W [2M, D].
 
@@ -203,8 +206,15 @@ class _ProjectedMixer(torch.autograd.Function):
         # the folded directions [W^T u_phase, b_phase], [W^T u_radial, b_radial]
         # in rows of a 16-byte multiple (each row a 16-byte aligned vector)
         v = torch.zeros(2, (D + 4) // 4 * 4, dtype=torch.float32, device=dev)
-        torch.mm(dirs[:, :W], weight.detach().float(), out=v[:, :D])
-        v[:, D] = dirs[:, W]
+        wc = aligned16(weight.detach())
+        if D <= _FOLD_MAX_DIM:  # sparc_controls_fold: one pass over W, no fp32 copy of it
+            fws = torch.empty(lib.sparc_controls_fold_workspace_bytes(W, D), dtype=torch.uint8, device=dev)
+            _lib.check(lib.sparc_controls_fold(W, D, _lib.io_code(wc.dtype), _lib.ptr(wc), _lib.ptr(dirs[0]),
+                                               _lib.ptr(dirs[1]), _lib.ptr(v[0]), _lib.ptr(v[1]), _lib.ptr(fws),
+                                               fws.numel(), _lib.stream_of(dev)), "sparc_controls_fold")
+        else:
+            torch.mm(dirs[:, :W], wc.float(), out=v[:, :D])
+            v[:, D] = dirs[:, W]
         xn2 = aligned16(xn.detach().reshape(-1, D))
         eta = torch.empty(B * T, dtype=torch.float32, device=dev)
         delta = torch.empty_like(eta)
@@ -269,7 +279,14 @@ class _ProjectedMixer(torch.autograd.Function):
             P(g_xn), P(dv[0]), P(dv[1]), P(cws), cws.numel(), _lib.stream_of(dev)), "sparc_controls_backward")
         dpx = dv[:, :D]                                                                # [2, D]
         g_w = dx2.t() @ xn2 + (dirs[:, :W].t() @ dpx).to(weight.dtype)
-        g_dirs = torch.cat((dpx @ weight.float().t(), dv[:, D:D + 1]), dim=1)          # [2, 2M + 1]
+        if D <= _FOLD_MAX_DIM:  # the folded directions' gradients back through W
+            g_dirs = torch.empty(2, W + 1, dtype=torch.float32, device=dev)
+            wc = aligned16(weight)
+            _lib.check(lib.sparc_controls_fold_backward(W, D, _lib.io_code(wc.dtype), P(wc), P(dv[0]), P(dv[1]),
+                                                        P(g_dirs[0]), P(g_dirs[1]), _lib.stream_of(dev)),
+                       "sparc_controls_fold_backward")
+        else:
+            g_dirs = torch.cat((dpx @ weight.float().t(), dv[:, D:D + 1]), dim=1)      # [2, 2M + 1]
         g_xn = g_xn.reshape(B, T, D)
         out = [g_dirs[0], g_dirs[1], *grads]
         out = [g.to(dt) for g, dt in zip(out, ctx.dtypes)]

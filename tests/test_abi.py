@@ -191,6 +191,32 @@ def test_rms_norm_entry_points_validate_on_host():
     assert st == 4 and b"workspace" in lib.sparc_last_error()
 
 
+def test_controls_fold_entry_points_validate_on_host():
+    """sparc_controls_fold*: width > 0, dim a positive multiple of 8 up to
+    4096, a known I/O type, non-NULL pointers, a large enough workspace (two
+    fp32 partial rows per 64 rows of W)."""
+    lib = _lib.load()
+    assert lib.sparc_controls_fold_workspace_bytes(0, 768) == 0
+    assert lib.sparc_controls_fold_workspace_bytes(64, 12) == 0
+    assert lib.sparc_controls_fold_workspace_bytes(64, 8192) == 0
+    assert lib.sparc_controls_fold_workspace_bytes(24576, 768) == 2 * 384 * 768 * 4 + 256
+    assert lib.sparc_controls_fold_workspace_bytes(65, 8) == 2 * 2 * 8 * 4 + 256
+    assert lib.sparc_controls_fold(64, 12, 0, *([None] * 6), 0, None) == 1
+    assert b"multiple of 8" in lib.sparc_last_error()
+    assert lib.sparc_controls_fold(64, 16, 7, *([None] * 6), 0, None) == 1
+    assert b"io_dtype" in lib.sparc_last_error()
+    assert lib.sparc_controls_fold(64, 16, 0, *([None] * 6), 0, None) == 1
+    assert b"NULL" in lib.sparc_last_error()
+    fake = ctypes.c_void_p(256)  # never dereferenced: the size check fails first
+    assert lib.sparc_controls_fold(64, 16, 0, *([fake] * 6), 16, None) == 4
+    assert b"workspace" in lib.sparc_last_error()
+    assert lib.sparc_controls_fold_backward(0, 16, 0, *([fake] * 5), None) == 1
+    assert lib.sparc_controls_fold_backward(64, 16, 0, None, *([fake] * 4), None) == 1
+    assert b"NULL" in lib.sparc_last_error()
+    assert lib.sparc_controls_fold_backward(64, 16, 0, ctypes.c_void_p(258), *([fake] * 4), None) == 1
+    assert b"aligned" in lib.sparc_last_error()
+
+
 def _raw_inputs(transition="p1", B=2, T=5, M=8, G=2, io=torch.float32):
     g = torch.float32 if transition == "p1" else io
     d = dict(g0=torch.zeros(B, T, G, dtype=g), g1=torch.zeros(B, T, G, dtype=g),

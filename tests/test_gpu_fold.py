@@ -1,0 +1,116 @@
+"""The library's controls fold (sparc_controls_fold / _backward: the
+controls' directions folded through the block stack's input projection)
+against float64 products, and the stack's projected mixer with and without
+it."""
+import pytest
+import torch
+
+from sparc_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(8, 8), (64, 16), (65, 24), (200, 520), (1536, 768), (24576, 768), (96, 4096)]
+
+
+def _case(width, dim, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(width, dim, generator=g, dtype=torch.float64) / dim ** 0.5).to(dtype)
+    u = torch.randn(2, width + 1, generator=g, dtype=torch.float64).float()
+    gf = torch.randn(2, dim + 1, generator=g, dtype=torch.float64).float()
+    return w, u, gf
+
+
+def _fold(w, u):
+    lib = _lib.load()
+    width, dim = w.shape
+    wc, uc = w.cuda(), u.cuda()
+    f = torch.full((2, dim + 1), float("nan"), device="cuda")
+    fpad = torch.full((2, (dim + 4) // 4 * 4), float("nan"), device="cuda")
+    ws = torch.empty(lib.sparc_controls_fold_workspace_bytes(width, dim), dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    P = _lib.ptr
+    _lib.check(lib.sparc_controls_fold(width, dim, _lib.io_code(w.dtype), P(wc), P(uc[0]), P(uc[1]), P(fpad[0]),
+                                       P(fpad[1]), P(ws), ws.numel(), st), "sparc_controls_fold")
+    f.copy_(fpad[:, :dim + 1])
+    return f.cpu()
+
+
+def _unfold(w, gf):
+    lib = _lib.load()
+    width, dim = w.shape
+    wc, gc = w.cuda(), gf.cuda()
+    du = torch.full((2, width + 1), float("nan"), device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    P = _lib.ptr
+    _lib.check(lib.sparc_controls_fold_backward(width, dim, _lib.io_code(w.dtype), P(wc), P(gc[0]), P(gc[1]),
+                                                P(du[0]), P(du[1]), st), "sparc_controls_fold_backward")
+    return du.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"{w}x{d}" for w, d in SHAPES])
+def test_fold_against_float64(shape, dtype):
+    print(f"[case] controls fold {shape} {dtype}", flush=True)
+    width, dim = shape
+    w, u, gf = _case(width, dim, dtype, seed=width * 7 + dim)
+    wd = w.double()
+    # forward: f_k = [u_k[:width] W, u_k[width]]
+    ref = torch.cat((u[:, :width].double() @ wd, u[:, width:].double()), dim=1)
+    got = _fold(w, u).double()
+    # fp32 sums of `width` products: error bound ~ width * 2^-24 * sum |u_w W_wd|
+    bound = (u[:, :width].double().abs() @ wd.abs()) * (width * 2.0 ** -23) + 1e-30
+    err = (got[:, :dim] - ref[:, :dim]).abs()
+    assert bool((err <= bound).all()), f"max err {err.max().item()} vs bound {bound.max().item()}"
+    assert torch.equal(got[:, dim], ref[:, dim])  # the bias passes through
+    # backward: du_k = [W g_k[:dim], g_k[dim]]
+    refb = torch.cat((gf[:, :dim].double() @ wd.t(), gf[:, dim:].double()), dim=1)
+    gotb = _unfold(w, gf).double()
+    boundb = (gf[:, :dim].double().abs() @ wd.abs().t()) * (dim * 2.0 ** -23) + 1e-30
+    errb = (gotb[:, :width] - refb[:, :width]).abs()
+    assert bool((errb <= boundb).all()), f"max err {errb.max().item()} vs bound {boundb.max().item()}"
+    assert torch.equal(gotb[:, width], refb[:, width])
+
+
+def test_fold_deterministic():
+    """The same bits on repeated calls (fixed-order sums, no atomics)."""
+    print("[case] controls fold determinism", flush=True)
+    w, u, gf = _case(24576, 768, torch.bfloat16, seed=3)
+    a, b = _fold(w, u), _fold(w, u)
+    assert torch.equal(a, b)
+    assert torch.equal(_unfold(w, gf), _unfold(w, gf))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_projected_mixer_fold_matches_torch_products(dtype, monkeypatch):
+    """The stack's projected mixer with the library fold and with torch's
+    fp32 products in its place (the path wider models take): the same
+    outputs and gradients up to fp32 summation order."""
+    print(f"[case] projected mixer fold vs torch products {dtype}", flush=True)
+    from sparc_amd import mixer as mx
+    from sparc_amd.sparc import SPARCMixer
+
+    torch.manual_seed(11)
+    D, M, B, T = 64, 48, 2, 40
+    mod = SPARCMixer(2 * M).cuda()
+    with torch.no_grad():
+        for p in (mod.phase_direction, mod.radial_direction):
+            p.normal_(0.0, 0.3)
+    w = (torch.randn(2 * M, D, device="cuda") / D ** 0.5).to(dtype).requires_grad_()
+    xn = torch.randn(B, T, D, device="cuda").to(dtype).requires_grad_()
+    dy = torch.randn(B, T, 2 * M, device="cuda").to(dtype)
+
+    def run():
+        for t in (w, xn, mod.phase_direction, mod.radial_direction):
+            t.grad = None
+        y, (lr, li) = mx.projected_sequence(mod, xn, w)
+        (y.float() * dy.float()).sum().add_(lr.sum() + li.sum()).backward()
+        return [y.detach().float().clone()] + [t.grad.detach().float().clone() for t in (
+            w, xn, mod.phase_direction, mod.radial_direction)]
+
+    a = run()
+    monkeypatch.setattr(mx, "_FOLD_MAX_DIM", 0)
+    b = run()
+    tol = dict(rtol=1e-4, atol=1e-4) if dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
+    for name, x, y in zip(("y", "dW", "dxn", "dphase", "dradial"), a, b):
+        scale = y.abs().max().item() + 1e-6
+        torch.testing.assert_close(x / scale, y / scale, **tol, msg=lambda m: f"{name}: {m}")
