@@ -513,17 +513,23 @@ sparc_status sparc_controls_backward(int64_t rows, int64_t width, int32_t io_dty
  * over x_n with them gives the controls of x.  sparc_controls_fold_backward
  * maps the gradients of the folded directions [dim + 1] back:
  * ddirection[w] = sum_d dfolded[d] W[w, d], ddirection[width] =
- * dfolded[dim].  No counterpart in the reference, which ships the layer, not
- * a network: the 12-layer stack that runs the layer in its training
- * configuration folds its controls this way. */
+ * dfolded[dim]; with dweight (io_dtype [width, dim], 16-byte aligned; NULL:
+ * skipped) it also adds the folded directions' share of the projection's
+ * gradient in place, dweight[w, d] += phase[w] dfolded_phase[d] +
+ * radial[w] dfolded_radial[d] (fp32, rounded once); the directions may be
+ * NULL without dweight.  No counterpart in the reference, which ships the
+ * layer, not a network: the 12-layer stack that runs the layer in its
+ * training configuration folds its controls this way. */
 size_t sparc_controls_fold_workspace_bytes(int64_t width, int64_t dim);
 sparc_status sparc_controls_fold(int64_t width, int64_t dim, int32_t io_dtype, const void* weight,
                                  const float* phase_direction, const float* radial_direction, float* folded_phase,
                                  float* folded_radial, void* workspace, size_t workspace_bytes,
                                  sparc_stream_t stream);
 sparc_status sparc_controls_fold_backward(int64_t width, int64_t dim, int32_t io_dtype, const void* weight,
+                                          const float* phase_direction, const float* radial_direction,
                                           const float* dfolded_phase, const float* dfolded_radial,
-                                          float* dphase_direction, float* dradial_direction, sparc_stream_t stream);
+                                          float* dphase_direction, float* dradial_direction, void* dweight,
+                                          sparc_stream_t stream);
 
 /* ---- RMSNorm (the block stack's pre-norm and final norm) -----------------
  * x, y [rows, cols] and weight [cols] in io_dtype (cols a positive multiple

@@ -156,7 +156,7 @@ def load() -> ctypes.CDLL:
         lib.sparc_controls_fold_workspace_bytes.restype = _SZ
         lib.sparc_controls_fold.argtypes = [_I64, _I64, _I32] + [_P] * 6 + [_SZ, _P]
         lib.sparc_controls_fold.restype = ctypes.c_int
-        lib.sparc_controls_fold_backward.argtypes = [_I64, _I64, _I32] + [_P] * 5 + [_P]
+        lib.sparc_controls_fold_backward.argtypes = [_I64, _I64, _I32] + [_P] * 8 + [_P]
         lib.sparc_controls_fold_backward.restype = ctypes.c_int
         lib.sparc_rms_norm_forward.argtypes = [_I64, _I64, _I32, _P, _P, ctypes.c_float, _P, _P, _P]
         lib.sparc_rms_norm_forward.restype = ctypes.c_int

@@ -4,13 +4,16 @@
 // over x_n with the folded directions
 //   forward   f_k[d] = sum_w u_k[w] W[w, d]  (d < dim),  f_k[dim] = u_k[width]
 //   backward  du_k[w] = sum_d g_k[d] W[w, d]  (w < width), du_k[width] = g_k[dim]
+//             dW[w, d] += u_0[w] g_0[d] + u_1[w] g_1[d]  (optional, in place)
 // for the phase (k = 0) and radial (k = 1) directions, g the gradients of the
-// folded directions.  W in the I/O type, everything else fp32, fp32
-// arithmetic.  The forward reads W once: one wave per block of rows, the
-// waves' per-column sums added in LDS in wave order into one partial row per
-// workgroup and direction, the partial rows summed in a fixed order
-// (sparc_column_sum); the backward is one wave per row block, two dot
-// products per row.  Replaces torch products over an fp32 copy of W.
+// folded directions.  W and dW in the I/O type, everything else fp32, fp32
+// arithmetic (dW rounded once, after the add).  The forward reads W once: one
+// wave per block of rows, the waves' per-column sums added in LDS in wave
+// order into one partial row per workgroup and direction, the partial rows
+// summed in a fixed order (sparc_column_sum); the backward is one wave per
+// row block, two dot products per row, and the rank-2 update of the same row
+// of dW.  Replaces torch products over an fp32 copy of W, and the fp32
+// rank-2 product, its cast and the add into the projection's gradient.
 
 #include "common.h"
 #include "sparc_hip.h"
@@ -38,6 +41,17 @@ __device__ __forceinline__ void load8w(const void* base, int64_t index, float (&
     unpack<float, 4>(load_raw<float, 4>(base, index + 4), b);
 #pragma unroll
     for (int i = 0; i < 4; ++i) { o[i] = a[i]; o[4 + i] = b[i]; }
+  }
+}
+
+template <typename IO>
+__device__ __forceinline__ void store8w(void* base, int64_t index, const float (&o)[8]) {
+  if constexpr (sizeof(IO) == 2) {
+    store_raw<bf16, 8>(base, index, pack<bf16, 8>(o));
+  } else {
+    const float a[4] = {o[0], o[1], o[2], o[3]}, b[4] = {o[4], o[5], o[6], o[7]};
+    store_raw<float, 4>(base, index, pack<float, 4>(a));
+    store_raw<float, 4>(base, index + 4, pack<float, 4>(b));
   }
 }
 
@@ -110,10 +124,12 @@ fold_fwd_kernel(int64_t width, int dim, const void* wt, const float* u0, const f
   }
 }
 
-// du_k[w] for the rows of this wave; one wave per kFoldRowsPerWave rows
-template <typename IO, int NCH>
+// du_k[w] for the rows of this wave (and with DW, the rank-2 update of the
+// same rows of dwt); one wave per kFoldRowsPerWave rows
+template <typename IO, int NCH, bool DW>
 __global__ void __launch_bounds__(64 * kFoldWaves)
-fold_bwd_kernel(int64_t width, int dim, const void* wt, const float* g0, const float* g1, float* du0, float* du1) {
+fold_bwd_kernel(int64_t width, int dim, const void* wt, const float* u0, const float* u1, const float* g0,
+                const float* g1, float* du0, float* du1, void* dwt) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   if (blockIdx.x == 0 && threadIdx.x == 0) {  // the bias entries pass through
@@ -136,16 +152,23 @@ fold_bwd_kernel(int64_t width, int dim, const void* wt, const float* g0, const f
     const int64_t r = r0 + j;
     if (r >= width) return;  // wave-uniform; no barrier in this kernel
     float s0 = 0.0f, s1 = 0.0f;
+    const float c0 = DW ? u0[r] : 0.0f, c1 = DW ? u1[r] : 0.0f;
 #pragma unroll
     for (int k = 0; k < NCH; ++k) {
       const int c = (k * 64 + lane) * 8;
       if (c < dim) {
-        float w[8];
+        float w[8], d[8];
         load8w<IO>(wt, r * dim + c, w);
+        if constexpr (DW) load8w<IO>(dwt, r * dim + c, d);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           s0 = fmaf(v0[k][i], w[i], s0);
           s1 = fmaf(v1[k][i], w[i], s1);
+        }
+        if constexpr (DW) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) d[i] += fmaf(c0, v0[k][i], c1 * v1[k][i]);
+          store8w<IO>(dwt, r * dim + c, d);
         }
       }
     }
@@ -169,16 +192,19 @@ void launch_fold_fwd(hipStream_t st, int64_t width, int dim, const void* wt, con
     default: hipLaunchKernelGGL((fold_fwd_kernel<IO, 8>), g, b, 0, st, width, dim, wt, u0, u1, part, f0, f1);
   }
 }
-template <typename IO>
-void launch_fold_bwd(hipStream_t st, int64_t width, int dim, const void* wt, const float* g0, const float* g1,
-                     float* du0, float* du1) {
+template <typename IO, bool DW>
+void launch_fold_bwd(hipStream_t st, int64_t width, int dim, const void* wt, const float* u0, const float* u1,
+                     const float* g0, const float* g1, float* du0, float* du1, void* dwt) {
   const dim3 g(static_cast<unsigned>(fold_blocks(width))), b(64 * kFoldWaves);
+#define SPARC_FOLD_BWD(n) \
+  hipLaunchKernelGGL((fold_bwd_kernel<IO, n, DW>), g, b, 0, st, width, dim, wt, u0, u1, g0, g1, du0, du1, dwt)
   switch (fold_nch(dim)) {
-    case 1: hipLaunchKernelGGL((fold_bwd_kernel<IO, 1>), g, b, 0, st, width, dim, wt, g0, g1, du0, du1); break;
-    case 2: hipLaunchKernelGGL((fold_bwd_kernel<IO, 2>), g, b, 0, st, width, dim, wt, g0, g1, du0, du1); break;
-    case 4: hipLaunchKernelGGL((fold_bwd_kernel<IO, 4>), g, b, 0, st, width, dim, wt, g0, g1, du0, du1); break;
-    default: hipLaunchKernelGGL((fold_bwd_kernel<IO, 8>), g, b, 0, st, width, dim, wt, g0, g1, du0, du1);
+    case 1: SPARC_FOLD_BWD(1); break;
+    case 2: SPARC_FOLD_BWD(2); break;
+    case 4: SPARC_FOLD_BWD(4); break;
+    default: SPARC_FOLD_BWD(8);
   }
+#undef SPARC_FOLD_BWD
 }
 
 sparc_status fold_fail(sparc_status s, const char* msg) {
@@ -245,20 +271,28 @@ sparc_status sparc_controls_fold(int64_t width, int64_t dim, int32_t io_dtype, c
 }
 
 sparc_status sparc_controls_fold_backward(int64_t width, int64_t dim, int32_t io_dtype, const void* weight,
+                                          const float* phase_direction, const float* radial_direction,
                                           const float* dfolded_phase, const float* dfolded_radial,
-                                          float* dphase_direction, float* dradial_direction, sparc_stream_t stream) {
+                                          float* dphase_direction, float* dradial_direction, void* dweight,
+                                          sparc_stream_t stream) {
   using namespace sparc;
   if (sparc_status s = check_fold(width, dim, io_dtype)) return s;
-  if (!weight || !dfolded_phase || !dfolded_radial || !dphase_direction || !dradial_direction)
+  if (!weight || !dfolded_phase || !dfolded_radial || !dphase_direction || !dradial_direction ||
+      (dweight && (!phase_direction || !radial_direction)))
     return fold_fail(SPARC_EINVAL, "controls fold backward: NULL pointer");
-  if (!fold_aligned(weight, 16)) return fold_fail(SPARC_EINVAL, "controls fold backward: weight must be 16-byte aligned");
+  if (!fold_aligned(weight, 16) || !fold_aligned(dweight, 16))
+    return fold_fail(SPARC_EINVAL, "controls fold backward: weight and dweight must be 16-byte aligned");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int D = static_cast<int>(dim);
-  if (io_dtype == SPARC_BF16)
-    launch_fold_bwd<sparc::bf16>(st, width, D, weight, dfolded_phase, dfolded_radial, dphase_direction,
-                                 dradial_direction);
-  else
-    launch_fold_bwd<float>(st, width, D, weight, dfolded_phase, dfolded_radial, dphase_direction, dradial_direction);
+  const float *u0 = phase_direction, *u1 = radial_direction, *g0 = dfolded_phase, *g1 = dfolded_radial;
+  float *du0 = dphase_direction, *du1 = dradial_direction;
+  if (io_dtype == SPARC_BF16) {
+    if (dweight) launch_fold_bwd<sparc::bf16, true>(st, width, D, weight, u0, u1, g0, g1, du0, du1, dweight);
+    else launch_fold_bwd<sparc::bf16, false>(st, width, D, weight, u0, u1, g0, g1, du0, du1, dweight);
+  } else {
+    if (dweight) launch_fold_bwd<float, true>(st, width, D, weight, u0, u1, g0, g1, du0, du1, dweight);
+    else launch_fold_bwd<float, false>(st, width, D, weight, u0, u1, g0, g1, du0, du1, dweight);
+  }
   return fold_hip_status("controls fold backward");
 }
 

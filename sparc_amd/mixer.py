@@ -278,14 +278,17 @@ class _ProjectedMixer(torch.autograd.Function):
             B * T, D, _lib.io_code(x.dtype), P(xn2), P(v[0]), P(v[1]), P(eta), P(delta), P(deta), P(ddelta),
             P(g_xn), P(dv[0]), P(dv[1]), P(cws), cws.numel(), _lib.stream_of(dev)), "sparc_controls_backward")
         dpx = dv[:, :D]                                                                # [2, D]
-        g_w = dx2.t() @ xn2 + (dirs[:, :W].t() @ dpx).to(weight.dtype)
-        if D <= _FOLD_MAX_DIM:  # the folded directions' gradients back through W
+        if D <= _FOLD_MAX_DIM:
+            # the folded directions' gradients back through W, and their rank-2
+            # share u^T dpx of dW added in place
+            g_w = aligned16(dx2.t() @ xn2)
             g_dirs = torch.empty(2, W + 1, dtype=torch.float32, device=dev)
             wc = aligned16(weight)
-            _lib.check(lib.sparc_controls_fold_backward(W, D, _lib.io_code(wc.dtype), P(wc), P(dv[0]), P(dv[1]),
-                                                        P(g_dirs[0]), P(g_dirs[1]), _lib.stream_of(dev)),
-                       "sparc_controls_fold_backward")
+            _lib.check(lib.sparc_controls_fold_backward(W, D, _lib.io_code(wc.dtype), P(wc), P(dirs[0]), P(dirs[1]),
+                                                        P(dv[0]), P(dv[1]), P(g_dirs[0]), P(g_dirs[1]), P(g_w),
+                                                        _lib.stream_of(dev)), "sparc_controls_fold_backward")
         else:
+            g_w = dx2.t() @ xn2 + (dirs[:, :W].t() @ dpx).to(weight.dtype)
             g_dirs = torch.cat((dpx @ weight.float().t(), dv[:, D:D + 1]), dim=1)      # [2, 2M + 1]
         g_xn = g_xn.reshape(B, T, D)
         out = [g_dirs[0], g_dirs[1], *grads]

@@ -210,10 +210,15 @@ def test_controls_fold_entry_points_validate_on_host():
     fake = ctypes.c_void_p(256)  # never dereferenced: the size check fails first
     assert lib.sparc_controls_fold(64, 16, 0, *([fake] * 6), 16, None) == 4
     assert b"workspace" in lib.sparc_last_error()
-    assert lib.sparc_controls_fold_backward(0, 16, 0, *([fake] * 5), None) == 1
-    assert lib.sparc_controls_fold_backward(64, 16, 0, None, *([fake] * 4), None) == 1
+    assert lib.sparc_controls_fold_backward(0, 16, 0, *([fake] * 8), None) == 1
+    assert lib.sparc_controls_fold_backward(64, 16, 0, None, *([fake] * 7), None) == 1
     assert b"NULL" in lib.sparc_last_error()
-    assert lib.sparc_controls_fold_backward(64, 16, 0, ctypes.c_void_p(258), *([fake] * 4), None) == 1
+    # dweight needs the directions
+    assert lib.sparc_controls_fold_backward(64, 16, 0, fake, None, None, *([fake] * 5), None) == 1
+    assert b"NULL" in lib.sparc_last_error()
+    assert lib.sparc_controls_fold_backward(64, 16, 0, ctypes.c_void_p(258), *([fake] * 7), None) == 1
+    assert b"aligned" in lib.sparc_last_error()
+    assert lib.sparc_controls_fold_backward(64, 16, 0, fake, *([fake] * 6), ctypes.c_void_p(264), None) == 1
     assert b"aligned" in lib.sparc_last_error()
 
 

@@ -35,16 +35,21 @@ def _fold(w, u):
     return f.cpu()
 
 
-def _unfold(w, gf):
+def _unfold(w, gf, u=None, dw=None):
+    """(ddirections, dweight after the in-place add, or None)"""
     lib = _lib.load()
     width, dim = w.shape
     wc, gc = w.cuda(), gf.cuda()
+    uc = u.cuda() if u is not None else None
+    dwc = dw.cuda() if dw is not None else None
     du = torch.full((2, width + 1), float("nan"), device="cuda")
     st = torch.cuda.current_stream().cuda_stream
     P = _lib.ptr
-    _lib.check(lib.sparc_controls_fold_backward(width, dim, _lib.io_code(w.dtype), P(wc), P(gc[0]), P(gc[1]),
-                                                P(du[0]), P(du[1]), st), "sparc_controls_fold_backward")
-    return du.cpu()
+    _lib.check(lib.sparc_controls_fold_backward(width, dim, _lib.io_code(w.dtype), P(wc),
+                                                P(uc[0]) if uc is not None else None,
+                                                P(uc[1]) if uc is not None else None, P(gc[0]), P(gc[1]),
+                                                P(du[0]), P(du[1]), P(dwc), st), "sparc_controls_fold_backward")
+    return du.cpu(), (dwc.cpu() if dwc is not None else None)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
@@ -64,11 +69,22 @@ def test_fold_against_float64(shape, dtype):
     assert torch.equal(got[:, dim], ref[:, dim])  # the bias passes through
     # backward: du_k = [W g_k[:dim], g_k[dim]]
     refb = torch.cat((gf[:, :dim].double() @ wd.t(), gf[:, dim:].double()), dim=1)
-    gotb = _unfold(w, gf).double()
-    boundb = (gf[:, :dim].double().abs() @ wd.abs().t()) * (dim * 2.0 ** -23) + 1e-30
-    errb = (gotb[:, :width] - refb[:, :width]).abs()
-    assert bool((errb <= boundb).all()), f"max err {errb.max().item()} vs bound {boundb.max().item()}"
-    assert torch.equal(gotb[:, width], refb[:, width])
+    for with_dw in (False, True):
+        dw0 = (torch.randn(width, dim, generator=torch.Generator().manual_seed(width + dim)) * 0.3).to(dtype)
+        gotb, dw = _unfold(w, gf, u if with_dw else None, dw0 if with_dw else None)
+        gotb = gotb.double()
+        boundb = (gf[:, :dim].double().abs() @ wd.abs().t()) * (dim * 2.0 ** -23) + 1e-30
+        errb = (gotb[:, :width] - refb[:, :width]).abs()
+        assert bool((errb <= boundb).all()), f"max err {errb.max().item()} vs bound {boundb.max().item()}"
+        assert torch.equal(gotb[:, width], refb[:, width])
+        if with_dw:
+            # dW + u^T g: three fp32 roundings (a product, an fma, the add; 2^-24
+            # of the sum's magnitude each), then one to the I/O type (bf16: 2^-9)
+            refw = dw0.double() + u[:, :width].double().t() @ gf[:, :dim].double()
+            mag = dw0.double().abs() + u[:, :width].double().abs().t() @ gf[:, :dim].double().abs()
+            ulp = 2.0 ** -21 if dtype == torch.float32 else 2.0 ** -8
+            errw = (dw.double() - refw).abs()
+            assert bool((errw <= mag * ulp + 1e-30).all()), f"dW max err {errw.max().item()}"
 
 
 def test_fold_deterministic():
@@ -77,7 +93,7 @@ def test_fold_deterministic():
     w, u, gf = _case(24576, 768, torch.bfloat16, seed=3)
     a, b = _fold(w, u), _fold(w, u)
     assert torch.equal(a, b)
-    assert torch.equal(_unfold(w, gf), _unfold(w, gf))
+    assert torch.equal(_unfold(w, gf)[0], _unfold(w, gf)[0])
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
