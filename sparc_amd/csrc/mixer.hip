@@ -1475,19 +1475,23 @@ mixer_bwd_kernel(Args a) {
           const float tr = tanh_fast(cxr[v]), ti = tanh_fast(cxi[v]);
           float w_r = l_r, w_i = l_i;  // the write's gradient
           if constexpr (kRoundWrite<IO>) round_bf16x2(w_r, w_i);
-          dxr[s][v] = w_r * gain * fmaf(-tr, tr, 1.0f);
-          dxi[s][v] = w_i * gain * fmaf(-ti, ti, 1.0f);
-          const float g = fmaf(w_r, tr, w_i * ti) * gain;
+          const float wgr = w_r * gain, wgi = w_i * gain;
+          dxr[s][v] = wgr * fmaf(-tr, tr, 1.0f);
+          dxi[s][v] = wgi * fmaf(-ti, ti, 1.0f);
+          const float g = fmaf(wgr, tr, wgi * ti);
           // radial + g wterm = E nu (tt - g rho^2 / e2) with rho^2 / e2 = 1 + g2 r^2
-          const float u = mc.nu[v] * fmaf(-g, fmaf(mc.g2[v], r * r, 1.0f), tt);
+          // (nu E is the transition's own product)
+          const float ue = (mc.nu[v] * E) * fmaf(-g, fmaf(mc.g2[v], r * r, 1.0f), tt);
           const float gs = g * (1.0f - sg);
-          se = fmaf(E, u, fmaf(gs, mc.wrr_s[v], se));
+          se = fmaf(gs, mc.wrr_s[v], se + ue);
           sd = fmaf(-em, zi, fmaf(gs, mc.wpr_s[v], sd));
-          acc[0][v] = fmaf(E, u, fmaf(-g, mc.kappa[v], acc[0][v]));
+          // constant factors applied once after the sums: d nu_log's
+          // -kappa sum g, d wpr's 2/pi, d wrr's 1/log16
+          acc[0][v] += ue;
           acc[1][v] += zi;
           acc[2][v] += g;
-          acc[3][v] = fmaf(gs, delta * kTwoOverPi, acc[3][v]);
-          acc[4][v] = fmaf(gs, Hs[s] * kInvLog16, acc[4][v]);
+          acc[3][v] = fmaf(gs, delta, acc[3][v]);
+          acc[4][v] = fmaf(gs, Hs[s], acc[4][v]);
         }
       }
       if constexpr (GW) {
@@ -1631,7 +1635,14 @@ mixer_bwd_kernel(Args a) {
     const int64_t rows = static_cast<int64_t>(a.B) * a.n_seg, row = static_cast<int64_t>(b) * a.n_seg + cp.seg;
     constexpr int NP = GW ? 2 : 5;  // GW: nu_log and theta_log only
 #pragma unroll
-    for (int v = 0; v < V; ++v) acc[1][v] *= mc.th[v];  // d theta_log = theta sum dphi
+    for (int v = 0; v < V; ++v) {
+      acc[1][v] *= mc.th[v];  // d theta_log = theta sum dphi
+      if constexpr (!GW) {    // the module's constant factors (run_block)
+        acc[0][v] = fmaf(-mc.kappa[v], acc[2][v], acc[0][v]);
+        acc[3][v] *= kTwoOverPi;
+        acc[4][v] *= kInvLog16;
+      }
+    }
 #pragma unroll
     for (int p = 0; p < NP; ++p)
 #pragma unroll
