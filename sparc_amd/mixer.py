@@ -202,7 +202,17 @@ class _ProjectedMixer(torch.autograd.Function):
         dev = _lib.require_gpu(xn, weight, phase_direction)
         M = W // 2
         x = torch.nn.functional.linear(xn, weight).contiguous()  # [B, T, 2M] in the activation dtype
-        dirs = torch.stack((phase_direction, radial_direction)).detach().float()  # [2, 2M + 1]
+        # the directions and the per-mode parameters in one fp32 buffer (one
+        # copy and at most one cast, not one per tensor): dirs [2, 2M + 1]
+        # (phase, radial), then five [M] views
+        ps = (phase_direction, radial_direction, nu_log, theta_log, write_log_gain, write_phase_response,
+              write_radial_response)
+        if all(p.dtype == ps[0].dtype for p in ps):
+            flat = torch.cat([p.detach().reshape(-1) for p in ps]).float()
+        else:
+            flat = torch.cat([p.detach().reshape(-1).float() for p in ps])
+        dirs = flat[:2 * (W + 1)].view(2, W + 1)
+        params = list(flat[2 * (W + 1):].split(M))
         # the folded directions [W^T u_phase, b_phase], [W^T u_radial, b_radial]
         # in rows of a 16-byte multiple (each row a 16-byte aligned vector)
         v = torch.zeros(2, (D + 4) // 4 * 4, dtype=torch.float32, device=dev)
@@ -221,8 +231,6 @@ class _ProjectedMixer(torch.autograd.Function):
         P = _lib.ptr
         _lib.check(lib.sparc_controls_forward(B * T, D, _lib.io_code(xn.dtype), P(xn2), P(v[0]), P(v[1]), P(eta),
                                               P(delta), _lib.stream_of(dev)), "sparc_controls_forward")
-        params = [t.detach().float().contiguous() for t in (
-            nu_log, theta_log, write_log_gain, write_phase_response, write_radial_response)]
         io = _lib.io_code(x.dtype)
         y = torch.empty_like(x)
         h_re = torch.empty(B, T, M, dtype=x.dtype, device=dev)
@@ -260,7 +268,11 @@ class _ProjectedMixer(torch.autograd.Function):
         dx = torch.empty_like(x)
         deta = torch.empty(B * T, dtype=torch.float32, device=dev)
         ddelta = torch.empty_like(deta)
-        grads = [torch.empty(M, dtype=torch.float32, device=dev) for _ in range(5)]
+        # every parameter gradient in one fp32 buffer, laid out as in forward
+        # (cast back in one kernel below)
+        gflat = torch.empty(2 * (W + 1) + 5 * M, dtype=torch.float32, device=dev)
+        g_dirs = gflat[:2 * (W + 1)].view(2, W + 1)
+        grads = list(gflat[2 * (W + 1):].split(M))
         ws = torch.empty(lib.sparc_mixer_workspace_bytes(B, T, M, 1), dtype=torch.uint8, device=dev)
         P = _lib.ptr
         _lib.check(lib.sparc_mixer_scan_backward(
@@ -282,17 +294,20 @@ class _ProjectedMixer(torch.autograd.Function):
             # the folded directions' gradients back through W, and their rank-2
             # share u^T dpx of dW added in place
             g_w = aligned16(dx2.t() @ xn2)
-            g_dirs = torch.empty(2, W + 1, dtype=torch.float32, device=dev)
             wc = aligned16(weight)
             _lib.check(lib.sparc_controls_fold_backward(W, D, _lib.io_code(wc.dtype), P(wc), P(dirs[0]), P(dirs[1]),
                                                         P(dv[0]), P(dv[1]), P(g_dirs[0]), P(g_dirs[1]), P(g_w),
                                                         _lib.stream_of(dev)), "sparc_controls_fold_backward")
         else:
             g_w = dx2.t() @ xn2 + (dirs[:, :W].t() @ dpx).to(weight.dtype)
-            g_dirs = torch.cat((dpx @ weight.float().t(), dv[:, D:D + 1]), dim=1)      # [2, 2M + 1]
+            g_dirs[:, :W] = dpx @ weight.float().t()                                    # [2, 2M + 1]
+            g_dirs[:, W] = dv[:, D]
         g_xn = g_xn.reshape(B, T, D)
-        out = [g_dirs[0], g_dirs[1], *grads]
-        out = [g.to(dt) for g, dt in zip(out, ctx.dtypes)]
+        if all(dt == ctx.dtypes[0] for dt in ctx.dtypes):
+            gc = gflat.to(ctx.dtypes[0])
+            out = [gc[:W + 1], gc[W + 1:2 * (W + 1)], *gc[2 * (W + 1):].split(M)]
+        else:
+            out = [g.to(dt) for g, dt in zip([g_dirs[0], g_dirs[1], *grads], ctx.dtypes)]
         shape, dt = ctx.energy
         return (g_xn, g_w.to(weight.dtype), *out, torch.zeros(shape, dtype=dt, device=dev))
 
