@@ -10,12 +10,13 @@
 // arithmetic (dW rounded once, after the add).  The forward reads W once: one
 // wave per block of rows, the waves' per-column sums added in LDS in wave
 // order into one partial row per workgroup and direction, the partial rows
-// summed in a fixed order (sparc_column_sum); the backward is one wave per
+// summed in a fixed order (column_sums); the backward is one wave per
 // row block, two dot products per row, and the rank-2 update of the same row
 // of dW.  Replaces torch products over an fp32 copy of W, and the fp32
 // rank-2 product, its cast and the add into the projection's gradient.
 
 #include "common.h"
+#include "reduce.h"
 #include "sparc_hip.h"
 
 namespace sparc {
@@ -266,8 +267,9 @@ sparc_status sparc_controls_fold(int64_t width, int64_t dim, int32_t io_dtype, c
                            folded_radial);
   if (sparc_status s = fold_hip_status("controls fold")) return s;
   const int64_t nb = fold_blocks(width);
-  if (sparc_status s = sparc_column_sum(nb, dim, part, folded_phase, 0, stream)) return s;
-  return sparc_column_sum(nb, dim, part + nb * dim, folded_radial, 0, stream);
+  const float* in[2] = {part, part + nb * dim};
+  float* out[2] = {folded_phase, folded_radial};
+  return column_sums(nb, dim, 2, in, out, stream);
 }
 
 sparc_status sparc_controls_fold_backward(int64_t width, int64_t dim, int32_t io_dtype, const void* weight,

@@ -49,6 +49,7 @@
 
 #include "common.h"
 #include "p1_fused.h"
+#include "reduce.h"
 #include "sparc_hip.h"
 
 namespace sparc {
@@ -2207,19 +2208,38 @@ sparc_status scan_backward_impl(const Layout& l, int64_t batch, int64_t length, 
     if (l.V == 2) run_bwd<float, 2>(a, st); else run_bwd<float, 1>(a, st);
   }
   // d eta, d delta per token: the sums over the mode blocks of part_tok [2][n_mb][R]
-  if (sparc_status s = sparc_column_sum(l.n_mb, l.R, part_tok, deta, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(l.n_mb, l.R, part_tok + static_cast<int64_t>(l.n_mb) * l.R, ddelta, 0, stream))
-    return s;
+  {
+    const float* in[2] = {part_tok, part_tok + static_cast<int64_t>(l.n_mb) * l.R};
+    float* out[2] = {deta, ddelta};
+    if (sparc_status s = sparc::column_sums(l.n_mb, l.R, 2, in, out, stream)) return s;
+  }
   const int64_t prow = batch * l.n_seg;  // one partial row per (batch row, segment)
-  for (int p = 0; p < 5; ++p)
-    if (sparc_status s = sparc_column_sum(prow, modes, part_mode + static_cast<int64_t>(p) * prow * modes, outs[p], 0, stream))
-      return s;
+  {
+    const float* in[5];
+    for (int p = 0; p < 5; ++p) in[p] = part_mode + static_cast<int64_t>(p) * prow * modes;
+    if (sparc_status s = sparc::column_sums(prow, modes, 5, in, outs, stream)) return s;
+  }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer scan backward: %s", hipGetErrorString(e));
 }
 
 bool params_ok(const float* a, const float* b, const float* c, const float* d, const float* e) {
   return a && b && c && d && e;
+}
+
+// The controls' direction gradients from their row-block partials: columns
+// 0..W-1 from pd [2][n_rb][W] (phase, radial), the bias entries (column W)
+// from pbias [2][n_rb]; two launches of paired column sums.
+sparc_status direction_sums(int64_t n_rb, int64_t W, const float* pd, const float* pbias, float* dphase,
+                            float* dradial, sparc_stream_t stream) {
+  {
+    const float* in[2] = {pd, pd + n_rb * W};
+    float* out[2] = {dphase, dradial};
+    if (sparc_status s = sparc::column_sums(n_rb, W, 2, in, out, stream)) return s;
+  }
+  const float* in[2] = {pbias, pbias + n_rb};
+  float* out[2] = {dphase + W, dradial + W};
+  return sparc::column_sums(n_rb, 1, 2, in, out, stream);
 }
 
 #ifndef SPARC_P1_FUSED
@@ -2362,12 +2382,17 @@ sparc_status p1_fused_backward(const sparc_scan_desc* d, const float* eta, const
   else run_bwd_mode<kPlanes>(a, bf, l.V, st);
   // d eta, d delta per token over the mode blocks; d nu_log, d theta_log per
   // mode over the (batch row, segment) partial rows
-  if (sparc_status s = sparc_column_sum(l.n_mb, l.R, part_tok, deta, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(l.n_mb, l.R, part_tok + static_cast<int64_t>(l.n_mb) * l.R, ddelta, 0, stream))
-    return s;
+  {
+    const float* in[2] = {part_tok, part_tok + static_cast<int64_t>(l.n_mb) * l.R};
+    float* out[2] = {deta, ddelta};
+    if (sparc_status s = sparc::column_sums(l.n_mb, l.R, 2, in, out, stream)) return s;
+  }
   const int64_t prow = d->batch * l.n_seg;
-  if (sparc_status s = sparc_column_sum(prow, d->modes, part_mode, dnu_log, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(prow, d->modes, part_mode + prow * d->modes, dtheta_log, 0, stream)) return s;
+  {
+    const float* in[2] = {part_mode, part_mode + prow * d->modes};
+    float* out[2] = {dnu_log, dtheta_log};
+    if (sparc_status s = sparc::column_sums(prow, d->modes, 2, in, out, stream)) return s;
+  }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "p1 fused backward: %s", hipGetErrorString(e));
 }
@@ -2533,8 +2558,9 @@ sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int6
     const float* pt = part_tok + static_cast<int64_t>(p) * 2 * l.n_mb * rows_p;
     float* de = deta + static_cast<int64_t>(p) * rows_p;
     float* dd = ddelta + static_cast<int64_t>(p) * rows_p;
-    sparc_status s = sparc_column_sum(l.n_mb, rows_p, pt, de, 0, stream);
-    if (!s) s = sparc_column_sum(l.n_mb, rows_p, pt + static_cast<int64_t>(l.n_mb) * rows_p, dd, 0, stream);
+    const float* in[2] = {pt, pt + static_cast<int64_t>(l.n_mb) * rows_p};
+    float* out[2] = {de, dd};
+    sparc_status s = sparc::column_sums(l.n_mb, rows_p, 2, in, out, stream);
     if (s) {
       (void)join();
       return s;
@@ -2562,14 +2588,12 @@ sparc_status piped_backward(const Layout& l, int64_t batch, int64_t length, int6
   if (e != hipSuccess) return fail(SPARC_EHIP, "mixer backward: stream join: %s", hipGetErrorString(e));
   float* outs[5] = {dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response};
   const int64_t prow = batch * l.n_seg;  // one partial row per (batch row, piece)
-  for (int p = 0; p < 5; ++p)
-    if (sparc_status s = sparc_column_sum(prow, modes, part_mode + static_cast<int64_t>(p) * prow * modes, outs[p], 0, stream))
-      return s;
-  const int64_t plane = static_cast<int64_t>(l.n_rb) * W;
-  if (sparc_status s = sparc_column_sum(l.n_rb, W, pd, dphase_direction, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(l.n_rb, W, pd + plane, dradial_direction, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(l.n_rb, 1, pbias, dphase_direction + W, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(l.n_rb, 1, pbias + l.n_rb, dradial_direction + W, 0, stream)) return s;
+  {
+    const float* in[5];
+    for (int p = 0; p < 5; ++p) in[p] = part_mode + static_cast<int64_t>(p) * prow * modes;
+    if (sparc_status s = sparc::column_sums(prow, modes, 5, in, outs, stream)) return s;
+  }
+  if (sparc_status s = direction_sums(l.n_rb, W, pd, pbias, dphase_direction, dradial_direction, stream)) return s;
   e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(e));
 }
@@ -2702,15 +2726,22 @@ sparc_status coop_backward(int kS, int64_t batch, int64_t length, int64_t modes,
     hipLaunchKernelGGL((mixer_bwd_kernel<float, 1, kCoopS, false, kC>), g, dim3(64), 0, st, a);
   if (hipError_t le = hipGetLastError()) return fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(le));
   float* outs[5] = {dnu_log, dtheta_log, dwrite_log_gain, dwrite_phase_response, dwrite_radial_response};
-  for (int p = 0; p < 5; ++p)
-    if (sparc_status s = sparc_column_sum(batch, modes, a.part_mode + static_cast<int64_t>(p) * batch * modes, outs[p],
-                                          0, stream))
-      return s;
+  {
+    const float* in[5];
+    for (int p = 0; p < 5; ++p) in[p] = a.part_mode + static_cast<int64_t>(p) * batch * modes;
+    if (sparc_status s = sparc::column_sums(batch, modes, 5, in, outs, stream)) return s;
+  }
   const int64_t R = batch * length;
-  if (sparc_status s = sparc_column_sum(batch, W, a.coop_pd, dphase_direction, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(batch, W, a.coop_pd + batch * W, dradial_direction, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(R, 1, a.coop_dtok, dphase_direction + W, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(R, 1, a.coop_dtok + R, dradial_direction + W, 0, stream)) return s;
+  {
+    const float* in[2] = {a.coop_pd, a.coop_pd + batch * W};
+    float* out[2] = {dphase_direction, dradial_direction};
+    if (sparc_status s = sparc::column_sums(batch, W, 2, in, out, stream)) return s;
+  }
+  {
+    const float* in[2] = {a.coop_dtok, a.coop_dtok + R};
+    float* out[2] = {dphase_direction + W, dradial_direction + W};
+    if (sparc_status s = sparc::column_sums(R, 1, 2, in, out, stream)) return s;
+  }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(e));
 }
@@ -2885,11 +2916,7 @@ sparc_status sparc_mixer_backward(int64_t batch, int64_t length, int64_t modes, 
     hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, st, l.R, W, kCtrlBwdRows, x, phase_direction,
                        radial_direction, eta, delta, deta, ddelta, dx, pd, pbias, l.R, int64_t(0), l.R, 0, l.n_rb);
   // direction gradients: columns 0..W-1 from the row-block partials, the bias from pbias
-  const int64_t plane = static_cast<int64_t>(l.n_rb) * W;
-  if (sparc_status s = sparc_column_sum(l.n_rb, W, pd, dphase_direction, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(l.n_rb, W, pd + plane, dradial_direction, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(l.n_rb, 1, pbias, dphase_direction + W, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(l.n_rb, 1, pbias + l.n_rb, dradial_direction + W, 0, stream)) return s;
+  if (sparc_status s = direction_sums(l.n_rb, W, pd, pbias, dphase_direction, dradial_direction, stream)) return s;
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "mixer backward: %s", hipGetErrorString(e));
 }
@@ -2955,11 +2982,7 @@ sparc_status sparc_controls_backward(int64_t rows, int64_t width, int32_t io_dty
   else
     hipLaunchKernelGGL(ctrl_bwd_kernel<float>, gb, dim3(256), 0, st, rows, W, c.rows, x, phase_direction,
                        radial_direction, eta, delta, deta, ddelta, dx, pd, pbias, rows, int64_t(0), rows, 0, c.n_rb);
-  const int64_t plane = static_cast<int64_t>(c.n_rb) * W;
-  if (sparc_status s = sparc_column_sum(c.n_rb, W, pd, dphase_direction, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(c.n_rb, W, pd + plane, dradial_direction, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(c.n_rb, 1, pbias, dphase_direction + W, 0, stream)) return s;
-  if (sparc_status s = sparc_column_sum(c.n_rb, 1, pbias + c.n_rb, dradial_direction + W, 0, stream)) return s;
+  if (sparc_status s = direction_sums(c.n_rb, W, pd, pbias, dphase_direction, dradial_direction, stream)) return s;
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? SPARC_OK : fail(SPARC_EHIP, "controls backward: %s", hipGetErrorString(e));
 }

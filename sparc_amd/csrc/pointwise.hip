@@ -12,6 +12,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "reduce.h"
 #include "sparc_hip.h"
 
 #include <atomic>
@@ -203,8 +204,8 @@ __global__ void row_sum_kernel(int64_t rows, int64_t cols, const float* in, floa
 // interleaved partial sums, combined in a fixed order), and the slices
 // combine in a fixed binary tree in LDS: the result does not depend on
 // timing, and a long column is read by S threads at once.
-__global__ void __launch_bounds__(1024)
-column_sum_kernel(int64_t rows, int64_t cols, int cw, const float* in, float* out, int accumulate) {
+__device__ __forceinline__ void column_sum_block(int64_t rows, int64_t cols, int cw, const float* in, float* out,
+                                                 int accumulate) {
   __shared__ float red[1024];
   const int t = threadIdx.x;
   const int cl = t & (cw - 1), slice = t / cw;
@@ -232,9 +233,29 @@ column_sum_kernel(int64_t rows, int64_t cols, int cw, const float* in, float* ou
   if (slice == 0 && c < cols) out[c] = accumulate ? out[c] + red[t] : red[t];
 }
 
-static void launch_column_sum(hipStream_t st, int64_t rows, int64_t cols, const float* in, float* out, int accumulate) {
+__global__ void __launch_bounds__(1024)
+column_sum_kernel(int64_t rows, int64_t cols, int cw, const float* in, float* out, int accumulate) {
+  column_sum_block(rows, cols, cw, in, out, accumulate);
+}
+
+// several column sums of one shape: problem blockIdx.y
+struct ColumnSumSet {
+  const float* in[kMaxColumnSums];
+  float* out[kMaxColumnSums];
+};
+__global__ void __launch_bounds__(1024)
+column_sums_kernel(int64_t rows, int64_t cols, int cw, ColumnSumSet set) {
+  column_sum_block(rows, cols, cw, set.in[blockIdx.y], set.out[blockIdx.y], 0);
+}
+
+static int column_sum_width(int64_t cols) {
   int cw = 1;
   while (cw < 64 && cw < cols) cw <<= 1;
+  return cw;
+}
+
+static void launch_column_sum(hipStream_t st, int64_t rows, int64_t cols, const float* in, float* out, int accumulate) {
+  const int cw = column_sum_width(cols);
   hipLaunchKernelGGL(column_sum_kernel, dim3(static_cast<unsigned>((cols + cw - 1) / cw)), dim3(1024), 0, st, rows,
                      cols, cw, in, out, accumulate);
 }
@@ -679,6 +700,25 @@ sparc_status noalloc_scratch(sparc_stream_t stream, void** out) {
   return SPARC_OK;
 }
 }  // namespace
+
+namespace sparc {
+sparc_status column_sums(int64_t rows, int64_t cols, int n, const float* const* ins, float* const* outs,
+                         sparc_stream_t stream) {
+  if (rows < 0 || cols <= 0 || n < 1 || n > kMaxColumnSums || !ins || !outs)
+    return fail2(SPARC_EINVAL, "column_sums: bad arguments");
+  ColumnSumSet set{};
+  for (int i = 0; i < n; ++i) {
+    if (!outs[i] || (rows > 0 && !ins[i])) return fail2(SPARC_EINVAL, "column_sums: NULL pointer");
+    set.in[i] = ins[i];
+    set.out[i] = outs[i];
+  }
+  const int cw = column_sum_width(cols);
+  hipLaunchKernelGGL(column_sums_kernel, dim3(static_cast<unsigned>((cols + cw - 1) / cw), static_cast<unsigned>(n)),
+                     dim3(1024), 0, reinterpret_cast<hipStream_t>(stream), rows, cols, cw, set);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SPARC_OK : fail2(SPARC_EHIP, "column_sums: %s", hipGetErrorString(e));
+}
+}  // namespace sparc
 
 extern "C" {
 
