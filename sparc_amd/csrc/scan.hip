@@ -41,6 +41,7 @@
 
 #include "common.h"
 #include "p1_fused.h"
+#include "reduce.h"
 #include "sparc_hip.h"
 
 // SPARC_SCAN_PART: which part of a split build this is (see the host side)
@@ -4159,8 +4160,9 @@ sparc_status sparc_scan_backward(const sparc_scan_desc* d, const void* gate0, co
   if (p1) {
     // one partial row per tile (look-back) or per batch row (chain)
     const int64_t prow = pl.chain ? d->batch : d->batch * pl.n_chunks;
-    if (sparc_status s = sparc_column_sum(prow, d->modes, a.part_nu, dnu_log, 0, stream)) return s;
-    if (sparc_status s = sparc_column_sum(prow, d->modes, a.part_theta, dtheta_log, 0, stream)) return s;
+    const float* in[2] = {a.part_nu, a.part_theta};
+    float* out[2] = {dnu_log, dtheta_log};
+    if (sparc_status s = sparc::column_sums(prow, d->modes, 2, in, out, stream)) return s;
   }
   e = hipGetLastError();
   if (e != hipSuccess) return fail(SPARC_EHIP, "scan backward reductions: %s", hipGetErrorString(e));
