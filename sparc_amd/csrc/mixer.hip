@@ -1683,7 +1683,9 @@ mixer_bwd_kernel(Args a) {
 __global__ void __launch_bounds__(64)
 mixer_seg_carry_kernel(int B, int M, int n_seg, int reverse, const float* seg_sum, const float* init_re,
                        const float* init_im, float* seg_state) {
-  const int i = blockIdx.x, lane = threadIdx.x;  // i = b * M + m
+  // i = b * M + m; neighbouring modes share the cache lines of seg_sum and
+  // seg_state (8 and 16 to a line), so they run on the same XCD (one L2)
+  const int i = xcd_swizzle(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x)), lane = threadIdx.x;
   const int b = i / M, m = i - b * M;
   float cr = init_re ? init_re[i] : 0.0f, ci = init_im ? init_im[i] : 0.0f;
   for (int g0 = 0; g0 < n_seg; g0 += 64) {
