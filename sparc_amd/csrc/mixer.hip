@@ -1730,9 +1730,13 @@ __global__ void fill_zero_f32_kernel(float* p, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i < n) p[i] = 0.0f;
 }
-__global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
+// p[0 .. 4 n4) = v in 16-byte stores, and the first thread also sets
+// head[0 .. n_head) = head_v (the one-launch backward's error words)
+__global__ void fill_u32x4_kernel(uint4* p, int64_t n4, uint32_t v, uint32_t* head, int n_head, uint32_t head_v) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i < n) p[i] = v;
+  if (i < n4) p[i] = make_uint4(v, v, v, v);
+  if (i == 0)
+    for (int k = 0; k < n_head; ++k) head[k] = head_v;
 }
 
 // ---------------------------------------------------------------------------
@@ -2695,10 +2699,10 @@ sparc_status coop_backward(int kS, int64_t batch, int64_t length, int64_t modes,
   // the error word starts at zero, the records and the blocks' gradients as
   // kCoopEmpty (fill kernels, not memsets: the call may be captured into a
   // graph; the records and gradients are adjacent)
-  const int64_t nfill = static_cast<int64_t>(c.dtok - c.part) / 4;
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(1), dim3(256), 0, st, reinterpret_cast<uint32_t*>(ws), int64_t(2), 0u);
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(static_cast<unsigned>((nfill + 255) / 256)), dim3(256), 0, st,
-                     reinterpret_cast<uint32_t*>(ws + c.part), nfill, kCoopEmpty);
+  // (one launch of 16-byte stores: the offsets are multiples of 256 bytes)
+  const int64_t nfill4 = static_cast<int64_t>(c.dtok - c.part) / 16;
+  hipLaunchKernelGGL(fill_u32x4_kernel, dim3(static_cast<unsigned>((nfill4 + 255) / 256)), dim3(256), 0, st,
+                     reinterpret_cast<uint4*>(ws + c.part), nfill4, kCoopEmpty, reinterpret_cast<uint32_t*>(ws), 2, 0u);
   Args a{};
   a.B = static_cast<int>(batch);
   a.T = static_cast<int>(length);
