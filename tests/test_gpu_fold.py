@@ -130,3 +130,43 @@ def test_projected_mixer_fold_matches_torch_products(dtype, monkeypatch):
     for name, x, y in zip(("y", "dW", "dxn", "dphase", "dradial"), a, b):
         scale = y.abs().max().item() + 1e-6
         torch.testing.assert_close(x / scale, y / scale, **tol, msg=lambda m: f"{name}: {m}")
+
+
+def test_projected_mixer_mixed_parameter_dtypes():
+    """Module parameters of different dtypes (here the directions in bf16, the
+    per-mode vectors in fp32) take the per-tensor casts: outputs and
+    gradients match the all-fp32 run with the same (bf16-representable)
+    values, and each gradient comes back in its parameter's dtype."""
+    print("[case] projected mixer, mixed parameter dtypes", flush=True)
+    from sparc_amd import mixer as mx
+    from sparc_amd.sparc import SPARCMixer
+
+    torch.manual_seed(12)
+    D, M, B, T = 32, 24, 2, 48
+    mod = SPARCMixer(2 * M).cuda()
+    with torch.no_grad():
+        for p in (mod.phase_direction, mod.radial_direction):
+            p.copy_((torch.randn_like(p) * 0.3).to(torch.bfloat16).float())
+    w = (torch.randn(2 * M, D, device="cuda") / D ** 0.5).requires_grad_()
+    xn = torch.randn(B, T, D, device="cuda").requires_grad_()
+    dy = torch.randn(B, T, 2 * M, device="cuda")
+
+    def run():
+        for t in [w, xn] + list(mod.parameters()):
+            t.grad = None
+        y, (lr, li) = mx.projected_sequence(mod, xn, w)
+        (y * dy).sum().add_(lr.sum() + li.sum()).backward()
+        return [y.detach().clone()] + [t.grad.detach().float().clone() for t in (
+            w, xn, mod.phase_direction, mod.radial_direction, mod.nu_log, mod.write_log_gain)]
+
+    a = run()
+    with torch.no_grad():
+        mod.phase_direction.data = mod.phase_direction.data.to(torch.bfloat16)
+        mod.radial_direction.data = mod.radial_direction.data.to(torch.bfloat16)
+    b = run()
+    assert mod.phase_direction.grad.dtype == torch.bfloat16 and mod.nu_log.grad.dtype == torch.float32
+    for name, x, y in zip(("y", "dW", "dxn", "dphase", "dradial", "dnu_log", "dwlg"), a, b):
+        scale = x.abs().max().item() + 1e-6
+        # the direction gradients are rounded to bf16 once; the rest is the same fp32 arithmetic
+        tol = 2 ** -7 if name in ("dphase", "dradial") else 1e-5
+        torch.testing.assert_close(y / scale, x / scale, rtol=tol, atol=tol, msg=lambda m: f"{name}: {m}")
