@@ -111,11 +111,32 @@ rms_norm_bwd_kernel(int64_t R, int D, const void* x, const void* w, const float*
     if (c < D) load8<IO>(w, c, wv[k]);
   }
   const float inv_d = 1.0f / static_cast<float>(D);
+  // row j + 1's x and dy are loaded before row j is reduced and its dx
+  // stored, so that they are in flight meanwhile (the compiler cannot move
+  // them above that store itself: dx might alias x or dy)
+  float xn[NCH][8] = {}, dn[NCH][8] = {};
+  auto load_row = [&](int64_t row) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+      const int c = (k * 64 + lane) * 8;
+      if (c < D) {
+        load8<IO>(x, row * D + c, xn[k]);
+        load8<IO>(dy, row * D + c, dn[k]);
+      }
+    }
+  };
+  if (r0 < R) load_row(r0);
   for (int j = 0; j < kNormBwdRows; ++j) {
     const int64_t row = r0 + j;
     if (row >= R) break;  // wave-uniform; every wave still reaches the barriers below
     const int64_t base = row * D;
     const float r = rstd[row];
+    float xv[NCH][8], dv[NCH][8];
+#pragma unroll
+    for (int k = 0; k < NCH; ++k)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) { xv[k][i] = xn[k][i]; dv[k][i] = dn[k][i]; }
+    if (j + 1 < kNormBwdRows && row + 1 < R) load_row(row + 1);  // wave-uniform
     float xh[NCH][8], g[NCH][8];
     float s = 0.0f;
 #pragma unroll
@@ -124,15 +145,12 @@ rms_norm_bwd_kernel(int64_t R, int D, const void* x, const void* w, const float*
 #pragma unroll
       for (int i = 0; i < 8; ++i) { xh[k][i] = 0.0f; g[k][i] = 0.0f; }
       if (c < D) {
-        float xv[8], dv[8];
-        load8<IO>(x, base + c, xv);
-        load8<IO>(dy, base + c, dv);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          xh[k][i] = xv[i] * r;
-          g[k][i] = dv[i] * wv[k][i];
+          xh[k][i] = xv[k][i] * r;
+          g[k][i] = dv[k][i] * wv[k][i];
           s = fmaf(g[k][i], xh[k][i], s);
-          acc[k][i] = fmaf(dv[i], xh[k][i], acc[k][i]);
+          acc[k][i] = fmaf(dv[k][i], xh[k][i], acc[k][i]);
         }
       }
     }
