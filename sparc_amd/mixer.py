@@ -214,8 +214,9 @@ class _ProjectedMixer(torch.autograd.Function):
         dirs = flat[:2 * (W + 1)].view(2, W + 1)
         params = list(flat[2 * (W + 1):].split(M))
         # the folded directions [W^T u_phase, b_phase], [W^T u_radial, b_radial]
-        # in rows of a 16-byte multiple (each row a 16-byte aligned vector)
-        v = torch.zeros(2, (D + 4) // 4 * 4, dtype=torch.float32, device=dev)
+        # in rows of a 16-byte multiple (each row a 16-byte aligned vector);
+        # entries 0..D are written below and the kernels read no others
+        v = torch.empty(2, (D + 4) // 4 * 4, dtype=torch.float32, device=dev)
         wc = aligned16(weight.detach())
         if D <= _FOLD_MAX_DIM:  # sparc_controls_fold: one pass over W, no fp32 copy of it
             fws = torch.empty(lib.sparc_controls_fold_workspace_bytes(W, D), dtype=torch.uint8, device=dev)
